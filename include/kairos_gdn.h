@@ -1,0 +1,129 @@
+/*
+ * kairos_gdn.h -- C ABI of the MI355X (gfx950) chunked GatedDeltaNet forward.
+ *
+ * Drop-in native backend for the op
+ *     chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state,
+ *                            output_final_state, use_qk_l2norm_in_kernel,
+ *                            cu_seqlens) -> (o, final_state)
+ * of flash-linear-attention 0.4.0 as vendored by Kairos
+ * (kairos/third_party/fla/ops/gated_delta_rule/chunk.py:217-323).
+ *
+ * Conventions (all entry points):
+ *  - Every tensor argument is a device pointer to a contiguous buffer in the
+ *    reference layout: q, k [B, T, H, K]; v, o [B, T, H, V]; g, beta [B, T, H];
+ *    initial_state / final_state [N, H, K, V].  Vector-loaded buffers (q, k, v,
+ *    o and the stage intermediates) must be 16-byte aligned.
+ *  - Variable length: pass cu_seqlens (device, int64 [n_seqs + 1], first entry
+ *    0, last entry T, non-decreasing) with B == 1 and n_seqs >= 1; the chunk
+ *    map is built on the device (no host synchronisation).  Fixed length:
+ *    cu_seqlens == NULL and n_seqs == 0 (N = B sequences of length T).
+ *  - dtype codes: KAIROS_GDN_F32, KAIROS_GDN_BF16, KAIROS_GDN_F8E4M3 (q/k only,
+ *    with per-head fp32 dequantisation scales q_scale[H], k_scale[H]).
+ *    bf16 q/k/v (or fp8 q/k with bf16 v) run the bf16 path; fp32 q/k/v the
+ *    fp32 path.  g is fp32 or bf16; beta fp32 or bf16; initial_state fp32 or
+ *    bf16; final_state is always fp32.
+ *  - Supported head dims: K in {64, 128}, V in {64, 128}.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *    is stream-ordered: no entry point synchronises or allocates.  Scratch
+ *    memory comes from the caller's `workspace`.  Entry points are reentrant;
+ *    concurrent calls must use distinct workspaces.
+ *  - Return value: KAIROS_GDN_OK or an error code; kairos_gdn_last_error()
+ *    returns the message of the calling thread's last failure.  No exception
+ *    crosses the ABI.
+ */
+#ifndef KAIROS_GDN_H
+#define KAIROS_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KAIROS_GDN_ABI_VERSION 1
+
+#define KAIROS_GDN_F32 0
+#define KAIROS_GDN_BF16 1
+#define KAIROS_GDN_F8E4M3 2
+
+#define KAIROS_GDN_OK 0
+#define KAIROS_GDN_EINVAL 1       /* invalid argument: shape, pointer, alignment, dtype mix */
+#define KAIROS_GDN_EUNSUPPORTED 2 /* head dims / dtype combination not built */
+#define KAIROS_GDN_EWORKSPACE 3   /* workspace too small */
+#define KAIROS_GDN_EHIP 4         /* HIP runtime error at launch */
+
+int kairos_gdn_abi_version(void);
+const char* kairos_gdn_last_error(void);
+
+/* Upper bound on the number of 64-token chunks over all sequences (exact for
+ * fixed length: B * ceil(T / 64); varlen: T / 64 + n_seqs).  Stage
+ * intermediates indexed by chunk are sized with it. */
+int64_t kairos_gdn_num_chunks_bound(int64_t B, int64_t T, int64_t n_seqs);
+
+/* Bytes of workspace kairos_gdn_chunk_fwd needs for this problem. */
+size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                           int64_t n_seqs, int qk_dtype, int v_dtype,
+                                           int use_qk_l2norm);
+
+/* Whole forward.  Replaces ChunkGatedDeltaRuleFunction.forward
+ * (chunk.py:154-186: optional q/k L2 norm, then chunk_gated_delta_rule_fwd,
+ * chunk.py:16-67).  o gets v's storage dtype.  final_state may be NULL
+ * (output_final_state=False); initial_state may be NULL (zero state).
+ * scale multiplies q.k and q.h (the reference defaults it to K^-0.5,
+ * chunk.py:309-310; the caller passes the value). */
+int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const float* q_scale, const float* k_scale, const void* initial_state, void* o,
+                         float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T,
+                         int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype, int g_dtype,
+                         int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* ---- stage entry points (parity testing and composition) ----------------
+ * Each stage replaces one reference function.  Varlen stage calls need
+ * kairos_gdn_stage_workspace_size(n_seqs) bytes of workspace (chunk map);
+ * fixed-length calls accept workspace = NULL. */
+size_t kairos_gdn_stage_workspace_size(int64_t n_seqs);
+
+/* chunk_local_cumsum (fla ops/utils/cumsum.py:247-279, scalar gates, chunk 64):
+ * gc [B, T, H] fp32. */
+int kairos_gdn_chunk_local_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu_seqlens,
+                                  int64_t n_seqs, int64_t B, int64_t T, int64_t H, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* chunk_local_cumsum + chunk_scaled_dot_kkt_fwd + solve_tril + recompute_w_u_fwd
+ * (cumsum.py:247-279, chunk_scaled_dot_kkt.py:76-124, solve_tril.py:334-382,
+ * wy_fast.py:213-248), fused.  Outputs: gc [B,T,H] fp32; w [B,T,H,K];
+ * uT [NCb, H, V, 64] (u of chunk c transposed, NCb = num_chunks_bound);
+ * optional A [B,T,H,64] fp32 and Ai [B,T,H,64] (storage dtype) -- pass NULL to skip. */
+int kairos_gdn_prepare_wy(const void* k, const void* v, const void* g, const void* beta, const float* k_scale,
+                          float* gc, void* w, void* uT, float* A, void* Ai, const int64_t* cu_seqlens,
+                          int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int k_dtype,
+                          int v_dtype, int g_dtype, int beta_dtype, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* chunk_gated_delta_rule_fwd_h (fla ops/common/chunk_delta_h.py:454-500).
+ * Outputs: hT [NCb, H, V, K] (state before chunk c, transposed per chunk);
+ * vnT [NCb, H, V, 64] (ungated v_new of chunk c, transposed); final_state
+ * [N, H, K, V] fp32 or NULL. */
+int kairos_gdn_fwd_h(const void* k, const float* k_scale, const void* w, const void* uT, const float* gc,
+                     const void* initial_state, void* hT, void* vnT, float* final_state,
+                     const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K,
+                     int64_t V, int k_dtype, int v_dtype, int h0_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* chunk_fwd_o (fla ops/common/chunk_o.py:498-535): o [B, T, H, V] in v's dtype. */
+int kairos_gdn_fwd_o(const void* q, const void* k, const float* q_scale, const float* k_scale, const void* hT,
+                     const void* vnT, const float* gc, void* o, float scale, const int64_t* cu_seqlens,
+                     int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
+                     int v_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* l2norm_fwd (fla modules/l2norm.py:157-196), y = x / sqrt(sum x^2 + 1e-6) over
+ * the last dim D (multiple of 8, <= 512), in x's dtype (fp32 or bf16). */
+int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KAIROS_GDN_H */

@@ -1,0 +1,335 @@
+// C ABI of the chunked GatedDeltaNet forward (declared in include/kairos_gdn.h):
+// argument validation, workspace carving and stage orchestration.  The
+// orchestration mirrors chunk_gated_delta_rule_fwd (fla
+// ops/gated_delta_rule/chunk.py:16-67) with the four prepare stages fused:
+//   [l2norm q, k] -> [chunk map] -> prepare (gc, w, u) -> fwd_h (h, v_new, ht) -> fwd_o (o)
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/kairos_gdn.h"
+#include "gdn_common.hpp"
+#include "gdn_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return KAIROS_GDN_OK;
+}
+
+int from_launch(int rc, const char* what) {
+  if (rc == 0) return KAIROS_GDN_OK;
+  if (rc == -2) return fail(KAIROS_GDN_EUNSUPPORTED, "%s: dtype / head-dim combination is not built", what);
+  return fail(KAIROS_GDN_EHIP, "%s: HIP launch failed: %s", what, hipGetErrorString(hipGetLastError()));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+size_t dt_size(int dt) { return dt == KAIROS_GDN_F32 ? 4 : dt == KAIROS_GDN_BF16 ? 2 : 1; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int64_t chunks_bound(int64_t B, int64_t T, int64_t n_seqs) {
+  if (n_seqs > 0) return T / kgdn::C + n_seqs;
+  return B * ((T + kgdn::C - 1) / kgdn::C);
+}
+
+struct Geometry {
+  int64_t B, T, H, K, V, n_seqs, N, nc;
+  bool varlen;
+};
+
+int check_geometry(Geometry& G, const int64_t* cu, int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K,
+                   int64_t V, const char* what) {
+  if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0)
+    return fail(KAIROS_GDN_EINVAL, "%s: invalid shape B=%lld T=%lld H=%lld K=%lld V=%lld", what, (long long)B,
+                (long long)T, (long long)H, (long long)K, (long long)V);
+  if (K > 256) return fail(KAIROS_GDN_EINVAL, "%s: head dimension K=%lld is larger than 256", what, (long long)K);
+  if ((cu == nullptr) != (n_seqs == 0))
+    return fail(KAIROS_GDN_EINVAL, "%s: cu_seqlens and n_seqs must be given together", what);
+  if (n_seqs < 0) return fail(KAIROS_GDN_EINVAL, "%s: n_seqs must be >= 0", what);
+  if (cu && B != 1)
+    return fail(KAIROS_GDN_EINVAL, "%s: the batch size is expected to be 1 rather than %lld when using cu_seqlens",
+                what, (long long)B);
+  if (H > 65535) return fail(KAIROS_GDN_EINVAL, "%s: H=%lld exceeds the grid limit", what, (long long)H);
+  G.B = B; G.T = T; G.H = H; G.K = K; G.V = V;
+  G.n_seqs = n_seqs;
+  G.varlen = cu != nullptr;
+  G.N = G.varlen ? n_seqs : B;
+  G.nc = chunks_bound(B, T, n_seqs);
+  if (G.nc > 0x7fffffff) return fail(KAIROS_GDN_EINVAL, "%s: too many chunks", what);
+  return KAIROS_GDN_OK;
+}
+
+// compute dtype of a (q/k, v) pair: bf16 path for bf16 v with bf16/fp8 q,k; fp32 for all-fp32.
+int compute_dtype(int qk_dtype, int v_dtype) {
+  if (v_dtype == KAIROS_GDN_BF16 && (qk_dtype == KAIROS_GDN_BF16 || qk_dtype == KAIROS_GDN_F8E4M3))
+    return KAIROS_GDN_BF16;
+  if (v_dtype == KAIROS_GDN_F32 && qk_dtype == KAIROS_GDN_F32) return KAIROS_GDN_F32;
+  return -1;
+}
+
+bool valid_scalar_dt(int dt) { return dt == KAIROS_GDN_F32 || dt == KAIROS_GDN_BF16; }
+
+// Workspace carving helper.
+struct Carver {
+  char* base;
+  size_t off = 0;
+  void* take(size_t bytes) {
+    void* p = base ? base + off : nullptr;
+    off += align_up(bytes);
+    return p;
+  }
+};
+
+// Build the varlen chunk map into the workspace (no-op for fixed length).
+int chunk_map(const Geometry& G, const int64_t* cu, Carver& cv, const int32_t** out, hipStream_t s) {
+  *out = nullptr;
+  if (!G.varlen) return KAIROS_GDN_OK;
+  int32_t* off = static_cast<int32_t*>(cv.take(sizeof(int32_t) * (G.N + 1)));
+  *out = off;
+  return from_launch(kgdn::launch_chunk_offsets(cu, (int)G.N, off, s), "chunk map");
+}
+
+size_t stage_ws(int64_t n_seqs) { return n_seqs > 0 ? align_up(sizeof(int32_t) * (n_seqs + 1)) : 0; }
+
+}  // namespace
+
+extern "C" {
+
+int kairos_gdn_abi_version(void) { return KAIROS_GDN_ABI_VERSION; }
+
+const char* kairos_gdn_last_error(void) { return g_last_error.c_str(); }
+
+int64_t kairos_gdn_num_chunks_bound(int64_t B, int64_t T, int64_t n_seqs) { return chunks_bound(B, T, n_seqs); }
+
+size_t kairos_gdn_stage_workspace_size(int64_t n_seqs) { return stage_ws(n_seqs); }
+
+size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs,
+                                           int qk_dtype, int v_dtype, int use_qk_l2norm) {
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
+  const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
+  const size_t tok = (size_t)(B * T * H);
+  size_t total = stage_ws(n_seqs);
+  if (use_qk_l2norm) total += 2 * align_up(tok * K * dt_size(qk_dtype));
+  total += align_up(tok * sizeof(float));                 // gc
+  total += align_up(tok * K * es);                        // w
+  total += align_up(nc * H * V * kgdn::C * es);           // uT
+  total += align_up(nc * H * V * K * es);                 // hT
+  total += align_up(nc * H * V * kgdn::C * es);           // vnT
+  return total;
+}
+
+int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const float* q_scale, const float* k_scale, const void* initial_state, void* o,
+                         float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T,
+                         int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype, int g_dtype, int beta_dtype,
+                         int h0_dtype, float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  const char* what = "kairos_gdn_chunk_fwd";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix q/k=%d v=%d", what, qk_dtype, v_dtype);
+  if (!valid_scalar_dt(g_dtype) || !valid_scalar_dt(beta_dtype) || (initial_state && !valid_scalar_dt(h0_dtype)))
+    return fail(KAIROS_GDN_EINVAL, "%s: g, beta and initial_state must be fp32 or bf16", what);
+  if (qk_dtype == KAIROS_GDN_F8E4M3 && (q_scale == nullptr || k_scale == nullptr))
+    return fail(KAIROS_GDN_EINVAL, "%s: fp8 q/k need per-head q_scale and k_scale", what);
+  if (qk_dtype == KAIROS_GDN_F8E4M3 && use_qk_l2norm)
+    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: the in-kernel L2 norm is not available for fp8 q/k", what);
+  if (!(K == 64 || K == 128) || !(V == 64 || V == 128))
+    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: head dims K=%lld V=%lld are not built (K, V in {64, 128})", what,
+                (long long)K, (long long)V);
+  if (!std::isfinite(scale)) return fail(KAIROS_GDN_EINVAL, "%s: scale must be finite", what);
+  const bool any_tokens = G.B * G.T > 0;
+  if (any_tokens && (!q || !k || !v || !g || !beta || !o))
+    return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(KAIROS_GDN_EINVAL, "%s: q, k, v and o must be 16-byte aligned", what);
+  const size_t need = kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, qk_dtype, v_dtype, use_qk_l2norm);
+  if (workspace_bytes < need)
+    return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace of %zu bytes is smaller than the %zu required", what,
+                workspace_bytes, need);
+  if (need && !aligned16(workspace)) return fail(KAIROS_GDN_EINVAL, "%s: workspace must be 16-byte aligned", what);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
+  const size_t tok = (size_t)(B * T * H);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  if (use_qk_l2norm && any_tokens) {
+    void* qn = cv.take(tok * K * dt_size(qk_dtype));
+    void* kn = cv.take(tok * K * dt_size(qk_dtype));
+    if (int rc = from_launch(kgdn::launch_l2norm(q, qn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q)")) return rc;
+    if (int rc = from_launch(kgdn::launch_l2norm(k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(k)")) return rc;
+    q = qn;
+    k = kn;
+  }
+  float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
+  void* w = cv.take(tok * K * es);
+  void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  void* hT = cv.take((size_t)G.nc * H * V * K * es);
+  void* vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+
+  const int N = (int)G.N;
+  if (G.nc > 0) {
+    kgdn::PrepareArgs pa{};
+    pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
+    pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
+    pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = T; pa.H = (int)H;
+    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = nullptr;
+    if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "prepare")) return rc;
+  }
+  kgdn::FwdHArgs ha{};
+  ha.k = k; ha.k_scale = k_scale; ha.w = w; ha.uT = uT; ha.gc = gc;
+  ha.h0 = initial_state; ha.h0_dtype = h0_dtype;
+  ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = N; ha.T = T; ha.H = (int)H;
+  ha.hT = hT; ha.vnT = vnT; ha.ht = final_state;
+  if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h")) return rc;
+  if (G.nc > 0) {
+    kgdn::FwdOArgs oa{};
+    oa.q = q; oa.k = k; oa.q_scale = q_scale; oa.k_scale = k_scale;
+    oa.hT = hT; oa.vnT = vnT; oa.gc = gc; oa.scale = scale;
+    oa.cu = cu_seqlens; oa.chunk_off = chunk_off; oa.N = N; oa.T = T; oa.H = (int)H; oa.o = o;
+    if (int rc = from_launch(kgdn::launch_fwd_o(oa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "fwd_o")) return rc;
+  }
+  return ok();
+}
+
+int kairos_gdn_chunk_local_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu_seqlens, int64_t n_seqs,
+                                  int64_t B, int64_t T, int64_t H, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const char* what = "kairos_gdn_chunk_local_cumsum";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, 64, 64, what)) return rc;
+  if (!valid_scalar_dt(g_dtype)) return fail(KAIROS_GDN_EINVAL, "%s: g must be fp32 or bf16", what);
+  if (workspace_bytes < stage_ws(n_seqs)) return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace too small", what);
+  if (G.nc == 0) return ok();
+  if (!g || !gc) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  if (int rc = from_launch(kgdn::launch_cumsum(g, g_dtype, gc, cu_seqlens, chunk_off, (int)G.N, T, (int)H, G.nc, s),
+                           what))
+    return rc;
+  return ok();
+}
+
+int kairos_gdn_prepare_wy(const void* k, const void* v, const void* g, const void* beta, const float* k_scale,
+                          float* gc, void* w, void* uT, float* A, void* Ai, const int64_t* cu_seqlens, int64_t n_seqs,
+                          int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int k_dtype, int v_dtype,
+                          int g_dtype, int beta_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_prepare_wy";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(k_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix k=%d v=%d", what, k_dtype, v_dtype);
+  if (!valid_scalar_dt(g_dtype) || !valid_scalar_dt(beta_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: g and beta must be fp32 or bf16", what);
+  if (k_dtype == KAIROS_GDN_F8E4M3 && !k_scale) return fail(KAIROS_GDN_EINVAL, "%s: fp8 k needs k_scale", what);
+  if (workspace_bytes < stage_ws(n_seqs)) return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace too small", what);
+  if (G.nc == 0) return ok();
+  if (!k || !v || !g || !beta || !gc || !w || !uT) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  if (!aligned16(k) || !aligned16(v) || !aligned16(w) || !aligned16(uT))
+    return fail(KAIROS_GDN_EINVAL, "%s: k, v, w and uT must be 16-byte aligned", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  kgdn::PrepareArgs pa{};
+  pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
+  pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
+  pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = (int)G.N; pa.T = T; pa.H = (int)H;
+  pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = A; pa.Ai_out = Ai;
+  if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, k_dtype, (int)K, (int)V, G.nc, s), what)) return rc;
+  return ok();
+}
+
+int kairos_gdn_fwd_h(const void* k, const float* k_scale, const void* w, const void* uT, const float* gc,
+                     const void* initial_state, void* hT, void* vnT, float* final_state, const int64_t* cu_seqlens,
+                     int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int k_dtype, int v_dtype,
+                     int h0_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_fwd_h";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(k_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix k=%d v=%d", what, k_dtype, v_dtype);
+  if (initial_state && !valid_scalar_dt(h0_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: initial_state must be fp32 or bf16", what);
+  if (k_dtype == KAIROS_GDN_F8E4M3 && !k_scale) return fail(KAIROS_GDN_EINVAL, "%s: fp8 k needs k_scale", what);
+  if (workspace_bytes < stage_ws(n_seqs)) return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace too small", what);
+  if (G.nc > 0 && (!k || !w || !uT || !gc || !hT || !vnT))
+    return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  kgdn::FwdHArgs ha{};
+  ha.k = k; ha.k_scale = k_scale; ha.w = w; ha.uT = uT; ha.gc = gc;
+  ha.h0 = initial_state; ha.h0_dtype = h0_dtype;
+  ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = (int)G.N; ha.T = T; ha.H = (int)H;
+  ha.hT = hT; ha.vnT = vnT; ha.ht = final_state;
+  if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, k_dtype, (int)K, (int)V, s), what)) return rc;
+  return ok();
+}
+
+int kairos_gdn_fwd_o(const void* q, const void* k, const float* q_scale, const float* k_scale, const void* hT,
+                     const void* vnT, const float* gc, void* o, float scale, const int64_t* cu_seqlens,
+                     int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
+                     int v_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_fwd_o";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix q/k=%d v=%d", what, qk_dtype, v_dtype);
+  if (qk_dtype == KAIROS_GDN_F8E4M3 && (!q_scale || !k_scale))
+    return fail(KAIROS_GDN_EINVAL, "%s: fp8 q/k need q_scale and k_scale", what);
+  if (workspace_bytes < stage_ws(n_seqs)) return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace too small", what);
+  if (G.nc == 0) return ok();
+  if (!q || !k || !hT || !vnT || !gc || !o) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(hT) || !aligned16(vnT) || !aligned16(o))
+    return fail(KAIROS_GDN_EINVAL, "%s: q, k, hT, vnT and o must be 16-byte aligned", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  kgdn::FwdOArgs oa{};
+  oa.q = q; oa.k = k; oa.q_scale = q_scale; oa.k_scale = k_scale;
+  oa.hT = hT; oa.vnT = vnT; oa.gc = gc; oa.scale = scale;
+  oa.cu = cu_seqlens; oa.chunk_off = chunk_off; oa.N = (int)G.N; oa.T = T; oa.H = (int)H; oa.o = o;
+  if (int rc = from_launch(kgdn::launch_fwd_o(oa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), what)) return rc;
+  return ok();
+}
+
+int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream) {
+  const char* what = "kairos_gdn_l2norm_fwd";
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 512)
+    return fail(KAIROS_GDN_EINVAL, "%s: D must be a positive multiple of 8, at most 512", what);
+  if (!valid_scalar_dt(dtype)) return fail(KAIROS_GDN_EINVAL, "%s: dtype must be fp32 or bf16", what);
+  if (rows == 0) return ok();
+  if (!x || !y || !aligned16(x) || !aligned16(y))
+    return fail(KAIROS_GDN_EINVAL, "%s: x and y must be non-null and 16-byte aligned", what);
+  if (int rc = from_launch(kgdn::launch_l2norm(x, y, dtype, rows, (int)D, static_cast<hipStream_t>(stream)), what))
+    return rc;
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,262 @@
+// Shared device helpers for the gfx950 chunked GatedDeltaNet forward.
+//
+// Conventions used by every kernel in this directory:
+//  * One "chunk" is 64 consecutive tokens of one sequence (C = 64).
+//  * Matrix products run on the CDNA4 matrix cores with 16x16 output tiles:
+//      bf16: v_mfma_f32_16x16x32_bf16 (one instruction per 32-deep K step)
+//      fp32: eight v_mfma_f32_16x16x4f32 per 32-deep K step
+//    Lane l of a 64-wide wave holds, for a K step of 32,
+//      A fragment: A[row0 + l%16][k0 + 8*(l/16) + e], e = 0..7
+//      B fragment: B[k0 + 8*(l/16) + e][col0 + l%16], e = 0..7
+//      C/D tile  : D[row0 + 4*(l/16) + j][col0 + l%16], j = 0..3
+//    Any permutation of the K index is allowed as long as A and B use the
+//    same one; several kernels exploit that to feed accumulator tiles back
+//    as operands without a shuffle.
+//  * Operands staged in LDS are stored "K-contiguous": A as [m][k] and B as
+//    [n][k], padded by 8 elements per row, so one fragment is one 16-byte read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kgdn {
+
+constexpr int C = 64;        // chunk length (tokens)
+constexpr int WAVE = 64;     // CDNA wavefront width
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+
+// ---------------------------------------------------------------------------
+// element conversion
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+// float -> bf16 with round-to-nearest-even (the hardware conversion on gfx950).
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// Round a float to the storage precision T and back (identity for float).
+template <typename T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
+
+// OCP fp8 e4m3 ("fn") code -> float, exact: sign, 4-bit exponent (bias 7),
+// 3-bit mantissa, subnormals at exponent 0, code 0x7f/0xff is NaN.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint8_t c) {
+  const uint32_t e = (c >> 3) & 0xF, m = c & 0x7;
+  float mag;
+  if (e == 0) {
+    mag = (float)m * (1.0f / 512.0f);                // m/8 * 2^-6
+  } else {
+    mag = __uint_as_float(((e + 120u) << 23) | (m << 20));  // (1 + m/8) * 2^(e-7)
+  }
+  if (e == 15 && m == 7) mag = __uint_as_float(0x7fc00000u);
+  return (c & 0x80) ? -mag : mag;
+}
+
+// exp(x) via the native base-2 exponential (v_exp_f32): exp(x) = 2^(x*log2(e)).
+__device__ __forceinline__ float gexp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA fragments
+// ---------------------------------------------------------------------------
+template <typename T> struct Frag;
+template <> struct Frag<bf16> { bf16x8 v; };
+template <> struct Frag<float> { f32x4 lo, hi; };
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
+
+// Fragment of a K-contiguous LDS matrix: rows row0 + l%16, k = k0 + 8*(l/16) .. +7.
+template <typename T>
+__device__ __forceinline__ Frag<T> lds_frag(const T* base, int ld, int row0, int k0) {
+  const int l = lane_id();
+  const T* p = base + (row0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
+  Frag<T> f;
+  if constexpr (sizeof(T) == 2) {
+    f.v = *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    f.lo = *reinterpret_cast<const f32x4*>(p);
+    f.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return f;
+}
+
+// acc (16x16 fp32) += A(16x32) * B(32x16)
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<float>& a, const Frag<float>& b) {
+  // step e feeds k = 8*(l/16) + e from every lane group: the 8 steps cover the 32-deep slice.
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[0], b.lo[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[1], b.lo[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[2], b.lo[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[3], b.lo[3], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[0], b.hi[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[1], b.hi[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[2], b.hi[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[3], b.hi[3], acc, 0, 0, 0);
+}
+
+// fp32 16x16x16 product from LDS with arbitrary strides (used by the triangular
+// solve): acc += A[16x16] * B[16x16], A row-major (lda), B row-major (ldb).
+// Step q feeds k = 4*(l/16) + q, so A is read as one 16-byte row piece.
+__device__ __forceinline__ void mma16_f32_lds(f32x4& acc, const float* A, int lda, const float* B, int ldb) {
+  const int l = lane_id();
+  const int g = l >> 4, c = l & 15;
+  const f32x4 a = *reinterpret_cast<const f32x4*>(A + c * lda + 4 * g);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], B[(4 * g + q) * ldb + c], acc, 0, 0, 0);
+  }
+}
+
+// Same product with the B operand taken from a C-layout accumulator tile held
+// in registers (lane holds B[4*(l/16) + q][l%16] in b[q]).
+__device__ __forceinline__ void mma16_f32_lds_reg(f32x4& acc, const float* A, int lda, const f32x4& b) {
+  const int l = lane_id();
+  const int g = l >> 4, c = l & 15;
+  const f32x4 a = *reinterpret_cast<const f32x4*>(A + c * lda + 4 * g);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], b[q], acc, 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// vector memory helpers
+// ---------------------------------------------------------------------------
+template <typename T> struct Vec8;   // 8 elements = 16 bytes (bf16) or 32 bytes (fp32)
+template <> struct Vec8<bf16> { bf16x8 v; };
+template <> struct Vec8<float> { f32x4 lo, hi; };
+
+template <typename T>
+__device__ __forceinline__ Vec8<T> ld8(const T* p) {
+  Vec8<T> r;
+  if constexpr (sizeof(T) == 2) {
+    r.v = *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    r.lo = *reinterpret_cast<const f32x4*>(p);
+    r.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const Vec8<T>& x) {
+  if constexpr (sizeof(T) == 2) {
+    *reinterpret_cast<bf16x8*>(p) = x.v;
+  } else {
+    *reinterpret_cast<f32x4*>(p) = x.lo;
+    *reinterpret_cast<f32x4*>(p + 4) = x.hi;
+  }
+}
+template <typename T> __device__ __forceinline__ float vget(const Vec8<T>& x, int e);
+template <> __device__ __forceinline__ float vget<bf16>(const Vec8<bf16>& x, int e) { return (float)x.v[e]; }
+template <> __device__ __forceinline__ float vget<float>(const Vec8<float>& x, int e) { return e < 4 ? x.lo[e] : x.hi[e - 4]; }
+template <typename T> __device__ __forceinline__ void vset(Vec8<T>& x, int e, float val);
+template <> __device__ __forceinline__ void vset<bf16>(Vec8<bf16>& x, int e, float val) { x.v[e] = (bf16)val; }
+template <> __device__ __forceinline__ void vset<float>(Vec8<float>& x, int e, float val) {
+  if (e < 4) x.lo[e] = val; else x.hi[e - 4] = val;
+}
+template <typename T>
+__device__ __forceinline__ Vec8<T> vzero() {
+  Vec8<T> r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) vset<T>(r, e, 0.0f);
+  return r;
+}
+
+// 4 consecutive storage elements from 4 floats (one C-layout column piece).
+template <typename T>
+__device__ __forceinline__ void st4(T* p, float a, float b, float c, float d) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x4 v = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+    *reinterpret_cast<bf16x4*>(p) = v;
+  } else {
+    f32x4 v = {a, b, c, d};
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
+template <typename T>
+__device__ __forceinline__ f32x4 ld4(const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    f32x4 r = {(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    return r;
+  } else {
+    return *reinterpret_cast<const f32x4*>(p);
+  }
+}
+
+// Load 8 consecutive q/k input elements (fp32, bf16 or fp8 e4m3 times a scale) as floats.
+template <typename TK>
+__device__ __forceinline__ void load8_in(const TK* p, float scale, float out[8]) {
+  if constexpr (sizeof(TK) == 1) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = fp8e4m3_to_f32((raw.x >> (8 * e)) & 0xFF) * scale;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[4 + e] = fp8e4m3_to_f32((raw.y >> (8 * e)) & 0xFF) * scale;
+  } else {
+    const Vec8<TK> x = ld8<TK>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = vget<TK>(x, e);
+  }
+}
+
+// Load one scalar of a runtime-typed per-token array (g, beta): 0 = fp32, 1 = bf16.
+__device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
+  return dt == 0 ? reinterpret_cast<const float*>(p)[i] : (float)reinterpret_cast<const bf16*>(p)[i];
+}
+
+// ---------------------------------------------------------------------------
+// sequence / chunk addressing
+// ---------------------------------------------------------------------------
+// Chunks of all sequences are numbered 0..NC-1 in order (sequence-major).
+// Fixed-length batches: sequence n covers tokens [n*T, n*T + T).
+// Varlen: sequence n covers [cu[n], cu[n+1]) and chunk_off[n] is the index
+// of its first chunk (chunk_off has N+1 entries; chunk_off[N] = NC).
+struct ChunkLoc {
+  int64_t bos;     // first token of the sequence (flattened B*T axis)
+  int64_t t0;      // first token of the chunk
+  int n;           // sequence index
+  int nv;          // valid rows in this chunk (1..64)
+  bool ok;
+};
+
+__device__ __forceinline__ ChunkLoc locate_chunk(int64_t c, const int64_t* cu, const int32_t* chunk_off,
+                                                 int N, int64_t T) {
+  ChunkLoc L;
+  L.ok = false;
+  if (cu == nullptr) {
+    const int64_t nt = (T + C - 1) / C;
+    if (c >= nt * N) return L;
+    L.n = (int)(c / nt);
+    const int64_t it = c % nt;
+    L.bos = (int64_t)L.n * T;
+    L.t0 = L.bos + it * C;
+    L.nv = (int)min((int64_t)C, T - it * C);
+    L.ok = true;
+    return L;
+  }
+  if (c >= chunk_off[N]) return L;
+  int lo = 0, hi = N - 1;              // last n with chunk_off[n] <= c
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (chunk_off[mid] <= c) lo = mid; else hi = mid - 1;
+  }
+  L.n = lo;
+  L.bos = cu[lo];
+  const int64_t it = c - chunk_off[lo];
+  L.t0 = L.bos + it * C;
+  L.nv = (int)min((int64_t)C, cu[lo + 1] - L.t0);
+  L.ok = true;
+  return L;
+}
+
+}  // namespace kgdn

@@ -1,0 +1,294 @@
+// Serial inter-chunk state recurrence of the chunked GatedDeltaNet forward
+// (fla ops/common/chunk_delta_h.py:52-224).  For each (sequence, head,
+// 16-column slice of V) one workgroup walks the chunks in order:
+//
+//   hT[c]  = S (stored, before the update)               chunk_delta_h.py:129-139
+//   v'     = u_c - w_c @ S_stored                        :141-157
+//   vnT[c] = v' (stored, ungated)                         :159-161
+//   S      = exp(g_last) S + k_c^T (v' exp(g_last - gc)) :163-211
+//   ht     = S after the last chunk (fp32)               :213-224
+//
+// The fp32 state slice S[K x 16] stays in VGPRs for the whole sequence, in the
+// MFMA accumulator layout, split over the waves along K (each wave owns KW
+// rows).  The accumulator tile is fed back as the B operand of w @ S without
+// a shuffle: the K index of a 32-deep step is permuted the same way in the w
+// fragment (two 4-element pieces per lane).  Partial w @ S products of the
+// waves are summed through LDS; the gated v' goes through LDS once more as the
+// B operand of the rank-64 update.  Everything the next chunk needs (w, k, u,
+// gc) is prefetched into registers while the current chunk computes.
+#include "gdn_common.hpp"
+#include "gdn_kernels.h"
+
+namespace kgdn {
+
+namespace {
+
+constexpr int BV = 16;     // V columns per workgroup
+constexpr int LDT = C + 8; // row stride of the [*][64] LDS tiles
+
+template <int K> struct HCfg {
+  static constexpr int NW = K == 64 ? 2 : 4;   // waves
+  static constexpr int KW = K / NW;            // state rows per wave
+  static constexpr int KT = KW / 16;           // 16-row accumulator tiles per wave
+  static constexpr int KS = KW / 32;           // 32-deep K steps per wave
+  static constexpr int OWN = 4 / NW;           // 16-row tiles of v' reduced by each wave
+};
+
+template <typename TC> struct Half;             // 4 storage elements (8 B bf16 / 16 B fp32)
+template <> struct Half<bf16> { bf16x4 v; };
+template <> struct Half<float> { f32x4 v; };
+
+template <typename TC>
+__device__ __forceinline__ Half<TC> ld_half(const TC* p) {
+  Half<TC> r;
+  if constexpr (sizeof(TC) == 2) r.v = *reinterpret_cast<const bf16x4*>(p);
+  else r.v = *reinterpret_cast<const f32x4*>(p);
+  return r;
+}
+template <typename TC>
+__device__ __forceinline__ Half<TC> zero_half() {
+  Half<TC> r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r.v[e] = (TC)0.f;
+  return r;
+}
+template <typename TC>
+__device__ __forceinline__ Frag<TC> join(const Half<TC>& a, const Half<TC>& b) {
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    f.v = __builtin_shufflevector(a.v, b.v, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    f.lo = a.v;
+    f.hi = b.v;
+  }
+  return f;
+}
+template <typename TC>
+__device__ __forceinline__ Frag<TC> frag_from_acc(const f32x4& a, const f32x4& b) {
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    bf16x8 v = {(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3], (bf16)b[0], (bf16)b[1], (bf16)b[2], (bf16)b[3]};
+    f.v = v;
+  } else {
+    f.lo = a;
+    f.hi = b;
+  }
+  return f;
+}
+
+template <typename TC, typename TK, int K>
+struct ChunkPrefetch {
+  using Cfg = HCfg<K>;
+  Frag<TC> wf[4][Cfg::KS];      // A fragments of w for the 4 row tiles
+  Vec8<TC> krow[Cfg::KW / 8];   // k[t = lane][wave's K slice]
+  f32x4 uv[Cfg::OWN];           // u (C layout) of the owned row tiles
+  f32x4 gv[Cfg::OWN];           // gc of the owned rows
+  float gl;                     // gc of the last valid row
+  int64_t t0;
+  int nv;
+};
+
+template <typename TC, typename TK, int K>
+__device__ __forceinline__ void prefetch_chunk(ChunkPrefetch<TC, TK, K>& P, const FwdHArgs& a, int64_t c,
+                                               int64_t t0, int nv, int h, int v0, int wid, int V) {
+  using Cfg = HCfg<K>;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int H = a.H;
+  P.t0 = t0;
+  P.nv = nv;
+  const TC* w = reinterpret_cast<const TC*>(a.w);
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) {
+    const int t = 16 * tm + lc;
+#pragma unroll
+    for (int ks = 0; ks < Cfg::KS; ++ks) {
+      if (t < nv) {
+        const TC* p = w + ((t0 + t) * H + h) * K + Cfg::KW * wid + 32 * ks + 4 * lg;
+        P.wf[tm][ks] = join<TC>(ld_half<TC>(p), ld_half<TC>(p + 16));
+      } else {
+        P.wf[tm][ks] = join<TC>(zero_half<TC>(), zero_half<TC>());
+      }
+    }
+  }
+  const TK* k = reinterpret_cast<const TK*>(a.k);
+  const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
+#pragma unroll
+  for (int d8 = 0; d8 < Cfg::KW / 8; ++d8) {
+    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (l < nv) load8_in<TK>(k + ((t0 + l) * H + h) * K + Cfg::KW * wid + 8 * d8, ks_, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vset<TC>(P.krow[d8], e, x[e]);
+  }
+  const TC* uT = reinterpret_cast<const TC*>(a.uT) + ((c * H + h) * V + v0 + lc) * C;
+#pragma unroll
+  for (int o = 0; o < Cfg::OWN; ++o) {
+    const int tm = wid + Cfg::NW * o;
+    P.uv[o] = ld4<TC>(uT + 16 * tm + 4 * lg);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tm + 4 * lg + j;
+      P.gv[o][j] = t < nv ? a.gc[(t0 + t) * H + h] : 0.f;
+    }
+  }
+  P.gl = a.gc[(t0 + nv - 1) * H + h];
+}
+
+template <typename TC, typename TK, int K>
+__global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int V, int total_units) {
+  using Cfg = HCfg<K>;
+  constexpr int NW = Cfg::NW, KW = Cfg::KW, KT = Cfg::KT, KS = Cfg::KS, OWN = Cfg::OWN;
+  __shared__ __align__(16) f32x4 s_red[NW][4][WAVE];
+  __shared__ __align__(16) TC s_vgT[BV * LDT];
+  __shared__ __align__(16) TC s_kT[NW][KW * LDT];
+
+  // XCD-aware unit order: consecutive work items share an XCD (and its L2),
+  // so the V slices of one head read w and k through the same cache.
+  const int per_xcd = gridDim.x / 8;
+  const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (o_idx >= total_units) return;
+  const int nvt = V / BV;
+  const int unit = o_idx / nvt;
+  const int v0 = (o_idx % nvt) * BV;
+  const int H = a.H;
+  const int n = unit / H, h = unit % H;
+
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+
+  int64_t bos, eos, c_first;
+  if (a.cu == nullptr) {
+    bos = (int64_t)n * a.T;
+    eos = bos + a.T;
+    c_first = (int64_t)n * ((a.T + C - 1) / C);
+  } else {
+    bos = a.cu[n];
+    eos = a.cu[n + 1];
+    c_first = a.chunk_off[n];
+  }
+  const int64_t nchunks = (eos - bos + C - 1) / C;
+
+  // state slice: rows KW*wid + 16*tt + 4*lg + j, column v0 + lc
+  f32x4 S[KT];
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x = 0.f;
+      if (a.h0) {
+        const int64_t off = (((int64_t)n * H + h) * K + KW * wid + 16 * tt + 4 * lg + j) * V + v0 + lc;
+        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
+                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
+      }
+      S[tt][j] = x;
+    }
+  }
+
+  ChunkPrefetch<TC, TK, K> cur, nxt;
+  if (nchunks > 0) prefetch_chunk<TC, TK, K>(cur, a, c_first, bos, (int)min((int64_t)C, eos - bos), h, v0, wid, V);
+
+  TC* hT = reinterpret_cast<TC*>(a.hT);
+  TC* vnT = reinterpret_cast<TC*>(a.vnT);
+  TC* kT = s_kT[wid];
+
+  for (int64_t it = 0; it < nchunks; ++it) {
+    const int64_t c = c_first + it;
+    if (it + 1 < nchunks) {
+      const int64_t t1 = bos + (it + 1) * C;
+      prefetch_chunk<TC, TK, K>(nxt, a, c + 1, t1, (int)min((int64_t)C, eos - t1), h, v0, wid, V);
+    }
+    const int nv = cur.nv;
+
+    // snapshot of the state before this chunk
+    TC* hrow = hT + ((c * H + h) * V + v0 + lc) * K + KW * wid + 4 * lg;
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) st4<TC>(hrow + 16 * tt, S[tt][0], S[tt][1], S[tt][2], S[tt][3]);
+
+    // partial w @ S over this wave's K slice
+    Frag<TC> hb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) hb[ks] = frag_from_acc<TC>(S[2 * ks], S[2 * ks + 1]);
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) mma(acc, cur.wf[tm][ks], hb[ks]);
+      s_red[wid][tm][l] = acc;
+    }
+    __syncthreads();
+
+    // k^T slice of this wave (read only by this wave, in the update below: t = lane)
+#pragma unroll
+    for (int d8 = 0; d8 < KW / 8; ++d8) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kT[(8 * d8 + e) * LDT + l] = from_f32<TC>(vget<TC>(cur.krow[d8], e));
+    }
+
+    // v' = u - w @ S for the owned row tiles; store v_new; gate into LDS
+    TC* vrow = vnT + ((c * H + h) * V + v0 + lc) * C;
+#pragma unroll
+    for (int o = 0; o < OWN; ++o) {
+      const int tm = wid + NW * o;
+      f32x4 vp = cur.uv[o];
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) vp -= s_red[w2][tm][l];
+      st4<TC>(vrow + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
+      float vg[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tm + 4 * lg + j;
+        vg[j] = t < nv ? vp[j] * gexp(cur.gl - cur.gv[o][j]) : 0.f;
+      }
+      st4<TC>(s_vgT + lc * LDT + 16 * tm + 4 * lg, vg[0], vg[1], vg[2], vg[3]);
+    }
+    __syncthreads();
+
+    // S = exp(g_last) S + k^T (v' gated)
+    const float eg = gexp(cur.gl);
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      S[tt] *= eg;
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2)
+        mma(S[tt], lds_frag<TC>(kT, LDT, 16 * tt, 32 * ks2), lds_frag<TC>(s_vgT, LDT, 0, 32 * ks2));
+    }
+    cur = nxt;
+  }
+
+  if (a.ht) {
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (((int64_t)n * H + h) * K + KW * wid + 16 * tt + 4 * lg + j) * V + v0 + lc;
+        a.ht[off] = S[tt][j];
+      }
+    }
+  }
+}
+
+template <typename TC, typename TK, int K>
+int launch_fwd_h_t(const FwdHArgs& a, int V, hipStream_t s) {
+  const int total = a.N * a.H * (V / BV);
+  const int grid = (total + 7) / 8 * 8;
+  hipLaunchKernelGGL((fwd_h_kernel<TC, TK, K>), dim3(grid), dim3(64 * HCfg<K>::NW), 0, s, a, V, total);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V, hipStream_t s) {
+  if (V % BV != 0 || a.N * a.H == 0) return -2;
+#define KGDN_H_CASE(TC, TK, KK) \
+  if (K == KK) return launch_fwd_h_t<TC, TK, KK>(a, V, s);
+  if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_H_CASE(float, float, 64) KGDN_H_CASE(float, float, 128) }
+  if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_H_CASE(bf16, bf16, 64) KGDN_H_CASE(bf16, bf16, 128) }
+  if (compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) {
+    KGDN_H_CASE(bf16, uint8_t, 64) KGDN_H_CASE(bf16, uint8_t, 128)
+  }
+#undef KGDN_H_CASE
+  return -2;
+}
+
+}  // namespace kgdn

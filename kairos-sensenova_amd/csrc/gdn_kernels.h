@@ -1,0 +1,88 @@
+// Internal launch interface between the C-ABI layer (gdn_api.hip) and the
+// kernel translation units.  Plain C++ structs of device pointers; no torch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kgdn {
+
+enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F8E4M3 = 2 };
+
+// Shared addressing: fixed-length batches use (cu == nullptr, N = B, T = per-sequence
+// length); varlen uses cu [N+1] (int64 token offsets) and chunk_off [N+1] (int32).
+struct SeqArgs {
+  const int64_t* cu;
+  const int32_t* chunk_off;
+  int N;
+  int64_t T;
+  int H;
+};
+
+struct PrepareArgs {
+  const void* k;          // [B*T, H, K]  k_dtype
+  const void* v;          // [B*T, H, V]  compute dtype
+  const void* g;          // [B*T, H]     g_dtype (0 fp32, 1 bf16)
+  const void* beta;       // [B*T, H]     beta_dtype
+  const float* k_scale;   // [H] dequant scale for fp8 k, else nullptr
+  int g_dtype, beta_dtype;
+  const int64_t* cu;
+  const int32_t* chunk_off;
+  int N;
+  int64_t T;
+  int H;
+  float* gc;              // out [B*T, H] fp32
+  void* w;                // out [B*T, H, K]
+  void* uT;               // out [NC, H, V, 64]
+  float* A_out;           // optional out [B*T, H, 64] fp32
+  void* Ai_out;           // optional out [B*T, H, 64]
+};
+
+struct FwdHArgs {
+  const void* k;          // [B*T, H, K]  (k_dtype)
+  const float* k_scale;   // [H] or nullptr
+  const void* w;          // [B*T, H, K]
+  const void* uT;         // [NC, H, V, 64]
+  const float* gc;        // [B*T, H]
+  const void* h0;         // [N, H, K, V] (h0_dtype) or nullptr
+  int h0_dtype;
+  const int64_t* cu;
+  const int32_t* chunk_off;
+  int N;
+  int64_t T;
+  int H;
+  void* hT;               // out [NC, H, V, K] state snapshots (before each chunk)
+  void* vnT;              // out [NC, H, V, 64] ungated v_new
+  float* ht;              // out [N, H, K, V] fp32 or nullptr
+};
+
+struct FwdOArgs {
+  const void* q;          // [B*T, H, K]  (qk_dtype)
+  const void* k;
+  const float* q_scale;   // [H] or nullptr
+  const float* k_scale;
+  const void* hT;         // [NC, H, V, K]
+  const void* vnT;        // [NC, H, V, 64]
+  const float* gc;        // [B*T, H]
+  float scale;
+  const int64_t* cu;
+  const int32_t* chunk_off;
+  int N;
+  int64_t T;
+  int H;
+  void* o;                // out [B*T, H, V] compute dtype
+};
+
+// Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported
+// (dtype, K, V) combination.
+int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, int V, int64_t nc_grid,
+                   hipStream_t s);
+int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V, hipStream_t s);
+int launch_fwd_o(const FwdOArgs& a, int compute_dtype, int qk_dtype, int K, int V, int64_t nc_grid,
+                 hipStream_t s);
+int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s);
+int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s);
+int launch_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu, const int32_t* chunk_off, int N,
+                  int64_t T, int H, int64_t nc_grid, hipStream_t s);
+
+}  // namespace kgdn

@@ -1,0 +1,272 @@
+// Chunk-parallel "prepare" stage of the chunked GatedDeltaNet forward, one
+// workgroup (4 waves) per (chunk, head):
+//   gc  = per-chunk prefix sum of g                 (fla ops/utils/cumsum.py:27-65)
+//   A   = beta_i exp(gc_i - gc_j) k_i.k_j, i > j    (ops/common/chunk_scaled_dot_kkt.py:57-73)
+//   Ai  = (I + A)^-1, fp32 in LDS, stored rounded   (ops/utils/solve_tril.py:184-331)
+//   w   = Ai (k beta exp(gc)),  u = Ai (v beta)     (ops/gated_delta_rule/wy_fast.py:55-81)
+// The reference runs these as four kernels with fp32 A and the Ai round trip
+// through HBM; here they are one pass that reads k, v, g, beta once and
+// writes gc, w and u (A / Ai only when a test asks for them).
+//
+// Output layouts: gc [B*T, H] fp32; w [B*T, H, K] (token-major, as the
+// reference); u per chunk transposed, uT [NC, H, V, 64], which is the
+// K-contiguous operand layout the state kernel reads.
+#include "gdn_common.hpp"
+#include "gdn_kernels.h"
+
+namespace kgdn {
+
+namespace {
+
+constexpr int NT_PREP = 256;   // 4 waves
+
+template <typename TC, int K, int V>
+struct PrepLds {
+  static constexpr int LDK = K + 8;      // s_k row stride (elements)
+  static constexpr int LDT = C + 8;      // transposed tiles / Ai row stride
+  static constexpr int LDA = C + 4;      // fp32 A / inverse row stride
+  static constexpr size_t k_bytes = sizeof(TC) * C * LDK;
+  static constexpr size_t ai_bytes = sizeof(TC) * C * LDT;
+  static constexpr size_t region0 = k_bytes > ai_bytes ? k_bytes : ai_bytes;   // s_k, later s_Ai
+  static constexpr size_t off_kbT = (region0 + 15) / 16 * 16;
+  static constexpr size_t off_vbT = off_kbT + sizeof(TC) * K * LDT;
+  static constexpr size_t off_A = off_vbT + sizeof(TC) * V * LDT;
+  static constexpr size_t off_g = off_A + sizeof(float) * C * LDA;
+  static constexpr size_t total = off_g + sizeof(float) * 3 * C;
+};
+
+template <typename TC, typename TK, int K, int V>
+__global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a) {
+  using L = PrepLds<TC, K, V>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  TC* s_k = reinterpret_cast<TC*>(smem);
+  TC* s_Ai = reinterpret_cast<TC*>(smem);                 // aliases s_k once K.K^T is done
+  TC* s_kbT = reinterpret_cast<TC*>(smem + L::off_kbT);
+  TC* s_vbT = reinterpret_cast<TC*>(smem + L::off_vbT);
+  float* s_A = reinterpret_cast<float*>(smem + L::off_A);
+  float* s_g = reinterpret_cast<float*>(smem + L::off_g);
+  float* s_eg = s_g + C;
+  float* s_b = s_g + 2 * C;
+
+  const int h = blockIdx.y;
+  const int H = a.H;
+  const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
+  if (!loc.ok) return;
+  const int64_t t0 = loc.t0;
+  const int nv = loc.nv;
+  const int tid = threadIdx.x;
+  const int wid = tid / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+
+  // ---- gates: chunk-local cumsum of g (one wave, inclusive scan over 64 lanes)
+  if (wid == 0) {
+    float gv = 0.f, bv = 0.f;
+    if (l < nv) {
+      gv = ld_scalar(a.g, (t0 + l) * H + h, a.g_dtype);
+      bv = ld_scalar(a.beta, (t0 + l) * H + h, a.beta_dtype);
+    }
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+      const float o = __shfl_up(gv, off, WAVE);
+      if (l >= off) gv += o;
+    }
+    s_g[l] = gv;
+    s_eg[l] = gexp(gv);
+    s_b[l] = bv;
+    if (l < nv) a.gc[(t0 + l) * H + h] = gv;
+  }
+  __syncthreads();
+
+  // ---- stage k (row-major, for K.K^T) and the transposed, scaled operands
+  //      kb^T[d][t] = k*beta*exp(gc), vb^T[v][t] = v*beta
+  const float kscale = a.k_scale ? a.k_scale[h] : 1.f;
+  const TK* kin = reinterpret_cast<const TK*>(a.k);
+  for (int idx = tid; idx < C * (K / 8); idx += NT_PREP) {
+    const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+    float x[8];
+    if (r < nv) {
+      load8_in<TK>(kin + ((t0 + r) * H + h) * K + c8, kscale, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+    Vec8<TC> row;
+    const float b = s_b[r], eg = s_eg[r];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float kv = round_to<TC>(x[e]);                 // stored k (fp8 input: dequantised)
+      vset<TC>(row, e, kv);
+      float kb = kv * b;
+      if (a.beta_dtype == 1) kb = round_to<TC>(kb);       // bf16*bf16 -> bf16 (wy_fast.py:77)
+      s_kbT[(c8 + e) * L::LDT + r] = from_f32<TC>(kb * eg);
+    }
+    st8<TC>(s_k + r * L::LDK + c8, row);
+  }
+  const TC* vin = reinterpret_cast<const TC*>(a.v);
+  for (int idx = tid; idx < C * (V / 8); idx += NT_PREP) {
+    const int r = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
+    Vec8<TC> x = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + c8) : vzero<TC>();
+    const float b = s_b[r];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_vbT[(c8 + e) * L::LDT + r] = from_f32<TC>(vget<TC>(x, e) * b);
+  }
+  __syncthreads();
+
+  // ---- A = beta exp(dg) K K^T, strictly lower (10 lower 16x16 tiles over 4 waves)
+  for (int tile = wid; tile < 10; tile += 4) {
+    const int tm = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
+    const int tn = tile - tm * (tm + 1) / 2;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks)
+      mma(acc, lds_frag<TC>(s_k, L::LDK, 16 * tm, 32 * ks), lds_frag<TC>(s_k, L::LDK, 16 * tn, 32 * ks));
+    const int j = 16 * tn + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int i = 16 * tm + 4 * lg + jj;
+      float val = 0.f;
+      if (i > j && i < nv) val = acc[jj] * gexp(s_g[i] - s_g[j]) * s_b[i];
+      s_A[i * L::LDA + j] = val;
+    }
+  }
+  __syncthreads();
+
+  if (a.A_out) {   // optional fp32 A, [B*T, H, 64] (test hook)
+    for (int idx = tid; idx < nv * C; idx += NT_PREP) {
+      const int i = idx / C, j = idx % C;
+      a.A_out[((t0 + i) * H + h) * C + j] = j < i ? s_A[i * L::LDA + j] : 0.f;
+    }
+    __syncthreads();
+  }
+
+  // ---- (I + A)^-1: invert the four 16x16 diagonal blocks by forward substitution
+  //      (wave 0; lane = one column of one block), overwriting the diagonal blocks.
+  {
+    float x[16];
+    float* Xb = s_A + (16 * lg) * L::LDA + 16 * lg;
+    if (wid == 0) {
+      const int c = lc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < i; ++r) s = fmaf(Xb[i * L::LDA + r], x[r], s);
+        x[i] = (i == c) ? 1.f : (i < c ? 0.f : -s);
+      }
+    }
+    __syncthreads();   // all reads of the diagonal blocks are done before they are overwritten
+    if (wid == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Xb[i * L::LDA + lc] = x[i];
+    }
+  }
+  __syncthreads();
+
+  // ---- block merges (fp32 MFMA), X_ij = -X_ii sum_k L_ik X_kj; X_ij (i > j) is
+  //      kept in the unused upper block (j, i) so L stays intact for later levels.
+  auto blk = [&](int i, int j) { return s_A + (16 * i) * L::LDA + 16 * j; };
+  auto put_neg = [&](float* dst, const f32x4& r) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) dst[(4 * lg + jj) * L::LDA + lc] = -r[jj];
+  };
+  if (wid < 3) {                                  // X_{w+1,w}
+    const int i = wid + 1, j = wid;
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
+    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
+    put_neg(blk(j, i), r);
+  }
+  __syncthreads();
+  if (wid < 2) {                                  // X_{w+2,w}
+    const int i = wid + 2, j = wid;
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
+    mma16_f32_lds(t, blk(i, j + 1), L::LDA, blk(j, j + 1), L::LDA);      // L_{i,j+1} X_{j+1,j}
+    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
+    put_neg(blk(j, i), r);
+  }
+  __syncthreads();
+  if (wid == 0) {                                 // X_{3,0}
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(3, 0), L::LDA, blk(0, 0), L::LDA);
+    mma16_f32_lds(t, blk(3, 1), L::LDA, blk(0, 1), L::LDA);               // L_31 X_10
+    mma16_f32_lds(t, blk(3, 2), L::LDA, blk(0, 2), L::LDA);               // L_32 X_20
+    mma16_f32_lds_reg(r, blk(3, 3), L::LDA, t);
+    put_neg(blk(0, 3), r);
+  }
+  __syncthreads();
+
+  // ---- Ai (rounded to the storage type) into LDS as the K-contiguous [t][s] operand
+  for (int idx = tid; idx < C * C; idx += NT_PREP) {
+    const int i = idx / C, j = idx % C;
+    const int bi = i >> 4, bj = j >> 4;
+    float x = 0.f;
+    if (bi == bj) x = s_A[i * L::LDA + j];
+    else if (bi > bj) x = s_A[(16 * bj + (i & 15)) * L::LDA + 16 * bi + (j & 15)];
+    const TC xs = from_f32<TC>(x);
+    s_Ai[i * L::LDT + j] = xs;
+    if (a.Ai_out && i < nv) reinterpret_cast<TC*>(a.Ai_out)[((t0 + i) * H + h) * C + j] = xs;
+  }
+  __syncthreads();
+
+  // ---- w^T = kb^T Ai^T  (rows d, cols t) -> token-major w, 4 consecutive d per lane
+  TC* w_out = reinterpret_cast<TC*>(a.w);
+  for (int tm = wid; tm < K / 16; tm += 4) {
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks <= tn / 2; ++ks)
+        mma(acc, lds_frag<TC>(s_kbT, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_Ai, L::LDT, 16 * tn, 32 * ks));
+      const int t = 16 * tn + lc;
+      if (t < nv) st4<TC>(w_out + ((t0 + t) * H + h) * K + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
+    }
+  }
+  // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane
+  TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
+  for (int tn = wid; tn < V / 16; tn += 4) {
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks <= tm / 2; ++ks)
+        mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_vbT, L::LDT, 16 * tn, 32 * ks));
+      st4<TC>(uT + (16 * tn + lc) * C + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
+    }
+  }
+}
+
+template <typename TC, typename TK, int K, int V>
+int launch_prepare_t(const PrepareArgs& a, int64_t nc_grid, hipStream_t s) {
+  using L = PrepLds<TC, K, V>;
+  static_assert(L::total <= 160 * 1024, "prepare tile does not fit in LDS");
+  auto kern = prepare_kernel<TC, TK, K, V>;
+  if (L::total > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)L::total) != hipSuccess)
+      return -1;
+  }
+  dim3 grid((unsigned)nc_grid, (unsigned)a.H);
+  hipLaunchKernelGGL(kern, grid, dim3(NT_PREP), L::total, s, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, int V, int64_t nc_grid,
+                   hipStream_t s) {
+#define KGDN_PREP_CASE(TC, TK, KK, VV) \
+  if (K == KK && V == VV) return launch_prepare_t<TC, TK, KK, VV>(a, nc_grid, s);
+#define KGDN_PREP_SHAPES(TC, TK) \
+  KGDN_PREP_CASE(TC, TK, 64, 64) KGDN_PREP_CASE(TC, TK, 64, 128) \
+  KGDN_PREP_CASE(TC, TK, 128, 64) KGDN_PREP_CASE(TC, TK, 128, 128)
+  if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_PREP_SHAPES(float, float) }
+  if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_PREP_SHAPES(bf16, bf16) }
+  if (compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) { KGDN_PREP_SHAPES(bf16, uint8_t) }
+#undef KGDN_PREP_SHAPES
+#undef KGDN_PREP_CASE
+  return -2;
+}
+
+}  // namespace kgdn

@@ -1,0 +1,309 @@
+"""Host side of the MI355X chunked GatedDeltaNet forward.
+
+``chunk_gated_delta_rule`` keeps the signature, argument meaning, defaults and
+error behaviour of the reference entry point
+(kairos/third_party/fla/ops/gated_delta_rule/chunk.py:217-323) and runs the
+forward through the HIP kernels of libkairos_gdn.so.  PyTorch only provides
+device memory and the current stream.  There is no other compute path: on a
+machine without the library or a HIP device every call raises.
+
+The stage functions below (``chunk_local_cumsum``, ``prepare_wy``, ``fwd_h``,
+``fwd_o``, ``l2norm_fwd``) expose the individual kernels with the reference's
+stage semantics, for parity tests and for callers that compose stages.
+"""
+from __future__ import annotations
+
+import warnings
+
+import torch
+
+from . import _lib
+
+CHUNK = 64
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+_FP8 = getattr(torch, "float8_e4m3fn", None)
+if _FP8 is not None:
+    _DTYPES[_FP8] = _lib.F8E4M3
+
+
+def _code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: unsupported dtype {t.dtype} (fp32, bf16, or fp8 e4m3 for q/k)") from None
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "kairos_gdn runs on a HIP device only (tensor on %s); there is no CPU path" % t.device)
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"all tensors must be on one device ({dev} vs {t.device})")
+    return dev
+
+
+_validated_cu: tuple | None = None
+
+
+def _prepare_cu_seqlens(cu_seqlens: torch.Tensor, device: torch.device, T: int) -> torch.Tensor:
+    """int64 device copy of cu_seqlens, checked once per tensor object.
+
+    The reference reads cu_seqlens on the host as well (prepare_chunk_indices
+    calls .tolist(), fla/ops/utils/index.py:118, cached by identity in
+    fla/utils.py:96-133); the same single check here guards the kernels
+    against offsets outside [0, T].
+    """
+    global _validated_cu
+    cu = cu_seqlens
+    if cu.dim() != 1 or cu.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor with at least two entries")
+    if _validated_cu is None or _validated_cu[0] is not cu_seqlens or _validated_cu[1] != T:
+        vals = cu.detach().to("cpu", torch.int64)
+        if int(vals[0]) != 0 or int(vals[-1]) != T or bool((vals[1:] < vals[:-1]).any()):
+            raise ValueError(
+                f"cu_seqlens must start at 0, end at T={T} and be non-decreasing (got {vals.tolist()[:8]}...)")
+        _validated_cu = (cu_seqlens, T)
+    return cu.to(device=device, dtype=torch.int64).contiguous()
+
+
+def _scales(q_scale, k_scale, H, device, fp8: bool):
+    if not fp8:
+        return None, None
+    if q_scale is None or k_scale is None:
+        raise ValueError("fp8 q/k need per-head q_scale and k_scale of shape [H]")
+    qs = q_scale.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    ks = k_scale.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if qs.numel() != H or ks.numel() != H:
+        raise ValueError(f"q_scale / k_scale must have H={H} entries")
+    return qs, ks
+
+
+def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens=None,
+                               use_qk_l2norm_in_kernel=False, q_scale=None, k_scale=None):
+    """One native call: [q/k L2 norm] -> prepare -> state recurrence -> output.
+
+    Mirrors chunk_gated_delta_rule_fwd (chunk.py:16-67) plus the optional
+    in-kernel L2 norm of ChunkGatedDeltaRuleFunction.forward (chunk.py:168-170).
+    Returns (o in v's dtype, final_state fp32 or None).
+    """
+    dev = _require_device(q, k, v, g, beta, initial_state)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if k.shape != q.shape or v.shape[:3] != (B, T, H) or g.shape != (B, T, H) or beta.shape != (B, T, H):
+        raise ValueError(
+            f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}, g {tuple(g.shape)}, "
+            f"beta {tuple(beta.shape)}")
+    if k.dtype != q.dtype:
+        raise TypeError("q and k must share a dtype")
+    qk_dt, v_dt = _code(q, "q"), _code(v, "v")
+    g_dt, b_dt = _code(g, "g"), _code(beta, "beta")
+    fp8 = qk_dt == _lib.F8E4M3
+    qs, ks = _scales(q_scale, k_scale, H, dev, fp8)
+    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
+    n_seqs, cu = 0, None
+    if cu_seqlens is not None:
+        cu = _prepare_cu_seqlens(cu_seqlens, dev, T)
+        n_seqs = cu.numel() - 1
+    N = n_seqs if cu is not None else B
+    h0, h0_dt = None, _lib.F32
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (N, H, K, V):
+            raise ValueError(f"initial_state must have shape {(N, H, K, V)}, got {tuple(initial_state.shape)}")
+        h0 = initial_state
+        if h0.dtype not in (torch.float32, torch.bfloat16):
+            h0 = h0.float()
+        h0 = h0.contiguous()
+        h0_dt = _code(h0, "initial_state")
+    o = torch.empty_like(v)
+    ht = torch.empty(N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, qk_dt, v_dt,
+                                                       int(bool(use_qk_l2norm_in_kernel)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("kairos_gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(qs), _ptr(ks),
+              _ptr(h0), _ptr(o), _ptr(ht), _ptr(cu), n_seqs, B, T, H, K, V, qk_dt, v_dt, g_dt, b_dt, h0_dt,
+              float(scale), int(bool(use_qk_l2norm_in_kernel)), _ptr(ws), ws_bytes, _stream(dev))
+    return o, ht
+
+
+class ChunkGatedDeltaRuleFunction(torch.autograd.Function):
+    """Forward-only autograd wrapper (the reference's is chunk.py:149-213).
+
+    The backward pass is outside this build: calling backward raises.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens=None,
+                use_qk_l2norm_in_kernel=False, q_scale=None, k_scale=None):
+        o, ht = chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_final_state,
+                                           cu_seqlens, use_qk_l2norm_in_kernel, q_scale, k_scale)
+        out_dtype = v.dtype if (_FP8 is not None and q.dtype == _FP8) else q.dtype
+        return o.to(out_dtype), ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        raise NotImplementedError("kairos_gdn implements the forward pass only; backward is not built")
+
+
+@torch.compiler.disable
+def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                           scale: float = None, initial_state: torch.Tensor = None, output_final_state: bool = False,
+                           use_qk_l2norm_in_kernel: bool = False, cu_seqlens: torch.LongTensor | None = None,
+                           **kwargs):
+    r"""Chunked gated delta rule forward on MI355X.
+
+    Same contract as the reference (chunk.py:217-323):
+      q, k [B, T, H, K]; v [B, T, H, V]; g (log-space gates) and beta [B, T, H];
+      initial_state [N, H, K, V]; cu_seqlens int64 [N+1] for packed variable
+      length input (B must be 1).  Returns (o [B, T, H, V], final_state
+      [N, H, K, V] fp32 or None).  ``scale`` defaults to K ** -0.5.
+    Extension: q/k may be torch.float8_e4m3fn with per-head fp32 dequantisation
+    scales passed as ``q_scale=`` / ``k_scale=`` (shape [H]); o then has v's dtype.
+    """
+    if 'head_first' in kwargs:
+        warnings.warn(
+            "head_first is deprecated and will be removed in a future version. "
+            "Please use head_first=False for now instead.",
+        )
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError(
+                f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`."
+                f"Please flatten variable-length inputs before processing.",
+            )
+        if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
+            raise ValueError(
+                f"The number of initial states is expected to be equal to the number of input sequences, "
+                f"i.e., {len(cu_seqlens) - 1} rather than {initial_state.shape[0]}.",
+            )
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    return ChunkGatedDeltaRuleFunction.apply(
+        q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens, use_qk_l2norm_in_kernel,
+        kwargs.get("q_scale"), kwargs.get("k_scale"))
+
+
+# ---------------------------------------------------------------------------
+# stages
+# ---------------------------------------------------------------------------
+def _stage_setup(ref: torch.Tensor, cu_seqlens, T):
+    dev = ref.device
+    n_seqs, cu = 0, None
+    if cu_seqlens is not None:
+        cu = _prepare_cu_seqlens(cu_seqlens, dev, T)
+        n_seqs = cu.numel() - 1
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_stage_workspace_size(n_seqs)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    return dev, cu, n_seqs, ws, ws_bytes
+
+
+def num_chunks_bound(B: int, T: int, n_seqs: int = 0) -> int:
+    return int(_lib.load().kairos_gdn_num_chunks_bound(B, T, n_seqs))
+
+
+def chunk_local_cumsum(g: torch.Tensor, chunk_size: int = CHUNK, cu_seqlens=None) -> torch.Tensor:
+    """Chunk-local prefix sum of scalar gates (fla ops/utils/cumsum.py:247-279), fp32 out."""
+    if chunk_size != CHUNK:
+        raise ValueError("only chunk_size=64 is built")
+    _require_device(g)
+    B, T, H = g.shape
+    g = g.contiguous()
+    dev, cu, n_seqs, ws, wsb = _stage_setup(g, cu_seqlens, T)
+    gc = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    _lib.call("kairos_gdn_chunk_local_cumsum", _ptr(g), _code(g, "g"), _ptr(gc), _ptr(cu), n_seqs, B, T, H,
+              _ptr(ws), wsb, _stream(dev))
+    return gc
+
+
+def prepare_wy(k, v, g, beta, cu_seqlens=None, return_A: bool = False, k_scale=None):
+    """Fused cumsum + scaled K.K^T + (I+A)^-1 + w/u (the first four reference stages).
+
+    Returns (gc [B,T,H] fp32, w [B,T,H,K], uT [NCb,H,V,64], A, Ai); A (fp32) and
+    Ai ([B,T,H,64], storage dtype) are None unless ``return_A``.
+    """
+    _require_device(k, v, g, beta)
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    k, v, g, beta = (x.contiguous() for x in (k, v, g, beta))
+    dev, cu, n_seqs, ws, wsb = _stage_setup(k, cu_seqlens, T)
+    nc = num_chunks_bound(B, T, n_seqs)
+    cdt = v.dtype
+    gc = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    w = torch.empty(B, T, H, K, device=dev, dtype=cdt)
+    uT = torch.empty(nc, H, V, CHUNK, device=dev, dtype=cdt)
+    A = torch.zeros(B, T, H, CHUNK, device=dev, dtype=torch.float32) if return_A else None
+    Ai = torch.zeros(B, T, H, CHUNK, device=dev, dtype=cdt) if return_A else None
+    ks = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+    _lib.call("kairos_gdn_prepare_wy", _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(ks), _ptr(gc), _ptr(w),
+              _ptr(uT), _ptr(A), _ptr(Ai), _ptr(cu), n_seqs, B, T, H, K, V, _code(k, "k"), _code(v, "v"),
+              _code(g, "g"), _code(beta, "beta"), _ptr(ws), wsb, _stream(dev))
+    return gc, w, uT, A, Ai
+
+
+def fwd_h(k, w, uT, gc, initial_state=None, output_final_state=False, cu_seqlens=None, k_scale=None):
+    """State recurrence (fla ops/common/chunk_delta_h.py:454-500).
+
+    Returns (hT [NCb,H,V,K], vnT [NCb,H,V,64], final_state [N,H,K,V] fp32 or None).
+    """
+    _require_device(k, w, uT, gc, initial_state)
+    B, T, H, K = k.shape
+    V = uT.shape[2]
+    dev, cu, n_seqs, ws, wsb = _stage_setup(k, cu_seqlens, T)
+    nc = num_chunks_bound(B, T, n_seqs)
+    N = n_seqs if cu is not None else B
+    cdt = w.dtype
+    hT = torch.empty(nc, H, V, K, device=dev, dtype=cdt)
+    vnT = torch.empty(nc, H, V, CHUNK, device=dev, dtype=cdt)
+    ht = torch.empty(N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
+    h0 = initial_state.contiguous() if initial_state is not None else None
+    h0_dt = _code(h0, "initial_state") if h0 is not None else _lib.F32
+    ks = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+    _lib.call("kairos_gdn_fwd_h", _ptr(k.contiguous()), _ptr(ks), _ptr(w.contiguous()), _ptr(uT.contiguous()),
+              _ptr(gc.contiguous()), _ptr(h0), _ptr(hT), _ptr(vnT), _ptr(ht), _ptr(cu), n_seqs, B, T, H, K, V,
+              _code(k, "k"), _code(w, "w"), h0_dt, _ptr(ws), wsb, _stream(dev))
+    return hT, vnT, ht
+
+
+def fwd_o(q, k, hT, vnT, gc, scale=None, cu_seqlens=None, q_scale=None, k_scale=None):
+    """Output stage (fla ops/common/chunk_o.py:498-535); o [B,T,H,V] in the storage dtype."""
+    _require_device(q, k, hT, vnT, gc)
+    B, T, H, K = q.shape
+    V = hT.shape[2]
+    if scale is None:
+        scale = K ** -0.5
+    dev, cu, n_seqs, ws, wsb = _stage_setup(q, cu_seqlens, T)
+    o = torch.empty(B, T, H, V, device=dev, dtype=hT.dtype)
+    qs = q_scale.to(device=dev, dtype=torch.float32).contiguous() if q_scale is not None else None
+    ks = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+    _lib.call("kairos_gdn_fwd_o", _ptr(q.contiguous()), _ptr(k.contiguous()), _ptr(qs), _ptr(ks),
+              _ptr(hT.contiguous()), _ptr(vnT.contiguous()), _ptr(gc.contiguous()), _ptr(o), float(scale),
+              _ptr(cu), n_seqs, B, T, H, K, V, _code(q, "q"), _code(hT, "hT"), _ptr(ws), wsb, _stream(dev))
+    return o
+
+
+def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Row L2 normalisation (fla modules/l2norm.py:157-196); eps is fixed at 1e-6."""
+    if eps != 1e-6:
+        raise ValueError("only eps=1e-6 is built (the reference default)")
+    _require_device(x)
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    D = x.shape[-1]
+    _lib.call("kairos_gdn_l2norm_fwd", _ptr(x), _ptr(y), _code(x, "x"), x.numel() // D, D, _stream(x.device))
+    return y

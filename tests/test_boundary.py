@@ -1,0 +1,180 @@
+"""CPU tests of the drop-in boundary: the C ABI library, its argument checks, the
+Python host mirror's validation (reference error behaviour) and the swap.
+
+No kernel is launched here: every C-ABI call below fails validation before
+any HIP call, and the Python calls fail before reaching the library.
+"""
+import ctypes
+import os
+import re
+import sys
+import types
+import warnings
+
+import pytest
+import torch
+
+import kairos_gdn
+from kairos_gdn import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kairos_gdn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(kairos_gdn_\w+)\s*\(", text)))
+
+
+def test_library_is_built_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+    lib = _lib.load()
+    assert lib.kairos_gdn_abi_version() == _lib.ABI_VERSION
+
+
+def test_library_exports_every_header_symbol():
+    names = header_functions()
+    assert len(names) >= 10
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), f"{n} declared in kairos_gdn.h but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+
+
+def test_num_chunks_bound():
+    lib = _lib.load()
+    assert lib.kairos_gdn_num_chunks_bound(1, 32760, 0) == 512
+    assert lib.kairos_gdn_num_chunks_bound(8, 1560, 0) == 8 * 25
+    # varlen bound covers {1560, 6240, 12480, 32760}: 25 + 98 + 195 + 512 = 830 chunks
+    assert lib.kairos_gdn_num_chunks_bound(1, 53040, 4) >= 830
+
+
+def test_workspace_size_grows_with_problem():
+    lib = _lib.load()
+    a = lib.kairos_gdn_chunk_fwd_workspace_size(1, 8192, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
+    b = lib.kairos_gdn_chunk_fwd_workspace_size(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
+    c = lib.kairos_gdn_chunk_fwd_workspace_size(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 1)
+    assert 0 < a < b < c
+
+
+FAKE = 0x100000  # aligned non-null address: never dereferenced, validation fails first
+
+
+def chunk_fwd_rc(**over):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, g=FAKE, beta=FAKE, q_scale=None, k_scale=None, h0=None, o=FAKE, ht=None,
+                cu=None, n_seqs=0, B=1, T=128, H=2, K=64, V=64, qk=_lib.BF16, vdt=_lib.BF16, gdt=_lib.F32,
+                bdt=_lib.BF16, h0dt=_lib.F32, scale=0.125, l2=0, ws=FAKE, wsb=0, stream=None)
+    args.update(over)
+    lib = _lib.load()
+    rc = lib.kairos_gdn_chunk_fwd(*args.values())
+    return rc, lib.kairos_gdn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(B=0), _lib.EINVAL, "invalid shape"),
+    (dict(K=512), _lib.EINVAL, "larger than 256"),
+    (dict(K=96), _lib.EUNSUPPORTED, "not built"),
+    (dict(B=2, cu=FAKE, n_seqs=1), _lib.EINVAL, "batch size is expected to be 1"),
+    (dict(cu=FAKE, n_seqs=0), _lib.EINVAL, "given together"),
+    (dict(qk=_lib.F8E4M3), _lib.EINVAL, "q_scale"),
+    (dict(qk=_lib.F32), _lib.EINVAL, "dtype mix"),
+    (dict(gdt=_lib.F8E4M3), _lib.EINVAL, "fp32 or bf16"),
+    (dict(q=None), _lib.EINVAL, "null tensor"),
+    (dict(v=FAKE + 2), _lib.EINVAL, "16-byte aligned"),
+    (dict(scale=float("nan")), _lib.EINVAL, "finite"),
+    (dict(wsb=16), _lib.EWORKSPACE, "workspace"),
+])
+def test_c_abi_rejects_invalid_arguments(over, code, msg):
+    rc, err = chunk_fwd_rc(**over)
+    assert rc == code
+    assert msg in err
+
+
+def test_stage_abi_rejects_invalid_arguments():
+    lib = _lib.load()
+    rc = lib.kairos_gdn_l2norm_fwd(FAKE, FAKE, _lib.BF16, 10, 100, None)
+    assert rc == _lib.EINVAL and b"multiple of 8" in lib.kairos_gdn_last_error()
+    rc = lib.kairos_gdn_fwd_o(FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0.1, None, 0, 1, 64, 1, 64, 64,
+                              _lib.F8E4M3, _lib.BF16, None, 0, None)
+    assert rc == _lib.EINVAL and b"q_scale" in lib.kairos_gdn_last_error()
+    rc = lib.kairos_gdn_prepare_wy(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, None, None, FAKE, 3, 1, 200, 2,
+                                   64, 64, _lib.BF16, _lib.BF16, _lib.F32, _lib.F32, None, 0, None)
+    assert rc == _lib.EWORKSPACE
+
+
+# ---------------------------------------------------------------------------
+# Python host mirror: the reference's checks and messages (chunk.py:292-310)
+# ---------------------------------------------------------------------------
+def cpu_inputs(B=1, T=16, H=2, K=64, V=64):
+    q = torch.randn(B, T, H, K)
+    return q, q.clone(), torch.randn(B, T, H, V), -torch.rand(B, T, H), torch.rand(B, T, H)
+
+
+def test_varlen_requires_batch_one():
+    q, k, v, g, b = cpu_inputs(B=2)
+    with pytest.raises(ValueError, match="batch size is expected to be 1 rather than 2"):
+        kairos_gdn.chunk_gated_delta_rule(q, k, v, g, b, cu_seqlens=torch.tensor([0, 8, 16]))
+
+
+def test_varlen_initial_state_count():
+    q, k, v, g, b = cpu_inputs()
+    h0 = torch.zeros(3, 2, 64, 64)
+    with pytest.raises(ValueError, match="i.e., 2 rather than 3"):
+        kairos_gdn.chunk_gated_delta_rule(q, k, v, g, b, initial_state=h0, cu_seqlens=torch.tensor([0, 8, 16]))
+
+
+def test_head_first_warns_and_cpu_tensors_are_refused():
+    q, k, v, g, b = cpu_inputs()
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter("always")
+        with pytest.raises(RuntimeError, match="HIP device only"):
+            kairos_gdn.chunk_gated_delta_rule(q, k, v, g, b, head_first=False)
+    assert any("head_first is deprecated" in str(w.message) for w in rec)
+
+
+def test_stages_refuse_cpu_tensors():
+    with pytest.raises(RuntimeError, match="HIP device only"):
+        kairos_gdn.l2norm_fwd(torch.randn(4, 64))
+    with pytest.raises(RuntimeError, match="HIP device only"):
+        kairos_gdn.chunk_local_cumsum(torch.randn(1, 64, 2))
+
+
+def test_backward_is_refused():
+    ctx = types.SimpleNamespace()
+    with pytest.raises(NotImplementedError):
+        kairos_gdn.ChunkGatedDeltaRuleFunction.backward(ctx, None, None)
+
+
+# ---------------------------------------------------------------------------
+# swap (kairos_engine_patch-style rebinding of the op name)
+# ---------------------------------------------------------------------------
+def test_swap_rebinds_and_restores(monkeypatch):
+    def reference_op(*a, **k):
+        return "reference"
+    layer = types.ModuleType("fla.layers.gated_deltanet")
+    layer.chunk_gated_delta_rule = reference_op
+    vendored = types.ModuleType("kairos.third_party.fla.ops.gated_delta_rule")
+    vendored.chunk_gated_delta_rule = reference_op
+    monkeypatch.setitem(sys.modules, "fla.layers.gated_deltanet", layer)
+    monkeypatch.setitem(sys.modules, "kairos.third_party.fla.ops.gated_delta_rule", vendored)
+    patched = kairos_gdn.swap.install()
+    assert set(patched) == {"fla.layers.gated_deltanet", "kairos.third_party.fla.ops.gated_delta_rule"}
+    assert layer.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
+    assert vendored.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
+    assert kairos_gdn.swap.install() == patched                  # idempotent
+    restored = kairos_gdn.swap.uninstall()
+    assert set(restored) == set(patched)
+    assert layer.chunk_gated_delta_rule is reference_op
+
+
+# ---------------------------------------------------------------------------
+# the product never routes through the oracle
+# ---------------------------------------------------------------------------
+def test_product_does_not_import_oracle():
+    pkg = os.path.join(ROOT, "kairos-sensenova_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), f
+                assert "gdn_oracle" not in text, f

@@ -1,0 +1,370 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI.
+
+Tolerances (relative L2 = RMS(err) / RMS(ref), fla's get_err_ratio):
+  bf16 path: o <= 1e-2, final_state <= 5e-3;
+             stage intermediates (w, u, h, v_new) <= 1e-2, fp32 gc / A <= 1e-5.
+  fp32 path: o, final_state and every intermediate <= 1e-4.
+Full-size configs compare every head on the GPU against the oracle on a
+subset of heads (heads are independent), plus size-independent properties:
+determinism, varlen == separate calls, split calls with state carry.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn_oracle as O
+from gdn_inputs import CONFIGS, make_inputs
+import kairos_gdn
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": dict(o=1e-2, ht=5e-3, mid=1e-2), "fp32": dict(o=1e-4, ht=1e-4, mid=1e-4)}
+TDT = {"bf16": torch.bfloat16, "fp32": torch.float32}
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev(x, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.detach().float().cpu().numpy()
+
+
+def to_dev(x, dt):
+    d = {k: dev(x[k], TDT[dt]) for k in ("q", "k", "v")}
+    d["beta"] = dev(x["beta"], TDT[dt])
+    d["g"] = dev(x["g"], torch.float32)
+    d["h0"] = dev(x["h0"]) if x["h0"] is not None else None
+    return d
+
+
+def chunk_T_to_tokens(xT, cm, rows=64):
+    """[NCb, H, V, 64] per-chunk transposed -> [B, T, H, V] (oracle ChunkMap order)."""
+    a = np.swapaxes(xT[:cm.nc], 2, 3)                    # [NC, H, 64, V]
+    return cm.scatter(a, np.float32)
+
+
+def tokens_to_chunk_T(x, cm, ncb):
+    """[B, T, H, V] -> [NCb, H, V, 64] (zeros in padded rows and spare chunks)."""
+    a = np.swapaxes(cm.gather(x, np.float32), 2, 3)       # [NC, H, V, 64]
+    out = np.zeros((ncb,) + a.shape[1:], np.float32)
+    out[:cm.nc] = a
+    return out
+
+
+def rel(a, b):
+    return O.rel_l2(a, b)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu_ready():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    kairos_gdn._lib.load()
+
+
+# ---------------------------------------------------------------------------
+# elementwise stages
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+def test_l2norm(dt):
+    note(f"l2norm {dt}")
+    rng = np.random.default_rng(0)
+    x = O.cast(rng.standard_normal((3, 777, 128)).astype(np.float32) * 3, dt)
+    y = host(kairos_gdn.l2norm_fwd(dev(x, TDT[dt])))
+    ref = O.l2norm(x, dtype=dt)
+    assert rel(y, ref) < (4e-3 if dt == "bf16" else 1e-6)
+
+
+@pytest.mark.parametrize("cu", [None, [0, 1, 64, 65, 200, 330]])
+def test_cumsum(cu):
+    note(f"cumsum cu={cu}")
+    rng = np.random.default_rng(1)
+    B = 1 if cu else 2
+    g = (-np.logaddexp(0, rng.standard_normal((B, 330, 5)))).astype(np.float32)
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
+    gc = host(kairos_gdn.chunk_local_cumsum(dev(g), cu_seqlens=cu_t))
+    ref = O.chunk_local_cumsum(g, cu_seqlens=np.array(cu) if cu else None)
+    np.testing.assert_allclose(gc, ref, rtol=1e-5, atol=2e-5)
+
+
+# ---------------------------------------------------------------------------
+# prepare (cumsum + K.K^T + solve + w/u), fed identical inputs
+# ---------------------------------------------------------------------------
+PREP_CASES = [
+    ("bf16", 1, 300, 3, 128, 128, None),
+    ("bf16", 2, 200, 2, 64, 128, None),
+    ("bf16", 1, 400, 2, 128, 64, [0, 10, 74, 74, 260, 400]),
+    ("fp32", 1, 200, 2, 64, 64, None),
+    ("fp32", 1, 150, 2, 128, 128, [0, 100, 150]),
+]
+
+
+@pytest.mark.parametrize("dt,B,T,H,K,V,cu", PREP_CASES)
+def test_prepare_stage(dt, B, T, H, K, V, cu):
+    note(f"prepare {dt} B={B} T={T} H={H} K={K} V={V} cu={cu}")
+    x = make_inputs(B, T, H, K, V, seed=T + K + V, dtype=dt, n_states=len(cu) - 1 if cu else None)
+    d = to_dev(x, dt)
+    cu_np = np.array(cu) if cu else None
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
+    gc, w, uT, A, Ai = kairos_gdn.prepare_wy(d["k"], d["v"], d["g"], d["beta"], cu_seqlens=cu_t, return_A=True)
+    torch.cuda.synchronize()
+    cm = O.ChunkMap(B, T, cu_np)
+    gc_r = O.chunk_local_cumsum(x["g"], cu_np, dtype=dt)
+    np.testing.assert_allclose(host(gc), gc_r, rtol=1e-5, atol=2e-5)
+    A_r = O.chunk_scaled_dot_kkt(x["k"], gc_r, x["beta"], cu_np, dtype=dt)
+    assert rel(host(A), A_r) < 1e-5
+    Ai_r = O.solve_tril(A_r, cu_np, dtype=dt)
+    assert rel(host(Ai), Ai_r) < TOL[dt]["mid"] / 2
+    w_r, u_r = O.recompute_w_u(x["k"], x["v"], x["beta"], Ai_r, gc_r, cu_np, dtype=dt)
+    assert rel(host(w), w_r) < TOL[dt]["mid"]
+    assert rel(chunk_T_to_tokens(host(uT), cm), u_r) < TOL[dt]["mid"]
+    # padded rows of the transposed u are exact zeros (the later stages rely on it)
+    ut = host(uT)[:cm.nc]
+    pad = ~cm.valid
+    assert np.all(np.swapaxes(ut, 2, 3)[pad[:, None, :].repeat(H, 1)] == 0)
+
+
+# ---------------------------------------------------------------------------
+# state recurrence and output, fed the oracle's own intermediates
+# ---------------------------------------------------------------------------
+H_CASES = [
+    ("bf16", 1, 520, 3, 128, 128, None, True),
+    ("bf16", 2, 130, 2, 64, 64, None, False),
+    ("bf16", 1, 500, 2, 128, 128, [0, 63, 64, 64, 300, 500], True),
+    ("fp32", 1, 260, 2, 64, 64, None, True),
+]
+
+
+@pytest.mark.parametrize("dt,B,T,H,K,V,cu,with_h0", H_CASES)
+def test_fwd_h_and_fwd_o_stages(dt, B, T, H, K, V, cu, with_h0):
+    note(f"fwd_h/fwd_o {dt} B={B} T={T} H={H} K={K} V={V} cu={cu} h0={with_h0}")
+    x = make_inputs(B, T, H, K, V, seed=7 * T + K, dtype=dt, n_states=len(cu) - 1 if cu else None,
+                    h0_scale=0.02 if with_h0 else 0.0)
+    cu_np = np.array(cu) if cu else None
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
+    o_r, ht_r, inter = O.chunk_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["h0"],
+                                                output_final_state=True, cu_seqlens=cu_np, dtype=dt,
+                                                return_intermediates=True)
+    cm = O.ChunkMap(B, T, cu_np)
+    ncb = kairos_gdn.num_chunks_bound(B, T, len(cu) - 1 if cu else 0)
+    d = to_dev(x, dt)
+    w = dev(inter["w"], TDT[dt])
+    uT = dev(tokens_to_chunk_T(inter["u"], cm, ncb), TDT[dt])
+    gc = dev(inter["gc"])
+    hT, vnT, ht = kairos_gdn.fwd_h(d["k"], w, uT, gc, initial_state=d["h0"], output_final_state=True,
+                                   cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    h_gpu = np.swapaxes(host(hT)[:cm.nc], 2, 3)
+    assert rel(h_gpu, inter["h"]) < TOL[dt]["mid"]
+    assert rel(chunk_T_to_tokens(host(vnT), cm), inter["v_new"]) < TOL[dt]["mid"]
+    assert rel(host(ht), ht_r) < TOL[dt]["ht"]
+    # output stage on the oracle's h and v_new
+    hT_r = np.zeros((ncb, H, V, K), np.float32)
+    hT_r[:cm.nc] = np.swapaxes(inter["h"], 2, 3)
+    o = kairos_gdn.fwd_o(d["q"], d["k"], dev(hT_r, TDT[dt]), dev(tokens_to_chunk_T(inter["v_new"], cm, ncb), TDT[dt]),
+                         gc, cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert rel(host(o), o_r) < TOL[dt]["o"]
+
+
+# ---------------------------------------------------------------------------
+# whole op
+# ---------------------------------------------------------------------------
+def run_gpu(x, dt, cu=None, l2=False, out_final=True, with_h0=True):
+    d = to_dev(x, dt)
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu is not None else None
+    o, ht = kairos_gdn.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"],
+                                              initial_state=d["h0"] if with_h0 else None,
+                                              output_final_state=out_final, cu_seqlens=cu_t,
+                                              use_qk_l2norm_in_kernel=l2)
+    torch.cuda.synchronize()
+    return o, ht
+
+
+def check_against_oracle(x, dt, o, ht, cu=None, heads=None, l2=False, with_h0=True):
+    sel = slice(None) if heads is None else np.array(heads)
+    xs = {k: (v[:, :, sel] if k != "h0" else (v[:, sel] if v is not None else None)) for k, v in x.items()}
+    o_r, ht_r = O.chunk_gated_delta_rule(xs["q"], xs["k"], xs["v"], xs["g"], xs["beta"],
+                                         initial_state=xs["h0"] if with_h0 else None, output_final_state=True,
+                                         cu_seqlens=np.array(cu) if cu is not None else None,
+                                         use_qk_l2norm_in_kernel=l2, dtype=dt)
+    eo = rel(host(o)[:, :, sel], o_r)
+    eh = rel(host(ht)[:, sel], ht_r) if ht is not None else 0.0
+    note(f"    rel-L2 o={eo:.3e} ht={eh:.3e}")
+    assert eo < TOL[dt]["o"]
+    assert eh < TOL[dt]["ht"]
+    return eo, eh
+
+
+EDGE_CASES = [
+    # dt, B, T, H, K, V, cu, l2, with_h0
+    ("bf16", 1, 1, 2, 64, 64, None, False, True),
+    ("bf16", 1, 63, 2, 128, 128, None, False, True),
+    ("bf16", 3, 200, 2, 128, 64, None, False, True),
+    ("bf16", 1, 1000, 4, 128, 128, None, True, True),
+    ("bf16", 1, 700, 3, 64, 128, [0, 1, 1, 129, 640, 700], False, True),
+    ("bf16", 2, 100, 2, 64, 64, None, False, False),
+    ("fp32", 2, 300, 2, 128, 128, None, False, True),
+]
+
+
+@pytest.mark.parametrize("dt,B,T,H,K,V,cu,l2,with_h0", EDGE_CASES)
+def test_full_op_edge_cases(dt, B, T, H, K, V, cu, l2, with_h0):
+    note(f"chunk_gated_delta_rule {dt} B={B} T={T} H={H} K={K} V={V} cu={cu} l2={l2} h0={with_h0}")
+    n = len(cu) - 1 if cu else None
+    x = make_inputs(B, T, H, K, V, seed=T * 3 + H, dtype=dt, n_states=n, h0_scale=0.02 if with_h0 else 0.0)
+    if l2:                                   # un-normalised q/k: the kernel normalises them
+        x["q"] = O.cast(x["q"] * 3.0, dt)
+        x["k"] = O.cast(x["k"] * 0.5, dt)
+    o, ht = run_gpu(x, dt, cu=cu, l2=l2, with_h0=with_h0)
+    assert o.dtype == TDT[dt] and tuple(o.shape) == (B, T, H, V)
+    assert ht.dtype == torch.float32
+    check_against_oracle(x, dt, o, ht, cu=cu, l2=l2, with_h0=with_h0)
+
+
+def test_empty_sequence_returns_initial_state():
+    note("T=0")
+    x = make_inputs(2, 0, 2, 64, 64, seed=1, dtype="bf16")
+    o, ht = run_gpu(x, "bf16")
+    assert o.numel() == 0
+    np.testing.assert_array_equal(host(ht), x["h0"])
+
+
+def test_bf16_gates_and_state_inputs():
+    note("bf16 g / beta / h0")
+    x = make_inputs(1, 300, 2, 128, 128, seed=5, dtype="bf16")
+    x["g"] = O.to_bf16(x["g"])
+    d = to_dev(x, "bf16")
+    o, ht = kairos_gdn.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"].bfloat16(), d["beta"],
+                                              initial_state=d["h0"].bfloat16(), output_final_state=True)
+    torch.cuda.synchronize()
+    x["h0"] = O.to_bf16(x["h0"])
+    check_against_oracle(x, "bf16", o, ht)
+
+
+@pytest.mark.parametrize("cfg", [0, 1])
+def test_baseline_config(cfg):
+    c = CONFIGS[cfg]
+    note(f"config {cfg}: {c}")
+    x = make_inputs(c["B"], c["T"], c["H"], c["K"], c["V"], seed=20260 + cfg, dtype=c["dtype"],
+                    h0_scale=0.0 if c.get("zero_h0") else 0.02)
+    if c.get("zero_h0"):
+        x["h0"] = np.zeros((c["B"], c["H"], c["K"], c["V"]), np.float32)
+    o, ht = run_gpu(x, c["dtype"])
+    check_against_oracle(x, c["dtype"], o, ht)
+    if cfg == 0:                             # config 0 also checks against the fp64 token recurrence
+        on, hn = O.naive_recurrent(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["h0"])
+        assert rel(host(o), on) < 1e-4 and rel(host(ht), hn) < 1e-4
+
+
+@pytest.mark.parametrize("cfg,heads", [(2, [0, 9, 19]), (3, [3, 16])])
+def test_baseline_config_full_size(cfg, heads):
+    c = CONFIGS[cfg]
+    note(f"config {cfg} (oracle on heads {heads})")
+    cu = c.get("cu")
+    x = make_inputs(c["B"], c["T"], c["H"], c["K"], c["V"], seed=20260 + cfg, dtype=c["dtype"],
+                    n_states=len(cu) - 1 if cu else None)
+    o, ht = run_gpu(x, c["dtype"], cu=cu)
+    assert bool(torch.isfinite(o).all()) and bool(torch.isfinite(ht).all())
+    check_against_oracle(x, c["dtype"], o, ht, cu=cu, heads=heads)
+
+
+# ---------------------------------------------------------------------------
+# size-independent properties at the full sizes
+# ---------------------------------------------------------------------------
+def test_full_size_properties():
+    c = CONFIGS[3]
+    cu = c["cu"]
+    note("properties: determinism, varlen == separate calls, split with state carry")
+    x = make_inputs(1, c["T"], c["H"], c["K"], c["V"], seed=99, dtype="bf16", n_states=len(cu) - 1)
+    d = to_dev(x, "bf16")
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda")
+    f = kairos_gdn.chunk_gated_delta_rule
+    o1, h1 = f(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["h0"], output_final_state=True,
+               cu_seqlens=cu_t)
+    o2, h2 = f(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=d["h0"], output_final_state=True,
+               cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)                  # deterministic
+    for n in range(len(cu) - 1):                                          # varlen == separate calls (bitwise)
+        s = slice(cu[n], cu[n + 1])
+        on, hn = f(d["q"][:, s], d["k"][:, s], d["v"][:, s], d["g"][:, s], d["beta"][:, s],
+                   initial_state=d["h0"][n:n + 1], output_final_state=True)
+        torch.cuda.synchronize()
+        assert torch.equal(on, o1[:, s]) and torch.equal(hn, h1[n:n + 1])
+    # the last sequence split at a chunk boundary with the state carried (bitwise: same chunk grid)
+    s0, s1 = cu[3], cu[4]
+    mid = s0 + 64 * 200
+    oa, ha = f(d["q"][:, s0:mid], d["k"][:, s0:mid], d["v"][:, s0:mid], d["g"][:, s0:mid], d["beta"][:, s0:mid],
+               initial_state=d["h0"][3:4], output_final_state=True)
+    ob, hb = f(d["q"][:, mid:s1], d["k"][:, mid:s1], d["v"][:, mid:s1], d["g"][:, mid:s1], d["beta"][:, mid:s1],
+               initial_state=ha, output_final_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([oa, ob], 1), o1[:, s0:s1]) and torch.equal(hb, h1[3:4])
+
+
+# ---------------------------------------------------------------------------
+# config 4: streaming frame-by-frame rollout with fp8 q/k
+# ---------------------------------------------------------------------------
+def quantize_fp8(x):
+    """Per-head e4m3 quantisation with scale = amax / 448."""
+    amax = np.abs(x).max(axis=(0, 1, 3))                               # [H]
+    scale = (amax / 448.0).astype(np.float32)
+    codes = O.fp8_e4m3_quantize(x / scale[None, None, :, None])
+    return codes, scale
+
+
+def dequant_bf16(codes, scale):
+    return O.to_bf16(O.fp8_e4m3_decode(codes) * scale[None, None, :, None])
+
+
+@pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
+def test_streaming_fp8_rollout():
+    B, H, K, V, Tf, frames = 8, 20, 128, 128, 1560, 21
+    note(f"config 4: B={B} H={H} {frames} calls of T={Tf}, fp8 q/k")
+    heads = [0, 13]
+    check_frames = {0, 10, 20}
+    h0 = (0.02 * np.random.default_rng(20264).standard_normal((B, H, K, V))).astype(np.float32)
+    state = dev(h0)
+    S_in = h0[:, heads]
+    parts = []
+    for f in range(frames):
+        x = make_inputs(B, Tf, H, K, V, seed=(20264, f), dtype="bf16", h0_scale=0.0)
+        qc, qs = quantize_fp8(x["q"])
+        kc, ks = quantize_fp8(x["k"])
+        q8 = torch.from_numpy(qc).to("cuda").view(torch.float8_e4m3fn)
+        k8 = torch.from_numpy(kc).to("cuda").view(torch.float8_e4m3fn)
+        d = to_dev(x, "bf16")
+        o, new_state = kairos_gdn.chunk_gated_delta_rule(q8, k8, d["v"], d["g"], d["beta"], initial_state=state,
+                                                         output_final_state=True, q_scale=dev(qs), k_scale=dev(ks))
+        parts.append({k_: x[k_][:, :, heads] for k_ in ("q", "k", "v", "g", "beta")})
+        if f in check_frames:
+            torch.cuda.synchronize()
+            assert o.dtype == torch.bfloat16
+            qd, kd = dequant_bf16(qc, qs), dequant_bf16(kc, ks)
+            o_r, S_next = O.chunk_gated_delta_rule(qd[:, :, heads], kd[:, :, heads], x["v"][:, :, heads],
+                                                   x["g"][:, :, heads], x["beta"][:, :, heads],
+                                                   initial_state=host(state)[:, heads], output_final_state=True,
+                                                   dtype="bf16")
+            eo = rel(host(o)[:, :, heads], o_r)
+            eh = rel(host(new_state)[:, heads], S_next)
+            note(f"    frame {f}: rel-L2 o={eo:.3e} state={eh:.3e}")
+            assert eo < 1e-2 and eh < 5e-3
+        state = new_state
+    torch.cuda.synchronize()
+    # drift of the streamed end state against one fp32 call over all 21 frames (unquantised q/k)
+    cat = {k_: np.concatenate([p_[k_] for p_ in parts], axis=1) for k_ in parts[0]}
+    _, h_single = O.chunk_gated_delta_rule(cat["q"], cat["k"], cat["v"], cat["g"], cat["beta"],
+                                           initial_state=S_in, output_final_state=True, dtype="fp32")
+    drift = rel(host(state)[:, heads], h_single)
+    note(f"    end-state drift vs single-call fp32 (unquantised q/k): {drift:.3e}")
+    assert math.isfinite(drift) and drift < 0.1
