@@ -105,16 +105,29 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=2)
     ap.add_argument("--T", type=int, default=32760)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="run only a plain elementwise copy of MIB MiB (fp32 y = x * 1) 5 times and exit: the "
+                         "reference kernel of known traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
 
-    import kairos_gdn
-    from kairos_gdn import _lib
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        x = torch.ones(n, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            torch.mul(x, 1.0, out=y)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": 4 * n, "calibrate_copy_bytes_written": 4 * n}), flush=True)
+        return
+
+    import kairos_gdn
+    from kairos_gdn import _lib
     B, T, H, K, V = 1, args.T, 20, 128, 128
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)
     scale = K ** -0.5

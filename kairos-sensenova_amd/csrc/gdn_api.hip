@@ -1,11 +1,19 @@
 // C ABI of the chunked GatedDeltaNet forward (declared in include/kairos_gdn.h):
-// argument validation, workspace carving and stage orchestration.  The
-// orchestration mirrors chunk_gated_delta_rule_fwd (fla
-// ops/gated_delta_rule/chunk.py:16-67) with the four prepare stages fused:
-//   [l2norm q, k] -> [chunk map] -> prepare (gc, w, u) -> fwd_h (h, v_new, ht) -> fwd_o (o)
+// argument validation, workspace carving and kernel orchestration.
+//
+// kairos_gdn_chunk_fwd computes chunk_gated_delta_rule_fwd (fla
+// ops/gated_delta_rule/chunk.py:16-67) with the segment-parallel fused kernels
+// of gdn_seg.hip:
+//   [l2norm q, k] -> [segment map] -> seg_trans (per-segment [M | R])
+//                 -> seg_combine (segment initial states) -> seg_out (o, ht)
+// The stage entry points (kairos_gdn_prepare_wy, _fwd_h, _fwd_o, ...) run
+// one reference stage each with the stage kernels and the reference's
+// intermediate tensors.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -108,6 +116,136 @@ int chunk_map(const Geometry& G, const int64_t* cu, Carver& cv, const int32_t** 
 
 size_t stage_ws(int64_t n_seqs) { return n_seqs > 0 ? align_up(sizeof(int32_t) * (n_seqs + 1)) : 0; }
 
+// Compute units of the current device (queried once; 256, the MI355X count, without a device).
+int device_cus() {
+  static int cached = 0;
+  if (cached > 0) return cached;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;
+  }
+  cached = cus;
+  return cached;
+}
+
+// Segment plan of the fused forward: L chunks per segment, chosen so that the
+// (segment, head) work items of the longest-running kernels fill the compute
+// units once (one 4-wave workgroup per CU).  KAIROS_GDN_SEG_CHUNKS overrides L.
+struct SegPlan {
+  int L;
+  int nseg_fixed;     // fixed length: segments per sequence
+  int64_t ns;         // segments (varlen: upper bound)
+  bool trans, combine;
+};
+
+SegPlan plan_segments(int64_t B, int64_t T, int64_t H, int64_t n_seqs) {
+  SegPlan P{1, 0, 0, false, false};
+  const int64_t cus = device_cus();
+  int64_t L_env = 0;
+  if (const char* e = std::getenv("KAIROS_GDN_SEG_CHUNKS")) L_env = std::atoll(e);
+  if (n_seqs == 0) {
+    const int64_t nc = (T + kgdn::C - 1) / kgdn::C;
+    if (nc == 0) {
+      P.combine = true;         // final_state of empty sequences = initial_state
+      return P;
+    }
+    int64_t L;
+    if (L_env > 0) {
+      L = L_env;
+    } else {
+      const int64_t target = std::max<int64_t>(1, cus / std::max<int64_t>(1, B * H));
+      const int64_t nseg = std::min(nc, target);
+      L = (nc + nseg - 1) / nseg;
+    }
+    P.L = (int)std::min<int64_t>(L, 1 << 20);
+    P.nseg_fixed = (int)((nc + P.L - 1) / P.L);
+    P.ns = B * P.nseg_fixed;
+    P.trans = P.combine = P.nseg_fixed > 1;
+    return P;
+  }
+  const int64_t cb = T / kgdn::C + n_seqs;       // bound on the total chunk count
+  int64_t L;
+  if (L_env > 0) {
+    L = L_env;
+  } else {
+    const int64_t free_slots = std::max<int64_t>(cus - n_seqs * H, cus / 2);
+    L = std::max<int64_t>(1, (cb * H + free_slots - 1) / free_slots);
+  }
+  P.L = (int)std::min<int64_t>(L, 1 << 20);
+  P.ns = cb / P.L + n_seqs;                      // sum_n ceil(nc_n / L) <= cb / L + N
+  P.trans = P.combine = true;
+  return P;
+}
+
+size_t seg_ws(int64_t H, int64_t K, int64_t V, int64_t n_seqs, const SegPlan& P) {
+  size_t total = n_seqs > 0 ? 2 * align_up(sizeof(int32_t) * (n_seqs + 1)) : 0;
+  if (P.trans || P.combine) {
+    const size_t blocks = (size_t)P.ns * H;
+    total += align_up(blocks * K * K * sizeof(float));        // M
+    total += align_up(blocks * K * V * sizeof(float));        // R
+    total += align_up(blocks * K * V * sizeof(float));        // segment initial states
+  }
+  return total;
+}
+
+// Workspace of the staged path (stage kernels with the reference's intermediates).
+size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt) {
+  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
+  const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
+  const size_t tok = (size_t)(B * T * H);
+  size_t total = stage_ws(n_seqs);
+  total += align_up(tok * sizeof(float));                 // gc
+  total += align_up(tok * K * es);                        // w
+  total += align_up(nc * H * V * kgdn::C * es);           // uT
+  total += align_up(nc * H * V * K * es);                 // hT
+  total += align_up(nc * H * V * kgdn::C * es);           // vnT
+  return total;
+}
+
+// Staged forward: prepare (gc, w, u) -> fwd_h (h, v_new, ht) -> fwd_o (o), the
+// reference's stage order with its intermediates in the workspace.  Used for the
+// shapes the fused kernels do not cover (fp32 with K = 128).
+int run_staged(const Geometry& G, const void* q, const void* k, const void* v, const void* g, const void* beta,
+               const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
+               const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
+               Carver& cv, hipStream_t s) {
+  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
+  const size_t tok = (size_t)(G.B * G.T * G.H);
+  const int K = (int)G.K, V = (int)G.V, H = (int)G.H;
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
+  void* w = cv.take(tok * K * es);
+  void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  void* hT = cv.take((size_t)G.nc * H * V * K * es);
+  void* vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  const int N = (int)G.N;
+  if (G.nc > 0) {
+    kgdn::PrepareArgs pa{};
+    pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
+    pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
+    pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
+    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = nullptr;
+    if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, G.nc, s), "prepare")) return rc;
+  }
+  kgdn::FwdHArgs ha{};
+  ha.k = k; ha.k_scale = k_scale; ha.w = w; ha.uT = uT; ha.gc = gc;
+  ha.h0 = h0; ha.h0_dtype = h0_dtype;
+  ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = N; ha.T = G.T; ha.H = H;
+  ha.hT = hT; ha.vnT = vnT; ha.ht = ht;
+  if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, K, V, s), "fwd_h")) return rc;
+  if (G.nc > 0) {
+    kgdn::FwdOArgs oa{};
+    oa.q = q; oa.k = k; oa.q_scale = q_scale; oa.k_scale = k_scale;
+    oa.hT = hT; oa.vnT = vnT; oa.gc = gc; oa.scale = scale;
+    oa.cu = cu_seqlens; oa.chunk_off = chunk_off; oa.N = N; oa.T = G.T; oa.H = H; oa.o = o;
+    if (int rc = from_launch(kgdn::launch_fwd_o(oa, cdt, qk_dtype, K, V, G.nc, s), "fwd_o")) return rc;
+  }
+  return KAIROS_GDN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -122,17 +260,12 @@ size_t kairos_gdn_stage_workspace_size(int64_t n_seqs) { return stage_ws(n_seqs)
 
 size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs,
                                            int qk_dtype, int v_dtype, int use_qk_l2norm) {
-  const int cdt = compute_dtype(qk_dtype, v_dtype);
-  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
-  const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
+  if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0) return 0;
   const size_t tok = (size_t)(B * T * H);
-  size_t total = stage_ws(n_seqs);
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  size_t total = kgdn::seg_fwd_supported(cdt, (int)K, (int)V) ? seg_ws(H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
+                                                              : staged_ws(B, T, H, K, V, n_seqs, cdt);
   if (use_qk_l2norm) total += 2 * align_up(tok * K * dt_size(qk_dtype));
-  total += align_up(tok * sizeof(float));                 // gc
-  total += align_up(tok * K * es);                        // w
-  total += align_up(nc * H * V * kgdn::C * es);           // uT
-  total += align_up(nc * H * V * K * es);                 // hT
-  total += align_up(nc * H * V * kgdn::C * es);           // vnT
   return total;
 }
 
@@ -169,11 +302,41 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
   if (need && !aligned16(workspace)) return fail(KAIROS_GDN_EINVAL, "%s: workspace must be 16-byte aligned", what);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(B * T * H);
   Carver cv{static_cast<char*>(workspace)};
+  if (!kgdn::seg_fwd_supported(cdt, (int)K, (int)V)) {
+    if (use_qk_l2norm && any_tokens) {
+      void* qn = cv.take(tok * K * dt_size(qk_dtype));
+      void* kn = cv.take(tok * K * dt_size(qk_dtype));
+      if (int rc = from_launch(kgdn::launch_l2norm(q, qn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q)")) return rc;
+      if (int rc = from_launch(kgdn::launch_l2norm(k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(k)")) return rc;
+      q = qn;
+      k = kn;
+    }
+    if (int rc = run_staged(G, q, k, v, g, beta, q_scale, k_scale, initial_state, h0_dtype, o, final_state,
+                            cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s))
+      return rc;
+    return ok();
+  }
+  const SegPlan P = plan_segments(B, T, H, n_seqs);
   const int32_t* chunk_off = nullptr;
-  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  const int32_t* seg_off = nullptr;
+  if (G.varlen) {
+    int32_t* co = static_cast<int32_t*>(cv.take(sizeof(int32_t) * (G.N + 1)));
+    int32_t* so = static_cast<int32_t*>(cv.take(sizeof(int32_t) * (G.N + 1)));
+    if (int rc = from_launch(kgdn::launch_seg_map(cu_seqlens, (int)G.N, P.L, co, so, s), "segment map")) return rc;
+    chunk_off = co;
+    seg_off = so;
+  }
+  float* M = nullptr;
+  float* R = nullptr;
+  float* s_init = nullptr;
+  if (P.trans || P.combine) {
+    const size_t blocks = (size_t)P.ns * H;
+    M = static_cast<float*>(cv.take(blocks * K * K * sizeof(float)));
+    R = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
+    s_init = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
+  }
   if (use_qk_l2norm && any_tokens) {
     void* qn = cv.take(tok * K * dt_size(qk_dtype));
     void* kn = cv.take(tok * K * dt_size(qk_dtype));
@@ -182,34 +345,18 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
     q = qn;
     k = kn;
   }
-  float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
-  void* w = cv.take(tok * K * es);
-  void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
-  void* hT = cv.take((size_t)G.nc * H * V * K * es);
-  void* vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  if (P.ns > 0x7fffffff / 2) return fail(KAIROS_GDN_EINVAL, "%s: too many segments", what);
 
-  const int N = (int)G.N;
-  if (G.nc > 0) {
-    kgdn::PrepareArgs pa{};
-    pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
-    pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
-    pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = T; pa.H = (int)H;
-    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = nullptr;
-    if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "prepare")) return rc;
-  }
-  kgdn::FwdHArgs ha{};
-  ha.k = k; ha.k_scale = k_scale; ha.w = w; ha.uT = uT; ha.gc = gc;
-  ha.h0 = initial_state; ha.h0_dtype = h0_dtype;
-  ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = N; ha.T = T; ha.H = (int)H;
-  ha.hT = hT; ha.vnT = vnT; ha.ht = final_state;
-  if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h")) return rc;
-  if (G.nc > 0) {
-    kgdn::FwdOArgs oa{};
-    oa.q = q; oa.k = k; oa.q_scale = q_scale; oa.k_scale = k_scale;
-    oa.hT = hT; oa.vnT = vnT; oa.gc = gc; oa.scale = scale;
-    oa.cu = cu_seqlens; oa.chunk_off = chunk_off; oa.N = N; oa.T = T; oa.H = (int)H; oa.o = o;
-    if (int rc = from_launch(kgdn::launch_fwd_o(oa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "fwd_o")) return rc;
-  }
+  kgdn::SegFwdArgs a{};
+  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.q_scale = q_scale; a.k_scale = k_scale;
+  a.g_dtype = g_dtype; a.beta_dtype = beta_dtype;
+  a.h0 = initial_state; a.h0_dtype = h0_dtype;
+  a.cu = cu_seqlens; a.chunk_off = chunk_off; a.seg_off = seg_off;
+  a.N = (int)G.N; a.T = T; a.H = (int)H; a.L = P.L; a.nseg_fixed = P.nseg_fixed; a.ns_grid = P.ns;
+  a.M = M; a.R = R; a.s_init = s_init; a.scale = scale; a.o = o; a.ht = final_state;
+  a.run_trans = P.trans && P.ns > 0;
+  a.run_combine = P.combine;
+  if (int rc = from_launch(kgdn::launch_seg_fwd(a, cdt, qk_dtype, (int)K, (int)V, s), "segment forward")) return rc;
   return ok();
 }
 

@@ -73,6 +73,39 @@ struct FwdOArgs {
   void* o;                // out [B*T, H, V] compute dtype
 };
 
+// Segment-parallel fused forward (gdn_seg.hip).  Sequences are cut into
+// segments of L chunks; M, R and s_init are fp32 workspaces of ns_grid * H
+// blocks of K x K, K x V and K x V.
+struct SegFwdArgs {
+  const void* q;          // [B*T, H, K]  (qk_dtype)
+  const void* k;
+  const void* v;          // [B*T, H, V]  compute dtype
+  const void* g;          // [B*T, H]     g_dtype
+  const void* beta;       // [B*T, H]     beta_dtype
+  const float* q_scale;   // [H] (fp8 q/k) or nullptr
+  const float* k_scale;
+  int g_dtype, beta_dtype;
+  const void* h0;         // [N, H, K, V] (h0_dtype) or nullptr
+  int h0_dtype;
+  const int64_t* cu;      // varlen: [N+1] token offsets, else nullptr
+  const int32_t* chunk_off;
+  const int32_t* seg_off; // varlen: [N+1] segment offsets
+  int N;
+  int64_t T;
+  int H;
+  int L;                  // chunks per segment
+  int nseg_fixed;         // fixed length: segments per sequence
+  int64_t ns_grid;        // number of segments (varlen: an upper bound)
+  float* M;               // [ns_grid, H, K, K]
+  float* R;               // [ns_grid, H, K, V]
+  float* s_init;          // [ns_grid, H, K, V]
+  float scale;
+  void* o;                // out [B*T, H, V]
+  float* ht;              // out [N, H, K, V] or nullptr
+  bool run_trans;         // some sequence has more than one segment
+  bool run_combine;       // ... or final_state of empty sequences is needed
+};
+
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported
 // (dtype, K, V) combination.
 int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, int V, int64_t nc_grid,
@@ -80,6 +113,9 @@ int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, 
 int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V, hipStream_t s);
 int launch_fwd_o(const FwdOArgs& a, int compute_dtype, int qk_dtype, int K, int V, int64_t nc_grid,
                  hipStream_t s);
+bool seg_fwd_supported(int compute_dtype, int K, int V);
+int launch_seg_fwd(const SegFwdArgs& a, int compute_dtype, int qk_dtype, int K, int V, hipStream_t s);
+int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s);
 int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s);
 int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s);
 int launch_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu, const int32_t* chunk_off, int N,

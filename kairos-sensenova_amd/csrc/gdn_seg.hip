@@ -1,0 +1,1118 @@
+// Segment-parallel fused forward of the chunked GatedDeltaNet (the path behind
+// kairos_gdn_chunk_fwd).  It computes what the reference's six stages compute
+// (fla ops/gated_delta_rule/chunk.py:16-67: cumsum, K.K^T, solve_tril, w/u,
+// chunk_fwd_h, chunk_fwd_o) without materialising any stage output in HBM.
+//
+// Every sequence is cut into segments of L consecutive 64-token chunks, so
+// that (segment, head) work items fill the GPU even for one long sequence.
+// Per chunk c the state recurrence is affine in the incoming state S:
+//     S' = M_c S + R_c,   M_c = g I - k^T diag(gate) w,   R_c = k^T diag(gate) u,
+// with g = exp(gc_last) and gate_t = exp(gc_last - gc_t) (chunk_delta_h.py:163-211).
+//
+//   seg_trans_kernel    (segment, head): recomputes the chunk-local WY
+//                       representation and accumulates the segment's affine map
+//                       [M | R] (K x (K+V), fp32) starting from [I | 0].
+//   seg_combine_kernel  (sequence, head, 16 V columns): serial over segments,
+//                       S_{j+1} = M_j S_j + R_j in fp32, from initial_state.
+//   seg_out_kernel      (segment, head): recomputes the WY representation,
+//                       runs the exact recurrence of chunk_delta_h.py from the
+//                       segment's initial state and emits o (chunk_o.py:84-128)
+//                       and, for the last segment, final_state.
+//
+// One workgroup = 4 waves.  Per chunk, the chunk's q, k (row-major and
+// transposed) and v (transposed) are staged in LDS; the state tile of each
+// wave (K rows x V/4 columns) lives in VGPRs in the MFMA accumulator layout
+// for the whole segment.  The next chunk's inputs are loaded into registers
+// while the current chunk computes.
+//
+// LDS operand layout.  All MFMA operands are read as one 8-element fragment
+// per lane (16 bytes for bf16).  Lane l of a 16x16x32 product feeds the K
+// indices {4(l/16)..+3} and {16+4(l/16)..+3} of a 32-wide step (the order in
+// which an accumulator tile pair is converted into an operand), so every
+// operand row stores each 32-column block permuted by pcol(): logical column
+// 16*hh + 4*lg + j sits at 8*lg + 4*hh + j.  Transposed tiles ([d][t], [v][t])
+// additionally XOR the 8-element chunk index with bits 3..5 of the row to
+// spread the transposing stores over the LDS banks.
+#include "gdn_common.hpp"
+#include "gdn_kernels.h"
+
+namespace kgdn {
+
+namespace {
+
+// Workgroup sizes: seg_out runs one wave per 16 V columns (V/16 waves), seg_trans
+// one wave per 32 columns of [M | R] ((K+V)/32 waves), seg_combine 4 waves.
+template <int K, int V> struct OutCfg { static constexpr int NW = V / 16, NT = 64 * NW; };
+template <int K, int V> struct TransCfg { static constexpr int NW = (K + V) / 32, NT = 64 * NW; };
+constexpr int NT_COMB = 256;
+constexpr int NW_COMB = 4;
+
+__device__ __forceinline__ int pcol(int c) {
+  return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
+}
+// physical column of logical token t in row `row` of a transposed [*][64] tile
+__device__ __forceinline__ int tcol(int row, int t) { return pcol(t) ^ (((row >> 3) & 7) << 3); }
+// physical start of the 8-element fragment chunk `chunk8` (a multiple of 8, already in pcol order)
+__device__ __forceinline__ int tchunk(int row, int chunk8) { return chunk8 ^ (((row >> 3) & 7) << 3); }
+
+template <typename TC>
+__device__ __forceinline__ Frag<TC> frag_at(const TC* p) {
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    f.v = *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    f.lo = *reinterpret_cast<const f32x4*>(p);
+    f.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return f;
+}
+// the two bf16 values packed in a dword, as floats
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// 8 consecutive LDS elements as floats
+template <typename TC>
+__device__ __forceinline__ void lds_get8(const TC* p, float (&x)[8]) {
+  if constexpr (sizeof(TC) == 2) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    x[0] = bf16_lo(r.x); x[1] = bf16_hi(r.x); x[2] = bf16_lo(r.y); x[3] = bf16_hi(r.y);
+    x[4] = bf16_lo(r.z); x[5] = bf16_hi(r.z); x[6] = bf16_lo(r.w); x[7] = bf16_hi(r.w);
+  } else {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = b[e];
+    }
+  }
+}
+// operand fragment from 8 floats, rounded to TC
+template <typename TC>
+__device__ __forceinline__ Frag<TC> frag_pack(const float (&x)[8]) {
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    bf16x8 v = {(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3], (bf16)x[4], (bf16)x[5], (bf16)x[6], (bf16)x[7]};
+    f.v = v;
+  } else {
+    f.lo = f32x4{x[0], x[1], x[2], x[3]};
+    f.hi = f32x4{x[4], x[5], x[6], x[7]};
+  }
+  return f;
+}
+// Operand fragment from two accumulator tiles (rows 4*lg+j of tile a, then of tile b), rounded to TC.
+template <typename TC>
+__device__ __forceinline__ Frag<TC> acc_frag(const f32x4& a, const f32x4& b) {
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    bf16x8 v = {(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3], (bf16)b[0], (bf16)b[1], (bf16)b[2], (bf16)b[3]};
+    f.v = v;
+  } else {
+    f.lo = a;
+    f.hi = b;
+  }
+  return f;
+}
+// logical token index of element e of the fragment a lane of group lg holds for 32-step ks
+__device__ __forceinline__ int frag_t(int ks, int lg, int e) { return 32 * ks + 16 * (e >> 2) + 4 * lg + (e & 3); }
+
+// 2 consecutive storage elements
+template <typename TC>
+__device__ __forceinline__ void st2(TC* p, float a, float b) {
+  if constexpr (sizeof(TC) == 2) {
+    typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+    bf16x2 v = {(bf16)a, (bf16)b};
+    *reinterpret_cast<bf16x2*>(p) = v;
+  } else {
+    f32x2 v = {a, b};
+    *reinterpret_cast<f32x2*>(p) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// problem geometry shared by the three kernels
+// ---------------------------------------------------------------------------
+struct SegGeom {
+  const int64_t* cu;          // varlen token offsets [N+1] or nullptr
+  const int32_t* chunk_off;   // varlen chunk offsets [N+1]
+  const int32_t* seg_off;     // varlen segment offsets [N+1]
+  int N;
+  int64_t T;                  // fixed length: per-sequence length
+  int H;
+  int L;                      // chunks per segment
+  int nseg_fixed;             // fixed length: segments per sequence
+};
+
+struct SegLoc {
+  int n, j, nseg;             // sequence, segment index within it, segments of the sequence
+  int64_t bos, eos;           // token range of the sequence
+  int64_t c0;                 // first chunk (within the sequence) of the segment
+  int nch;                    // chunks in the segment
+  bool ok;
+};
+
+__device__ __forceinline__ SegLoc locate_seg(int s, const SegGeom& G) {
+  SegLoc r;
+  r.ok = false;
+  if (G.cu == nullptr) {
+    if (s >= G.N * G.nseg_fixed) return r;
+    r.n = s / G.nseg_fixed;
+    r.j = s % G.nseg_fixed;
+    r.nseg = G.nseg_fixed;
+    r.bos = (int64_t)r.n * G.T;
+    r.eos = r.bos + G.T;
+  } else {
+    if (s >= G.seg_off[G.N]) return r;
+    int lo = 0, hi = G.N - 1;      // last n with seg_off[n] <= s
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (G.seg_off[mid] <= s) lo = mid; else hi = mid - 1;
+    }
+    r.n = lo;
+    r.j = s - G.seg_off[lo];
+    r.nseg = G.seg_off[lo + 1] - G.seg_off[lo];
+    r.bos = G.cu[lo];
+    r.eos = G.cu[lo + 1];
+  }
+  const int64_t nc = (r.eos - r.bos + C - 1) / C;
+  r.c0 = (int64_t)r.j * G.L;
+  r.nch = (int)min((int64_t)G.L, nc - r.c0);
+  r.ok = r.nch > 0;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// LDS layout of one workgroup
+// ---------------------------------------------------------------------------
+template <typename TC, int K, int V, bool WITH_Q>
+struct SegLds {
+  static constexpr int LDK = K + 8;        // row stride of [64][K] tiles (q, k, w)
+  static constexpr int LDT = C + 8;        // row stride of [*][64] tiles (kT, vT, Ai, Aqk)
+  static constexpr int LDA = C + 4;        // row stride of the fp32 solve workspace
+  static constexpr size_t a16(size_t x) { return (x + 15) / 16 * 16; }
+  static constexpr size_t k_bytes = sizeof(TC) * C * LDK;
+  static constexpr size_t A_bytes = sizeof(float) * C * LDA;
+  // s_k, later s_w (w is produced after the last read of k)
+  static constexpr size_t off_k = 0;
+  static constexpr size_t off_q = a16(off_k + k_bytes);
+  static constexpr size_t off_kT = a16(off_q + (WITH_Q ? k_bytes : 0));
+  static constexpr size_t off_vT = a16(off_kT + sizeof(TC) * K * LDT);
+  static constexpr size_t off_A = a16(off_vT + sizeof(TC) * V * LDT);
+  static constexpr size_t off_Ai = a16(off_A + A_bytes);
+  static constexpr size_t off_Aqk = a16(off_Ai + sizeof(TC) * C * LDT);
+  static constexpr size_t off_g = a16(off_Aqk + (WITH_Q ? sizeof(TC) * C * LDT : 0));
+  static constexpr size_t total = off_g + sizeof(float) * 3 * C;
+};
+
+// ---------------------------------------------------------------------------
+// chunk inputs held in registers between chunks (the prefetch), in storage format
+// ---------------------------------------------------------------------------
+template <typename T> struct Raw8;                    // 8 consecutive input elements, as loaded
+template <> struct Raw8<bf16> { uint4 v; };
+template <> struct Raw8<float> { f32x4 lo, hi; };
+template <> struct Raw8<uint8_t> { uint2 v; };        // fp8 e4m3 codes
+
+template <typename T>
+__device__ __forceinline__ Raw8<T> raw_load(const T* p) {
+  Raw8<T> r;
+  if constexpr (sizeof(T) == 1) {
+    r.v = *reinterpret_cast<const uint2*>(p);
+  } else if constexpr (sizeof(T) == 2) {
+    r.v = *reinterpret_cast<const uint4*>(p);
+  } else {
+    r.lo = *reinterpret_cast<const f32x4*>(p);
+    r.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ Raw8<T> raw_zero() {
+  Raw8<T> r;
+  if constexpr (sizeof(T) == 1) {
+    r.v = make_uint2(0u, 0u);
+  } else if constexpr (sizeof(T) == 2) {
+    r.v = make_uint4(0u, 0u, 0u, 0u);
+  } else {
+    r.lo = f32x4{0.f, 0.f, 0.f, 0.f};
+    r.hi = r.lo;
+  }
+  return r;
+}
+// the 8 elements as floats (fp8 codes are dequantised with the per-head scale)
+template <typename T>
+__device__ __forceinline__ void raw_get8(const Raw8<T>& r, float scale, float (&x)[8]) {
+  if constexpr (sizeof(T) == 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = fp8e4m3_to_f32((r.v.x >> (8 * e)) & 0xFF) * scale;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[4 + e] = fp8e4m3_to_f32((r.v.y >> (8 * e)) & 0xFF) * scale;
+  } else if constexpr (sizeof(T) == 2) {
+    x[0] = bf16_lo(r.v.x); x[1] = bf16_hi(r.v.x); x[2] = bf16_lo(r.v.y); x[3] = bf16_hi(r.v.y);
+    x[4] = bf16_lo(r.v.z); x[5] = bf16_hi(r.v.z); x[6] = bf16_lo(r.v.w); x[7] = bf16_hi(r.v.w);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = r.lo[e];
+      x[4 + e] = r.hi[e];
+    }
+  }
+}
+
+template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
+struct ChunkRegs {
+  static constexpr int QU = C * (K / 8), KU = (C / 2) * (K / 8), VU = (C / 2) * (V / 8);   // work units
+  static constexpr int QJ = (QU + NT - 1) / NT;     // 8-element row pieces of q per thread
+  static constexpr int KJ = (KU + NT - 1) / NT;     // row-pair pieces of k per thread
+  static constexpr int VJ = (VU + NT - 1) / NT;     // row-pair pieces of v per thread
+  Raw8<TQ> q[WITH_Q ? QJ : 1];
+  Raw8<TQ> k[KJ][2];
+  Raw8<TC> v[VJ][2];
+  float g, b;
+};
+
+template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
+__device__ __forceinline__ void load_chunk(ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, const void* qp, const void* kp,
+                                           const void* vp, const void* gp, const void* bp, int g_dt, int b_dt,
+                                           int64_t t0, int nv, int h, int H) {
+  using CR = ChunkRegs<TC, TQ, K, V, WITH_Q, NT>;
+  const int tid = threadIdx.x;
+  const TQ* q = reinterpret_cast<const TQ*>(qp);
+  const TQ* k = reinterpret_cast<const TQ*>(kp);
+  const TC* v = reinterpret_cast<const TC*>(vp);
+  if constexpr (WITH_Q) {
+#pragma unroll
+    for (int i = 0; i < CR::QJ; ++i) {
+      const int idx = tid + NT * i;
+      const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+      if (idx < CR::QU && r < nv) R.q[i] = raw_load<TQ>(q + ((t0 + r) * H + h) * K + c8);
+      else R.q[i] = raw_zero<TQ>();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CR::KJ; ++i) {
+    const int idx = tid + NT * i;
+    const int p = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = 2 * p + rr;
+      if (idx < CR::KU && r < nv) R.k[i][rr] = raw_load<TQ>(k + ((t0 + r) * H + h) * K + c8);
+      else R.k[i][rr] = raw_zero<TQ>();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CR::VJ; ++i) {
+    const int idx = tid + NT * i;
+    const int p = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = 2 * p + rr;
+      if (idx < CR::VU && r < nv) R.v[i][rr] = raw_load<TC>(v + ((t0 + r) * H + h) * V + c8);
+      else R.v[i][rr] = raw_zero<TC>();
+    }
+  }
+  R.g = 0.f;
+  R.b = 0.f;
+  if (tid < C && tid < nv) {
+    R.g = ld_scalar(gp, (t0 + tid) * H + h, g_dt);
+    R.b = ld_scalar(bp, (t0 + tid) * H + h, b_dt);
+  }
+}
+
+// Registers -> LDS; wave 0 also forms the chunk-local cumsum of g (fla ops/utils/cumsum.py:58-65).
+template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
+__device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, unsigned char* smem,
+                                            float qs, float ks) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  using CR = ChunkRegs<TC, TQ, K, V, WITH_Q, NT>;
+  TC* s_k = reinterpret_cast<TC*>(smem + L::off_k);
+  TC* s_q = reinterpret_cast<TC*>(smem + L::off_q);
+  TC* s_kT = reinterpret_cast<TC*>(smem + L::off_kT);
+  TC* s_vT = reinterpret_cast<TC*>(smem + L::off_vT);
+  float* s_g = reinterpret_cast<float*>(smem + L::off_g);
+  const int tid = threadIdx.x;
+  if constexpr (WITH_Q) {
+#pragma unroll
+    for (int i = 0; i < CR::QJ; ++i) {
+      const int idx = tid + NT * i;
+      if (CR::QJ * NT != CR::QU && idx >= CR::QU) continue;
+      const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+      float x[8];
+      raw_get8<TQ>(R.q[i], qs, x);
+      st4<TC>(s_q + r * L::LDK + pcol(c8), x[0], x[1], x[2], x[3]);
+      st4<TC>(s_q + r * L::LDK + pcol(c8 + 4), x[4], x[5], x[6], x[7]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CR::KJ; ++i) {
+    const int idx = tid + NT * i;
+    if (CR::KJ * NT != CR::KU && idx >= CR::KU) continue;
+    const int p = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+    float x[2][8];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      raw_get8<TQ>(R.k[i][rr], ks, x[rr]);
+      TC* row = s_k + (2 * p + rr) * L::LDK;
+      st4<TC>(row + pcol(c8), x[rr][0], x[rr][1], x[rr][2], x[rr][3]);
+      st4<TC>(row + pcol(c8 + 4), x[rr][4], x[rr][5], x[rr][6], x[rr][7]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = c8 + e;
+      st2<TC>(s_kT + d * L::LDT + tcol(d, 2 * p), x[0][e], x[1][e]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CR::VJ; ++i) {
+    const int idx = tid + NT * i;
+    if (CR::VJ * NT != CR::VU && idx >= CR::VU) continue;
+    const int p = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
+    float x0[8], x1[8];
+    raw_get8<TC>(R.v[i][0], 1.f, x0);
+    raw_get8<TC>(R.v[i][1], 1.f, x1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int vv = c8 + e;
+      st2<TC>(s_vT + vv * L::LDT + tcol(vv, 2 * p), x0[e], x1[e]);
+    }
+  }
+  if (tid < WAVE) {
+    float gv = R.g;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+      const float o = __shfl_up(gv, off, WAVE);
+      if (tid >= off) gv += o;
+    }
+    s_g[tid] = gv;                 // gc
+    s_g[C + tid] = gexp(gv);       // exp(gc)
+    s_g[2 * C + tid] = R.b;        // beta
+  }
+}
+
+// ---------------------------------------------------------------------------
+// chunk-local WY representation, shared by seg_trans and seg_out
+//   A   = beta_i exp(gc_i - gc_j) k_i.k_j (i > j)      chunk_scaled_dot_kkt.py:57-73
+//   Aqk = exp(gc_i - gc_j) q_i.k_j (i >= j)             chunk_o.py:109-118
+//   Ai  = (I + A)^-1, rounded to TC                      solve_tril.py:184-331
+//   w   = Ai (k beta exp(gc)) -> LDS (row-major)        wy_fast.py:67-81
+// u = Ai (v beta) is formed by the caller for the columns it owns.
+// ---------------------------------------------------------------------------
+template <typename TC, int K, int V, bool WITH_Q, int NW>
+__device__ __forceinline__ void wy_chunk(unsigned char* smem, int nv, bool beta_lowp) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  TC* s_k = reinterpret_cast<TC*>(smem + L::off_k);
+  TC* s_w = s_k;
+  const TC* s_q = reinterpret_cast<const TC*>(smem + L::off_q);
+  const TC* s_kT = reinterpret_cast<const TC*>(smem + L::off_kT);
+  float* s_A = reinterpret_cast<float*>(smem + L::off_A);
+  TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);
+  TC* s_Aqk = reinterpret_cast<TC*>(smem + L::off_Aqk);
+  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
+  const float* s_eg = s_g + C;
+  const float* s_b = s_g + 2 * C;
+  const int tid = threadIdx.x;
+  const int wid = tid / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+
+  // ---- A (10 lower tiles) and, with q, Aqk (10 lower tiles + the 2 upper tiles its
+  //      fragments touch, written as zeros)
+  constexpr int NJOB = WITH_Q ? 22 : 10;
+  for (int job = wid; job < NJOB; job += NW) {
+    const bool isA = job < 10;
+    int tm, tn;
+    bool zero = false;
+    if (job < 20) {
+      const int tile = isA ? job : job - 10;
+      tm = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
+      tn = tile - tm * (tm + 1) / 2;
+    } else {
+      tm = job == 20 ? 0 : 2;
+      tn = tm + 1;
+      zero = true;
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (!zero) {
+      const TC* a_src = isA ? s_k : s_q;
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks)
+        mma(acc, frag_at<TC>(a_src + (16 * tm + lc) * L::LDK + 32 * ks + 8 * lg),
+            frag_at<TC>(s_k + (16 * tn + lc) * L::LDK + 32 * ks + 8 * lg));
+    }
+    const int j = 16 * tn + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int i = 16 * tm + 4 * lg + jj;
+      if (isA) {
+        float val = 0.f;
+        if (i > j && i < nv) val = acc[jj] * gexp(s_g[i] - s_g[j]) * s_b[i];
+        s_A[i * L::LDA + j] = val;
+      } else {
+        float val = 0.f;
+        if (!zero && i >= j && i < nv) val = acc[jj] * gexp(s_g[i] - s_g[j]);
+        s_Aqk[i * L::LDT + pcol(j)] = from_f32<TC>(val);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- (I + A)^-1: the four 16x16 diagonal blocks by forward substitution
+  //      (wave 0, lane = one column of one block), in place
+  {
+    float x[16];
+    float* Xb = s_A + (16 * lg) * L::LDA + 16 * lg;
+    if (wid == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < i; ++r) s = fmaf(Xb[i * L::LDA + r], x[r], s);
+        x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -s);
+      }
+    }
+    __syncthreads();
+    if (wid == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Xb[i * L::LDA + lc] = x[i];
+    }
+  }
+  __syncthreads();
+  //      block merges (fp32 MFMA): X_ij = -X_ii sum_k L_ik X_kj, kept in the unused
+  //      upper block (j, i) so the strictly lower blocks stay intact for later levels
+  auto blk = [&](int i, int j) { return s_A + (16 * i) * L::LDA + 16 * j; };
+  auto put_neg = [&](float* dst, const f32x4& r) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) dst[(4 * lg + jj) * L::LDA + lc] = -r[jj];
+  };
+  if (wid < 3) {
+    const int i = wid + 1, j = wid;
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
+    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
+    put_neg(blk(j, i), r);
+  }
+  __syncthreads();
+  if (wid < 2) {
+    const int i = wid + 2, j = wid;
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
+    mma16_f32_lds(t, blk(i, j + 1), L::LDA, blk(j, j + 1), L::LDA);
+    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
+    put_neg(blk(j, i), r);
+  }
+  __syncthreads();
+  if (wid == 0) {
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(3, 0), L::LDA, blk(0, 0), L::LDA);
+    mma16_f32_lds(t, blk(3, 1), L::LDA, blk(0, 1), L::LDA);
+    mma16_f32_lds(t, blk(3, 2), L::LDA, blk(0, 2), L::LDA);
+    mma16_f32_lds_reg(r, blk(3, 3), L::LDA, t);
+    put_neg(blk(0, 3), r);
+  }
+  __syncthreads();
+
+  // ---- Ai rounded to TC, row-major [t][t'] in pcol order
+  for (int idx = tid; idx < C * C / 2; idx += 64 * NW) {
+    const int i = idx / (C / 2), j = 2 * (idx % (C / 2));
+    const int bi = i >> 4, bj = j >> 4;
+    float x0 = 0.f, x1 = 0.f;
+    if (bi == bj) {
+      x0 = s_A[i * L::LDA + j];
+      x1 = s_A[i * L::LDA + j + 1];
+    } else if (bi > bj) {
+      x0 = s_A[(16 * bj + (i & 15)) * L::LDA + 16 * bi + (j & 15)];
+      x1 = s_A[(16 * bj + (i & 15)) * L::LDA + 16 * bi + (j & 15) + 1];
+    }
+    st2<TC>(s_Ai + i * L::LDT + pcol(j), x0, x1);
+  }
+  __syncthreads();
+
+  // ---- w^T = kb^T Ai^T (rows d, cols t): K/16 x 4 tiles over the waves -> s_w[t][d]
+  for (int job = wid; job < (K / 16) * 4; job += NW) {
+    const int dt = job >> 2, tn = job & 3;
+    const int d = 16 * dt + lc;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks <= tn / 2) {
+        float x[8];
+        lds_get8<TC>(s_kT + d * L::LDT + tchunk(d, 32 * ks + 8 * lg), x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = frag_t(ks, lg, e);
+          float kb = x[e] * s_b[t];
+          if (beta_lowp) kb = round_to<TC>(kb);
+          x[e] = kb * s_eg[t];
+        }
+        mma(acc, frag_pack<TC>(x), frag_at<TC>(s_Ai + (16 * tn + lc) * L::LDT + 32 * ks + 8 * lg));
+      }
+    }
+    st4<TC>(s_w + (16 * tn + lc) * L::LDK + pcol(16 * dt + 4 * lg), acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
+// u tile (rows 16*tm.., V columns v0..v0+15) = Ai (v beta), rounded to TC (wy_fast.py:61-66)
+template <typename TC, int K, int V, bool WITH_Q>
+__device__ __forceinline__ f32x4 u_tile(const unsigned char* smem, int tm, int v0) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  const TC* s_vT = reinterpret_cast<const TC*>(smem + L::off_vT);
+  const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
+  const float* s_b = reinterpret_cast<const float*>(smem + L::off_g) + 2 * C;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int vv = v0 + lc;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    if (ks <= tm / 2) {
+      float x[8];
+      lds_get8<TC>(s_vT + vv * L::LDT + tchunk(vv, 32 * ks + 8 * lg), x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= s_b[frag_t(ks, lg, e)];
+      mma(acc, frag_at<TC>(s_Ai + (16 * tm + lc) * L::LDT + 32 * ks + 8 * lg), frag_pack<TC>(x));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = round_to<TC>(acc[j]);
+  return acc;
+}
+
+// S (K x 16*CT per wave, accumulator tiles) <- exp(g_last) S + k^T vg, with vg given as operand fragments
+template <typename TC, int K, int V, bool WITH_Q, int CT>
+__device__ __forceinline__ void state_update(f32x4 (&S)[K / 16][CT], const Frag<TC> (&vg)[2][CT],
+                                             const unsigned char* smem, float gamma) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  const TC* s_kT = reinterpret_cast<const TC*>(smem + L::off_kT);
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+#pragma unroll
+  for (int tt = 0; tt < K / 16; ++tt) {
+    const int d = 16 * tt + lc;
+    const Frag<TC> a0 = frag_at<TC>(s_kT + d * L::LDT + tchunk(d, 8 * lg));
+    const Frag<TC> a1 = frag_at<TC>(s_kT + d * L::LDT + tchunk(d, 32 + 8 * lg));
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      S[tt][ct] *= gamma;
+      mma(S[tt][ct], a0, vg[0][ct]);
+      mma(S[tt][ct], a1, vg[1][ct]);
+    }
+  }
+}
+
+// Y (64 x 16*CT) = U - w X, with X given as operand fragments of its K rows
+template <typename TC, int K, int V, bool WITH_Q, int CT>
+__device__ __forceinline__ void sub_wx(f32x4 (&Y)[4][CT], const Frag<TC> (&xb)[K / 32][CT], const unsigned char* smem) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  const TC* s_w = reinterpret_cast<const TC*>(smem + L::off_k);
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) {
+    f32x4 p[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) p[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) {
+      const Frag<TC> a = frag_at<TC>(s_w + (16 * tm + lc) * L::LDK + 32 * ks + 8 * lg);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) mma(p[ct], a, xb[ks][ct]);
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) Y[tm][ct] -= p[ct];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// seg_out: exact recurrence + output over one segment
+// ---------------------------------------------------------------------------
+struct SegOutArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* q_scale;
+  const float* k_scale;
+  int g_dtype, beta_dtype;
+  const void* h0;             // [N, H, K, V] or nullptr
+  int h0_dtype;
+  const float* s_init;        // [NS, H, K, V] fp32 state at each segment start (j >= 1)
+  float scale;
+  void* o;                    // [B*T, H, V]
+  float* ht;                  // [N, H, K, V] or nullptr
+};
+
+template <typename TC, typename TQ, int K, int V>
+__global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
+  using L = SegLds<TC, K, V, true>;
+  constexpr int NW = OutCfg<K, V>::NW, NT = OutCfg<K, V>::NT;
+  using CR = ChunkRegs<TC, TQ, K, V, true, NT>;
+  constexpr int CT = 1;                 // 16-column tiles per wave
+  constexpr int KT = K / 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const TC* s_q = reinterpret_cast<const TC*>(smem + L::off_q);
+  const TC* s_Aqk = reinterpret_cast<const TC*>(smem + L::off_Aqk);
+  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
+
+  const int h = blockIdx.y;
+  const int H = G.H;
+  const SegLoc sl = locate_seg(blockIdx.x, G);
+  if (!sl.ok) return;
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int vw = wid * 16 * CT;         // first V column of this wave
+  const float qs = a.q_scale ? a.q_scale[h] : 1.f;
+  const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
+  const bool beta_lowp = a.beta_dtype == DT_BF16 && sizeof(TC) == 2;
+
+  // ---- initial state of the segment (lane element (tt, ct, j): row 16*tt + 4*lg + j, column vw + 16*ct + lc)
+  f32x4 S[KT][CT];
+  {
+    const int lane_off = 4 * lg * V + vw + lc;
+    if (sl.j == 0 && a.h0 && a.h0_dtype == DT_F32) {
+      const float* p = reinterpret_cast<const float*>(a.h0) + ((int64_t)sl.n * H + h) * K * V + lane_off;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[tt][ct][j] = p[(16 * tt + j) * V + 16 * ct];
+    } else if (sl.j == 0 && a.h0) {
+      const bf16* p = reinterpret_cast<const bf16*>(a.h0) + ((int64_t)sl.n * H + h) * K * V + lane_off;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[tt][ct][j] = (float)p[(16 * tt + j) * V + 16 * ct];
+    } else if (sl.j > 0) {
+      const float* p = a.s_init + ((int64_t)blockIdx.x * H + h) * K * V + lane_off;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[tt][ct][j] = p[(16 * tt + j) * V + 16 * ct];
+    } else {
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) S[tt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  CR cur;
+  int64_t t0 = sl.bos + sl.c0 * C;
+  int nv = (int)min((int64_t)C, sl.eos - t0);
+  load_chunk<TC, TQ, K, V, true, NT>(cur, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
+  TC* o = reinterpret_cast<TC*>(a.o);
+
+  for (int ci = 0; ci < sl.nch; ++ci) {
+    stage_chunk<TC, TQ, K, V, true, NT>(cur, smem, qs, ks_);
+    __syncthreads();
+    const int64_t t0c = t0;
+    const int nvc = nv;
+    if (ci + 1 < sl.nch) {
+      t0 += C;
+      nv = (int)min((int64_t)C, sl.eos - t0);
+      load_chunk<TC, TQ, K, V, true, NT>(cur, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
+    }
+    wy_chunk<TC, K, V, true, NW>(smem, nvc, beta_lowp);
+    // u of the owned columns (independent of w; overlaps the w stores of other waves)
+    f32x4 Y[4][CT];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) Y[tm][ct] = u_tile<TC, K, V, true>(smem, tm, vw + 16 * ct);
+    }
+    __syncthreads();   // w complete
+
+    // ---- h = S rounded (the snapshot of chunk_delta_h.py:129-139) as operand fragments
+    Frag<TC> hb[K / 32][CT];
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) hb[ks][ct] = acc_frag<TC>(S[2 * ks][ct], S[2 * ks + 1][ct]);
+    }
+    // ---- v' = u - w h                                   (chunk_delta_h.py:141-157)
+    sub_wx<TC, K, V, true, CT>(Y, hb, smem);
+
+    // ---- o^T = scale (h^T q^T exp(gc) + v_new^T Aqk^T)   (chunk_o.py:84-128)
+    Frag<TC> vn[2][CT];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) vn[ks][ct] = acc_frag<TC>(Y[2 * ks][ct], Y[2 * ks + 1][ct]);
+    }
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      const int t = 16 * tn + lc;
+      f32x4 o1[CT], o2[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        o1[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        o2[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks) {
+        const Frag<TC> bq = frag_at<TC>(s_q + t * L::LDK + 32 * ks + 8 * lg);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) mma(o1[ct], hb[ks][ct], bq);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks <= tn / 2) {
+          const Frag<TC> ba = frag_at<TC>(s_Aqk + t * L::LDT + 32 * ks + 8 * lg);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) mma(o2[ct], vn[ks][ct], ba);
+        }
+      }
+      if (t < nvc) {
+        const float eg = s_g[C + t] * a.scale;
+        TC* orow = o + ((t0c + t) * H + h) * V + vw + 4 * lg;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          st4<TC>(orow + 16 * ct, o1[ct][0] * eg + o2[ct][0] * a.scale, o1[ct][1] * eg + o2[ct][1] * a.scale,
+                  o1[ct][2] * eg + o2[ct][2] * a.scale, o1[ct][3] * eg + o2[ct][3] * a.scale);
+        }
+      }
+    }
+
+    // ---- S = exp(g_last) S + k^T (v' exp(g_last - gc))   (chunk_delta_h.py:163-211)
+    const float gl = s_g[nvc - 1];
+    Frag<TC> vg[2][CT];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        f32x4 ya = Y[2 * ks][ct], yb = Y[2 * ks + 1][ct];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ta = 32 * ks + 4 * lg + j, tb = ta + 16;
+          ya[j] = ta < nvc ? ya[j] * gexp(gl - s_g[ta]) : 0.f;
+          yb[j] = tb < nvc ? yb[j] * gexp(gl - s_g[tb]) : 0.f;
+        }
+        vg[ks][ct] = acc_frag<TC>(ya, yb);
+      }
+    }
+    state_update<TC, K, V, true, CT>(S, vg, smem, gexp(gl));
+    __syncthreads();   // LDS is restaged for the next chunk
+  }
+
+  if (a.ht && sl.j == sl.nseg - 1) {
+    float* p = a.ht + ((int64_t)sl.n * H + h) * K * V + 4 * lg * V + vw + lc;
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * V + 16 * ct] = S[tt][ct][j];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// seg_trans: affine map [M | R] of one segment (all but the last segment of a sequence)
+// ---------------------------------------------------------------------------
+struct SegTransArgs {
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const float* k_scale;
+  int g_dtype, beta_dtype;
+  float* M;                   // [NS, H, K, K]
+  float* R;                   // [NS, H, K, V]
+};
+
+template <typename TC, typename TQ, int K, int V>
+__global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTransArgs a, SegGeom G) {
+  using L = SegLds<TC, K, V, false>;
+  constexpr int NW = TransCfg<K, V>::NW, NT = TransCfg<K, V>::NT;
+  using CR = ChunkRegs<TC, TQ, K, V, false, NT>;
+  constexpr int XC = K + V;             // columns of [M | R]
+  static_assert(XC % 32 == 0, "K + V must be a multiple of 32");
+  constexpr int CT = 2;                 // 16-column tiles per wave
+  constexpr int KT = K / 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
+
+  const int h = blockIdx.y;
+  const int H = G.H;
+  const SegLoc sl = locate_seg(blockIdx.x, G);
+  if (!sl.ok || sl.j == sl.nseg - 1) return;
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int xw = wid * 16 * CT;         // first column of [M | R] owned by this wave
+  const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
+  const bool beta_lowp = a.beta_dtype == DT_BF16 && sizeof(TC) == 2;
+
+  f32x4 X[KT][CT];
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) X[tt][ct][j] = (16 * tt + 4 * lg + j == xw + 16 * ct + lc) ? 1.f : 0.f;
+    }
+  }
+
+  CR cur;
+  int64_t t0 = sl.bos + sl.c0 * C;
+  int nv = (int)min((int64_t)C, sl.eos - t0);
+  load_chunk<TC, TQ, K, V, false, NT>(cur, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
+  for (int ci = 0; ci < sl.nch; ++ci) {
+    stage_chunk<TC, TQ, K, V, false, NT>(cur, smem, 1.f, ks_);
+    __syncthreads();
+    const int nvc = nv;
+    if (ci + 1 < sl.nch) {
+      t0 += C;
+      nv = (int)min((int64_t)C, sl.eos - t0);
+      load_chunk<TC, TQ, K, V, false, NT>(cur, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h,
+                                          H);
+    }
+    wy_chunk<TC, K, V, false, NW>(smem, nvc, beta_lowp);
+    f32x4 Y[4][CT];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const int c0 = xw + 16 * ct;
+        Y[tm][ct] = c0 >= K ? u_tile<TC, K, V, false>(smem, tm, c0 - K) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    __syncthreads();   // w complete
+    Frag<TC> xb[K / 32][CT];
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag<TC>(X[2 * ks][ct], X[2 * ks + 1][ct]);
+    }
+    sub_wx<TC, K, V, false, CT>(Y, xb, smem);
+    const float gl = s_g[nvc - 1];
+    Frag<TC> yg[2][CT];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        f32x4 ya = Y[2 * ks][ct], yb = Y[2 * ks + 1][ct];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ta = 32 * ks + 4 * lg + j, tb = ta + 16;
+          ya[j] = ta < nvc ? ya[j] * gexp(gl - s_g[ta]) : 0.f;
+          yb[j] = tb < nvc ? yb[j] * gexp(gl - s_g[tb]) : 0.f;
+        }
+        yg[ks][ct] = acc_frag<TC>(ya, yb);
+      }
+    }
+    state_update<TC, K, V, false, CT>(X, yg, smem, gexp(gl));
+    __syncthreads();
+  }
+
+  const int64_t s = blockIdx.x;
+  float* pm = a.M + (s * H + h) * K * K + 4 * lg * K + xw + lc;
+  float* pr = a.R + (s * H + h) * K * V + 4 * lg * V + xw - K + lc;
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    if (xw + 16 * ct < K) {
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pm[(16 * tt + j) * K + 16 * ct] = X[tt][ct][j];
+    } else {
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pr[(16 * tt + j) * V + 16 * ct] = X[tt][ct][j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// seg_combine: S_{j+1} = M_j S_j + R_j over the segments of a sequence, 16 V
+// columns per workgroup, fp32 (v_mfma_f32_16x16x4f32).  Also writes
+// final_state of sequences without tokens.
+// ---------------------------------------------------------------------------
+struct SegCombineArgs {
+  const float* M;
+  const float* R;
+  const void* h0;
+  int h0_dtype;
+  float* s_init;              // out [NS, H, K, V]
+  float* ht;                  // final_state, written here only for empty sequences
+  int V;
+};
+
+template <int K>
+__global__ __launch_bounds__(NT_COMB) void seg_combine_kernel(SegCombineArgs a, SegGeom G, int total) {
+  constexpr int RT = K / 16 / NW_COMB >= 1 ? K / 16 / NW_COMB : 1;   // row tiles per wave
+  constexpr int NWA = K / 16 / RT;                          // active waves
+  __shared__ __align__(16) float s_S[K][16];
+  const int V = a.V;
+  const int nvt = V / 16;
+  // XCD-aware order: the V slices of one head run on one XCD and share M through its L2
+  const int per_xcd = gridDim.x / 8;
+  const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (o_idx >= total) return;
+  const int unit = o_idx / nvt;
+  const int v0 = (o_idx % nvt) * 16;
+  const int H = G.H;
+  const int n = unit / H, h = unit % H;
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+
+  int nseg, s_first;
+  if (G.cu == nullptr) {
+    nseg = G.T > 0 ? G.nseg_fixed : 0;
+    s_first = n * G.nseg_fixed;
+  } else {
+    nseg = G.seg_off[n + 1] - G.seg_off[n];
+    s_first = G.seg_off[n];
+  }
+  for (int idx = threadIdx.x; idx < K * 16; idx += NT_COMB) {
+    const int r = idx / 16, c = idx % 16;
+    float x = 0.f;
+    if (a.h0) {
+      const int64_t off = (((int64_t)n * H + h) * K + r) * V + v0 + c;
+      x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
+                               : (float)reinterpret_cast<const bf16*>(a.h0)[off];
+    }
+    s_S[r][c] = x;
+  }
+  if (nseg == 0) {
+    if (a.ht) {
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < K * 16; idx += NT_COMB) {
+        const int r = idx / 16, c = idx % 16;
+        a.ht[(((int64_t)n * H + h) * K + r) * V + v0 + c] = s_S[r][c];
+      }
+    }
+    return;
+  }
+  __syncthreads();
+  for (int j = 0; j + 1 < nseg; ++j) {
+    const int64_t s = s_first + j;
+    const float* Ms = a.M + (s * H + h) * K * K;
+    const float* Rs = a.R + (s * H + h) * K * V;
+    f32x4 acc[RT];
+    if (wid < NWA) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int r0 = 16 * (wid * RT + rt);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[rt][jj] = Rs[(int64_t)(r0 + 4 * lg + jj) * V + v0 + lc];
+#pragma unroll 4
+        for (int kk = 0; kk < K / 16; ++kk) {
+          const f32x4 m = *reinterpret_cast<const f32x4*>(Ms + (int64_t)(r0 + lc) * K + 16 * kk + 4 * lg);
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(m[qq], s_S[16 * kk + 4 * lg + qq][lc], acc[rt], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+    if (wid < NWA) {
+      float* out = a.s_init + ((s + 1) * H + h) * K * V;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int r0 = 16 * (wid * RT + rt);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int r = r0 + 4 * lg + jj;
+          s_S[r][lc] = acc[rt][jj];
+          out[(int64_t)r * V + v0 + lc] = acc[rt][jj];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void seg_map_kernel(const int64_t* __restrict__ cu, int N, int L, int32_t* __restrict__ chunk_off,
+                               int32_t* __restrict__ seg_off) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int32_t ca = 0, sa = 0;
+  chunk_off[0] = 0;
+  seg_off[0] = 0;
+  for (int n = 0; n < N; ++n) {
+    const int64_t len = cu[n + 1] - cu[n];
+    const int32_t nc = (int32_t)((len + C - 1) / C);
+    ca += nc;
+    sa += (nc + L - 1) / L;
+    chunk_off[n + 1] = ca;
+    seg_off[n + 1] = sa;
+  }
+}
+
+template <typename Kern>
+int set_lds(Kern kern, size_t bytes) {
+  if (bytes > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)bytes) != hipSuccess)
+      return -1;
+  }
+  return 0;
+}
+
+template <typename TC, typename TQ, int K, int V>
+int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
+  SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
+  const dim3 grid((unsigned)p.ns_grid, (unsigned)p.H);
+  if (p.run_trans) {
+    using LT = SegLds<TC, K, V, false>;
+    static_assert(LT::total <= 160 * 1024, "seg_trans tile does not fit in LDS");
+    auto kt = seg_trans_kernel<TC, TQ, K, V>;
+    if (set_lds(kt, LT::total)) return -1;
+    SegTransArgs ta{p.k, p.v, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, p.M, p.R};
+    hipLaunchKernelGGL(kt, grid, dim3(TransCfg<K, V>::NT), LT::total, s, ta, G);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  if (p.run_combine) {
+    const int total = p.N * p.H * (V / 16);
+    const int cgrid = (total + 7) / 8 * 8;
+    SegCombineArgs ca{p.M, p.R, p.h0, p.h0_dtype, p.s_init, p.ht, V};
+    hipLaunchKernelGGL(seg_combine_kernel<K>, dim3(cgrid), dim3(NT_COMB), 0, s, ca, G, total);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  if (p.ns_grid > 0) {
+    using LO = SegLds<TC, K, V, true>;
+    static_assert(LO::total <= 160 * 1024, "seg_out tile does not fit in LDS");
+    auto ko = seg_out_kernel<TC, TQ, K, V>;
+    if (set_lds(ko, LO::total)) return -1;
+    SegOutArgs oa{p.q, p.k, p.v, p.g, p.beta, p.q_scale, p.k_scale, p.g_dtype, p.beta_dtype,
+                  p.h0, p.h0_dtype, p.s_init, p.scale, p.o, p.ht};
+    hipLaunchKernelGGL(ko, grid, dim3(OutCfg<K, V>::NT), LO::total, s, oa, G);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+bool seg_fwd_supported(int compute_dtype, int K, int V) {
+  if (!(K == 64 || K == 128) || !(V == 64 || V == 128)) return false;
+  return compute_dtype == DT_BF16 || K == 64;
+}
+
+int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s) {
+  hipLaunchKernelGGL(seg_map_kernel, dim3(1), dim3(64), 0, s, cu, N, L, chunk_off, seg_off);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_seg_fwd(const SegFwdArgs& p, int compute_dtype, int qk_dtype, int K, int V, hipStream_t s) {
+#define KGDN_SEG_CASE(TC, TQ, KK, VV) \
+  if (K == KK && V == VV) return launch_seg_t<TC, TQ, KK, VV>(p, s);
+#define KGDN_SEG_SHAPES(TC, TQ) \
+  KGDN_SEG_CASE(TC, TQ, 64, 64) KGDN_SEG_CASE(TC, TQ, 64, 128) \
+  KGDN_SEG_CASE(TC, TQ, 128, 64) KGDN_SEG_CASE(TC, TQ, 128, 128)
+  // fp32 tiles of K = 128 exceed the LDS of one CU: those shapes run the staged kernels
+  if (compute_dtype == DT_F32 && qk_dtype == DT_F32) { KGDN_SEG_CASE(float, float, 64, 64) KGDN_SEG_CASE(float, float, 64, 128) }
+  if (compute_dtype == DT_BF16 && qk_dtype == DT_BF16) { KGDN_SEG_SHAPES(bf16, bf16) }
+  if (compute_dtype == DT_BF16 && qk_dtype == DT_F8E4M3) { KGDN_SEG_SHAPES(bf16, uint8_t) }
+#undef KGDN_SEG_SHAPES
+#undef KGDN_SEG_CASE
+  return -2;
+}
+
+}  // namespace kgdn

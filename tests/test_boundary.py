@@ -49,12 +49,21 @@ def test_num_chunks_bound():
     assert lib.kairos_gdn_num_chunks_bound(1, 53040, 4) >= 830
 
 
-def test_workspace_size_grows_with_problem():
+def test_workspace_size():
+    """The fused bf16 path keeps only per-segment [M | R] maps and segment states in the
+    workspace (bounded by the CU count, not by T); the in-kernel L2 norm adds two q/k
+    copies; the staged fp32 K=128 path holds the reference's per-chunk intermediates."""
     lib = _lib.load()
     a = lib.kairos_gdn_chunk_fwd_workspace_size(1, 8192, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
     b = lib.kairos_gdn_chunk_fwd_workspace_size(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
     c = lib.kairos_gdn_chunk_fwd_workspace_size(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 1)
-    assert 0 < a < b < c
+    assert 0 < a <= b < c
+    assert b < 128 << 20
+    assert c - b == 2 * 32760 * 20 * 128 * 2
+    single = lib.kairos_gdn_chunk_fwd_workspace_size(8, 1560, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
+    assert single == 0                       # one segment per sequence: no scan state
+    staged = lib.kairos_gdn_chunk_fwd_workspace_size(1, 8192, 20, 128, 128, 0, _lib.F32, _lib.F32, 0)
+    assert staged > 8192 * 20 * 128 * 4 * 3
 
 
 FAKE = 0x100000  # aligned non-null address: never dereferenced, validation fails first
