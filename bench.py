@@ -2,17 +2,26 @@
 
 One step = one chunk_gated_delta_rule forward over BASELINE config 2
 (B=1, T=32760, H=20, dk=dv=128, chunk 64, bf16 q/k/v/beta, fp32 g and h0,
-output_final_state=True) with inputs resident in HBM.  Prints ONE JSON line.
+output_final_state=True) with inputs resident in HBM, through the C ABI
+(kairos_gdn_chunk_fwd).  Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+  python bench.py --calibrate-copy 1024     # reference copy kernel for rocprofv3 counter scaling
 
-Per-kernel times come from HIP events recorded on the launch stream around
-each stage (prepare, fwd_h, fwd_o) in a separate staged loop; the roofline
-block uses the slowest kernel's algorithmic bytes per launch.
+`value` is tokens/s of whole forward calls (wall clock between two device
+synchronisations around `steps` back-to-back calls).  Per-kernel times come
+from a second loop in which the library records hipEvents on the launch
+stream around each of its kernels (kairos_gdn_profile_begin/_end).  The
+roofline block is the dominant kernel's algorithmic HBM bytes per launch over
+its average duration; `traffic` is that kernel's measured HBM bytes per launch
+from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, when present.
 """
 import argparse
+import ctypes
 import json
 import os
+import re
+import statistics
 import sys
 import time
 
@@ -25,6 +34,8 @@ METRIC = "GDN chunk-fwd tokens/s + TFLOP/s (% bf16 MFMA peak) at T=32760,H=20,d=
 PEAK_BF16_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 C = 64
+KERNELS = ["seg_trans_kernel", "seg_combine_kernel", "seg_out_kernel"]
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2_hbm_traffic.md")
 
 
 def flops_per_tok_head(K, V):
@@ -32,25 +43,49 @@ def flops_per_tok_head(K, V):
     return 6 * K * V + 6 * C * K + 4 * C * V
 
 
-def kernel_models(B, T, H, K, V, s=2):
-    """Per-launch algorithmic FLOPs and HBM bytes of each kernel (compulsory reads + writes)."""
+def kernel_models(B, T, H, K, V, L, s=2, s_g=4, s_b=2):
+    """Algorithmic HBM bytes (compulsory reads + writes) and FLOPs of one launch of each kernel.
+
+    seg_out reads q, k, v, g, beta and the segment initial states, writes o and
+    final_state; seg_trans reads k, v, g, beta of every segment but the last of
+    each sequence and writes its [M | R]; seg_combine reads [M | R] and h0 and
+    writes the segment initial states.
+    """
+    nc = (T + C - 1) // C
+    nseg = (nc + L - 1) // L
     tok = B * T * H
-    nch = B * ((T + C - 1) // C) * H
+    tok_trans = B * H * min(T, (nseg - 1) * L * C)
+    state = K * V * 4
+    mr = (K * K + K * V) * 4
     return {
-        # reads k, v, g, beta; writes w, u, gc
-        "prepare": dict(flops=tok * 2 * C * (2 * K + V),
-                        bytes=tok * (K * s + V * s + 4 + s) + tok * (K * s + V * s + 4)),
-        # reads k, w, u, gc, h0; writes state snapshots, v_new, final state
-        "fwd_h": dict(flops=tok * 4 * K * V,
-                      bytes=tok * (K * s + K * s + V * s + 4) + nch * K * V * s + tok * V * s + 2 * B * H * K * V * 4),
-        # reads q, k, snapshots, v_new, gc; writes o
-        "fwd_o": dict(flops=tok * (2 * K * V + 2 * C * (K + V)),
-                      bytes=tok * (K * s * 2 + V * s + 4) + nch * K * V * s + tok * V * s),
+        "seg_out_kernel": dict(
+            bytes=tok * (2 * K * s + V * s + V * s + s_g + s_b) + B * H * (nseg - 1) * state + 2 * B * H * state,
+            flops=tok * flops_per_tok_head(K, V)),
+        "seg_trans_kernel": dict(
+            bytes=tok_trans * (K * s + V * s + s_g + s_b) + B * H * (nseg - 1) * mr,
+            flops=tok_trans * (2 * C * (2 * K + V) + 4 * K * (K + V))),
+        "seg_combine_kernel": dict(
+            bytes=B * H * (nseg - 1) * (mr + state) + B * H * state,
+            flops=B * H * (nseg - 1) * 2 * K * K * V),
     }
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                m = re.match(r"\s*traffic_bytes_per_launch\s+(\S+)\s+(\d+)", ln)
+                if m and m.group(1) == kernel:
+                    return int(m.group(2))
+    except OSError:
+        pass
+    return None
 
 
 def make_inputs(B, T, H, K, V, seed, device):
     g_ = torch.Generator(device="cpu").manual_seed(seed)
+
     def unit(shape):
         x = torch.randn(shape, generator=g_)
         return torch.nn.functional.normalize(x, dim=-1)
@@ -63,26 +98,34 @@ def make_inputs(B, T, H, K, V, seed, device):
     return q, k, v, g, beta, h0
 
 
-def cpu_baseline(T, H, K, V, heads, seed):
-    """Time the numpy oracle (bf16-emulating chunked restatement) on `heads` of the config on the host."""
+def cpu_baseline(T, H, K, V, seed, min_seconds=10.0):
+    """Time the numpy oracle (bf16-emulating chunked restatement) on the host cores.
+
+    The sample is the full config (all H heads of T tokens), repeated until at
+    least `min_seconds` of CPU work; the rate is the median over repeats.
+    """
     sys.path.insert(0, ROOT)
     import numpy as np
     from threadpoolctl import threadpool_info, threadpool_limits
     from oracle import gdn_oracle as O
     cores = min(os.cpu_count() or 1, 16)
     rng = np.random.default_rng(seed)
+
     def unit(shape):
         x = rng.standard_normal(shape, dtype=np.float32)
         return O.to_bf16(x / np.sqrt((x * x).sum(-1, keepdims=True)))
-    q, k = unit((1, T, heads, K)), unit((1, T, heads, K))
-    v = O.to_bf16(rng.standard_normal((1, T, heads, V), dtype=np.float32))
-    beta = O.to_bf16(1 / (1 + np.exp(-rng.standard_normal((1, T, heads), dtype=np.float32))))
-    g = (-np.logaddexp(0, rng.standard_normal((1, T, heads), dtype=np.float32))).astype(np.float32)
-    h0 = (0.02 * rng.standard_normal((1, heads, K, V), dtype=np.float32)).astype(np.float32)
+    q, k = unit((1, T, H, K)), unit((1, T, H, K))
+    v = O.to_bf16(rng.standard_normal((1, T, H, V), dtype=np.float32))
+    beta = O.to_bf16(1 / (1 + np.exp(-rng.standard_normal((1, T, H), dtype=np.float32))))
+    g = (-np.logaddexp(0, rng.standard_normal((1, T, H), dtype=np.float32))).astype(np.float32)
+    h0 = (0.02 * rng.standard_normal((1, H, K, V), dtype=np.float32)).astype(np.float32)
+    times = []
     with threadpool_limits(cores):
-        t0 = time.perf_counter()
-        O.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True, dtype="bf16")
-        dt = time.perf_counter() - t0
+        t_start = time.perf_counter()
+        while not times or (time.perf_counter() - t_start < min_seconds and len(times) < 10):
+            t0 = time.perf_counter()
+            O.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True, dtype="bf16")
+            times.append(time.perf_counter() - t0)
         blas = [i.get("num_threads") for i in threadpool_info()]
     model = ""
     try:
@@ -90,11 +133,11 @@ def cpu_baseline(T, H, K, V, heads, seed):
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
-    # tokens/s of the full H-head config: the sample covers heads/H of the work
-    value = T * heads / H / dt
-    return {"value": value, "unit": "tokens/s", "cores": max(blas) if blas else cores, "kind": "port",
-            "sample": f"numpy oracle (oracle/gdn_oracle.py, bf16 cast points) on T={T}, {heads} of {H} heads; "
-                      f"{dt:.2f} s; rate scaled to all {H} heads; host CPU: {model}"}
+    dt = statistics.median(times)
+    return {"value": T / dt, "unit": "tokens/s", "cores": max(blas) if blas else cores, "kind": "port",
+            "sample": f"numpy oracle (oracle/gdn_oracle.py, bf16 cast points) on the full workload "
+                      f"(T={T}, all {H} heads), {len(times)} runs in {sum(times):.1f} s, median {dt:.2f} s per "
+                      f"forward; host CPU: {model}"}
 
 
 def main():
@@ -103,7 +146,6 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=2)
     ap.add_argument("--T", type=int, default=32760)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a plain elementwise copy of MIB MiB (fp32 y = x * 1) 5 times and exit: the "
@@ -126,14 +168,14 @@ def main():
         print(json.dumps({"calibrate_copy_bytes_read": 4 * n, "calibrate_copy_bytes_written": 4 * n}), flush=True)
         return
 
-    import kairos_gdn
+    import kairos_gdn  # noqa: F401
     from kairos_gdn import _lib
     B, T, H, K, V = 1, args.T, 20, 128, 128
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)
     scale = K ** -0.5
     lib = _lib.load()
     ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     o = torch.empty_like(v)
     ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
@@ -153,45 +195,26 @@ def main():
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
 
-    # ---- per-kernel times: the same three launches issued stage by stage, HIP events on the launch stream
-    nc = lib.kairos_gdn_num_chunks_bound(B, T, 0)
-    gc = torch.empty(B, T, H, dtype=torch.float32, device=dev)
-    w = torch.empty(B, T, H, K, dtype=torch.bfloat16, device=dev)
-    uT = torch.empty(nc, H, V, C, dtype=torch.bfloat16, device=dev)
-    hT = torch.empty(nc, H, V, K, dtype=torch.bfloat16, device=dev)
-    vnT = torch.empty(nc, H, V, C, dtype=torch.bfloat16, device=dev)
-    names = ["prepare", "fwd_h", "fwd_o"]
+    # ---- per-kernel times: hipEvents recorded by the library on the launch stream
+    lib.kairos_gdn_profile_begin()
+    for _ in range(args.steps):
+        step()
+    avg = (ctypes.c_double * 3)()
+    ncalls = lib.kairos_gdn_profile_end(avg, 3)
+    if ncalls != args.steps:
+        raise RuntimeError(f"kernel timing recorded {ncalls} calls: {lib.kairos_gdn_last_error().decode()}")
+    per = {n: avg[i] for i, n in enumerate(KERNELS)}
 
-    def stages(ev=None):
-        if ev: ev[0].record(stream)
-        _lib.call("kairos_gdn_prepare_wy", P(k), P(v), P(g), P(beta), None, P(gc), P(w), P(uT), None, None, None, 0,
-                  B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, None, 0, sp)
-        if ev: ev[1].record(stream)
-        _lib.call("kairos_gdn_fwd_h", P(k), None, P(w), P(uT), P(gc), P(h0), P(hT), P(vnT), P(ht), None, 0,
-                  B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, None, 0, sp)
-        if ev: ev[2].record(stream)
-        _lib.call("kairos_gdn_fwd_o", P(q), P(k), None, None, P(hT), P(vnT), P(gc), P(o), scale, None, 0,
-                  B, T, H, K, V, _lib.BF16, _lib.BF16, None, 0, sp)
-        if ev: ev[3].record(stream)
-
-    for _ in range(max(2, args.warmup)):
-        stages()
-    per = {n: 0.0 for n in names}
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for i in range(args.steps):
-        stages(evs[i])
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        for j, n in enumerate(names):
-            per[n] += evs[i][j].elapsed_time(evs[i][j + 1]) / args.steps    # ms
-
-    tok = B * T
-    flops = B * T * H * flops_per_tok_head(K, V)
-    models = kernel_models(B, T, H, K, V)
-    dom = max(names, key=lambda n: per[n])
+    L = lib.kairos_gdn_segment_chunks(B, T, H, 0)
+    models = kernel_models(B, T, H, K, V, L)
+    dom = max(KERNELS, key=lambda n: per[n])
     dom_s = per[dom] / 1e3
     achieved = models[dom]["bytes"] / dom_s / 1e9
+    traffic = measured_traffic(dom)
+    tok = B * T
+    flops = B * T * H * flops_per_tok_head(K, V)
     tflops = flops / wall / 1e12
+    nc = (T + C - 1) // C
     out = {
         "metric": METRIC,
         "value": tok / wall,
@@ -206,10 +229,14 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": f"BASELINE config 2: chunk_gated_delta_rule fwd B={B} T={T} H={H} dk=dv={K} "
-                               "chunk 64, bf16 q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM"},
+                               "chunk 64, bf16 q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM",
+                   "segments_per_sequence": (nc + L - 1) // L, "chunks_per_segment": L},
         "tflops": tflops,
         "mfma_peak_frac": tflops / PEAK_BF16_TFLOPS,
+        "hbm_gbs_whole_op": (B * T * H * (2 * K * 2 + 2 * V * 2 + 4 + 2) + 2 * B * H * K * V * 4) / wall / 1e9,
         "kernels_ms": per,
+        "kernels_tflops": {n: models[n]["flops"] / (per[n] / 1e3) / 1e12 if per[n] > 0 else 0.0 for n in KERNELS},
+        "kernels_gbs": {n: models[n]["bytes"] / (per[n] / 1e3) / 1e9 if per[n] > 0 else 0.0 for n in KERNELS},
         "roofline": {
             "bound": "hbm",
             "kernel": dom,
@@ -217,11 +244,11 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBS,
-            "traffic": None,
+            "traffic": traffic,
         },
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(T, H, K, V, args.cpu_heads, 20262)
+        out["cpu_baseline"] = cpu_baseline(T, H, K, V, 20262)
     print(json.dumps(out), flush=True)
 
 

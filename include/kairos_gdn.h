@@ -79,6 +79,24 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
                          int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* Chunks per segment that kairos_gdn_chunk_fwd uses for this problem (the
+ * segment plan: sequences are cut into segments of this many 64-token chunks
+ * so that (segment, head) work items fill the GPU; the environment variable
+ * KAIROS_GDN_SEG_CHUNKS overrides it).  No counterpart in the reference. */
+int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs);
+
+/* ---- kernel timing (measurement hook, no counterpart in the reference) ----
+ * kairos_gdn_profile_begin() makes every following kairos_gdn_chunk_fwd call
+ * of the fused path record hipEvents on its stream around its three kernels
+ * (seg_trans, seg_combine, seg_out).  kairos_gdn_profile_end() waits for the
+ * recorded events, stops recording, writes the average milliseconds of the
+ * three kernels per call into avg_ms[0..min(n,3)-1] and returns the number of
+ * calls recorded, or -1 on a HIP error (message in kairos_gdn_last_error()).
+ * A kernel the call did not need (seg_trans / seg_combine for single-segment
+ * sequences) reports ~0 ms.  The staged fp32 K = 128 path records nothing. */
+int kairos_gdn_profile_begin(void);
+int kairos_gdn_profile_end(double* avg_ms, int n);
+
 /* ---- stage entry points (parity testing and composition) ----------------
  * Each stage replaces one reference function.  Varlen stage calls need
  * kairos_gdn_stage_workspace_size(n_seqs) bytes of workspace (chunk map);

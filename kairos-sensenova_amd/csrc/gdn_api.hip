@@ -15,7 +15,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/kairos_gdn.h"
 #include "gdn_common.hpp"
@@ -190,6 +192,35 @@ size_t seg_ws(int64_t H, int64_t K, int64_t V, int64_t n_seqs, const SegPlan& P)
   return total;
 }
 
+// Kernel timing of kairos_gdn_chunk_fwd (kairos_gdn_profile_begin / _end): while
+// enabled, every fused call records 4 hipEvents on its stream around its three kernels.
+struct Profile {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> pool;   // 4 events per recorded call
+  size_t used = 0;
+};
+Profile& profile() {
+  static Profile p;
+  return p;
+}
+// Next set of 4 events while profiling is on, else nullptr.
+hipEvent_t* profile_events() {
+  Profile& P = profile();
+  std::lock_guard<std::mutex> lk(P.mu);
+  if (!P.on) return nullptr;
+  if (P.used + 4 > P.pool.size()) {
+    for (int i = 0; i < 4; ++i) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) return nullptr;
+      P.pool.push_back(e);
+    }
+  }
+  hipEvent_t* ev = P.pool.data() + P.used;
+  P.used += 4;
+  return ev;
+}
+
 // Workspace of the staged path (stage kernels with the reference's intermediates).
 size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
@@ -356,8 +387,49 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
   a.M = M; a.R = R; a.s_init = s_init; a.scale = scale; a.o = o; a.ht = final_state;
   a.run_trans = P.trans && P.ns > 0;
   a.run_combine = P.combine;
+  a.events = profile_events();
   if (int rc = from_launch(kgdn::launch_seg_fwd(a, cdt, qk_dtype, (int)K, (int)V, s), "segment forward")) return rc;
   return ok();
+}
+
+int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs) {
+  if (B <= 0 || T < 0 || H <= 0 || n_seqs < 0) return 0;
+  return plan_segments(B, T, H, n_seqs).L;
+}
+
+int kairos_gdn_profile_begin(void) {
+  Profile& P = profile();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.on = true;
+  P.used = 0;
+  return ok();
+}
+
+int kairos_gdn_profile_end(double* avg_ms, int n) {
+  Profile& P = profile();
+  std::lock_guard<std::mutex> lk(P.mu);
+  P.on = false;
+  const size_t calls = P.used / 4;
+  double acc[3] = {0.0, 0.0, 0.0};
+  for (size_t c = 0; c < calls; ++c) {
+    hipEvent_t* e = P.pool.data() + 4 * c;
+    if (hipEventSynchronize(e[3]) != hipSuccess) {
+      fail(KAIROS_GDN_EHIP, "kairos_gdn_profile_end: %s", hipGetErrorString(hipGetLastError()));
+      return -1;
+    }
+    for (int k = 0; k < 3; ++k) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, e[k], e[k + 1]) != hipSuccess) {
+        fail(KAIROS_GDN_EHIP, "kairos_gdn_profile_end: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+      }
+      acc[k] += ms;
+    }
+  }
+  for (int k = 0; k < 3 && k < n; ++k) avg_ms[k] = calls ? acc[k] / (double)calls : 0.0;
+  P.used = 0;
+  g_last_error.clear();
+  return (int)calls;
 }
 
 int kairos_gdn_chunk_local_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu_seqlens, int64_t n_seqs,

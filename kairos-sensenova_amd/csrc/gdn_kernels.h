@@ -104,6 +104,7 @@ struct SegFwdArgs {
   float* ht;              // out [N, H, K, V] or nullptr
   bool run_trans;         // some sequence has more than one segment
   bool run_combine;       // ... or final_state of empty sequences is needed
+  hipEvent_t* events;     // optional [4]: recorded before seg_trans, seg_combine, seg_out and after seg_out
 };
 
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported

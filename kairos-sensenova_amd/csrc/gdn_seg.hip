@@ -1059,6 +1059,8 @@ template <typename TC, typename TQ, int K, int V>
 int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
   const dim3 grid((unsigned)p.ns_grid, (unsigned)p.H);
+  auto mark = [&](int i) { return p.events == nullptr || hipEventRecord(p.events[i], s) == hipSuccess; };
+  if (!mark(0)) return -1;
   if (p.run_trans) {
     using LT = SegLds<TC, K, V, false>;
     static_assert(LT::total <= 160 * 1024, "seg_trans tile does not fit in LDS");
@@ -1068,6 +1070,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     hipLaunchKernelGGL(kt, grid, dim3(TransCfg<K, V>::NT), LT::total, s, ta, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
+  if (!mark(1)) return -1;
   if (p.run_combine) {
     const int total = p.N * p.H * (V / 16);
     const int cgrid = (total + 7) / 8 * 8;
@@ -1075,6 +1078,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     hipLaunchKernelGGL(seg_combine_kernel<K>, dim3(cgrid), dim3(NT_COMB), 0, s, ca, G, total);
     if (hipGetLastError() != hipSuccess) return -1;
   }
+  if (!mark(2)) return -1;
   if (p.ns_grid > 0) {
     using LO = SegLds<TC, K, V, true>;
     static_assert(LO::total <= 160 * 1024, "seg_out tile does not fit in LDS");
@@ -1085,6 +1089,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     hipLaunchKernelGGL(ko, grid, dim3(OutCfg<K, V>::NT), LO::total, s, oa, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
+  if (!mark(3)) return -1;
   return 0;
 }
 
