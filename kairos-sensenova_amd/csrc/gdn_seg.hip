@@ -201,7 +201,7 @@ struct SegLds {
   static constexpr size_t off_Ai = a16(off_A + A_bytes);
   static constexpr size_t off_Aqk = a16(off_Ai + sizeof(TC) * C * LDT);
   static constexpr size_t off_g = a16(off_Aqk + (WITH_Q ? sizeof(TC) * C * LDT : 0));
-  static constexpr size_t total = off_g + sizeof(float) * 3 * C;
+  static constexpr size_t total = off_g + sizeof(float) * 4 * C;   // gc, exp(gc), beta, gate
 };
 
 // ---------------------------------------------------------------------------
@@ -318,10 +318,12 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& 
   }
 }
 
-// Registers -> LDS; wave 0 also forms the chunk-local cumsum of g (fla ops/utils/cumsum.py:58-65).
+// Registers -> LDS.  Wave 0 also forms the chunk vectors: gc = chunk-local
+// cumsum of g (fla ops/utils/cumsum.py:58-65), exp(gc), beta and the update
+// gate exp(gc_last - gc) (0 beyond the valid rows, chunk_delta_h.py:163-169).
 template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
 __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, unsigned char* smem,
-                                            float qs, float ks) {
+                                            float qs, float ks, int nv) {
   using L = SegLds<TC, K, V, WITH_Q>;
   using CR = ChunkRegs<TC, TQ, K, V, WITH_Q, NT>;
   TC* s_k = reinterpret_cast<TC*>(smem + L::off_k);
@@ -382,177 +384,199 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q
       const float o = __shfl_up(gv, off, WAVE);
       if (tid >= off) gv += o;
     }
-    s_g[tid] = gv;                 // gc
-    s_g[C + tid] = gexp(gv);       // exp(gc)
-    s_g[2 * C + tid] = R.b;        // beta
+    const float gl = __shfl(gv, nv - 1, WAVE);
+    s_g[tid] = gv;                                         // gc
+    s_g[C + tid] = gexp(gv);                               // exp(gc)
+    s_g[2 * C + tid] = R.b;                                // beta
+    s_g[3 * C + tid] = tid < nv ? gexp(gl - gv) : 0.f;     // gate
   }
 }
 
-// ---------------------------------------------------------------------------
-// chunk-local WY representation, shared by seg_trans and seg_out
-//   A   = beta_i exp(gc_i - gc_j) k_i.k_j (i > j)      chunk_scaled_dot_kkt.py:57-73
-//   Aqk = exp(gc_i - gc_j) q_i.k_j (i >= j)             chunk_o.py:109-118
-//   Ai  = (I + A)^-1, rounded to TC                      solve_tril.py:184-331
-//   w   = Ai (k beta exp(gc)) -> LDS (row-major)        wy_fast.py:67-81
-// u = Ai (v beta) is formed by the caller for the columns it owns.
-// ---------------------------------------------------------------------------
-template <typename TC, int K, int V, bool WITH_Q, int NW>
-__device__ __forceinline__ void wy_chunk(unsigned char* smem, int nv, bool beta_lowp) {
+// Zero the upper 16x16 tiles of Ai (and Aqk) that operand fragments read
+// (col tile 2ks+1 of row tile 2ks): they are never written per chunk.
+template <typename TC, int K, int V, bool WITH_Q, int NT>
+__device__ __forceinline__ void zero_upper_tiles(unsigned char* smem) {
   using L = SegLds<TC, K, V, WITH_Q>;
-  TC* s_k = reinterpret_cast<TC*>(smem + L::off_k);
-  TC* s_w = s_k;
-  const TC* s_q = reinterpret_cast<const TC*>(smem + L::off_q);
-  const TC* s_kT = reinterpret_cast<const TC*>(smem + L::off_kT);
-  float* s_A = reinterpret_cast<float*>(smem + L::off_A);
   TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);
   TC* s_Aqk = reinterpret_cast<TC*>(smem + L::off_Aqk);
+  for (int idx = threadIdx.x; idx < 2 * 16 * 16; idx += NT) {
+    const int tile = idx >> 8, r = (idx >> 4) & 15, c = idx & 15;
+    const int row = 32 * tile + r, col = 32 * tile + 16 + c;
+    s_Ai[row * L::LDT + pcol(col)] = from_f32<TC>(0.f);
+    if constexpr (WITH_Q) s_Aqk[row * L::LDT + pcol(col)] = from_f32<TC>(0.f);
+  }
+}
+
+// One 16-row block tm of A (beta_i exp(gc_i - gc_j) k_i.k_j, i > j; fp32 for the
+// solve, chunk_scaled_dot_kkt.py:57-73) or of Aqk (exp(gc_i - gc_j) q_i.k_j,
+// i >= j; rounded to TC, chunk_o.py:109-118).
+template <typename TC, int K, int V, bool WITH_Q, bool IS_Q>
+__device__ __forceinline__ void kkt_rowblock(unsigned char* smem, int tm) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  const TC* s_k = reinterpret_cast<const TC*>(smem + L::off_k);
+  const TC* s_q = reinterpret_cast<const TC*>(smem + L::off_q);
+  float* s_A = reinterpret_cast<float*>(smem + L::off_A);
+  TC* s_Aqk = reinterpret_cast<TC*>(smem + L::off_Aqk);
   const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
-  const float* s_eg = s_g + C;
-  const float* s_b = s_g + 2 * C;
-  const int tid = threadIdx.x;
-  const int wid = tid / WAVE;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
-
-  // ---- A (10 lower tiles) and, with q, Aqk (10 lower tiles + the 2 upper tiles its
-  //      fragments touch, written as zeros)
-  constexpr int NJOB = WITH_Q ? 22 : 10;
-  for (int job = wid; job < NJOB; job += NW) {
-    const bool isA = job < 10;
-    int tm, tn;
-    bool zero = false;
-    if (job < 20) {
-      const int tile = isA ? job : job - 10;
-      tm = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
-      tn = tile - tm * (tm + 1) / 2;
-    } else {
-      tm = job == 20 ? 0 : 2;
-      tn = tm + 1;
-      zero = true;
-    }
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (!zero) {
-      const TC* a_src = isA ? s_k : s_q;
+  const TC* asrc = IS_Q ? s_q : s_k;
+  Frag<TC> a[K / 32];
 #pragma unroll
-      for (int ks = 0; ks < K / 32; ++ks)
-        mma(acc, frag_at<TC>(a_src + (16 * tm + lc) * L::LDK + 32 * ks + 8 * lg),
-            frag_at<TC>(s_k + (16 * tn + lc) * L::LDK + 32 * ks + 8 * lg));
-    }
+  for (int ks = 0; ks < K / 32; ++ks) a[ks] = frag_at<TC>(asrc + (16 * tm + lc) * L::LDK + 32 * ks + 8 * lg);
+  const int i0 = 16 * tm + 4 * lg;
+  const f32x4 gi = *reinterpret_cast<const f32x4*>(s_g + i0);
+  f32x4 bi = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (!IS_Q) bi = *reinterpret_cast<const f32x4*>(s_g + 2 * C + i0);
+  for (int tn = 0; tn <= tm; ++tn) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) mma(acc, a[ks], frag_at<TC>(s_k + (16 * tn + lc) * L::LDK + 32 * ks + 8 * lg));
     const int j = 16 * tn + lc;
+    const float gj = s_g[j];
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * tm + 4 * lg + jj;
-      if (isA) {
-        float val = 0.f;
-        if (i > j && i < nv) val = acc[jj] * gexp(s_g[i] - s_g[j]) * s_b[i];
-        s_A[i * L::LDA + j] = val;
-      } else {
-        float val = 0.f;
-        if (!zero && i >= j && i < nv) val = acc[jj] * gexp(s_g[i] - s_g[j]);
-        s_Aqk[i * L::LDT + pcol(j)] = from_f32<TC>(val);
-      }
+      const int i = i0 + jj;
+      const bool keep = IS_Q ? i >= j : i > j;
+      const float val = keep ? acc[jj] * gexp(gi[jj] - gj) * bi[jj] : 0.f;
+      if constexpr (IS_Q) s_Aqk[i * L::LDT + pcol(j)] = from_f32<TC>(val);
+      else s_A[i * L::LDA + j] = val;
     }
   }
-  __syncthreads();
+}
 
-  // ---- (I + A)^-1: the four 16x16 diagonal blocks by forward substitution
-  //      (wave 0, lane = one column of one block), in place
-  {
+// A (and Aqk) row blocks over the waves: job order A0..A3, Q3..Q0 so that with
+// 4 waves each wave gets one A block and the complementary Aqk block.
+template <typename TC, int K, int V, bool WITH_Q, int NW>
+__device__ __forceinline__ void kkt_phase(unsigned char* smem) {
+  constexpr int NJ = WITH_Q ? 8 : 4;
+  const int wid = threadIdx.x / WAVE;
+  for (int j = wid; j < NJ; j += NW) {
+    if (j < 4) kkt_rowblock<TC, K, V, WITH_Q, false>(smem, j);
+    else kkt_rowblock<TC, K, V, WITH_Q, true>(smem, 7 - j);
+  }
+}
+
+// (I + A)^-1 for the solver waves (solve_tril.py:184-331, fp32 throughout):
+// diagonal 16x16 blocks by forward substitution (one wave, lane = one column of
+// one block), then block merges X_ij = -X_ii sum_k A_ik X_kj with fp32 MFMA.
+// Every block is written rounded to TC into s_Ai ([t][pcol(t')]); the fp32
+// copies needed by later merge levels stay in s_A (the strictly lower blocks
+// keep A, X_ij is kept in the unused upper block (j, i)).
+// Waves: diagonal by wave W0; level 1 by W0, W0-1, W0-2; level 2 by W0, W0-1;
+// level 3 by W0 (W0 = NW - 1).  `other` runs on the waves while they are idle.
+template <typename TC, int K, int V, bool WITH_Q, int NW, typename Other>
+__device__ __forceinline__ void solve_phase(unsigned char* smem, Other&& other) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  static_assert(NW >= 3, "the block merges use three waves");
+  float* s_A = reinterpret_cast<float*>(smem + L::off_A);
+  TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  constexpr int W0 = NW - 1;
+  const int role = W0 - wid;            // 0 = the solver wave
+  if (role == 0) {
     float x[16];
     float* Xb = s_A + (16 * lg) * L::LDA + 16 * lg;
-    if (wid == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s = 0.f;
+    for (int i = 0; i < 16; ++i) {
+      float s = 0.f;
 #pragma unroll
-        for (int r = 0; r < i; ++r) s = fmaf(Xb[i * L::LDA + r], x[r], s);
-        x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -s);
-      }
+      for (int r = 0; r < i; ++r) s = fmaf(Xb[i * L::LDA + r], x[r], s);
+      x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -s);
     }
-    __syncthreads();
-    if (wid == 0) {
+    // same wave: the reads above are done before these writes
 #pragma unroll
-      for (int i = 0; i < 16; ++i) Xb[i * L::LDA + lc] = x[i];
+    for (int i = 0; i < 16; ++i) {
+      Xb[i * L::LDA + lc] = x[i];
+      s_Ai[(16 * lg + i) * L::LDT + pcol(16 * lg + lc)] = from_f32<TC>(x[i]);
     }
+  } else if (role >= 3) {
+    other();
   }
   __syncthreads();
-  //      block merges (fp32 MFMA): X_ij = -X_ii sum_k L_ik X_kj, kept in the unused
-  //      upper block (j, i) so the strictly lower blocks stay intact for later levels
   auto blk = [&](int i, int j) { return s_A + (16 * i) * L::LDA + 16 * j; };
-  auto put_neg = [&](float* dst, const f32x4& r) {
+  auto put = [&](int i, int j, const f32x4& r) {
+    float* up = blk(j, i);
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) dst[(4 * lg + jj) * L::LDA + lc] = -r[jj];
+    for (int jj = 0; jj < 4; ++jj) {
+      up[(4 * lg + jj) * L::LDA + lc] = -r[jj];
+      s_Ai[(16 * i + 4 * lg + jj) * L::LDT + pcol(16 * j + lc)] = from_f32<TC>(-r[jj]);
+    }
   };
-  if (wid < 3) {
-    const int i = wid + 1, j = wid;
+  if (role < 3) {                                   // X_{i,i-1}, i = 3 - role
+    const int i = 3 - role, j = i - 1;
     f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
     mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
     mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
-    put_neg(blk(j, i), r);
+    put(i, j, r);
   }
+  if (role == 2) other();
   __syncthreads();
-  if (wid < 2) {
-    const int i = wid + 2, j = wid;
+  if (role < 2) {                                   // X_{i,i-2}, i = 3 - role
+    const int i = 3 - role, j = i - 2;
     f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
     mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
     mma16_f32_lds(t, blk(i, j + 1), L::LDA, blk(j, j + 1), L::LDA);
     mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
-    put_neg(blk(j, i), r);
+    put(i, j, r);
   }
+  if (role == 1) other();
   __syncthreads();
-  if (wid == 0) {
+  if (role == 0) {                                  // X_{3,0}
     f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
     mma16_f32_lds(t, blk(3, 0), L::LDA, blk(0, 0), L::LDA);
     mma16_f32_lds(t, blk(3, 1), L::LDA, blk(0, 1), L::LDA);
     mma16_f32_lds(t, blk(3, 2), L::LDA, blk(0, 2), L::LDA);
     mma16_f32_lds_reg(r, blk(3, 3), L::LDA, t);
-    put_neg(blk(0, 3), r);
-  }
-  __syncthreads();
-
-  // ---- Ai rounded to TC, row-major [t][t'] in pcol order
-  for (int idx = tid; idx < C * C / 2; idx += 64 * NW) {
-    const int i = idx / (C / 2), j = 2 * (idx % (C / 2));
-    const int bi = i >> 4, bj = j >> 4;
-    float x0 = 0.f, x1 = 0.f;
-    if (bi == bj) {
-      x0 = s_A[i * L::LDA + j];
-      x1 = s_A[i * L::LDA + j + 1];
-    } else if (bi > bj) {
-      x0 = s_A[(16 * bj + (i & 15)) * L::LDA + 16 * bi + (j & 15)];
-      x1 = s_A[(16 * bj + (i & 15)) * L::LDA + 16 * bi + (j & 15) + 1];
-    }
-    st2<TC>(s_Ai + i * L::LDT + pcol(j), x0, x1);
-  }
-  __syncthreads();
-
-  // ---- w^T = kb^T Ai^T (rows d, cols t): K/16 x 4 tiles over the waves -> s_w[t][d]
-  for (int job = wid; job < (K / 16) * 4; job += NW) {
-    const int dt = job >> 2, tn = job & 3;
-    const int d = 16 * dt + lc;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (ks <= tn / 2) {
-        float x[8];
-        lds_get8<TC>(s_kT + d * L::LDT + tchunk(d, 32 * ks + 8 * lg), x);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int t = frag_t(ks, lg, e);
-          float kb = x[e] * s_b[t];
-          if (beta_lowp) kb = round_to<TC>(kb);
-          x[e] = kb * s_eg[t];
-        }
-        mma(acc, frag_pack<TC>(x), frag_at<TC>(s_Ai + (16 * tn + lc) * L::LDT + 32 * ks + 8 * lg));
-      }
-    }
-    st4<TC>(s_w + (16 * tn + lc) * L::LDK + pcol(16 * dt + 4 * lg), acc[0], acc[1], acc[2], acc[3]);
+    put(3, 0, r);
+    other();
   }
 }
 
-// u tile (rows 16*tm.., V columns v0..v0+15) = Ai (v beta), rounded to TC (wy_fast.py:61-66)
+// w^T = kb^T Ai^T for the 16-row d tiles dt = wid, wid + NW, ... -> s_w[t][d]
+// (kb = k beta exp(gc) with the reference's roundings, wy_fast.py:67-81).
+template <typename TC, int K, int V, bool WITH_Q, int NW>
+__device__ __forceinline__ void w_phase(unsigned char* smem, bool beta_lowp) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  TC* s_w = reinterpret_cast<TC*>(smem + L::off_k);
+  const TC* s_kT = reinterpret_cast<const TC*>(smem + L::off_kT);
+  const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
+  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  for (int dt = wid; dt < K / 16; dt += NW) {
+    const int d = 16 * dt + lc;
+    Frag<TC> kb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float x[8];
+      lds_get8<TC>(s_kT + d * L::LDT + tchunk(d, 32 * ks + 8 * lg), x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = frag_t(ks, lg, e);
+        float v = x[e] * s_g[2 * C + t];
+        if (beta_lowp) v = round_to<TC>(v);
+        x[e] = v * s_g[C + t];
+      }
+      kb[ks] = frag_pack<TC>(x);
+    }
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks <= tn / 2; ++ks)
+        mma(acc, kb[ks], frag_at<TC>(s_Ai + (16 * tn + lc) * L::LDT + 32 * ks + 8 * lg));
+      st4<TC>(s_w + (16 * tn + lc) * L::LDK + pcol(16 * dt + 4 * lg), acc[0], acc[1], acc[2], acc[3]);
+    }
+  }
+}
+
+// u (64 rows x V columns v0..v0+15) = Ai (v beta), rounded to TC (wy_fast.py:61-66), in accumulator tiles
 template <typename TC, int K, int V, bool WITH_Q>
-__device__ __forceinline__ f32x4 u_tile(const unsigned char* smem, int tm, int v0) {
+__device__ __forceinline__ void u_cols(const unsigned char* smem, int v0, f32x4 (&u)[4]) {
   using L = SegLds<TC, K, V, WITH_Q>;
   const TC* s_vT = reinterpret_cast<const TC*>(smem + L::off_vT);
   const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
@@ -560,23 +584,28 @@ __device__ __forceinline__ f32x4 u_tile(const unsigned char* smem, int tm, int v
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
   const int vv = v0 + lc;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  Frag<TC> vb[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    if (ks <= tm / 2) {
-      float x[8];
-      lds_get8<TC>(s_vT + vv * L::LDT + tchunk(vv, 32 * ks + 8 * lg), x);
+    float x[8];
+    lds_get8<TC>(s_vT + vv * L::LDT + tchunk(vv, 32 * ks + 8 * lg), x);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] *= s_b[frag_t(ks, lg, e)];
-      mma(acc, frag_at<TC>(s_Ai + (16 * tm + lc) * L::LDT + 32 * ks + 8 * lg), frag_pack<TC>(x));
-    }
+    for (int e = 0; e < 8; ++e) x[e] *= s_b[frag_t(ks, lg, e)];
+    vb[ks] = frag_pack<TC>(x);
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = round_to<TC>(acc[j]);
-  return acc;
+  for (int tm = 0; tm < 4; ++tm) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks <= tm / 2; ++ks)
+      mma(acc, frag_at<TC>(s_Ai + (16 * tm + lc) * L::LDT + 32 * ks + 8 * lg), vb[ks]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = round_to<TC>(acc[j]);
+    u[tm] = acc;
+  }
 }
 
-// S (K x 16*CT per wave, accumulator tiles) <- exp(g_last) S + k^T vg, with vg given as operand fragments
+// S (K x 16*CT, accumulator tiles) <- gamma S + k^T vg, vg given as operand fragments
 template <typename TC, int K, int V, bool WITH_Q, int CT>
 __device__ __forceinline__ void state_update(f32x4 (&S)[K / 16][CT], const Frag<TC> (&vg)[2][CT],
                                              const unsigned char* smem, float gamma) {
@@ -598,7 +627,7 @@ __device__ __forceinline__ void state_update(f32x4 (&S)[K / 16][CT], const Frag<
   }
 }
 
-// Y (64 x 16*CT) = U - w X, with X given as operand fragments of its K rows
+// Y (64 x 16*CT) -= w X, X given as operand fragments of its K rows
 template <typename TC, int K, int V, bool WITH_Q, int CT>
 __device__ __forceinline__ void sub_wx(f32x4 (&Y)[4][CT], const Frag<TC> (&xb)[K / 32][CT], const unsigned char* smem) {
   using L = SegLds<TC, K, V, WITH_Q>;
@@ -618,6 +647,19 @@ __device__ __forceinline__ void sub_wx(f32x4 (&Y)[4][CT], const Frag<TC> (&xb)[K
     }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) Y[tm][ct] -= p[ct];
+  }
+}
+
+// operand fragments of the gated update input vg = Y * gate (rows t), rounded to TC
+template <typename TC, int CT>
+__device__ __forceinline__ void gate_frags(const f32x4 (&Y)[4][CT], const float* s_gate, Frag<TC> (&vg)[2][CT]) {
+  const int lg = lane_id() >> 4;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const f32x4 ga = *reinterpret_cast<const f32x4*>(s_gate + 32 * ks + 4 * lg);
+    const f32x4 gb = *reinterpret_cast<const f32x4*>(s_gate + 32 * ks + 16 + 4 * lg);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) vg[ks][ct] = acc_frag<TC>(Y[2 * ks][ct] * ga, Y[2 * ks + 1][ct] * gb);
   }
 }
 
@@ -700,6 +742,7 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
         for (int ct = 0; ct < CT; ++ct) S[tt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
+  zero_upper_tiles<TC, K, V, true, NT>(smem);
 
   CR cur;
   int64_t t0 = sl.bos + sl.c0 * C;
@@ -708,7 +751,7 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
   TC* o = reinterpret_cast<TC*>(a.o);
 
   for (int ci = 0; ci < sl.nch; ++ci) {
-    stage_chunk<TC, TQ, K, V, true, NT>(cur, smem, qs, ks_);
+    stage_chunk<TC, TQ, K, V, true, NT>(cur, smem, qs, ks_, nv);
     __syncthreads();
     const int64_t t0c = t0;
     const int nvc = nv;
@@ -717,15 +760,8 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
       nv = (int)min((int64_t)C, sl.eos - t0);
       load_chunk<TC, TQ, K, V, true, NT>(cur, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
     }
-    wy_chunk<TC, K, V, true, NW>(smem, nvc, beta_lowp);
-    // u of the owned columns (independent of w; overlaps the w stores of other waves)
-    f32x4 Y[4][CT];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) Y[tm][ct] = u_tile<TC, K, V, true>(smem, tm, vw + 16 * ct);
-    }
-    __syncthreads();   // w complete
+    kkt_phase<TC, K, V, true, NW>(smem);
+    __syncthreads();
 
     // ---- h = S rounded (the snapshot of chunk_delta_h.py:129-139) as operand fragments
     Frag<TC> hb[K / 32][CT];
@@ -734,10 +770,41 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) hb[ks][ct] = acc_frag<TC>(S[2 * ks][ct], S[2 * ks + 1][ct]);
     }
+    // ---- o1^T = h^T q^T (chunk_o.py:84-101), on each wave while it is not solving
+    f32x4 o1[4][CT];
+    auto inter_chunk_out = [&]() {
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) o1[tn][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks) {
+          const Frag<TC> bq = frag_at<TC>(s_q + (16 * tn + lc) * L::LDK + 32 * ks + 8 * lg);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) mma(o1[tn][ct], hb[ks][ct], bq);
+        }
+      }
+    };
+    solve_phase<TC, K, V, true, NW>(smem, inter_chunk_out);
+    __syncthreads();   // Ai complete
+
+    w_phase<TC, K, V, true, NW>(smem, beta_lowp);
+    f32x4 Y[4][CT];
+    {
+      f32x4 u[4];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        u_cols<TC, K, V, true>(smem, vw + 16 * ct, u);
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u[tm];
+      }
+    }
+    __syncthreads();   // w complete
+
     // ---- v' = u - w h                                   (chunk_delta_h.py:141-157)
     sub_wx<TC, K, V, true, CT>(Y, hb, smem);
 
-    // ---- o^T = scale (h^T q^T exp(gc) + v_new^T Aqk^T)   (chunk_o.py:84-128)
+    // ---- o^T = scale (o1^T exp(gc) + v_new^T Aqk^T)     (chunk_o.py:102-128)
     Frag<TC> vn[2][CT];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -747,18 +814,9 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) {
       const int t = 16 * tn + lc;
-      f32x4 o1[CT], o2[CT];
+      f32x4 o2[CT];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        o1[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-        o2[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int ks = 0; ks < K / 32; ++ks) {
-        const Frag<TC> bq = frag_at<TC>(s_q + t * L::LDK + 32 * ks + 8 * lg);
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) mma(o1[ct], hb[ks][ct], bq);
-      }
+      for (int ct = 0; ct < CT; ++ct) o2[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         if (ks <= tn / 2) {
@@ -772,30 +830,16 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
         TC* orow = o + ((t0c + t) * H + h) * V + vw + 4 * lg;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
-          st4<TC>(orow + 16 * ct, o1[ct][0] * eg + o2[ct][0] * a.scale, o1[ct][1] * eg + o2[ct][1] * a.scale,
-                  o1[ct][2] * eg + o2[ct][2] * a.scale, o1[ct][3] * eg + o2[ct][3] * a.scale);
+          const f32x4 r = o1[tn][ct] * eg + o2[ct] * a.scale;
+          st4<TC>(orow + 16 * ct, r[0], r[1], r[2], r[3]);
         }
       }
     }
 
     // ---- S = exp(g_last) S + k^T (v' exp(g_last - gc))   (chunk_delta_h.py:163-211)
-    const float gl = s_g[nvc - 1];
     Frag<TC> vg[2][CT];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        f32x4 ya = Y[2 * ks][ct], yb = Y[2 * ks + 1][ct];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ta = 32 * ks + 4 * lg + j, tb = ta + 16;
-          ya[j] = ta < nvc ? ya[j] * gexp(gl - s_g[ta]) : 0.f;
-          yb[j] = tb < nvc ? yb[j] * gexp(gl - s_g[tb]) : 0.f;
-        }
-        vg[ks][ct] = acc_frag<TC>(ya, yb);
-      }
-    }
-    state_update<TC, K, V, true, CT>(S, vg, smem, gexp(gl));
+    gate_frags<TC, CT>(Y, s_g + 3 * C, vg);
+    state_update<TC, K, V, true, CT>(S, vg, smem, gexp(s_g[nvc - 1]));
     __syncthreads();   // LDS is restaged for the next chunk
   }
 
@@ -856,13 +900,14 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
       for (int j = 0; j < 4; ++j) X[tt][ct][j] = (16 * tt + 4 * lg + j == xw + 16 * ct + lc) ? 1.f : 0.f;
     }
   }
+  zero_upper_tiles<TC, K, V, false, NT>(smem);
 
   CR cur;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
   load_chunk<TC, TQ, K, V, false, NT>(cur, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
   for (int ci = 0; ci < sl.nch; ++ci) {
-    stage_chunk<TC, TQ, K, V, false, NT>(cur, smem, 1.f, ks_);
+    stage_chunk<TC, TQ, K, V, false, NT>(cur, smem, 1.f, ks_, nv);
     __syncthreads();
     const int nvc = nv;
     if (ci + 1 < sl.nch) {
@@ -871,14 +916,23 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
       load_chunk<TC, TQ, K, V, false, NT>(cur, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h,
                                           H);
     }
-    wy_chunk<TC, K, V, false, NW>(smem, nvc, beta_lowp);
+    kkt_phase<TC, K, V, false, NW>(smem);
+    __syncthreads();
+    solve_phase<TC, K, V, false, NW>(smem, []() {});
+    __syncthreads();   // Ai complete
+    w_phase<TC, K, V, false, NW>(smem, beta_lowp);
     f32x4 Y[4][CT];
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
+    for (int ct = 0; ct < CT; ++ct) {
+      const int c0 = xw + 16 * ct;
+      if (c0 >= K) {
+        f32x4 u[4];
+        u_cols<TC, K, V, false>(smem, c0 - K, u);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const int c0 = xw + 16 * ct;
-        Y[tm][ct] = c0 >= K ? u_tile<TC, K, V, false>(smem, tm, c0 - K) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u[tm];
+      } else {
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
     __syncthreads();   // w complete
@@ -889,23 +943,9 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
       for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag<TC>(X[2 * ks][ct], X[2 * ks + 1][ct]);
     }
     sub_wx<TC, K, V, false, CT>(Y, xb, smem);
-    const float gl = s_g[nvc - 1];
     Frag<TC> yg[2][CT];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        f32x4 ya = Y[2 * ks][ct], yb = Y[2 * ks + 1][ct];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ta = 32 * ks + 4 * lg + j, tb = ta + 16;
-          ya[j] = ta < nvc ? ya[j] * gexp(gl - s_g[ta]) : 0.f;
-          yb[j] = tb < nvc ? yb[j] * gexp(gl - s_g[tb]) : 0.f;
-        }
-        yg[ks][ct] = acc_frag<TC>(ya, yb);
-      }
-    }
-    state_update<TC, K, V, false, CT>(X, yg, smem, gexp(gl));
+    gate_frags<TC, CT>(Y, s_g + 3 * C, yg);
+    state_update<TC, K, V, false, CT>(X, yg, smem, gexp(s_g[nvc - 1]));
     __syncthreads();
   }
 
