@@ -30,9 +30,12 @@
 // indices {4(l/16)..+3} and {16+4(l/16)..+3} of a 32-wide step (the order in
 // which an accumulator tile pair is converted into an operand), so every
 // operand row stores each 32-column block permuted by pcol(): logical column
-// 16*hh + 4*lg + j sits at 8*lg + 4*hh + j.  Transposed tiles ([d][t], [v][t])
-// additionally XOR the 8-element chunk index with bits 3..5 of the row to
-// spread the transposing stores over the LDS banks.
+// 16*hh + 4*lg + j sits at 8*lg + 4*hh + j.  Rows are padded by 8 elements,
+// so the 16 rows one fragment read touches fall on distinct banks; the
+// transposing stores of k and v ([d][t], [v][t]) run with consecutive lanes on
+// consecutive token pairs of one row, which is conflict-free as well.
+#include <type_traits>
+
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
 
@@ -47,13 +50,23 @@ template <int K, int V> struct TransCfg { static constexpr int NW = (K + V) / 32
 constexpr int NT_COMB = 256;
 constexpr int NW_COMB = 4;
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences global
+// memory, which makes every barrier wait for all outstanding vector memory
+// operations -- the next chunk's prefetch and the output stores included.  The
+// waves of a workgroup share nothing but LDS, so an LDS fence is sufficient.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ int pcol(int c) {
   return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
 }
-// physical column of logical token t in row `row` of a transposed [*][64] tile
-__device__ __forceinline__ int tcol(int row, int t) { return pcol(t) ^ (((row >> 3) & 7) << 3); }
+// physical column of logical token t in a transposed [*][64] tile row
+__device__ __forceinline__ int tcol(int, int t) { return pcol(t); }
 // physical start of the 8-element fragment chunk `chunk8` (a multiple of 8, already in pcol order)
-__device__ __forceinline__ int tchunk(int row, int chunk8) { return chunk8 ^ (((row >> 3) & 7) << 3); }
+__device__ __forceinline__ int tchunk(int, int chunk8) { return chunk8; }
 
 template <typename TC>
 __device__ __forceinline__ Frag<TC> frag_at(const TC* p) {
@@ -66,6 +79,13 @@ __device__ __forceinline__ Frag<TC> frag_at(const TC* p) {
   }
   return f;
 }
+// two floats -> two bf16 (round to nearest even) packed in a dword, a in the low half
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  bf16x2_t v = {(bf16)a, (bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // the two bf16 values packed in a dword, as floats
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -201,7 +221,8 @@ struct SegLds {
   static constexpr size_t off_Ai = a16(off_A + A_bytes);
   static constexpr size_t off_Aqk = a16(off_Ai + sizeof(TC) * C * LDT);
   static constexpr size_t off_g = a16(off_Aqk + (WITH_Q ? sizeof(TC) * C * LDT : 0));
-  static constexpr size_t total = off_g + sizeof(float) * 4 * C;   // gc, exp(gc), beta, gate
+  static constexpr size_t vec_end = off_g + sizeof(float) * 4 * C;   // gc, exp(gc), beta, gate
+  static constexpr size_t raw_off = a16(vec_end);                    // raw staging area of the next chunk
 };
 
 // ---------------------------------------------------------------------------
@@ -258,63 +279,169 @@ __device__ __forceinline__ void raw_get8(const Raw8<T>& r, float scale, float (&
   }
 }
 
+// Bytes of 8 input elements and how they are fetched by direct global->LDS loads
+// (global_load_lds_dword / _dwordx4: lane L of a wave writes SIZE bytes at the
+// wave's LDS base + L * SIZE).
+template <typename T> struct GroupIO {
+  static constexpr int G = 8 * (int)sizeof(T);
+  static constexpr int SIZE = G >= 16 ? 16 : 4;
+  static constexpr int N = G / SIZE;
+};
+
+// The next chunk's inputs, fetched while the current chunk computes.  On the
+// bf16 path (DIRECT) q, k and v go straight to a raw staging area in LDS
+// (no registers held, and no register wait can stall on them); the fp32 path,
+// whose operand tiles leave no room for that area, holds them in registers.
 template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
 struct ChunkRegs {
   static constexpr int QU = C * (K / 8), KU = (C / 2) * (K / 8), VU = (C / 2) * (V / 8);   // work units
   static constexpr int QJ = (QU + NT - 1) / NT;     // 8-element row pieces of q per thread
   static constexpr int KJ = (KU + NT - 1) / NT;     // row-pair pieces of k per thread
   static constexpr int VJ = (VU + NT - 1) / NT;     // row-pair pieces of v per thread
-  Raw8<TQ> q[WITH_Q ? QJ : 1];
-  Raw8<TQ> k[KJ][2];
-  Raw8<TC> v[VJ][2];
-  float g, b;
+  static constexpr bool DIRECT = sizeof(TC) == 2;
+  // raw staging area: block b of a stream holds NT groups, wave w's 64 at (b * NT + 64 w) * G
+  static constexpr size_t RAW_Q = WITH_Q ? (size_t)QJ * NT * GroupIO<TQ>::G : 0;
+  static constexpr size_t RAW_K = (size_t)KJ * 2 * NT * GroupIO<TQ>::G;
+  static constexpr size_t RAW_V = (size_t)VJ * 2 * NT * GroupIO<TC>::G;
+  static constexpr size_t RAW = DIRECT ? RAW_Q + RAW_K + RAW_V : 0;
+  Raw8<TQ> q[DIRECT ? 1 : (WITH_Q ? QJ : 1)];
+  Raw8<TQ> k[DIRECT ? 1 : KJ][2];
+  Raw8<TC> v[DIRECT ? 1 : VJ][2];
+  uint32_t g, b;              // raw bits of g and beta of row tid (fp32, or bf16 in the low half)
 };
 
+typedef __attribute__((address_space(1))) void gmem_void;
+typedef __attribute__((address_space(3))) void lmem_void;
+
+// Direct loads of one group per lane (the wave's 64 groups land contiguously per load).
+template <typename T>
+__device__ __forceinline__ void group_to_lds(const T* src, unsigned char* blk) {
+  using IO = GroupIO<T>;
+  const unsigned char* p = reinterpret_cast<const unsigned char*>(src);
+#pragma unroll
+  for (int j = 0; j < IO::N; ++j) {
+    // the builtin takes the size as a literal
+    if constexpr (IO::SIZE == 16)
+      __builtin_amdgcn_global_load_lds((gmem_void*)(p + j * 16), (lmem_void*)(blk + j * WAVE * 16), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((gmem_void*)(p + j * 4), (lmem_void*)(blk + j * WAVE * 4), 4, 0, 0);
+  }
+}
+// This lane's group back from the staging area.
+template <typename T>
+__device__ __forceinline__ Raw8<T> group_from_lds(const unsigned char* blk) {
+  using IO = GroupIO<T>;
+  const int l = lane_id();
+  Raw8<T> r;
+  if constexpr (sizeof(T) == 1) {
+    r.v.x = *reinterpret_cast<const uint32_t*>(blk + l * 4);
+    r.v.y = *reinterpret_cast<const uint32_t*>(blk + WAVE * 4 + l * 4);
+  } else if constexpr (sizeof(T) == 2) {
+    r.v = *reinterpret_cast<const uint4*>(blk + l * 16);
+  } else {
+    r.lo = *reinterpret_cast<const f32x4*>(blk + l * 16);
+    r.hi = *reinterpret_cast<const f32x4*>(blk + WAVE * 16 + l * 16);
+  }
+  return r;
+}
+
+// raw per-token scalar (fp32 or bf16 bits) -> float; converted only when staged, so
+// that the loads of the next chunk stay in flight while the current one computes
+__device__ __forceinline__ uint32_t ld_raw(const void* p, int64_t i, int dt) {
+  return dt == DT_F32 ? reinterpret_cast<const uint32_t*>(p)[i] : (uint32_t)reinterpret_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float raw_to_f32(uint32_t r, int dt) {
+  return dt == DT_F32 ? __uint_as_float(r) : __uint_as_float(r << 16);
+}
+
 template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
-__device__ __forceinline__ void load_chunk(ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, const void* qp, const void* kp,
-                                           const void* vp, const void* gp, const void* bp, int g_dt, int b_dt,
-                                           int64_t t0, int nv, int h, int H) {
+__device__ __forceinline__ void load_chunk(ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, unsigned char* raw, const void* qp,
+                                           const void* kp, const void* vp, const void* gp, const void* bp, int g_dt,
+                                           int b_dt, int64_t t0, int nv, int h, int H) {
   using CR = ChunkRegs<TC, TQ, K, V, WITH_Q, NT>;
   const int tid = threadIdx.x;
+  const int wid = tid / WAVE;
   const TQ* q = reinterpret_cast<const TQ*>(qp);
   const TQ* k = reinterpret_cast<const TQ*>(kp);
   const TC* v = reinterpret_cast<const TC*>(vp);
-  if constexpr (WITH_Q) {
+  if constexpr (CR::DIRECT) {
+    // rows beyond nv read row 0 of the chunk (in bounds) and are zeroed when staged
+    if constexpr (WITH_Q) {
 #pragma unroll
-    for (int i = 0; i < CR::QJ; ++i) {
+      for (int i = 0; i < CR::QJ; ++i) {
+        const int idx = tid + NT * i;
+        if (CR::QJ * NT != CR::QU && idx >= CR::QU) break;        // uniform per wave
+        const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+        const int rs = r < nv ? r : 0;
+        group_to_lds<TQ>(q + ((t0 + rs) * H + h) * K + c8, raw + ((size_t)i * NT + WAVE * wid) * GroupIO<TQ>::G);
+      }
+    }
+    unsigned char* rk = raw + CR::RAW_Q;
+#pragma unroll
+    for (int i = 0; i < CR::KJ; ++i) {
       const int idx = tid + NT * i;
-      const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
-      if (idx < CR::QU && r < nv) R.q[i] = raw_load<TQ>(q + ((t0 + r) * H + h) * K + c8);
-      else R.q[i] = raw_zero<TQ>();
+      if (CR::KJ * NT != CR::KU && idx >= CR::KU) break;
+      const int p = idx % (C / 2), c8 = (idx / (C / 2)) * 8;     // token pair fastest
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * p + rr;
+        const int rs = r < nv ? r : 0;
+        group_to_lds<TQ>(k + ((t0 + rs) * H + h) * K + c8,
+                         rk + ((size_t)(2 * i + rr) * NT + WAVE * wid) * GroupIO<TQ>::G);
+      }
+    }
+    unsigned char* rv = raw + CR::RAW_Q + CR::RAW_K;
+#pragma unroll
+    for (int i = 0; i < CR::VJ; ++i) {
+      const int idx = tid + NT * i;
+      if (CR::VJ * NT != CR::VU && idx >= CR::VU) break;
+      const int p = idx % (C / 2), c8 = (idx / (C / 2)) * 8;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * p + rr;
+        const int rs = r < nv ? r : 0;
+        group_to_lds<TC>(v + ((t0 + rs) * H + h) * V + c8,
+                         rv + ((size_t)(2 * i + rr) * NT + WAVE * wid) * GroupIO<TC>::G);
+      }
+    }
+  } else {
+    if constexpr (WITH_Q) {
+#pragma unroll
+      for (int i = 0; i < CR::QJ; ++i) {
+        const int idx = tid + NT * i;
+        const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+        if (idx < CR::QU && r < nv) R.q[i] = raw_load<TQ>(q + ((t0 + r) * H + h) * K + c8);
+        else R.q[i] = raw_zero<TQ>();
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CR::KJ; ++i) {
+      const int idx = tid + NT * i;
+      const int p = idx % (C / 2), c8 = (idx / (C / 2)) * 8;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * p + rr;
+        if (idx < CR::KU && r < nv) R.k[i][rr] = raw_load<TQ>(k + ((t0 + r) * H + h) * K + c8);
+        else R.k[i][rr] = raw_zero<TQ>();
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CR::VJ; ++i) {
+      const int idx = tid + NT * i;
+      const int p = idx % (C / 2), c8 = (idx / (C / 2)) * 8;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * p + rr;
+        if (idx < CR::VU && r < nv) R.v[i][rr] = raw_load<TC>(v + ((t0 + r) * H + h) * V + c8);
+        else R.v[i][rr] = raw_zero<TC>();
+      }
     }
   }
-#pragma unroll
-  for (int i = 0; i < CR::KJ; ++i) {
-    const int idx = tid + NT * i;
-    const int p = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int r = 2 * p + rr;
-      if (idx < CR::KU && r < nv) R.k[i][rr] = raw_load<TQ>(k + ((t0 + r) * H + h) * K + c8);
-      else R.k[i][rr] = raw_zero<TQ>();
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < CR::VJ; ++i) {
-    const int idx = tid + NT * i;
-    const int p = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int r = 2 * p + rr;
-      if (idx < CR::VU && r < nv) R.v[i][rr] = raw_load<TC>(v + ((t0 + r) * H + h) * V + c8);
-      else R.v[i][rr] = raw_zero<TC>();
-    }
-  }
-  R.g = 0.f;
-  R.b = 0.f;
+  R.g = 0u;
+  R.b = 0u;
   if (tid < C && tid < nv) {
-    R.g = ld_scalar(gp, (t0 + tid) * H + h, g_dt);
-    R.b = ld_scalar(bp, (t0 + tid) * H + h, b_dt);
+    R.g = ld_raw(gp, (t0 + tid) * H + h, g_dt);
+    R.b = ld_raw(bp, (t0 + tid) * H + h, b_dt);
   }
 }
 
@@ -322,10 +449,15 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& 
 // cumsum of g (fla ops/utils/cumsum.py:58-65), exp(gc), beta and the update
 // gate exp(gc_last - gc) (0 beyond the valid rows, chunk_delta_h.py:163-169).
 template <typename TC, typename TQ, int K, int V, bool WITH_Q, int NT>
-__device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, unsigned char* smem,
-                                            float qs, float ks, int nv) {
+__device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q, NT>& R, const unsigned char* raw,
+                                            unsigned char* smem, float qs, float ks, int nv, int g_dt, int b_dt) {
   using L = SegLds<TC, K, V, WITH_Q>;
   using CR = ChunkRegs<TC, TQ, K, V, WITH_Q, NT>;
+  if constexpr (CR::DIRECT) {
+    // the direct global->LDS loads of this wave have landed (the compiler does not
+    // track them as a dependency of the LDS reads below)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
   TC* s_k = reinterpret_cast<TC*>(smem + L::off_k);
   TC* s_q = reinterpret_cast<TC*>(smem + L::off_q);
   TC* s_kT = reinterpret_cast<TC*>(smem + L::off_kT);
@@ -339,7 +471,13 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q
       if (CR::QJ * NT != CR::QU && idx >= CR::QU) continue;
       const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
       float x[8];
-      raw_get8<TQ>(R.q[i], qs, x);
+      if constexpr (CR::DIRECT) {
+        const Raw8<TQ> g8 = r < nv ? group_from_lds<TQ>(raw + ((size_t)i * NT + WAVE * (tid / WAVE)) * GroupIO<TQ>::G)
+                                   : raw_zero<TQ>();
+        raw_get8<TQ>(g8, qs, x);
+      } else {
+        raw_get8<TQ>(R.q[i], qs, x);
+      }
       st4<TC>(s_q + r * L::LDK + pcol(c8), x[0], x[1], x[2], x[3]);
       st4<TC>(s_q + r * L::LDK + pcol(c8 + 4), x[4], x[5], x[6], x[7]);
     }
@@ -348,11 +486,19 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q
   for (int i = 0; i < CR::KJ; ++i) {
     const int idx = tid + NT * i;
     if (CR::KJ * NT != CR::KU && idx >= CR::KU) continue;
-    const int p = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
+    const int p = idx % (C / 2), c8 = (idx / (C / 2)) * 8;
     float x[2][8];
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
-      raw_get8<TQ>(R.k[i][rr], ks, x[rr]);
+      if constexpr (CR::DIRECT) {
+        const Raw8<TQ> g8 =
+            2 * p + rr < nv
+                ? group_from_lds<TQ>(raw + CR::RAW_Q + ((size_t)(2 * i + rr) * NT + WAVE * (tid / WAVE)) * GroupIO<TQ>::G)
+                : raw_zero<TQ>();
+        raw_get8<TQ>(g8, ks, x[rr]);
+      } else {
+        raw_get8<TQ>(R.k[i][rr], ks, x[rr]);
+      }
       TC* row = s_k + (2 * p + rr) * L::LDK;
       st4<TC>(row + pcol(c8), x[rr][0], x[rr][1], x[rr][2], x[rr][3]);
       st4<TC>(row + pcol(c8 + 4), x[rr][4], x[rr][5], x[rr][6], x[rr][7]);
@@ -367,10 +513,21 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q
   for (int i = 0; i < CR::VJ; ++i) {
     const int idx = tid + NT * i;
     if (CR::VJ * NT != CR::VU && idx >= CR::VU) continue;
-    const int p = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
+    const int p = idx % (C / 2), c8 = (idx / (C / 2)) * 8;
     float x0[8], x1[8];
-    raw_get8<TC>(R.v[i][0], 1.f, x0);
-    raw_get8<TC>(R.v[i][1], 1.f, x1);
+    if constexpr (CR::DIRECT) {
+      const unsigned char* rv = raw + CR::RAW_Q + CR::RAW_K;
+      const Raw8<TC> a0 = 2 * p < nv ? group_from_lds<TC>(rv + ((size_t)(2 * i) * NT + WAVE * (tid / WAVE)) * GroupIO<TC>::G)
+                                     : raw_zero<TC>();
+      const Raw8<TC> a1 = 2 * p + 1 < nv
+                              ? group_from_lds<TC>(rv + ((size_t)(2 * i + 1) * NT + WAVE * (tid / WAVE)) * GroupIO<TC>::G)
+                              : raw_zero<TC>();
+      raw_get8<TC>(a0, 1.f, x0);
+      raw_get8<TC>(a1, 1.f, x1);
+    } else {
+      raw_get8<TC>(R.v[i][0], 1.f, x0);
+      raw_get8<TC>(R.v[i][1], 1.f, x1);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int vv = c8 + e;
@@ -378,7 +535,7 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q
     }
   }
   if (tid < WAVE) {
-    float gv = R.g;
+    float gv = raw_to_f32(R.g, g_dt);
 #pragma unroll
     for (int off = 1; off < WAVE; off <<= 1) {
       const float o = __shfl_up(gv, off, WAVE);
@@ -387,7 +544,7 @@ __device__ __forceinline__ void stage_chunk(const ChunkRegs<TC, TQ, K, V, WITH_Q
     const float gl = __shfl(gv, nv - 1, WAVE);
     s_g[tid] = gv;                                         // gc
     s_g[C + tid] = gexp(gv);                               // exp(gc)
-    s_g[2 * C + tid] = R.b;                                // beta
+    s_g[2 * C + tid] = raw_to_f32(R.b, b_dt);              // beta
     s_g[3 * C + tid] = tid < nv ? gexp(gl - gv) : 0.f;     // gate
   }
 }
@@ -457,142 +614,154 @@ __device__ __forceinline__ void kkt_phase(unsigned char* smem) {
   }
 }
 
-// (I + A)^-1 for the solver waves (solve_tril.py:184-331, fp32 throughout):
-// diagonal 16x16 blocks by forward substitution (one wave, lane = one column of
-// one block), then block merges X_ij = -X_ii sum_k A_ik X_kj with fp32 MFMA.
-// Every block is written rounded to TC into s_Ai ([t][pcol(t')]); the fp32
-// copies needed by later merge levels stay in s_A (the strictly lower blocks
-// keep A, X_ij is kept in the unused upper block (j, i)).
-// Waves: diagonal by wave W0; level 1 by W0, W0-1, W0-2; level 2 by W0, W0-1;
-// level 3 by W0 (W0 = NW - 1).  `other` runs on the waves while they are idle.
-template <typename TC, int K, int V, bool WITH_Q, int NW, typename Other>
-__device__ __forceinline__ void solve_phase(unsigned char* smem, Other&& other) {
+// (I + A)^-1 (solve_tril.py:184-331, fp32 throughout, rounded to TC once):
+//   diag_solve:  the four 16x16 diagonal blocks D_i = (I + A_ii)^-1 by forward
+//                substitution on one wave (lane = one column of one block), in
+//                place in s_A, and rounded into s_Ai;
+//   chain_solve: column block j of the inverse, X_ij = -D_i sum_{k=j}^{i-1} A_ik X_kj
+//                for i = j+1..3, on one wave per j (j = 0, 1, 2); the X_kj stay in
+//                registers as the B operand of the next product, so the three
+//                chains need no barrier between their steps.
+// Ai is stored [t][pcol(t')].
+template <typename TC, int K, int V, bool WITH_Q>
+__device__ __forceinline__ void diag_solve(unsigned char* smem) {
   using L = SegLds<TC, K, V, WITH_Q>;
-  static_assert(NW >= 3, "the block merges use three waves");
   float* s_A = reinterpret_cast<float*>(smem + L::off_A);
   TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);
-  const int wid = threadIdx.x / WAVE;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
-  constexpr int W0 = NW - 1;
-  const int role = W0 - wid;            // 0 = the solver wave
-  if (role == 0) {
-    float x[16];
-    float* Xb = s_A + (16 * lg) * L::LDA + 16 * lg;
+  float x[16];
+  float* Xb = s_A + (16 * lg) * L::LDA + 16 * lg;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float s = 0.f;
+  for (int i = 0; i < 16; ++i) {
+    float s = 0.f;
 #pragma unroll
-      for (int r = 0; r < i; ++r) s = fmaf(Xb[i * L::LDA + r], x[r], s);
-      x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -s);
-    }
-    // same wave: the reads above are done before these writes
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      Xb[i * L::LDA + lc] = x[i];
-      s_Ai[(16 * lg + i) * L::LDT + pcol(16 * lg + lc)] = from_f32<TC>(x[i]);
-    }
-  } else if (role >= 3) {
-    other();
+    for (int r = 0; r < i; ++r) s = fmaf(Xb[i * L::LDA + r], x[r], s);
+    x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -s);
   }
-  __syncthreads();
-  auto blk = [&](int i, int j) { return s_A + (16 * i) * L::LDA + 16 * j; };
-  auto put = [&](int i, int j, const f32x4& r) {
-    float* up = blk(j, i);
+  // same wave: the reads above are complete before these writes
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      up[(4 * lg + jj) * L::LDA + lc] = -r[jj];
-      s_Ai[(16 * i + 4 * lg + jj) * L::LDT + pcol(16 * j + lc)] = from_f32<TC>(-r[jj]);
-    }
-  };
-  if (role < 3) {                                   // X_{i,i-1}, i = 3 - role
-    const int i = 3 - role, j = i - 1;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
-    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
-    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
-    put(i, j, r);
-  }
-  if (role == 2) other();
-  __syncthreads();
-  if (role < 2) {                                   // X_{i,i-2}, i = 3 - role
-    const int i = 3 - role, j = i - 2;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
-    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);
-    mma16_f32_lds(t, blk(i, j + 1), L::LDA, blk(j, j + 1), L::LDA);
-    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);
-    put(i, j, r);
-  }
-  if (role == 1) other();
-  __syncthreads();
-  if (role == 0) {                                  // X_{3,0}
-    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
-    mma16_f32_lds(t, blk(3, 0), L::LDA, blk(0, 0), L::LDA);
-    mma16_f32_lds(t, blk(3, 1), L::LDA, blk(0, 1), L::LDA);
-    mma16_f32_lds(t, blk(3, 2), L::LDA, blk(0, 2), L::LDA);
-    mma16_f32_lds_reg(r, blk(3, 3), L::LDA, t);
-    put(3, 0, r);
-    other();
+  for (int i = 0; i < 16; ++i) {
+    Xb[i * L::LDA + lc] = x[i];
+    s_Ai[(16 * lg + i) * L::LDT + pcol(16 * lg + lc)] = from_f32<TC>(x[i]);
   }
 }
 
-// w^T = kb^T Ai^T for the 16-row d tiles dt = wid, wid + NW, ... -> s_w[t][d]
-// (kb = k beta exp(gc) with the reference's roundings, wy_fast.py:67-81).
-template <typename TC, int K, int V, bool WITH_Q, int NW>
-__device__ __forceinline__ void w_phase(unsigned char* smem, bool beta_lowp) {
+template <typename TC, int K, int V, bool WITH_Q>
+__device__ __forceinline__ void chain_solve(unsigned char* smem, int j) {
   using L = SegLds<TC, K, V, WITH_Q>;
-  TC* s_w = reinterpret_cast<TC*>(smem + L::off_k);
+  const float* s_A = reinterpret_cast<const float*>(smem + L::off_A);
+  TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  auto blk = [&](int r, int c) { return s_A + (16 * r) * L::LDA + 16 * c; };
+  f32x4 X[3];                                   // X_{j+1,j}, X_{j+2,j}, X_{j+3,j}
+  for (int i = j + 1; i < 4; ++i) {
+    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+    mma16_f32_lds(t, blk(i, j), L::LDA, blk(j, j), L::LDA);           // A_ij D_j
+#pragma unroll
+    for (int k = 1; k < 3; ++k)
+      if (j + k < i) mma16_f32_lds_reg(t, blk(i, j + k), L::LDA, X[k - 1]);   // A_ik X_kj
+    mma16_f32_lds_reg(r, blk(i, i), L::LDA, t);                       // D_i (...)
+    r = -r;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      if (k == i - j - 1) X[k] = r;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      s_Ai[(16 * i + 4 * lg + jj) * L::LDT + pcol(16 * j + lc)] = from_f32<TC>(r[jj]);
+  }
+}
+
+// kb^T fragments (kb = k beta exp(gc) with the reference's roundings, wy_fast.py:67-81)
+// of the d tiles dt = wid + NW * n; independent of Ai.
+template <typename TC, int K, int V, bool WITH_Q, int NW>
+struct WFrags {
+  static constexpr int ND = (K / 16 + NW - 1) / NW;
+  Frag<TC> kb[ND][2];
+};
+template <typename TC, int K, int V, bool WITH_Q, int NW>
+__device__ __forceinline__ void w_frags(const unsigned char* smem, bool beta_lowp, WFrags<TC, K, V, WITH_Q, NW>& F) {
+  using L = SegLds<TC, K, V, WITH_Q>;
   const TC* s_kT = reinterpret_cast<const TC*>(smem + L::off_kT);
-  const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
   const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
   const int wid = threadIdx.x / WAVE;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
-  for (int dt = wid; dt < K / 16; dt += NW) {
+#pragma unroll
+  for (int n = 0; n < WFrags<TC, K, V, WITH_Q, NW>::ND; ++n) {
+    const int dt = wid + NW * n;
+    if (dt >= K / 16) break;
     const int d = 16 * dt + lc;
-    Frag<TC> kb[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       float x[8];
       lds_get8<TC>(s_kT + d * L::LDT + tchunk(d, 32 * ks + 8 * lg), x);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_g + 2 * C + 32 * ks + 4 * lg);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(s_g + 2 * C + 32 * ks + 16 + 4 * lg);
+      const f32x4 e0 = *reinterpret_cast<const f32x4*>(s_g + C + 32 * ks + 4 * lg);
+      const f32x4 e1 = *reinterpret_cast<const f32x4*>(s_g + C + 32 * ks + 16 + 4 * lg);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int t = frag_t(ks, lg, e);
-        float v = x[e] * s_g[2 * C + t];
+        float v = x[e] * (e < 4 ? b0[e] : b1[e - 4]);
         if (beta_lowp) v = round_to<TC>(v);
-        x[e] = v * s_g[C + t];
+        x[e] = v * (e < 4 ? e0[e] : e1[e - 4]);
       }
-      kb[ks] = frag_pack<TC>(x);
+      F.kb[n][ks] = frag_pack<TC>(x);
     }
+  }
+}
+// w^T = kb^T Ai^T for this wave's d tiles -> s_w[t][pcol(d)]
+template <typename TC, int K, int V, bool WITH_Q, int NW>
+__device__ __forceinline__ void w_products(unsigned char* smem, const WFrags<TC, K, V, WITH_Q, NW>& F) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  TC* s_w = reinterpret_cast<TC*>(smem + L::off_k);
+  const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+#pragma unroll
+  for (int n = 0; n < WFrags<TC, K, V, WITH_Q, NW>::ND; ++n) {
+    const int dt = wid + NW * n;
+    if (dt >= K / 16) break;
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks <= tn / 2; ++ks)
-        mma(acc, kb[ks], frag_at<TC>(s_Ai + (16 * tn + lc) * L::LDT + 32 * ks + 8 * lg));
+        mma(acc, F.kb[n][ks], frag_at<TC>(s_Ai + (16 * tn + lc) * L::LDT + 32 * ks + 8 * lg));
       st4<TC>(s_w + (16 * tn + lc) * L::LDK + pcol(16 * dt + 4 * lg), acc[0], acc[1], acc[2], acc[3]);
     }
   }
 }
 
-// u (64 rows x V columns v0..v0+15) = Ai (v beta), rounded to TC (wy_fast.py:61-66), in accumulator tiles
+// vb^T fragments (vb = v beta, wy_fast.py:61-65) of V columns v0..v0+15; independent of Ai
 template <typename TC, int K, int V, bool WITH_Q>
-__device__ __forceinline__ void u_cols(const unsigned char* smem, int v0, f32x4 (&u)[4]) {
+__device__ __forceinline__ void u_frags(const unsigned char* smem, int v0, Frag<TC> (&vb)[2]) {
   using L = SegLds<TC, K, V, WITH_Q>;
   const TC* s_vT = reinterpret_cast<const TC*>(smem + L::off_vT);
-  const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
   const float* s_b = reinterpret_cast<const float*>(smem + L::off_g) + 2 * C;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
   const int vv = v0 + lc;
-  Frag<TC> vb[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     float x[8];
     lds_get8<TC>(s_vT + vv * L::LDT + tchunk(vv, 32 * ks + 8 * lg), x);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_b + 32 * ks + 4 * lg);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(s_b + 32 * ks + 16 + 4 * lg);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] *= s_b[frag_t(ks, lg, e)];
+    for (int e = 0; e < 8; ++e) x[e] *= (e < 4 ? b0[e] : b1[e - 4]);
     vb[ks] = frag_pack<TC>(x);
   }
+}
+// u (64 rows x 16 columns) = Ai vb, rounded to TC, in accumulator tiles
+template <typename TC, int K, int V, bool WITH_Q>
+__device__ __forceinline__ void u_products(const unsigned char* smem, const Frag<TC> (&vb)[2], f32x4 (&u)[4]) {
+  using L = SegLds<TC, K, V, WITH_Q>;
+  const TC* s_Ai = reinterpret_cast<const TC*>(smem + L::off_Ai);
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -662,6 +831,39 @@ __device__ __forceinline__ void gate_frags(const f32x4 (&Y)[4][CT], const float*
     for (int ct = 0; ct < CT; ++ct) vg[ks][ct] = acc_frag<TC>(Y[2 * ks][ct] * ga, Y[2 * ks + 1][ct] * gb);
   }
 }
+
+// The output tile of a wave (64 tokens x 16*CT columns, o^T accumulator layout:
+// lane holds 4 consecutive columns of token 16*tn + lane%16), held in storage
+// precision until it is stored.
+template <typename TC, int CT>
+struct OutPending {
+  typedef typename std::conditional<sizeof(TC) == 2, uint2, f32x4>::type Piece;
+  Piece v[4][CT];
+  int64_t t0;
+  int nv;                     // valid tokens; 0 = nothing pending
+  __device__ __forceinline__ void set(int tn, int ct, const f32x4& r) {
+    if constexpr (sizeof(TC) == 2) {
+      v[tn][ct].x = pack_bf16x2(r[0], r[1]);
+      v[tn][ct].y = pack_bf16x2(r[2], r[3]);
+    } else {
+      v[tn][ct] = r;
+    }
+  }
+  __device__ __forceinline__ void store(TC* o, int H, int h, int V, int vw) {
+    const int l = lane_id();
+    const int lg = l >> 4, lc = l & 15;
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      const int t = 16 * tn + lc;
+      if (t < nv) {
+        TC* orow = o + ((t0 + t) * H + h) * V + vw + 4 * lg;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) *reinterpret_cast<Piece*>(orow + 16 * ct) = v[tn][ct];
+      }
+    }
+    nv = 0;
+  }
+};
 
 // ---------------------------------------------------------------------------
 // seg_out: exact recurrence + output over one segment
@@ -745,23 +947,27 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
   zero_upper_tiles<TC, K, V, true, NT>(smem);
 
   CR cur;
+  unsigned char* raw = smem + L::raw_off;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
-  load_chunk<TC, TQ, K, V, true, NT>(cur, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
+  load_chunk<TC, TQ, K, V, true, NT>(cur, raw, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
   TC* o = reinterpret_cast<TC*>(a.o);
+  OutPending<TC, CT> op;
+  op.nv = 0;
 
   for (int ci = 0; ci < sl.nch; ++ci) {
-    stage_chunk<TC, TQ, K, V, true, NT>(cur, smem, qs, ks_, nv);
-    __syncthreads();
+    stage_chunk<TC, TQ, K, V, true, NT>(cur, raw, smem, qs, ks_, nv, a.g_dtype, a.beta_dtype);
+    op.store(o, H, h, V, vw);
+    lds_barrier();
     const int64_t t0c = t0;
     const int nvc = nv;
     if (ci + 1 < sl.nch) {
       t0 += C;
       nv = (int)min((int64_t)C, sl.eos - t0);
-      load_chunk<TC, TQ, K, V, true, NT>(cur, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
+      load_chunk<TC, TQ, K, V, true, NT>(cur, raw, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
     }
     kkt_phase<TC, K, V, true, NW>(smem);
-    __syncthreads();
+    lds_barrier();
 
     // ---- h = S rounded (the snapshot of chunk_delta_h.py:129-139) as operand fragments
     Frag<TC> hb[K / 32][CT];
@@ -770,7 +976,7 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) hb[ks][ct] = acc_frag<TC>(S[2 * ks][ct], S[2 * ks + 1][ct]);
     }
-    // ---- o1^T = h^T q^T (chunk_o.py:84-101), on each wave while it is not solving
+    // ---- o1^T = h^T q^T (chunk_o.py:84-101)
     f32x4 o1[4][CT];
     auto inter_chunk_out = [&]() {
 #pragma unroll
@@ -785,26 +991,39 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
         }
       }
     };
-    solve_phase<TC, K, V, true, NW>(smem, inter_chunk_out);
-    __syncthreads();   // Ai complete
+    constexpr int W0 = NW - 1;            // the solver wave; waves W0, W0-1, W0-2 run the column chains
+    const int role = W0 - wid;
+    if (role == 0) diag_solve<TC, K, V, true>(smem);
+    lds_barrier();   // diagonal blocks
+    if (role < 3) chain_solve<TC, K, V, true>(smem, role);
+    WFrags<TC, K, V, true, NW> wf;
+    w_frags<TC, K, V, true, NW>(smem, beta_lowp, wf);
+    Frag<TC> vb[CT][2];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) u_frags<TC, K, V, true>(smem, vw + 16 * ct, vb[ct]);
+    lds_barrier();   // Ai complete
 
-    w_phase<TC, K, V, true, NW>(smem, beta_lowp);
+    w_products<TC, K, V, true, NW>(smem, wf);
     f32x4 Y[4][CT];
     {
       f32x4 u[4];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        u_cols<TC, K, V, true>(smem, vw + 16 * ct, u);
+        u_products<TC, K, V, true>(smem, vb[ct], u);
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u[tm];
       }
     }
-    __syncthreads();   // w complete
+    lds_barrier();   // w complete
 
     // ---- v' = u - w h                                   (chunk_delta_h.py:141-157)
     sub_wx<TC, K, V, true, CT>(Y, hb, smem);
+    inter_chunk_out();
 
-    // ---- o^T = scale (o1^T exp(gc) + v_new^T Aqk^T)     (chunk_o.py:102-128)
+    // ---- o^T = scale (o1^T exp(gc) + v_new^T Aqk^T)     (chunk_o.py:102-128); stored
+    //      after the next chunk is staged, so that no wait for loads covers the stores
+    op.t0 = t0c;
+    op.nv = nvc;
     Frag<TC> vn[2][CT];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -825,24 +1044,19 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
           for (int ct = 0; ct < CT; ++ct) mma(o2[ct], vn[ks][ct], ba);
         }
       }
-      if (t < nvc) {
-        const float eg = s_g[C + t] * a.scale;
-        TC* orow = o + ((t0c + t) * H + h) * V + vw + 4 * lg;
+      const float eg = s_g[C + t] * a.scale;
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          const f32x4 r = o1[tn][ct] * eg + o2[ct] * a.scale;
-          st4<TC>(orow + 16 * ct, r[0], r[1], r[2], r[3]);
-        }
-      }
+      for (int ct = 0; ct < CT; ++ct) op.set(tn, ct, o1[tn][ct] * eg + o2[ct] * a.scale);
     }
 
     // ---- S = exp(g_last) S + k^T (v' exp(g_last - gc))   (chunk_delta_h.py:163-211)
     Frag<TC> vg[2][CT];
     gate_frags<TC, CT>(Y, s_g + 3 * C, vg);
     state_update<TC, K, V, true, CT>(S, vg, smem, gexp(s_g[nvc - 1]));
-    __syncthreads();   // LDS is restaged for the next chunk
+    lds_barrier();   // LDS is restaged for the next chunk
   }
 
+  op.store(o, H, h, V, vw);
   if (a.ht && sl.j == sl.nseg - 1) {
     float* p = a.ht + ((int64_t)sl.n * H + h) * K * V + 4 * lg * V + vw + lc;
 #pragma unroll
@@ -903,31 +1117,45 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
   zero_upper_tiles<TC, K, V, false, NT>(smem);
 
   CR cur;
+  unsigned char* raw = smem + L::raw_off;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
-  load_chunk<TC, TQ, K, V, false, NT>(cur, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
+  load_chunk<TC, TQ, K, V, false, NT>(cur, raw, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h,
+                                      H);
   for (int ci = 0; ci < sl.nch; ++ci) {
-    stage_chunk<TC, TQ, K, V, false, NT>(cur, smem, 1.f, ks_, nv);
-    __syncthreads();
+    stage_chunk<TC, TQ, K, V, false, NT>(cur, raw, smem, 1.f, ks_, nv, a.g_dtype, a.beta_dtype);
+    lds_barrier();
     const int nvc = nv;
     if (ci + 1 < sl.nch) {
       t0 += C;
       nv = (int)min((int64_t)C, sl.eos - t0);
-      load_chunk<TC, TQ, K, V, false, NT>(cur, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h,
-                                          H);
+      load_chunk<TC, TQ, K, V, false, NT>(cur, raw, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv,
+                                          h, H);
     }
     kkt_phase<TC, K, V, false, NW>(smem);
-    __syncthreads();
-    solve_phase<TC, K, V, false, NW>(smem, []() {});
-    __syncthreads();   // Ai complete
-    w_phase<TC, K, V, false, NW>(smem, beta_lowp);
+    lds_barrier();
+    constexpr int W0 = NW - 1;
+    const int role = W0 - wid;
+    if (role == 0) diag_solve<TC, K, V, false>(smem);
+    lds_barrier();   // diagonal blocks
+    if (role < 3) chain_solve<TC, K, V, false>(smem, role);
+    WFrags<TC, K, V, false, NW> wf;
+    w_frags<TC, K, V, false, NW>(smem, beta_lowp, wf);
+    Frag<TC> vb[CT][2];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int c0 = xw + 16 * ct;
+      if (c0 >= K) u_frags<TC, K, V, false>(smem, c0 - K, vb[ct]);
+    }
+    lds_barrier();   // Ai complete
+    w_products<TC, K, V, false, NW>(smem, wf);
     f32x4 Y[4][CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const int c0 = xw + 16 * ct;
       if (c0 >= K) {
         f32x4 u[4];
-        u_cols<TC, K, V, false>(smem, c0 - K, u);
+        u_products<TC, K, V, false>(smem, vb[ct], u);
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u[tm];
       } else {
@@ -935,7 +1163,8 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
         for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    __syncthreads();   // w complete
+    lds_barrier();   // w complete
+    __builtin_amdgcn_sched_barrier(0);
     Frag<TC> xb[K / 32][CT];
 #pragma unroll
     for (int ks = 0; ks < K / 32; ++ks) {
@@ -943,10 +1172,11 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
       for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag<TC>(X[2 * ks][ct], X[2 * ks + 1][ct]);
     }
     sub_wx<TC, K, V, false, CT>(Y, xb, smem);
+    __builtin_amdgcn_sched_barrier(0);
     Frag<TC> yg[2][CT];
     gate_frags<TC, CT>(Y, s_g + 3 * C, yg);
     state_update<TC, K, V, false, CT>(X, yg, smem, gexp(s_g[nvc - 1]));
-    __syncthreads();
+    lds_barrier();
   }
 
   const int64_t s = blockIdx.x;
@@ -1103,11 +1333,12 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   if (!mark(0)) return -1;
   if (p.run_trans) {
     using LT = SegLds<TC, K, V, false>;
-    static_assert(LT::total <= 160 * 1024, "seg_trans tile does not fit in LDS");
+    constexpr size_t lds = LT::raw_off + ChunkRegs<TC, TQ, K, V, false, TransCfg<K, V>::NT>::RAW;
+    static_assert(lds <= 160 * 1024, "seg_trans tile does not fit in LDS");
     auto kt = seg_trans_kernel<TC, TQ, K, V>;
-    if (set_lds(kt, LT::total)) return -1;
+    if (set_lds(kt, lds)) return -1;
     SegTransArgs ta{p.k, p.v, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, p.M, p.R};
-    hipLaunchKernelGGL(kt, grid, dim3(TransCfg<K, V>::NT), LT::total, s, ta, G);
+    hipLaunchKernelGGL(kt, grid, dim3(TransCfg<K, V>::NT), lds, s, ta, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(1)) return -1;
@@ -1121,12 +1352,13 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   if (!mark(2)) return -1;
   if (p.ns_grid > 0) {
     using LO = SegLds<TC, K, V, true>;
-    static_assert(LO::total <= 160 * 1024, "seg_out tile does not fit in LDS");
+    constexpr size_t lds = LO::raw_off + ChunkRegs<TC, TQ, K, V, true, OutCfg<K, V>::NT>::RAW;
+    static_assert(lds <= 160 * 1024, "seg_out tile does not fit in LDS");
     auto ko = seg_out_kernel<TC, TQ, K, V>;
-    if (set_lds(ko, LO::total)) return -1;
+    if (set_lds(ko, lds)) return -1;
     SegOutArgs oa{p.q, p.k, p.v, p.g, p.beta, p.q_scale, p.k_scale, p.g_dtype, p.beta_dtype,
                   p.h0, p.h0_dtype, p.s_init, p.scale, p.o, p.ht};
-    hipLaunchKernelGGL(ko, grid, dim3(OutCfg<K, V>::NT), LO::total, s, oa, G);
+    hipLaunchKernelGGL(ko, grid, dim3(OutCfg<K, V>::NT), lds, s, oa, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(3)) return -1;
