@@ -87,11 +87,11 @@ int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs);
 
 /* ---- kernel timing (measurement hook, no counterpart in the reference) ----
  * kairos_gdn_profile_begin() makes every following kairos_gdn_chunk_fwd call
- * of the fused path record hipEvents on its stream around its three kernels
- * (seg_trans, seg_combine, seg_out).  kairos_gdn_profile_end() waits for the
- * recorded events, stops recording, writes the average milliseconds of the
- * three kernels per call into avg_ms[0..min(n,3)-1] and returns the number of
- * calls recorded, or -1 on a HIP error (message in kairos_gdn_last_error()).
+ * of the fused path record hipEvents on its stream around its four kernels
+ * (seg_prep, seg_trans, seg_combine, seg_out).  kairos_gdn_profile_end() waits
+ * for the recorded events, stops recording, writes the average milliseconds of
+ * the four kernels per call into avg_ms[0..min(n,4)-1] and returns the number
+ * of calls recorded, or -1 on a HIP error (message in kairos_gdn_last_error()).
  * A kernel the call did not need (seg_trans / seg_combine for single-segment
  * sequences) reports ~0 ms.  The staged fp32 K = 128 path records nothing. */
 int kairos_gdn_profile_begin(void);

@@ -181,8 +181,10 @@ SegPlan plan_segments(int64_t B, int64_t T, int64_t H, int64_t n_seqs) {
   return P;
 }
 
-size_t seg_ws(int64_t H, int64_t K, int64_t V, int64_t n_seqs, const SegPlan& P) {
+size_t seg_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, const SegPlan& P) {
   size_t total = n_seqs > 0 ? 2 * align_up(sizeof(int32_t) * (n_seqs + 1)) : 0;
+  // chunk inverses Ai: bf16 [chunks, H, 64, 64]
+  total += align_up((size_t)chunks_bound(B, T, n_seqs) * H * kgdn::C * kgdn::C * 2);
   if (P.trans || P.combine) {
     const size_t blocks = (size_t)P.ns * H;
     total += align_up(blocks * K * K * sizeof(float));        // M
@@ -193,31 +195,34 @@ size_t seg_ws(int64_t H, int64_t K, int64_t V, int64_t n_seqs, const SegPlan& P)
 }
 
 // Kernel timing of kairos_gdn_chunk_fwd (kairos_gdn_profile_begin / _end): while
-// enabled, every fused call records 4 hipEvents on its stream around its three kernels.
+// enabled, every fused call records kProfEvents hipEvents on its stream around
+// its kProfKernels kernels (seg_prep, seg_trans, seg_combine, seg_out).
+constexpr int kProfKernels = 4;
+constexpr int kProfEvents = kProfKernels + 1;
 struct Profile {
   std::mutex mu;
   bool on = false;
-  std::vector<hipEvent_t> pool;   // 4 events per recorded call
+  std::vector<hipEvent_t> pool;   // kProfEvents per recorded call
   size_t used = 0;
 };
 Profile& profile() {
   static Profile p;
   return p;
 }
-// Next set of 4 events while profiling is on, else nullptr.
+// Next set of kProfEvents events while profiling is on, else nullptr.
 hipEvent_t* profile_events() {
   Profile& P = profile();
   std::lock_guard<std::mutex> lk(P.mu);
   if (!P.on) return nullptr;
-  if (P.used + 4 > P.pool.size()) {
-    for (int i = 0; i < 4; ++i) {
+  if (P.used + kProfEvents > P.pool.size()) {
+    for (int i = 0; i < kProfEvents; ++i) {
       hipEvent_t e;
       if (hipEventCreate(&e) != hipSuccess) return nullptr;
       P.pool.push_back(e);
     }
   }
   hipEvent_t* ev = P.pool.data() + P.used;
-  P.used += 4;
+  P.used += kProfEvents;
   return ev;
 }
 
@@ -294,7 +299,7 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0) return 0;
   const size_t tok = (size_t)(B * T * H);
   const int cdt = compute_dtype(qk_dtype, v_dtype);
-  size_t total = kgdn::seg_fwd_supported(cdt, (int)K, (int)V) ? seg_ws(H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
+  size_t total = kgdn::seg_fwd_supported(cdt, (int)K, (int)V) ? seg_ws(B, T, H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
                                                               : staged_ws(B, T, H, K, V, n_seqs, cdt);
   if (use_qk_l2norm) total += 2 * align_up(tok * K * dt_size(qk_dtype));
   return total;
@@ -359,6 +364,8 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
     chunk_off = co;
     seg_off = so;
   }
+  const int64_t nc_grid = chunks_bound(B, T, n_seqs);
+  void* Ai = cv.take((size_t)nc_grid * H * kgdn::C * kgdn::C * 2);
   float* M = nullptr;
   float* R = nullptr;
   float* s_init = nullptr;
@@ -385,6 +392,7 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
   a.cu = cu_seqlens; a.chunk_off = chunk_off; a.seg_off = seg_off;
   a.N = (int)G.N; a.T = T; a.H = (int)H; a.L = P.L; a.nseg_fixed = P.nseg_fixed; a.ns_grid = P.ns;
   a.M = M; a.R = R; a.s_init = s_init; a.scale = scale; a.o = o; a.ht = final_state;
+  a.Ai = Ai; a.nc_grid = nc_grid;
   a.run_trans = P.trans && P.ns > 0;
   a.run_combine = P.combine;
   a.events = profile_events();
@@ -409,15 +417,15 @@ int kairos_gdn_profile_end(double* avg_ms, int n) {
   Profile& P = profile();
   std::lock_guard<std::mutex> lk(P.mu);
   P.on = false;
-  const size_t calls = P.used / 4;
-  double acc[3] = {0.0, 0.0, 0.0};
+  const size_t calls = P.used / kProfEvents;
+  double acc[kProfKernels] = {};
   for (size_t c = 0; c < calls; ++c) {
-    hipEvent_t* e = P.pool.data() + 4 * c;
-    if (hipEventSynchronize(e[3]) != hipSuccess) {
+    hipEvent_t* e = P.pool.data() + kProfEvents * c;
+    if (hipEventSynchronize(e[kProfKernels]) != hipSuccess) {
       fail(KAIROS_GDN_EHIP, "kairos_gdn_profile_end: %s", hipGetErrorString(hipGetLastError()));
       return -1;
     }
-    for (int k = 0; k < 3; ++k) {
+    for (int k = 0; k < kProfKernels; ++k) {
       float ms = 0.f;
       if (hipEventElapsedTime(&ms, e[k], e[k + 1]) != hipSuccess) {
         fail(KAIROS_GDN_EHIP, "kairos_gdn_profile_end: %s", hipGetErrorString(hipGetLastError()));
@@ -426,7 +434,7 @@ int kairos_gdn_profile_end(double* avg_ms, int n) {
       acc[k] += ms;
     }
   }
-  for (int k = 0; k < 3 && k < n; ++k) avg_ms[k] = calls ? acc[k] / (double)calls : 0.0;
+  for (int k = 0; k < kProfKernels && k < n; ++k) avg_ms[k] = calls ? acc[k] / (double)calls : 0.0;
   P.used = 0;
   g_last_error.clear();
   return (int)calls;

@@ -102,9 +102,11 @@ struct SegFwdArgs {
   float scale;
   void* o;                // out [B*T, H, V]
   float* ht;              // out [N, H, K, V] or nullptr
+  void* Ai;               // [nc_grid, H, 64, 64] bf16 chunk inverses (seg_prep -> seg_trans, seg_out)
+  int64_t nc_grid;        // number of chunks (varlen: an upper bound)
   bool run_trans;         // some sequence has more than one segment
   bool run_combine;       // ... or final_state of empty sequences is needed
-  hipEvent_t* events;     // optional [4]: recorded before seg_trans, seg_combine, seg_out and after seg_out
+  hipEvent_t* events;     // optional [5]: recorded before seg_prep, seg_trans, seg_combine, seg_out and after seg_out
 };
 
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported

@@ -50,19 +50,29 @@ def test_num_chunks_bound():
 
 
 def test_workspace_size():
-    """The fused bf16 path keeps only per-segment [M | R] maps and segment states in the
-    workspace (bounded by the CU count, not by T); the in-kernel L2 norm adds two q/k
+    """The fused bf16 path holds the bf16 chunk inverses Ai (64 x 64 per chunk and
+    head) and, for multi-segment sequences, the per-segment [M | R] maps and segment
+    states (bounded by the CU count, not by T); the in-kernel L2 norm adds two q/k
     copies; the staged fp32 K=128 path holds the reference's per-chunk intermediates."""
     lib = _lib.load()
-    a = lib.kairos_gdn_chunk_fwd_workspace_size(1, 8192, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
-    b = lib.kairos_gdn_chunk_fwd_workspace_size(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
-    c = lib.kairos_gdn_chunk_fwd_workspace_size(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 1)
-    assert 0 < a <= b < c
-    assert b < 128 << 20
+
+    def ai(nchunks, H):
+        return nchunks * H * 64 * 64 * 2
+
+    def seg_state(B, T, H, K, V):
+        L = lib.kairos_gdn_segment_chunks(B, T, H, 0)
+        nseg = -(-(-(-T // 64)) // L)
+        return 0 if nseg == 1 else B * nseg * H * (K * K + 2 * K * V) * 4
+
+    ws = lib.kairos_gdn_chunk_fwd_workspace_size
+    a = ws(1, 8192, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
+    b = ws(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
+    c = ws(1, 32760, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 1)
+    assert a == ai(128, 20) + seg_state(1, 8192, 20, 128, 128)
+    assert b == ai(512, 20) + seg_state(1, 32760, 20, 128, 128)
     assert c - b == 2 * 32760 * 20 * 128 * 2
-    single = lib.kairos_gdn_chunk_fwd_workspace_size(8, 1560, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0)
-    assert single == 0                       # one segment per sequence: no scan state
-    staged = lib.kairos_gdn_chunk_fwd_workspace_size(1, 8192, 20, 128, 128, 0, _lib.F32, _lib.F32, 0)
+    assert ws(8, 1560, 20, 128, 128, 0, _lib.BF16, _lib.BF16, 0) == ai(8 * 25, 20)   # one segment each
+    staged = ws(1, 8192, 20, 128, 128, 0, _lib.F32, _lib.F32, 0)
     assert staged > 8192 * 20 * 128 * 4 * 3
 
 

@@ -342,11 +342,10 @@ def test_segment_scan_slow_gates(L, K, V, cu, monkeypatch):
     check_against_oracle(x, "bf16", o, ht, cu=cu)
 
 
-def test_segment_scan_fp32_against_recurrence(monkeypatch):
-    """fp32 fused path with 1-chunk segments against the fp64 token recurrence (slow gates)."""
+def test_fp32_against_recurrence():
+    """fp32 compute (the stage kernels) against the fp64 token recurrence with slow gates."""
     B, T, H, K, V = 2, 700, 2, 64, 64
-    note("segment scan fp32 L=1 vs fp64 token recurrence")
-    monkeypatch.setenv("KAIROS_GDN_SEG_CHUNKS", "1")
+    note("fp32 stage path vs fp64 token recurrence")
     x = make_inputs(B, T, H, K, V, seed=3, dtype="fp32", h0_scale=0.5)
     x["g"] = (x["g"] * 0.004).astype(np.float32)
     o, ht = run_gpu(x, "fp32")
