@@ -54,17 +54,20 @@ namespace {
 
 template <int K, int V> struct OutCfg { static constexpr int NW = V / 16, NT = 64 * NW; };
 template <int K, int V> struct TransCfg { static constexpr int NW = (K + V) / 32, NT = 64 * NW; };
-constexpr int NT_COMB = 256;
-constexpr int NW_COMB = 4;
 
-// Workgroup barrier that orders LDS only.  __syncthreads() also fences global
-// memory, which makes every barrier wait for all outstanding vector memory
-// operations -- the next chunk's loads and the output stores included.  The
-// waves of a workgroup share nothing but LDS, so an LDS fence is sufficient.
+// Workgroup barrier that orders LDS only: this wave's LDS reads and writes are
+// complete (lgkmcnt(0)), then s_barrier.  __syncthreads(), and even a
+// workgroup fence on LDS alone, also waits for vmcnt(0), because the direct
+// global->LDS loads count as LDS writes: every barrier would then wait for the
+// next chunk's prefetch and the output stores.  The waves of a workgroup share
+// nothing but LDS, and the direct loads are waited for explicitly
+// (wait_loads) before the barrier that publishes them.  The empty asm
+// statements keep the compiler from moving memory accesses across the barrier.
 __device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0); vmcnt, expcnt at their maxima
   __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  asm volatile("" ::: "memory");
 }
 
 // Column permutation of the LDS tiles the kernel writes itself (w, Ai, Aqk):
@@ -74,10 +77,14 @@ __device__ __forceinline__ int pcol(int c) {
   return (c & ~31) | (((c >> 2) & 3) << 3) | (((c >> 4) & 1) << 2) | (c & 3);
 }
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lmem_void;
+
+// LDS byte address of a pointer into this workgroup's LDS
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lmem_void*)p;
+}
 
 template <typename TC>
 __device__ __forceinline__ Frag<TC> frag_at(const TC* p) {
@@ -147,22 +154,71 @@ struct Tile {
   // Transposed fragment: lane (l%16 = j, l/16 = lg) gets t[32ks + 4lg + e][c0 + j] (e = 0..3) and
   // t[32ks + 16 + 4lg + e][c0 + j].  ds_read_b64_tr_b16 within a 16-lane group: lane i reads 4
   // columns of one row, lane j receives element j%4 of lane 4e + j/4's read as its element e.
-  __device__ static __forceinline__ Frag<bf16> col_tr(const bf16* t, int ks, int c0) {
+  // col_tr_addr gives the LDS byte addresses of the two reads (rows r0 and r0 + 16).
+  __device__ static __forceinline__ void col_tr_addr(const bf16* t, int ks, int c0, uint32_t& a0, uint32_t& a1) {
     const int l = lane_id();
     const int lg = l >> 4, i = l & 15;
     const int col = c0 + 4 * (i & 3);
     const int r0 = 32 * ks + 4 * lg + (i >> 2);
     const int r1 = r0 + 16;
-    const bf16* p0 = t + off(r0, col >> 3) + (col & 7);
-    const bf16* p1 = t + off(r1, col >> 3) + (col & 7);
-    const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
-    const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
-    const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
-    Frag<bf16> f;
-    f.v = __builtin_bit_cast(bf16x8, make_uint4(ua.x, ua.y, ub.x, ub.y));
-    return f;
+    a0 = lds_addr(t + off(r0, col >> 3) + (col & 7));
+    a1 = lds_addr(t + off(r1, col >> 3) + (col & 7));
   }
 };
+
+// Transposed fragments through inline asm.  The compiler's wait tracking treats
+// ds_read_b64_tr_b16 (the builtin) as a possible reader of whatever an
+// in-flight direct global->LDS load writes, and puts a vmcnt(0) before it --
+// a wait for the next chunk's prefetch in the middle of the current chunk.
+// The asm form is outside that tracking; it waits for its own reads
+// (lgkmcnt(0)) before returning, so its results are ready when used.
+__device__ __forceinline__ Frag<bf16> tr_pair(u32x2 a, u32x2 b) {
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+  return f;
+}
+// N = 2 fragments from 4 addresses (fragment f from reads 2f, 2f + 1)
+__device__ __forceinline__ void tr_read2(const uint32_t (&a)[4], Frag<bf16> (&f)[2]) {
+  u32x2 r0, r1, r2, r3;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4\n\t"
+      "ds_read_b64_tr_b16 %1, %5\n\t"
+      "ds_read_b64_tr_b16 %2, %6\n\t"
+      "ds_read_b64_tr_b16 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
+  f[0] = tr_pair(r0, r1);
+  f[1] = tr_pair(r2, r3);
+}
+// N = 4 fragments from 8 addresses
+__device__ __forceinline__ void tr_read4(const uint32_t (&a)[8], Frag<bf16> (&f)[4]) {
+  u32x2 r0, r1, r2, r3, r4, r5, r6, r7;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+  f[0] = tr_pair(r0, r1);
+  f[1] = tr_pair(r2, r3);
+  f[2] = tr_pair(r4, r5);
+  f[3] = tr_pair(r6, r7);
+}
+// both K steps (ks = 0, 1) of the transposed fragment of columns c0 .. c0 + 15
+template <int NC>
+__device__ __forceinline__ void col_tr2(const bf16* t, int c0, Frag<bf16> (&f)[2]) {
+  uint32_t a[4];
+  Tile<NC>::col_tr_addr(t, 0, c0, a[0], a[1]);
+  Tile<NC>::col_tr_addr(t, 1, c0, a[2], a[3]);
+  tr_read2(a, f);
+}
 
 // ---------------------------------------------------------------------------
 // problem geometry shared by the kernels
@@ -634,10 +690,12 @@ __device__ __forceinline__ void w_frags(const unsigned char* smem, const ChunkTi
   for (int n = 0; n < WFrags<K, NW>::ND; ++n) {
     const int dt = wid + NW * n;
     if (dt >= K / 16) break;
+    Frag<bf16> kt[2];
+    col_tr2<K>(T.k, 16 * dt, kt);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       float x[8];
-      frag_unpack(Tile<K>::col_tr(T.k, ks, 16 * dt), x);
+      frag_unpack(kt[ks], x);
       const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_g + 2 * C + 32 * ks + 4 * lg);
       const f32x4 b1 = *reinterpret_cast<const f32x4*>(s_g + 2 * C + 32 * ks + 16 + 4 * lg);
       const f32x4 e0 = *reinterpret_cast<const f32x4*>(s_g + C + 32 * ks + 4 * lg);
@@ -680,10 +738,12 @@ __device__ __forceinline__ void u_frags(const unsigned char* smem, const ChunkTi
   using L = SegLds<TQ, K, V, WITH_Q>;
   const float* s_b = reinterpret_cast<const float*>(smem + L::off_g) + 2 * C;
   const int lg = lane_id() >> 4;
+  Frag<bf16> vt[2];
+  col_tr2<V>(T.v, v0, vt);
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     float x[8];
-    frag_unpack(Tile<V>::col_tr(T.v, ks, v0), x);
+    frag_unpack(vt[ks], x);
     const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_b + 32 * ks + 4 * lg);
     const f32x4 b1 = *reinterpret_cast<const f32x4*>(s_b + 32 * ks + 16 + 4 * lg);
 #pragma unroll
@@ -711,14 +771,23 @@ template <int K, int CT>
 __device__ __forceinline__ void state_update(f32x4 (&S)[K / 16][CT], const Frag<bf16> (&vg)[2][CT],
                                              const ChunkTiles& T, float gamma) {
 #pragma unroll
-  for (int tt = 0; tt < K / 16; ++tt) {
-    const Frag<bf16> a0 = Tile<K>::col_tr(T.k, 0, 16 * tt);
-    const Frag<bf16> a1 = Tile<K>::col_tr(T.k, 1, 16 * tt);
+  for (int tp = 0; tp < K / 16; tp += 2) {      // two row tiles per read batch
+    uint32_t ad[8];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      S[tt][ct] *= gamma;
-      mma(S[tt][ct], a0, vg[0][ct]);
-      mma(S[tt][ct], a1, vg[1][ct]);
+    for (int e = 0; e < 2; ++e) {
+      Tile<K>::col_tr_addr(T.k, 0, 16 * (tp + e), ad[4 * e], ad[4 * e + 1]);
+      Tile<K>::col_tr_addr(T.k, 1, 16 * (tp + e), ad[4 * e + 2], ad[4 * e + 3]);
+    }
+    Frag<bf16> a[4];
+    tr_read4(ad, a);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        S[tp + e][ct] *= gamma;
+        mma(S[tp + e][ct], a[2 * e], vg[0][ct]);
+        mma(S[tp + e][ct], a[2 * e + 1], vg[1][ct]);
+      }
     }
   }
 }
@@ -1072,6 +1141,12 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
 // seg_combine: S_{j+1} = M_j S_j + R_j over the segments of a sequence, 16 V
 // columns per workgroup, fp32 (v_mfma_f32_16x16x4f32).  Also writes
 // final_state of sequences without tokens.
+//
+// The chain is serial, so each step must cost only its arithmetic: wave w owns
+// output rows 16w .. 16w + 15 and holds its rows of M_j (A operand) and its
+// tile of R_j in registers, loaded one step ahead, while the state columns
+// (B operand, shared by all waves) sit transposed in LDS so that the four K
+// values a lane needs per 16-deep step are one 16-byte read.
 // ---------------------------------------------------------------------------
 struct SegCombineArgs {
   const float* M;
@@ -1084,10 +1159,30 @@ struct SegCombineArgs {
 };
 
 template <int K>
-__global__ __launch_bounds__(NT_COMB) void seg_combine_kernel(SegCombineArgs a, SegGeom G, int total) {
-  constexpr int RT = K / 16 / NW_COMB >= 1 ? K / 16 / NW_COMB : 1;   // row tiles per wave
-  constexpr int NWA = K / 16 / RT;                          // active waves
-  __shared__ __align__(16) float s_S[K][16];
+struct CombineMaps {
+  f32x4 m[K / 16];            // M_j[r0 + lane%16][16 kk + 4 (lane/16) .. +3]
+  f32x4 r;                    // R_j[r0 + 4 (lane/16) + jj][v0 + lane%16]
+};
+
+template <int K>
+__device__ __forceinline__ void load_maps(CombineMaps<K>& c, const float* M, const float* R, int V, int r0, int v0) {
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const float* pm = M + (int64_t)(r0 + lc) * K + 4 * lg;
+#pragma unroll
+  for (int kk = 0; kk < K / 16; ++kk) c.m[kk] = *reinterpret_cast<const f32x4*>(pm + 16 * kk);
+  const float* pr = R + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) c.r[jj] = pr[(int64_t)jj * V];
+}
+
+template <int K> struct CombCfg { static constexpr int NT = K / 16 * WAVE; };   // one 16-row tile per wave
+
+template <int K>
+__global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineArgs a, SegGeom G, int total) {
+  constexpr int NT = CombCfg<K>::NT;
+  constexpr int LDS_T = K + 4;                              // row stride of the transposed state
+  __shared__ __align__(16) float s_St[16][LDS_T];           // s_St[c][r] = S[r][v0 + c]
   const int V = a.V;
   const int nvt = V / 16;
   // XCD-aware order: the V slices of one head run on one XCD and share M through its L2
@@ -1101,6 +1196,7 @@ __global__ __launch_bounds__(NT_COMB) void seg_combine_kernel(SegCombineArgs a, 
   const int wid = threadIdx.x / WAVE;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
+  const int r0 = 16 * wid;
 
   int nseg, s_first;
   if (G.cu == nullptr) {
@@ -1110,7 +1206,22 @@ __global__ __launch_bounds__(NT_COMB) void seg_combine_kernel(SegCombineArgs a, 
     nseg = G.seg_off[n + 1] - G.seg_off[n];
     s_first = G.seg_off[n];
   }
-  for (int idx = threadIdx.x; idx < K * 16; idx += NT_COMB) {
+  // Maps of steps j, j + 1, j + 2 in flight (stage j % 3).  Every stage is
+  // loaded unconditionally (past the last step: the last step's maps again) so
+  // that the number of loads issued after each stage is fixed and the wait for
+  // a stage counts only the loads before it.
+  constexpr int NST = 3;
+  const int nsteps = nseg - 1;
+  CombineMaps<K> st[NST];
+  auto issue = [&](CombineMaps<K>& c, int j) {
+    const int64_t s = s_first + max(0, min(j, nsteps - 1));
+    load_maps<K>(c, a.M + (s * H + h) * K * K, a.R + (s * H + h) * K * V, V, r0, v0);
+  };
+  if (nsteps > 0) {
+#pragma unroll
+    for (int u = 0; u < NST; ++u) issue(st[u], u);
+  }
+  for (int idx = threadIdx.x; idx < K * 16; idx += NT) {
     const int r = idx / 16, c = idx % 16;
     float x = 0.f;
     if (a.h0) {
@@ -1118,54 +1229,40 @@ __global__ __launch_bounds__(NT_COMB) void seg_combine_kernel(SegCombineArgs a, 
       x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
                                : (float)reinterpret_cast<const bf16*>(a.h0)[off];
     }
-    s_S[r][c] = x;
+    s_St[c][r] = x;
   }
   if (nseg == 0) {
     if (a.ht) {
       __syncthreads();
-      for (int idx = threadIdx.x; idx < K * 16; idx += NT_COMB) {
+      for (int idx = threadIdx.x; idx < K * 16; idx += NT) {
         const int r = idx / 16, c = idx % 16;
-        a.ht[(((int64_t)n * H + h) * K + r) * V + v0 + c] = s_S[r][c];
+        a.ht[(((int64_t)n * H + h) * K + r) * V + v0 + c] = s_St[c][r];
       }
     }
     return;
   }
   __syncthreads();
-  for (int j = 0; j + 1 < nseg; ++j) {
-    const int64_t s = s_first + j;
-    const float* Ms = a.M + (s * H + h) * K * K;
-    const float* Rs = a.R + (s * H + h) * K * V;
-    f32x4 acc[RT];
-    if (wid < NWA) {
+  for (int j0 = 0; j0 < nsteps; j0 += NST) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int r0 = 16 * (wid * RT + rt);
+    for (int u = 0; u < NST; ++u) {
+      const int j = j0 + u;
+      if (j >= nsteps) break;                               // uniform
+      f32x4 acc = st[u].r;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) acc[rt][jj] = Rs[(int64_t)(r0 + 4 * lg + jj) * V + v0 + lc];
-#pragma unroll 4
-        for (int kk = 0; kk < K / 16; ++kk) {
-          const f32x4 m = *reinterpret_cast<const f32x4*>(Ms + (int64_t)(r0 + lc) * K + 16 * kk + 4 * lg);
+      for (int kk = 0; kk < K / 16; ++kk) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>(&s_St[lc][16 * kk + 4 * lg]);
 #pragma unroll
-          for (int qq = 0; qq < 4; ++qq)
-            acc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(m[qq], s_S[16 * kk + 4 * lg + qq][lc], acc[rt], 0, 0, 0);
-        }
+        for (int qq = 0; qq < 4; ++qq)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(st[u].m[kk][qq], b[qq], acc, 0, 0, 0);
       }
-    }
-    __syncthreads();
-    if (wid < NWA) {
-      float* out = a.s_init + ((s + 1) * H + h) * K * V;
+      issue(st[u], j + NST);                                // this stage's registers are free again
+      __syncthreads();
+      *reinterpret_cast<f32x4*>(&s_St[lc][r0 + 4 * lg]) = acc;
+      float* out = a.s_init + ((s_first + j + 1) * (int64_t)H + h) * K * V + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const int r0 = 16 * (wid * RT + rt);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int r = r0 + 4 * lg + jj;
-          s_S[r][lc] = acc[rt][jj];
-          out[(int64_t)r * V + v0 + lc] = acc[rt][jj];
-        }
-      }
+      for (int jj = 0; jj < 4; ++jj) out[(int64_t)jj * V] = acc[jj];
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
@@ -1225,7 +1322,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     const int total = p.N * p.H * (V / 16);
     const int cgrid = (total + 7) / 8 * 8;
     SegCombineArgs ca{p.M, p.R, p.h0, p.h0_dtype, p.s_init, p.ht, V};
-    hipLaunchKernelGGL(seg_combine_kernel<K>, dim3(cgrid), dim3(NT_COMB), 0, s, ca, G, total);
+    hipLaunchKernelGGL(seg_combine_kernel<K>, dim3(cgrid), dim3(CombCfg<K>::NT), 0, s, ca, G, total);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(3)) return -1;
