@@ -25,10 +25,6 @@
 //                       state and emits o (chunk_o.py:84-128) and, for the last
 //                       segment, final_state.
 //
-// Workgroup: seg_out runs one wave per 16 V columns, seg_trans one wave per 32
-// columns of [M | R]; each wave keeps its fp32 state tile (K rows) in VGPRs in
-// the MFMA accumulator layout for the whole segment.
-//
 // Chunk inputs.  q, k, v and Ai of a chunk live in LDS as row-major tiles (row
 // = token) whose 16-byte chunks are XOR-swizzled by row.  They arrive by direct
 // global->LDS loads (global_load_lds_dwordx4) into one of two buffers while the
@@ -39,10 +35,11 @@
 //   * q as the partner of the state (o = q h): two 8-byte pieces per lane, in
 //     the K order in which an accumulator tile pair becomes an operand
 //     ({4*lg..+3} and {16+4*lg..+3} of a 32-wide step, lg = lane/16);
-//   * k^T, (k beta e^g)^T and (v beta)^T, whose contraction index is the token:
-//     ds_read_b64_tr_b16 transposes a 4-token x 16-column block across the 16
-//     lanes of a lane group (lane j receives column j of the 4 rows).
+//   * k^T and v^T, whose contraction index is the token: ds_read_b64_tr_b16
+//     transposes a 4-token x 16-column block across the 16 lanes of a lane
+//     group (lane j receives column j of the 4 rows).
 // fp8 q/k are converted once per chunk into bf16 tiles of the same layout.
+// The chunk step itself is described at the chunk engine below.
 #include <type_traits>
 
 #include "gdn_common.hpp"
@@ -51,9 +48,6 @@
 namespace kgdn {
 
 namespace {
-
-template <int K, int V> struct OutCfg { static constexpr int NW = V / 16, NT = 64 * NW; };
-template <int K, int V> struct TransCfg { static constexpr int NW = (K + V) / 32, NT = 64 * NW; };
 
 // Workgroup barrier that orders LDS only: this wave's LDS reads and writes are
 // complete (lgkmcnt(0)), then s_barrier.  __syncthreads(), and even a
@@ -125,10 +119,15 @@ __device__ __forceinline__ Frag<bf16> acc_frag(const f32x4& a, const f32x4& b) {
 
 // ---------------------------------------------------------------------------
 // swizzled row-major bf16 tiles [64 rows][NC columns]: 16-byte chunk c of row r
-// sits at chunk position c ^ swz(r).  Rows of 256 bytes (NC = 128) take
-// swz(r) = r mod 16; rows of 128 bytes (NC = 64, two rows per 256-byte bank
-// row) take a permutation of r/2 that keeps 16 consecutive rows on distinct
-// banks for 16-byte row reads.
+// sits at chunk position c ^ swz(r).  LDS serves 256 bytes per clock (64 banks
+// of 4 bytes); a read is conflict-free when the lanes served together touch
+// distinct banks.  Rows of 256 bytes (NC = 128) take swz(r) = 2 (r mod 8) +
+// (r / 8 mod 2): 16 consecutive rows get 16 distinct chunk positions (16-byte
+// row reads), and the 8 rows x 2 chunks of a transposed read
+// (ds_read_b64_tr_b16, 32 lanes of 8 bytes) get 16 distinct positions too,
+// where swz(r) = r mod 16 leaves them two-way conflicted.  Rows of 128 bytes
+// (NC = 64, two rows per 256-byte bank row) take a permutation of r/2 with the
+// same two properties.
 // ---------------------------------------------------------------------------
 template <int NC>
 struct Tile {
@@ -136,7 +135,7 @@ struct Tile {
   static constexpr int CPR = NC / 8;                  // 16-byte chunks per row
   __device__ static __forceinline__ int swz(int r) {
     if constexpr (NC == 64) return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
-    else return r & (CPR - 1);
+    else return ((r & 7) << 1) | ((r >> 3) & 1);
   }
   // element offset of chunk c8 (columns 8*c8 .. +7) of row r
   __device__ static __forceinline__ int off(int r, int c8) { return r * NC + ((c8 ^ swz(r)) << 3); }
@@ -177,49 +176,6 @@ __device__ __forceinline__ Frag<bf16> tr_pair(u32x2 a, u32x2 b) {
   f.v = __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
   return f;
 }
-// N = 2 fragments from 4 addresses (fragment f from reads 2f, 2f + 1)
-__device__ __forceinline__ void tr_read2(const uint32_t (&a)[4], Frag<bf16> (&f)[2]) {
-  u32x2 r0, r1, r2, r3;
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %4\n\t"
-      "ds_read_b64_tr_b16 %1, %5\n\t"
-      "ds_read_b64_tr_b16 %2, %6\n\t"
-      "ds_read_b64_tr_b16 %3, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]));
-  f[0] = tr_pair(r0, r1);
-  f[1] = tr_pair(r2, r3);
-}
-// N = 4 fragments from 8 addresses
-__device__ __forceinline__ void tr_read4(const uint32_t (&a)[8], Frag<bf16> (&f)[4]) {
-  u32x2 r0, r1, r2, r3, r4, r5, r6, r7;
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %9\n\t"
-      "ds_read_b64_tr_b16 %2, %10\n\t"
-      "ds_read_b64_tr_b16 %3, %11\n\t"
-      "ds_read_b64_tr_b16 %4, %12\n\t"
-      "ds_read_b64_tr_b16 %5, %13\n\t"
-      "ds_read_b64_tr_b16 %6, %14\n\t"
-      "ds_read_b64_tr_b16 %7, %15\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
-  f[0] = tr_pair(r0, r1);
-  f[1] = tr_pair(r2, r3);
-  f[2] = tr_pair(r4, r5);
-  f[3] = tr_pair(r6, r7);
-}
-// both K steps (ks = 0, 1) of the transposed fragment of columns c0 .. c0 + 15
-template <int NC>
-__device__ __forceinline__ void col_tr2(const bf16* t, int c0, Frag<bf16> (&f)[2]) {
-  uint32_t a[4];
-  Tile<NC>::col_tr_addr(t, 0, c0, a[0], a[1]);
-  Tile<NC>::col_tr_addr(t, 1, c0, a[2], a[3]);
-  tr_read2(a, f);
-}
-
 // ---------------------------------------------------------------------------
 // problem geometry shared by the kernels
 // ---------------------------------------------------------------------------
@@ -278,28 +234,6 @@ __device__ __forceinline__ SegLoc locate_seg(int s, const SegGeom& G) {
 // ---------------------------------------------------------------------------
 // LDS layouts
 // ---------------------------------------------------------------------------
-// seg_trans / seg_out
-template <typename TQ, int K, int V, bool WITH_Q>
-struct SegLds {
-  static constexpr bool FP8 = sizeof(TQ) == 1;
-  static constexpr int LDK = K + 8;        // row stride of s_w [64][K] (pcol order)
-  static constexpr int LDT = C + 8;        // row stride of s_Aqk [64][64] (pcol order)
-  static constexpr size_t a16(size_t x) { return (x + 15) / 16 * 16; }
-  // one input buffer: q (if WITH_Q), k as loaded (TQ), v (bf16), Ai (bf16)
-  static constexpr size_t qk_in = (size_t)C * K * sizeof(TQ);
-  static constexpr size_t buf_q = 0;
-  static constexpr size_t buf_k = WITH_Q ? qk_in : 0;
-  static constexpr size_t buf_v = buf_k + qk_in;
-  static constexpr size_t buf_ai = buf_v + (size_t)C * V * 2;
-  static constexpr size_t buf_bytes = a16(buf_ai + (size_t)C * C * 2);
-  static constexpr size_t off_buf = 0;                                   // two input buffers
-  static constexpr size_t off_cq = off_buf + 2 * buf_bytes;              // fp8: bf16 q / k tiles
-  static constexpr size_t off_ck = off_cq + (FP8 && WITH_Q ? (size_t)C * K * 2 : 0);
-  static constexpr size_t off_w = off_ck + (FP8 ? (size_t)C * K * 2 : 0);
-  static constexpr size_t off_Aqk = a16(off_w + 2 * (size_t)C * LDK);
-  static constexpr size_t off_g = a16(off_Aqk + (WITH_Q ? 2 * (size_t)C * LDT : 0));
-  static constexpr size_t total = off_g + sizeof(float) * 4 * C;         // gc, exp(gc), beta, gate
-};
 
 // seg_prep
 template <typename TQ, int K>
@@ -316,27 +250,45 @@ struct PrepLds {
   static constexpr size_t total = off_g + sizeof(float) * 2 * C;               // gc, beta
 };
 
-// Pointers of the tiles the current chunk computes from.
-struct ChunkTiles {
-  const bf16* q;
-  const bf16* k;
-  const bf16* v;
-  const bf16* ai;
-};
 
 // ---------------------------------------------------------------------------
 // chunk input: direct global -> LDS loads
 // ---------------------------------------------------------------------------
+// Direct global->LDS loads, issued through inline asm: lane l's 16 (4) bytes
+// at base + off land at LDS address lds_dst + 16 l (4 l); base is wave-uniform
+// (SGPRs), off a 32-bit lane offset.  The compiler's wait tracking treats every
+// LDS read that follows a direct load (the builtin) as a possible reader of it
+// and waits for vmcnt first -- for the next chunk's prefetch, in the middle of
+// the current chunk.  Hidden in asm, the loads are waited for explicitly
+// (wait_loads) before the barrier that publishes their data.  M0 carries the
+// LDS address.  The hazard rules are the asm's own: a VALU write of an SGPR
+// (v_readfirstlane of the base) needs 5 wait states before a VMEM instruction
+// reads that SGPR, and an SALU write of M0 one before the load reads it, hence
+// s_nop 4 ahead of each load.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_dst) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(uniform_ptr(base)), "{m0}"(lds_dst)
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds_dst) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(uniform_ptr(base)), "{m0}"(lds_dst)
+               : "memory");
+}
+
 // 8 input elements per lane: bf16 -> one dwordx4 direct load; fp8 -> two dword loads.
-// (the builtin takes the size as a literal)
 template <typename T>
-__device__ __forceinline__ void direct8(const T* src, unsigned char* wave_blk) {
+__device__ __forceinline__ void direct8(const void* base, uint32_t off, unsigned char* wave_blk) {
+  const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(wave_blk));
   if constexpr (sizeof(T) == 2) {
-    __builtin_amdgcn_global_load_lds((gmem_void*)src, (lmem_void*)wave_blk, 16, 0, 0);
+    dma16(base, off, d);
   } else {
-    const unsigned char* p = reinterpret_cast<const unsigned char*>(src);
-    __builtin_amdgcn_global_load_lds((gmem_void*)p, (lmem_void*)wave_blk, 4, 0, 0);
-    __builtin_amdgcn_global_load_lds((gmem_void*)(p + 4), (lmem_void*)(wave_blk + WAVE * 4), 4, 0, 0);
+    dma4(base, off, d);
+    dma4(base, off + 4, d + WAVE * 4);
   }
 }
 
@@ -362,7 +314,7 @@ __device__ __forceinline__ void load_tile(const T* base_t, uint32_t row_bytes, i
     const int c8 = sizeof(T) == 2 ? (pos ^ Tile<NC>::swz(r)) : pos;
     const uint32_t rs = r < nv ? r : 0;
     unsigned char* blk = dst + (NT * i + WAVE * wid) * 8 * sizeof(T);
-    direct8<T>(reinterpret_cast<const T*>(base + (rs * row_bytes + (uint32_t)(8 * c8 * sizeof(T)))), blk);
+    direct8<T>(base, rs * row_bytes + (uint32_t)(8 * c8 * sizeof(T)), blk);
   }
 }
 
@@ -387,21 +339,6 @@ __device__ __forceinline__ void load_gates(GateRaw& gr, const void* gp, const vo
     gr.g = ld_raw(gp, (t0 + tid) * H + h, g_dt);
     gr.b = ld_raw(bp, (t0 + tid) * H + h, b_dt);
   }
-}
-
-// q (if WITH_Q), k, v of tokens t0.. and the chunk's Ai tile (ai: its first row)
-template <typename TQ, int K, int V, bool WITH_Q, int NT>
-__device__ __forceinline__ void load_chunk(unsigned char* buf, GateRaw& gr, const void* qp, const void* kp,
-                                           const void* vp, const void* gp, const void* bp, int g_dt, int b_dt,
-                                           int64_t t0, int nv, int h, int H, const bf16* ai) {
-  using L = SegLds<TQ, K, V, WITH_Q>;
-  load_gates(gr, gp, bp, g_dt, b_dt, t0, nv, h, H);
-  const int64_t e0 = t0 * H + h;
-  if constexpr (WITH_Q)
-    load_tile<TQ, K, NT>(reinterpret_cast<const TQ*>(qp) + e0 * K, (uint32_t)(H * K * sizeof(TQ)), nv, buf + L::buf_q);
-  load_tile<TQ, K, NT>(reinterpret_cast<const TQ*>(kp) + e0 * K, (uint32_t)(H * K * sizeof(TQ)), nv, buf + L::buf_k);
-  load_tile<bf16, V, NT>(reinterpret_cast<const bf16*>(vp) + e0 * V, (uint32_t)(H * V * 2), nv, buf + L::buf_v);
-  load_tile<bf16, C, NT>(ai, (uint32_t)(C * 2), C, buf + L::buf_ai);
 }
 
 // fp8 tile (plain order, two dwords per unit) -> dequantised bf16 swizzled tile
@@ -443,66 +380,27 @@ __device__ __forceinline__ void wait_loads() {
 // the raw g bits of token tid; returns gc of token tid and sets gl = gc of the
 // last valid token.
 __device__ __forceinline__ float chunk_cumsum(const GateRaw& gr, int g_dt, int nv, float& gl) {
-  const int tid = threadIdx.x;
+  const int l = lane_id();
   float gv = raw_to_f32(gr.g, g_dt);
 #pragma unroll
   for (int off = 1; off < WAVE; off <<= 1) {
     const float o = __shfl_up(gv, off, WAVE);
-    if (tid >= off) gv += o;
+    if (l >= off) gv += o;
   }
   gl = __shfl(gv, nv - 1, WAVE);
   return gv;
 }
 
-// Top of a chunk: its loads have landed, fp8 inputs are converted (each lane
-// converts the units it loaded itself), and wave 0 forms the chunk vectors: gc,
-// exp(gc), beta and the update gate exp(gc_last - gc) (chunk_delta_h.py:163-169).
-// Rows nv..63 of a partial chunk hold a copy of row 0 and need no clearing:
-// beta and the gate are 0 there, so their rows of A, w and u are zero, they
-// add nothing to the state, and their rows of o are not stored.
-template <typename TQ, int K, int V, bool WITH_Q, int NT>
-__device__ __forceinline__ ChunkTiles stage_chunk(unsigned char* smem, unsigned char* buf, const GateRaw& gr, float qs,
-                                                  float ks, int nv, int g_dt, int b_dt) {
-  using L = SegLds<TQ, K, V, WITH_Q>;
-  wait_loads();
-  ChunkTiles T;
-  if constexpr (L::FP8) {
-    T.q = reinterpret_cast<const bf16*>(smem + L::off_cq);
-    T.k = reinterpret_cast<const bf16*>(smem + L::off_ck);
-    if constexpr (WITH_Q) convert_fp8<K, NT>(buf + L::buf_q, reinterpret_cast<bf16*>(smem + L::off_cq), qs, nv);
-    convert_fp8<K, NT>(buf + L::buf_k, reinterpret_cast<bf16*>(smem + L::off_ck), ks, nv);
-  } else {
-    T.q = reinterpret_cast<const bf16*>(buf + L::buf_q);
-    T.k = reinterpret_cast<const bf16*>(buf + L::buf_k);
-  }
-  T.v = reinterpret_cast<const bf16*>(buf + L::buf_v);
-  T.ai = reinterpret_cast<const bf16*>(buf + L::buf_ai);
-  const int tid = threadIdx.x;
-  if (tid < WAVE) {
-    float* s_g = reinterpret_cast<float*>(smem + L::off_g);
-    float gl;
-    const float gv = chunk_cumsum(gr, g_dt, nv, gl);
-    s_g[tid] = gv;                                         // gc
-    s_g[C + tid] = gexp(gv);                               // exp(gc)
-    s_g[2 * C + tid] = raw_to_f32(gr.b, b_dt);             // beta
-    s_g[3 * C + tid] = tid < nv ? gexp(gl - gv) : 0.f;     // gate
-  }
-  return T;
-}
-
 // Tile (tm, tn), tn <= tm, of the 64 x 64 chunk products (16 x 16 tiles t = 0..9
-// in row order: tm = 0, 1, 1, 2, 2, 2, 3, ...):
-//   IS_Q false: A = beta_i exp(gc_i - gc_j) k_i.k_j for i > j, fp32 into out[i][j]
-//               (chunk_scaled_dot_kkt.py:57-73);
-//   IS_Q true:  Aqk = exp(gc_i - gc_j) q_i.k_j for i >= j, bf16 into out[i][pcol(j)]
-//               (chunk_o.py:109-118).
+// in row order: tm = 0, 1, 1, 2, 2, 2, 3, ...).
 __device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
   tm = (t >= 1) + (t >= 3) + (t >= 6);
   tn = t - tm * (tm + 1) / 2;
 }
-template <int K, bool IS_Q, int LDO>
-__device__ __forceinline__ void kkt_tile(const bf16* asrc, const bf16* k, const float* s_gc, const float* s_beta,
-                                         void* out, int t) {
+// seg_prep: A = beta_i exp(gc_i - gc_j) k_i.k_j for i > j, fp32 into out[i][j]
+// (chunk_scaled_dot_kkt.py:57-73), tile t.
+template <int K, int LDO>
+__device__ __forceinline__ void kkt_tile(const bf16* k, const float* s_gc, const float* s_beta, float* out, int t) {
   using TK = Tile<K>;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
@@ -511,20 +409,16 @@ __device__ __forceinline__ void kkt_tile(const bf16* asrc, const bf16* k, const 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < K / 32; ++ks)
-    mma(acc, TK::row8(asrc, 16 * tm + lc, 4 * ks + lg), TK::row8(k, 16 * tn + lc, 4 * ks + lg));
+    mma(acc, TK::row8(k, 16 * tm + lc, 4 * ks + lg), TK::row8(k, 16 * tn + lc, 4 * ks + lg));
   const int i0 = 16 * tm + 4 * lg;
   const int j = 16 * tn + lc;
   const f32x4 gi = *reinterpret_cast<const f32x4*>(s_gc + i0);
-  f32x4 bi = {1.f, 1.f, 1.f, 1.f};
-  if constexpr (!IS_Q) bi = *reinterpret_cast<const f32x4*>(s_beta + i0);
+  const f32x4 bi = *reinterpret_cast<const f32x4*>(s_beta + i0);
   const float gj = s_gc[j];
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
     const int i = i0 + jj;
-    const bool keep = IS_Q ? i >= j : i > j;
-    const float val = keep ? acc[jj] * gexp(gi[jj] - gj) * bi[jj] : 0.f;
-    if constexpr (IS_Q) reinterpret_cast<bf16*>(out)[i * LDO + pcol(j)] = (bf16)val;
-    else reinterpret_cast<float*>(out)[i * LDO + j] = val;
+    out[i * LDO + j] = i > j ? acc[jj] * gexp(gi[jj] - gj) * bi[jj] : 0.f;
   }
 }
 
@@ -656,7 +550,7 @@ __global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeo
     s_g[C + tid] = raw_to_f32(gr.b, a.beta_dtype);
   }
   lds_barrier();
-  for (int t = wid; t < 10; t += NW) kkt_tile<K, false, P::LDA>(kt, kt, s_g, s_g + C, s_A, t);
+  for (int t = wid; t < 10; t += NW) kkt_tile<K, P::LDA>(kt, s_g, s_g + C, s_A, t);
   lds_barrier();
   if (wid == 0) diag_solve<P::LDA, P::LDT>(s_A, s_Ai);
   lds_barrier();
@@ -670,149 +564,359 @@ __global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeo
 }
 
 // ---------------------------------------------------------------------------
-// w, u and the recurrence
+// seg_trans / seg_out: the chunk engine
 // ---------------------------------------------------------------------------
-// kb^T fragments (kb = k beta exp(gc) with the reference's roundings,
-// wy_fast.py:67-81) of the d tiles dt = wid + NW * n.
-template <int K, int NW>
-struct WFrags {
-  static constexpr int ND = (K / 16 + NW - 1) / NW;
-  Frag<bf16> kb[ND][2];
+// Workgroup: seg_out runs one wave per 16 V columns, seg_trans one wave per two
+// 16-column tiles of [M | R] (tiles wid and wid + NW).  Each wave keeps its fp32
+// state tiles (K rows) in VGPRs in the MFMA accumulator layout.
+//
+// Per chunk (two workgroup barriers):
+//   top      this wave's direct loads of the chunk have landed; the wave forms
+//            the chunk vectors itself, in its own LDS slot, so no wave waits
+//            for another: gc, exp(gc) scale, beta exp(gc), the update gate
+//            exp(gc_last - gc), beta.  (fp8: q/k dequantised after a barrier.)
+//   barrier 1; the next chunk's loads go into the other buffer (every wave is
+//            done with the chunk that used it).
+//   phase A  [own]    h = bf16(S) as operand fragments; o_inter = q h (seg_out);
+//                     u = Ai bf16(v beta) for the wave's V columns;
+//            [shared] Aqk'^T tiles (seg_out) and w tiles into LDS.  w is formed
+//                     as (Ai diag(beta exp(gc))) k and stored negated, so that
+//                     v' = u - w h is one MFMA accumulation onto u.
+//   barrier 2
+//   phase B  v' = u + (-w) h; o = o_inter exp(gc) scale + Aqk' bf16(v');
+//            S = exp(gc_last) S + k^T bf16(v' gate).
+// LDS lane offsets are computed once per segment and tile bases are
+// compile-time constants (the chunk loop is unrolled over the two buffers), so
+// a fragment read is a fixed VGPR plus an immediate offset.
+template <typename TQ, int K, int V, bool OUT>
+struct Eng {
+  static constexpr bool FP8 = sizeof(TQ) == 1;
+  static constexpr int NW = OUT ? V / 16 : (K + V) / 32;
+  static constexpr int NT = NW * WAVE;
+  static constexpr int CT = OUT ? 1 : 2;                  // 16-column state tiles per wave
+  static constexpr int KT = K / 16;
+  static constexpr int NDG = K / 64;                      // w units per token tile (4 d tiles each)
+  static constexpr int LDW = K + 8;                       // s_w row stride (elements), pcol order
+  static constexpr int LDQ = C + 8;                       // s_Aqk row stride
+  static constexpr uint32_t KB = C * K * 2, VB = C * V * 2, AB = C * C * 2, RAW = C * K;
+  // Tiles read transposed (k, v) lie in the first 64 KB, so that one lane VGPR
+  // plus a 16-bit immediate reaches them: bf16 k of both buffers (or the one
+  // dequantised fp8 k tile), then v of both buffers.
+  static constexpr uint32_t k_tile(int p) { return FP8 ? 0u : (uint32_t)p * KB; }
+  static constexpr uint32_t v_tile(int p) { return (FP8 ? KB : 2 * KB) + (uint32_t)p * VB; }
+  static constexpr uint32_t tr_end = (FP8 ? KB : 2 * KB) + 2 * VB;
+  static constexpr uint32_t q_tile(int p) { return FP8 ? tr_end : tr_end + (uint32_t)p * KB; }
+  static constexpr uint32_t q_end = OUT ? (FP8 ? tr_end + KB : tr_end + 2 * KB) : tr_end;
+  static constexpr uint32_t kraw(int p) { return q_end + (uint32_t)p * RAW; }        // fp8 inputs as loaded
+  static constexpr uint32_t qraw(int p) { return q_end + 2 * RAW + (uint32_t)p * RAW; }
+  static constexpr uint32_t raw_end = FP8 ? q_end + (OUT ? 4 : 2) * RAW : q_end;
+  static constexpr uint32_t ai_tile(int p) { return raw_end + (uint32_t)p * AB; }
+  static constexpr uint32_t off_w = raw_end + 2 * AB;
+  static constexpr uint32_t off_aqk = off_w + C * LDW * 2;
+  static constexpr uint32_t off_vec = off_aqk + (OUT ? C * LDQ * 2 : 0);
+  static constexpr int NVEC = 5;
+  static constexpr uint32_t total = off_vec + NW * NVEC * C * 4;
+  static_assert(tr_end + 0 <= 65536, "transposed tiles must lie in the first 64 KB of LDS");
+  static_assert(total <= 160 * 1024, "chunk tiles do not fit in LDS");
 };
-template <typename TQ, int K, int V, bool WITH_Q, int NW>
-__device__ __forceinline__ void w_frags(const unsigned char* smem, const ChunkTiles& T, bool beta_lowp,
-                                        WFrags<K, NW>& F) {
-  using L = SegLds<TQ, K, V, WITH_Q>;
-  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
-  const int wid = threadIdx.x / WAVE;
-  const int lg = lane_id() >> 4;
-#pragma unroll
-  for (int n = 0; n < WFrags<K, NW>::ND; ++n) {
-    const int dt = wid + NW * n;
-    if (dt >= K / 16) break;
-    Frag<bf16> kt[2];
-    col_tr2<K>(T.k, 16 * dt, kt);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float x[8];
-      frag_unpack(kt[ks], x);
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_g + 2 * C + 32 * ks + 4 * lg);
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(s_g + 2 * C + 32 * ks + 16 + 4 * lg);
-      const f32x4 e0 = *reinterpret_cast<const f32x4*>(s_g + C + 32 * ks + 4 * lg);
-      const f32x4 e1 = *reinterpret_cast<const f32x4*>(s_g + C + 32 * ks + 16 + 4 * lg);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float v = x[e] * (e < 4 ? b0[e] : b1[e - 4]);
-        if (beta_lowp) v = round_to<bf16>(v);
-        x[e] = v * (e < 4 ? e0[e] : e1[e - 4]);
-      }
-      F.kb[n][ks] = frag_pack(x);
-    }
-  }
+
+// Per-lane LDS byte offsets, fixed for the whole segment (lane l: lc = l % 16, lg = l / 16).
+template <int K>
+struct LaneOffs {
+  uint32_t krow[K / 32];        // Tile<K> row lc, chunk 4ks + lg (q, k rows; rows 16t + lc add 32 t K)
+  uint32_t qacc[K / 32][2];     // Tile<K> row lc, the two 8-byte pieces of the accumulator K order
+  uint32_t ktr[K / 16];         // absolute LDS address of the transposed read of column tile dt
+  uint32_t airow[2];            // Tile<64> row lc, chunk 4ks + lg
+  uint32_t w;                   // s_w: row lc, position 8 lg
+  uint32_t aqk;                 // s_Aqk: row lc, position 8 lg
+};
+
+// LDS address of the transposed read (see Tile::col_tr_addr, rows r0 of K step 0)
+// of column tile ct of a Tile<NC>
+template <int NC>
+__device__ __forceinline__ uint32_t tr_lane_addr(uint32_t lds0, int ct) {
+  const int l = lane_id();
+  const int lg = l >> 4, i = l & 15;
+  const int col = 16 * ct + 4 * (i & 3);
+  return lds0 + 2 * (Tile<NC>::off(4 * lg + (i >> 2), col >> 3) + (col & 7));
 }
-// w^T = kb^T Ai^T for this wave's d tiles -> s_w[t][pcol(d)]
-template <typename TQ, int K, int V, bool WITH_Q, int NW>
-__device__ __forceinline__ void w_products(unsigned char* smem, const ChunkTiles& T, const WFrags<K, NW>& F) {
-  using L = SegLds<TQ, K, V, WITH_Q>;
-  bf16* s_w = reinterpret_cast<bf16*>(smem + L::off_w);
-  const int wid = threadIdx.x / WAVE;
+
+template <int K, int LDW, int LDQ>
+__device__ __forceinline__ void lane_offsets(LaneOffs<K>& o, uint32_t lds0) {
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
 #pragma unroll
-  for (int n = 0; n < WFrags<K, NW>::ND; ++n) {
-    const int dt = wid + NW * n;
-    if (dt >= K / 16) break;
+  for (int ks = 0; ks < K / 32; ++ks) {
+    o.krow[ks] = 2 * Tile<K>::off(lc, 4 * ks + lg);
+    o.qacc[ks][0] = 2 * (Tile<K>::off(lc, 4 * ks + (lg >> 1)) + 4 * (lg & 1));
+    o.qacc[ks][1] = 2 * (Tile<K>::off(lc, 4 * ks + (lg >> 1) + 2) + 4 * (lg & 1));
+  }
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < K / 16; ++dt) o.ktr[dt] = tr_lane_addr<K>(lds0, dt);
 #pragma unroll
-      for (int ks = 0; ks <= tn / 2; ++ks) mma(acc, F.kb[n][ks], Tile<C>::row8(T.ai, 16 * tn + lc, 4 * ks + lg));
-      st4<bf16>(s_w + (16 * tn + lc) * L::LDK + pcol(16 * dt + 4 * lg), acc[0], acc[1], acc[2], acc[3]);
+  for (int ks = 0; ks < 2; ++ks) o.airow[ks] = 2 * Tile<C>::off(lc, 4 * ks + lg);
+  o.w = 2 * (lc * LDW + 8 * lg);
+  o.aqk = 2 * (lc * LDQ + 8 * lg);
+}
+
+// Transposed reads (ds_read_b64_tr_b16) through inline asm -- see tr_pair --
+// at one or two lane addresses plus immediate byte offsets, one wait for all.
+template <int O0, int O1>
+__device__ __forceinline__ Frag<bf16> tr2(uint32_t a) {
+  u32x2 r0, r1;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
+      "ds_read_b64_tr_b16 %1, %2 offset:%4\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1)
+      : "v"(a), "i"(O0), "i"(O1));
+  return tr_pair(r0, r1);
+}
+template <int O0, int O1, int O2, int O3>
+__device__ __forceinline__ void tr4(uint32_t a, Frag<bf16>& f0, Frag<bf16>& f1) {
+  u32x2 r0, r1, r2, r3;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4 offset:%5\n\t"
+      "ds_read_b64_tr_b16 %1, %4 offset:%6\n\t"
+      "ds_read_b64_tr_b16 %2, %4 offset:%7\n\t"
+      "ds_read_b64_tr_b16 %3, %4 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a), "i"(O0), "i"(O1), "i"(O2), "i"(O3));
+  f0 = tr_pair(r0, r1);
+  f1 = tr_pair(r2, r3);
+}
+template <int O0, int O1, int O2, int O3>
+__device__ __forceinline__ void tr4x2(uint32_t a, uint32_t b, Frag<bf16>& fa0, Frag<bf16>& fa1, Frag<bf16>& fb0,
+                                      Frag<bf16>& fb1) {
+  u32x2 r0, r1, r2, r3, r4, r5, r6, r7;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %4, %9 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %5, %9 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %6, %9 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %7, %9 offset:%13\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+      : "v"(a), "v"(b), "i"(O0), "i"(O1), "i"(O2), "i"(O3));
+  fa0 = tr_pair(r0, r1);
+  fa1 = tr_pair(r2, r3);
+  fb0 = tr_pair(r4, r5);
+  fb1 = tr_pair(r6, r7);
+}
+// K step 0 (tokens 0-31) or both K steps of a transposed fragment of the
+// [64][NC] tile at LDS byte offset TB: rows r0 and r0 + 16 of each step.
+template <int NC, uint32_t TB>
+__device__ __forceinline__ Frag<bf16> trT1(uint32_t a) {
+  return tr2<TB, TB + 32 * NC>(a);
+}
+template <int NC, uint32_t TB>
+__device__ __forceinline__ void trT(uint32_t a, Frag<bf16>& f0, Frag<bf16>& f1) {
+  tr4<TB, TB + 32 * NC, TB + 64 * NC, TB + 96 * NC>(a, f0, f1);
+}
+template <int NC, uint32_t TB>
+__device__ __forceinline__ void trT2(uint32_t a, uint32_t b, Frag<bf16>& fa0, Frag<bf16>& fa1, Frag<bf16>& fb0,
+                                     Frag<bf16>& fb1) {
+  tr4x2<TB, TB + 32 * NC, TB + 64 * NC, TB + 96 * NC>(a, b, fa0, fa1, fb0, fb1);
+}
+
+// Direct loads of one [64][NC] input tile with the lane source offsets
+// computed once (full chunks; a partial chunk takes load_tile).
+template <typename T, int NC, int NT>
+struct LoadOffs {
+  static constexpr int CPR = NC / 8;
+  static constexpr int UNITS = 64 * CPR;
+  static constexpr int N = (UNITS + NT - 1) / NT;
+  uint32_t o[N];
+  __device__ __forceinline__ void init(uint32_t row_bytes) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int u = min(tid + NT * i, UNITS - 1);
+      const int r = u / CPR, pos = u % CPR;
+      const int c8 = sizeof(T) == 2 ? (pos ^ Tile<NC>::swz(r)) : pos;
+      o[i] = (uint32_t)r * row_bytes + (uint32_t)(8 * c8 * sizeof(T));
     }
+  }
+  __device__ __forceinline__ void issue(const T* base_t, unsigned char* dst) const {
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    const unsigned char* base = reinterpret_cast<const unsigned char*>(base_t);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (UNITS % NT != 0 && NT * i + WAVE * wid >= UNITS) break;      // uniform per wave
+      direct8<T>(base, o[i], dst + (NT * i + WAVE * wid) * 8 * sizeof(T));
+    }
+  }
+};
+
+template <typename TQ, int K, int V, bool OUT>
+struct ChunkLoads {
+  using E = Eng<TQ, K, V, OUT>;
+  LoadOffs<TQ, K, E::NT> qk;
+  LoadOffs<bf16, V, E::NT> v;
+  LoadOffs<bf16, C, E::NT> ai;
+  __device__ __forceinline__ void init(int H) {
+    qk.init((uint32_t)(H * K * sizeof(TQ)));
+    v.init((uint32_t)(H * V * 2));
+    ai.init((uint32_t)(C * 2));
+  }
+  // q (seg_out), k, v and Ai of the chunk at tokens t0 .. t0 + nv - 1 into
+  // buffer P; the raw g and beta of token t0 + lane into gr.
+  template <int P>
+  __device__ __forceinline__ void issue(unsigned char* smem, GateRaw& gr, const void* qp, const void* kp,
+                                        const void* vp, const void* gp, const void* bp, int g_dt, int b_dt,
+                                        int64_t t0, int nv, int h, int H, const bf16* ai_src) const {
+    const int l = lane_id();
+    gr.g = 0u;
+    gr.b = 0u;
+    if (l < nv) {
+      gr.g = ld_raw(gp, (t0 + l) * H + h, g_dt);
+      gr.b = ld_raw(bp, (t0 + l) * H + h, b_dt);
+    }
+    const int64_t e0 = t0 * H + h;
+    const TQ* q0 = reinterpret_cast<const TQ*>(qp) + e0 * K;
+    const TQ* k0 = reinterpret_cast<const TQ*>(kp) + e0 * K;
+    const bf16* v0 = reinterpret_cast<const bf16*>(vp) + e0 * V;
+    unsigned char* dq = smem + (E::FP8 ? E::qraw(P) : E::q_tile(P));
+    unsigned char* dk = smem + (E::FP8 ? E::kraw(P) : E::k_tile(P));
+    if (nv == C) {
+      if constexpr (OUT) qk.issue(q0, dq);
+      qk.issue(k0, dk);
+      v.issue(v0, smem + E::v_tile(P));
+    } else {
+      if constexpr (OUT) load_tile<TQ, K, E::NT>(q0, (uint32_t)(H * K * sizeof(TQ)), nv, dq);
+      load_tile<TQ, K, E::NT>(k0, (uint32_t)(H * K * sizeof(TQ)), nv, dk);
+      load_tile<bf16, V, E::NT>(v0, (uint32_t)(H * V * 2), nv, smem + E::v_tile(P));
+    }
+    ai.issue(ai_src, smem + E::ai_tile(P));
+  }
+};
+
+// The chunk vectors of a wave (lane = token), written to the wave's own LDS
+// slot: gc, exp(gc) * scale, beta exp(gc), gate = exp(gc_last - gc) (0 past
+// the last valid token), beta.  Returns exp(gc_last).
+__device__ __forceinline__ float chunk_vectors(float* vec, const GateRaw& gr, int g_dt, int b_dt, int nv,
+                                               float scale) {
+  const int l = lane_id();
+  float gl;
+  const float gc = chunk_cumsum(gr, g_dt, nv, gl);
+  const float b = raw_to_f32(gr.b, b_dt);
+  const float eg = gexp(gc);
+  vec[l] = gc;
+  vec[C + l] = eg * scale;
+  vec[2 * C + l] = b * eg;
+  vec[3 * C + l] = l < nv ? gexp(gl - gc) : 0.f;
+  vec[4 * C + l] = b;
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gexp(gl))));
+}
+
+// Scale the 8 bf16 values of fragment f (K order of an accumulator tile pair:
+// indices 32 ks + 4 lg + e, 32 ks + 16 + 4 lg + e) by the vector x, rounded to bf16.
+__device__ __forceinline__ Frag<bf16> scale_frag(const Frag<bf16>& f, const float* x, int ks) {
+  const int lg = lane_id() >> 4;
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(x + 32 * ks + 4 * lg);
+  const f32x4 s1 = *reinterpret_cast<const f32x4*>(x + 32 * ks + 16 + 4 * lg);
+  float y[8];
+  frag_unpack(f, y);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] *= s0[e];
+    y[4 + e] *= s1[e];
+  }
+  return frag_pack(y);
+}
+
+// Round the 4 floats of an accumulator tile to bf16 and back (two packed conversions).
+__device__ __forceinline__ f32x4 round4(const f32x4& a) {
+  const uint32_t p0 = pack_bf16x2(a[0], a[1]), p1 = pack_bf16x2(a[2], a[3]);
+  return f32x4{bf16_lo(p0), bf16_hi(p0), bf16_lo(p1), bf16_hi(p1)};
+}
+
+// One w unit: token tile tn, d tiles 4 DG .. 4 DG + 3.  B = Ai rows 16 tn + lc
+// scaled by beta exp(gc) (wy_fast.py:67-81, with the scaling moved from k to the
+// columns of Ai), A = k^T; the tile -w^T[d][i] goes to s_w[i][pcol(d)].
+template <typename E, int K, int DG, int P>
+__device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& lo, const float* vec, int tn) {
+  const unsigned char* ai = smem + E::ai_tile(P) + 32 * tn * C;
+  const int nks = tn / 2 + 1;                                   // Ai is lower triangular
+  Frag<bf16> b0 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0])), vec + 2 * C, 0);
+  Frag<bf16> b1 = b0;
+  if (nks == 2) b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
+  unsigned char* wt = smem + E::off_w + lo.w + 32 * tn * E::LDW;
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) {
+    const int dt = 4 * DG + dd;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (nks == 2) {
+      Frag<bf16> a0, a1;
+      trT<K, E::k_tile(P)>(lo.ktr[dt], a0, a1);
+      mma(acc, a0, b0);
+      mma(acc, a1, b1);
+    } else {
+      mma(acc, trT1<K, E::k_tile(P)>(lo.ktr[dt]), b0);
+    }
+    uint2 pk;
+    pk.x = pack_bf16x2(-acc[0], -acc[1]);
+    pk.y = pack_bf16x2(-acc[2], -acc[3]);
+    *reinterpret_cast<uint2*>(wt + 2 * (32 * (dt >> 1) + 4 * (dt & 1))) = pk;
   }
 }
 
-// (v beta)^T fragments (wy_fast.py:61-65) of V columns v0..v0+15
-template <typename TQ, int K, int V, bool WITH_Q>
-__device__ __forceinline__ void u_frags(const unsigned char* smem, const ChunkTiles& T, int v0, Frag<bf16> (&vb)[2]) {
-  using L = SegLds<TQ, K, V, WITH_Q>;
-  const float* s_b = reinterpret_cast<const float*>(smem + L::off_g) + 2 * C;
-  const int lg = lane_id() >> 4;
-  Frag<bf16> vt[2];
-  col_tr2<V>(T.v, v0, vt);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    float x[8];
-    frag_unpack(vt[ks], x);
-    const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_b + 32 * ks + 4 * lg);
-    const f32x4 b1 = *reinterpret_cast<const f32x4*>(s_b + 32 * ks + 16 + 4 * lg);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] *= (e < 4 ? b0[e] : b1[e - 4]);
-    vb[ks] = frag_pack(x);
-  }
-}
-// u (64 rows x 16 columns) = Ai vb, rounded to bf16, in accumulator tiles
-__device__ __forceinline__ void u_products(const ChunkTiles& T, const Frag<bf16> (&vb)[2], f32x4 (&u)[4]) {
-  const int l = lane_id();
-  const int lg = l >> 4, lc = l & 15;
+// u (64 tokens x 16 columns) = Ai bf16(v beta) of the V column tile whose
+// transposed read starts at vtr, rounded to bf16 (wy_fast.py:55-65).
+template <typename E, int V, int P>
+__device__ __forceinline__ void u_tile(const unsigned char* smem, const uint32_t (&airow)[2], uint32_t vtr,
+                                       const float* vec, f32x4 (&Y)[4]) {
+  Frag<bf16> t0, t1;
+  trT<V, E::v_tile(P)>(vtr, t0, t1);
+  const Frag<bf16> vb0 = scale_frag(t0, vec + 4 * C, 0);
+  const Frag<bf16> vb1 = scale_frag(t1, vec + 4 * C, 1);
+  const unsigned char* ai = smem + E::ai_tile(P);
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks <= tm / 2; ++ks) mma(acc, Tile<C>::row8(T.ai, 16 * tm + lc, 4 * ks + lg), vb[ks]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = round_to<bf16>(acc[j]);
-    u[tm] = acc;
+    mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + airow[0])), vb0);
+    if (tm >= 2) mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + airow[1])), vb1);
+    Y[tm] = round4(acc);
   }
 }
 
-// S (K x 16*CT, accumulator tiles) <- gamma S + k^T vg, vg given as operand fragments
-template <int K, int CT>
-__device__ __forceinline__ void state_update(f32x4 (&S)[K / 16][CT], const Frag<bf16> (&vg)[2][CT],
-                                             const ChunkTiles& T, float gamma) {
-#pragma unroll
-  for (int tp = 0; tp < K / 16; tp += 2) {      // two row tiles per read batch
-    uint32_t ad[8];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      Tile<K>::col_tr_addr(T.k, 0, 16 * (tp + e), ad[4 * e], ad[4 * e + 1]);
-      Tile<K>::col_tr_addr(T.k, 1, 16 * (tp + e), ad[4 * e + 2], ad[4 * e + 3]);
-    }
-    Frag<bf16> a[4];
-    tr_read4(ad, a);
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        S[tp + e][ct] *= gamma;
-        mma(S[tp + e][ct], a[2 * e], vg[0][ct]);
-        mma(S[tp + e][ct], a[2 * e + 1], vg[1][ct]);
-      }
-    }
-  }
-}
-
-// Y (64 x 16*CT) -= w X, X given as operand fragments of its K rows
-template <typename TQ, int K, int V, bool WITH_Q, int CT>
-__device__ __forceinline__ void sub_wx(f32x4 (&Y)[4][CT], const Frag<bf16> (&xb)[K / 32][CT],
-                                       const unsigned char* smem) {
-  using L = SegLds<TQ, K, V, WITH_Q>;
-  const bf16* s_w = reinterpret_cast<const bf16*>(smem + L::off_w);
-  const int l = lane_id();
-  const int lg = l >> 4, lc = l & 15;
+// Y (64 tokens x 16 CT columns) += (-w) X, X given as operand fragments of its K rows
+template <typename E, int K, int CT>
+__device__ __forceinline__ void add_wx(const unsigned char* smem, uint32_t w_lane, const Frag<bf16> (&xb)[K / 32][CT],
+                                       f32x4 (&Y)[4][CT]) {
+  const unsigned char* wt = smem + E::off_w + w_lane;
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) {
-    f32x4 p[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) p[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < K / 32; ++ks) {
-      const Frag<bf16> a = frag_at<bf16>(s_w + (16 * tm + lc) * L::LDK + 32 * ks + 8 * lg);
+      const Frag<bf16> a = frag_at<bf16>(reinterpret_cast<const bf16*>(wt + 32 * tm * E::LDW + 64 * ks));
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) mma(p[ct], a, xb[ks][ct]);
+      for (int ct = 0; ct < CT; ++ct) mma(Y[tm][ct], a, xb[ks][ct]);
     }
+  }
+}
+
+// S (K x 16 CT, accumulator tiles) <- gamma S + k^T vg
+template <typename E, int K, int CT, int P>
+__device__ __forceinline__ void update_state(const LaneOffs<K>& lo, const Frag<bf16> (&vg)[2][CT], float gamma,
+                                             f32x4 (&S)[K / 16][CT]) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) Y[tm][ct] -= p[ct];
+  for (int tp = 0; tp < K / 16; tp += 2) {
+    Frag<bf16> a0, a1, b0, b1;
+    trT2<K, E::k_tile(P)>(lo.ktr[tp], lo.ktr[tp + 1], a0, a1, b0, b1);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      S[tp][ct] *= gamma;
+      mma(S[tp][ct], a0, vg[0][ct]);
+      mma(S[tp][ct], a1, vg[1][ct]);
+      S[tp + 1][ct] *= gamma;
+      mma(S[tp + 1][ct], b0, vg[0][ct]);
+      mma(S[tp + 1][ct], b1, vg[1][ct]);
+    }
   }
 }
 
@@ -854,6 +958,39 @@ struct OutPending {
   }
 };
 
+// The Aqk' tiles of a wave (seg_out): tile t (tm >= tn, tri_tile order) gives
+// lane i = 16 tm + lc (q side) and j = 16 tn + 4 lg + jj (k side):
+// Aqk'[i][j] = scale exp(gc_i - gc_j) q_i.k_j for i >= j (chunk_o.py:109-118,
+// the output scale folded in), stored bf16 at s_Aqk[i][pcol(j)] -- four
+// consecutive positions, one 8-byte write.
+template <typename E, int K, int P>
+__device__ __forceinline__ void aqk_tile(unsigned char* smem, const LaneOffs<K>& lo, const float* vec, float log2s,
+                                         int t) {
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  int tm, tn;
+  tri_tile(t, tm, tn);
+  const unsigned char* kt = smem + E::k_tile(P) + 32 * tn * K;
+  const unsigned char* qt = smem + E::q_tile(P) + 32 * tm * K;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < K / 32; ++ks)
+    mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(kt + lo.krow[ks])),
+        frag_at<bf16>(reinterpret_cast<const bf16*>(qt + lo.krow[ks])));
+  const float gi = vec[16 * tm + lc];
+  const f32x4 gj = *reinterpret_cast<const f32x4*>(vec + 16 * tn + 4 * lg);
+  float x[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    x[jj] = acc[jj] * __builtin_amdgcn_exp2f(fmaf(gi - gj[jj], 1.4426950408889634f, log2s));
+    if (tm == tn && lc < 4 * lg + jj) x[jj] = 0.f;
+  }
+  uint2 pk;
+  pk.x = pack_bf16x2(x[0], x[1]);
+  pk.y = pack_bf16x2(x[2], x[3]);
+  *reinterpret_cast<uint2*>(smem + E::off_aqk + lo.aqk + 2 * (16 * tm * E::LDQ + 32 * (tn >> 1) + 4 * (tn & 1))) = pk;
+}
+
 // ---------------------------------------------------------------------------
 // seg_out: exact recurrence + output over one segment
 // ---------------------------------------------------------------------------
@@ -876,25 +1013,24 @@ struct SegOutArgs {
 };
 
 template <typename TQ, int K, int V>
-__global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
-  using L = SegLds<TQ, K, V, true>;
-  constexpr int NW = OutCfg<K, V>::NW, NT = OutCfg<K, V>::NT;
-  constexpr int KT = K / 16;
+__global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
+  using E = Eng<TQ, K, V, true>;
+  constexpr int NW = E::NW, NT = E::NT, KT = K / 16, KS = K / 32;
   extern __shared__ __align__(16) unsigned char smem[];
-  bf16* s_Aqk = reinterpret_cast<bf16*>(smem + L::off_Aqk);
-  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
 
   const int h = blockIdx.y;
   const int H = G.H;
   const SegLoc sl = locate_seg(blockIdx.x, G);
   if (!sl.ok) return;
-  const int wid = threadIdx.x / WAVE;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
   const int vw = wid * 16;              // first V column of this wave
   const float qs = a.q_scale ? a.q_scale[h] : 1.f;
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
-  const bool beta_lowp = a.beta_dtype == DT_BF16;
+  const float log2s = __builtin_amdgcn_logf(a.scale);
+  const uint32_t lds0 = lds_addr(smem);
+  float* vec = reinterpret_cast<float*>(smem + E::off_vec) + wid * E::NVEC * C;
 
   // ---- initial state of the segment (lane element (tt, j): row 16*tt + 4*lg + j, column vw + lc)
   f32x4 S[KT][1];
@@ -923,88 +1059,125 @@ __global__ __launch_bounds__((OutCfg<K, V>::NT)) void seg_out_kernel(SegOutArgs 
       for (int tt = 0; tt < KT; ++tt) S[tt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  // upper 16x16 tiles of Aqk that operand fragments read (col tile 2ks+1 of row
-  // tile 2ks) are zero; no chunk writes them
-  for (int idx = threadIdx.x; idx < 2 * 16 * 16; idx += NT) {
-    const int tile = idx >> 8, r = (idx >> 4) & 15, c = idx & 15;
-    s_Aqk[(32 * tile + r) * L::LDT + pcol(32 * tile + 16 + c)] = (bf16)0.f;
+  // Upper 16x16 tiles of Aqk' that operand fragments read (column tile 2 ks + 1
+  // of row tile 2 ks) are zero; no chunk writes them.
+  {
+    bf16* s_aqk = reinterpret_cast<bf16*>(smem + E::off_aqk);
+    for (int idx = threadIdx.x; idx < 2 * 16 * 16; idx += NT) {
+      const int tile = idx >> 8, r = (idx >> 4) & 15, c = idx & 15;
+      s_aqk[(32 * tile + r) * E::LDQ + pcol(32 * tile + 16 + c)] = (bf16)0.f;
+    }
   }
+  LaneOffs<K> lo;
+  lane_offsets<K, E::LDW, E::LDQ>(lo, lds0);
+  const uint32_t vtr = tr_lane_addr<V>(lds0, wid);
+  ChunkLoads<TQ, K, V, true> LD;
+  LD.init(H);
 
   GateRaw gr;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
   const bf16* ai = a.Ai + ((sl.cbase + sl.c0) * H + h) * C * C;
   const int64_t ai_step = (int64_t)H * C * C;
-  load_chunk<TQ, K, V, true, NT>(smem + L::off_buf, gr, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h,
-                                 H, ai);
+  LD.template issue<0>(smem, gr, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
   bf16* o = reinterpret_cast<bf16*>(a.o);
   OutPending op;
   op.nv = 0;
 
-  for (int ci = 0; ci < sl.nch; ++ci) {
-    unsigned char* buf = smem + L::off_buf + (ci & 1) * L::buf_bytes;
-    const ChunkTiles T = stage_chunk<TQ, K, V, true, NT>(smem, buf, gr, qs, ks_, nv, a.g_dtype, a.beta_dtype);
-    op.store(o, H, h, V, vw);            // the previous chunk's output, after this chunk's wait
+  auto step = [&](auto PP, int ci) {
+    constexpr int P = decltype(PP)::value;
+    wait_loads();
+    op.store(o, H, h, V, vw);            // the previous chunk's output
     const int64_t t0c = t0;
     const int nvc = nv;
-    if (ci + 1 < sl.nch) {                // the next chunk streams into the other buffer
+    const float gamma = chunk_vectors(vec, gr, a.g_dtype, a.beta_dtype, nvc, a.scale);
+    if constexpr (E::FP8) {
+      lds_barrier();                     // every wave is done with the previous chunk's q/k tiles
+      convert_fp8<K, NT>(smem + E::qraw(P), reinterpret_cast<bf16*>(smem + E::q_tile(P)), qs, nvc);
+      convert_fp8<K, NT>(smem + E::kraw(P), reinterpret_cast<bf16*>(smem + E::k_tile(P)), ks_, nvc);
+    }
+    lds_barrier();                       // barrier 1: the chunk's tiles are complete
+    if (ci + 1 < sl.nch) {
       t0 += C;
       nv = (int)min((int64_t)C, sl.eos - t0);
       ai += ai_step;
-      load_chunk<TQ, K, V, true, NT>(smem + L::off_buf + ((ci + 1) & 1) * L::buf_bytes, gr, a.q, a.k, a.v, a.g,
-                                     a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
+      LD.template issue<1 - P>(smem, gr, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
     }
-    lds_barrier();   // chunk tiles and vectors ready
 
-    // ---- Aqk tiles, w = Ai kb -> LDS, u = Ai vb (this wave's columns) -> registers
-    for (int t = wid; t < 10; t += NW) kkt_tile<K, true, L::LDT>(T.q, T.k, s_g, nullptr, s_Aqk, t);
+    // ---- phase A
+    Frag<bf16> hb[KS][1];                // h = S rounded (chunk_delta_h.py:129-139)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) hb[ks][0] = acc_frag(S[2 * ks][0], S[2 * ks + 1][0]);
+    f32x4 oi[4];                         // o_inter^T = h^T q^T (chunk_o.py:84-107)
     {
-      WFrags<K, NW> wf;
-      w_frags<TQ, K, V, true, NW>(smem, T, beta_lowp, wf);
-      w_products<TQ, K, V, true, NW>(smem, T, wf);
+      const unsigned char* qt = smem + E::q_tile(P);
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        oi[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint2 pa = *reinterpret_cast<const uint2*>(qt + 32 * tn * K + lo.qacc[ks][0]);
+          const uint2 pb = *reinterpret_cast<const uint2*>(qt + 32 * tn * K + lo.qacc[ks][1]);
+          Frag<bf16> b;
+          b.v = __builtin_bit_cast(bf16x8, make_uint4(pa.x, pa.y, pb.x, pb.y));
+          mma(oi[tn], hb[ks][0], b);
+        }
+      }
+    }
+    if constexpr (NW == 8) {
+      if (wid < 4) {
+        aqk_tile<E, K, P>(smem, lo, vec, log2s, 2 * wid);
+        aqk_tile<E, K, P>(smem, lo, vec, log2s, 2 * wid + 1);
+      } else if (wid < 6) {
+        aqk_tile<E, K, P>(smem, lo, vec, log2s, wid + 4);
+      }
+    } else {
+      for (int t = wid; t < 10; t += NW) aqk_tile<E, K, P>(smem, lo, vec, log2s, t);
+    }
+    for (int u = wid; u < 4 * E::NDG; u += NW) {
+      if constexpr (E::NDG == 2) {
+        if (u & 1) w_unit<E, K, 1, P>(smem, lo, vec, u >> 1);
+        else w_unit<E, K, 0, P>(smem, lo, vec, u >> 1);
+      } else {
+        w_unit<E, K, 0, P>(smem, lo, vec, u);
+      }
     }
     f32x4 Y[4][1];
     {
-      Frag<bf16> vb[2];
-      u_frags<TQ, K, V, true>(smem, T, vw, vb);
-      f32x4 u[4];
-      u_products(T, vb, u);
+      f32x4 u4[4];
+      u_tile<E, V, P>(smem, lo.airow, vtr, vec, u4);
 #pragma unroll
-      for (int tm = 0; tm < 4; ++tm) Y[tm][0] = u[tm];
+      for (int tm = 0; tm < 4; ++tm) Y[tm][0] = u4[tm];
     }
-    lds_barrier();   // w and Aqk complete
+    lds_barrier();                       // barrier 2: w and Aqk' complete
 
-    // ---- h = S rounded (the snapshot of chunk_delta_h.py:129-139) as operand fragments
-    Frag<bf16> hb[K / 32][1];
+    // ---- phase B: v' = u - w h                       (chunk_delta_h.py:141-157)
+    add_wx<E, K, 1>(smem, lo.w, hb, Y);
+    // ---- o^T = o_inter^T exp(gc) scale + v_new^T Aqk'^T  (chunk_o.py:84-128)
+    {
+      Frag<bf16> vn[2];
 #pragma unroll
-    for (int ks = 0; ks < K / 32; ++ks) hb[ks][0] = acc_frag(S[2 * ks][0], S[2 * ks + 1][0]);
-    // ---- v' = u - w h                                   (chunk_delta_h.py:141-157)
-    sub_wx<TQ, K, V, true, 1>(Y, hb, smem);
-
-    // ---- o^T = scale (h^T q^T exp(gc) + v_new^T Aqk^T)  (chunk_o.py:84-128)
-    op.t0 = t0c;
-    op.nv = nvc;
-    Frag<bf16> vn[2];
+      for (int ks = 0; ks < 2; ++ks) vn[ks] = acc_frag(Y[2 * ks][0], Y[2 * ks + 1][0]);
+      const unsigned char* aq = smem + E::off_aqk + lo.aqk;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) vn[ks] = acc_frag(Y[2 * ks][0], Y[2 * ks + 1][0]);
+      for (int tn = 0; tn < 4; ++tn) {
+        f32x4 r = oi[tn] * vec[C + 16 * tn + lc];
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-      const int t = 16 * tn + lc;
-      f32x4 o1 = {0.f, 0.f, 0.f, 0.f}, o2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < K / 32; ++ks) mma(o1, hb[ks][0], Tile<K>::row_acc_order(T.q, t, ks, lg));
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        if (ks <= tn / 2) mma(o2, vn[ks], frag_at<bf16>(s_Aqk + t * L::LDT + 32 * ks + 8 * lg));
-      const float eg = s_g[C + t] * a.scale;
-      op.set(tn, o1 * eg + o2 * a.scale);
+        for (int ks = 0; ks < 2; ++ks)
+          if (ks <= tn / 2) mma(r, vn[ks], frag_at<bf16>(reinterpret_cast<const bf16*>(aq + 32 * tn * E::LDQ + 64 * ks)));
+        op.set(tn, r);
+      }
+      op.t0 = t0c;
+      op.nv = nvc;
     }
-
     // ---- S = exp(g_last) S + k^T (v' exp(g_last - gc))   (chunk_delta_h.py:163-211)
     Frag<bf16> vg[2][1];
-    gate_frags<1>(Y, s_g + 3 * C, vg);
-    state_update<K, 1>(S, vg, T, gexp(s_g[nvc - 1]));
-    lds_barrier();   // the tiles of this chunk are free for the chunk after next
+    gate_frags<1>(Y, vec + 3 * C, vg);
+    update_state<E, K, 1, P>(lo, vg, gamma, S);
+  };
+  for (int ci = 0; ci < sl.nch; ci += 2) {
+    step(std::integral_constant<int, 0>{}, ci);
+    if (ci + 1 < sl.nch) step(std::integral_constant<int, 1>{}, ci + 1);
   }
   op.store(o, H, h, V, vw);
 
@@ -1033,26 +1206,29 @@ struct SegTransArgs {
 };
 
 template <typename TQ, int K, int V>
-__global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTransArgs a, SegGeom G) {
-  using L = SegLds<TQ, K, V, false>;
-  constexpr int NW = TransCfg<K, V>::NW, NT = TransCfg<K, V>::NT;
-  constexpr int XC = K + V;             // columns of [M | R]
-  static_assert(XC % 32 == 0, "K + V must be a multiple of 32");
-  constexpr int CT = 2;                 // 16-column tiles per wave
-  constexpr int KT = K / 16;
+__global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(SegTransArgs a, SegGeom G) {
+  using E = Eng<TQ, K, V, false>;
+  constexpr int NW = E::NW, NT = E::NT, KT = K / 16, KS = K / 32, CT = 2;
   extern __shared__ __align__(16) unsigned char smem[];
-  const float* s_g = reinterpret_cast<const float*>(smem + L::off_g);
 
   const int h = blockIdx.y;
   const int H = G.H;
   const SegLoc sl = locate_seg(blockIdx.x, G);
   if (!sl.ok || sl.j == sl.nseg - 1) return;
-  const int wid = threadIdx.x / WAVE;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
-  const int xw = wid * 16 * CT;         // first column of [M | R] owned by this wave
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
-  const bool beta_lowp = a.beta_dtype == DT_BF16;
+  const uint32_t lds0 = lds_addr(smem);
+  float* vec = reinterpret_cast<float*>(smem + E::off_vec) + wid * E::NVEC * C;
+  // column tiles of [M | R] owned by this wave: c = wid + NW ct; c < K/16 are M tiles
+  int ctile[CT];
+  uint32_t vtr[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    ctile[ct] = wid + NW * ct;
+    vtr[ct] = tr_lane_addr<V>(lds0, max(ctile[ct] - KT, 0));
+  }
 
   f32x4 X[KT][CT];
 #pragma unroll
@@ -1060,79 +1236,89 @@ __global__ __launch_bounds__((TransCfg<K, V>::NT)) void seg_trans_kernel(SegTran
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) X[tt][ct][j] = (16 * tt + 4 * lg + j == xw + 16 * ct + lc) ? 1.f : 0.f;
+      for (int j = 0; j < 4; ++j) X[tt][ct][j] = (16 * tt + 4 * lg + j == 16 * ctile[ct] + lc) ? 1.f : 0.f;
     }
   }
+  LaneOffs<K> lo;
+  lane_offsets<K, E::LDW, E::LDQ>(lo, lds0);
+  ChunkLoads<TQ, K, V, false> LD;
+  LD.init(H);
 
   GateRaw gr;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
   const bf16* ai = a.Ai + ((sl.cbase + sl.c0) * H + h) * C * C;
   const int64_t ai_step = (int64_t)H * C * C;
-  load_chunk<TQ, K, V, false, NT>(smem + L::off_buf, gr, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0,
-                                  nv, h, H, ai);
-  for (int ci = 0; ci < sl.nch; ++ci) {
-    unsigned char* buf = smem + L::off_buf + (ci & 1) * L::buf_bytes;
-    const ChunkTiles T = stage_chunk<TQ, K, V, false, NT>(smem, buf, gr, 1.f, ks_, nv, a.g_dtype, a.beta_dtype);
+  LD.template issue<0>(smem, gr, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
+
+  auto step = [&](auto PP, int ci) {
+    constexpr int P = decltype(PP)::value;
+    wait_loads();
     const int nvc = nv;
+    const float gamma = chunk_vectors(vec, gr, a.g_dtype, a.beta_dtype, nvc, 1.f);
+    if constexpr (E::FP8) {
+      lds_barrier();
+      convert_fp8<K, NT>(smem + E::kraw(P), reinterpret_cast<bf16*>(smem + E::k_tile(P)), ks_, nvc);
+    }
+    lds_barrier();                       // barrier 1
     if (ci + 1 < sl.nch) {
       t0 += C;
       nv = (int)min((int64_t)C, sl.eos - t0);
       ai += ai_step;
-      load_chunk<TQ, K, V, false, NT>(smem + L::off_buf + ((ci + 1) & 1) * L::buf_bytes, gr, nullptr, a.k, a.v, a.g,
-                                      a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
+      LD.template issue<1 - P>(smem, gr, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H,
+                               ai);
     }
-    lds_barrier();   // chunk tiles and vectors ready
-    {
-      WFrags<K, NW> wf;
-      w_frags<TQ, K, V, false, NW>(smem, T, beta_lowp, wf);
-      w_products<TQ, K, V, false, NW>(smem, T, wf);
+    // ---- phase A
+    Frag<bf16> xb[KS][CT];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag(X[2 * ks][ct], X[2 * ks + 1][ct]);
+    }
+    for (int u = wid; u < 4 * E::NDG; u += NW) {
+      if constexpr (E::NDG == 2) {
+        if (u & 1) w_unit<E, K, 1, P>(smem, lo, vec, u >> 1);
+        else w_unit<E, K, 0, P>(smem, lo, vec, u >> 1);
+      } else {
+        w_unit<E, K, 0, P>(smem, lo, vec, u);
+      }
     }
     f32x4 Y[4][CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      const int c0 = xw + 16 * ct;
-      if (c0 >= K) {
-        Frag<bf16> vb[2];
-        u_frags<TQ, K, V, false>(smem, T, c0 - K, vb);
-        f32x4 u[4];
-        u_products(T, vb, u);
+      f32x4 u4[4] = {};
+      if (ctile[ct] >= KT) u_tile<E, V, P>(smem, lo.airow, vtr[ct], vec, u4);
 #pragma unroll
-        for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u[tm];
-      } else {
-#pragma unroll
-        for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+      for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u4[tm];
     }
-    lds_barrier();   // w complete
-    Frag<bf16> xb[K / 32][CT];
-#pragma unroll
-    for (int ks = 0; ks < K / 32; ++ks) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag(X[2 * ks][ct], X[2 * ks + 1][ct]);
-    }
-    sub_wx<TQ, K, V, false, CT>(Y, xb, smem);
+    lds_barrier();                       // barrier 2: w complete
+    // ---- phase B
+    add_wx<E, K, CT>(smem, lo.w, xb, Y);
     Frag<bf16> yg[2][CT];
-    gate_frags<CT>(Y, s_g + 3 * C, yg);
-    state_update<K, CT>(X, yg, T, gexp(s_g[nvc - 1]));
-    lds_barrier();
+    gate_frags<CT>(Y, vec + 3 * C, yg);
+    update_state<E, K, CT, P>(lo, yg, gamma, X);
+  };
+  for (int ci = 0; ci < sl.nch; ci += 2) {
+    step(std::integral_constant<int, 0>{}, ci);
+    if (ci + 1 < sl.nch) step(std::integral_constant<int, 1>{}, ci + 1);
   }
 
   const int64_t s = blockIdx.x;
-  float* pm = a.M + (s * H + h) * K * K + 4 * lg * K + xw + lc;
-  float* pr = a.R + (s * H + h) * K * V + 4 * lg * V + xw - K + lc;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    if (xw + 16 * ct < K) {
+    const int c0 = 16 * ctile[ct];
+    if (c0 < K) {
+      float* pm = a.M + (s * H + h) * K * K + 4 * lg * K + c0 + lc;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pm[(16 * tt + j) * K + 16 * ct] = X[tt][ct][j];
+        for (int j = 0; j < 4; ++j) pm[(16 * tt + j) * K] = X[tt][ct][j];
     } else {
+      float* pr = a.R + (s * H + h) * K * V + 4 * lg * V + c0 - K + lc;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pr[(16 * tt + j) * V + 16 * ct] = X[tt][ct][j];
+        for (int j = 0; j < 4; ++j) pr[(16 * tt + j) * V] = X[tt][ct][j];
     }
   }
 }
@@ -1309,12 +1495,11 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   }
   if (!mark(1)) return -1;
   if (p.run_trans) {
-    constexpr size_t lds = SegLds<TQ, K, V, false>::total;
-    static_assert(lds <= 160 * 1024, "seg_trans tiles do not fit in LDS");
+    constexpr size_t lds = Eng<TQ, K, V, false>::total;
     auto kt = seg_trans_kernel<TQ, K, V>;
     if (set_lds(kt, lds)) return -1;
     SegTransArgs ta{p.k, p.v, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, Ai, p.M, p.R};
-    hipLaunchKernelGGL(kt, grid, dim3(TransCfg<K, V>::NT), lds, s, ta, G);
+    hipLaunchKernelGGL(kt, grid, dim3(Eng<TQ, K, V, false>::NT), lds, s, ta, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(2)) return -1;
@@ -1327,13 +1512,12 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   }
   if (!mark(3)) return -1;
   if (p.ns_grid > 0) {
-    constexpr size_t lds = SegLds<TQ, K, V, true>::total;
-    static_assert(lds <= 160 * 1024, "seg_out tiles do not fit in LDS");
+    constexpr size_t lds = Eng<TQ, K, V, true>::total;
     auto ko = seg_out_kernel<TQ, K, V>;
     if (set_lds(ko, lds)) return -1;
     SegOutArgs oa{p.q, p.k, p.v, p.g, p.beta, p.q_scale, p.k_scale, p.g_dtype, p.beta_dtype,
                   p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht};
-    hipLaunchKernelGGL(ko, grid, dim3(OutCfg<K, V>::NT), lds, s, oa, G);
+    hipLaunchKernelGGL(ko, grid, dim3(Eng<TQ, K, V, true>::NT), lds, s, oa, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(4)) return -1;
