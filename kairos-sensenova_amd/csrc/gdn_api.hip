@@ -183,8 +183,8 @@ SegPlan plan_segments(int64_t B, int64_t T, int64_t H, int64_t n_seqs) {
 
 size_t seg_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, const SegPlan& P) {
   size_t total = n_seqs > 0 ? 2 * align_up(sizeof(int32_t) * (n_seqs + 1)) : 0;
-  // chunk inverses Ai: bf16 [chunks, H, 64, 64]
-  total += align_up((size_t)chunks_bound(B, T, n_seqs) * H * kgdn::C * kgdn::C * 2);
+  // chunk records: bf16 inverse [64][64] + chunk vectors, per (chunk, head)
+  total += align_up((size_t)chunks_bound(B, T, n_seqs) * H * kgdn::kSegRecordBytes);
   if (P.trans || P.combine) {
     const size_t blocks = (size_t)P.ns * H;
     total += align_up(blocks * K * K * sizeof(float));        // M
@@ -365,7 +365,7 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
     seg_off = so;
   }
   const int64_t nc_grid = chunks_bound(B, T, n_seqs);
-  void* Ai = cv.take((size_t)nc_grid * H * kgdn::C * kgdn::C * 2);
+  void* Ai = cv.take((size_t)nc_grid * H * kgdn::kSegRecordBytes);
   float* M = nullptr;
   float* R = nullptr;
   float* s_init = nullptr;

@@ -73,6 +73,13 @@ struct FwdOArgs {
   void* o;                // out [B*T, H, V] compute dtype
 };
 
+// Per (chunk, head) record written by seg_prep and streamed by seg_trans and
+// seg_out: the bf16 chunk inverse (I + A)^-1 [64][64] (row t holding columns in
+// pcol order), then eight fp32 vectors of 64: gc, exp(gc) * scale,
+// beta * exp(gc), the update gate exp(gc_last - gc), beta, exp(gc_last)
+// (repeated), and two unused.
+constexpr int kSegRecordBytes = 64 * 64 * 2 + 8 * 64 * 4;
+
 // Segment-parallel fused forward (gdn_seg.hip).  Sequences are cut into
 // segments of L chunks; M, R and s_init are fp32 workspaces of ns_grid * H
 // blocks of K x K, K x V and K x V.
@@ -102,7 +109,7 @@ struct SegFwdArgs {
   float scale;
   void* o;                // out [B*T, H, V]
   float* ht;              // out [N, H, K, V] or nullptr
-  void* Ai;               // [nc_grid, H, 64, 64] bf16 chunk inverses (seg_prep -> seg_trans, seg_out)
+  void* Ai;               // [nc_grid, H] chunk records of kSegRecordBytes (seg_prep -> seg_trans, seg_out)
   int64_t nc_grid;        // number of chunks (varlen: an upper bound)
   bool run_trans;         // some sequence has more than one segment
   bool run_combine;       // ... or final_state of empty sequences is needed

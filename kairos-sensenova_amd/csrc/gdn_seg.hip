@@ -165,12 +165,7 @@ struct Tile {
   }
 };
 
-// Transposed fragments through inline asm.  The compiler's wait tracking treats
-// ds_read_b64_tr_b16 (the builtin) as a possible reader of whatever an
-// in-flight direct global->LDS load writes, and puts a vmcnt(0) before it --
-// a wait for the next chunk's prefetch in the middle of the current chunk.
-// The asm form is outside that tracking; it waits for its own reads
-// (lgkmcnt(0)) before returning, so its results are ready when used.
+// Transposed fragments: the two 8-byte halves read by ds_read_b64_tr_b16.
 __device__ __forceinline__ Frag<bf16> tr_pair(u32x2 a, u32x2 b) {
   Frag<bf16> f;
   f.v = __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
@@ -281,9 +276,10 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t ld
 }
 
 // 8 input elements per lane: bf16 -> one dwordx4 direct load; fp8 -> two dword loads.
+// (wave_blk: the LDS byte address of the wave's destination block, wave-uniform)
 template <typename T>
-__device__ __forceinline__ void direct8(const void* base, uint32_t off, unsigned char* wave_blk) {
-  const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(wave_blk));
+__device__ __forceinline__ void direct8(const void* base, uint32_t off, uint32_t wave_blk) {
+  const uint32_t d = __builtin_amdgcn_readfirstlane(wave_blk);
   if constexpr (sizeof(T) == 2) {
     dma16(base, off, d);
   } else {
@@ -300,7 +296,7 @@ __device__ __forceinline__ void direct8(const void* base, uint32_t off, unsigned
 // lane byte offset, the form the saddr encoding takes, so no 64-bit per-lane
 // address stays live.
 template <typename T, int NC, int NT>
-__device__ __forceinline__ void load_tile(const T* base_t, uint32_t row_bytes, int nv, unsigned char* dst) {
+__device__ __forceinline__ void load_tile(const T* base_t, uint32_t row_bytes, int nv, uint32_t dst) {
   constexpr int CPR = NC / 8;
   constexpr int UNITS = 64 * CPR;
   const int tid = threadIdx.x;
@@ -313,8 +309,7 @@ __device__ __forceinline__ void load_tile(const T* base_t, uint32_t row_bytes, i
     const int r = u / CPR, pos = u % CPR;
     const int c8 = sizeof(T) == 2 ? (pos ^ Tile<NC>::swz(r)) : pos;
     const uint32_t rs = r < nv ? r : 0;
-    unsigned char* blk = dst + (NT * i + WAVE * wid) * 8 * sizeof(T);
-    direct8<T>(base, rs * row_bytes + (uint32_t)(8 * c8 * sizeof(T)), blk);
+    direct8<T>(base, rs * row_bytes + (uint32_t)(8 * c8 * sizeof(T)), dst + (NT * i + WAVE * wid) * 8 * sizeof(T));
   }
 }
 
@@ -376,18 +371,31 @@ __device__ __forceinline__ void wait_loads() {
   asm volatile("" ::: "memory");
 }
 
-// Chunk-local cumsum gc of g (fla ops/utils/cumsum.py:58-65) over wave 0, from
-// the raw g bits of token tid; returns gc of token tid and sets gl = gc of the
-// last valid token.
+// v + (v of the lane selected by DPP control CTRL), 0 where the source lane is
+// outside the pattern or its row is masked off (ROWS).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_plus(float v) {
+  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false);
+  return v + __int_as_float(s);
+}
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves (no LDS):
+// shifts by 1, 2, 4, 8 within each row of 16 lanes, then row_bcast:15 and
+// row_bcast:31 carry the row totals into the rows above.
+__device__ __forceinline__ float wave_prefix_sum(float v) {
+  v = dpp_plus<0x111, 0xf>(v);      // row_shr:1
+  v = dpp_plus<0x112, 0xf>(v);      // row_shr:2
+  v = dpp_plus<0x114, 0xf>(v);      // row_shr:4
+  v = dpp_plus<0x118, 0xf>(v);      // row_shr:8
+  v = dpp_plus<0x142, 0xa>(v);      // row_bcast:15 into rows 1 and 3
+  v = dpp_plus<0x143, 0xc>(v);      // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Chunk-local cumsum gc of g (fla ops/utils/cumsum.py:58-65), lane = token:
+// returns gc of token lane and sets gl = gc of the last valid token (nv - 1).
 __device__ __forceinline__ float chunk_cumsum(const GateRaw& gr, int g_dt, int nv, float& gl) {
-  const int l = lane_id();
-  float gv = raw_to_f32(gr.g, g_dt);
-#pragma unroll
-  for (int off = 1; off < WAVE; off <<= 1) {
-    const float o = __shfl_up(gv, off, WAVE);
-    if (l >= off) gv += o;
-  }
-  gl = __shfl(gv, nv - 1, WAVE);
+  const float gv = wave_prefix_sum(raw_to_f32(gr.g, g_dt));
+  gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gv), nv - 1));
   return gv;
 }
 
@@ -484,7 +492,8 @@ struct SegPrepArgs {
   const void* beta;
   const float* k_scale;
   int g_dtype, beta_dtype;
-  bf16* Ai;                   // out [chunks, H, 64, 64], row t holds columns pcol(t')
+  float scale;                // output scale (the record's exp(gc) * scale vector)
+  unsigned char* rec;         // out [chunks, H] records of kSegRecordBytes (see gdn_kernels.h)
 };
 
 constexpr int NT_PREP = 256;
@@ -527,7 +536,7 @@ __global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeo
   GateRaw gr;
   load_gates(gr, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
   load_tile<TQ, K, NT>(reinterpret_cast<const TQ*>(a.k) + (t0 * H + h) * K, (uint32_t)(H * K * sizeof(TQ)), nv,
-                       smem + P::off_in);
+                       lds_addr(smem) + (uint32_t)P::off_in);
   // the upper 16x16 blocks of Ai are zero
   for (int idx = tid; idx < 6 * 256; idx += NT) {
     const int b = idx >> 8, r = (idx >> 4) & 15, cc = idx & 15;
@@ -544,10 +553,24 @@ __global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeo
   } else {
     kt = reinterpret_cast<const bf16*>(smem + P::off_in);
   }
+  unsigned char* rec = a.rec + (ci * H + h) * (int64_t)kSegRecordBytes;
   if (tid < WAVE) {
+    // the chunk vectors of the record (lane = token)
     float gl;
-    s_g[tid] = chunk_cumsum(gr, a.g_dtype, nv, gl);
-    s_g[C + tid] = raw_to_f32(gr.b, a.beta_dtype);
+    const float gc = chunk_cumsum(gr, a.g_dtype, nv, gl);
+    const float b = raw_to_f32(gr.b, a.beta_dtype);
+    const float eg = gexp(gc);
+    s_g[tid] = gc;
+    s_g[C + tid] = b;
+    float* vec = reinterpret_cast<float*>(rec + C * C * 2);
+    vec[tid] = gc;
+    vec[C + tid] = eg * a.scale;
+    vec[2 * C + tid] = b * eg;
+    vec[3 * C + tid] = tid < nv ? gexp(gl - gc) : 0.f;
+    vec[4 * C + tid] = b;
+    vec[5 * C + tid] = gexp(gl);
+    vec[6 * C + tid] = 0.f;
+    vec[7 * C + tid] = 0.f;
   }
   lds_barrier();
   for (int t = wid; t < 10; t += NW) kkt_tile<K, P::LDA>(kt, s_g, s_g + C, s_A, t);
@@ -556,7 +579,7 @@ __global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeo
   lds_barrier();
   if (wid >= 1 && wid <= 3) chain_solve<P::LDA, P::LDT>(s_A, s_Ai, wid - 1);
   lds_barrier();
-  bf16* dst = a.Ai + (ci * H + h) * C * C;
+  bf16* dst = reinterpret_cast<bf16*>(rec);
   for (int u = tid; u < C * C / 8; u += NT) {
     const int r = u >> 3, c8 = u & 7;
     *reinterpret_cast<uint4*>(dst + r * C + 8 * c8) = *reinterpret_cast<const uint4*>(s_Ai + r * P::LDT + 8 * c8);
@@ -571,12 +594,15 @@ __global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeo
 // state tiles (K rows) in VGPRs in the MFMA accumulator layout.
 //
 // Per chunk (two workgroup barriers):
-//   top      this wave's direct loads of the chunk have landed; the wave forms
-//            the chunk vectors itself, in its own LDS slot, so no wave waits
-//            for another: gc, exp(gc) scale, beta exp(gc), the update gate
-//            exp(gc_last - gc), beta.  (fp8: q/k dequantised after a barrier.)
+//   top      this wave's direct loads of the chunk have landed (q, k, v and
+//            the chunk record: Ai and the chunk vectors gc, exp(gc) scale,
+//            beta exp(gc), the update gate exp(gc_last - gc), beta and
+//            exp(gc_last), formed once by seg_prep).  (fp8: q/k dequantised
+//            after a barrier.)
 //   barrier 1; the next chunk's loads go into the other buffer (every wave is
-//            done with the chunk that used it).
+//            done with the chunk that used it), one direct-load instruction at
+//            a time between the steps of phase A, so that no wave stalls on a
+//            full memory queue.
 //   phase A  [own]    h = bf16(S) as operand fragments; o_inter = q h (seg_out);
 //                     u = Ai bf16(v beta) for the wave's V columns;
 //            [shared] Aqk'^T tiles (seg_out) and w tiles into LDS.  w is formed
@@ -610,12 +636,13 @@ struct Eng {
   static constexpr uint32_t kraw(int p) { return q_end + (uint32_t)p * RAW; }        // fp8 inputs as loaded
   static constexpr uint32_t qraw(int p) { return q_end + 2 * RAW + (uint32_t)p * RAW; }
   static constexpr uint32_t raw_end = FP8 ? q_end + (OUT ? 4 : 2) * RAW : q_end;
-  static constexpr uint32_t ai_tile(int p) { return raw_end + (uint32_t)p * AB; }
-  static constexpr uint32_t off_w = raw_end + 2 * AB;
+  // the chunk record as loaded: Ai, then the chunk vectors (vec_tile)
+  static constexpr uint32_t RB = kSegRecordBytes;
+  static constexpr uint32_t ai_tile(int p) { return raw_end + (uint32_t)p * RB; }
+  static constexpr uint32_t vec_tile(int p) { return ai_tile(p) + AB; }
+  static constexpr uint32_t off_w = raw_end + 2 * RB;
   static constexpr uint32_t off_aqk = off_w + C * LDW * 2;
-  static constexpr uint32_t off_vec = off_aqk + (OUT ? C * LDQ * 2 : 0);
-  static constexpr int NVEC = 5;
-  static constexpr uint32_t total = off_vec + NW * NVEC * C * 4;
+  static constexpr uint32_t total = off_aqk + (OUT ? C * LDQ * 2 : 0);
   static_assert(tr_end + 0 <= 65536, "transposed tiles must lie in the first 64 KB of LDS");
   static_assert(total <= 160 * 1024, "chunk tiles do not fit in LDS");
 };
@@ -659,53 +686,32 @@ __device__ __forceinline__ void lane_offsets(LaneOffs<K>& o, uint32_t lds0) {
   o.aqk = 2 * (lc * LDQ + 8 * lg);
 }
 
-// Transposed reads (ds_read_b64_tr_b16) through inline asm -- see tr_pair --
-// at one or two lane addresses plus immediate byte offsets, one wait for all.
+// ds_read_b64_tr_b16 at LDS byte address a + O: the constant O folds into the
+// instruction's offset field, so the lane address stays one fixed VGPR.  (The
+// compiler schedules these reads and their waits; the direct loads it cannot
+// see -- they are asm -- so it adds no vmcnt wait for the prefetch in flight.)
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+template <uint32_t O>
+__device__ __forceinline__ u32x2 tr_rd(uint32_t a) {
+  lds_u8* p = reinterpret_cast<lds_u8*>(a) + O;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_s16x4*>(p)));
+}
 template <int O0, int O1>
 __device__ __forceinline__ Frag<bf16> tr2(uint32_t a) {
-  u32x2 r0, r1;
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
-      "ds_read_b64_tr_b16 %1, %2 offset:%4\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r0), "=&v"(r1)
-      : "v"(a), "i"(O0), "i"(O1));
-  return tr_pair(r0, r1);
+  return tr_pair(tr_rd<O0>(a), tr_rd<O1>(a));
 }
 template <int O0, int O1, int O2, int O3>
 __device__ __forceinline__ void tr4(uint32_t a, Frag<bf16>& f0, Frag<bf16>& f1) {
-  u32x2 r0, r1, r2, r3;
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %4 offset:%5\n\t"
-      "ds_read_b64_tr_b16 %1, %4 offset:%6\n\t"
-      "ds_read_b64_tr_b16 %2, %4 offset:%7\n\t"
-      "ds_read_b64_tr_b16 %3, %4 offset:%8\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
-      : "v"(a), "i"(O0), "i"(O1), "i"(O2), "i"(O3));
-  f0 = tr_pair(r0, r1);
-  f1 = tr_pair(r2, r3);
+  f0 = tr_pair(tr_rd<O0>(a), tr_rd<O1>(a));
+  f1 = tr_pair(tr_rd<O2>(a), tr_rd<O3>(a));
 }
 template <int O0, int O1, int O2, int O3>
 __device__ __forceinline__ void tr4x2(uint32_t a, uint32_t b, Frag<bf16>& fa0, Frag<bf16>& fa1, Frag<bf16>& fb0,
                                       Frag<bf16>& fb1) {
-  u32x2 r0, r1, r2, r3, r4, r5, r6, r7;
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %8 offset:%10\n\t"
-      "ds_read_b64_tr_b16 %1, %8 offset:%11\n\t"
-      "ds_read_b64_tr_b16 %2, %8 offset:%12\n\t"
-      "ds_read_b64_tr_b16 %3, %8 offset:%13\n\t"
-      "ds_read_b64_tr_b16 %4, %9 offset:%10\n\t"
-      "ds_read_b64_tr_b16 %5, %9 offset:%11\n\t"
-      "ds_read_b64_tr_b16 %6, %9 offset:%12\n\t"
-      "ds_read_b64_tr_b16 %7, %9 offset:%13\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
-      : "v"(a), "v"(b), "i"(O0), "i"(O1), "i"(O2), "i"(O3));
-  fa0 = tr_pair(r0, r1);
-  fa1 = tr_pair(r2, r3);
-  fb0 = tr_pair(r4, r5);
-  fb1 = tr_pair(r6, r7);
+  tr4<O0, O1, O2, O3>(a, fa0, fa1);
+  tr4<O0, O1, O2, O3>(b, fb0, fb1);
 }
 // K step 0 (tokens 0-31) or both K steps of a transposed fragment of the
 // [64][NC] tile at LDS byte offset TB: rows r0 and r0 + 16 of each step.
@@ -721,6 +727,27 @@ template <int NC, uint32_t TB>
 __device__ __forceinline__ void trT2(uint32_t a, uint32_t b, Frag<bf16>& fa0, Frag<bf16>& fa1, Frag<bf16>& fb0,
                                      Frag<bf16>& fb1) {
   tr4x2<TB, TB + 32 * NC, TB + 64 * NC, TB + 96 * NC>(a, b, fa0, fa1, fb0, fb1);
+}
+
+// Four column tiles at once (lane addresses a[0..3]): K step 0 only or both K steps.
+template <int O0, int O1>
+__device__ __forceinline__ void tr8x(const uint32_t (&a)[4], Frag<bf16> (&f)[4][2]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) f[e][0] = tr_pair(tr_rd<O0>(a[e]), tr_rd<O1>(a[e]));
+}
+template <int O0, int O1, int O2, int O3>
+__device__ __forceinline__ void tr16x(const uint32_t (&a)[4], Frag<bf16> (&f)[4][2]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) tr4<O0, O1, O2, O3>(a[e], f[e][0], f[e][1]);
+}
+// Four column tiles of a [64][NC] tile at LDS byte offset TB, K step 0 or both K steps.
+template <int NC, uint32_t TB>
+__device__ __forceinline__ void trT4x1(const uint32_t (&a)[4], Frag<bf16> (&f)[4][2]) {
+  tr8x<TB, TB + 32 * NC>(a, f);
+}
+template <int NC, uint32_t TB>
+__device__ __forceinline__ void trT4x2(const uint32_t (&a)[4], Frag<bf16> (&f)[4][2]) {
+  tr16x<TB, TB + 32 * NC, TB + 64 * NC, TB + 96 * NC>(a, f);
 }
 
 // Direct loads of one [64][NC] input tile with the lane source offsets
@@ -741,7 +768,12 @@ struct LoadOffs {
       o[i] = (uint32_t)r * row_bytes + (uint32_t)(8 * c8 * sizeof(T));
     }
   }
-  __device__ __forceinline__ void issue(const T* base_t, unsigned char* dst) const {
+  __device__ __forceinline__ void issue1(int i, const T* base_t, uint32_t dst) const {
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    if (UNITS % NT != 0 && NT * i + WAVE * wid >= UNITS) return;      // uniform per wave
+    direct8<T>(base_t, o[i], dst + (NT * i + WAVE * wid) * 8 * sizeof(T));
+  }
+  __device__ __forceinline__ void issue(const T* base_t, uint32_t dst) const {
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
     const unsigned char* base = reinterpret_cast<const unsigned char*>(base_t);
 #pragma unroll
@@ -752,66 +784,89 @@ struct LoadOffs {
   }
 };
 
-template <typename TQ, int K, int V, bool OUT>
-struct ChunkLoads {
-  using E = Eng<TQ, K, V, OUT>;
-  LoadOffs<TQ, K, E::NT> qk;
-  LoadOffs<bf16, V, E::NT> v;
-  LoadOffs<bf16, C, E::NT> ai;
-  __device__ __forceinline__ void init(int H) {
-    qk.init((uint32_t)(H * K * sizeof(TQ)));
-    v.init((uint32_t)(H * V * 2));
-    ai.init((uint32_t)(C * 2));
+// Lane source offsets of the chunk record (kSegRecordBytes): the Ai tile in
+// 16-byte units with the Tile<64> swizzle, then the vectors in plain order.
+template <int NT>
+struct RecOffs {
+  static constexpr int AU = C * C * 2 / 16;              // Ai units
+  static constexpr int UNITS = kSegRecordBytes / 16;
+  static constexpr int N = (UNITS + NT - 1) / NT;
+  uint32_t o[N];
+  __device__ __forceinline__ void init() {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int u = min(tid + NT * i, UNITS - 1);
+      if (u < AU) {
+        const int r = u / 8, pos = u % 8;
+        o[i] = (uint32_t)(r * C * 2 + 16 * (pos ^ Tile<C>::swz(r)));
+      } else {
+        o[i] = (uint32_t)(16 * u);
+      }
+    }
   }
-  // q (seg_out), k, v and Ai of the chunk at tokens t0 .. t0 + nv - 1 into
-  // buffer P; the raw g and beta of token t0 + lane into gr.
-  template <int P>
-  __device__ __forceinline__ void issue(unsigned char* smem, GateRaw& gr, const void* qp, const void* kp,
-                                        const void* vp, const void* gp, const void* bp, int g_dt, int b_dt,
-                                        int64_t t0, int nv, int h, int H, const bf16* ai_src) const {
-    const int l = lane_id();
-    gr.g = 0u;
-    gr.b = 0u;
-    if (l < nv) {
-      gr.g = ld_raw(gp, (t0 + l) * H + h, g_dt);
-      gr.b = ld_raw(bp, (t0 + l) * H + h, b_dt);
-    }
-    const int64_t e0 = t0 * H + h;
-    const TQ* q0 = reinterpret_cast<const TQ*>(qp) + e0 * K;
-    const TQ* k0 = reinterpret_cast<const TQ*>(kp) + e0 * K;
-    const bf16* v0 = reinterpret_cast<const bf16*>(vp) + e0 * V;
-    unsigned char* dq = smem + (E::FP8 ? E::qraw(P) : E::q_tile(P));
-    unsigned char* dk = smem + (E::FP8 ? E::kraw(P) : E::k_tile(P));
-    if (nv == C) {
-      if constexpr (OUT) qk.issue(q0, dq);
-      qk.issue(k0, dk);
-      v.issue(v0, smem + E::v_tile(P));
-    } else {
-      if constexpr (OUT) load_tile<TQ, K, E::NT>(q0, (uint32_t)(H * K * sizeof(TQ)), nv, dq);
-      load_tile<TQ, K, E::NT>(k0, (uint32_t)(H * K * sizeof(TQ)), nv, dk);
-      load_tile<bf16, V, E::NT>(v0, (uint32_t)(H * V * 2), nv, smem + E::v_tile(P));
-    }
-    ai.issue(ai_src, smem + E::ai_tile(P));
+  __device__ __forceinline__ void issue1(int i, const unsigned char* base, uint32_t dst) const {
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    if (UNITS % NT != 0 && NT * i + WAVE * wid >= UNITS) return;      // uniform per wave
+    direct8<bf16>(base, o[i], dst + (NT * i + WAVE * wid) * 16);
   }
 };
 
-// The chunk vectors of a wave (lane = token), written to the wave's own LDS
-// slot: gc, exp(gc) * scale, beta exp(gc), gate = exp(gc_last - gc) (0 past
-// the last valid token), beta.  Returns exp(gc_last).
-__device__ __forceinline__ float chunk_vectors(float* vec, const GateRaw& gr, int g_dt, int b_dt, int nv,
-                                               float scale) {
-  const int l = lane_id();
-  float gl;
-  const float gc = chunk_cumsum(gr, g_dt, nv, gl);
-  const float b = raw_to_f32(gr.b, b_dt);
-  const float eg = gexp(gc);
-  vec[l] = gc;
-  vec[C + l] = eg * scale;
-  vec[2 * C + l] = b * eg;
-  vec[3 * C + l] = l < nv ? gexp(gl - gc) : 0.f;
-  vec[4 * C + l] = b;
-  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(gexp(gl))));
-}
+// The direct loads of one chunk, as a fixed sequence of per-wave load
+// instructions ("slots"): [q (seg_out)], k, v, then the chunk record.  Slot S
+// of the next chunk is issued at a fixed point of the current chunk's step.
+template <typename TQ, int K, int V, bool OUT>
+struct ChunkLoads {
+  using E = Eng<TQ, K, V, OUT>;
+  static constexpr int NTL = E::NT;                      // loader threads: every wave
+  static constexpr int NQ = LoadOffs<TQ, K, NTL>::N;
+  static constexpr int NV = LoadOffs<bf16, V, NTL>::N;
+  static constexpr int NR = RecOffs<NTL>::N;
+  static constexpr int NS = (OUT ? 2 * NQ : NQ) + NV + NR;   // slots per chunk
+  LoadOffs<TQ, K, NTL> qk;
+  LoadOffs<bf16, V, NTL> v;
+  RecOffs<NTL> rec;
+  __device__ __forceinline__ void init(int H) {
+    qk.init((uint32_t)(H * K * sizeof(TQ)));
+    v.init((uint32_t)(H * V * 2));
+    rec.init();
+  }
+  // Slot S of the chunk at tokens t0 .. t0 + nv - 1 (record rec_src) into
+  // buffer P.  A partial chunk (nv < 64) loads a whole q/k/v tile at the
+  // tile's first slot, rows past the end reading row 0.
+  template <int P, int S>
+  __device__ __forceinline__ void slot(uint32_t lds0, const void* qp, const void* kp, const void* vp, int64_t t0,
+                                       int nv, int h, int H, const unsigned char* rec_src) const {
+    constexpr int S0 = OUT ? NQ : 0;                       // first k slot
+    constexpr int S1 = S0 + NQ;                            // first v slot
+    constexpr int S2 = S1 + NV;                            // first record slot
+    const int64_t e0 = t0 * H + h;
+    if constexpr (S < S1) {
+      constexpr bool isq = S < S0;
+      constexpr int i = isq ? S : S - S0;
+      const TQ* src = reinterpret_cast<const TQ*>(isq ? qp : kp) + e0 * K;
+      const uint32_t dst = lds0 + (isq ? (E::FP8 ? E::qraw(P) : E::q_tile(P)) : (E::FP8 ? E::kraw(P) : E::k_tile(P)));
+      if (nv == C) qk.issue1(i, src, dst);
+      else if (i == 0) load_tile<TQ, K, NTL>(src, (uint32_t)(H * K * sizeof(TQ)), nv, dst);
+    } else if constexpr (S < S2) {
+      constexpr int i = S - S1;
+      const bf16* src = reinterpret_cast<const bf16*>(vp) + e0 * V;
+      if (nv == C) v.issue1(i, src, lds0 + E::v_tile(P));
+      else if (i == 0) load_tile<bf16, V, NTL>(src, (uint32_t)(H * V * 2), nv, lds0 + E::v_tile(P));
+    } else if constexpr (S < NS) {
+      rec.issue1(S - S2, rec_src, lds0 + E::ai_tile(P));
+    }
+  }
+  // slots S .. NS - 1
+  template <int P, int S>
+  __device__ __forceinline__ void slots_from(uint32_t lds0, const void* qp, const void* kp, const void* vp, int64_t t0,
+                                             int nv, int h, int H, const unsigned char* rec_src) const {
+    if constexpr (S < NS) {
+      slot<P, S>(lds0, qp, kp, vp, t0, nv, h, H, rec_src);
+      slots_from<P, S + 1>(lds0, qp, kp, vp, t0, nv, h, H, rec_src);
+    }
+  }
+};
 
 // Scale the 8 bf16 values of fragment f (K order of an accumulator tile pair:
 // indices 32 ks + 4 lg + e, 32 ks + 16 + 4 lg + e) by the vector x, rounded to bf16.
@@ -846,18 +901,16 @@ __device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& l
   Frag<bf16> b1 = b0;
   if (nks == 2) b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
   unsigned char* wt = smem + E::off_w + lo.w + 32 * tn * E::LDW;
+  const uint32_t ka[4] = {lo.ktr[4 * DG], lo.ktr[4 * DG + 1], lo.ktr[4 * DG + 2], lo.ktr[4 * DG + 3]};
+  Frag<bf16> kf[4][2];
+  if (nks == 2) trT4x2<K, E::k_tile(P)>(ka, kf);
+  else trT4x1<K, E::k_tile(P)>(ka, kf);
 #pragma unroll
   for (int dd = 0; dd < 4; ++dd) {
     const int dt = 4 * DG + dd;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (nks == 2) {
-      Frag<bf16> a0, a1;
-      trT<K, E::k_tile(P)>(lo.ktr[dt], a0, a1);
-      mma(acc, a0, b0);
-      mma(acc, a1, b1);
-    } else {
-      mma(acc, trT1<K, E::k_tile(P)>(lo.ktr[dt]), b0);
-    }
+    mma(acc, kf[dd][0], b0);
+    if (nks == 2) mma(acc, kf[dd][1], b1);
     uint2 pk;
     pk.x = pack_bf16x2(-acc[0], -acc[1]);
     pk.y = pack_bf16x2(-acc[2], -acc[3]);
@@ -905,17 +958,18 @@ template <typename E, int K, int CT, int P>
 __device__ __forceinline__ void update_state(const LaneOffs<K>& lo, const Frag<bf16> (&vg)[2][CT], float gamma,
                                              f32x4 (&S)[K / 16][CT]) {
 #pragma unroll
-  for (int tp = 0; tp < K / 16; tp += 2) {
-    Frag<bf16> a0, a1, b0, b1;
-    trT2<K, E::k_tile(P)>(lo.ktr[tp], lo.ktr[tp + 1], a0, a1, b0, b1);
+  for (int tq = 0; tq < K / 16; tq += 4) {
+    const uint32_t ka[4] = {lo.ktr[tq], lo.ktr[tq + 1], lo.ktr[tq + 2], lo.ktr[tq + 3]};
+    Frag<bf16> kf[4][2];
+    trT4x2<K, E::k_tile(P)>(ka, kf);
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      S[tp][ct] *= gamma;
-      mma(S[tp][ct], a0, vg[0][ct]);
-      mma(S[tp][ct], a1, vg[1][ct]);
-      S[tp + 1][ct] *= gamma;
-      mma(S[tp + 1][ct], b0, vg[0][ct]);
-      mma(S[tp + 1][ct], b1, vg[1][ct]);
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        S[tq + e][ct] *= gamma;
+        mma(S[tq + e][ct], kf[e][0], vg[0][ct]);
+        mma(S[tq + e][ct], kf[e][1], vg[1][ct]);
+      }
     }
   }
 }
@@ -1006,7 +1060,7 @@ struct SegOutArgs {
   const void* h0;             // [N, H, K, V] or nullptr
   int h0_dtype;
   const float* s_init;        // [NS, H, K, V] fp32 state at each segment start (j >= 1)
-  const bf16* Ai;             // [chunks, H, 64, 64] from seg_prep
+  const void* Ai;             // [chunks, H] chunk records from seg_prep
   float scale;
   void* o;                    // [B*T, H, V]
   float* ht;                  // [N, H, K, V] or nullptr
@@ -1030,7 +1084,6 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
   const float log2s = __builtin_amdgcn_logf(a.scale);
   const uint32_t lds0 = lds_addr(smem);
-  float* vec = reinterpret_cast<float*>(smem + E::off_vec) + wid * E::NVEC * C;
 
   // ---- initial state of the segment (lane element (tt, j): row 16*tt + 4*lg + j, column vw + lc)
   f32x4 S[KT][1];
@@ -1074,12 +1127,12 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
   ChunkLoads<TQ, K, V, true> LD;
   LD.init(H);
 
-  GateRaw gr;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
-  const bf16* ai = a.Ai + ((sl.cbase + sl.c0) * H + h) * C * C;
-  const int64_t ai_step = (int64_t)H * C * C;
-  LD.template issue<0>(smem, gr, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
+  const unsigned char* rec = reinterpret_cast<const unsigned char*>(a.Ai) +
+                             ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
+  const int64_t rec_step = (int64_t)H * kSegRecordBytes;
+  LD.template slots_from<0, 0>(lds0, a.q, a.k, a.v, t0, nv, h, H, rec);
   bf16* o = reinterpret_cast<bf16*>(a.o);
   OutPending op;
   op.nv = 0;
@@ -1090,19 +1143,28 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
     op.store(o, H, h, V, vw);            // the previous chunk's output
     const int64_t t0c = t0;
     const int nvc = nv;
-    const float gamma = chunk_vectors(vec, gr, a.g_dtype, a.beta_dtype, nvc, a.scale);
+    const float* vec = reinterpret_cast<const float*>(smem + E::vec_tile(P));
     if constexpr (E::FP8) {
       lds_barrier();                     // every wave is done with the previous chunk's q/k tiles
       convert_fp8<K, NT>(smem + E::qraw(P), reinterpret_cast<bf16*>(smem + E::q_tile(P)), qs, nvc);
       convert_fp8<K, NT>(smem + E::kraw(P), reinterpret_cast<bf16*>(smem + E::k_tile(P)), ks_, nvc);
     }
     lds_barrier();                       // barrier 1: the chunk's tiles are complete
-    if (ci + 1 < sl.nch) {
+    const float gamma = vec[5 * C];      // exp(gc_last)
+    // the next chunk's loads go into the other buffer, one slot at a time
+    const bool more = ci + 1 < sl.nch;
+    if (more) {
       t0 += C;
       nv = (int)min((int64_t)C, sl.eos - t0);
-      ai += ai_step;
-      LD.template issue<1 - P>(smem, gr, a.q, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
+      rec += rec_step;
     }
+    auto slot = [&](auto SS) {
+      if (more) LD.template slot<1 - P, decltype(SS)::value>(lds0, a.q, a.k, a.v, t0, nv, h, H, rec);
+    };
+    auto slots_from = [&](auto SS) {
+      if (more) LD.template slots_from<1 - P, decltype(SS)::value>(lds0, a.q, a.k, a.v, t0, nv, h, H, rec);
+    };
+    slot(std::integral_constant<int, 0>{});
 
     // ---- phase A
     Frag<bf16> hb[KS][1];                // h = S rounded (chunk_delta_h.py:129-139)
@@ -1122,6 +1184,8 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
           b.v = __builtin_bit_cast(bf16x8, make_uint4(pa.x, pa.y, pb.x, pb.y));
           mma(oi[tn], hb[ks][0], b);
         }
+        if (tn == 1) slot(std::integral_constant<int, 1>{});
+        if (tn == 3) slot(std::integral_constant<int, 2>{});
       }
     }
     if constexpr (NW == 8) {
@@ -1134,6 +1198,7 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
     } else {
       for (int t = wid; t < 10; t += NW) aqk_tile<E, K, P>(smem, lo, vec, log2s, t);
     }
+    slot(std::integral_constant<int, 3>{});
     for (int u = wid; u < 4 * E::NDG; u += NW) {
       if constexpr (E::NDG == 2) {
         if (u & 1) w_unit<E, K, 1, P>(smem, lo, vec, u >> 1);
@@ -1142,6 +1207,8 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
         w_unit<E, K, 0, P>(smem, lo, vec, u);
       }
     }
+    slot(std::integral_constant<int, 4>{});
+    slot(std::integral_constant<int, 5>{});
     f32x4 Y[4][1];
     {
       f32x4 u4[4];
@@ -1149,6 +1216,8 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) Y[tm][0] = u4[tm];
     }
+    slot(std::integral_constant<int, 6>{});
+    slots_from(std::integral_constant<int, 7>{});
     lds_barrier();                       // barrier 2: w and Aqk' complete
 
     // ---- phase B: v' = u - w h                       (chunk_delta_h.py:141-157)
@@ -1200,7 +1269,7 @@ struct SegTransArgs {
   const void* beta;
   const float* k_scale;
   int g_dtype, beta_dtype;
-  const bf16* Ai;             // [chunks, H, 64, 64] from seg_prep
+  const void* Ai;             // [chunks, H] chunk records from seg_prep
   float* M;                   // [NS, H, K, K]
   float* R;                   // [NS, H, K, V]
 };
@@ -1220,7 +1289,6 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
   const int lg = l >> 4, lc = l & 15;
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
   const uint32_t lds0 = lds_addr(smem);
-  float* vec = reinterpret_cast<float*>(smem + E::off_vec) + wid * E::NVEC * C;
   // column tiles of [M | R] owned by this wave: c = wid + NW ct; c < K/16 are M tiles
   int ctile[CT];
   uint32_t vtr[CT];
@@ -1244,30 +1312,37 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
   ChunkLoads<TQ, K, V, false> LD;
   LD.init(H);
 
-  GateRaw gr;
   int64_t t0 = sl.bos + sl.c0 * C;
   int nv = (int)min((int64_t)C, sl.eos - t0);
-  const bf16* ai = a.Ai + ((sl.cbase + sl.c0) * H + h) * C * C;
-  const int64_t ai_step = (int64_t)H * C * C;
-  LD.template issue<0>(smem, gr, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H, ai);
+  const unsigned char* rec = reinterpret_cast<const unsigned char*>(a.Ai) +
+                             ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
+  const int64_t rec_step = (int64_t)H * kSegRecordBytes;
+  LD.template slots_from<0, 0>(lds0, nullptr, a.k, a.v, t0, nv, h, H, rec);
 
   auto step = [&](auto PP, int ci) {
     constexpr int P = decltype(PP)::value;
     wait_loads();
     const int nvc = nv;
-    const float gamma = chunk_vectors(vec, gr, a.g_dtype, a.beta_dtype, nvc, 1.f);
+    const float* vec = reinterpret_cast<const float*>(smem + E::vec_tile(P));
     if constexpr (E::FP8) {
       lds_barrier();
       convert_fp8<K, NT>(smem + E::kraw(P), reinterpret_cast<bf16*>(smem + E::k_tile(P)), ks_, nvc);
     }
     lds_barrier();                       // barrier 1
-    if (ci + 1 < sl.nch) {
+    const float gamma = vec[5 * C];      // exp(gc_last)
+    const bool more = ci + 1 < sl.nch;
+    if (more) {
       t0 += C;
       nv = (int)min((int64_t)C, sl.eos - t0);
-      ai += ai_step;
-      LD.template issue<1 - P>(smem, gr, nullptr, a.k, a.v, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H,
-                               ai);
+      rec += rec_step;
     }
+    auto slot = [&](auto SS) {
+      if (more) LD.template slot<1 - P, decltype(SS)::value>(lds0, nullptr, a.k, a.v, t0, nv, h, H, rec);
+    };
+    auto slots_from = [&](auto SS) {
+      if (more) LD.template slots_from<1 - P, decltype(SS)::value>(lds0, nullptr, a.k, a.v, t0, nv, h, H, rec);
+    };
+    slot(std::integral_constant<int, 0>{});
     // ---- phase A
     Frag<bf16> xb[KS][CT];
 #pragma unroll
@@ -1275,6 +1350,7 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag(X[2 * ks][ct], X[2 * ks + 1][ct]);
     }
+    slot(std::integral_constant<int, 1>{});
     for (int u = wid; u < 4 * E::NDG; u += NW) {
       if constexpr (E::NDG == 2) {
         if (u & 1) w_unit<E, K, 1, P>(smem, lo, vec, u >> 1);
@@ -1283,6 +1359,8 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
         w_unit<E, K, 0, P>(smem, lo, vec, u);
       }
     }
+    slot(std::integral_constant<int, 2>{});
+    slot(std::integral_constant<int, 3>{});
     f32x4 Y[4][CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -1290,7 +1368,9 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
       if (ctile[ct] >= KT) u_tile<E, V, P>(smem, lo.airow, vtr[ct], vec, u4);
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) Y[tm][ct] = u4[tm];
+      if (ct == 0) slot(std::integral_constant<int, 4>{});
     }
+    slots_from(std::integral_constant<int, 5>{});
     lds_barrier();                       // barrier 2: w complete
     // ---- phase B
     add_wx<E, K, CT>(smem, lo.w, xb, Y);
@@ -1482,13 +1562,13 @@ template <typename TQ, int K, int V>
 int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
   const dim3 grid((unsigned)p.ns_grid, (unsigned)p.H);
-  bf16* Ai = static_cast<bf16*>(p.Ai);
+  const void* Ai = p.Ai;
   auto mark = [&](int i) { return p.events == nullptr || hipEventRecord(p.events[i], s) == hipSuccess; };
   if (!mark(0)) return -1;
   if (p.ns_grid > 0 && p.nc_grid > 0) {
     constexpr size_t lds = PrepLds<TQ, K>::total;
     static_assert(lds <= 64 * 1024, "seg_prep tiles exceed the default LDS limit");
-    SegPrepArgs pa{p.k, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, Ai};
+    SegPrepArgs pa{p.k, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, p.scale, static_cast<unsigned char*>(p.Ai)};
     hipLaunchKernelGGL((seg_prep_kernel<TQ, K>), dim3((unsigned)p.nc_grid, (unsigned)p.H), dim3(NT_PREP), lds, s, pa,
                        G);
     if (hipGetLastError() != hipSuccess) return -1;

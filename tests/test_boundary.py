@@ -50,14 +50,15 @@ def test_num_chunks_bound():
 
 
 def test_workspace_size():
-    """The fused bf16 path holds the bf16 chunk inverses Ai (64 x 64 per chunk and
-    head) and, for multi-segment sequences, the per-segment [M | R] maps and segment
-    states (bounded by the CU count, not by T); the in-kernel L2 norm adds two q/k
-    copies; the staged fp32 K=128 path holds the reference's per-chunk intermediates."""
+    """The fused bf16 path holds one record per (chunk, head) -- the bf16 chunk
+    inverse Ai (64 x 64) and eight fp32 chunk vectors of 64 -- and, for
+    multi-segment sequences, the per-segment [M | R] maps and segment states
+    (bounded by the CU count, not by T); the in-kernel L2 norm adds two q/k copies;
+    the staged fp32 K=128 path holds the reference's per-chunk intermediates."""
     lib = _lib.load()
 
     def ai(nchunks, H):
-        return nchunks * H * 64 * 64 * 2
+        return nchunks * H * (64 * 64 * 2 + 8 * 64 * 4)
 
     def seg_state(B, T, H, K, V):
         L = lib.kairos_gdn_segment_chunks(B, T, H, 0)
