@@ -34,6 +34,7 @@ METRIC = "GDN chunk-fwd tokens/s + TFLOP/s (% bf16 MFMA peak) at T=32760,H=20,d=
 PEAK_BF16_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 C = 64
+RECORD = C * C * 2 + 8 * C * 4      # bytes of one (chunk, head) record written by seg_prep
 KERNELS = ["seg_prep_kernel", "seg_trans_kernel", "seg_combine_kernel", "seg_out_kernel"]
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2_hbm_traffic.md")
 
@@ -46,33 +47,35 @@ def flops_per_tok_head(K, V):
 def kernel_models(B, T, H, K, V, L, s=2, s_g=4, s_b=2):
     """Algorithmic HBM bytes (compulsory reads + writes) and FLOPs of one launch of each kernel.
 
-    seg_prep reads k, g, beta and writes the bf16 chunk inverses Ai (64 x 64 per
-    chunk and head); seg_out reads q, k, v, g, beta, Ai and the segment initial
-    states, writes o and final_state; seg_trans reads k, v, g, beta, Ai of every
-    segment but the last of each sequence and writes its [M | R]; seg_combine
-    reads [M | R] and h0 and writes the segment initial states.  FLOPs count
-    every MMA tile at full size: K.K^T (2CK per token) in seg_prep, the rest of
-    the chunk algebra in seg_out, w, u and the two [M | R] products in seg_trans.
+    seg_prep reads k, g, beta and writes one chunk record per (chunk, head):
+    the bf16 inverse Ai (64 x 64) and eight fp32 vectors of 64 (cumulative
+    gates and the gate / beta products the later kernels use), RECORD bytes.
+    seg_out reads q, k, v, the records and the segment initial states, writes
+    o and final_state; seg_trans reads k, v and the records of every segment
+    but the last of each sequence and writes its [M | R]; seg_combine reads
+    [M | R] and h0 and writes the segment initial states.  FLOPs count every
+    MMA tile at full size: K.K^T (2CK per token) in seg_prep, the rest of the
+    chunk algebra in seg_out, w, u and the two [M | R] products in seg_trans.
     """
     nc = (T + C - 1) // C
     nseg = (nc + L - 1) // L
     tok = B * T * H
     tok_trans = B * H * min(T, (nseg - 1) * L * C)
+    rec_trans = B * H * min(nc, (nseg - 1) * L) * RECORD
     state = K * V * 4
     mr = (K * K + K * V) * 4
-    ai = C * 2                       # Ai bytes per (token, head)
     return {
         "seg_prep_kernel": dict(
-            bytes=tok * (K * s + s_g + s_b) + B * H * nc * C * ai,
+            bytes=tok * (K * s + s_g + s_b) + B * H * nc * RECORD,
             flops=tok * 2 * C * K),
         "seg_trans_kernel": dict(
-            bytes=tok_trans * (K * s + V * s + s_g + s_b + ai) + B * H * (nseg - 1) * mr,
+            bytes=tok_trans * (K * s + V * s) + rec_trans + B * H * (nseg - 1) * mr,
             flops=tok_trans * (2 * C * (K + V) + 4 * K * (K + V))),
         "seg_combine_kernel": dict(
             bytes=B * H * (nseg - 1) * (mr + state) + B * H * state,
             flops=B * H * (nseg - 1) * 2 * K * K * V),
         "seg_out_kernel": dict(
-            bytes=tok * (2 * K * s + V * s + V * s + s_g + s_b + ai) + B * H * (nseg - 1) * state
+            bytes=tok * (2 * K * s + V * s + V * s) + B * H * nc * RECORD + B * H * (nseg - 1) * state
             + 2 * B * H * state,
             flops=tok * (flops_per_tok_head(K, V) - 2 * C * K)),
     }

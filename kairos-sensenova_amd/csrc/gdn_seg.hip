@@ -1052,11 +1052,8 @@ struct SegOutArgs {
   const void* q;
   const void* k;
   const void* v;
-  const void* g;
-  const void* beta;
   const float* q_scale;
   const float* k_scale;
-  int g_dtype, beta_dtype;
   const void* h0;             // [N, H, K, V] or nullptr
   int h0_dtype;
   const float* s_init;        // [NS, H, K, V] fp32 state at each segment start (j >= 1)
@@ -1265,10 +1262,7 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
 struct SegTransArgs {
   const void* k;
   const void* v;
-  const void* g;
-  const void* beta;
   const float* k_scale;
-  int g_dtype, beta_dtype;
   const void* Ai;             // [chunks, H] chunk records from seg_prep
   float* M;                   // [NS, H, K, K]
   float* R;                   // [NS, H, K, V]
@@ -1578,7 +1572,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     constexpr size_t lds = Eng<TQ, K, V, false>::total;
     auto kt = seg_trans_kernel<TQ, K, V>;
     if (set_lds(kt, lds)) return -1;
-    SegTransArgs ta{p.k, p.v, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, Ai, p.M, p.R};
+    SegTransArgs ta{p.k, p.v, p.k_scale, Ai, p.M, p.R};
     hipLaunchKernelGGL(kt, grid, dim3(Eng<TQ, K, V, false>::NT), lds, s, ta, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
@@ -1595,7 +1589,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     constexpr size_t lds = Eng<TQ, K, V, true>::total;
     auto ko = seg_out_kernel<TQ, K, V>;
     if (set_lds(ko, lds)) return -1;
-    SegOutArgs oa{p.q, p.k, p.v, p.g, p.beta, p.q_scale, p.k_scale, p.g_dtype, p.beta_dtype,
+    SegOutArgs oa{p.q, p.k, p.v, p.q_scale, p.k_scale,
                   p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht};
     hipLaunchKernelGGL(ko, grid, dim3(Eng<TQ, K, V, true>::NT), lds, s, oa, G);
     if (hipGetLastError() != hipSuccess) return -1;
