@@ -231,19 +231,21 @@ __device__ __forceinline__ SegLoc locate_seg(int s, const SegGeom& G) {
 // ---------------------------------------------------------------------------
 
 // seg_prep
-template <typename TQ, int K>
+// seg_prep LDS of one wave (one (chunk, head) item per wave): the ten lower
+// 16x16 blocks of A in fp32 (block (r, c), c <= r, at index r(r+1)/2 + c, row
+// stride LDB), then gc and beta of the chunk.  After the solve the block area
+// stages the bf16 Ai (64 rows of 64, pcol order) for the record store.
 struct PrepLds {
-  static constexpr bool FP8 = sizeof(TQ) == 1;
-  static constexpr int LDA = C + 4;        // row stride of the fp32 A / solve workspace
-  static constexpr int LDT = C + 8;        // row stride of the bf16 Ai staging tile (pcol order)
-  static constexpr size_t a16(size_t x) { return (x + 15) / 16 * 16; }
-  static constexpr size_t off_in = 0;                                          // k as loaded
-  static constexpr size_t off_ck = a16(off_in + (size_t)C * K * sizeof(TQ));   // fp8: bf16 k tile
-  static constexpr size_t off_A = a16(off_ck + (FP8 ? (size_t)C * K * 2 : 0));
-  static constexpr size_t off_Ai = a16(off_A + 4 * (size_t)C * LDA);
-  static constexpr size_t off_g = a16(off_Ai + 2 * (size_t)C * LDT);
-  static constexpr size_t total = off_g + sizeof(float) * 2 * C;               // gc, beta
+  static constexpr int LDB = 20;
+  static constexpr int BLK = 16 * LDB;                   // floats per block
+  static constexpr size_t off_A = 0;
+  static constexpr size_t off_g = 10 * BLK * sizeof(float);
+  static constexpr size_t per_wave = off_g + 2 * C * sizeof(float);
+  static constexpr int WAVES = 4;                        // waves (items) per workgroup
+  static constexpr size_t total = WAVES * per_wave;
+  static_assert(C * C * 2 <= off_g, "Ai staging must fit in the block area");
 };
+__device__ __forceinline__ int tri_blk(int r, int c) { return r * (r + 1) / 2 + c; }
 
 
 // ---------------------------------------------------------------------------
@@ -405,87 +407,17 @@ __device__ __forceinline__ void tri_tile(int t, int& tm, int& tn) {
   tm = (t >= 1) + (t >= 3) + (t >= 6);
   tn = t - tm * (tm + 1) / 2;
 }
-// seg_prep: A = beta_i exp(gc_i - gc_j) k_i.k_j for i > j, fp32 into out[i][j]
-// (chunk_scaled_dot_kkt.py:57-73), tile t.
-template <int K, int LDO>
-__device__ __forceinline__ void kkt_tile(const bf16* k, const float* s_gc, const float* s_beta, float* out, int t) {
-  using TK = Tile<K>;
-  const int l = lane_id();
-  const int lg = l >> 4, lc = l & 15;
-  int tm, tn;
-  tri_tile(t, tm, tn);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < K / 32; ++ks)
-    mma(acc, TK::row8(k, 16 * tm + lc, 4 * ks + lg), TK::row8(k, 16 * tn + lc, 4 * ks + lg));
-  const int i0 = 16 * tm + 4 * lg;
-  const int j = 16 * tn + lc;
-  const f32x4 gi = *reinterpret_cast<const f32x4*>(s_gc + i0);
-  const f32x4 bi = *reinterpret_cast<const f32x4*>(s_beta + i0);
-  const float gj = s_gc[j];
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    const int i = i0 + jj;
-    out[i * LDO + j] = i > j ? acc[jj] * gexp(gi[jj] - gj) * bi[jj] : 0.f;
-  }
-}
-
 // ---------------------------------------------------------------------------
-// seg_prep: Ai = (I + A)^-1 of one chunk (solve_tril.py:184-331, fp32
-// throughout, rounded to bf16 once)
+// seg_prep: one chunk record per (chunk, head), one wave per item, no barriers
 // ---------------------------------------------------------------------------
-//   diag_solve:  the four 16x16 diagonal blocks D_i = (I + A_ii)^-1 by forward
-//                substitution on one wave (lane = one column of one block), in
-//                place in s_A, and rounded into s_Ai;
-//   chain_solve: column block j of the inverse, X_ij = -D_i sum_{k=j}^{i-1} A_ik X_kj
-//                for i = j+1..3, on one wave per j (j = 0, 1, 2); the X_kj stay in
-//                registers as the B operand of the next product, so the three
-//                chains need no barrier between their steps.
-// s_Ai is [t][pcol(t')].
-template <int LDA, int LDT>
-__device__ __forceinline__ void diag_solve(float* s_A, bf16* s_Ai) {
-  const int l = lane_id();
-  const int lg = l >> 4, lc = l & 15;
-  float x[16];
-  float* Xb = s_A + (16 * lg) * LDA + 16 * lg;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    float s = 0.f;
-#pragma unroll
-    for (int r = 0; r < i; ++r) s = fmaf(Xb[i * LDA + r], x[r], s);
-    x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -s);
-  }
-  // same wave: the reads above are complete before these writes
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    Xb[i * LDA + lc] = x[i];
-    s_Ai[(16 * lg + i) * LDT + pcol(16 * lg + lc)] = (bf16)x[i];
-  }
-}
-
-template <int LDA, int LDT>
-__device__ __forceinline__ void chain_solve(const float* s_A, bf16* s_Ai, int j) {
-  const int l = lane_id();
-  const int lg = l >> 4, lc = l & 15;
-  auto blk = [&](int r, int c) { return s_A + (16 * r) * LDA + 16 * c; };
-  f32x4 X[3];                                   // X_{j+1,j}, X_{j+2,j}, X_{j+3,j}
-  for (int i = j + 1; i < 4; ++i) {
-    f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
-    mma16_f32_lds(t, blk(i, j), LDA, blk(j, j), LDA);           // A_ij D_j
-#pragma unroll
-    for (int k = 1; k < 3; ++k)
-      if (j + k < i) mma16_f32_lds_reg(t, blk(i, j + k), LDA, X[k - 1]);   // A_ik X_kj
-    mma16_f32_lds_reg(r, blk(i, i), LDA, t);                       // D_i (...)
-    r = -r;
-#pragma unroll
-    for (int k = 0; k < 3; ++k)
-      if (k == i - j - 1) X[k] = r;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-      s_Ai[(16 * i + 4 * lg + jj) * LDT + pcol(16 * j + lc)] = (bf16)r[jj];
-  }
-}
-
+//   k rows as MFMA operand fragments in registers: lane (lc, lg) of row tile rt
+//   holds k[16 rt + lc][32 ks + 8 lg .. + 7] (rows >= nv read row 0);
+//   A = beta_i exp(gc_i - gc_j) k_i.k_j, i > j (chunk_scaled_dot_kkt.py:57-73),
+//   as ten fp32 16x16 blocks in LDS;
+//   Ai = (I + A)^-1 (solve_tril.py:184-331, fp32 throughout, rounded to bf16
+//   once): the four diagonal blocks by forward substitution (lane = one column
+//   of one block), then X_ij = -D_i sum_{k=j}^{i-1} A_ik X_kj by fp32 MFMA with
+//   the X in registers; Ai staged in LDS and written to the record.
 struct SegPrepArgs {
   const void* k;
   const void* g;
@@ -496,94 +428,185 @@ struct SegPrepArgs {
   unsigned char* rec;         // out [chunks, H] records of kSegRecordBytes (see gdn_kernels.h)
 };
 
-constexpr int NT_PREP = 256;
+// One (chunk, head) item of seg_prep: item = chunk * H + head.
+struct PrepItem {
+  int64_t ci;                 // global chunk index
+  int64_t t0;                 // first token
+  int nv;                     // valid tokens
+  int h;
+};
 
-template <typename TQ, int K>
-__global__ __launch_bounds__(NT_PREP) void seg_prep_kernel(SegPrepArgs a, SegGeom G) {
-  using P = PrepLds<TQ, K>;
-  constexpr int NT = NT_PREP, NW = NT / WAVE;
-  extern __shared__ __align__(16) unsigned char smem[];
-  float* s_A = reinterpret_cast<float*>(smem + P::off_A);
-  bf16* s_Ai = reinterpret_cast<bf16*>(smem + P::off_Ai);
-  float* s_g = reinterpret_cast<float*>(smem + P::off_g);
-  const int h = blockIdx.y;
-  const int H = G.H;
-  const int64_t ci = blockIdx.x;              // global chunk index
+template <bool VARLEN>
+__device__ __forceinline__ PrepItem prep_item(int64_t item, const SegGeom& G) {
+  PrepItem it;
+  it.ci = item / G.H;
+  it.h = (int)(item - it.ci * G.H);
   int64_t bos, eos, c;
-  if (G.cu == nullptr) {
+  if constexpr (!VARLEN) {
     const int64_t nc = (G.T + C - 1) / C;
-    if (ci >= (int64_t)G.N * nc) return;
-    const int64_t n = ci / nc;
-    c = ci - n * nc;
+    const int64_t n = it.ci / nc;
+    c = it.ci - n * nc;
     bos = n * G.T;
     eos = bos + G.T;
   } else {
-    if (ci >= G.chunk_off[G.N]) return;
     int lo = 0, hi = G.N - 1;                 // last n with chunk_off[n] <= ci
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (G.chunk_off[mid] <= ci) lo = mid; else hi = mid - 1;
+      if (G.chunk_off[mid] <= it.ci) lo = mid; else hi = mid - 1;
     }
-    c = ci - G.chunk_off[lo];
+    c = it.ci - G.chunk_off[lo];
     bos = G.cu[lo];
     eos = G.cu[lo + 1];
   }
-  const int64_t t0 = bos + c * C;
-  const int nv = (int)min((int64_t)C, eos - t0);
-  const int tid = threadIdx.x;
-  const int wid = tid / WAVE;
+  it.t0 = bos + c * C;
+  it.nv = (int)min((int64_t)C, eos - it.t0);
+  return it;
+}
 
-  GateRaw gr;
-  load_gates(gr, a.g, a.beta, a.g_dtype, a.beta_dtype, t0, nv, h, H);
-  load_tile<TQ, K, NT>(reinterpret_cast<const TQ*>(a.k) + (t0 * H + h) * K, (uint32_t)(H * K * sizeof(TQ)), nv,
-                       lds_addr(smem) + (uint32_t)P::off_in);
-  // the upper 16x16 blocks of Ai are zero
-  for (int idx = tid; idx < 6 * 256; idx += NT) {
-    const int b = idx >> 8, r = (idx >> 4) & 15, cc = idx & 15;
-    const int bi = b < 3 ? 0 : (b < 5 ? 1 : 2);
-    const int bj = b < 3 ? b + 1 : (b < 5 ? b - 1 : 3);
-    s_Ai[(16 * bi + r) * P::LDT + pcol(16 * bj + cc)] = (bf16)0.f;
-  }
-  wait_loads();
-  const bf16* kt;
-  if constexpr (P::FP8) {
-    convert_fp8<K, NT>(smem + P::off_in, reinterpret_cast<bf16*>(smem + P::off_ck), a.k_scale ? a.k_scale[h] : 1.f,
-                       nv);
-    kt = reinterpret_cast<const bf16*>(smem + P::off_ck);
+// k fragment of row r (already clamped), columns 32 ks + 8 lg .. + 7, as bf16.
+template <typename TQ, int K>
+__device__ __forceinline__ Frag<bf16> k_frag(const TQ* row, int ks, float kscale) {
+  const int lg = lane_id() >> 4;
+  Frag<bf16> f;
+  if constexpr (sizeof(TQ) == 1) {
+    float x[8];
+    load8_in<TQ>(row + 32 * ks + 8 * lg, kscale, x);
+    f = frag_pack(x);
   } else {
-    kt = reinterpret_cast<const bf16*>(smem + P::off_in);
+    f.v = *reinterpret_cast<const bf16x8*>(row + 32 * ks + 8 * lg);
   }
-  unsigned char* rec = a.rec + (ci * H + h) * (int64_t)kSegRecordBytes;
-  if (tid < WAVE) {
-    // the chunk vectors of the record (lane = token)
+  return f;
+}
+
+// Forward substitution of the four diagonal blocks (lane group lg = block,
+// lane column lc): D = (I + A_bb)^-1 replaces A_bb in LDS; x returns column lc
+// of D (rows 0..15) for the bf16 output.
+__device__ __forceinline__ void diag_blocks(float* s_A, float (&x)[16]) {
+  constexpr int LDB = PrepLds::LDB;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  float* Xb = s_A + tri_blk(lg, lg) * PrepLds::BLK;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    float sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < i; ++r) sum = fmaf(Xb[i * LDB + r], x[r], sum);
+    x[i] = (i == lc) ? 1.f : (i < lc ? 0.f : -sum);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) Xb[i * LDB + lc] = x[i];
+}
+
+template <typename TQ, int K, bool VARLEN>
+__global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrepArgs a, SegGeom G) {
+  using P = PrepLds;
+  constexpr int LDB = P::LDB;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int H = G.H;
+  const int64_t n_items = (VARLEN ? (int64_t)G.chunk_off[G.N] : (int64_t)G.N * ((G.T + C - 1) / C)) * H;
+  const int64_t item = (int64_t)blockIdx.x * P::WAVES + wid;
+  if (item >= n_items) return;
+  const PrepItem it = prep_item<VARLEN>(item, G);
+  float* s_A = reinterpret_cast<float*>(smem + wid * P::per_wave + P::off_A);
+  float* s_g = reinterpret_cast<float*>(smem + wid * P::per_wave + P::off_g);
+
+  // gates (lane = token) and the k fragments
+  uint32_t graw = 0u, braw = 0u;
+  if (l < it.nv) {
+    graw = ld_raw(a.g, (it.t0 + l) * H + it.h, a.g_dtype);
+    braw = ld_raw(a.beta, (it.t0 + l) * H + it.h, a.beta_dtype);
+  }
+  const float kscale = (sizeof(TQ) == 1 && a.k_scale) ? a.k_scale[it.h] : 1.f;
+  const TQ* kb = reinterpret_cast<const TQ*>(a.k) + (it.t0 * H + it.h) * K;
+  Frag<bf16> kf[4][K / 32];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const int r = 16 * rt + lc;
+    const TQ* row = kb + (int64_t)(r < it.nv ? r : 0) * H * K;
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) kf[rt][ks] = k_frag<TQ, K>(row, ks, kscale);
+  }
+
+  // chunk vectors of the record (lane = token)
+  unsigned char* rec = a.rec + (it.ci * H + it.h) * (int64_t)kSegRecordBytes;
+  {
+    GateRaw gr;
+    gr.g = graw;
+    gr.b = braw;
     float gl;
-    const float gc = chunk_cumsum(gr, a.g_dtype, nv, gl);
-    const float b = raw_to_f32(gr.b, a.beta_dtype);
+    const float gc = chunk_cumsum(gr, a.g_dtype, it.nv, gl);
+    const float b = raw_to_f32(braw, a.beta_dtype);
     const float eg = gexp(gc);
-    s_g[tid] = gc;
-    s_g[C + tid] = b;
+    s_g[l] = gc;
+    s_g[C + l] = b;
     float* vec = reinterpret_cast<float*>(rec + C * C * 2);
-    vec[tid] = gc;
-    vec[C + tid] = eg * a.scale;
-    vec[2 * C + tid] = b * eg;
-    vec[3 * C + tid] = tid < nv ? gexp(gl - gc) : 0.f;
-    vec[4 * C + tid] = b;
-    vec[5 * C + tid] = gexp(gl);
-    vec[6 * C + tid] = 0.f;
-    vec[7 * C + tid] = 0.f;
+    vec[l] = gc;
+    vec[C + l] = eg * a.scale;
+    vec[2 * C + l] = b * eg;
+    vec[3 * C + l] = l < it.nv ? gexp(gl - gc) : 0.f;
+    vec[4 * C + l] = b;
+    vec[5 * C + l] = gexp(gl);
+    vec[6 * C + l] = 0.f;
+    vec[7 * C + l] = 0.f;
   }
-  lds_barrier();
-  for (int t = wid; t < 10; t += NW) kkt_tile<K, P::LDA>(kt, s_g, s_g + C, s_A, t);
-  lds_barrier();
-  if (wid == 0) diag_solve<P::LDA, P::LDT>(s_A, s_Ai);
-  lds_barrier();
-  if (wid >= 1 && wid <= 3) chain_solve<P::LDA, P::LDT>(s_A, s_Ai, wid - 1);
-  lds_barrier();
+
+  // A: ten 16x16 tiles; lane element (jj): i = 16 tm + 4 lg + jj, j = 16 tn + lc
+#pragma unroll
+  for (int t = 0; t < 10; ++t) {
+    int tm, tn;
+    tri_tile(t, tm, tn);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) mma(acc, kf[tm][ks], kf[tn][ks]);
+    const int i0 = 16 * tm + 4 * lg;
+    const int j = 16 * tn + lc;
+    const f32x4 gi = *reinterpret_cast<const f32x4*>(s_g + i0);
+    const f32x4 bi = *reinterpret_cast<const f32x4*>(s_g + C + i0);
+    const float gj = s_g[j];
+    float* blk = s_A + tri_blk(tm, tn) * P::BLK + (4 * lg) * LDB + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) blk[jj * LDB] = i0 + jj > j ? acc[jj] * gexp(gi[jj] - gj) * bi[jj] : 0.f;
+  }
+
+  // diagonal blocks, then the off-diagonal blocks row block by row block
+  float x[16];
+  diag_blocks(s_A, x);
+  auto blk = [&](int r, int c) { return s_A + tri_blk(r, c) * P::BLK; };
+  f32x4 X[6];                                            // X_ij at index tri_blk(i - 1, j)
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < i; ++j) {
+      f32x4 t = {0.f, 0.f, 0.f, 0.f}, r = {0.f, 0.f, 0.f, 0.f};
+      mma16_f32_lds(t, blk(i, j), LDB, blk(j, j), LDB);                     // A_ij D_j
+#pragma unroll
+      for (int k = j + 1; k < i; ++k) mma16_f32_lds_reg(t, blk(i, k), LDB, X[tri_blk(k - 1, j)]);   // A_ik X_kj
+      mma16_f32_lds_reg(r, blk(i, i), LDB, t);                               // D_i (...)
+      X[tri_blk(i - 1, j)] = -r;
+    }
+  }
+
+  // Ai (bf16, rows in pcol order) staged over the dead block area, then stored
+  bf16* s_Ai = reinterpret_cast<bf16*>(s_A);
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    *reinterpret_cast<uint4*>(s_Ai + 8 * (64 * q + l)) = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s_Ai[(16 * lg + i) * C + pcol(16 * lg + lc)] = (bf16)x[i];
+#pragma unroll
+  for (int i = 1; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < i; ++j)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        s_Ai[(16 * i + 4 * lg + jj) * C + pcol(16 * j + lc)] = (bf16)X[tri_blk(i - 1, j)][jj];
   bf16* dst = reinterpret_cast<bf16*>(rec);
-  for (int u = tid; u < C * C / 8; u += NT) {
-    const int r = u >> 3, c8 = u & 7;
-    *reinterpret_cast<uint4*>(dst + r * C + 8 * c8) = *reinterpret_cast<const uint4*>(s_Ai + r * P::LDT + 8 * c8);
-  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    *reinterpret_cast<uint4*>(dst + 8 * (64 * q + l)) = *reinterpret_cast<const uint4*>(s_Ai + 8 * (64 * q + l));
 }
 
 // ---------------------------------------------------------------------------
@@ -1560,11 +1583,15 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   auto mark = [&](int i) { return p.events == nullptr || hipEventRecord(p.events[i], s) == hipSuccess; };
   if (!mark(0)) return -1;
   if (p.ns_grid > 0 && p.nc_grid > 0) {
-    constexpr size_t lds = PrepLds<TQ, K>::total;
+    constexpr size_t lds = PrepLds::total;
     static_assert(lds <= 64 * 1024, "seg_prep tiles exceed the default LDS limit");
     SegPrepArgs pa{p.k, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, p.scale, static_cast<unsigned char*>(p.Ai)};
-    hipLaunchKernelGGL((seg_prep_kernel<TQ, K>), dim3((unsigned)p.nc_grid, (unsigned)p.H), dim3(NT_PREP), lds, s, pa,
-                       G);
+    const dim3 pgrid((unsigned)((p.nc_grid * p.H + PrepLds::WAVES - 1) / PrepLds::WAVES));
+    const dim3 pblock(PrepLds::WAVES * WAVE);
+    if (p.cu != nullptr)
+      hipLaunchKernelGGL((seg_prep_kernel<TQ, K, true>), pgrid, pblock, lds, s, pa, G);
+    else
+      hipLaunchKernelGGL((seg_prep_kernel<TQ, K, false>), pgrid, pblock, lds, s, pa, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(1)) return -1;
