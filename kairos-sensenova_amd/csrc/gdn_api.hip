@@ -366,12 +366,12 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
   }
   const int64_t nc_grid = chunks_bound(B, T, n_seqs);
   void* Ai = cv.take((size_t)nc_grid * H * kgdn::kSegRecordBytes);
-  float* M = nullptr;
+  uint16_t* M = nullptr;
   float* R = nullptr;
   float* s_init = nullptr;
   if (P.trans || P.combine) {
     const size_t blocks = (size_t)P.ns * H;
-    M = static_cast<float*>(cv.take(blocks * K * K * sizeof(float)));
+    M = static_cast<uint16_t*>(cv.take(blocks * 2 * K * K * sizeof(uint16_t)));
     R = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
     s_init = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
   }

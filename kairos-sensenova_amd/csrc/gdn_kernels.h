@@ -81,8 +81,8 @@ struct FwdOArgs {
 constexpr int kSegRecordBytes = 64 * 64 * 2 + 8 * 64 * 4;
 
 // Segment-parallel fused forward (gdn_seg.hip).  Sequences are cut into
-// segments of L chunks; M, R and s_init are fp32 workspaces of ns_grid * H
-// blocks of K x K, K x V and K x V.
+// segments of L chunks; M is ns_grid * H blocks of K x K as a bf16 pair (hi, lo),
+// R and s_init fp32 workspaces of ns_grid * H blocks of K x V.
 struct SegFwdArgs {
   const void* q;          // [B*T, H, K]  (qk_dtype)
   const void* k;
@@ -103,7 +103,7 @@ struct SegFwdArgs {
   int L;                  // chunks per segment
   int nseg_fixed;         // fixed length: segments per sequence
   int64_t ns_grid;        // number of segments (varlen: an upper bound)
-  float* M;               // [ns_grid, H, K, K]
+  uint16_t* M;            // [ns_grid, H] blocks of K x K bf16 M_hi, then K x K bf16 M_lo (M = M_hi + M_lo)
   float* R;               // [ns_grid, H, K, V]
   float* s_init;          // [ns_grid, H, K, V]
   float scale;

@@ -1287,8 +1287,8 @@ struct SegTransArgs {
   const void* v;
   const float* k_scale;
   const void* Ai;             // [chunks, H] chunk records from seg_prep
-  float* M;                   // [NS, H, K, K]
-  float* R;                   // [NS, H, K, V]
+  uint16_t* M;                // [NS, H] blocks of K x K bf16 M_hi then M_lo
+  float* R;                   // [NS, H] blocks of K x V in accumulator-tile order (see seg_combine)
 };
 
 template <typename TQ, int K, int V>
@@ -1405,35 +1405,46 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
   for (int ct = 0; ct < CT; ++ct) {
     const int c0 = 16 * ctile[ct];
     if (c0 < K) {
-      float* pm = a.M + (s * H + h) * K * K + 4 * lg * K + c0 + lc;
+      // M as the bf16 pair (hi, lo = bf16(M - hi)) that seg_combine multiplies in three bf16 products
+      bf16* ph = reinterpret_cast<bf16*>(a.M) + (s * H + h) * 2 * K * K + 4 * lg * K + c0 + lc;
+      bf16* pl = ph + K * K;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pm[(16 * tt + j) * K] = X[tt][ct][j];
+        for (int j = 0; j < 4; ++j) {
+          const float x = X[tt][ct][j];
+          const bf16 hi = (bf16)x;
+          ph[(16 * tt + j) * K] = hi;
+          pl[(16 * tt + j) * K] = (bf16)(x - (float)hi);
+        }
     } else {
-      float* pr = a.R + (s * H + h) * K * V + 4 * lg * V + c0 - K + lc;
+      // R in accumulator-tile order: tile (row tile tt, column tile cv) is 64 lanes x 4 floats
+      const int cv = (c0 - K) / 16;
+      float* pr = a.R + (s * H + h) * K * V + 4 * l;
 #pragma unroll
-      for (int tt = 0; tt < KT; ++tt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pr[(16 * tt + j) * V] = X[tt][ct][j];
+      for (int tt = 0; tt < KT; ++tt) *reinterpret_cast<f32x4*>(pr + (tt * (V / 16) + cv) * 256) = X[tt][ct];
     }
   }
 }
 
 // ---------------------------------------------------------------------------
 // seg_combine: S_{j+1} = M_j S_j + R_j over the segments of a sequence, 16 V
-// columns per workgroup, fp32 (v_mfma_f32_16x16x4f32).  Also writes
-// final_state of sequences without tokens.
+// columns per workgroup.  Also writes final_state of sequences without tokens.
 //
-// The chain is serial, so each step must cost only its arithmetic: wave w owns
-// output rows 16w .. 16w + 15 and holds its rows of M_j (A operand) and its
-// tile of R_j in registers, loaded one step ahead, while the state columns
-// (B operand, shared by all waves) sit transposed in LDS so that the four K
-// values a lane needs per 16-deep step are one 16-byte read.
+// The chain is serial, so each step must cost only its arithmetic.  M_j and
+// S_j enter as bf16 pairs (x = hi + lo, lo = bf16(x - hi), 16 significant bits)
+// and M_j S_j as hi.hi + hi.lo + lo.hi on v_mfma_f32_16x16x32_bf16 with fp32
+// accumulation onto R_j: the dropped lo.lo term and the split leave a relative
+// error near 2^-17, far below the bf16 rounding of the state snapshot that
+// seg_out applies.  Wave w owns output rows 16w .. 16w + 15 and holds its rows
+// of M_j (A operand) and its tile of R_j in registers, loaded three steps
+// ahead; the state columns (B operand, shared by all waves) sit transposed in
+// LDS, double buffered so that one barrier per step suffices.
 // ---------------------------------------------------------------------------
 struct SegCombineArgs {
-  const float* M;
-  const float* R;
+  const uint16_t* M;          // [NS, H] blocks of K x K bf16 M_hi then M_lo
+  const float* R;             // [NS, H] blocks of K x V: 16x16 tile (rt, ct) at 256 (rt V/16 + ct), lane l's
+                              // elements (rows 16 rt + 4 (l/16) + jj, column 16 ct + l%16) at 4 l + jj
   const void* h0;
   int h0_dtype;
   float* s_init;              // out [NS, H, K, V]
@@ -1443,29 +1454,35 @@ struct SegCombineArgs {
 
 template <int K>
 struct CombineMaps {
-  f32x4 m[K / 16];            // M_j[r0 + lane%16][16 kk + 4 (lane/16) .. +3]
+  Frag<bf16> mh[K / 32];      // M_hi[r0 + lane%16][32 kb + 8 (lane/16) .. +7]
+  Frag<bf16> ml[K / 32];      // M_lo, same positions
   f32x4 r;                    // R_j[r0 + 4 (lane/16) + jj][v0 + lane%16]
 };
 
 template <int K>
-__device__ __forceinline__ void load_maps(CombineMaps<K>& c, const float* M, const float* R, int V, int r0, int v0) {
+__device__ __forceinline__ void load_maps(CombineMaps<K>& c, const bf16* M, const float* R, int V, int r0, int v0) {
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
-  const float* pm = M + (int64_t)(r0 + lc) * K + 4 * lg;
+  const bf16* pm = M + (int64_t)(r0 + lc) * K + 8 * lg;
 #pragma unroll
-  for (int kk = 0; kk < K / 16; ++kk) c.m[kk] = *reinterpret_cast<const f32x4*>(pm + 16 * kk);
-  const float* pr = R + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
-#pragma unroll
-  for (int jj = 0; jj < 4; ++jj) c.r[jj] = pr[(int64_t)jj * V];
+  for (int kb = 0; kb < K / 32; ++kb) {
+    c.mh[kb].v = *reinterpret_cast<const bf16x8*>(pm + 32 * kb);
+    c.ml[kb].v = *reinterpret_cast<const bf16x8*>(pm + K * K + 32 * kb);
+  }
+  c.r = *reinterpret_cast<const f32x4*>(R + ((r0 / 16) * (V / 16) + v0 / 16) * 256 + 4 * l);
 }
 
-template <int K> struct CombCfg { static constexpr int NT = K / 16 * WAVE; };   // one 16-row tile per wave
+template <int K> struct CombCfg {
+  static constexpr int NT = K / 16 * WAVE;                  // one 16-row tile per wave
+  static constexpr int LDS_T = K + 8;                       // row stride (bf16) of a transposed state half
+};
 
 template <int K>
 __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineArgs a, SegGeom G, int total) {
   constexpr int NT = CombCfg<K>::NT;
-  constexpr int LDS_T = K + 4;                              // row stride of the transposed state
-  __shared__ __align__(16) float s_St[16][LDS_T];           // s_St[c][r] = S[r][v0 + c]
+  constexpr int LDS_T = CombCfg<K>::LDS_T;
+  // s_S[buf][half][c][r]: half 0 = bf16 hi, 1 = bf16 lo of S[r][v0 + c]
+  __shared__ __align__(16) bf16 s_S[2][2][16][LDS_T];
   const int V = a.V;
   const int nvt = V / 16;
   // XCD-aware order: the V slices of one head run on one XCD and share M through its L2
@@ -1495,52 +1512,85 @@ __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineA
   // a stage counts only the loads before it.
   constexpr int NST = 3;
   const int nsteps = nseg - 1;
+  const bf16* Mb = reinterpret_cast<const bf16*>(a.M);
   CombineMaps<K> st[NST];
   auto issue = [&](CombineMaps<K>& c, int j) {
     const int64_t s = s_first + max(0, min(j, nsteps - 1));
-    load_maps<K>(c, a.M + (s * H + h) * K * K, a.R + (s * H + h) * K * V, V, r0, v0);
+    load_maps<K>(c, Mb + (s * H + h) * 2 * K * K, a.R + (s * H + h) * K * V, V, r0, v0);
   };
-  if (nsteps > 0) {
-#pragma unroll
-    for (int u = 0; u < NST; ++u) issue(st[u], u);
-  }
-  for (int idx = threadIdx.x; idx < K * 16; idx += NT) {
-    const int r = idx / 16, c = idx % 16;
-    float x = 0.f;
-    if (a.h0) {
-      const int64_t off = (((int64_t)n * H + h) * K + r) * V + v0 + c;
-      x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
-                               : (float)reinterpret_cast<const bf16*>(a.h0)[off];
-    }
-    s_St[c][r] = x;
-  }
   if (nseg == 0) {
     if (a.ht) {
-      __syncthreads();
       for (int idx = threadIdx.x; idx < K * 16; idx += NT) {
         const int r = idx / 16, c = idx % 16;
-        a.ht[(((int64_t)n * H + h) * K + r) * V + v0 + c] = s_St[c][r];
+        const int64_t off = (((int64_t)n * H + h) * K + r) * V + v0 + c;
+        float x = 0.f;
+        if (a.h0)
+          x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
+                                   : (float)reinterpret_cast<const bf16*>(a.h0)[off];
+        a.ht[off] = x;
       }
     }
     return;
   }
+  // S_0 = h0: its loads go out before the maps', so that waiting for them does
+  // not wait for the maps
+  float x0[K * 16 / NT];
+#pragma unroll
+  for (int e = 0; e < K * 16 / NT; ++e) {
+    const int idx = threadIdx.x + NT * e;
+    const int r = idx / 16, c = idx % 16;
+    x0[e] = 0.f;
+    if (a.h0) {
+      const int64_t off = (((int64_t)n * H + h) * K + r) * V + v0 + c;
+      x0[e] = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
+                                   : (float)reinterpret_cast<const bf16*>(a.h0)[off];
+    }
+  }
+  if (nsteps > 0) {
+#pragma unroll
+    for (int u = 0; u < NST; ++u) issue(st[u], u);
+  }
+#pragma unroll
+  for (int e = 0; e < K * 16 / NT; ++e) {
+    const int idx = threadIdx.x + NT * e;
+    const int r = idx / 16, c = idx % 16;
+    const bf16 hi = (bf16)x0[e];
+    s_S[0][0][c][r] = hi;
+    s_S[0][1][c][r] = (bf16)(x0[e] - (float)hi);
+  }
   __syncthreads();
-  for (int j0 = 0; j0 < nsteps; j0 += NST) {
+  for (int j0 = 0; j0 < nsteps; j0 += 2 * NST) {
 #pragma unroll
-    for (int u = 0; u < NST; ++u) {
-      const int j = j0 + u;
+    for (int u2 = 0; u2 < 2 * NST; ++u2) {
+      const int u = u2 % NST, b = u2 & 1;                   // map stage, state buffer (j % 2)
+      const int j = j0 + u2;
       if (j >= nsteps) break;                               // uniform
-      f32x4 acc = st[u].r;
+      Frag<bf16> sh[K / 32], sl[K / 32];
 #pragma unroll
-      for (int kk = 0; kk < K / 16; ++kk) {
-        const f32x4 b = *reinterpret_cast<const f32x4*>(&s_St[lc][16 * kk + 4 * lg]);
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(st[u].m[kk][qq], b[qq], acc, 0, 0, 0);
+      for (int kb = 0; kb < K / 32; ++kb) {
+        sh[kb].v = *reinterpret_cast<const bf16x8*>(&s_S[b][0][lc][32 * kb + 8 * lg]);
+        sl[kb].v = *reinterpret_cast<const bf16x8*>(&s_S[b][1][lc][32 * kb + 8 * lg]);
       }
+      f32x4 acc = st[u].r, acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < K / 32; ++kb) {
+        mma(acc2, st[u].ml[kb], sh[kb]);
+        mma(acc2, st[u].mh[kb], sl[kb]);
+        mma(acc, st[u].mh[kb], sh[kb]);
+      }
+      acc += acc2;
       issue(st[u], j + NST);                                // this stage's registers are free again
-      __syncthreads();
-      *reinterpret_cast<f32x4*>(&s_St[lc][r0 + 4 * lg]) = acc;
+      // S_{j+1}: rows r0 + 4 lg + jj, column lc -> the other buffer, and s_init
+      uint32_t ph[2], pl[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const bf16 h0_ = (bf16)acc[2 * q], h1_ = (bf16)acc[2 * q + 1];
+        ph[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0_) | ((uint32_t)__builtin_bit_cast(uint16_t, h1_) << 16);
+        const bf16 l0_ = (bf16)(acc[2 * q] - (float)h0_), l1_ = (bf16)(acc[2 * q + 1] - (float)h1_);
+        pl[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0_) | ((uint32_t)__builtin_bit_cast(uint16_t, l1_) << 16);
+      }
+      *reinterpret_cast<uint2*>(&s_S[b ^ 1][0][lc][r0 + 4 * lg]) = make_uint2(ph[0], ph[1]);
+      *reinterpret_cast<uint2*>(&s_S[b ^ 1][1][lc][r0 + 4 * lg]) = make_uint2(pl[0], pl[1]);
       float* out = a.s_init + ((s_first + j + 1) * (int64_t)H + h) * K * V + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) out[(int64_t)jj * V] = acc[jj];
