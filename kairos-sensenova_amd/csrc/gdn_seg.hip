@@ -93,6 +93,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   bf16x2_t v = {(bf16)a, (bf16)b};
   return __builtin_bit_cast(uint32_t, v);
 }
+// the same conversion, kept as one packed value: the empty asm hides the
+// packing from the optimizer, which otherwise splits it into one conversion per
+// value when only the rounded values are used, as floats (the conversion
+// itself stays a compiler-generated instruction, under its hazard tracking)
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  uint32_t r = pack_bf16x2(a, b);
+  asm("" : "+v"(r));
+  return r;
+}
 // the two bf16 values packed in a dword, as floats
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -545,7 +554,7 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
     float* vec = reinterpret_cast<float*>(rec + C * C * 2);
     vec[l] = gc;
     vec[C + l] = eg * a.scale;
-    vec[2 * C + l] = b * eg;
+    vec[2 * C + l] = eg;
     vec[3 * C + l] = l < it.nv ? gexp(gl - gc) : 0.f;
     vec[4 * C + l] = b;
     vec[5 * C + l] = gexp(gl);
@@ -590,19 +599,26 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
   }
 
   // Ai (bf16, rows in pcol order) staged over the dead block area, then stored
+  // column c of Ai is scaled by beta_c: u = (Ai diag(beta)) v, w = (Ai diag(beta)) diag(exp(gc)) k
+  float bcol[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) bcol[b] = s_g[C + 16 * b + lc];
   bf16* s_Ai = reinterpret_cast<bf16*>(s_A);
 #pragma unroll
   for (int q = 0; q < 8; ++q)
     *reinterpret_cast<uint4*>(s_Ai + 8 * (64 * q + l)) = make_uint4(0u, 0u, 0u, 0u);
+  float bdiag = bcol[0];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) s_Ai[(16 * lg + i) * C + pcol(16 * lg + lc)] = (bf16)x[i];
+  for (int b = 1; b < 4; ++b) bdiag = lg == b ? bcol[b] : bdiag;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s_Ai[(16 * lg + i) * C + pcol(16 * lg + lc)] = (bf16)(x[i] * bdiag);
 #pragma unroll
   for (int i = 1; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < i; ++j)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
-        s_Ai[(16 * i + 4 * lg + jj) * C + pcol(16 * j + lc)] = (bf16)X[tri_blk(i - 1, j)][jj];
+        s_Ai[(16 * i + 4 * lg + jj) * C + pcol(16 * j + lc)] = (bf16)(X[tri_blk(i - 1, j)][jj] * bcol[j]);
   bf16* dst = reinterpret_cast<bf16*>(rec);
 #pragma unroll
   for (int q = 0; q < 8; ++q)
@@ -618,18 +634,18 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
 //
 // Per chunk (two workgroup barriers):
 //   top      this wave's direct loads of the chunk have landed (q, k, v and
-//            the chunk record: Ai and the chunk vectors gc, exp(gc) scale,
-//            beta exp(gc), the update gate exp(gc_last - gc), beta and
-//            exp(gc_last), formed once by seg_prep).  (fp8: q/k dequantised
-//            after a barrier.)
+//            the chunk record: Ai diag(beta) and the chunk vectors gc,
+//            exp(gc) scale, exp(gc), the update gate exp(gc_last - gc), beta
+//            and exp(gc_last), formed once by seg_prep).  (fp8: q/k
+//            dequantised after a barrier.)
 //   barrier 1; the next chunk's loads go into the other buffer (every wave is
 //            done with the chunk that used it), one direct-load instruction at
 //            a time between the steps of phase A, so that no wave stalls on a
 //            full memory queue.
 //   phase A  [own]    h = bf16(S) as operand fragments; o_inter = q h (seg_out);
-//                     u = Ai bf16(v beta) for the wave's V columns;
+//                     u = (Ai diag(beta)) v for the wave's V columns;
 //            [shared] Aqk'^T tiles (seg_out) and w tiles into LDS.  w is formed
-//                     as (Ai diag(beta exp(gc))) k and stored negated, so that
+//                     as (Ai diag(beta) diag(exp(gc))) k and stored negated, so that
 //                     v' = u - w h is one MFMA accumulation onto u.
 //   barrier 2
 //   phase B  v' = u + (-w) h; o = o_inter exp(gc) scale + Aqk' bf16(v');
@@ -909,13 +925,14 @@ __device__ __forceinline__ Frag<bf16> scale_frag(const Frag<bf16>& f, const floa
 
 // Round the 4 floats of an accumulator tile to bf16 and back (two packed conversions).
 __device__ __forceinline__ f32x4 round4(const f32x4& a) {
-  const uint32_t p0 = pack_bf16x2(a[0], a[1]), p1 = pack_bf16x2(a[2], a[3]);
+  const uint32_t p0 = cvt_pk_bf16(a[0], a[1]), p1 = cvt_pk_bf16(a[2], a[3]);
   return f32x4{bf16_lo(p0), bf16_hi(p0), bf16_lo(p1), bf16_hi(p1)};
 }
 
-// One w unit: token tile tn, d tiles 4 DG .. 4 DG + 3.  B = Ai rows 16 tn + lc
-// scaled by beta exp(gc) (wy_fast.py:67-81, with the scaling moved from k to the
-// columns of Ai), A = k^T; the tile -w^T[d][i] goes to s_w[i][pcol(d)].
+// One w unit: token tile tn, d tiles 4 DG .. 4 DG + 3.  B = rows 16 tn + lc of
+// Ai diag(beta) scaled by exp(gc) (wy_fast.py:67-81, with the k-side scaling
+// beta exp(gc) moved to the columns of Ai), A = k^T; the tile -w^T[d][i] goes
+// to s_w[i][pcol(d)].
 template <typename E, int K, int DG, int P>
 __device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& lo, const float* vec, int tn) {
   const unsigned char* ai = smem + E::ai_tile(P) + 32 * tn * C;
@@ -941,15 +958,14 @@ __device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& l
   }
 }
 
-// u (64 tokens x 16 columns) = Ai bf16(v beta) of the V column tile whose
-// transposed read starts at vtr, rounded to bf16 (wy_fast.py:55-65).
+// u (64 tokens x 16 columns) = (Ai diag(beta)) v of the V column tile whose
+// transposed read starts at vtr, rounded to bf16 (wy_fast.py:55-65, with the
+// v-side scaling by beta moved to the columns of Ai).
 template <typename E, int V, int P>
 __device__ __forceinline__ void u_tile(const unsigned char* smem, const uint32_t (&airow)[2], uint32_t vtr,
                                        const float* vec, f32x4 (&Y)[4]) {
-  Frag<bf16> t0, t1;
-  trT<V, E::v_tile(P)>(vtr, t0, t1);
-  const Frag<bf16> vb0 = scale_frag(t0, vec + 4 * C, 0);
-  const Frag<bf16> vb1 = scale_frag(t1, vec + 4 * C, 1);
+  Frag<bf16> vb0, vb1;
+  trT<V, E::v_tile(P)>(vtr, vb0, vb1);
   const unsigned char* ai = smem + E::ai_tile(P);
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) {
