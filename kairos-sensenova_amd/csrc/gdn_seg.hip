@@ -72,6 +72,7 @@ __device__ __forceinline__ int pcol(int c) {
 }
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lmem_void;
 
@@ -1026,45 +1027,20 @@ __device__ __forceinline__ void gate_frags(const f32x4 (&Y)[4][CT], const float*
   }
 }
 
-// The output tile of a wave (64 tokens x 16 columns, o^T accumulator layout:
-// lane holds 4 consecutive columns of token 16*tn + lane%16) as packed bf16,
-// held until it is stored.
-struct OutPending {
-  uint2 v[4];
-  int64_t t0;
-  int nv;                     // valid tokens; 0 = nothing pending
-  __device__ __forceinline__ void set(int tn, const f32x4& r) {
-    v[tn].x = pack_bf16x2(r[0], r[1]);
-    v[tn].y = pack_bf16x2(r[2], r[3]);
-  }
-  __device__ __forceinline__ void store(bf16* o, int H, int h, int V, int vw) {
-    const int l = lane_id();
-    const int lg = l >> 4, lc = l & 15;
-    unsigned char* base = reinterpret_cast<unsigned char*>(o + (t0 * H + h) * V + vw);
-    const uint32_t row_bytes = (uint32_t)H * V * 2;
-#pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-      const uint32_t t = 16 * tn + lc;
-      if ((int)t < nv) *reinterpret_cast<uint2*>(base + (t * row_bytes + 8 * lg)) = v[tn];
-    }
-    nv = 0;
-  }
-};
-
-// The Aqk' tiles of a wave (seg_out): tile t (tm >= tn, tri_tile order) gives
-// lane i = 16 tm + lc (q side) and j = 16 tn + 4 lg + jj (k side):
-// Aqk'[i][j] = scale exp(gc_i - gc_j) q_i.k_j for i >= j (chunk_o.py:109-118,
-// the output scale folded in), stored bf16 at s_Aqk[i][pcol(j)] -- four
-// consecutive positions, one 8-byte write.
-template <typename E, int K, int P>
-__device__ __forceinline__ void aqk_tile(unsigned char* smem, const LaneOffs<K>& lo, const float* vec, float log2s,
-                                         int t) {
+// One Aqk' tile t (tm >= tn, tri_tile order) of a chunk whose k and q tiles
+// start at kt0 and qt0: lane i = 16 tm + lc (q side) and j = 16 tn + 4 lg + jj
+// (k side): Aqk'[i][j] = scale exp(gc_i - gc_j) q_i.k_j for i >= j
+// (chunk_o.py:109-118, the output scale folded in), stored bf16 at
+// s_Aqk[i][pcol(j)] -- four consecutive positions, one 8-byte write.
+template <int K, int LDQ>
+__device__ __forceinline__ void aqk_tile_at(const unsigned char* kt0, const unsigned char* qt0, unsigned char* s_aqk,
+                                            const LaneOffs<K>& lo, const float* vec, float log2s, int t) {
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
   int tm, tn;
   tri_tile(t, tm, tn);
-  const unsigned char* kt = smem + E::k_tile(P) + 32 * tn * K;
-  const unsigned char* qt = smem + E::q_tile(P) + 32 * tm * K;
+  const unsigned char* kt = kt0 + 32 * tn * K;
+  const unsigned char* qt = qt0 + 32 * tm * K;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < K / 32; ++ks)
@@ -1078,15 +1054,34 @@ __device__ __forceinline__ void aqk_tile(unsigned char* smem, const LaneOffs<K>&
     x[jj] = acc[jj] * __builtin_amdgcn_exp2f(fmaf(gi - gj[jj], 1.4426950408889634f, log2s));
     if (tm == tn && lc < 4 * lg + jj) x[jj] = 0.f;
   }
-  uint2 pk;
-  pk.x = pack_bf16x2(x[0], x[1]);
-  pk.y = pack_bf16x2(x[2], x[3]);
-  *reinterpret_cast<uint2*>(smem + E::off_aqk + lo.aqk + 2 * (16 * tm * E::LDQ + 32 * (tn >> 1) + 4 * (tn & 1))) = pk;
+  *reinterpret_cast<uint2*>(s_aqk + lo.aqk + 2 * (16 * tm * LDQ + 32 * (tn >> 1) + 4 * (tn & 1))) =
+      make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
 }
 
 // ---------------------------------------------------------------------------
-// seg_out: exact recurrence + output over one segment
+// seg_out: exact recurrence + output over one segment, on two kinds of wave
 // ---------------------------------------------------------------------------
+// Only part of a chunk step needs the state S: o_inter = q h, v' = u - w h,
+// o = o_inter exp(gc) scale + Aqk' v', and the update S = exp(gc_last) S +
+// k^T (v' gate).  w, u and Aqk' depend on the chunk's inputs alone.  The
+// consumer waves (one per 16 state columns, NCW = V/16) run the
+// state-dependent part of chunk c and, after it, Aqk' of chunk c + 1; four
+// producer waves meanwhile form w and u of chunk c + 1 in registers, write
+// them to LDS after the mid-step barrier, and stage the inputs of the chunks
+// ahead through registers: the k tile and chunk vectors of chunk c + 2 go to
+// LDS in the first half of the step, q, v and Ai diag(beta) in the second
+// half, each followed by the loads of the same parts of chunk c + 3.
+//
+// Iteration c (c = -1 .. nch - 1), two workgroup barriers:
+//   B1; consumers: h = bf16(S), v' = u + (-w) h, o_inter and o (stored);
+//       producers: k, vectors of chunk c + 2 to LDS (+ loads of chunk c + 3),
+//                  w and u of chunk c + 1 into registers;
+//   B2; consumers: S update with k of chunk c, Aqk' of chunk c + 1;
+//       producers: w, u of chunk c + 1 to LDS, q, v, Ai of chunk c + 2 to LDS
+//                  (+ loads of chunk c + 3).
+// Buffers: q of chunk x in q_tile(x % 2), k in k_tile(x % 3), the chunk
+// vectors in vec_tile(x % 3); v and Ai diag(beta) of chunk c + 1 only (the
+// producers' inputs); w, Aqk' and u of chunk c only.
 struct SegOutArgs {
   const void* q;
   const void* k;
@@ -1103,9 +1098,154 @@ struct SegOutArgs {
 };
 
 template <typename TQ, int K, int V>
-__global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
-  using E = Eng<TQ, K, V, true>;
-  constexpr int NW = E::NW, NT = E::NT, KT = K / 16, KS = K / 32;
+struct OutPlan {
+  static constexpr bool FP8 = sizeof(TQ) == 1;
+  static constexpr int NCW = V / 16;                     // consumer waves 0 .. NCW-1, one per 16 state columns
+  static constexpr int NPW = 4;                          // producer waves NCW .. NCW+3
+  static constexpr int NW = NCW + NPW, NT = NW * WAVE;
+  static constexpr int CTN = 1;                          // 16-column state tiles per consumer
+  static constexpr int KT = K / 16, KS = K / 32, NDG = K / 64;
+  static constexpr int LDW = K + 8;                      // -w rows (pcol order)
+  static constexpr int LDQ = C + 8;                      // Aqk' rows (pcol order)
+  static constexpr int LDU = C + 8;                      // u^T rows (token order)
+  static constexpr uint32_t KB = C * K * 2, VB = C * V * 2, AB = C * C * 2, VECB = 8 * C * 4;
+  // tiles read transposed first (16-bit offset field): k (three buffers), v
+  static constexpr uint32_t k_tile(int b) { return (uint32_t)b * KB; }
+  static constexpr uint32_t v_tile = 3 * KB;
+  static constexpr uint32_t tr_end = v_tile + VB;
+  static_assert(tr_end <= 65536, "transposed-read tiles must lie in the first 64 KB");
+  static constexpr uint32_t q_tile(int b) { return tr_end + (uint32_t)b * KB; }
+  static constexpr uint32_t ai_tile = tr_end + 2 * KB;
+  static constexpr uint32_t vec_tile(int b) { return ai_tile + AB + (uint32_t)b * VECB; }
+  static constexpr uint32_t off_w = vec_tile(3);
+  static constexpr uint32_t off_aqk = off_w + C * LDW * 2;
+  static constexpr uint32_t off_u = off_aqk + C * LDQ * 2;
+  static constexpr uint32_t total = off_u + V * LDU * 2;
+  // staging: units of 8 elements (16 bytes bf16, 8 bytes fp8)
+  static constexpr int PT = NPW * WAVE;                  // producer threads
+  static constexpr int QU = C * K / 8, VU = C * V / 8, RU = kSegRecordBytes / 16, AU = AB / 16;
+};
+
+// The inputs of a chunk on their way to LDS.  Producer threads (NPW waves)
+// hold q and k, consumer threads (NCW waves) hold v and the record, as units of
+// 8 elements (16 bytes bf16, 8 bytes fp8): unit u = thread + threads * i, row
+// u / (cols / 8), 8-column group u % (cols / 8); rows past the chunk end read
+// row 0.  Record units below AU are Ai diag(beta) (swizzled rows), the rest
+// the chunk vectors.
+template <typename TQ, int K, int V>
+struct ChunkSrc {
+  const unsigned char *q, *k, *v, *rec;
+  int nv;
+  __device__ __forceinline__ ChunkSrc(const SegOutArgs& a, int64_t t0, int nv_, int h, int H, const unsigned char* r)
+      : q(reinterpret_cast<const unsigned char*>(a.q) + (t0 * H + h) * K * sizeof(TQ)),
+        k(reinterpret_cast<const unsigned char*>(a.k) + (t0 * H + h) * K * sizeof(TQ)),
+        v(reinterpret_cast<const unsigned char*>(a.v) + (t0 * H + h) * V * 2),
+        rec(r),
+        nv(nv_) {}
+};
+
+template <typename TQ, int K, int V>
+struct ProdStage {
+  using P = OutPlan<TQ, K, V>;
+  using QT = typename std::conditional<P::FP8, u32x2, u32x4>::type;
+  static constexpr int N = P::QU / P::PT;
+  static_assert(P::QU % P::PT == 0, "q/k units split evenly over the producer threads");
+  QT q[N], k[N];
+  __device__ __forceinline__ static uint32_t src_off(int i, int nv, int H) {
+    const int u = (int)threadIdx.x - P::NCW * WAVE + P::PT * i;
+    const int r = u / (K / 8), c8 = u % (K / 8);
+    return (uint32_t)(r < nv ? r : 0) * (uint32_t)(H * K * sizeof(TQ)) + (uint32_t)(c8 * 8 * sizeof(TQ));
+  }
+  __device__ __forceinline__ static uint32_t dst_off(int i) {
+    const int u = (int)threadIdx.x - P::NCW * WAVE + P::PT * i;
+    return 2 * Tile<K>::off(u / (K / 8), u % (K / 8));
+  }
+  __device__ __forceinline__ static u32x4 to_bf16(const QT& x, float scale) {
+    if constexpr (P::FP8) {
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[e] = fp8e4m3_to_f32((x[0] >> (8 * e)) & 0xFF) * scale;
+        f[4 + e] = fp8e4m3_to_f32((x[1] >> (8 * e)) & 0xFF) * scale;
+      }
+      return __builtin_bit_cast(u32x4, frag_pack(f).v);
+    } else {
+      return x;
+    }
+  }
+  __device__ __forceinline__ void load_k(const ChunkSrc<TQ, K, V>& s, int H) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) k[i] = *reinterpret_cast<const QT*>(s.k + src_off(i, s.nv, H));
+  }
+  __device__ __forceinline__ void load_q(const ChunkSrc<TQ, K, V>& s, int H) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = *reinterpret_cast<const QT*>(s.q + src_off(i, s.nv, H));
+  }
+  __device__ __forceinline__ void store_k(unsigned char* smem, int kb, float ks) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) *reinterpret_cast<u32x4*>(smem + P::k_tile(kb) + dst_off(i)) = to_bf16(k[i], ks);
+  }
+  __device__ __forceinline__ void store_q(unsigned char* smem, int qb, float qs) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) *reinterpret_cast<u32x4*>(smem + P::q_tile(qb) + dst_off(i)) = to_bf16(q[i], qs);
+  }
+};
+
+template <typename TQ, int K, int V>
+struct ConsStage {
+  using P = OutPlan<TQ, K, V>;
+  static constexpr int CTH = P::NCW * WAVE;              // consumer threads
+  static constexpr int NV = P::VU / CTH, NR = (P::RU + CTH - 1) / CTH;
+  static_assert(P::VU % CTH == 0 && P::AU % WAVE == 0 && P::RU % WAVE == 0, "units split per wave");
+  u32x4 v[NV], r[NR];
+  __device__ __forceinline__ void load(const ChunkSrc<TQ, K, V>& s, int H) {
+    const int ct = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int u = ct + CTH * i;
+      const int row = u / (V / 8), c8 = u % (V / 8);
+      v[i] = *reinterpret_cast<const u32x4*>(s.v + (uint32_t)(row < s.nv ? row : 0) * (uint32_t)(H * V * 2) +
+                                             (uint32_t)(c8 * 16));
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) r[i] = *reinterpret_cast<const u32x4*>(s.rec + 16 * min(ct + CTH * i, P::RU - 1));
+  }
+  __device__ __forceinline__ void store(unsigned char* smem, int cb) const {
+    const int ct = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int u = ct + CTH * i;
+      *reinterpret_cast<u32x4*>(smem + P::v_tile + 2 * Tile<V>::off(u / (V / 8), u % (V / 8))) = v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int u = ct + CTH * i;                        // uniform per wave against AU and RU
+      if (u < P::AU) {
+        const int row = u / 8, pos = u % 8;
+        *reinterpret_cast<u32x4*>(smem + P::ai_tile + (uint32_t)(row * C * 2 + 16 * (pos ^ Tile<C>::swz(row)))) = r[i];
+      } else if (u < P::RU) {
+        *reinterpret_cast<u32x4*>(smem + P::vec_tile(cb) + 16 * (uint32_t)(u - P::AU)) = r[i];
+      }
+    }
+  }
+};
+
+// The state-independent products of one chunk that the producer waves form,
+// held from their computation until the mid-step barrier: w units (u = pw +
+// 4 i: token tile u / NDG, d group u % NDG) and u column tiles (ct = pw + 4 i),
+// each as packed bf16.
+template <int K, int V>
+struct OutProducts {
+  static constexpr int NWU = (4 * (K / 64) + 3) / 4, NU = (V / 16 + 3) / 4;
+  uint2 w[NWU][4];
+  uint2 u[NU][4];
+};
+
+template <typename TQ, int K, int V>
+__global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
+  using P = OutPlan<TQ, K, V>;
+  constexpr int KT = P::KT, KS = P::KS, CTN = P::CTN, NDG = P::NDG;
+  constexpr int LDW = P::LDW, LDQ = P::LDQ, LDU = P::LDU;
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int h = blockIdx.y;
@@ -1113,185 +1253,326 @@ __global__ __launch_bounds__((Eng<TQ, K, V, true>::NT)) void seg_out_kernel(SegO
   const SegLoc sl = locate_seg(blockIdx.x, G);
   if (!sl.ok) return;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const bool consumer = wid < P::NCW;
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
-  const int vw = wid * 16;              // first V column of this wave
+  const uint32_t lds0 = lds_addr(smem);
   const float qs = a.q_scale ? a.q_scale[h] : 1.f;
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
   const float log2s = __builtin_amdgcn_logf(a.scale);
-  const uint32_t lds0 = lds_addr(smem);
+  const int64_t t_seg = sl.bos + sl.c0 * C;                 // first token of the segment
+  const unsigned char* rec0 = reinterpret_cast<const unsigned char*>(a.Ai) +
+                              ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
+  const int64_t rec_step = (int64_t)H * kSegRecordBytes;
+  auto chunk_nv = [&](int c) { return (int)min((int64_t)C, sl.eos - (t_seg + (int64_t)c * C)); };
 
-  // ---- initial state of the segment (lane element (tt, j): row 16*tt + 4*lg + j, column vw + lc)
-  f32x4 S[KT][1];
+  LaneOffs<K> lo;
+  lane_offsets<K, LDW, LDQ>(lo, lds0);
+  // Upper 16x16 tiles of Aqk' that operand fragments read (column tile 2 ks + 1
+  // of row tile 2 ks) are zero; no chunk writes them.
   {
+    bf16* s_aqk = reinterpret_cast<bf16*>(smem + P::off_aqk);
+    for (int idx = threadIdx.x; idx < 2 * 16 * 16; idx += P::NT) {
+      const int tile = idx >> 8, r = (idx >> 4) & 15, c = idx & 15;
+      s_aqk[(32 * tile + r) * LDQ + pcol(32 * tile + 16 + c)] = (bf16)0.f;
+    }
+  }
+
+  // consumer state: lane element (tt, ct, j) = S[16 tt + 4 lg + j][vw + 16 ct + lc]
+  const int vw = wid * 16;
+  f32x4 S[KT][CTN];
+  using SRC = ChunkSrc<TQ, K, V>;
+  bf16* o = reinterpret_cast<bf16*>(a.o);
+  if (consumer) {
+    ConsStage<TQ, K, V> cs;
     const int lane_off = 4 * lg * V + vw + lc;
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int ct = 0; ct < CTN; ++ct) S[tt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (sl.j == 0 && a.h0 && a.h0_dtype == DT_F32) {
       const float* p = reinterpret_cast<const float*>(a.h0) + ((int64_t)sl.n * H + h) * K * V + lane_off;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[tt][0][j] = p[(16 * tt + j) * V];
+        for (int ct = 0; ct < CTN; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[tt][ct][j] = p[(16 * tt + j) * V + 16 * ct];
     } else if (sl.j == 0 && a.h0) {
       const bf16* p = reinterpret_cast<const bf16*>(a.h0) + ((int64_t)sl.n * H + h) * K * V + lane_off;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[tt][0][j] = (float)p[(16 * tt + j) * V];
+        for (int ct = 0; ct < CTN; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) S[tt][ct][j] = (float)p[(16 * tt + j) * V + 16 * ct];
     } else if (sl.j > 0) {
       const float* p = a.s_init + ((int64_t)blockIdx.x * H + h) * K * V + lane_off;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S[tt][0][j] = p[(16 * tt + j) * V];
-    } else {
+        for (int ct = 0; ct < CTN; ++ct)
 #pragma unroll
-      for (int tt = 0; tt < KT; ++tt) S[tt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int j = 0; j < 4; ++j) S[tt][ct][j] = p[(16 * tt + j) * V + 16 * ct];
     }
-  }
-  // Upper 16x16 tiles of Aqk' that operand fragments read (column tile 2 ks + 1
-  // of row tile 2 ks) are zero; no chunk writes them.
-  {
-    bf16* s_aqk = reinterpret_cast<bf16*>(smem + E::off_aqk);
-    for (int idx = threadIdx.x; idx < 2 * 16 * 16; idx += NT) {
-      const int tile = idx >> 8, r = (idx >> 4) & 15, c = idx & 15;
-      s_aqk[(32 * tile + r) * E::LDQ + pcol(32 * tile + 16 + c)] = (bf16)0.f;
-    }
-  }
-  LaneOffs<K> lo;
-  lane_offsets<K, E::LDW, E::LDQ>(lo, lds0);
-  const uint32_t vtr = tr_lane_addr<V>(lds0, wid);
-  ChunkLoads<TQ, K, V, true> LD;
-  LD.init(H);
-
-  int64_t t0 = sl.bos + sl.c0 * C;
-  int nv = (int)min((int64_t)C, sl.eos - t0);
-  const unsigned char* rec = reinterpret_cast<const unsigned char*>(a.Ai) +
-                             ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
-  const int64_t rec_step = (int64_t)H * kSegRecordBytes;
-  LD.template slots_from<0, 0>(lds0, a.q, a.k, a.v, t0, nv, h, H, rec);
-  bf16* o = reinterpret_cast<bf16*>(a.o);
-  OutPending op;
-  op.nv = 0;
-
-  auto step = [&](auto PP, int ci) {
-    constexpr int P = decltype(PP)::value;
-    wait_loads();
-    op.store(o, H, h, V, vw);            // the previous chunk's output
-    const int64_t t0c = t0;
-    const int nvc = nv;
-    const float* vec = reinterpret_cast<const float*>(smem + E::vec_tile(P));
-    if constexpr (E::FP8) {
-      lds_barrier();                     // every wave is done with the previous chunk's q/k tiles
-      convert_fp8<K, NT>(smem + E::qraw(P), reinterpret_cast<bf16*>(smem + E::q_tile(P)), qs, nvc);
-      convert_fp8<K, NT>(smem + E::kraw(P), reinterpret_cast<bf16*>(smem + E::k_tile(P)), ks_, nvc);
-    }
-    lds_barrier();                       // barrier 1: the chunk's tiles are complete
-    const float gamma = vec[5 * C];      // exp(gc_last)
-    // the next chunk's loads go into the other buffer, one slot at a time
-    const bool more = ci + 1 < sl.nch;
-    if (more) {
-      t0 += C;
-      nv = (int)min((int64_t)C, sl.eos - t0);
-      rec += rec_step;
-    }
-    auto slot = [&](auto SS) {
-      if (more) LD.template slot<1 - P, decltype(SS)::value>(lds0, a.q, a.k, a.v, t0, nv, h, H, rec);
-    };
-    auto slots_from = [&](auto SS) {
-      if (more) LD.template slots_from<1 - P, decltype(SS)::value>(lds0, a.q, a.k, a.v, t0, nv, h, H, rec);
-    };
-    slot(std::integral_constant<int, 0>{});
-
-    // ---- phase A
-    Frag<bf16> hb[KS][1];                // h = S rounded (chunk_delta_h.py:129-139)
+    cs.load(SRC(a, t_seg, chunk_nv(0), h, H, rec0), H);
+    cs.store(smem, 0);
+    if (sl.nch > 1) cs.load(SRC(a, t_seg + C, chunk_nv(1), h, H, rec0 + rec_step), H);
+    lds_barrier();
+    for (int c = -1; c < sl.nch; ++c) {
+      // ---------------- B1 .. B2: h, o_inter, v', o of chunk c
+      f32x4 Y[4][CTN];
+      if (c >= 0) {
+        const int qb = c & 1;
+        const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(c % 3));
+        const int nvc = chunk_nv(c);
+        Frag<bf16> hb[KS][CTN];                          // h = S rounded (chunk_delta_h.py:129-139)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) hb[ks][0] = acc_frag(S[2 * ks][0], S[2 * ks + 1][0]);
-    f32x4 oi[4];                         // o_inter^T = h^T q^T (chunk_o.py:84-107)
-    {
-      const unsigned char* qt = smem + E::q_tile(P);
+        for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        oi[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int ct = 0; ct < CTN; ++ct) hb[ks][ct] = acc_frag(S[2 * ks][ct], S[2 * ks + 1][ct]);
+        // v' = u + (-w) h                               (chunk_delta_h.py:141-157)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const uint2 pa = *reinterpret_cast<const uint2*>(qt + 32 * tn * K + lo.qacc[ks][0]);
-          const uint2 pb = *reinterpret_cast<const uint2*>(qt + 32 * tn * K + lo.qacc[ks][1]);
-          Frag<bf16> b;
-          b.v = __builtin_bit_cast(bf16x8, make_uint4(pa.x, pa.y, pb.x, pb.y));
-          mma(oi[tn], hb[ks][0], b);
+        for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+          for (int ct = 0; ct < CTN; ++ct) {
+            const uint2 uu = *reinterpret_cast<const uint2*>(
+                smem + P::off_u + 2 * ((vw + 16 * ct + lc) * LDU + 16 * tm + 4 * lg));
+            Y[tm][ct] = f32x4{bf16_lo(uu.x), bf16_hi(uu.x), bf16_lo(uu.y), bf16_hi(uu.y)};
+          }
+        {
+          const unsigned char* wt = smem + P::off_w + lo.w;
+#pragma unroll
+          for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              const Frag<bf16> wa = frag_at<bf16>(reinterpret_cast<const bf16*>(wt + 32 * tm * LDW + 64 * ks));
+#pragma unroll
+              for (int ct = 0; ct < CTN; ++ct) mma(Y[tm][ct], wa, hb[ks][ct]);
+            }
         }
-        if (tn == 1) slot(std::integral_constant<int, 1>{});
-        if (tn == 3) slot(std::integral_constant<int, 2>{});
-      }
-    }
-    if constexpr (NW == 8) {
-      if (wid < 4) {
-        aqk_tile<E, K, P>(smem, lo, vec, log2s, 2 * wid);
-        aqk_tile<E, K, P>(smem, lo, vec, log2s, 2 * wid + 1);
-      } else if (wid < 6) {
-        aqk_tile<E, K, P>(smem, lo, vec, log2s, wid + 4);
-      }
-    } else {
-      for (int t = wid; t < 10; t += NW) aqk_tile<E, K, P>(smem, lo, vec, log2s, t);
-    }
-    slot(std::integral_constant<int, 3>{});
-    for (int u = wid; u < 4 * E::NDG; u += NW) {
-      if constexpr (E::NDG == 2) {
-        if (u & 1) w_unit<E, K, 1, P>(smem, lo, vec, u >> 1);
-        else w_unit<E, K, 0, P>(smem, lo, vec, u >> 1);
-      } else {
-        w_unit<E, K, 0, P>(smem, lo, vec, u);
-      }
-    }
-    slot(std::integral_constant<int, 4>{});
-    slot(std::integral_constant<int, 5>{});
-    f32x4 Y[4][1];
-    {
-      f32x4 u4[4];
-      u_tile<E, V, P>(smem, lo.airow, vtr, vec, u4);
-#pragma unroll
-      for (int tm = 0; tm < 4; ++tm) Y[tm][0] = u4[tm];
-    }
-    slot(std::integral_constant<int, 6>{});
-    slots_from(std::integral_constant<int, 7>{});
-    lds_barrier();                       // barrier 2: w and Aqk' complete
-
-    // ---- phase B: v' = u - w h                       (chunk_delta_h.py:141-157)
-    add_wx<E, K, 1>(smem, lo.w, hb, Y);
-    // ---- o^T = o_inter^T exp(gc) scale + v_new^T Aqk'^T  (chunk_o.py:84-128)
-    {
-      Frag<bf16> vn[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) vn[ks] = acc_frag(Y[2 * ks][0], Y[2 * ks + 1][0]);
-      const unsigned char* aq = smem + E::off_aqk + lo.aqk;
-#pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        f32x4 r = oi[tn] * vec[C + 16 * tn + lc];
+        // o^T = o_inter^T exp(gc) scale + v'^T Aqk'^T  (chunk_o.py:84-128), with
+        // o_inter^T = h^T q^T (chunk_o.py:84-107)
+        Frag<bf16> vn[2][CTN];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-          if (ks <= tn / 2) mma(r, vn[ks], frag_at<bf16>(reinterpret_cast<const bf16*>(aq + 32 * tn * E::LDQ + 64 * ks)));
-        op.set(tn, r);
+#pragma unroll
+          for (int ct = 0; ct < CTN; ++ct) vn[ks][ct] = acc_frag(Y[2 * ks][ct], Y[2 * ks + 1][ct]);
+        const unsigned char* qt = smem + P::q_tile(qb);
+        const unsigned char* aq = smem + P::off_aqk + lo.aqk;
+        // o_inter^T of the four token tiles (independent accumulation chains)
+        f32x4 oi[4][CTN];
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+          for (int ct = 0; ct < CTN; ++ct) oi[tn][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int tn = 0; tn < 4; ++tn) {
+            const uint2 pa = *reinterpret_cast<const uint2*>(qt + 32 * tn * K + lo.qacc[ks][0]);
+            const uint2 pb = *reinterpret_cast<const uint2*>(qt + 32 * tn * K + lo.qacc[ks][1]);
+            Frag<bf16> b;
+            b.v = __builtin_bit_cast(bf16x8, make_uint4(pa.x, pa.y, pb.x, pb.y));
+#pragma unroll
+            for (int ct = 0; ct < CTN; ++ct) mma(oi[tn][ct], hb[ks][ct], b);
+          }
+        uint2 ov[4][CTN];
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+          const float es = vec[C + 16 * tn + lc];
+#pragma unroll
+          for (int ct = 0; ct < CTN; ++ct) {
+            f32x4 r = oi[tn][ct] * es;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+              if (ks <= tn / 2)
+                mma(r, vn[ks][ct], frag_at<bf16>(reinterpret_cast<const bf16*>(aq + 32 * tn * LDQ + 64 * ks)));
+            ov[tn][ct] = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+          }
+        }
+        // store o (token 16 tn + lc, columns vw + 16 ct + 4 lg .. +3)
+        unsigned char* ob = reinterpret_cast<unsigned char*>(o + ((t_seg + (int64_t)c * C) * H + h) * V + vw) +
+                            8 * lg;
+        const uint32_t row_bytes = (uint32_t)H * V * 2;
+        if (nvc == C) {
+#pragma unroll
+          for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+            for (int ct = 0; ct < CTN; ++ct)
+              *reinterpret_cast<uint2*>(ob + ((16 * tn + lc) * row_bytes + 32 * ct)) = ov[tn][ct];
+        } else {
+#pragma unroll
+          for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+            for (int ct = 0; ct < CTN; ++ct)
+              if (16 * tn + lc < nvc) *reinterpret_cast<uint2*>(ob + ((16 * tn + lc) * row_bytes + 32 * ct)) = ov[tn][ct];
+        }
       }
-      op.t0 = t0c;
-      op.nv = nvc;
+      lds_barrier();                                     // B2
+      // ---------------- B2 .. B1: state update with chunk c
+      if (c >= 0) {
+        // S = exp(gc_last) S + k^T (v' exp(gc_last - gc))   (chunk_delta_h.py:163-211)
+        const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(c % 3));
+        const float gamma = vec[5 * C];
+        Frag<bf16> vg[2][CTN];
+        gate_frags<CTN>(Y, vec + 3 * C, vg);
+        const uint32_t kbo = P::k_tile(c % 3);
+#pragma unroll
+        for (int tq = 0; tq < KT; tq += 4) {
+          Frag<bf16> kf[4][2];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tr4<0, 32 * K, 64 * K, 96 * K>(lo.ktr[tq + e] + kbo, kf[e][0], kf[e][1]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int ct = 0; ct < CTN; ++ct) {
+              S[tq + e][ct] *= gamma;
+              mma(S[tq + e][ct], kf[e][0], vg[0][ct]);
+              mma(S[tq + e][ct], kf[e][1], vg[1][ct]);
+            }
+        }
+      }
+      // Aqk' of chunk c + 1 (its q and k arrived in the previous step; chunk c's
+      // Aqk' was last read before B2): tiles wid, wid + NCW, ... (< 10)
+      if (c + 1 < sl.nch) {
+        const int cn = c + 1;
+        const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(cn % 3));
+#pragma unroll
+        for (int i = 0; i < (10 + P::NCW - 1) / P::NCW; ++i) {
+          const int t = wid + P::NCW * i;
+          if (t < 10) aqk_tile_at<K, LDQ>(smem + P::k_tile(cn % 3), smem + P::q_tile(cn & 1), smem + P::off_aqk, lo, vec,
+                                          log2s, t);
+        }
+      }
+      // v, Ai diag(beta) and the vectors of chunk c + 2 (the producers are done
+      // with those of chunk c + 1), then the loads of chunk c + 3
+      if (c + 2 < sl.nch) {
+        cs.store(smem, (c + 2) % 3);
+        if (c + 3 < sl.nch) cs.load(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0 + (c + 3) * rec_step), H);
+      }
+      lds_barrier();                                     // B1
     }
-    // ---- S = exp(g_last) S + k^T (v' exp(g_last - gc))   (chunk_delta_h.py:163-211)
-    Frag<bf16> vg[2][1];
-    gate_frags<1>(Y, vec + 3 * C, vg);
-    update_state<E, K, 1, P>(lo, vg, gamma, S);
-  };
-  for (int ci = 0; ci < sl.nch; ci += 2) {
-    step(std::integral_constant<int, 0>{}, ci);
-    if (ci + 1 < sl.nch) step(std::integral_constant<int, 1>{}, ci + 1);
+  } else {
+    ProdStage<TQ, K, V> ps;
+    const SRC s0(a, t_seg, chunk_nv(0), h, H, rec0);
+    ps.load_q(s0, H);
+    ps.load_k(s0, H);
+    ps.store_q(smem, 0, qs);
+    ps.store_k(smem, 0, ks_);
+    if (sl.nch > 1) {
+      const SRC s1(a, t_seg + C, chunk_nv(1), h, H, rec0 + rec_step);
+      ps.load_q(s1, H);
+      ps.load_k(s1, H);
+    }
+    lds_barrier();
+    const int pw = wid - P::NCW;
+    OutProducts<K, V> pr;
+    for (int c = -1; c < sl.nch; ++c) {
+      // ---------------- B1 .. B2
+      // producers: w and u of chunk c + 1; k of chunk c + 2 goes to a buffer
+      // free in this half, then the loads of k of chunk c + 3
+      if (c + 2 < sl.nch) {
+        ps.store_k(smem, (c + 2) % 3, ks_);
+        if (c + 3 < sl.nch) ps.load_k(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
+      }
+      if (c + 1 < sl.nch) {
+      const int cn = c + 1;
+      const int kb = cn % 3;
+      const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(cn % 3));
+      auto issue = [&](auto) {
+        __builtin_amdgcn_sched_barrier(0);               // one product at a time: bounded live registers
+      };
+      // -w (token tile tn, d tiles 4 dg .. +3) = -(Ai diag(beta) diag(exp(gc))) k  (wy_fast.py:67-81)
+      auto w_item = [&](auto I) {
+        constexpr int i = decltype(I)::value;
+        if constexpr (i >= OutProducts<K, V>::NWU) return;
+        const int u = pw + 4 * i;
+        if (u < 4 * NDG) {
+          const int tn = u / NDG, dg = u % NDG;
+          const unsigned char* ai = smem + P::ai_tile + 32 * tn * C;
+          const Frag<bf16> b0 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0])), vec + 2 * C, 0);
+          const Frag<bf16> b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
+#pragma unroll
+          for (int dd = 0; dd < 4; ++dd) {
+            const uint32_t ka = (NDG == 2 && dg ? lo.ktr[4 + dd] : lo.ktr[dd]) + P::k_tile(kb);
+            Frag<bf16> k0, k1;
+            tr4<0, 32 * K, 64 * K, 96 * K>(ka, k0, k1);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            mma(acc, k0, b0);
+            if (tn >= 2) mma(acc, k1, b1);
+            pr.w[i][dd] = make_uint2(pack_bf16x2(-acc[0], -acc[1]), pack_bf16x2(-acc[2], -acc[3]));
+          }
+        }
+      };
+      // u (column tile ctu) = (Ai diag(beta)) v     (wy_fast.py:55-65)
+      auto u_item = [&](auto I) {
+        constexpr int i = decltype(I)::value;
+        if constexpr (i >= OutProducts<K, V>::NU) return;
+        const int ctu = pw + 4 * i;
+        if (ctu < V / 16) {
+          Frag<bf16> vb0, vb1;
+          tr4<0, 32 * V, 64 * V, 96 * V>(tr_lane_addr<V>(lds0, ctu) + P::v_tile, vb0, vb1);
+          const unsigned char* ai = smem + P::ai_tile;
+#pragma unroll
+          for (int tm = 0; tm < 4; ++tm) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + lo.airow[0])), vb0);
+            if (tm >= 2) mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + lo.airow[1])), vb1);
+            pr.u[i][tm] = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+          }
+        }
+      };
+      w_item(std::integral_constant<int, 0>{});
+      issue(0);
+      w_item(std::integral_constant<int, 1>{});
+      issue(0);
+      u_item(std::integral_constant<int, 0>{});
+      issue(0);
+      u_item(std::integral_constant<int, 1>{});
+      issue(0);
+      }
+      lds_barrier();                                     // B2
+      // ---------------- B2 .. B1: w, u of chunk c + 1 and q of chunk c + 2 to LDS
+      if (c + 1 < sl.nch) {
+#pragma unroll
+        for (int i = 0; i < OutProducts<K, V>::NWU; ++i) {
+          const int u = pw + 4 * i;
+          if (u < 4 * NDG) {
+            const int tn = u / NDG, dg = u % NDG;
+            unsigned char* wt = smem + P::off_w + lo.w + 32 * tn * LDW;
+#pragma unroll
+            for (int dd = 0; dd < 4; ++dd) {
+              const int dt = 4 * dg + dd;
+              *reinterpret_cast<uint2*>(wt + 2 * (32 * (dt >> 1) + 4 * (dt & 1))) = pr.w[i][dd];
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < OutProducts<K, V>::NU; ++i) {
+          const int ctu = pw + 4 * i;
+          if (ctu < V / 16) {
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm)
+              *reinterpret_cast<uint2*>(smem + P::off_u + 2 * ((16 * ctu + lc) * LDU + 16 * tm + 4 * lg)) = pr.u[i][tm];
+          }
+        }
+      }
+      if (c + 2 < sl.nch) {
+        ps.store_q(smem, (c + 2) & 1, qs);
+        if (c + 3 < sl.nch) ps.load_q(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
+      }
+      lds_barrier();                                     // B1
+    }
   }
-  op.store(o, H, h, V, vw);
-
-  if (a.ht && sl.j == sl.nseg - 1) {
+  if (consumer && a.ht && sl.j == sl.nseg - 1) {
     float* p = a.ht + ((int64_t)sl.n * H + h) * K * V + 4 * lg * V + vw + lc;
 #pragma unroll
     for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) p[(16 * tt + j) * V] = S[tt][0][j];
+      for (int ct = 0; ct < CTN; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * V + 16 * ct] = S[tt][ct][j];
   }
 }
 
@@ -1679,12 +1960,12 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   }
   if (!mark(3)) return -1;
   if (p.ns_grid > 0) {
-    constexpr size_t lds = Eng<TQ, K, V, true>::total;
+    constexpr size_t lds = OutPlan<TQ, K, V>::total;
     auto ko = seg_out_kernel<TQ, K, V>;
     if (set_lds(ko, lds)) return -1;
     SegOutArgs oa{p.q, p.k, p.v, p.q_scale, p.k_scale,
                   p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht};
-    hipLaunchKernelGGL(ko, grid, dim3(Eng<TQ, K, V, true>::NT), lds, s, oa, G);
+    hipLaunchKernelGGL(ko, grid, dim3(OutPlan<TQ, K, V>::NT), lds, s, oa, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(4)) return -1;
