@@ -1725,6 +1725,253 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
 }
 
 // ---------------------------------------------------------------------------
+// seg_trans for bf16 q/k: software-pipelined chunk steps, one barrier per chunk
+// ---------------------------------------------------------------------------
+// Each wave owns two 16-column tiles of [M | R] as in the chunk engine, but the
+// state-independent half of a step runs one chunk ahead: in the step of chunk
+// c every wave forms its w unit and its u tiles of chunk c + 1 (w into the
+// other of two w tiles, u in registers) between the MFMA of chunk c's update,
+// so one barrier per chunk publishes w and the inputs of the next chunk, and
+// the state chain's MFMA and the w/u work fill each other's latency.  The
+// chunk inputs are triple buffered (chunk c: update; c + 1: w, u; c + 2:
+// direct loads in flight).  The w tile has no padding: its 16-byte chunks are
+// swizzled like the input tiles (Tile<K>), so the lane offsets of a K row
+// fragment (krow) address it.
+template <int K, int V>
+struct TransPlan {
+  static constexpr int NW = (K + V) / 32, NT = NW * WAVE, CT = 2;
+  static constexpr int KT = K / 16, KS = K / 32, NDG = K / 64;
+  static constexpr uint32_t KB = C * K * 2, VB = C * V * 2, RB = kSegRecordBytes, AB = C * C * 2;
+  static constexpr uint32_t k_tile(int b) { return (uint32_t)b * KB; }
+  static constexpr uint32_t v_tile(int b) { return 3 * KB + (uint32_t)b * VB; }
+  static constexpr uint32_t ai_tile(int b) { return 3 * KB + 3 * VB + (uint32_t)b * RB; }
+  static constexpr uint32_t vec_tile(int b) { return ai_tile(b) + AB; }
+  static constexpr uint32_t w_tile(int b) { return 3 * KB + 3 * VB + 3 * RB + (uint32_t)b * KB; }
+  static constexpr uint32_t total = w_tile(2);
+  static_assert(3 * KB <= 65536, "the k tiles are read transposed with 16-bit offsets from one lane address");
+};
+
+// The direct loads of one chunk (k, v, record) into buffer b of a TransPlan.
+template <int K, int V>
+struct TransLoads {
+  using P = TransPlan<K, V>;
+  LoadOffs<bf16, K, P::NT> ko;
+  LoadOffs<bf16, V, P::NT> vo;
+  RecOffs<P::NT> ro;
+  __device__ __forceinline__ void init(int H) {
+    ko.init((uint32_t)(H * K * 2));
+    vo.init((uint32_t)(H * V * 2));
+    ro.init();
+  }
+  // the three parts of a chunk's inputs, issued at separate points of a chunk
+  // step so that no wave stalls long on a full load queue
+  __device__ __forceinline__ void issue_k(uint32_t lds0, int b, const bf16* kp, int64_t e0, int nv, int H) const {
+    if (nv == C)
+      ko.issue(kp + e0 * K, lds0 + P::k_tile(b));
+    else
+      load_tile<bf16, K, P::NT>(kp + e0 * K, (uint32_t)(H * K * 2), nv, lds0 + P::k_tile(b));
+  }
+  __device__ __forceinline__ void issue_v(uint32_t lds0, int b, const bf16* vp, int64_t e0, int nv, int H) const {
+    if (nv == C)
+      vo.issue(vp + e0 * V, lds0 + P::v_tile(b));
+    else
+      load_tile<bf16, V, P::NT>(vp + e0 * V, (uint32_t)(H * V * 2), nv, lds0 + P::v_tile(b));
+  }
+  __device__ __forceinline__ void issue_rec(uint32_t lds0, int b, const unsigned char* rec) const {
+#pragma unroll
+    for (int i = 0; i < RecOffs<P::NT>::N; ++i) ro.issue1(i, rec, lds0 + P::ai_tile(b));
+  }
+};
+
+template <int K, int V>
+__global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_pipe_kernel(SegTransArgs a, SegGeom G) {
+  using P = TransPlan<K, V>;
+  constexpr int KT = P::KT, KS = P::KS, CT = P::CT, NDG = P::NDG, NW = P::NW;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int h = blockIdx.y;
+  const int H = G.H;
+  const SegLoc sl = locate_seg(blockIdx.x, G);
+  if (!sl.ok || sl.j == sl.nseg - 1) return;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const uint32_t lds0 = lds_addr(smem);
+  // column tiles of [M | R] owned by this wave: c = wid + NW ct; c < K/16 are M tiles
+  int ctile[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) ctile[ct] = wid + NW * ct;
+  // whether tile ct is an R tile (known at compile time when K = V: tile 0 is M, tile 1 is R)
+  auto is_r = [&](int ct) { return K == V ? ct == 1 : ctile[ct] >= KT; };
+
+  f32x4 X[KT][CT];
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) X[tt][ct][j] = (16 * tt + 4 * lg + j == 16 * ctile[ct] + lc) ? 1.f : 0.f;
+  LaneOffs<K> lo;
+  lane_offsets<K, K + 8, C + 8>(lo, lds0);
+  TransLoads<K, V> LD;
+  LD.init(H);
+  const bf16* kp = reinterpret_cast<const bf16*>(a.k);
+  const bf16* vp = reinterpret_cast<const bf16*>(a.v);
+  const int64_t t_seg = sl.bos + sl.c0 * C;
+  const unsigned char* rec0 = reinterpret_cast<const unsigned char*>(a.Ai) +
+                              ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
+  const int64_t rec_step = (int64_t)H * kSegRecordBytes;
+  auto chunk_nv = [&](int c) { return (int)min((int64_t)C, sl.eos - (t_seg + (int64_t)c * C)); };
+  auto load_k = [&](int c) { LD.issue_k(lds0, c % 3, kp, (t_seg + (int64_t)c * C) * H + h, chunk_nv(c), H); };
+  auto load_v = [&](int c) { LD.issue_v(lds0, c % 3, vp, (t_seg + (int64_t)c * C) * H + h, chunk_nv(c), H); };
+  auto load_rec = [&](int c) { LD.issue_rec(lds0, c % 3, rec0 + c * rec_step); };
+  auto load_chunk = [&](int c) {
+    load_k(c);
+    load_v(c);
+    load_rec(c);
+  };
+
+  // w unit (token tile tn, d tiles 4 dg .. +3) and u tiles of chunk cn
+  // (wy_fast.py:55-81, with the k-side scaling beta exp(gc) and the v-side beta
+  // on the columns of Ai): -w to w_tile(cn % 2), u packed into up
+  uint2 up[CT][4];
+  auto products = [&](int cn) {
+    const int b = cn % 3;
+    const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(b));
+    // w units wid, wid + NW, ... (< 4 NDG); exactly one per wave when NW = 4 NDG (K = V = 128)
+#pragma unroll
+    for (int r = 0; r < (4 * NDG + NW - 1) / NW; ++r) {
+      const int unit = wid + NW * r;
+      if (4 * NDG % NW != 0 && unit >= 4 * NDG) break;  // uniform per wave
+      const int tn = unit / NDG, dg = unit % NDG;
+      const unsigned char* ai = smem + P::ai_tile(b) + 32 * tn * C;
+      const Frag<bf16> b0 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0])), vec + 2 * C, 0);
+      const Frag<bf16> b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
+      unsigned char* wt = smem + P::w_tile(cn & 1) + 32 * tn * K;
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) {
+        const uint32_t ka = (NDG == 2 && dg ? lo.ktr[4 + dd] : lo.ktr[dd]) + P::k_tile(b);
+        Frag<bf16> k0, k1;
+        tr4<0, 32 * K, 64 * K, 96 * K>(ka, k0, k1);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        mma(acc, k0, b0);
+        mma(acc, k1, b1);                                // zero for tn < 2: Ai is lower triangular
+        const int dt = 4 * dg + dd;
+        const uint32_t kr = (NDG == 2 && dg ? lo.krow[2 + (dd >> 1)] : lo.krow[dd >> 1]);
+        *reinterpret_cast<uint2*>(wt + kr + 8 * (dt & 1)) =
+            make_uint2(pack_bf16x2(-acc[0], -acc[1]), pack_bf16x2(-acc[2], -acc[3]));
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      if (is_r(ct)) {
+        Frag<bf16> vb0, vb1;
+        tr4<0, 32 * V, 64 * V, 96 * V>(tr_lane_addr<V>(lds0, ctile[ct] - KT) + P::v_tile(b), vb0, vb1);
+        const unsigned char* ai = smem + P::ai_tile(b);
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + lo.airow[0])), vb0);
+          if (tm >= 2) mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + lo.airow[1])), vb1);
+          up[ct][tm] = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+        }
+      }
+    }
+  };
+
+  load_chunk(0);
+  if (sl.nch > 1) load_chunk(1);
+  wait_loads();
+  lds_barrier();
+  products(0);
+  for (int c = 0; c < sl.nch; ++c) {
+    wait_loads();                        // this wave's loads of chunk c + 1
+    lds_barrier();                       // w of chunk c and the inputs of chunk c + 1 are complete
+    // chunk c + 2 goes to the buffers of chunk c - 1, which every wave has left
+    const bool more = c + 2 < sl.nch;
+    if (more) load_rec(c + 2);
+    const int b = c % 3;
+    const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(b));
+    // v' = u + (-w) X
+    Frag<bf16> xb[KS][CT];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) xb[ks][ct] = acc_frag(X[2 * ks][ct], X[2 * ks + 1][ct]);
+    f32x4 Y[4][CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+        Y[tm][ct] = is_r(ct) ? f32x4{bf16_lo(up[ct][tm].x), bf16_hi(up[ct][tm].x), bf16_lo(up[ct][tm].y),
+                                            bf16_hi(up[ct][tm].y)}
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      const unsigned char* wt = smem + P::w_tile(c & 1);
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const Frag<bf16> wa = frag_at<bf16>(reinterpret_cast<const bf16*>(wt + 32 * tm * K + lo.krow[ks]));
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) mma(Y[tm][ct], wa, xb[ks][ct]);
+        }
+    }
+    if (more) load_k(c + 2);
+    // the next chunk's w and u, independent of the state chain (in the same
+    // basic block, so that the two interleave; after the last chunk they are
+    // formed from stale buffers and never used)
+    products(c + 1);
+    if (more) load_v(c + 2);
+    // X = exp(gc_last) X + k^T (v' gate)
+    const float gamma = vec[5 * C];
+    Frag<bf16> vg[2][CT];
+    gate_frags<CT>(Y, vec + 3 * C, vg);
+    const uint32_t kbo = P::k_tile(b);
+#pragma unroll
+    for (int tq = 0; tq < KT; tq += 4) {
+      Frag<bf16> kf[4][2];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tr4<0, 32 * K, 64 * K, 96 * K>(lo.ktr[tq + e] + kbo, kf[e][0], kf[e][1]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          X[tq + e][ct] *= gamma;
+          mma(X[tq + e][ct], kf[e][0], vg[0][ct]);
+          mma(X[tq + e][ct], kf[e][1], vg[1][ct]);
+        }
+    }
+  }
+
+  const int64_t s = blockIdx.x;
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int c0 = 16 * ctile[ct];
+    if (c0 < K) {
+      // M as the bf16 pair (hi, lo = bf16(M - hi)) that seg_combine multiplies in three bf16 products
+      bf16* ph = reinterpret_cast<bf16*>(a.M) + (s * H + h) * 2 * K * K + 4 * lg * K + c0 + lc;
+      bf16* pl = ph + K * K;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = X[tt][ct][j];
+          const bf16 hi = (bf16)x;
+          ph[(16 * tt + j) * K] = hi;
+          pl[(16 * tt + j) * K] = (bf16)(x - (float)hi);
+        }
+    } else {
+      // R in accumulator-tile order: tile (row tile tt, column tile cv) is 64 lanes x 4 floats
+      const int cv = (c0 - K) / 16;
+      float* pr = a.R + (s * H + h) * K * V + 4 * l;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt) *reinterpret_cast<f32x4*>(pr + (tt * (V / 16) + cv) * 256) = X[tt][ct];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // seg_combine: S_{j+1} = M_j S_j + R_j over the segments of a sequence, 16 V
 // columns per workgroup.  Also writes final_state of sequences without tokens.
 //
@@ -1944,10 +2191,17 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   if (!mark(1)) return -1;
   if (p.run_trans) {
     constexpr size_t lds = Eng<TQ, K, V, false>::total;
-    auto kt = seg_trans_kernel<TQ, K, V>;
-    if (set_lds(kt, lds)) return -1;
     SegTransArgs ta{p.k, p.v, p.k_scale, Ai, p.M, p.R};
-    hipLaunchKernelGGL(kt, grid, dim3(Eng<TQ, K, V, false>::NT), lds, s, ta, G);
+    if constexpr (sizeof(TQ) == 2) {
+      constexpr size_t lds_p = TransPlan<K, V>::total;
+      auto kt = seg_trans_pipe_kernel<K, V>;
+      if (set_lds(kt, lds_p)) return -1;
+      hipLaunchKernelGGL(kt, grid, dim3(TransPlan<K, V>::NT), lds_p, s, ta, G);
+    } else {
+      auto kt = seg_trans_kernel<TQ, K, V>;
+      if (set_lds(kt, lds)) return -1;
+      hipLaunchKernelGGL(kt, grid, dim3(Eng<TQ, K, V, false>::NT), lds, s, ta, G);
+    }
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(2)) return -1;
