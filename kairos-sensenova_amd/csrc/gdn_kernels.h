@@ -74,10 +74,10 @@ struct FwdOArgs {
 };
 
 // Per (chunk, head) record written by seg_prep and streamed by seg_trans and
-// seg_out: the chunk inverse with its columns scaled by beta, (I + A)^-1 diag(beta),
-// in bf16 [64][64] (row t holding columns in pcol order), then eight fp32
-// vectors of 64: gc, exp(gc) * scale, exp(gc), the update gate
-// exp(gc_last - gc), beta, exp(gc_last) (repeated), and two unused.
+// seg_out: the chunk inverse (I + A)^-1 rounded to bf16 [64][64] (row t holding
+// columns in pcol order), then eight fp32 vectors of 64: gc, exp(gc) * scale,
+// exp(gc), the update gate exp(gc_last - gc), beta, exp(gc_last) (repeated),
+// and two unused.
 constexpr int kSegRecordBytes = 64 * 64 * 2 + 8 * 64 * 4;
 
 // Segment-parallel fused forward (gdn_seg.hip).  Sequences are cut into

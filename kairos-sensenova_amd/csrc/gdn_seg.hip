@@ -599,27 +599,21 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
     }
   }
 
-  // Ai (bf16, rows in pcol order) staged over the dead block area, then stored
-  // column c of Ai is scaled by beta_c: u = (Ai diag(beta)) v, w = (Ai diag(beta)) diag(exp(gc)) k
-  float bcol[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) bcol[b] = s_g[C + 16 * b + lc];
+  // Ai rounded to bf16 once (solve_tril.py:331 stores it in k's dtype), rows
+  // in pcol order, staged over the dead block area, then stored
   bf16* s_Ai = reinterpret_cast<bf16*>(s_A);
 #pragma unroll
   for (int q = 0; q < 8; ++q)
     *reinterpret_cast<uint4*>(s_Ai + 8 * (64 * q + l)) = make_uint4(0u, 0u, 0u, 0u);
-  float bdiag = bcol[0];
 #pragma unroll
-  for (int b = 1; b < 4; ++b) bdiag = lg == b ? bcol[b] : bdiag;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s_Ai[(16 * lg + i) * C + pcol(16 * lg + lc)] = (bf16)(x[i] * bdiag);
+  for (int i = 0; i < 16; ++i) s_Ai[(16 * lg + i) * C + pcol(16 * lg + lc)] = (bf16)x[i];
 #pragma unroll
   for (int i = 1; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < i; ++j)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
-        s_Ai[(16 * i + 4 * lg + jj) * C + pcol(16 * j + lc)] = (bf16)(X[tri_blk(i - 1, j)][jj] * bcol[j]);
+        s_Ai[(16 * i + 4 * lg + jj) * C + pcol(16 * j + lc)] = (bf16)X[tri_blk(i - 1, j)][jj];
   bf16* dst = reinterpret_cast<bf16*>(rec);
 #pragma unroll
   for (int q = 0; q < 8; ++q)
@@ -627,43 +621,43 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
 }
 
 // ---------------------------------------------------------------------------
-// seg_trans / seg_out: the chunk engine
+// the chunk engine: seg_trans on fp8 k (two barriers per chunk)
 // ---------------------------------------------------------------------------
-// Workgroup: seg_out runs one wave per 16 V columns, seg_trans one wave per two
-// 16-column tiles of [M | R] (tiles wid and wid + NW).  Each wave keeps its fp32
-// state tiles (K rows) in VGPRs in the MFMA accumulator layout.
+// Workgroup: one wave per two 16-column tiles of [M | R] (tiles wid and wid +
+// NW).  Each wave keeps its fp32 state tiles (K rows) in VGPRs in the MFMA
+// accumulator layout.  (bf16 inputs run the pipelined seg_trans_kernel and the
+// producer/consumer seg_out_kernel, which reuse the tiles, lane offsets and
+// products defined here.)
 //
 // Per chunk (two workgroup barriers):
-//   top      this wave's direct loads of the chunk have landed (q, k, v and
-//            the chunk record: Ai diag(beta) and the chunk vectors gc,
-//            exp(gc) scale, exp(gc), the update gate exp(gc_last - gc), beta
-//            and exp(gc_last), formed once by seg_prep).  (fp8: q/k
-//            dequantised after a barrier.)
+//   top      this wave's direct loads of the chunk have landed (k, v and the
+//            chunk record: Ai = (I + A)^-1 and the chunk vectors gc, exp(gc)
+//            scale, exp(gc), the update gate exp(gc_last - gc), beta and
+//            exp(gc_last), formed once by seg_prep); fp8 k is dequantised to
+//            bf16 after a barrier.
 //   barrier 1; the next chunk's loads go into the other buffer (every wave is
 //            done with the chunk that used it), one direct-load instruction at
 //            a time between the steps of phase A, so that no wave stalls on a
 //            full memory queue.
-//   phase A  [own]    h = bf16(S) as operand fragments; o_inter = q h (seg_out);
-//                     u = (Ai diag(beta)) v for the wave's V columns;
-//            [shared] Aqk'^T tiles (seg_out) and w tiles into LDS.  w is formed
-//                     as (Ai diag(beta) diag(exp(gc))) k and stored negated, so that
-//                     v' = u - w h is one MFMA accumulation onto u.
+//   phase A  [own]    X as bf16 operand fragments; u = Ai bf16(v beta) for
+//                     the wave's R columns;
+//            [shared] w tiles into LDS.  w = Ai bf16(bf16(k beta) exp(gc)),
+//                     stored negated, so that v' = u - w X is one MFMA
+//                     accumulation onto u.
 //   barrier 2
-//   phase B  v' = u + (-w) h; o = o_inter exp(gc) scale + Aqk' bf16(v');
-//            S = exp(gc_last) S + k^T bf16(v' gate).
+//   phase B  v' = u + (-w) X; X = exp(gc_last) X + k^T bf16(v' gate).
 // LDS lane offsets are computed once per segment and tile bases are
 // compile-time constants (the chunk loop is unrolled over the two buffers), so
 // a fragment read is a fixed VGPR plus an immediate offset.
-template <typename TQ, int K, int V, bool OUT>
+template <typename TQ, int K, int V>
 struct Eng {
   static constexpr bool FP8 = sizeof(TQ) == 1;
-  static constexpr int NW = OUT ? V / 16 : (K + V) / 32;
+  static constexpr int NW = (K + V) / 32;
   static constexpr int NT = NW * WAVE;
-  static constexpr int CT = OUT ? 1 : 2;                  // 16-column state tiles per wave
+  static constexpr int CT = 2;                            // 16-column state tiles per wave
   static constexpr int KT = K / 16;
   static constexpr int NDG = K / 64;                      // w units per token tile (4 d tiles each)
   static constexpr int LDW = K + 8;                       // s_w row stride (elements), pcol order
-  static constexpr int LDQ = C + 8;                       // s_Aqk row stride
   static constexpr uint32_t KB = C * K * 2, VB = C * V * 2, AB = C * C * 2, RAW = C * K;
   // Tiles read transposed (k, v) lie in the first 64 KB, so that one lane VGPR
   // plus a 16-bit immediate reaches them: bf16 k of both buffers (or the one
@@ -671,18 +665,14 @@ struct Eng {
   static constexpr uint32_t k_tile(int p) { return FP8 ? 0u : (uint32_t)p * KB; }
   static constexpr uint32_t v_tile(int p) { return (FP8 ? KB : 2 * KB) + (uint32_t)p * VB; }
   static constexpr uint32_t tr_end = (FP8 ? KB : 2 * KB) + 2 * VB;
-  static constexpr uint32_t q_tile(int p) { return FP8 ? tr_end : tr_end + (uint32_t)p * KB; }
-  static constexpr uint32_t q_end = OUT ? (FP8 ? tr_end + KB : tr_end + 2 * KB) : tr_end;
-  static constexpr uint32_t kraw(int p) { return q_end + (uint32_t)p * RAW; }        // fp8 inputs as loaded
-  static constexpr uint32_t qraw(int p) { return q_end + 2 * RAW + (uint32_t)p * RAW; }
-  static constexpr uint32_t raw_end = FP8 ? q_end + (OUT ? 4 : 2) * RAW : q_end;
+  static constexpr uint32_t kraw(int p) { return tr_end + (uint32_t)p * RAW; }       // fp8 inputs as loaded
+  static constexpr uint32_t raw_end = FP8 ? tr_end + 2 * RAW : tr_end;
   // the chunk record as loaded: Ai, then the chunk vectors (vec_tile)
   static constexpr uint32_t RB = kSegRecordBytes;
   static constexpr uint32_t ai_tile(int p) { return raw_end + (uint32_t)p * RB; }
   static constexpr uint32_t vec_tile(int p) { return ai_tile(p) + AB; }
   static constexpr uint32_t off_w = raw_end + 2 * RB;
-  static constexpr uint32_t off_aqk = off_w + C * LDW * 2;
-  static constexpr uint32_t total = off_aqk + (OUT ? C * LDQ * 2 : 0);
+  static constexpr uint32_t total = off_w + C * LDW * 2;
   static_assert(tr_end + 0 <= 65536, "transposed tiles must lie in the first 64 KB of LDS");
   static_assert(total <= 160 * 1024, "chunk tiles do not fit in LDS");
 };
@@ -853,16 +843,16 @@ struct RecOffs {
 };
 
 // The direct loads of one chunk, as a fixed sequence of per-wave load
-// instructions ("slots"): [q (seg_out)], k, v, then the chunk record.  Slot S
-// of the next chunk is issued at a fixed point of the current chunk's step.
-template <typename TQ, int K, int V, bool OUT>
+// instructions ("slots"): k, v, then the chunk record.  Slot S of the next
+// chunk is issued at a fixed point of the current chunk's step.
+template <typename TQ, int K, int V>
 struct ChunkLoads {
-  using E = Eng<TQ, K, V, OUT>;
+  using E = Eng<TQ, K, V>;
   static constexpr int NTL = E::NT;                      // loader threads: every wave
   static constexpr int NQ = LoadOffs<TQ, K, NTL>::N;
   static constexpr int NV = LoadOffs<bf16, V, NTL>::N;
   static constexpr int NR = RecOffs<NTL>::N;
-  static constexpr int NS = (OUT ? 2 * NQ : NQ) + NV + NR;   // slots per chunk
+  static constexpr int NS = NQ + NV + NR;                 // slots per chunk
   LoadOffs<TQ, K, NTL> qk;
   LoadOffs<bf16, V, NTL> v;
   RecOffs<NTL> rec;
@@ -872,20 +862,18 @@ struct ChunkLoads {
     rec.init();
   }
   // Slot S of the chunk at tokens t0 .. t0 + nv - 1 (record rec_src) into
-  // buffer P.  A partial chunk (nv < 64) loads a whole q/k/v tile at the
+  // buffer P.  A partial chunk (nv < 64) loads a whole k/v tile at the
   // tile's first slot, rows past the end reading row 0.
   template <int P, int S>
-  __device__ __forceinline__ void slot(uint32_t lds0, const void* qp, const void* kp, const void* vp, int64_t t0,
-                                       int nv, int h, int H, const unsigned char* rec_src) const {
-    constexpr int S0 = OUT ? NQ : 0;                       // first k slot
-    constexpr int S1 = S0 + NQ;                            // first v slot
+  __device__ __forceinline__ void slot(uint32_t lds0, const void* kp, const void* vp, int64_t t0, int nv, int h,
+                                       int H, const unsigned char* rec_src) const {
+    constexpr int S1 = NQ;                                 // first v slot
     constexpr int S2 = S1 + NV;                            // first record slot
     const int64_t e0 = t0 * H + h;
     if constexpr (S < S1) {
-      constexpr bool isq = S < S0;
-      constexpr int i = isq ? S : S - S0;
-      const TQ* src = reinterpret_cast<const TQ*>(isq ? qp : kp) + e0 * K;
-      const uint32_t dst = lds0 + (isq ? (E::FP8 ? E::qraw(P) : E::q_tile(P)) : (E::FP8 ? E::kraw(P) : E::k_tile(P)));
+      constexpr int i = S;
+      const TQ* src = reinterpret_cast<const TQ*>(kp) + e0 * K;
+      const uint32_t dst = lds0 + (E::FP8 ? E::kraw(P) : E::k_tile(P));
       if (nv == C) qk.issue1(i, src, dst);
       else if (i == 0) load_tile<TQ, K, NTL>(src, (uint32_t)(H * K * sizeof(TQ)), nv, dst);
     } else if constexpr (S < S2) {
@@ -899,11 +887,11 @@ struct ChunkLoads {
   }
   // slots S .. NS - 1
   template <int P, int S>
-  __device__ __forceinline__ void slots_from(uint32_t lds0, const void* qp, const void* kp, const void* vp, int64_t t0,
-                                             int nv, int h, int H, const unsigned char* rec_src) const {
+  __device__ __forceinline__ void slots_from(uint32_t lds0, const void* kp, const void* vp, int64_t t0, int nv, int h,
+                                             int H, const unsigned char* rec_src) const {
     if constexpr (S < NS) {
-      slot<P, S>(lds0, qp, kp, vp, t0, nv, h, H, rec_src);
-      slots_from<P, S + 1>(lds0, qp, kp, vp, t0, nv, h, H, rec_src);
+      slot<P, S>(lds0, kp, vp, t0, nv, h, H, rec_src);
+      slots_from<P, S + 1>(lds0, kp, vp, t0, nv, h, H, rec_src);
     }
   }
 };
@@ -924,6 +912,36 @@ __device__ __forceinline__ Frag<bf16> scale_frag(const Frag<bf16>& f, const floa
   return frag_pack(y);
 }
 
+// The w operand of wy_fast.py:74-78 for the 8 tokens of fragment f (K order as
+// in scale_frag): bf16(bf16(k beta) exp(gc)).  k beta is a bf16 product (exact
+// in fp32, rounded once), then scaled by exp(gc) in fp32 and rounded again.
+__device__ __forceinline__ Frag<bf16> kb_frag(const Frag<bf16>& f, const float* beta, const float* eg, int ks) {
+  const int lg = lane_id() >> 4;
+  const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + 32 * ks + 4 * lg);
+  const f32x4 b1 = *reinterpret_cast<const f32x4*>(beta + 32 * ks + 16 + 4 * lg);
+  const f32x4 e0 = *reinterpret_cast<const f32x4*>(eg + 32 * ks + 4 * lg);
+  const f32x4 e1 = *reinterpret_cast<const f32x4*>(eg + 32 * ks + 16 + 4 * lg);
+  float y[8];
+  frag_unpack(f, y);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] *= b0[e];
+    y[4 + e] *= b1[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t r = cvt_pk_bf16(y[e], y[e + 1]);
+    y[e] = bf16_lo(r);
+    y[e + 1] = bf16_hi(r);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] *= e0[e];
+    y[4 + e] *= e1[e];
+  }
+  return frag_pack(y);
+}
+
 // Round the 4 floats of an accumulator tile to bf16 and back (two packed conversions).
 __device__ __forceinline__ f32x4 round4(const f32x4& a) {
   const uint32_t p0 = cvt_pk_bf16(a[0], a[1]), p1 = cvt_pk_bf16(a[2], a[3]);
@@ -931,16 +949,15 @@ __device__ __forceinline__ f32x4 round4(const f32x4& a) {
 }
 
 // One w unit: token tile tn, d tiles 4 DG .. 4 DG + 3.  B = rows 16 tn + lc of
-// Ai diag(beta) scaled by exp(gc) (wy_fast.py:67-81, with the k-side scaling
-// beta exp(gc) moved to the columns of Ai), A = k^T; the tile -w^T[d][i] goes
-// to s_w[i][pcol(d)].
+// Ai, A = kb^T with kb = bf16(bf16(k beta) exp(gc)) (wy_fast.py:67-81); the
+// tile -w^T[d][i] goes to s_w[i][pcol(d)].
 template <typename E, int K, int DG, int P>
 __device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& lo, const float* vec, int tn) {
   const unsigned char* ai = smem + E::ai_tile(P) + 32 * tn * C;
   const int nks = tn / 2 + 1;                                   // Ai is lower triangular
-  Frag<bf16> b0 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0])), vec + 2 * C, 0);
+  Frag<bf16> b0 = frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0]));
   Frag<bf16> b1 = b0;
-  if (nks == 2) b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
+  if (nks == 2) b1 = frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1]));
   unsigned char* wt = smem + E::off_w + lo.w + 32 * tn * E::LDW;
   const uint32_t ka[4] = {lo.ktr[4 * DG], lo.ktr[4 * DG + 1], lo.ktr[4 * DG + 2], lo.ktr[4 * DG + 3]};
   Frag<bf16> kf[4][2];
@@ -950,8 +967,8 @@ __device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& l
   for (int dd = 0; dd < 4; ++dd) {
     const int dt = 4 * DG + dd;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma(acc, kf[dd][0], b0);
-    if (nks == 2) mma(acc, kf[dd][1], b1);
+    mma(acc, kb_frag(kf[dd][0], vec + 4 * C, vec + 2 * C, 0), b0);
+    if (nks == 2) mma(acc, kb_frag(kf[dd][1], vec + 4 * C, vec + 2 * C, 1), b1);
     uint2 pk;
     pk.x = pack_bf16x2(-acc[0], -acc[1]);
     pk.y = pack_bf16x2(-acc[2], -acc[3]);
@@ -959,14 +976,15 @@ __device__ __forceinline__ void w_unit(unsigned char* smem, const LaneOffs<K>& l
   }
 }
 
-// u (64 tokens x 16 columns) = (Ai diag(beta)) v of the V column tile whose
-// transposed read starts at vtr, rounded to bf16 (wy_fast.py:55-65, with the
-// v-side scaling by beta moved to the columns of Ai).
+// u (64 tokens x 16 columns) = Ai bf16(v beta) of the V column tile whose
+// transposed read starts at vtr, rounded to bf16 (wy_fast.py:55-65).
 template <typename E, int V, int P>
 __device__ __forceinline__ void u_tile(const unsigned char* smem, const uint32_t (&airow)[2], uint32_t vtr,
                                        const float* vec, f32x4 (&Y)[4]) {
   Frag<bf16> vb0, vb1;
   trT<V, E::v_tile(P)>(vtr, vb0, vb1);
+  vb0 = scale_frag(vb0, vec + 4 * C, 0);
+  vb1 = scale_frag(vb1, vec + 4 * C, 1);
   const unsigned char* ai = smem + E::ai_tile(P);
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) {
@@ -1027,14 +1045,14 @@ __device__ __forceinline__ void gate_frags(const f32x4 (&Y)[4][CT], const float*
   }
 }
 
-// One Aqk' tile t (tm >= tn, tri_tile order) of a chunk whose k and q tiles
+// One Aqk tile t (tm >= tn, tri_tile order) of a chunk whose k and q tiles
 // start at kt0 and qt0: lane i = 16 tm + lc (q side) and j = 16 tn + 4 lg + jj
-// (k side): Aqk'[i][j] = scale exp(gc_i - gc_j) q_i.k_j for i >= j
-// (chunk_o.py:109-118, the output scale folded in), stored bf16 at
-// s_Aqk[i][pcol(j)] -- four consecutive positions, one 8-byte write.
+// (k side): Aqk[i][j] = exp(gc_i - gc_j) q_i.k_j for i >= j
+// (chunk_o.py:99-118), stored bf16 at s_Aqk[i][pcol(j)] -- four consecutive
+// positions, one 8-byte write.
 template <int K, int LDQ>
 __device__ __forceinline__ void aqk_tile_at(const unsigned char* kt0, const unsigned char* qt0, unsigned char* s_aqk,
-                                            const LaneOffs<K>& lo, const float* vec, float log2s, int t) {
+                                            const LaneOffs<K>& lo, const float* vec, int t) {
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
   int tm, tn;
@@ -1051,7 +1069,7 @@ __device__ __forceinline__ void aqk_tile_at(const unsigned char* kt0, const unsi
   float x[4];
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
-    x[jj] = acc[jj] * __builtin_amdgcn_exp2f(fmaf(gi - gj[jj], 1.4426950408889634f, log2s));
+    x[jj] = acc[jj] * __builtin_amdgcn_exp2f((gi - gj[jj]) * 1.4426950408889634f);
     if (tm == tn && lc < 4 * lg + jj) x[jj] = 0.f;
   }
   *reinterpret_cast<uint2*>(s_aqk + lo.aqk + 2 * (16 * tm * LDQ + 32 * (tn >> 1) + 4 * (tn & 1))) =
@@ -1062,26 +1080,26 @@ __device__ __forceinline__ void aqk_tile_at(const unsigned char* kt0, const unsi
 // seg_out: exact recurrence + output over one segment, on two kinds of wave
 // ---------------------------------------------------------------------------
 // Only part of a chunk step needs the state S: o_inter = q h, v' = u - w h,
-// o = o_inter exp(gc) scale + Aqk' v', and the update S = exp(gc_last) S +
-// k^T (v' gate).  w, u and Aqk' depend on the chunk's inputs alone.  The
+// o = (o_inter exp(gc) + Aqk v') scale, and the update S = exp(gc_last) S +
+// k^T (v' gate).  w, u and Aqk depend on the chunk's inputs alone.  The
 // consumer waves (one per 16 state columns, NCW = V/16) run the
-// state-dependent part of chunk c and, after it, Aqk' of chunk c + 1; four
+// state-dependent part of chunk c and, after it, Aqk of chunk c + 1; four
 // producer waves meanwhile form w and u of chunk c + 1 in registers, write
 // them to LDS after the mid-step barrier, and stage the inputs of the chunks
 // ahead through registers: the k tile and chunk vectors of chunk c + 2 go to
-// LDS in the first half of the step, q, v and Ai diag(beta) in the second
+// LDS in the first half of the step, q, v and Ai in the second
 // half, each followed by the loads of the same parts of chunk c + 3.
 //
 // Iteration c (c = -1 .. nch - 1), two workgroup barriers:
 //   B1; consumers: h = bf16(S), v' = u + (-w) h, o_inter and o (stored);
 //       producers: k, vectors of chunk c + 2 to LDS (+ loads of chunk c + 3),
 //                  w and u of chunk c + 1 into registers;
-//   B2; consumers: S update with k of chunk c, Aqk' of chunk c + 1;
+//   B2; consumers: S update with k of chunk c, Aqk of chunk c + 1;
 //       producers: w, u of chunk c + 1 to LDS, q, v, Ai of chunk c + 2 to LDS
 //                  (+ loads of chunk c + 3).
 // Buffers: q of chunk x in q_tile(x % 2), k in k_tile(x % 3), the chunk
-// vectors in vec_tile(x % 3); v and Ai diag(beta) of chunk c + 1 only (the
-// producers' inputs); w, Aqk' and u of chunk c only.
+// vectors in vec_tile(x % 3); v and Ai of chunk c + 1 only (the
+// producers' inputs); w, Aqk and u of chunk c only.
 struct SegOutArgs {
   const void* q;
   const void* k;
@@ -1106,7 +1124,7 @@ struct OutPlan {
   static constexpr int CTN = 1;                          // 16-column state tiles per consumer
   static constexpr int KT = K / 16, KS = K / 32, NDG = K / 64;
   static constexpr int LDW = K + 8;                      // -w rows (pcol order)
-  static constexpr int LDQ = C + 8;                      // Aqk' rows (pcol order)
+  static constexpr int LDQ = C + 8;                      // Aqk rows (pcol order)
   static constexpr int LDU = C + 8;                      // u^T rows (token order)
   static constexpr uint32_t KB = C * K * 2, VB = C * V * 2, AB = C * C * 2, VECB = 8 * C * 4;
   // tiles read transposed first (16-bit offset field): k (three buffers), v
@@ -1130,7 +1148,7 @@ struct OutPlan {
 // hold q and k, consumer threads (NCW waves) hold v and the record, as units of
 // 8 elements (16 bytes bf16, 8 bytes fp8): unit u = thread + threads * i, row
 // u / (cols / 8), 8-column group u % (cols / 8); rows past the chunk end read
-// row 0.  Record units below AU are Ai diag(beta) (swizzled rows), the rest
+// row 0.  Record units below AU are Ai (swizzled rows), the rest
 // the chunk vectors.
 template <typename TQ, int K, int V>
 struct ChunkSrc {
@@ -1231,12 +1249,12 @@ struct ConsStage {
 };
 
 // The state-independent products of one chunk that the producer waves form,
-// held from their computation until the mid-step barrier: w units (u = pw +
-// 4 i: token tile u / NDG, d group u % NDG) and u column tiles (ct = pw + 4 i),
+// held from their computation until the mid-step barrier: the -w tiles of d
+// tile pw + 4 i (all four token tiles) and the u column tiles ct = pw + 4 i,
 // each as packed bf16.
 template <int K, int V>
 struct OutProducts {
-  static constexpr int NWU = (4 * (K / 64) + 3) / 4, NU = (V / 16 + 3) / 4;
+  static constexpr int NWU = K / 64, NU = (V / 16 + 3) / 4;
   uint2 w[NWU][4];
   uint2 u[NU][4];
 };
@@ -1244,7 +1262,7 @@ struct OutProducts {
 template <typename TQ, int K, int V>
 __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
   using P = OutPlan<TQ, K, V>;
-  constexpr int KT = P::KT, KS = P::KS, CTN = P::CTN, NDG = P::NDG;
+  constexpr int KT = P::KT, KS = P::KS, CTN = P::CTN;
   constexpr int LDW = P::LDW, LDQ = P::LDQ, LDU = P::LDU;
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -1259,7 +1277,6 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
   const uint32_t lds0 = lds_addr(smem);
   const float qs = a.q_scale ? a.q_scale[h] : 1.f;
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
-  const float log2s = __builtin_amdgcn_logf(a.scale);
   const int64_t t_seg = sl.bos + sl.c0 * C;                 // first token of the segment
   const unsigned char* rec0 = reinterpret_cast<const unsigned char*>(a.Ai) +
                               ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
@@ -1268,7 +1285,7 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
 
   LaneOffs<K> lo;
   lane_offsets<K, LDW, LDQ>(lo, lds0);
-  // Upper 16x16 tiles of Aqk' that operand fragments read (column tile 2 ks + 1
+  // Upper 16x16 tiles of Aqk that operand fragments read (column tile 2 ks + 1
   // of row tile 2 ks) are zero; no chunk writes them.
   {
     bf16* s_aqk = reinterpret_cast<bf16*>(smem + P::off_aqk);
@@ -1351,7 +1368,7 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
               for (int ct = 0; ct < CTN; ++ct) mma(Y[tm][ct], wa, hb[ks][ct]);
             }
         }
-        // o^T = o_inter^T exp(gc) scale + v'^T Aqk'^T  (chunk_o.py:84-128), with
+        // o^T = (o_inter^T exp(gc) + v'^T bf16(Aqk)^T) scale  (chunk_o.py:84-128), with
         // o_inter^T = h^T q^T (chunk_o.py:84-107)
         Frag<bf16> vn[2][CTN];
 #pragma unroll
@@ -1380,14 +1397,15 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
         uint2 ov[4][CTN];
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
-          const float es = vec[C + 16 * tn + lc];
+          const float eg = vec[2 * C + 16 * tn + lc];
 #pragma unroll
           for (int ct = 0; ct < CTN; ++ct) {
-            f32x4 r = oi[tn][ct] * es;
+            f32x4 r = oi[tn][ct] * eg;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
               if (ks <= tn / 2)
                 mma(r, vn[ks][ct], frag_at<bf16>(reinterpret_cast<const bf16*>(aq + 32 * tn * LDQ + 64 * ks)));
+            r *= a.scale;
             ov[tn][ct] = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
           }
         }
@@ -1433,19 +1451,18 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
             }
         }
       }
-      // Aqk' of chunk c + 1 (its q and k arrived in the previous step; chunk c's
-      // Aqk' was last read before B2): tiles wid, wid + NCW, ... (< 10)
+      // Aqk of chunk c + 1 (its q and k arrived in the previous step; chunk c's
+      // Aqk was last read before B2): tiles wid, wid + NCW, ... (< 10)
       if (c + 1 < sl.nch) {
         const int cn = c + 1;
         const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(cn % 3));
 #pragma unroll
         for (int i = 0; i < (10 + P::NCW - 1) / P::NCW; ++i) {
           const int t = wid + P::NCW * i;
-          if (t < 10) aqk_tile_at<K, LDQ>(smem + P::k_tile(cn % 3), smem + P::q_tile(cn & 1), smem + P::off_aqk, lo, vec,
-                                          log2s, t);
+          if (t < 10) aqk_tile_at<K, LDQ>(smem + P::k_tile(cn % 3), smem + P::q_tile(cn & 1), smem + P::off_aqk, lo, vec, t);
         }
       }
-      // v, Ai diag(beta) and the vectors of chunk c + 2 (the producers are done
+      // v, Ai and the vectors of chunk c + 2 (the producers are done
       // with those of chunk c + 1), then the loads of chunk c + 3
       if (c + 2 < sl.nch) {
         cs.store(smem, (c + 2) % 3);
@@ -1468,6 +1485,10 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     lds_barrier();
     const int pw = wid - P::NCW;
     OutProducts<K, V> pr;
+    // transposed-read lane addresses of this producer's d tiles pw + 4 i
+    uint32_t ktr_w[OutProducts<K, V>::NWU];
+#pragma unroll
+    for (int i = 0; i < OutProducts<K, V>::NWU; ++i) ktr_w[i] = tr_lane_addr<K>(lds0, pw + 4 * i);
     for (int c = -1; c < sl.nch; ++c) {
       // ---------------- B1 .. B2
       // producers: w and u of chunk c + 1; k of chunk c + 2 goes to a buffer
@@ -1483,29 +1504,24 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
       auto issue = [&](auto) {
         __builtin_amdgcn_sched_barrier(0);               // one product at a time: bounded live registers
       };
-      // -w (token tile tn, d tiles 4 dg .. +3) = -(Ai diag(beta) diag(exp(gc))) k  (wy_fast.py:67-81)
+      // -w (all token tiles tn, d tile pw + 4 i) = -Ai bf16(bf16(k beta) exp(gc))  (wy_fast.py:67-81)
       auto w_item = [&](auto I) {
         constexpr int i = decltype(I)::value;
         if constexpr (i >= OutProducts<K, V>::NWU) return;
-        const int u = pw + 4 * i;
-        if (u < 4 * NDG) {
-          const int tn = u / NDG, dg = u % NDG;
-          const unsigned char* ai = smem + P::ai_tile + 32 * tn * C;
-          const Frag<bf16> b0 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0])), vec + 2 * C, 0);
-          const Frag<bf16> b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
+        Frag<bf16> k0, k1;
+        tr4<0, 32 * K, 64 * K, 96 * K>(ktr_w[i] + P::k_tile(kb), k0, k1);
+        const Frag<bf16> kb0 = kb_frag(k0, vec + 4 * C, vec + 2 * C, 0);
+        const Frag<bf16> kb1 = kb_frag(k1, vec + 4 * C, vec + 2 * C, 1);
+        const unsigned char* ai = smem + P::ai_tile;
 #pragma unroll
-          for (int dd = 0; dd < 4; ++dd) {
-            const uint32_t ka = (NDG == 2 && dg ? lo.ktr[4 + dd] : lo.ktr[dd]) + P::k_tile(kb);
-            Frag<bf16> k0, k1;
-            tr4<0, 32 * K, 64 * K, 96 * K>(ka, k0, k1);
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            mma(acc, k0, b0);
-            if (tn >= 2) mma(acc, k1, b1);
-            pr.w[i][dd] = make_uint2(pack_bf16x2(-acc[0], -acc[1]), pack_bf16x2(-acc[2], -acc[3]));
-          }
+        for (int tn = 0; tn < 4; ++tn) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          mma(acc, kb0, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tn * C + lo.airow[0])));
+          if (tn >= 2) mma(acc, kb1, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tn * C + lo.airow[1])));
+          pr.w[i][tn] = make_uint2(pack_bf16x2(-acc[0], -acc[1]), pack_bf16x2(-acc[2], -acc[3]));
         }
       };
-      // u (column tile ctu) = (Ai diag(beta)) v     (wy_fast.py:55-65)
+      // u (column tile ctu) = Ai bf16(v beta)     (wy_fast.py:55-65)
       auto u_item = [&](auto I) {
         constexpr int i = decltype(I)::value;
         if constexpr (i >= OutProducts<K, V>::NU) return;
@@ -1513,6 +1529,8 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
         if (ctu < V / 16) {
           Frag<bf16> vb0, vb1;
           tr4<0, 32 * V, 64 * V, 96 * V>(tr_lane_addr<V>(lds0, ctu) + P::v_tile, vb0, vb1);
+          vb0 = scale_frag(vb0, vec + 4 * C, 0);
+          vb1 = scale_frag(vb1, vec + 4 * C, 1);
           const unsigned char* ai = smem + P::ai_tile;
 #pragma unroll
           for (int tm = 0; tm < 4; ++tm) {
@@ -1537,16 +1555,10 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
       if (c + 1 < sl.nch) {
 #pragma unroll
         for (int i = 0; i < OutProducts<K, V>::NWU; ++i) {
-          const int u = pw + 4 * i;
-          if (u < 4 * NDG) {
-            const int tn = u / NDG, dg = u % NDG;
-            unsigned char* wt = smem + P::off_w + lo.w + 32 * tn * LDW;
+          const int dt = pw + 4 * i;
+          unsigned char* wt = smem + P::off_w + lo.w + 2 * (32 * (dt >> 1) + 4 * (dt & 1));
 #pragma unroll
-            for (int dd = 0; dd < 4; ++dd) {
-              const int dt = 4 * dg + dd;
-              *reinterpret_cast<uint2*>(wt + 2 * (32 * (dt >> 1) + 4 * (dt & 1))) = pr.w[i][dd];
-            }
-          }
+          for (int tn = 0; tn < 4; ++tn) *reinterpret_cast<uint2*>(wt + 32 * tn * LDW) = pr.w[i][tn];
         }
 #pragma unroll
         for (int i = 0; i < OutProducts<K, V>::NU; ++i) {
@@ -1577,7 +1589,9 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
 }
 
 // ---------------------------------------------------------------------------
-// seg_trans: affine map [M | R] of one segment (all but the last segment of a sequence)
+// seg_trans: affine map [M | R] of one segment (all but the last segment of a
+// sequence).  seg_trans_fp8_kernel below serves fp8 k on the chunk engine;
+// bf16 q/k take the pipelined seg_trans_kernel that follows it.
 // ---------------------------------------------------------------------------
 struct SegTransArgs {
   const void* k;
@@ -1589,8 +1603,8 @@ struct SegTransArgs {
 };
 
 template <typename TQ, int K, int V>
-__global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(SegTransArgs a, SegGeom G) {
-  using E = Eng<TQ, K, V, false>;
+__global__ __launch_bounds__((Eng<TQ, K, V>::NT)) void seg_trans_fp8_kernel(SegTransArgs a, SegGeom G) {
+  using E = Eng<TQ, K, V>;
   constexpr int NW = E::NW, NT = E::NT, KT = K / 16, KS = K / 32, CT = 2;
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -1622,8 +1636,8 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
     }
   }
   LaneOffs<K> lo;
-  lane_offsets<K, E::LDW, E::LDQ>(lo, lds0);
-  ChunkLoads<TQ, K, V, false> LD;
+  lane_offsets<K, E::LDW, C + 8>(lo, lds0);
+  ChunkLoads<TQ, K, V> LD;
   LD.init(H);
 
   int64_t t0 = sl.bos + sl.c0 * C;
@@ -1631,7 +1645,7 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
   const unsigned char* rec = reinterpret_cast<const unsigned char*>(a.Ai) +
                              ((sl.cbase + sl.c0) * H + h) * (int64_t)kSegRecordBytes;
   const int64_t rec_step = (int64_t)H * kSegRecordBytes;
-  LD.template slots_from<0, 0>(lds0, nullptr, a.k, a.v, t0, nv, h, H, rec);
+  LD.template slots_from<0, 0>(lds0, a.k, a.v, t0, nv, h, H, rec);
 
   auto step = [&](auto PP, int ci) {
     constexpr int P = decltype(PP)::value;
@@ -1651,10 +1665,10 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
       rec += rec_step;
     }
     auto slot = [&](auto SS) {
-      if (more) LD.template slot<1 - P, decltype(SS)::value>(lds0, nullptr, a.k, a.v, t0, nv, h, H, rec);
+      if (more) LD.template slot<1 - P, decltype(SS)::value>(lds0, a.k, a.v, t0, nv, h, H, rec);
     };
     auto slots_from = [&](auto SS) {
-      if (more) LD.template slots_from<1 - P, decltype(SS)::value>(lds0, nullptr, a.k, a.v, t0, nv, h, H, rec);
+      if (more) LD.template slots_from<1 - P, decltype(SS)::value>(lds0, a.k, a.v, t0, nv, h, H, rec);
     };
     slot(std::integral_constant<int, 0>{});
     // ---- phase A
@@ -1729,12 +1743,17 @@ __global__ __launch_bounds__((Eng<TQ, K, V, false>::NT)) void seg_trans_kernel(S
 // ---------------------------------------------------------------------------
 // Each wave owns two 16-column tiles of [M | R] as in the chunk engine, but the
 // state-independent half of a step runs one chunk ahead: in the step of chunk
-// c every wave forms its w unit and its u tiles of chunk c + 1 (w into the
-// other of two w tiles, u in registers) between the MFMA of chunk c's update,
+// c every wave forms its w d tile (all 64 tokens) and its u tiles of chunk
+// c + 1 (w into the other of two w tiles, u in registers) between the MFMA of
+// chunk c's update,
 // so one barrier per chunk publishes w and the inputs of the next chunk, and
 // the state chain's MFMA and the w/u work fill each other's latency.  The
 // chunk inputs are triple buffered (chunk c: update; c + 1: w, u; c + 2:
-// direct loads in flight).  The w tile has no padding: its 16-byte chunks are
+// direct loads in flight), and the loads of chunk c + 2 go out in three parts
+// (record after the barrier, k after the w.X products, v after the next
+// chunk's w and u): a CU accepts direct loads at a limited rate, and one burst
+// of all three stalled the issuing waves for over a thousand cycles while
+// their SIMD partners idled at the barrier.  The w tile has no padding: its 16-byte chunks are
 // swizzled like the input tiles (Tile<K>), so the lane offsets of a K row
 // fragment (krow) address it.
 template <int K, int V>
@@ -1784,9 +1803,9 @@ struct TransLoads {
 };
 
 template <int K, int V>
-__global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_pipe_kernel(SegTransArgs a, SegGeom G) {
+__global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_kernel(SegTransArgs a, SegGeom G) {
   using P = TransPlan<K, V>;
-  constexpr int KT = P::KT, KS = P::KS, CT = P::CT, NDG = P::NDG, NW = P::NW;
+  constexpr int KT = P::KT, KS = P::KS, CT = P::CT, NW = P::NW;
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int h = blockIdx.y;
@@ -1831,34 +1850,39 @@ __global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_pipe_kernel(S
     load_rec(c);
   };
 
-  // w unit (token tile tn, d tiles 4 dg .. +3) and u tiles of chunk cn
-  // (wy_fast.py:55-81, with the k-side scaling beta exp(gc) and the v-side beta
-  // on the columns of Ai): -w to w_tile(cn % 2), u packed into up
+  // d tiles of w formed by this wave: dt = wid + NW r (< KT); the lane
+  // addresses of their transposed k reads and of their -w stores
+  constexpr int DTW = (KT + NW - 1) / NW;
+  uint32_t ktr_w[DTW], wst[DTW];
+#pragma unroll
+  for (int r = 0; r < DTW; ++r) {
+    const int dt = min(wid + NW * r, KT - 1);
+    ktr_w[r] = tr_lane_addr<K>(lds0, dt);
+    wst[r] = 2 * Tile<K>::off(lc, 4 * (dt >> 1) + lg) + 8 * (dt & 1);
+  }
+
+  // -w (d tile dt, all token tiles) and the u tiles of chunk cn (wy_fast.py:55-81):
+  // w = Ai bf16(bf16(k beta) exp(gc)) to w_tile(cn % 2), u = Ai bf16(v beta) packed into up
   uint2 up[CT][4];
   auto products = [&](int cn) {
     const int b = cn % 3;
     const float* vec = reinterpret_cast<const float*>(smem + P::vec_tile(b));
-    // w units wid, wid + NW, ... (< 4 NDG); exactly one per wave when NW = 4 NDG (K = V = 128)
+    const unsigned char* ai = smem + P::ai_tile(b);
 #pragma unroll
-    for (int r = 0; r < (4 * NDG + NW - 1) / NW; ++r) {
-      const int unit = wid + NW * r;
-      if (4 * NDG % NW != 0 && unit >= 4 * NDG) break;  // uniform per wave
-      const int tn = unit / NDG, dg = unit % NDG;
-      const unsigned char* ai = smem + P::ai_tile(b) + 32 * tn * C;
-      const Frag<bf16> b0 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[0])), vec + 2 * C, 0);
-      const Frag<bf16> b1 = scale_frag(frag_at<bf16>(reinterpret_cast<const bf16*>(ai + lo.airow[1])), vec + 2 * C, 1);
-      unsigned char* wt = smem + P::w_tile(cn & 1) + 32 * tn * K;
+    for (int r = 0; r < DTW; ++r) {
+      if (KT % NW != 0 && wid + NW * r >= KT) break;   // uniform per wave
+      Frag<bf16> k0, k1;
+      tr4<0, 32 * K, 64 * K, 96 * K>(ktr_w[r] + P::k_tile(b), k0, k1);
+      const Frag<bf16> kb0 = kb_frag(k0, vec + 4 * C, vec + 2 * C, 0);
+      const Frag<bf16> kb1 = kb_frag(k1, vec + 4 * C, vec + 2 * C, 1);
+      unsigned char* wt = smem + P::w_tile(cn & 1) + wst[r];
 #pragma unroll
-      for (int dd = 0; dd < 4; ++dd) {
-        const uint32_t ka = (NDG == 2 && dg ? lo.ktr[4 + dd] : lo.ktr[dd]) + P::k_tile(b);
-        Frag<bf16> k0, k1;
-        tr4<0, 32 * K, 64 * K, 96 * K>(ka, k0, k1);
+      for (int tn = 0; tn < 4; ++tn) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma(acc, k0, b0);
-        mma(acc, k1, b1);                                // zero for tn < 2: Ai is lower triangular
-        const int dt = 4 * dg + dd;
-        const uint32_t kr = (NDG == 2 && dg ? lo.krow[2 + (dd >> 1)] : lo.krow[dd >> 1]);
-        *reinterpret_cast<uint2*>(wt + kr + 8 * (dt & 1)) =
+        mma(acc, kb0, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tn * C + lo.airow[0])));
+        if (tn >= 2)                                      // Ai is lower triangular
+          mma(acc, kb1, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tn * C + lo.airow[1])));
+        *reinterpret_cast<uint2*>(wt + 32 * tn * K) =
             make_uint2(pack_bf16x2(-acc[0], -acc[1]), pack_bf16x2(-acc[2], -acc[3]));
       }
     }
@@ -1867,7 +1891,8 @@ __global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_pipe_kernel(S
       if (is_r(ct)) {
         Frag<bf16> vb0, vb1;
         tr4<0, 32 * V, 64 * V, 96 * V>(tr_lane_addr<V>(lds0, ctile[ct] - KT) + P::v_tile(b), vb0, vb1);
-        const unsigned char* ai = smem + P::ai_tile(b);
+        vb0 = scale_frag(vb0, vec + 4 * C, 0);
+        vb1 = scale_frag(vb1, vec + 4 * C, 1);
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -2190,17 +2215,17 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   }
   if (!mark(1)) return -1;
   if (p.run_trans) {
-    constexpr size_t lds = Eng<TQ, K, V, false>::total;
+    constexpr size_t lds = Eng<TQ, K, V>::total;
     SegTransArgs ta{p.k, p.v, p.k_scale, Ai, p.M, p.R};
     if constexpr (sizeof(TQ) == 2) {
       constexpr size_t lds_p = TransPlan<K, V>::total;
-      auto kt = seg_trans_pipe_kernel<K, V>;
+      auto kt = seg_trans_kernel<K, V>;
       if (set_lds(kt, lds_p)) return -1;
       hipLaunchKernelGGL(kt, grid, dim3(TransPlan<K, V>::NT), lds_p, s, ta, G);
     } else {
-      auto kt = seg_trans_kernel<TQ, K, V>;
+      auto kt = seg_trans_fp8_kernel<TQ, K, V>;
       if (set_lds(kt, lds)) return -1;
-      hipLaunchKernelGGL(kt, grid, dim3(Eng<TQ, K, V, false>::NT), lds, s, ta, G);
+      hipLaunchKernelGGL(kt, grid, dim3(Eng<TQ, K, V>::NT), lds, s, ta, G);
     }
     if (hipGetLastError() != hipSuccess) return -1;
   }
