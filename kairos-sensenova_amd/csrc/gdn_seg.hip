@@ -1084,18 +1084,20 @@ __device__ __forceinline__ void aqk_tile_at(const unsigned char* kt0, const unsi
 // k^T (v' gate).  w, u and Aqk depend on the chunk's inputs alone.  The
 // consumer waves (one per 16 state columns, NCW = V/16) run the
 // state-dependent part of chunk c and, after it, Aqk of chunk c + 1; four
-// producer waves meanwhile form w and u of chunk c + 1 in registers, write
-// them to LDS after the mid-step barrier, and stage the inputs of the chunks
-// ahead through registers: the k tile and chunk vectors of chunk c + 2 go to
-// LDS in the first half of the step, q, v and Ai in the second
-// half, each followed by the loads of the same parts of chunk c + 3.
+// producer waves meanwhile form w and u of chunk c + 1 in registers (the Ai
+// rows they share read once) and write them to LDS after the mid-step
+// barrier.  The inputs of chunk c + 2 reach LDS through registers, into
+// buffers no wave reads then, each part followed by the loads of the same part
+// of chunk c + 3; the parts are spread over both halves of the step, since a
+// CU issues global loads at a limited rate.
 //
 // Iteration c (c = -1 .. nch - 1), two workgroup barriers:
 //   B1; consumers: h = bf16(S), v' = u + (-w) h, o_inter and o (stored);
-//       producers: k, vectors of chunk c + 2 to LDS (+ loads of chunk c + 3),
-//                  w and u of chunk c + 1 into registers;
-//   B2; consumers: S update with k of chunk c, Aqk of chunk c + 1;
-//       producers: w, u of chunk c + 1 to LDS, q, v, Ai of chunk c + 2 to LDS
+//       producers: k of chunk c + 2 to LDS (+ loads of chunk c + 3), w and u
+//                  of chunk c + 1 into registers;
+//   B2; consumers: S update with k of chunk c, Aqk of chunk c + 1; v, Ai and
+//                  the vectors of chunk c + 2 to LDS (+ loads of chunk c + 3);
+//       producers: w, u of chunk c + 1 to LDS; q of chunk c + 2 to LDS
 //                  (+ loads of chunk c + 3).
 // Buffers: q of chunk x in q_tile(x % 2), k in k_tile(x % 3), the chunk
 // vectors in vec_tile(x % 3); v and Ai of chunk c + 1 only (the
@@ -1504,6 +1506,17 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
       auto issue = [&](auto) {
         __builtin_amdgcn_sched_barrier(0);               // one product at a time: bounded live registers
       };
+      // rows 16 t + lc of Ai (K steps 0, 1; the upper blocks are zero): the
+      // operand of both w and u, read once
+      Frag<bf16> af[4][2];
+      {
+        const unsigned char* ai = smem + P::ai_tile;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+            if (ks <= t / 2) af[t][ks] = frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * t * C + lo.airow[ks]));
+      }
       // -w (all token tiles tn, d tile pw + 4 i) = -Ai bf16(bf16(k beta) exp(gc))  (wy_fast.py:67-81)
       auto w_item = [&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -1512,12 +1525,11 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
         tr4<0, 32 * K, 64 * K, 96 * K>(ktr_w[i] + P::k_tile(kb), k0, k1);
         const Frag<bf16> kb0 = kb_frag(k0, vec + 4 * C, vec + 2 * C, 0);
         const Frag<bf16> kb1 = kb_frag(k1, vec + 4 * C, vec + 2 * C, 1);
-        const unsigned char* ai = smem + P::ai_tile;
 #pragma unroll
         for (int tn = 0; tn < 4; ++tn) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          mma(acc, kb0, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tn * C + lo.airow[0])));
-          if (tn >= 2) mma(acc, kb1, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tn * C + lo.airow[1])));
+          mma(acc, kb0, af[tn][0]);
+          if (tn >= 2) mma(acc, kb1, af[tn][1]);
           pr.w[i][tn] = make_uint2(pack_bf16x2(-acc[0], -acc[1]), pack_bf16x2(-acc[2], -acc[3]));
         }
       };
@@ -1531,12 +1543,11 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
           tr4<0, 32 * V, 64 * V, 96 * V>(tr_lane_addr<V>(lds0, ctu) + P::v_tile, vb0, vb1);
           vb0 = scale_frag(vb0, vec + 4 * C, 0);
           vb1 = scale_frag(vb1, vec + 4 * C, 1);
-          const unsigned char* ai = smem + P::ai_tile;
 #pragma unroll
           for (int tm = 0; tm < 4; ++tm) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + lo.airow[0])), vb0);
-            if (tm >= 2) mma(acc, frag_at<bf16>(reinterpret_cast<const bf16*>(ai + 32 * tm * C + lo.airow[1])), vb1);
+            mma(acc, af[tm][0], vb0);
+            if (tm >= 2) mma(acc, af[tm][1], vb1);
             pr.u[i][tm] = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
           }
         }
