@@ -5,8 +5,9 @@ One step = one chunk_gated_delta_rule forward over BASELINE config 2
 output_final_state=True) with inputs resident in HBM, through the C ABI
 (kairos_gdn_chunk_fwd).  Prints ONE JSON line.
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
   python bench.py --calibrate-copy 1024     # reference copy kernel for rocprofv3 counter scaling
+  python bench.py --epilogue                # the gated RMSNorm output epilogue on config 2's o
 
 `value` is tokens/s of whole forward calls (wall clock between two device
 synchronisations around `steps` back-to-back calls).  Per-kernel times come
@@ -151,6 +152,46 @@ def cpu_baseline(T, H, K, V, seed, min_seconds=10.0):
                       f"forward; host CPU: {model}"}
 
 
+def bench_epilogue(args, dev):
+    """Gated RMSNorm (fla FusedRMSNormGated, the layer's o_norm) over config 2's output rows:
+    algorithmic bytes = rows * V * (2 + 2 + 2) (read o and the gate, write y, bf16)."""
+    from kairos_gdn import _lib
+    T, H, V = args.T, 20, 128
+    rows = T * H
+    gen = torch.Generator(device="cpu").manual_seed(20262)
+    x = torch.randn(rows, V, generator=gen).to(dev, torch.bfloat16)
+    gate = torch.randn(rows, V, generator=gen).to(dev, torch.bfloat16)
+    w = torch.rand(V, generator=gen).add_(0.5).to(dev)
+    y = torch.empty_like(x)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        _lib.call("kairos_gdn_rms_norm_gated", x.data_ptr(), gate.data_ptr(), w.data_ptr(), None, y.data_ptr(),
+                  None, _lib.BF16, _lib.BF16, _lib.F32, rows, V, 1e-5, _lib.ACT_SWISH, sp)
+
+    for _ in range(args.warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = rows * V * 6
+    gbs = nbytes / (ms / 1e3) / 1e9
+    print(json.dumps({
+        "metric": "gated RMSNorm epilogue GB/s at T=32760,H=20,dv=128", "value": gbs, "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "FusedRMSNormGated(128, eps=1e-5, swish) on o [T*H, 128] bf16, bf16 gate, "
+                               "fp32 weight", "rows": rows},
+        "roofline": {"bound": "hbm", "kernel": "rmsnorm_gated_kernel", "achieved": gbs, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +202,9 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a plain elementwise copy of MIB MiB (fp32 y = x * 1) 5 times and exit: the "
                          "reference kernel of known traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--epilogue", action="store_true",
+                    help="measure only the gated RMSNorm epilogue (kairos_gdn_rms_norm_gated) on o-shaped rows "
+                         "[T*H, V] bf16 with a bf16 gate and fp32 weight; prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -181,6 +225,9 @@ def main():
 
     import kairos_gdn  # noqa: F401
     from kairos_gdn import _lib
+    if args.epilogue:
+        bench_epilogue(args, dev)
+        return
     B, T, H, K, V = 1, args.T, 20, 128, 128
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)
     scale = K ** -0.5

@@ -140,6 +140,23 @@ int kairos_gdn_fwd_o(const void* q, const void* k, const float* q_scale, const f
  * the last dim D (multiple of 8, <= 512), in x's dtype (fp32 or bf16). */
 int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream);
 
+/* ---- output epilogue -------------------------------------------------------
+ * Gated RMSNorm of the GatedDeltaNet layer's output (o_norm = FusedRMSNormGated,
+ * fla layers/gated_deltanet.py:197,311), replacing layer_norm_gated_fwd with
+ * is_rms_norm=True (fla modules/fused_norm_gate.py:449-525, kernel :42-127)
+ * without residual:
+ *   rstd = 1 / sqrt(mean_d x^2 + eps);  y = x rstd weight [+ bias];
+ *   y *= g sigmoid(g) (KAIROS_GDN_ACT_SWISH, 'swish' / 'silu') or
+ *   y *= sigmoid(g)   (KAIROS_GDN_ACT_SIGMOID).
+ * x, g: [rows, D] (fp32 or bf16 each; 16-byte aligned); weight, bias: [D] in
+ * w_dtype (16-byte aligned), either may be NULL (no affine weight / no bias); y: [rows, D] in
+ * x's dtype; rstd: [rows] fp32 or NULL.  D a multiple of 8, at most 512. */
+#define KAIROS_GDN_ACT_SWISH 0
+#define KAIROS_GDN_ACT_SIGMOID 1
+int kairos_gdn_rms_norm_gated(const void* x, const void* g, const void* weight, const void* bias, void* y,
+                              float* rstd, int x_dtype, int g_dtype, int w_dtype, int64_t rows, int64_t D,
+                              float eps, int activation, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -559,4 +559,28 @@ int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64
   return ok();
 }
 
+int kairos_gdn_rms_norm_gated(const void* x, const void* g, const void* weight, const void* bias, void* y,
+                              float* rstd, int x_dtype, int g_dtype, int w_dtype, int64_t rows, int64_t D,
+                              float eps, int activation, void* stream) {
+  const char* what = "kairos_gdn_rms_norm_gated";
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > 512)
+    return fail(KAIROS_GDN_EINVAL, "%s: D must be a positive multiple of 8, at most 512", what);
+  if (!valid_scalar_dt(x_dtype) || !valid_scalar_dt(g_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: x and g must be fp32 or bf16", what);
+  if ((weight || bias) && !valid_scalar_dt(w_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: weight and bias must be fp32 or bf16", what);
+  if (activation != KAIROS_GDN_ACT_SWISH && activation != KAIROS_GDN_ACT_SIGMOID)
+    return fail(KAIROS_GDN_EINVAL, "%s: activation must be KAIROS_GDN_ACT_SWISH or KAIROS_GDN_ACT_SIGMOID", what);
+  if (!(eps >= 0.f)) return fail(KAIROS_GDN_EINVAL, "%s: eps must be non-negative", what);
+  if (rows == 0) return ok();
+  if (!x || !g || !y || !aligned16(x) || !aligned16(g) || !aligned16(y))
+    return fail(KAIROS_GDN_EINVAL, "%s: x, g and y must be non-null and 16-byte aligned", what);
+  if ((weight && !aligned16(weight)) || (bias && !aligned16(bias)))
+    return fail(KAIROS_GDN_EINVAL, "%s: weight and bias must be 16-byte aligned", what);
+  kgdn::NormArgs a{x, g, weight, bias, y, rstd, x_dtype, g_dtype, w_dtype, rows, (int)D, eps,
+                   activation == KAIROS_GDN_ACT_SIGMOID ? 1 : 0};
+  if (int rc = from_launch(kgdn::launch_rmsnorm_gated(a, static_cast<hipStream_t>(stream)), what)) return rc;
+  return ok();
+}
+
 }  // extern "C"

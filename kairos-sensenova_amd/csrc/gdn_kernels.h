@@ -127,6 +127,22 @@ bool seg_fwd_supported(int compute_dtype, int K, int V);
 int launch_seg_fwd(const SegFwdArgs& a, int compute_dtype, int qk_dtype, int K, int V, hipStream_t s);
 int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s);
 int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s);
+
+// Gated RMSNorm (gdn_norm.hip): y = x rstd w [+ b] * act(g) per row of D.
+struct NormArgs {
+  const void* x;          // [rows, D] x_dtype
+  const void* g;          // [rows, D] g_dtype
+  const void* w;          // [D] w_dtype or nullptr
+  const void* b;          // [D] w_dtype or nullptr
+  void* y;                // [rows, D] x_dtype
+  float* rstd;            // [rows] or nullptr
+  int x_dtype, g_dtype, w_dtype;
+  int64_t rows;
+  int D;
+  float eps;
+  int sigmoid_only;       // 0: y *= g sigmoid(g) (swish / silu); 1: y *= sigmoid(g)
+};
+int launch_rmsnorm_gated(const NormArgs& a, hipStream_t s);
 int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s);
 int launch_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu, const int32_t* chunk_off, int N,
                   int64_t T, int H, int64_t nc_grid, hipStream_t s);

@@ -13,6 +13,7 @@ LIB_NAME = "libkairos_gdn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 F32, BF16, F8E4M3 = 0, 1, 2
+ACT_SWISH, ACT_SIGMOID = 0, 1
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, EHIP = 0, 1, 2, 3, 4
 ABI_VERSION = 1
 
@@ -40,6 +41,7 @@ SIGNATURES = {
     "kairos_gdn_fwd_o": (_i, [_p, _p, _fp, _fp, _p, _p, _fp, _p, _f, _p, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i, _i, _p, _sz, _p]),
     "kairos_gdn_l2norm_fwd": (_i, [_p, _p, _i, _i64, _i64, _p]),
+    "kairos_gdn_rms_norm_gated": (_i, [_p, _p, _p, _p, _p, _fp, _i, _i, _i, _i64, _i64, _f, _i, _p]),
     "kairos_gdn_segment_chunks": (_i, [_i64, _i64, _i64, _i64]),
     "kairos_gdn_profile_begin": (_i, []),
     "kairos_gdn_profile_end": (_i, [ctypes.POINTER(ctypes.c_double), _i]),

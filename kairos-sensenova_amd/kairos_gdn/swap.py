@@ -1,20 +1,24 @@
-"""Swap the reference op for the MI355X one, in place.
+"""Swap the reference op (and the layer's output norm) for the MI355X ones, in place.
 
 The reference's GDN layers bind the op by name at import time
 (``from ...gated_delta_rule import chunk_gated_delta_rule`` in
 fla/layers/gated_deltanet.py:16 and gated_deltanet_with_tp.py:17), the same
 way Kairos' own engine swap monkey-patches the DiT (kairos_ext/kairos_engine_patch.py:1773).
-``install()`` rebinds that name in every already-imported module that holds
-it, so the layers call this build's kernels; ``uninstall()`` restores the
-originals.
+The layer's output norm class is bound the same way
+(``from ...modules import FusedRMSNormGated``, gated_deltanet.py:15) and
+instantiated in the layer's constructor (:197).  ``install()`` rebinds those
+names in every already-imported module that holds them, so the layers call
+this build's kernels (layers constructed afterwards get the MI355X norm);
+``uninstall()`` restores the originals.
 """
 from __future__ import annotations
 
 import sys
 
 from .chunk import chunk_gated_delta_rule
+from .norm import FusedRMSNormGated
 
-# module names (pip fla and the copy vendored under kairos/third_party) that bind the op
+# module names (pip fla and the copy vendored under kairos/third_party) that bind the op or the norm
 SITES = (
     "fla.ops.gated_delta_rule",
     "fla.ops.gated_delta_rule.chunk",
@@ -25,34 +29,42 @@ SITES = (
     "kairos.third_party.fla.layers.gated_deltanet",
     "kairos.third_party.fla.layers.gated_deltanet_with_tp",
 )
+# the names install() rebinds, with their replacements
+REPLACEMENTS = {
+    "chunk_gated_delta_rule": chunk_gated_delta_rule,
+    "FusedRMSNormGated": FusedRMSNormGated,
+}
 
-_saved: dict[str, object] = {}
+_saved: dict[tuple[str, str], object] = {}
 
 
-def install(sites=SITES) -> list[str]:
-    """Rebind ``chunk_gated_delta_rule`` in the imported modules among ``sites``; returns the patched names."""
+def install(sites=SITES, names=tuple(REPLACEMENTS)) -> list[str]:
+    """Rebind ``names`` (default: the op and the norm class) in the imported modules among
+    ``sites``; returns the patched ``module.name`` entries."""
     patched = []
-    for name in sites:
-        mod = sys.modules.get(name)
-        if mod is None or not hasattr(mod, "chunk_gated_delta_rule"):
+    for mod_name in sites:
+        mod = sys.modules.get(mod_name)
+        if mod is None:
             continue
-        cur = getattr(mod, "chunk_gated_delta_rule")
-        if cur is chunk_gated_delta_rule:
-            patched.append(name)
-            continue
-        _saved.setdefault(name, cur)
-        setattr(mod, "chunk_gated_delta_rule", chunk_gated_delta_rule)
-        patched.append(name)
+        for attr in names:
+            if not hasattr(mod, attr):
+                continue
+            new = REPLACEMENTS[attr]
+            cur = getattr(mod, attr)
+            if cur is not new:
+                _saved.setdefault((mod_name, attr), cur)
+                setattr(mod, attr, new)
+            patched.append(f"{mod_name}.{attr}")
     return patched
 
 
 def uninstall() -> list[str]:
-    """Restore every binding ``install`` replaced; returns the restored names."""
+    """Restore every binding ``install`` replaced; returns the restored ``module.name`` entries."""
     restored = []
-    for name, fn in list(_saved.items()):
-        mod = sys.modules.get(name)
+    for (mod_name, attr), obj in list(_saved.items()):
+        mod = sys.modules.get(mod_name)
         if mod is not None:
-            setattr(mod, "chunk_gated_delta_rule", fn)
-            restored.append(name)
-        del _saved[name]
+            setattr(mod, attr, obj)
+            restored.append(f"{mod_name}.{attr}")
+        del _saved[(mod_name, attr)]
     return restored

@@ -20,6 +20,8 @@ It restates, stage by stage, the reference op
   chunk_gated_delta_rule     ops/gated_delta_rule/chunk.py:16-67, :149-186, :217-323
   naive_recurrent            ops/gated_delta_product/naive.py:23-35 (num_householder=1),
                              ops/gated_delta_rule/fused_recurrent.py:88-119
+  rms_norm_gated             modules/fused_norm_gate.py:42-127 (RMS path, no residual),
+                             the layer's output epilogue (layers/gated_deltanet.py:197,311)
 
 Precision model (``dtype`` argument):
   "bf16"  storage values are bf16 held in float32 arrays; every cast point of
@@ -49,6 +51,11 @@ How each function is pinned (tests/test_oracle.py):
                          gives exact recall S^T k_t = v_t; a hand-computed
                          two-token case.
   l2norm                 closed form x / sqrt(sum x^2 + eps).
+  rms_norm_gated         torch.nn.functional.rms_norm times silu / sigmoid of the
+                         gate (library routines, fp64); closed forms: g = 0 gives
+                         0 (swish) or half the normalised row (sigmoid), a
+                         constant row normalises to sign * |c| / sqrt(c^2 + eps),
+                         scaling x leaves y unchanged when eps = 0.
 Every function above has at least one such check: no function is left
 "parity unpinned".
 """
@@ -64,7 +71,7 @@ __all__ = [
     "CHUNK", "to_bf16", "cast", "seq_spans", "l2norm", "chunk_local_cumsum",
     "chunk_scaled_dot_kkt", "solve_tril", "recompute_w_u", "chunk_fwd_h",
     "chunk_fwd_o", "chunk_gated_delta_rule", "naive_recurrent", "rel_l2",
-    "fp8_e4m3_quantize", "fp8_e4m3_decode",
+    "fp8_e4m3_quantize", "fp8_e4m3_decode", "rms_norm_gated",
 ]
 
 
@@ -293,6 +300,32 @@ def _fwd_o_c(cm, qc, kc, vnc, h, gcc, scale, f, dtype):
 # ----------------------------------------------------------------------------
 # public stages ([B, T, H, ...] layout, as the reference's stage functions)
 # ----------------------------------------------------------------------------
+def rms_norm_gated(x, g, weight=None, bias=None, activation: str = "swish", eps: float = 1e-6,
+                   dtype: str = "fp32"):
+    """Gated RMSNorm over the last axis (fused_norm_gate.py:42-127 with
+    IS_RMS_NORM, no residual): x and g upcast, rstd = 1/sqrt(mean(x^2) + eps)
+    (:83-89), y = x rstd [* w] [+ b] (:94-100), then y * g * sigmoid(g) for
+    'swish'/'silu' or y * sigmoid(g) for 'sigmoid' (:102-108); y stored in
+    ``dtype`` (the input's storage dtype).  Returns (y, rstd)."""
+    f = _f(dtype)
+    xf = np.asarray(x, f)
+    gf = np.asarray(g, f)
+    rstd = (1.0 / np.sqrt(np.mean(xf * xf, axis=-1) + eps)).astype(f)
+    y = xf * rstd[..., None]
+    if weight is not None:
+        y = y * np.asarray(weight, f)
+    if bias is not None:
+        y = y + np.asarray(bias, f)
+    sig = 1.0 / (1.0 + np.exp(-gf))
+    if activation in ("swish", "silu"):
+        y = y * gf * sig
+    elif activation == "sigmoid":
+        y = y * sig
+    else:
+        raise ValueError(f"Unsupported activation: {activation}")
+    return cast(y, dtype), rstd
+
+
 def l2norm(x, eps: float = 1e-6, dtype: str = "fp32") -> np.ndarray:
     """y = x / sqrt(sum(x^2) + eps) along the last axis (l2norm.py:114-118), stored in ``dtype``."""
     xf = np.asarray(x, _f(dtype))

@@ -171,20 +171,31 @@ def test_backward_is_refused():
 def test_swap_rebinds_and_restores(monkeypatch):
     def reference_op(*a, **k):
         return "reference"
+
+    class ReferenceNorm:
+        pass
     layer = types.ModuleType("fla.layers.gated_deltanet")
     layer.chunk_gated_delta_rule = reference_op
+    layer.FusedRMSNormGated = ReferenceNorm
     vendored = types.ModuleType("kairos.third_party.fla.ops.gated_delta_rule")
     vendored.chunk_gated_delta_rule = reference_op
     monkeypatch.setitem(sys.modules, "fla.layers.gated_deltanet", layer)
     monkeypatch.setitem(sys.modules, "kairos.third_party.fla.ops.gated_delta_rule", vendored)
     patched = kairos_gdn.swap.install()
-    assert set(patched) == {"fla.layers.gated_deltanet", "kairos.third_party.fla.ops.gated_delta_rule"}
+    assert set(patched) == {"fla.layers.gated_deltanet.chunk_gated_delta_rule",
+                            "fla.layers.gated_deltanet.FusedRMSNormGated",
+                            "kairos.third_party.fla.ops.gated_delta_rule.chunk_gated_delta_rule"}
     assert layer.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
+    assert layer.FusedRMSNormGated is kairos_gdn.FusedRMSNormGated
     assert vendored.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
     assert kairos_gdn.swap.install() == patched                  # idempotent
     restored = kairos_gdn.swap.uninstall()
     assert set(restored) == set(patched)
     assert layer.chunk_gated_delta_rule is reference_op
+    assert layer.FusedRMSNormGated is ReferenceNorm
+    patched = kairos_gdn.swap.install(names=("chunk_gated_delta_rule",))   # the op alone
+    assert layer.FusedRMSNormGated is ReferenceNorm and layer.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
+    kairos_gdn.swap.uninstall()
 
 
 # ---------------------------------------------------------------------------
