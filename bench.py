@@ -8,6 +8,7 @@ output_final_state=True) with inputs resident in HBM, through the C ABI
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
   python bench.py --calibrate-copy 1024     # reference copy kernel for rocprofv3 counter scaling
   python bench.py --epilogue                # the gated RMSNorm output epilogue on config 2's o
+  python bench.py --model-shape             # the Kairos 4B layer's head dims dk=256, dv=512
 
 `value` is tokens/s of whole forward calls (wall clock between two device
 synchronisations around `steps` back-to-back calls).  Per-kernel times come
@@ -192,6 +193,48 @@ def bench_epilogue(args, dev):
     }), flush=True)
 
 
+def bench_model_shape(args, dev):
+    """The Kairos 4B layer's own head dims (GatedDeltaNet(hidden_size=2560, num_heads=20) with the
+    layer defaults head_dim=256, expand_v=2): B=1, H=20, K=256, V=512 at the headline T, bf16.
+    These dims run the stage kernels (prepare -> fwd_h -> fwd_o) with the reference's
+    intermediates; FLOPs counted as for the headline metric (every MMA tile at full size)."""
+    from kairos_gdn import _lib
+    B, T, H, K, V = 1, args.T, 20, 256, 512
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20270, dev)
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty_like(v)
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def step():
+        _lib.call("kairos_gdn_chunk_fwd", P(q), P(k), P(v), P(g), P(beta), None, None, P(h0), P(o), P(ht), None, 0,
+                  B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, P(ws), ws_bytes,
+                  sp)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    tflops = B * T * H * flops_per_tok_head(K, V) / wall / 1e12
+    nbytes = B * T * H * (2 * K * 2 + 2 * V * 2 + 4 + 2) + 2 * B * H * K * V * 4
+    print(json.dumps({
+        "metric": "GDN chunk-fwd tokens/s at the Kairos 4B layer shape T=32760,H=20,dk=256,dv=512", "value": T / wall,
+        "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"chunk_gated_delta_rule fwd B={B} T={T} H={H} dk={K} dv={V} chunk 64, bf16 "
+                               "q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM (stage kernels)"},
+        "tflops": tflops, "mfma_peak_frac": tflops / PEAK_BF16_TFLOPS,
+        "hbm_gbs_whole_op": nbytes / wall / 1e9,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +248,9 @@ def main():
     ap.add_argument("--epilogue", action="store_true",
                     help="measure only the gated RMSNorm epilogue (kairos_gdn_rms_norm_gated) on o-shaped rows "
                          "[T*H, V] bf16 with a bf16 gate and fp32 weight; prints its own JSON line")
+    ap.add_argument("--model-shape", action="store_true",
+                    help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T; prints its own "
+                         "JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -227,6 +273,9 @@ def main():
     from kairos_gdn import _lib
     if args.epilogue:
         bench_epilogue(args, dev)
+        return
+    if args.model_shape:
+        bench_model_shape(args, dev)
         return
     B, T, H, K, V = 1, args.T, 20, 128, 128
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)

@@ -22,7 +22,10 @@
  *    bf16 q/k/v (or fp8 q/k with bf16 v) run the bf16 path; fp32 q/k/v the
  *    fp32 path.  g is fp32 or bf16; beta fp32 or bf16; initial_state fp32 or
  *    bf16; final_state is always fp32.
- *  - Supported head dims: K in {64, 128}, V in {64, 128}.
+ *  - Supported head dims: K in {64, 128, 256}; V a multiple of 16, at most
+ *    1024 (the Kairos 4B layer runs K = 256, V = 512).  bf16 with K, V in
+ *    {64, 128} runs the segment-parallel fused kernels; every other shape runs
+ *    the stage kernels in sequence.
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *    is stream-ordered: no entry point synchronises or allocates.  Scratch
  *    memory comes from the caller's `workspace`.  Entry points are reentrant;

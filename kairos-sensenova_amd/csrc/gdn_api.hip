@@ -242,7 +242,8 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
 
 // Staged forward: prepare (gc, w, u) -> fwd_h (h, v_new, ht) -> fwd_o (o), the
 // reference's stage order with its intermediates in the workspace.  Used for the
-// shapes the fused kernels do not cover (fp32 with K = 128).
+// shapes the fused kernels do not cover: fp32, and the Kairos model's head dims
+// K = 256, V = 512 (any K in {64, 128, 256} with V a multiple of 16).
 int run_staged(const Geometry& G, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
                const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
@@ -322,9 +323,10 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
     return fail(KAIROS_GDN_EINVAL, "%s: fp8 q/k need per-head q_scale and k_scale", what);
   if (qk_dtype == KAIROS_GDN_F8E4M3 && use_qk_l2norm)
     return fail(KAIROS_GDN_EUNSUPPORTED, "%s: the in-kernel L2 norm is not available for fp8 q/k", what);
-  if (!(K == 64 || K == 128) || !(V == 64 || V == 128))
-    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: head dims K=%lld V=%lld are not built (K, V in {64, 128})", what,
-                (long long)K, (long long)V);
+  if (!(K == 64 || K == 128 || K == 256) || V % 16 != 0 || V > 1024)
+    return fail(KAIROS_GDN_EUNSUPPORTED,
+                "%s: head dims K=%lld V=%lld are not built (K in {64, 128, 256}, V a multiple of 16 up to 1024)",
+                what, (long long)K, (long long)V);
   if (!std::isfinite(scale)) return fail(KAIROS_GDN_EINVAL, "%s: scale must be finite", what);
   const bool any_tokens = G.B * G.T > 0;
   if (any_tokens && (!q || !k || !v || !g || !beta || !o))

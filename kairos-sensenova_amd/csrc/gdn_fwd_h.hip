@@ -282,11 +282,11 @@ int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V
   if (V % BV != 0 || a.N * a.H == 0) return -2;
 #define KGDN_H_CASE(TC, TK, KK) \
   if (K == KK) return launch_fwd_h_t<TC, TK, KK>(a, V, s);
-  if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_H_CASE(float, float, 64) KGDN_H_CASE(float, float, 128) }
-  if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_H_CASE(bf16, bf16, 64) KGDN_H_CASE(bf16, bf16, 128) }
-  if (compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) {
-    KGDN_H_CASE(bf16, uint8_t, 64) KGDN_H_CASE(bf16, uint8_t, 128)
-  }
+#define KGDN_H_SHAPES(TC, TK) KGDN_H_CASE(TC, TK, 64) KGDN_H_CASE(TC, TK, 128) KGDN_H_CASE(TC, TK, 256)
+  if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_H_SHAPES(float, float) }
+  if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_H_SHAPES(bf16, bf16) }
+  if (compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) { KGDN_H_SHAPES(bf16, uint8_t) }
+#undef KGDN_H_SHAPES
 #undef KGDN_H_CASE
   return -2;
 }

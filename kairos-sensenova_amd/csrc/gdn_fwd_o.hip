@@ -151,11 +151,11 @@ int launch_fwd_o(const FwdOArgs& a, int compute_dtype, int qk_dtype, int K, int 
   if (V % 16 != 0) return -2;
 #define KGDN_O_CASE(TC, TQ, KK) \
   if (K == KK) return launch_fwd_o_t<TC, TQ, KK>(a, V, nc_grid, s);
-  if (compute_dtype == DT_F32 && qk_dtype == DT_F32) { KGDN_O_CASE(float, float, 64) KGDN_O_CASE(float, float, 128) }
-  if (compute_dtype == DT_BF16 && qk_dtype == DT_BF16) { KGDN_O_CASE(bf16, bf16, 64) KGDN_O_CASE(bf16, bf16, 128) }
-  if (compute_dtype == DT_BF16 && qk_dtype == DT_F8E4M3) {
-    KGDN_O_CASE(bf16, uint8_t, 64) KGDN_O_CASE(bf16, uint8_t, 128)
-  }
+#define KGDN_O_SHAPES(TC, TQ) KGDN_O_CASE(TC, TQ, 64) KGDN_O_CASE(TC, TQ, 128) KGDN_O_CASE(TC, TQ, 256)
+  if (compute_dtype == DT_F32 && qk_dtype == DT_F32) { KGDN_O_SHAPES(float, float) }
+  if (compute_dtype == DT_BF16 && qk_dtype == DT_BF16) { KGDN_O_SHAPES(bf16, bf16) }
+  if (compute_dtype == DT_BF16 && qk_dtype == DT_F8E4M3) { KGDN_O_SHAPES(bf16, uint8_t) }
+#undef KGDN_O_SHAPES
 #undef KGDN_O_CASE
   return -2;
 }

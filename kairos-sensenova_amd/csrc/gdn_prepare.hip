@@ -20,29 +20,38 @@ namespace {
 
 constexpr int NT_PREP = 256;   // 4 waves
 
-template <typename TC, int K, int V>
+// LDS plan.  Region 0 holds k row-major for K.K^T; once A is formed it is
+// reused for the rounded inverse Ai and, after it, the v^T pass buffer: v is
+// staged VP columns at a time (u is separable over V), so V = 512 fits.
+template <typename TC, int K>
 struct PrepLds {
   static constexpr int LDK = K + 8;      // s_k row stride (elements)
   static constexpr int LDT = C + 8;      // transposed tiles / Ai row stride
   static constexpr int LDA = C + 4;      // fp32 A / inverse row stride
   static constexpr size_t k_bytes = sizeof(TC) * C * LDK;
-  static constexpr size_t ai_bytes = sizeof(TC) * C * LDT;
-  static constexpr size_t region0 = k_bytes > ai_bytes ? k_bytes : ai_bytes;   // s_k, later s_Ai
-  static constexpr size_t off_kbT = (region0 + 15) / 16 * 16;
-  static constexpr size_t off_vbT = off_kbT + sizeof(TC) * K * LDT;
-  static constexpr size_t off_A = off_vbT + sizeof(TC) * V * LDT;
+  static constexpr size_t ai_bytes = (sizeof(TC) * C * LDT + 15) / 16 * 16;
+  static constexpr size_t fixed = sizeof(TC) * K * LDT + sizeof(float) * C * LDA + sizeof(float) * 3 * C;
+  static constexpr size_t region0_for(int vp) {
+    return k_bytes > ai_bytes + sizeof(TC) * vp * LDT ? k_bytes : ai_bytes + sizeof(TC) * vp * LDT;
+  }
+  static constexpr int VP = region0_for(256) + fixed <= 160 * 1024 ? 256
+                          : region0_for(128) + fixed <= 160 * 1024 ? 128 : 64;   // v columns per pass
+  static constexpr size_t region0 = (region0_for(VP) + 15) / 16 * 16;
+  static constexpr size_t off_vbT = ai_bytes;                   // inside region 0, after Ai
+  static constexpr size_t off_kbT = region0;
+  static constexpr size_t off_A = off_kbT + sizeof(TC) * K * LDT;
   static constexpr size_t off_g = off_A + sizeof(float) * C * LDA;
   static constexpr size_t total = off_g + sizeof(float) * 3 * C;
 };
 
-template <typename TC, typename TK, int K, int V>
-__global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a) {
-  using L = PrepLds<TC, K, V>;
+template <typename TC, typename TK, int K>
+__global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) {
+  using L = PrepLds<TC, K>;
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_k = reinterpret_cast<TC*>(smem);
   TC* s_Ai = reinterpret_cast<TC*>(smem);                 // aliases s_k once K.K^T is done
+  TC* s_vbT = reinterpret_cast<TC*>(smem + L::off_vbT);   // aliases s_k too (after Ai)
   TC* s_kbT = reinterpret_cast<TC*>(smem + L::off_kbT);
-  TC* s_vbT = reinterpret_cast<TC*>(smem + L::off_vbT);
   float* s_A = reinterpret_cast<float*>(smem + L::off_A);
   float* s_g = reinterpret_cast<float*>(smem + L::off_g);
   float* s_eg = s_g + C;
@@ -78,8 +87,8 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a) {
   }
   __syncthreads();
 
-  // ---- stage k (row-major, for K.K^T) and the transposed, scaled operands
-  //      kb^T[d][t] = k*beta*exp(gc), vb^T[v][t] = v*beta
+  // ---- stage k (row-major, for K.K^T) and the transposed, scaled operand
+  //      kb^T[d][t] = k*beta*exp(gc)
   const float kscale = a.k_scale ? a.k_scale[h] : 1.f;
   const TK* kin = reinterpret_cast<const TK*>(a.k);
   for (int idx = tid; idx < C * (K / 8); idx += NT_PREP) {
@@ -102,14 +111,6 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a) {
       s_kbT[(c8 + e) * L::LDT + r] = from_f32<TC>(kb * eg);
     }
     st8<TC>(s_k + r * L::LDK + c8, row);
-  }
-  const TC* vin = reinterpret_cast<const TC*>(a.v);
-  for (int idx = tid; idx < C * (V / 8); idx += NT_PREP) {
-    const int r = idx / (V / 8), c8 = (idx % (V / 8)) * 8;
-    Vec8<TC> x = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + c8) : vzero<TC>();
-    const float b = s_b[r];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s_vbT[(c8 + e) * L::LDT + r] = from_f32<TC>(vget<TC>(x, e) * b);
   }
   __syncthreads();
 
@@ -223,32 +224,47 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a) {
       if (t < nv) st4<TC>(w_out + ((t0 + t) * H + h) * K + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
     }
   }
-  // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane
+  // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
+  //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 (k is dead,
+  //      Ai sits below the pass buffer), so staging overlaps the w products above
+  const TC* vin = reinterpret_cast<const TC*>(a.v);
   TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
-  for (int tn = wid; tn < V / 16; tn += 4) {
+  for (int p0 = 0; p0 < V; p0 += L::VP) {
+    const int vw = min(L::VP, V - p0);             // a multiple of 16
+    for (int idx = tid; idx < C * (vw / 8); idx += NT_PREP) {
+      const int r = idx / (vw / 8), c8 = (idx % (vw / 8)) * 8;
+      Vec8<TC> x = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + p0 + c8) : vzero<TC>();
+      const float b = s_b[r];
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks <= tm / 2; ++ks)
-        mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_vbT, L::LDT, 16 * tn, 32 * ks));
-      st4<TC>(uT + (16 * tn + lc) * C + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
+      for (int e = 0; e < 8; ++e) s_vbT[(c8 + e) * L::LDT + r] = from_f32<TC>(vget<TC>(x, e) * b);
     }
+    __syncthreads();
+    for (int tn = wid; tn < vw / 16; tn += 4) {
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks <= tm / 2; ++ks)
+          mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_vbT, L::LDT, 16 * tn, 32 * ks));
+        st4<TC>(uT + (p0 + 16 * tn + lc) * C + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
+      }
+    }
+    if (p0 + L::VP < V) __syncthreads();           // the next pass overwrites vb^T
   }
 }
 
-template <typename TC, typename TK, int K, int V>
-int launch_prepare_t(const PrepareArgs& a, int64_t nc_grid, hipStream_t s) {
-  using L = PrepLds<TC, K, V>;
+template <typename TC, typename TK, int K>
+int launch_prepare_t(const PrepareArgs& a, int V, int64_t nc_grid, hipStream_t s) {
+  using L = PrepLds<TC, K>;
   static_assert(L::total <= 160 * 1024, "prepare tile does not fit in LDS");
-  auto kern = prepare_kernel<TC, TK, K, V>;
+  auto kern = prepare_kernel<TC, TK, K>;
   if (L::total > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)L::total) != hipSuccess)
       return -1;
   }
   dim3 grid((unsigned)nc_grid, (unsigned)a.H);
-  hipLaunchKernelGGL(kern, grid, dim3(NT_PREP), L::total, s, a);
+  hipLaunchKernelGGL(kern, grid, dim3(NT_PREP), L::total, s, a, V);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -256,11 +272,10 @@ int launch_prepare_t(const PrepareArgs& a, int64_t nc_grid, hipStream_t s) {
 
 int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, int V, int64_t nc_grid,
                    hipStream_t s) {
-#define KGDN_PREP_CASE(TC, TK, KK, VV) \
-  if (K == KK && V == VV) return launch_prepare_t<TC, TK, KK, VV>(a, nc_grid, s);
-#define KGDN_PREP_SHAPES(TC, TK) \
-  KGDN_PREP_CASE(TC, TK, 64, 64) KGDN_PREP_CASE(TC, TK, 64, 128) \
-  KGDN_PREP_CASE(TC, TK, 128, 64) KGDN_PREP_CASE(TC, TK, 128, 128)
+  if (V <= 0 || V % 16 != 0) return -2;
+#define KGDN_PREP_CASE(TC, TK, KK) \
+  if (K == KK) return launch_prepare_t<TC, TK, KK>(a, V, nc_grid, s);
+#define KGDN_PREP_SHAPES(TC, TK) KGDN_PREP_CASE(TC, TK, 64) KGDN_PREP_CASE(TC, TK, 128) KGDN_PREP_CASE(TC, TK, 256)
   if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_PREP_SHAPES(float, float) }
   if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_PREP_SHAPES(bf16, bf16) }
   if (compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) { KGDN_PREP_SHAPES(bf16, uint8_t) }

@@ -94,6 +94,8 @@ def chunk_fwd_rc(**over):
     (dict(B=0), _lib.EINVAL, "invalid shape"),
     (dict(K=512), _lib.EINVAL, "larger than 256"),
     (dict(K=96), _lib.EUNSUPPORTED, "not built"),
+    (dict(K=256, V=520), _lib.EUNSUPPORTED, "multiple of 16"),
+    (dict(K=256, V=2048), _lib.EUNSUPPORTED, "not built"),
     (dict(B=2, cu=FAKE, n_seqs=1), _lib.EINVAL, "batch size is expected to be 1"),
     (dict(cu=FAKE, n_seqs=0), _lib.EINVAL, "given together"),
     (dict(qk=_lib.F8E4M3), _lib.EINVAL, "q_scale"),

@@ -105,6 +105,12 @@ PREP_CASES = [
     ("bf16", 1, 400, 2, 128, 64, [0, 10, 74, 74, 260, 400]),
     ("fp32", 1, 200, 2, 64, 64, None),
     ("fp32", 1, 150, 2, 128, 128, [0, 100, 150]),
+    # Kairos model head dims (K = 256, V = 512): v staged in two 256-column passes
+    ("bf16", 1, 200, 2, 256, 512, None),
+    # fp32 K = 256 at the LDS limit: 128-column passes
+    ("fp32", 1, 130, 1, 256, 256, None),
+    # V = 320: a ragged last pass of 64 columns
+    ("bf16", 1, 150, 2, 128, 320, [0, 70, 150]),
 ]
 
 
@@ -141,6 +147,8 @@ H_CASES = [
     ("bf16", 2, 130, 2, 64, 64, None, False),
     ("bf16", 1, 500, 2, 128, 128, [0, 63, 64, 64, 300, 500], True),
     ("fp32", 1, 260, 2, 64, 64, None, True),
+    ("bf16", 1, 300, 2, 256, 512, None, True),
+    ("fp32", 1, 150, 1, 256, 128, [0, 20, 150], True),
 ]
 
 
@@ -214,6 +222,12 @@ EDGE_CASES = [
     ("bf16", 1, 700, 3, 64, 128, [0, 1, 1, 129, 640, 700], False, True),
     ("bf16", 2, 100, 2, 64, 64, None, False, False),
     ("fp32", 2, 300, 2, 128, 128, None, False, True),
+    # the Kairos 4B layer's head dims and its in-kernel L2 norm (GatedDeltaNet defaults
+    # head_dim=256, expand_v=2: layers/gated_deltanet.py:90-93,122-123)
+    ("bf16", 1, 300, 2, 256, 512, None, True, True),
+    ("bf16", 1, 400, 2, 256, 512, [0, 1, 130, 400], False, True),
+    ("fp32", 1, 200, 1, 256, 256, None, False, True),
+    ("bf16", 2, 150, 2, 128, 48, None, False, True),
 ]
 
 
@@ -276,6 +290,17 @@ def test_baseline_config_full_size(cfg, heads):
     o, ht = run_gpu(x, c["dtype"], cu=cu)
     assert bool(torch.isfinite(o).all()) and bool(torch.isfinite(ht).all())
     check_against_oracle(x, c["dtype"], o, ht, cu=cu, heads=heads)
+
+
+def test_model_shape_full_size():
+    """The Kairos 4B layer at the headline clip length: H=20, K=256, V=512, T=32760, bf16."""
+    B, T, H, K, V = 1, 32760, 20, 256, 512
+    heads = [0, 19]
+    note(f"model shape B={B} T={T} H={H} K={K} V={V} (oracle on heads {heads})")
+    x = make_inputs(B, T, H, K, V, seed=20270, dtype="bf16")
+    o, ht = run_gpu(x, "bf16")
+    assert bool(torch.isfinite(o).all()) and bool(torch.isfinite(ht).all())
+    check_against_oracle(x, "bf16", o, ht, heads=heads)
 
 
 # ---------------------------------------------------------------------------
