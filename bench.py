@@ -9,6 +9,7 @@ output_final_state=True) with inputs resident in HBM, through the C ABI
   python bench.py --calibrate-copy 1024     # reference copy kernel for rocprofv3 counter scaling
   python bench.py --epilogue                # the gated RMSNorm output epilogue on config 2's o
   python bench.py --model-shape             # the Kairos 4B layer's head dims dk=256, dv=512
+  python bench.py --recurrent               # the short-sequence mode's decoding step (fused_recurrent)
 
 `value` is tokens/s of whole forward calls (wall clock between two device
 synchronisations around `steps` back-to-back calls).  Per-kernel times come
@@ -235,6 +236,48 @@ def bench_model_shape(args, dev):
     }), flush=True)
 
 
+def bench_recurrent(args, dev):
+    """Decoding step of the layer's short-sequence mode (fused_recurrent_gated_delta_rule, q_len <= 64):
+    B=8 streams, one token each, at the Kairos 4B layer's head dims (H=20, K=256, V=512), bf16 q/k/v,
+    fp32 state carried in and out.  Algorithmic bytes = state read + write (2 * B*H*K*V*4) + the
+    token's q, k, v, o, g, beta; the kernel is bound by the two state passes in HBM."""
+    from kairos_gdn import _lib
+    B, T, H, K, V = 8, 1, 20, 256, 512
+    q, k, v, g, beta, _ = make_inputs(B, T, H, K, V, 20271, dev)
+    h0 = (0.02 * torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(1))).to(dev)
+    o = torch.empty_like(v)
+    ht = torch.empty_like(h0)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def step():
+        _lib.call("kairos_gdn_fused_recurrent_fwd", P(q), P(k), P(v), P(g), None, None, P(beta), P(h0), P(o), P(ht),
+                  None, 0, B, T, H, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.F32, _lib.F32, _lib.BF16, 1, _lib.F32,
+                  K ** -0.5, 1, sp)
+
+    for _ in range(args.warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = 2 * B * H * K * V * 4 + B * T * H * (2 * K * 2 + 2 * V * 2 + 4 + 2)
+    gbs = nbytes / (ms / 1e3) / 1e9
+    print(json.dumps({
+        "metric": "GDN fused_recurrent decode step (B=8, T=1, H=20, dk=256, dv=512) GB/s", "value": gbs,
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "fused_recurrent_gated_delta_rule fwd, 8 streams x 1 token, H=20 dk=256 dv=512, "
+                               "bf16 q/k/v/beta, fp32 g and state, in-kernel q/k L2 norm, state in HBM"},
+        "roofline": {"bound": "hbm", "kernel": "fused_recurrent_kernel", "achieved": gbs, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,6 +294,9 @@ def main():
     ap.add_argument("--model-shape", action="store_true",
                     help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T; prints its own "
                          "JSON line")
+    ap.add_argument("--recurrent", action="store_true",
+                    help="measure the short-sequence mode's decoding step (kairos_gdn_fused_recurrent_fwd, 8 streams "
+                         "x 1 token at dk=256, dv=512); prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -276,6 +322,9 @@ def main():
         return
     if args.model_shape:
         bench_model_shape(args, dev)
+        return
+    if args.recurrent:
+        bench_recurrent(args, dev)
         return
     B, T, H, K, V = 1, args.T, 20, 128, 128
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)

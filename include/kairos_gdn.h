@@ -160,6 +160,24 @@ int kairos_gdn_rms_norm_gated(const void* x, const void* g, const void* weight, 
                               float* rstd, int x_dtype, int g_dtype, int w_dtype, int64_t rows, int64_t D,
                               float eps, int activation, void* stream);
 
+/* ---- short-sequence mode -------------------------------------------------
+ * Token-by-token gated delta rule in fp32, replacing
+ * fused_recurrent_gated_delta_rule_fwd (fla ops/gated_delta_rule/fused_recurrent.py:138-185,
+ * kernel :21-135), the layer's mode for q_len <= 64 (layers/gated_deltanet.py:220).
+ * q, k [B, T, H, K] (fp32 or bf16, 16-byte aligned); v [B, T, HV, V] with HV a
+ * multiple of H (q/k head i_hv / (HV / H) serves value head i_hv); optional
+ * gates g [B, T, HV], gk [B, T, HV, K], gv [B, T, HV, V] (log space, fp32 or
+ * bf16, NULL = absent); beta [B, T, HV] (beta_headwise = 1) or [B, T, HV, V]
+ * (beta_headwise = 0), NULL = ones; initial_state [N, HV, K, V] (fp32 or bf16,
+ * NULL = zeros); o [B, T, HV, V] in v's dtype; final_state [N, HV, K, V] fp32
+ * or NULL.  K in {16, 32, 64, 128, 256}, V at most 4096.  No workspace. */
+int kairos_gdn_fused_recurrent_fwd(const void* q, const void* k, const void* v, const void* g, const void* gk,
+                                   const void* gv, const void* beta, const void* initial_state, void* o,
+                                   float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                   int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int qk_dtype,
+                                   int v_dtype, int g_dtype, int gk_dtype, int gv_dtype, int beta_dtype,
+                                   int beta_headwise, int h0_dtype, float scale, int use_qk_l2norm, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

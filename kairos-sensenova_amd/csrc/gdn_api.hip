@@ -585,4 +585,40 @@ int kairos_gdn_rms_norm_gated(const void* x, const void* g, const void* weight, 
   return ok();
 }
 
+int kairos_gdn_fused_recurrent_fwd(const void* q, const void* k, const void* v, const void* g, const void* gk,
+                                   const void* gv, const void* beta, const void* initial_state, void* o,
+                                   float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                   int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, int qk_dtype, int v_dtype,
+                                   int g_dtype, int gk_dtype, int gv_dtype, int beta_dtype, int beta_headwise,
+                                   int h0_dtype, float scale, int use_qk_l2norm, void* stream) {
+  const char* what = "kairos_gdn_fused_recurrent_fwd";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, HV, K, V, what)) return rc;
+  if (H <= 0 || HV % H != 0)
+    return fail(KAIROS_GDN_EINVAL, "%s: the value heads HV=%lld must be a multiple of the q/k heads H=%lld", what,
+                (long long)HV, (long long)H);
+  if (!(K == 16 || K == 32 || K == 64 || K == 128 || K == 256))
+    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: K=%lld is not built (K in {16, 32, 64, 128, 256})", what,
+                (long long)K);
+  if (V > 4096) return fail(KAIROS_GDN_EUNSUPPORTED, "%s: V=%lld is larger than 4096", what, (long long)V);
+  if (!valid_scalar_dt(qk_dtype) || !valid_scalar_dt(v_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: q/k and v must be fp32 or bf16", what);
+  if ((g && !valid_scalar_dt(g_dtype)) || (gk && !valid_scalar_dt(gk_dtype)) || (gv && !valid_scalar_dt(gv_dtype)) ||
+      (beta && !valid_scalar_dt(beta_dtype)) || (initial_state && !valid_scalar_dt(h0_dtype)))
+    return fail(KAIROS_GDN_EINVAL, "%s: g, gk, gv, beta and initial_state must be fp32 or bf16", what);
+  if (!std::isfinite(scale)) return fail(KAIROS_GDN_EINVAL, "%s: scale must be finite", what);
+  if (G.B * G.T > 0 && (!q || !k || !v || !o)) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  if (!aligned16(q) || !aligned16(k))
+    return fail(KAIROS_GDN_EINVAL, "%s: q and k must be 16-byte aligned", what);
+  kgdn::RecArgs a{};
+  a.q = q; a.k = k; a.v = v; a.g = g; a.gk = gk; a.gv = gv; a.beta = beta; a.h0 = initial_state;
+  a.o = o; a.ht = final_state; a.cu = cu_seqlens; a.T = T;
+  a.N = (int)G.N; a.H = (int)H; a.HV = (int)HV; a.K = (int)K; a.V = (int)V;
+  a.qk_dtype = qk_dtype; a.v_dtype = v_dtype; a.g_dtype = g_dtype; a.gk_dtype = gk_dtype; a.gv_dtype = gv_dtype;
+  a.beta_dtype = beta_dtype; a.h0_dtype = h0_dtype; a.beta_headwise = beta_headwise ? 1 : 0;
+  a.l2 = use_qk_l2norm ? 1 : 0; a.scale = scale;
+  if (int rc = from_launch(kgdn::launch_fused_recurrent(a, static_cast<hipStream_t>(stream)), what)) return rc;
+  return ok();
+}
+
 }  // extern "C"

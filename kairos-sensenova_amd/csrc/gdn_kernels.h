@@ -143,6 +143,28 @@ struct NormArgs {
   int sigmoid_only;       // 0: y *= g sigmoid(g) (swish / silu); 1: y *= sigmoid(g)
 };
 int launch_rmsnorm_gated(const NormArgs& a, hipStream_t s);
+
+// Token-by-token gated delta rule (gdn_recurrent.hip), fused_recurrent.py:21-135.
+struct RecArgs {
+  const void* q;          // [B*T, H, K]  qk_dtype
+  const void* k;
+  const void* v;          // [B*T, HV, V] v_dtype
+  const void* g;          // [B*T, HV] g_dtype or nullptr
+  const void* gk;         // [B*T, HV, K] gk_dtype or nullptr
+  const void* gv;         // [B*T, HV, V] gv_dtype or nullptr
+  const void* beta;       // [B*T, HV] (headwise) or [B*T, HV, V], beta_dtype; nullptr = ones
+  const void* h0;         // [N, HV, K, V] h0_dtype or nullptr
+  void* o;                // out [B*T, HV, V] v_dtype
+  float* ht;              // out [N, HV, K, V] fp32 or nullptr
+  const int64_t* cu;      // varlen [N+1] or nullptr
+  int64_t T;              // tokens per sequence (fixed length)
+  int N, H, HV, K, V;
+  int qk_dtype, v_dtype, g_dtype, gk_dtype, gv_dtype, beta_dtype, h0_dtype;
+  int beta_headwise;
+  int l2;
+  float scale;
+};
+int launch_fused_recurrent(const RecArgs& a, hipStream_t s);
 int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s);
 int launch_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu, const int32_t* chunk_off, int N,
                   int64_t T, int H, int64_t nc_grid, hipStream_t s);

@@ -19,10 +19,12 @@ from .chunk import (
     prepare_wy,
 )
 from .norm import FusedRMSNormGated, rms_norm_gated, rms_norm_gated_fwd
+from .recurrent import FusedRecurrentFunction, fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_fwd
 from . import swap
 
 __all__ = [
     "CHUNK", "ChunkGatedDeltaRuleFunction", "KairosGdnError", "LIB_PATH", "chunk_gated_delta_rule",
     "chunk_gated_delta_rule_fwd", "chunk_local_cumsum", "fwd_h", "fwd_o", "l2norm_fwd", "num_chunks_bound",
     "prepare_wy", "swap", "FusedRMSNormGated", "rms_norm_gated", "rms_norm_gated_fwd",
+    "FusedRecurrentFunction", "fused_recurrent_gated_delta_rule", "fused_recurrent_gated_delta_rule_fwd",
 ]

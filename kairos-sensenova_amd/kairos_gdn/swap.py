@@ -1,7 +1,7 @@
 """Swap the reference op (and the layer's output norm) for the MI355X ones, in place.
 
-The reference's GDN layers bind the op by name at import time
-(``from ...gated_delta_rule import chunk_gated_delta_rule`` in
+The reference's GDN layers bind the ops by name at import time
+(``from ...gated_delta_rule import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule`` in
 fla/layers/gated_deltanet.py:16 and gated_deltanet_with_tp.py:17), the same
 way Kairos' own engine swap monkey-patches the DiT (kairos_ext/kairos_engine_patch.py:1773).
 The layer's output norm class is bound the same way
@@ -17,21 +17,25 @@ import sys
 
 from .chunk import chunk_gated_delta_rule
 from .norm import FusedRMSNormGated
+from .recurrent import fused_recurrent_gated_delta_rule
 
 # module names (pip fla and the copy vendored under kairos/third_party) that bind the op or the norm
 SITES = (
     "fla.ops.gated_delta_rule",
     "fla.ops.gated_delta_rule.chunk",
+    "fla.ops.gated_delta_rule.fused_recurrent",
     "fla.layers.gated_deltanet",
     "fla.layers.gated_deltanet_with_tp",
     "kairos.third_party.fla.ops.gated_delta_rule",
     "kairos.third_party.fla.ops.gated_delta_rule.chunk",
+    "kairos.third_party.fla.ops.gated_delta_rule.fused_recurrent",
     "kairos.third_party.fla.layers.gated_deltanet",
     "kairos.third_party.fla.layers.gated_deltanet_with_tp",
 )
 # the names install() rebinds, with their replacements
 REPLACEMENTS = {
     "chunk_gated_delta_rule": chunk_gated_delta_rule,
+    "fused_recurrent_gated_delta_rule": fused_recurrent_gated_delta_rule,
     "FusedRMSNormGated": FusedRMSNormGated,
 }
 
@@ -39,7 +43,7 @@ _saved: dict[tuple[str, str], object] = {}
 
 
 def install(sites=SITES, names=tuple(REPLACEMENTS)) -> list[str]:
-    """Rebind ``names`` (default: the op and the norm class) in the imported modules among
+    """Rebind ``names`` (default: both ops and the norm class) in the imported modules among
     ``sites``; returns the patched ``module.name`` entries."""
     patched = []
     for mod_name in sites:

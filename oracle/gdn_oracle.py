@@ -20,6 +20,8 @@ It restates, stage by stage, the reference op
   chunk_gated_delta_rule     ops/gated_delta_rule/chunk.py:16-67, :149-186, :217-323
   naive_recurrent            ops/gated_delta_product/naive.py:23-35 (num_householder=1),
                              ops/gated_delta_rule/fused_recurrent.py:88-119
+  fused_recurrent            ops/gated_delta_rule/fused_recurrent.py:21-135, :238-349
+                             (gk / gv decays, per-column beta, grouped value heads)
   rms_norm_gated             modules/fused_norm_gate.py:42-127 (RMS path, no residual),
                              the layer's output epilogue (layers/gated_deltanet.py:197,311)
 
@@ -50,6 +52,15 @@ How each function is pinned (tests/test_oracle.py):
   naive_recurrent        closed forms: beta=0 pure decay; beta=1, g=0, unit k
                          gives exact recall S^T k_t = v_t; a hand-computed
                          two-token case.
+  fused_recurrent        == naive_recurrent (fp64) for scalar gates and per-head
+                         beta; gk (resp. gv) equal to g broadcast over K (V)
+                         == the g path; beta = 0 closed forms S_T = diag(e^{sum gk})
+                         h0 and h0 diag(e^{sum gv}); per-column beta of equal
+                         columns == per-head beta, one-token closed form
+                         S = k (beta v)^T; grouped value heads == q/k repeated;
+                         in-kernel L2 norm == normalised inputs; planted
+                         mistakes (gk applied over V, decay after the delta,
+                         wrong q/k head for a value head) each fail one check.
   l2norm                 closed form x / sqrt(sum x^2 + eps).
   rms_norm_gated         torch.nn.functional.rms_norm times silu / sigmoid of the
                          gate (library routines, fp64); closed forms: g = 0 gives
@@ -71,7 +82,7 @@ __all__ = [
     "CHUNK", "to_bf16", "cast", "seq_spans", "l2norm", "chunk_local_cumsum",
     "chunk_scaled_dot_kkt", "solve_tril", "recompute_w_u", "chunk_fwd_h",
     "chunk_fwd_o", "chunk_gated_delta_rule", "naive_recurrent", "rel_l2",
-    "fp8_e4m3_quantize", "fp8_e4m3_decode", "rms_norm_gated",
+    "fp8_e4m3_quantize", "fp8_e4m3_decode", "rms_norm_gated", "fused_recurrent",
 ]
 
 
@@ -458,6 +469,77 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None, out
                      w=cm.scatter(wc, f), u=cm.scatter(uc, f), h=h, v_new=cm.scatter(vnc, f), q=q, k=k)
         return o, ht, inter
     return o, ht
+
+
+def _rec_heads(x, rep):
+    """q/k heads -> value heads: head h serves value heads h*rep .. h*rep+rep-1 (fused_recurrent.py:53)."""
+    return np.repeat(x, rep, axis=2)
+
+
+def _rec_decay(f, g_t, gk_t, gv_t, HV, K, V):
+    """Multiplicative decay of the [HV, K, V] state for one token (fused_recurrent.py:104-114)."""
+    d = np.ones((HV, K, V), f)
+    if g_t is not None:
+        d = d * np.exp(np.asarray(g_t, f))[:, None, None]
+    if gk_t is not None:
+        d = d * np.exp(np.asarray(gk_t, f))[:, :, None]
+    if gv_t is not None:
+        d = d * np.exp(np.asarray(gv_t, f))[:, None, :]
+    return d
+
+
+def _rec_token(S, decay, qt, kt, vt, bt):
+    """One token: decay, delta-rule write, read (fused_recurrent.py:104-122).  Returns (S, o_t)."""
+    S = S * decay
+    vp = bt * (vt - np.sum(S * kt[:, :, None], axis=1))
+    S = S + kt[:, :, None] * vp[:, None, :]
+    return S, np.sum(S * qt[:, :, None], axis=1)
+
+
+def fused_recurrent(q, k, v, g=None, gk=None, gv=None, beta=None, scale=None, initial_state=None, cu_seqlens=None,
+                    use_qk_l2norm_in_kernel=False, dtype: str = "fp32", o_dtype: str = "fp32"):
+    """The short-sequence mode fused_recurrent_gated_delta_rule (fused_recurrent.py:21-135, :238-349),
+    restated per token in ``dtype`` arithmetic ("fp32" as the kernel, or "fp64"):
+
+        q, k <- [l2-normalised];  q <- q * scale
+        S <- S * exp(g) * exp(gk)[:, None] * exp(gv)[None, :]     (each decay optional)
+        v' = beta * (v - S^T k)                                    (beta per head or per column)
+        S <- S + k v'^T ;  o = S^T q   (o rounded to ``o_dtype``, v's storage dtype)
+    Shapes: q, k [B, T, H, K]; v [B, T, HV, V], HV a multiple of H, q/k head
+    hv // (HV // H) serving value head hv (fused_recurrent.py:53); g [B, T, HV];
+    gk [B, T, HV, K]; gv [B, T, HV, V]; beta [B, T, HV] or [B, T, HV, V] (None:
+    ones).  Returns (o [B, T, HV, V], ht [N, HV, K, V]) as float32 (float64 for "fp64").
+    """
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[3]
+    f = np.float64 if dtype == "fp64" else np.float32
+    if scale is None:
+        scale = K ** -0.5
+    qf = _rec_heads(np.asarray(q, f), HV // H)              # [B, T, HV, K]
+    kf = _rec_heads(np.asarray(k, f), HV // H)
+    vf = np.asarray(v, f)
+    if use_qk_l2norm_in_kernel:
+        qf = qf / np.sqrt(np.sum(qf * qf, axis=-1, keepdims=True) + f(1e-6))
+        kf = kf / np.sqrt(np.sum(kf * kf, axis=-1, keepdims=True) + f(1e-6))
+    qf = qf * f(scale)
+    if beta is None:
+        bf = np.ones((B, T, HV, 1), f)
+    else:
+        bf = np.asarray(beta, f)
+        bf = bf[..., None] if bf.ndim == 3 else bf            # [B, T, HV, 1 or V]
+    spans = seq_spans(B, T, cu_seqlens)
+    o = np.zeros((B, T, HV, V), f)
+    ht = np.zeros((len(spans), HV, K, V), f)
+    pick = lambda x, b, t: None if x is None else x[b, t]   # noqa: E731
+    for n, (b, bos, eos) in enumerate(spans):
+        S = np.zeros((HV, K, V), f)
+        if initial_state is not None:
+            S = S + np.asarray(initial_state[n], f)
+        for t in range(bos, eos):
+            decay = _rec_decay(f, pick(g, b, t), pick(gk, b, t), pick(gv, b, t), HV, K, V)
+            S, o[b, t] = _rec_token(S, decay, qf[b, t], kf[b, t], vf[b, t], bf[b, t])
+        ht[n] = S
+    return cast(o, o_dtype) if dtype != "fp64" else o, ht
 
 
 def naive_recurrent(q, k, v, g, beta, scale=None, initial_state=None, cu_seqlens=None, dtype: str = "fp64"):
