@@ -268,6 +268,241 @@ __global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide form for K = 256 (the Kairos model's head dim), bf16 compute.  Here the
+// split-K form above re-reads the whole w and k chunk (64 KB) for every 16
+// state columns; instead one workgroup of WW waves stages the chunk's w
+// (row-major) and k^T in LDS once, and each wave owns 16 state columns over all
+// 256 rows (16 accumulator tiles in VGPRs), so w @ S needs no cross-wave
+// reduction and the gated v' stays in wave-private LDS.  Same outputs as the
+// split-K form (hT, vnT, ht) and the same cast points.
+// ---------------------------------------------------------------------------
+constexpr int WW = 4;                     // waves (x 16 columns) per workgroup
+constexpr int WK = 256;
+constexpr int LDW = WK + 8;               // w row stride (elements)
+
+template <typename TK>
+struct WideChunk {
+  uint4 w[8];            // this thread's 8 x 8 elements of w (row-major items tid + 256 i)
+  uint32_t k[32];        // k^T pairs: (k[2p][d], k[2p+1][d]) as bf16 lo / hi, d = 32 (tid / 32) + i, p = tid % 32
+  f32x4 uv[4];           // u of the wave's 16 columns, C layout, 4 row tiles
+  f32x4 gv[4];           // gc of those rows
+  float gl;
+  int nv;
+};
+
+template <typename TK>
+__device__ __forceinline__ void wide_prefetch(WideChunk<TK>& P, const FwdHArgs& a, int64_t c, int64_t t0, int nv,
+                                              int h, int vcol, bool active, int V) {
+  const int tid = threadIdx.x;
+  const int l = lane_id();
+  const int lg = l >> 4;
+  const int H = a.H;
+  P.nv = nv;
+  const bf16* w = reinterpret_cast<const bf16*>(a.w);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int item = tid + 256 * i;                 // 64 rows x 32 blocks of 8
+    const int r = item >> 5, cb = item & 31;
+    P.w[i] = r < nv ? *reinterpret_cast<const uint4*>(w + ((t0 + r) * H + h) * WK + 8 * cb) : make_uint4(0, 0, 0, 0);
+  }
+  const TK* k = reinterpret_cast<const TK*>(a.k);
+  const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
+  const int p = tid & 31, cb = tid >> 5;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float x0[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, x1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (2 * p < nv) load8_in<TK>(k + ((t0 + 2 * p) * H + h) * WK + 32 * cb + 8 * b, ks_, x0);
+    if (2 * p + 1 < nv) load8_in<TK>(k + ((t0 + 2 * p + 1) * H + h) * WK + 32 * cb + 8 * b, ks_, x1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // scalar locals: __builtin_bit_cast of a vector-element expression reads element 0 (hipcc 7.2)
+      const bf16 lo = (bf16)x0[e], hi = (bf16)x1[e];
+      P.k[8 * b + e] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+  }
+  if (active) {
+    const bf16* uT = reinterpret_cast<const bf16*>(a.uT) + ((c * H + h) * V + vcol) * C;
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      P.uv[tm] = ld4<bf16>(uT + 16 * tm + 4 * lg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tm + 4 * lg + j;
+        P.gv[tm][j] = t < nv ? a.gc[(t0 + t) * H + h] : 0.f;
+      }
+    }
+  }
+  P.gl = a.gc[(t0 + nv - 1) * H + h];
+}
+
+// Workgroup barrier that waits for LDS operations only, so the next chunk's
+// global loads (registers) and this chunk's hT / vnT stores stay in flight
+// across it; the compiler waits for those loads where their registers are used.
+// The empty asm statements keep memory accesses from moving across the barrier.
+__device__ __forceinline__ void wide_lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0); vmcnt, expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <typename TK>
+__global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, int total_units) {
+  __shared__ __align__(16) bf16 s_w[C * LDW];            // w rows [t][k]
+  __shared__ __align__(16) bf16 s_kT[WK * LDT];          // k^T [k][t]
+  __shared__ __align__(16) bf16 s_vg[WW][16 * LDT];      // per wave: gated v'^T [col][t]
+
+  const int per_xcd = gridDim.x / 8;                      // XCD-aware order (see fwd_h_kernel)
+  const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (o_idx >= total_units) return;
+  const int nvt = (V + 16 * WW - 1) / (16 * WW);
+  const int unit = o_idx / nvt;
+  const int H = a.H;
+  const int n = unit / H, h = unit % H;
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int v0 = (o_idx % nvt) * 16 * WW + 16 * wid;      // this wave's first column
+  const bool active = v0 < V;
+  const int vcol = active ? v0 + lc : 0;
+
+  int64_t bos, eos, c_first;
+  if (a.cu == nullptr) {
+    bos = (int64_t)n * a.T;
+    eos = bos + a.T;
+    c_first = (int64_t)n * ((a.T + C - 1) / C);
+  } else {
+    bos = a.cu[n];
+    eos = a.cu[n + 1];
+    c_first = a.chunk_off[n];
+  }
+  const int64_t nchunks = (eos - bos + C - 1) / C;
+
+  // state: rows 16 kt + 4 lg + j, column vcol
+  f32x4 S[16];
+#pragma unroll
+  for (int kt = 0; kt < 16; ++kt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x = 0.f;
+      if (a.h0 && active) {
+        const int64_t off = (((int64_t)n * H + h) * WK + 16 * kt + 4 * lg + j) * V + vcol;
+        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
+                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
+      }
+      S[kt][j] = x;
+    }
+  }
+
+  WideChunk<TK> cur, nxt;
+  if (nchunks > 0) wide_prefetch<TK>(cur, a, c_first, bos, (int)min((int64_t)C, eos - bos), h, vcol, active, V);
+  bf16* hT = reinterpret_cast<bf16*>(a.hT);
+  bf16* vnT = reinterpret_cast<bf16*>(a.vnT);
+  bf16* vg = s_vg[wid];
+  const int tid = threadIdx.x;
+
+  for (int64_t it = 0; it < nchunks; ++it) {
+    const int64_t c = c_first + it;
+    // ---- stage this chunk's w and k^T
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int item = tid + 256 * i;
+      *reinterpret_cast<uint4*>(s_w + (item >> 5) * LDW + 8 * (item & 31)) = cur.w[i];
+    }
+    {
+      const int p = tid & 31, cb = tid >> 5;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) *reinterpret_cast<uint32_t*>(s_kT + (32 * cb + i) * LDT + 2 * p) = cur.k[i];
+    }
+    wide_lds_barrier();
+    if (it + 1 < nchunks) {
+      const int64_t t1 = bos + (it + 1) * C;
+      wide_prefetch<TK>(nxt, a, c + 1, t1, (int)min((int64_t)C, eos - t1), h, vcol, active, V);
+    }
+    const int nv = cur.nv;
+    if (active) {
+      // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139)
+      bf16* hrow = hT + ((c * H + h) * V + vcol) * WK + 4 * lg;
+#pragma unroll
+      for (int kt = 0; kt < 16; ++kt) st4<bf16>(hrow + 16 * kt, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+      // w @ bf16(S): the B fragment of a 32-deep step is two accumulator tiles; the A
+      // fragment takes the same K order (rows 4 lg .. and 16 + 4 lg .. of the step).
+      // K steps outermost: one B fragment live, the 4 row tiles' A reads batched.
+      f32x4 acc[4];
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const Frag<bf16> hb = frag_from_acc<bf16>(S[2 * ks], S[2 * ks + 1]);
+        Frag<bf16> wa[4];
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+          const bf16* wr = s_w + (16 * tm + lc) * LDW + 4 * lg + 32 * ks;
+          wa[tm] = join<bf16>(ld_half<bf16>(wr), ld_half<bf16>(wr + 16));
+        }
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) mma(acc[tm], wa[tm], hb);
+      }
+      float vgv[4][4];
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) {
+        const f32x4 vp = cur.uv[tm] - acc[tm];      // v' = u - w h (chunk_delta_h.py:141-157)
+        st4<bf16>(vnT + ((c * H + h) * V + vcol) * C + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = 16 * tm + 4 * lg + j;
+          vgv[tm][j] = t < nv ? vp[j] * gexp(cur.gl - cur.gv[tm][j]) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+        st4<bf16>(vg + lc * LDT + 16 * tm + 4 * lg, vgv[tm][0], vgv[tm][1], vgv[tm][2], vgv[tm][3]);
+      // the gated v' tile is read back by other lanes of this wave only
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const Frag<bf16> b0 = lds_frag<bf16>(vg, LDT, 0, 0), b1 = lds_frag<bf16>(vg, LDT, 0, 32);
+      // S = exp(g_last) S + k^T (v' gated) (chunk_delta_h.py:163-211)
+      const float eg = gexp(cur.gl);
+#pragma unroll
+      for (int k4 = 0; k4 < 16; k4 += 4) {           // 8 A fragments read per batch of 4 row tiles
+        Frag<bf16> ka[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ka[q][0] = lds_frag<bf16>(s_kT, LDT, 16 * (k4 + q), 0);
+          ka[q][1] = lds_frag<bf16>(s_kT, LDT, 16 * (k4 + q), 32);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          S[k4 + q] *= eg;
+          mma(S[k4 + q], ka[q][0], b0);
+          mma(S[k4 + q], ka[q][1], b1);
+        }
+      }
+    }
+    wide_lds_barrier();                               // w / k^T are overwritten next step
+    cur = nxt;
+  }
+
+  if (a.ht && active) {
+#pragma unroll
+    for (int kt = 0; kt < 16; ++kt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (((int64_t)n * H + h) * WK + 16 * kt + 4 * lg + j) * V + vcol;
+        a.ht[off] = S[kt][j];
+      }
+    }
+  }
+}
+
+template <typename TK>
+int launch_fwd_h_wide(const FwdHArgs& a, int V, hipStream_t s) {
+  const int total = a.N * a.H * ((V + 16 * WW - 1) / (16 * WW));
+  const int grid = (total + 7) / 8 * 8;
+  hipLaunchKernelGGL((fwd_h_wide_kernel<TK>), dim3(grid), dim3(64 * WW), 0, s, a, V, total);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <typename TC, typename TK, int K>
 int launch_fwd_h_t(const FwdHArgs& a, int V, hipStream_t s) {
   const int total = a.N * a.H * (V / BV);
@@ -283,6 +518,9 @@ int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V
 #define KGDN_H_CASE(TC, TK, KK) \
   if (K == KK) return launch_fwd_h_t<TC, TK, KK>(a, V, s);
 #define KGDN_H_SHAPES(TC, TK) KGDN_H_CASE(TC, TK, 64) KGDN_H_CASE(TC, TK, 128) KGDN_H_CASE(TC, TK, 256)
+  // bf16 K = 256 runs the wide form; the split-K form stays for fp32 (and K <= 128)
+  if (K == 256 && compute_dtype == DT_BF16 && k_dtype == DT_BF16) return launch_fwd_h_wide<bf16>(a, V, s);
+  if (K == 256 && compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) return launch_fwd_h_wide<uint8_t>(a, V, s);
   if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_H_SHAPES(float, float) }
   if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_H_SHAPES(bf16, bf16) }
   if (compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) { KGDN_H_SHAPES(bf16, uint8_t) }
