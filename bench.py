@@ -10,6 +10,7 @@ output_final_state=True) with inputs resident in HBM, through the C ABI
   python bench.py --epilogue                # the gated RMSNorm output epilogue on config 2's o
   python bench.py --model-shape             # the Kairos 4B layer's head dims dk=256, dv=512
   python bench.py --recurrent               # the short-sequence mode's decoding step (fused_recurrent)
+  python bench.py --prologue                # the layer prologue: causal conv + SiLU (+ q/k L2 norm), gates
 
 `value` is tokens/s of whole forward calls (wall clock between two device
 synchronisations around `steps` back-to-back calls).  Per-kernel times come
@@ -278,6 +279,59 @@ def bench_recurrent(args, dev):
     }), flush=True)
 
 
+def bench_prologue(args, dev):
+    """The layer's prologue at the Kairos 4B shape (hidden 2560 -> H=20, dk=256, dv=512): causal conv
+    k=4 + SiLU over the q and k projections (D=5120, fused per-head L2 norm) and the v projection
+    (D=10240), bf16, caches out, plus the gates.  Algorithmic bytes = each projection read once and
+    written once (2 + 2 B per element) + caches + gate rows."""
+    from kairos_gdn import _lib
+    T, H, K, V, W = args.T, 20, 256, 512, 4
+    gen = torch.Generator(device="cpu").manual_seed(20272)
+    xs = [torch.randn(T, D, generator=gen).to(dev, torch.bfloat16) for D in (H * K, H * K, H * V)]
+    ws = [(0.5 * torch.randn(x.shape[1], W, generator=gen)).to(dev, torch.bfloat16) for x in xs]
+    ys = [torch.empty_like(x) for x in xs]
+    hs = [torch.empty(1, x.shape[1], W, dtype=torch.bfloat16, device=dev) for x in xs]
+    a = torch.randn(T, H, generator=gen).to(dev, torch.bfloat16)
+    b = torch.randn(T, H, generator=gen).to(dev, torch.bfloat16)
+    A_log = torch.rand(H, generator=gen).mul_(16).log_().to(dev)
+    dt_bias = torch.randn(H, generator=gen).to(dev)
+    g = torch.empty(T, H, dtype=torch.float32, device=dev)
+    beta = torch.empty_like(b)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    l2 = (K, K, 0)
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def step():
+        for x, w, y, h, hd in zip(xs, ws, ys, hs, l2):
+            _lib.call("kairos_gdn_causal_conv1d_fwd", P(x), P(w), None, None, P(y), P(h), None, 0, 1, T, x.shape[1], W,
+                      _lib.BF16, _lib.BF16, 1, hd, sp)
+        _lib.call("kairos_gdn_gates_fwd", P(a), P(b), P(A_log), P(dt_bias), P(g), P(beta), T, H, _lib.BF16, _lib.BF16,
+                  _lib.F32, 0, sp)
+
+    for _ in range(args.warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = sum(x.numel() * 4 + x.shape[1] * W * 2 * 2 for x in xs) + T * H * (2 + 2 + 4 + 2)
+    gbs = nbytes / (ms / 1e3) / 1e9
+    print(json.dumps({
+        "metric": "GDN layer prologue (conv k=4 + SiLU on q/k/v with fused q/k L2 norm, gates) GB/s at "
+                  "T=32760, H=20, dk=256, dv=512", "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "kairos_gdn_causal_conv1d_fwd x3 (q, k: D=5120 with per-head L2 norm; v: D=10240), "
+                               "bf16, W=4, caches out, + kairos_gdn_gates_fwd (T x 20)"},
+        "roofline": {"bound": "hbm", "kernel": "conv1d_kernel", "achieved": gbs, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -297,6 +351,9 @@ def main():
     ap.add_argument("--recurrent", action="store_true",
                     help="measure the short-sequence mode's decoding step (kairos_gdn_fused_recurrent_fwd, 8 streams "
                          "x 1 token at dk=256, dv=512); prints its own JSON line")
+    ap.add_argument("--prologue", action="store_true",
+                    help="measure the layer prologue (causal conv + SiLU + q/k L2 norm, gates) at the model shape; "
+                         "prints its own JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -325,6 +382,9 @@ def main():
         return
     if args.recurrent:
         bench_recurrent(args, dev)
+        return
+    if args.prologue:
+        bench_prologue(args, dev)
         return
     B, T, H, K, V = 1, args.T, 20, 128, 128
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)

@@ -178,6 +178,37 @@ int kairos_gdn_fused_recurrent_fwd(const void* q, const void* k, const void* v, 
                                    int v_dtype, int g_dtype, int gk_dtype, int gv_dtype, int beta_dtype,
                                    int beta_headwise, int h0_dtype, float scale, int use_qk_l2norm, void* stream);
 
+/* ---- layer prologue --------------------------------------------------------
+ * Short causal convolution of the q/k/v projections (ShortConvolution with
+ * activation 'silu', fla layers/gated_deltanet.py:176-189,235-253), replacing
+ * causal_conv1d_fwd and causal_conv1d_update_states (fla modules/convolution.py:410-458,
+ * :539-602, Triton backend):
+ *   y[t, d] = act( sum_{i<W} weight[d, i] x~[t - W + 1 + i, d] + bias[d] )
+ * with x~ = x inside each sequence and, before its first token, initial_state
+ * (the cache [N, D, W], slot W-1 the most recent input; NULL = zeros).
+ * x, y: [B*T, D] fp32 or bf16 (16-byte aligned, D a multiple of 8); weight
+ * [D, W] and bias [D] (NULL = none) in w_dtype; initial_state / final_state
+ * [N, D, W] in x's dtype, final_state = the last W entries of [cache, x] per
+ * sequence (NULL = not wanted; must not alias initial_state).  W in 1..4.
+ * activation_silu: y = z sigmoid(z).  l2norm_head_dim (0 = off, else 64, 128,
+ * 256 or 512 dividing D): y, rounded to x's dtype, is then normalised per head,
+ * y / sqrt(sum y^2 + 1e-6) (fla modules/l2norm.py:115-118) -- the q/k
+ * normalisation the layer asks of the chunked op, fused here (no counterpart
+ * in the reference as one kernel). */
+int kairos_gdn_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, const void* initial_state,
+                                 void* y, void* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                 int64_t T, int64_t D, int64_t W, int x_dtype, int w_dtype, int activation_silu,
+                                 int l2norm_head_dim, void* stream);
+
+/* Gates of the GatedDeltaNet layer (fla layers/gated_deltanet.py:265-271):
+ * g = -exp(A_log) softplus(a + dt_bias) (fp32, softplus threshold 20) and
+ * beta = sigmoid(b) in b's dtype, doubled when allow_neg_eigval.  a, b: [rows, HV]
+ * (fp32 or bf16 each); A_log, dt_bias: [HV] in param_dtype; g: [rows, HV] fp32;
+ * beta: [rows, HV] in b's dtype. */
+int kairos_gdn_gates_fwd(const void* a, const void* b, const void* A_log, const void* dt_bias, float* g, void* beta,
+                         int64_t rows, int64_t HV, int a_dtype, int b_dtype, int param_dtype, int allow_neg_eigval,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

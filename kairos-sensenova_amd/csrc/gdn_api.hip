@@ -621,4 +621,59 @@ int kairos_gdn_fused_recurrent_fwd(const void* q, const void* k, const void* v, 
   return ok();
 }
 
+int kairos_gdn_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, const void* initial_state,
+                                 void* y, void* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                 int64_t T, int64_t D, int64_t W, int x_dtype, int w_dtype, int activation_silu,
+                                 int l2norm_head_dim, void* stream) {
+  const char* what = "kairos_gdn_causal_conv1d_fwd";
+  if (B <= 0 || T < 0 || D <= 0)
+    return fail(KAIROS_GDN_EINVAL, "%s: invalid shape B=%lld T=%lld D=%lld", what, (long long)B, (long long)T,
+                (long long)D);
+  if ((cu_seqlens == nullptr) != (n_seqs == 0) || n_seqs < 0)
+    return fail(KAIROS_GDN_EINVAL, "%s: cu_seqlens and n_seqs must be given together", what);
+  if (cu_seqlens && B != 1)
+    return fail(KAIROS_GDN_EINVAL, "%s: the batch size is expected to be 1 rather than %lld when using cu_seqlens",
+                what, (long long)B);
+  if (W < 1 || W > 4) return fail(KAIROS_GDN_EUNSUPPORTED, "%s: kernel size W=%lld is not built (1..4)", what,
+                                  (long long)W);
+  if (D % 8 != 0) return fail(KAIROS_GDN_EINVAL, "%s: D=%lld must be a multiple of 8", what, (long long)D);
+  if (!valid_scalar_dt(x_dtype) || !valid_scalar_dt(w_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: x and weight must be fp32 or bf16", what);
+  int head_lanes = 0;
+  if (l2norm_head_dim) {
+    const int64_t hd = l2norm_head_dim;
+    if (!(hd == 64 || hd == 128 || hd == 256 || hd == 512) || D % hd != 0)
+      return fail(KAIROS_GDN_EUNSUPPORTED, "%s: l2norm_head_dim=%lld must be 64, 128, 256 or 512 and divide D",
+                  what, (long long)hd);
+    head_lanes = (int)(hd / 8);
+  }
+  const int64_t N = cu_seqlens ? n_seqs : B;
+  if (N > 0x7fffffff || D > 0x7fffffff) return fail(KAIROS_GDN_EINVAL, "%s: too many sequences or channels", what);
+  if (B * T > 0 && (!x || !weight || !y)) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  if (!aligned16(x) || !aligned16(y)) return fail(KAIROS_GDN_EINVAL, "%s: x and y must be 16-byte aligned", what);
+  if (final_state && final_state == initial_state)
+    return fail(KAIROS_GDN_EINVAL, "%s: final_state must not alias initial_state", what);
+  kgdn::ConvArgs a{};
+  a.x = x; a.y = y; a.w = weight; a.bias = bias; a.h0 = initial_state; a.ht = final_state; a.cu = cu_seqlens;
+  a.T = T; a.total_tokens = B * T; a.N = (int)N; a.D = (int)D; a.W = (int)W;
+  a.x_dtype = x_dtype; a.w_dtype = w_dtype; a.silu = activation_silu ? 1 : 0; a.head_lanes = head_lanes;
+  if (int rc = from_launch(kgdn::launch_conv1d(a, static_cast<hipStream_t>(stream)), what)) return rc;
+  return ok();
+}
+
+int kairos_gdn_gates_fwd(const void* a, const void* b, const void* A_log, const void* dt_bias, float* g, void* beta,
+                         int64_t rows, int64_t HV, int a_dtype, int b_dtype, int param_dtype, int allow_neg_eigval,
+                         void* stream) {
+  const char* what = "kairos_gdn_gates_fwd";
+  if (rows < 0 || HV <= 0 || HV > 0x7fffffff) return fail(KAIROS_GDN_EINVAL, "%s: invalid shape", what);
+  if (!valid_scalar_dt(a_dtype) || !valid_scalar_dt(b_dtype) || !valid_scalar_dt(param_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: a, b and the parameters must be fp32 or bf16", what);
+  if (rows > 0 && (!a || !b || !A_log || !dt_bias || !g || !beta))
+    return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  kgdn::GateArgs ga{a, b, A_log, dt_bias, g, beta, rows, (int)HV, a_dtype, b_dtype, param_dtype,
+                    allow_neg_eigval ? 1 : 0};
+  if (int rc = from_launch(kgdn::launch_gates(ga, static_cast<hipStream_t>(stream)), what)) return rc;
+  return ok();
+}
+
 }  // extern "C"

@@ -165,6 +165,39 @@ struct RecArgs {
   float scale;
 };
 int launch_fused_recurrent(const RecArgs& a, hipStream_t s);
+
+// Short causal convolution (gdn_prologue.hip), causal_conv1d_fwd of fla modules/convolution.py.
+struct ConvArgs {
+  const void* x;          // [B*T, D] x_dtype
+  void* y;                // [B*T, D] x_dtype
+  const void* w;          // [D, W] w_dtype
+  const void* bias;       // [D] w_dtype or nullptr
+  const void* h0;         // cache in [N, D, W] x_dtype or nullptr
+  void* ht;               // cache out [N, D, W] x_dtype or nullptr
+  const int64_t* cu;      // varlen [N+1] or nullptr
+  int64_t T;              // tokens per sequence (fixed length)
+  int64_t total_tokens;   // B*T
+  int N, D, W;
+  int x_dtype, w_dtype;
+  int silu;               // apply y * sigmoid(y)
+  int head_lanes;         // 0, or hd / 8: L2-normalise the rounded y per head of hd channels
+};
+int launch_conv1d(const ConvArgs& a, hipStream_t s);
+
+// GatedDeltaNet gates (gdn_prologue.hip), layers/gated_deltanet.py:265-271.
+struct GateArgs {
+  const void* a;          // [rows, HV] a_dtype
+  const void* b;          // [rows, HV] b_dtype
+  const void* A_log;      // [HV] p_dtype
+  const void* dt_bias;    // [HV] p_dtype
+  float* g;               // out [rows, HV] fp32
+  void* beta;             // out [rows, HV] b_dtype
+  int64_t rows;
+  int HV;
+  int a_dtype, b_dtype, p_dtype;
+  int neg_eigval;
+};
+int launch_gates(const GateArgs& a, hipStream_t s);
 int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s);
 int launch_cumsum(const void* g, int g_dtype, float* gc, const int64_t* cu, const int32_t* chunk_off, int N,
                   int64_t T, int H, int64_t nc_grid, hipStream_t s);

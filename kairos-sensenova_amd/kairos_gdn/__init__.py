@@ -20,6 +20,7 @@ from .chunk import (
 )
 from .norm import FusedRMSNormGated, rms_norm_gated, rms_norm_gated_fwd
 from .recurrent import FusedRecurrentFunction, fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_fwd
+from .conv import ShortConvolution, causal_conv1d, gdn_gates
 from . import swap
 
 __all__ = [
@@ -27,4 +28,5 @@ __all__ = [
     "chunk_gated_delta_rule_fwd", "chunk_local_cumsum", "fwd_h", "fwd_o", "l2norm_fwd", "num_chunks_bound",
     "prepare_wy", "swap", "FusedRMSNormGated", "rms_norm_gated", "rms_norm_gated_fwd",
     "FusedRecurrentFunction", "fused_recurrent_gated_delta_rule", "fused_recurrent_gated_delta_rule_fwd",
+    "ShortConvolution", "causal_conv1d", "gdn_gates",
 ]

@@ -44,6 +44,9 @@ SIGNATURES = {
     "kairos_gdn_rms_norm_gated": (_i, [_p, _p, _p, _p, _p, _fp, _i, _i, _i, _i64, _i64, _f, _i, _p]),
     "kairos_gdn_fused_recurrent_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _fp, _p, _i64, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "kairos_gdn_causal_conv1d_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _i,
+                                          _p]),
+    "kairos_gdn_gates_fwd": (_i, [_p, _p, _p, _p, _fp, _p, _i64, _i64, _i, _i, _i, _i, _p]),
     "kairos_gdn_segment_chunks": (_i, [_i64, _i64, _i64, _i64]),
     "kairos_gdn_profile_begin": (_i, []),
     "kairos_gdn_profile_end": (_i, [ctypes.POINTER(ctypes.c_double), _i]),

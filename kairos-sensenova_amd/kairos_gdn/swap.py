@@ -4,11 +4,11 @@ The reference's GDN layers bind the ops by name at import time
 (``from ...gated_delta_rule import chunk_gated_delta_rule, fused_recurrent_gated_delta_rule`` in
 fla/layers/gated_deltanet.py:16 and gated_deltanet_with_tp.py:17), the same
 way Kairos' own engine swap monkey-patches the DiT (kairos_ext/kairos_engine_patch.py:1773).
-The layer's output norm class is bound the same way
-(``from ...modules import FusedRMSNormGated``, gated_deltanet.py:15) and
-instantiated in the layer's constructor (:197).  ``install()`` rebinds those
+The layer's output norm and short-convolution classes are bound the same way
+(``from ...modules import FusedRMSNormGated, RMSNorm, ShortConvolution``,
+gated_deltanet.py:15) and instantiated in the layer's constructor (:176-197).  ``install()`` rebinds those
 names in every already-imported module that holds them, so the layers call
-this build's kernels (layers constructed afterwards get the MI355X norm);
+this build's kernels (layers constructed afterwards get the MI355X norm and convolutions);
 ``uninstall()`` restores the originals.
 """
 from __future__ import annotations
@@ -16,6 +16,7 @@ from __future__ import annotations
 import sys
 
 from .chunk import chunk_gated_delta_rule
+from .conv import ShortConvolution
 from .norm import FusedRMSNormGated
 from .recurrent import fused_recurrent_gated_delta_rule
 
@@ -37,13 +38,14 @@ REPLACEMENTS = {
     "chunk_gated_delta_rule": chunk_gated_delta_rule,
     "fused_recurrent_gated_delta_rule": fused_recurrent_gated_delta_rule,
     "FusedRMSNormGated": FusedRMSNormGated,
+    "ShortConvolution": ShortConvolution,
 }
 
 _saved: dict[tuple[str, str], object] = {}
 
 
 def install(sites=SITES, names=tuple(REPLACEMENTS)) -> list[str]:
-    """Rebind ``names`` (default: both ops and the norm class) in the imported modules among
+    """Rebind ``names`` (default: both ops, the norm and the convolution class) in the imported modules among
     ``sites``; returns the patched ``module.name`` entries."""
     patched = []
     for mod_name in sites:

@@ -22,6 +22,9 @@ It restates, stage by stage, the reference op
                              ops/gated_delta_rule/fused_recurrent.py:88-119
   fused_recurrent            ops/gated_delta_rule/fused_recurrent.py:21-135, :238-349
                              (gk / gv decays, per-column beta, grouped value heads)
+  causal_conv1d              modules/convolution.py:54-141, :410-458, :539-602 (the
+                             layer's ShortConvolution with SiLU, cache in / out)
+  gdn_gates                  layers/gated_deltanet.py:265-271
   rms_norm_gated             modules/fused_norm_gate.py:42-127 (RMS path, no residual),
                              the layer's output epilogue (layers/gated_deltanet.py:197,311)
 
@@ -61,6 +64,12 @@ How each function is pinned (tests/test_oracle.py):
                          in-kernel L2 norm == normalised inputs; planted
                          mistakes (gk applied over V, decay after the delta,
                          wrong q/k head for a value head) each fail one check.
+  causal_conv1d          torch.nn.functional.conv1d (fp64, groups=D, causal
+                         padding) without a cache; split calls with the cache
+                         carried == one call; final state == last W of [cache, x];
+                         varlen == separate calls; planted reversed taps fail.
+  gdn_gates              torch softplus / sigmoid / exp (fp64) and the closed
+                         form a + dt_bias = 0 -> g = -exp(A_log) log 2.
   l2norm                 closed form x / sqrt(sum x^2 + eps).
   rms_norm_gated         torch.nn.functional.rms_norm times silu / sigmoid of the
                          gate (library routines, fp64); closed forms: g = 0 gives
@@ -82,7 +91,7 @@ __all__ = [
     "CHUNK", "to_bf16", "cast", "seq_spans", "l2norm", "chunk_local_cumsum",
     "chunk_scaled_dot_kkt", "solve_tril", "recompute_w_u", "chunk_fwd_h",
     "chunk_fwd_o", "chunk_gated_delta_rule", "naive_recurrent", "rel_l2",
-    "fp8_e4m3_quantize", "fp8_e4m3_decode", "rms_norm_gated", "fused_recurrent",
+    "fp8_e4m3_quantize", "fp8_e4m3_decode", "rms_norm_gated", "fused_recurrent", "causal_conv1d", "gdn_gates",
 ]
 
 
@@ -540,6 +549,56 @@ def fused_recurrent(q, k, v, g=None, gk=None, gv=None, beta=None, scale=None, in
             S, o[b, t] = _rec_token(S, decay, qf[b, t], kf[b, t], vf[b, t], bf[b, t])
         ht[n] = S
     return cast(o, o_dtype) if dtype != "fp64" else o, ht
+
+
+def causal_conv1d(x, weight, bias=None, initial_state=None, cu_seqlens=None, activation=None,
+                  l2norm_head_dim=0, dtype: str = "fp32"):
+    """Short causal convolution per channel (fla modules/convolution.py:54-141, :410-458):
+    y[t, d] = act(sum_i weight[d, i] x~[t - W + 1 + i, d] + bias[d]), x~ = x inside the
+    sequence, else the cache initial_state [N, D, W] (slot W-1 the most recent input),
+    else 0; fp32 arithmetic, y rounded to ``dtype`` (x's storage dtype).  With
+    ``l2norm_head_dim`` the rounded y is L2-normalised per head (l2norm.py:115-118)
+    and rounded again.  Returns (y [B, T, D], final_state [N, D, W]) where final_state
+    is the last W entries of [cache, x] per sequence (convolution.py:539-574).
+    """
+    B, T, D = x.shape
+    W = weight.shape[1]
+    xf = np.asarray(x, np.float64)
+    wf = np.asarray(weight, np.float64)
+    spans = seq_spans(B, T, cu_seqlens)
+    y = np.zeros((B, T, D), np.float64)
+    final = np.zeros((len(spans), D, W), np.float64)
+    for n, (b, bos, eos) in enumerate(spans):
+        cache = np.zeros((W, D)) if initial_state is None else np.asarray(initial_state[n], np.float64).T
+        ext = np.concatenate([cache, xf[b, bos:eos]], axis=0)          # [W + T_n, D], x~ from slot 0
+        for t in range(eos - bos):
+            win = ext[t + 1:t + 1 + W]                                  # x~[t - W + 1 .. t]
+            y[b, bos + t] = np.sum(win * wf.T, axis=0)
+        final[n] = ext[-W:].T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    y = y.astype(np.float32)                                            # fp32 accumulation
+    if activation in ("silu", "swish"):
+        y = y / (1.0 + np.exp(-y))
+    y = cast(y, dtype)
+    if l2norm_head_dim:
+        yh = y.reshape(B, T, D // l2norm_head_dim, l2norm_head_dim)
+        yh = yh / np.sqrt(np.sum(yh * yh, axis=-1, keepdims=True, dtype=np.float32) + np.float32(1e-6))
+        y = cast(yh.reshape(B, T, D), dtype)
+    return y, cast(final.astype(np.float32), dtype)
+
+
+def gdn_gates(a, b, A_log, dt_bias, allow_neg_eigval=False, b_dtype: str = "fp32"):
+    """Gates of the GatedDeltaNet layer (layers/gated_deltanet.py:265-271): g = -exp(A_log)
+    softplus(a + dt_bias) in fp32 (torch softplus, threshold 20) and beta = sigmoid(b) rounded
+    to b's dtype, doubled with allow_neg_eigval.  a, b: [..., HV]; returns (g, beta)."""
+    z = np.asarray(a, np.float32) + np.asarray(dt_bias, np.float32)
+    sp = np.where(z > 20, z, np.log1p(np.exp(np.minimum(z, 20)))).astype(np.float32)
+    g = (-np.exp(np.asarray(A_log, np.float32)) * sp).astype(np.float32)
+    beta = cast(1.0 / (1.0 + np.exp(-np.asarray(b, np.float64))), b_dtype)
+    if allow_neg_eigval:
+        beta = beta * 2
+    return g, beta
 
 
 def naive_recurrent(q, k, v, g, beta, scale=None, initial_state=None, cu_seqlens=None, dtype: str = "fp64"):

@@ -176,25 +176,34 @@ def test_swap_rebinds_and_restores(monkeypatch):
 
     class ReferenceNorm:
         pass
+
+    class ReferenceConv:
+        pass
     layer = types.ModuleType("fla.layers.gated_deltanet")
     layer.chunk_gated_delta_rule = reference_op
+    layer.fused_recurrent_gated_delta_rule = reference_op
     layer.FusedRMSNormGated = ReferenceNorm
+    layer.ShortConvolution = ReferenceConv
     vendored = types.ModuleType("kairos.third_party.fla.ops.gated_delta_rule")
     vendored.chunk_gated_delta_rule = reference_op
     monkeypatch.setitem(sys.modules, "fla.layers.gated_deltanet", layer)
     monkeypatch.setitem(sys.modules, "kairos.third_party.fla.ops.gated_delta_rule", vendored)
     patched = kairos_gdn.swap.install()
     assert set(patched) == {"fla.layers.gated_deltanet.chunk_gated_delta_rule",
+                            "fla.layers.gated_deltanet.fused_recurrent_gated_delta_rule",
                             "fla.layers.gated_deltanet.FusedRMSNormGated",
+                            "fla.layers.gated_deltanet.ShortConvolution",
                             "kairos.third_party.fla.ops.gated_delta_rule.chunk_gated_delta_rule"}
     assert layer.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
+    assert layer.fused_recurrent_gated_delta_rule is kairos_gdn.fused_recurrent_gated_delta_rule
     assert layer.FusedRMSNormGated is kairos_gdn.FusedRMSNormGated
+    assert layer.ShortConvolution is kairos_gdn.ShortConvolution
     assert vendored.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
     assert kairos_gdn.swap.install() == patched                  # idempotent
     restored = kairos_gdn.swap.uninstall()
     assert set(restored) == set(patched)
     assert layer.chunk_gated_delta_rule is reference_op
-    assert layer.FusedRMSNormGated is ReferenceNorm
+    assert layer.FusedRMSNormGated is ReferenceNorm and layer.ShortConvolution is ReferenceConv
     patched = kairos_gdn.swap.install(names=("chunk_gated_delta_rule",))   # the op alone
     assert layer.FusedRMSNormGated is ReferenceNorm and layer.chunk_gated_delta_rule is kairos_gdn.chunk_gated_delta_rule
     kairos_gdn.swap.uninstall()
