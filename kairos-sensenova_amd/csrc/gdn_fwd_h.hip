@@ -281,13 +281,15 @@ constexpr int WW = 4;                     // waves (x 16 columns) per workgroup
 constexpr int WK = 256;
 constexpr int LDW = WK + 8;               // w row stride (elements)
 
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 template <typename TK>
 struct WideChunk {
   uint4 w[8];            // this thread's 8 x 8 elements of w (row-major items tid + 256 i)
   uint32_t k[32];        // k^T pairs: (k[2p][d], k[2p+1][d]) as bf16 lo / hi, d = 32 (tid / 32) + i, p = tid % 32
-  f32x4 uv[4];           // u of the wave's 16 columns, C layout, 4 row tiles
-  f32x4 gv[4];           // gc of those rows
-  float gl;
+  uint2 u[4];            // u of the wave's 16 columns, C layout, 4 row tiles, 4 bf16 each
+  float gcl;             // gc of token t0 + lane (0 past the chunk's end); rows get theirs by shuffle
   int nv;
 };
 
@@ -324,16 +326,9 @@ __device__ __forceinline__ void wide_prefetch(WideChunk<TK>& P, const FwdHArgs& 
   if (active) {
     const bf16* uT = reinterpret_cast<const bf16*>(a.uT) + ((c * H + h) * V + vcol) * C;
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-      P.uv[tm] = ld4<bf16>(uT + 16 * tm + 4 * lg);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = 16 * tm + 4 * lg + j;
-        P.gv[tm][j] = t < nv ? a.gc[(t0 + t) * H + h] : 0.f;
-      }
-    }
+    for (int tm = 0; tm < 4; ++tm) P.u[tm] = *reinterpret_cast<const uint2*>(uT + 16 * tm + 4 * lg);
   }
-  P.gl = a.gc[(t0 + nv - 1) * H + h];
+  P.gcl = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
 }
 
 // Workgroup barrier that waits for LDS operations only, so the next chunk's
@@ -395,8 +390,14 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
     }
   }
 
-  WideChunk<TK> cur, nxt;
+  // two chunks of loads in flight: a chunk's loads are issued two steps before it is staged
+  // (measured: with one step of distance the step waits on its global loads for most of its time)
+  WideChunk<TK> cur, nx1, nx2;
   if (nchunks > 0) wide_prefetch<TK>(cur, a, c_first, bos, (int)min((int64_t)C, eos - bos), h, vcol, active, V);
+  if (nchunks > 1) {
+    const int64_t t1 = bos + C;
+    wide_prefetch<TK>(nx1, a, c_first + 1, t1, (int)min((int64_t)C, eos - t1), h, vcol, active, V);
+  }
   bf16* hT = reinterpret_cast<bf16*>(a.hT);
   bf16* vnT = reinterpret_cast<bf16*>(a.vnT);
   bf16* vg = s_vg[wid];
@@ -416,9 +417,9 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       for (int i = 0; i < 32; ++i) *reinterpret_cast<uint32_t*>(s_kT + (32 * cb + i) * LDT + 2 * p) = cur.k[i];
     }
     wide_lds_barrier();
-    if (it + 1 < nchunks) {
-      const int64_t t1 = bos + (it + 1) * C;
-      wide_prefetch<TK>(nxt, a, c + 1, t1, (int)min((int64_t)C, eos - t1), h, vcol, active, V);
+    if (it + 2 < nchunks) {
+      const int64_t t2 = bos + (it + 2) * C;
+      wide_prefetch<TK>(nx2, a, c + 2, t2, (int)min((int64_t)C, eos - t2), h, vcol, active, V);
     }
     const int nv = cur.nv;
     if (active) {
@@ -445,14 +446,17 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
         for (int tm = 0; tm < 4; ++tm) mma(acc[tm], wa[tm], hb);
       }
       float vgv[4][4];
+      const float gl = __shfl(cur.gcl, nv - 1);     // gc of the chunk's last token
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
-        const f32x4 vp = cur.uv[tm] - acc[tm];      // v' = u - w h (chunk_delta_h.py:141-157)
+        const f32x4 uv = {bf16_lo(cur.u[tm].x), bf16_hi(cur.u[tm].x), bf16_lo(cur.u[tm].y), bf16_hi(cur.u[tm].y)};
+        const f32x4 vp = uv - acc[tm];              // v' = u - w h (chunk_delta_h.py:141-157)
         st4<bf16>(vnT + ((c * H + h) * V + vcol) * C + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int t = 16 * tm + 4 * lg + j;
-          vgv[tm][j] = t < nv ? vp[j] * gexp(cur.gl - cur.gv[tm][j]) : 0.f;
+          const float gt = __shfl(cur.gcl, t);
+          vgv[tm][j] = t < nv ? vp[j] * gexp(gl - gt) : 0.f;
         }
       }
 #pragma unroll
@@ -462,7 +466,7 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const Frag<bf16> b0 = lds_frag<bf16>(vg, LDT, 0, 0), b1 = lds_frag<bf16>(vg, LDT, 0, 32);
       // S = exp(g_last) S + k^T (v' gated) (chunk_delta_h.py:163-211)
-      const float eg = gexp(cur.gl);
+      const float eg = gexp(gl);
 #pragma unroll
       for (int k4 = 0; k4 < 16; k4 += 4) {           // 8 A fragments read per batch of 4 row tiles
         Frag<bf16> ka[4][2];
@@ -480,7 +484,8 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       }
     }
     wide_lds_barrier();                               // w / k^T are overwritten next step
-    cur = nxt;
+    cur = nx1;
+    nx1 = nx2;
   }
 
   if (a.ht && active) {
