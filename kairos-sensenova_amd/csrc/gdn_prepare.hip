@@ -20,6 +20,19 @@ namespace {
 
 constexpr int NT_PREP = 256;   // 4 waves
 
+// Two values of consecutive tokens into a transposed tile [d][t] at t even: one
+// packed 4-byte store for bf16 (rounded), one 8-byte store for fp32.
+template <typename TC>
+__device__ __forceinline__ void st_pair(TC* p, float a, float b) {
+  if constexpr (sizeof(TC) == 2) {
+    const bf16 lo = (bf16)a, hi = (bf16)b;     // scalar locals for the bit casts
+    *reinterpret_cast<uint32_t*>(p) =
+        (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  } else {
+    *reinterpret_cast<f32x2*>(p) = f32x2{a, b};
+  }
+}
+
 // LDS plan.  Region 0 holds k row-major for K.K^T; once A is formed it is
 // reused for the rounded inverse Ai and, after it, the v^T pass buffer: v is
 // staged VP columns at a time (u is separable over V), so V = 512 fits.
@@ -87,30 +100,57 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
   __syncthreads();
 
+  // ---- v of the first pass (below) into registers now, so its loads overlap K.K^T and the solve
+  const TC* vin = reinterpret_cast<const TC*>(a.v);
+  const int pr = tid & 31, cg = tid >> 5;                // token pair (2 pr, 2 pr + 1), column group of 8
+  const bool v_vec = V % 64 == 0;                         // every pass width a multiple of 64 (VP is)
+  Vec8<TC> vr[2][L::VP / 64];
+  auto load_v = [&](int p0) {
+    const int cpg = min(L::VP, V - p0) / 8;               // columns per group, a multiple of 8
+#pragma unroll
+    for (int ch = 0; ch < L::VP / 64; ++ch) {
+      if (8 * ch >= cpg) break;
+      const int c = p0 + cg * cpg + 8 * ch;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * pr + rr;
+        vr[rr][ch] = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + c) : vzero<TC>();
+      }
+    }
+  };
+  if (v_vec) load_v(0);
+
   // ---- stage k (row-major, for K.K^T) and the transposed, scaled operand
-  //      kb^T[d][t] = k*beta*exp(gc)
+  //      kb^T[d][t] = k*beta*exp(gc).  Lane = token pair, so each transposed store packs the pair
+  //      (one 4-byte store in bf16) and the 32 lanes of a group hit 32 consecutive banks.
   const float kscale = a.k_scale ? a.k_scale[h] : 1.f;
   const TK* kin = reinterpret_cast<const TK*>(a.k);
-  for (int idx = tid; idx < C * (K / 8); idx += NT_PREP) {
-    const int r = idx / (K / 8), c8 = (idx % (K / 8)) * 8;
-    float x[8];
-    if (r < nv) {
-      load8_in<TK>(kin + ((t0 + r) * H + h) * K + c8, kscale, x);
-    } else {
+  {
+    const float b0 = s_b[2 * pr], b1 = s_b[2 * pr + 1], e0 = s_eg[2 * pr], e1 = s_eg[2 * pr + 1];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.f;
-    }
-    Vec8<TC> row;
-    const float b = s_b[r], eg = s_eg[r];
+    for (int ch = 0; ch < K / 64; ++ch) {
+      const int c8 = cg * (K / 8) + 8 * ch;
+      float x0[8], x1[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float kv = round_to<TC>(x[e]);                 // stored k (fp8 input: dequantised)
-      vset<TC>(row, e, kv);
-      float kb = kv * b;
-      if (a.beta_dtype == 1) kb = round_to<TC>(kb);       // bf16*bf16 -> bf16 (wy_fast.py:77)
-      s_kbT[(c8 + e) * L::LDT + r] = from_f32<TC>(kb * eg);
+      for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.f;
+      if (2 * pr < nv) load8_in<TK>(kin + ((t0 + 2 * pr) * H + h) * K + c8, kscale, x0);
+      if (2 * pr + 1 < nv) load8_in<TK>(kin + ((t0 + 2 * pr + 1) * H + h) * K + c8, kscale, x1);
+      Vec8<TC> r0, r1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float kv0 = round_to<TC>(x0[e]), kv1 = round_to<TC>(x1[e]);   // stored k (fp8: dequantised)
+        vset<TC>(r0, e, kv0);
+        vset<TC>(r1, e, kv1);
+        float kb0 = kv0 * b0, kb1 = kv1 * b1;
+        if (a.beta_dtype == 1) {                           // bf16*bf16 -> bf16 (wy_fast.py:77)
+          kb0 = round_to<TC>(kb0);
+          kb1 = round_to<TC>(kb1);
+        }
+        st_pair<TC>(s_kbT + (c8 + e) * L::LDT + 2 * pr, kb0 * e0, kb1 * e1);
+      }
+      st8<TC>(s_k + (2 * pr) * L::LDK + c8, r0);
+      st8<TC>(s_k + (2 * pr + 1) * L::LDK + c8, r1);
     }
-    st8<TC>(s_k + r * L::LDK + c8, row);
   }
   __syncthreads();
 
@@ -227,16 +267,29 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
   //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 (k is dead,
   //      Ai sits below the pass buffer), so staging overlaps the w products above
-  const TC* vin = reinterpret_cast<const TC*>(a.v);
   TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
   for (int p0 = 0; p0 < V; p0 += L::VP) {
     const int vw = min(L::VP, V - p0);             // a multiple of 16
-    for (int idx = tid; idx < C * (vw / 8); idx += NT_PREP) {
-      const int r = idx / (vw / 8), c8 = (idx % (vw / 8)) * 8;
-      Vec8<TC> x = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + p0 + c8) : vzero<TC>();
-      const float b = s_b[r];
+    if (v_vec) {                                   // from registers, token pairs packed per store
+      const float b0 = s_b[2 * pr], b1 = s_b[2 * pr + 1];
+      const int cpg = vw / 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s_vbT[(c8 + e) * L::LDT + r] = from_f32<TC>(vget<TC>(x, e) * b);
+      for (int ch = 0; ch < L::VP / 64; ++ch) {
+        if (8 * ch >= cpg) break;
+        const int c8 = cg * cpg + 8 * ch;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          st_pair<TC>(s_vbT + (c8 + e) * L::LDT + 2 * pr, vget<TC>(vr[0][ch], e) * b0, vget<TC>(vr[1][ch], e) * b1);
+      }
+      if (p0 + L::VP < V) load_v(p0 + L::VP);      // the next pass's loads overlap this pass's products
+    } else {
+      for (int idx = tid; idx < C * (vw / 8); idx += NT_PREP) {
+        const int r = idx / (vw / 8), c8 = (idx % (vw / 8)) * 8;
+        Vec8<TC> x = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + p0 + c8) : vzero<TC>();
+        const float b = s_b[r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_vbT[(c8 + e) * L::LDT + r] = from_f32<TC>(vget<TC>(x, e) * b);
+      }
     }
     __syncthreads();
     for (int tn = wid; tn < vw / 16; tn += 4) {
