@@ -187,7 +187,7 @@ int kairos_gdn_fused_recurrent_fwd(const void* q, const void* k, const void* v, 
  * with x~ = x inside each sequence and, before its first token, initial_state
  * (the cache [N, D, W], slot W-1 the most recent input; NULL = zeros).
  * x, y: [B*T, D] fp32 or bf16 (16-byte aligned, D a multiple of 8); weight
- * [D, W] and bias [D] (NULL = none) in w_dtype; initial_state / final_state
+ * [D, W] (16-byte aligned) and bias [D] (NULL = none) in w_dtype; initial_state / final_state
  * [N, D, W] in x's dtype, final_state = the last W entries of [cache, x] per
  * sequence (NULL = not wanted; must not alias initial_state).  W in 1..4.
  * activation_silu: y = z sigmoid(z).  l2norm_head_dim (0 = off, else 64, 128,

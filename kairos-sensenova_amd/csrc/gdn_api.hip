@@ -650,7 +650,8 @@ int kairos_gdn_causal_conv1d_fwd(const void* x, const void* weight, const void* 
   const int64_t N = cu_seqlens ? n_seqs : B;
   if (N > 0x7fffffff || D > 0x7fffffff) return fail(KAIROS_GDN_EINVAL, "%s: too many sequences or channels", what);
   if (B * T > 0 && (!x || !weight || !y)) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
-  if (!aligned16(x) || !aligned16(y)) return fail(KAIROS_GDN_EINVAL, "%s: x and y must be 16-byte aligned", what);
+  if (!aligned16(x) || !aligned16(y) || !aligned16(weight))
+    return fail(KAIROS_GDN_EINVAL, "%s: x, y and weight must be 16-byte aligned", what);
   if (final_state && final_state == initial_state)
     return fail(KAIROS_GDN_EINVAL, "%s: final_state must not alias initial_state", what);
   kgdn::ConvArgs a{};

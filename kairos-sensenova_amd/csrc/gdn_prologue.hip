@@ -28,7 +28,7 @@ namespace kgdn {
 
 namespace {
 
-constexpr int kConvRun = 32;     // tokens per wave
+constexpr int kConvRun = 64;     // tokens per wave (a sweep of 8..256 at the model shape: 64 fastest)
 constexpr int kConvWaves = 4;
 
 __device__ __forceinline__ float sigmoid_f(float z) {
@@ -81,13 +81,23 @@ __global__ __launch_bounds__(WAVE * kConvWaves) void conv1d_kernel(ConvArgs a, i
   const TX* x = static_cast<const TX*>(a.x);
   TX* y = static_cast<TX*>(a.y);
 
+  // taps of the lane's 8 channels: 8 W consecutive elements of weight [D, W], read 8 at a time
   float wt[W][8], bias[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int q = 0; q < W; ++q) {
+    float w8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (ok) {
+      if (a.w_dtype == DT_F32) ld_row8<float>(static_cast<const float*>(a.w) + (int64_t)c0 * W + 8 * q, w8);
+      else ld_row8<bf16>(static_cast<const bf16*>(a.w) + (int64_t)c0 * W + 8 * q, w8);
+    }
 #pragma unroll
-    for (int i = 0; i < W; ++i) wt[i][e] = ok ? ld_scalar(a.w, (int64_t)(c0 + e) * W + i, a.w_dtype) : 0.f;
-    bias[e] = 0.f;
+    for (int e = 0; e < 8; ++e) {
+      const int f = 8 * q + e;                       // flat index (channel c0 + f / W, tap f % W)
+      wt[f % W][f / W] = w8[e];
+    }
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) bias[e] = 0.f;
   if (a.bias && ok) ld_chan8(a.bias, c0, a.w_dtype, bias);
 
   int n;

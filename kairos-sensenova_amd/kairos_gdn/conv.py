@@ -49,6 +49,8 @@ def causal_conv1d(x: torch.Tensor, weight: torch.Tensor | None = None, bias: tor
         raise ValueError(f"The batch size is expected to be 1 rather than {B} when using `cu_seqlens`.")
     x = x.contiguous()
     weight = weight.contiguous()
+    if weight.data_ptr() % 16:                       # the kernel reads the taps 16 bytes at a time
+        weight = weight.clone()
     bias = bias.contiguous() if bias is not None else None
     if bias is not None and bias.dtype != weight.dtype:
         bias = bias.to(weight.dtype)
