@@ -163,6 +163,9 @@ GPU_CASES = [
     ("gk_gv_colbeta", 1, 33, 3, 3, 32, 40, None, "fp32", "gk,gv,colbeta"),
     ("k16_v_ragged", 3, 9, 2, 2, 16, 20, None, "bf16", "nobeta"),
     ("no_h0_no_g", 1, 17, 2, 2, 128, 64, None, "bf16", "nog,noh0"),
+    # the vector form (K in {64, 128, 256}, V a multiple of 16) with every optional input
+    ("vec_gk_gv_colbeta", 2, 21, 2, 4, 64, 32, None, "fp32", "gk,gv,colbeta"),
+    ("vec_varlen_k256", 1, 40, 2, 2, 256, 64, [0, 7, 7, 40], "bf16", "l2"),
 ]
 
 
