@@ -281,13 +281,45 @@ constexpr int WW = 4;                     // waves (x 16 columns) per workgroup
 constexpr int WK = 256;
 constexpr int LDW = WK + 8;               // w row stride (elements)
 
+// k tile [64 tokens][256] in LDS: 16-byte chunk c of row r at chunk position c ^ kswz(r).  Only the
+// position mod 16 decides the bank group of a 16-byte piece (rows are 512 bytes), and the 8 rows x 2
+// chunks of a transposed read (ds_read_b64_tr_b16, 32 lanes of 8 bytes) get 16 distinct positions.
+__device__ __forceinline__ int kswz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int kswz_off(int r, int c8) { return r * WK + ((c8 ^ kswz(r)) << 3); }
+
+typedef short wide_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) wide_s16x4 wide_lds_s16x4;
+typedef __attribute__((address_space(3))) const void wide_lds_void;
+
+// LDS address space pointer of a pointer into this workgroup's shared memory
+__device__ __forceinline__ wide_lds_s16x4* wide_lds_ptr(const void* p) {
+  return (wide_lds_s16x4*)(uintptr_t)(uint32_t)(uintptr_t)(wide_lds_void*)p;
+}
+
+// A fragment of k^T for the update: rows d = d0 + l%16, K index = tokens 32 ks + {4 lg + e, 16 + 4 lg + e}
+// (the accumulator order).  ds_read_b64_tr_b16: within 16 lanes, lane i reads 4 columns of one token
+// row and lane j receives element j % 4 of lane 4e + j / 4's read as its element e.
+__device__ __forceinline__ Frag<bf16> k_tr_frag(const bf16* s_k, int ks, int d0) {
+  const int l = lane_id();
+  const int lg = l >> 4, i = l & 15;
+  const int col = d0 + 4 * (i & 3);
+  const int r0 = 32 * ks + 4 * lg + (i >> 2);
+  const bf16* p0 = s_k + kswz_off(r0, col >> 3) + (col & 7);
+  const bf16* p1 = s_k + kswz_off(r0 + 16, col >> 3) + (col & 7);
+  const wide_s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(wide_lds_ptr(p0));
+  const wide_s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(wide_lds_ptr(p1));
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  return f;
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 template <typename TK>
 struct WideChunk {
   uint4 w[8];            // this thread's 8 x 8 elements of w (row-major items tid + 256 i)
-  uint32_t k[32];        // k^T pairs: (k[2p][d], k[2p+1][d]) as bf16 lo / hi, d = 32 (tid / 32) + i, p = tid % 32
+  uint4 k[8];            // the same items of k, as bf16 (fp8 k dequantised at load)
   uint2 u[4];            // u of the wave's 16 columns, C layout, 4 row tiles, 4 bf16 each
   float gcl;             // gc of token t0 + lane (0 past the chunk's end); rows get theirs by shuffle
   int nv;
@@ -310,17 +342,22 @@ __device__ __forceinline__ void wide_prefetch(WideChunk<TK>& P, const FwdHArgs& 
   }
   const TK* k = reinterpret_cast<const TK*>(a.k);
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
-  const int p = tid & 31, cb = tid >> 5;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    float x0[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, x1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (2 * p < nv) load8_in<TK>(k + ((t0 + 2 * p) * H + h) * WK + 32 * cb + 8 * b, ks_, x0);
-    if (2 * p + 1 < nv) load8_in<TK>(k + ((t0 + 2 * p + 1) * H + h) * WK + 32 * cb + 8 * b, ks_, x1);
+  for (int i = 0; i < 8; ++i) {
+    const int item = tid + 256 * i;
+    const int r = item >> 5, cb = item & 31;
+    if constexpr (sizeof(TK) == 2) {
+      P.k[i] = r < nv ? *reinterpret_cast<const uint4*>(k + ((t0 + r) * H + h) * WK + 8 * cb) : make_uint4(0, 0, 0, 0);
+    } else {                                          // fp8: dequantise to bf16 (scalar locals for the bit casts)
+      float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (r < nv) load8_in<TK>(k + ((t0 + r) * H + h) * WK + 8 * cb, ks_, x);
+      uint32_t wd[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      // scalar locals: __builtin_bit_cast of a vector-element expression reads element 0 (hipcc 7.2)
-      const bf16 lo = (bf16)x0[e], hi = (bf16)x1[e];
-      P.k[8 * b + e] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      for (int q = 0; q < 4; ++q) {
+        const bf16 lo = (bf16)x[2 * q], hi = (bf16)x[2 * q + 1];
+        wd[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+      P.k[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
     }
   }
   if (active) {
@@ -345,7 +382,7 @@ __device__ __forceinline__ void wide_lds_barrier() {
 template <typename TK>
 __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, int total_units) {
   __shared__ __align__(16) bf16 s_w[C * LDW];            // w rows [t][k]
-  __shared__ __align__(16) bf16 s_kT[WK * LDT];          // k^T [k][t]
+  __shared__ __align__(16) bf16 s_k[C * WK];              // k rows [t][k], 16-byte chunks swizzled (kswz)
   __shared__ __align__(16) bf16 s_vg[WW][16 * LDT];      // per wave: gated v'^T [col][t]
 
   const int per_xcd = gridDim.x / 8;                      // XCD-aware order (see fwd_h_kernel)
@@ -411,10 +448,10 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       const int item = tid + 256 * i;
       *reinterpret_cast<uint4*>(s_w + (item >> 5) * LDW + 8 * (item & 31)) = cur.w[i];
     }
-    {
-      const int p = tid & 31, cb = tid >> 5;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) *reinterpret_cast<uint32_t*>(s_kT + (32 * cb + i) * LDT + 2 * p) = cur.k[i];
+    for (int i = 0; i < 8; ++i) {
+      const int item = tid + 256 * i;
+      *reinterpret_cast<uint4*>(s_k + kswz_off(item >> 5, item & 31)) = cur.k[i];
     }
     wide_lds_barrier();
     if (it + 2 < nchunks) {
@@ -462,9 +499,12 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm)
         st4<bf16>(vg + lc * LDT + 16 * tm + 4 * lg, vgv[tm][0], vgv[tm][1], vgv[tm][2], vgv[tm][3]);
-      // the gated v' tile is read back by other lanes of this wave only
+      // the gated v' tile is read back by other lanes of this wave only, in the accumulator K
+      // order of the transposed k fragments (tokens 32 ks + 4 lg .. and 32 ks + 16 + 4 lg ..)
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      const Frag<bf16> b0 = lds_frag<bf16>(vg, LDT, 0, 0), b1 = lds_frag<bf16>(vg, LDT, 0, 32);
+      const bf16* vgr = vg + lc * LDT + 4 * lg;
+      const Frag<bf16> b0 = join<bf16>(ld_half<bf16>(vgr), ld_half<bf16>(vgr + 16));
+      const Frag<bf16> b1 = join<bf16>(ld_half<bf16>(vgr + 32), ld_half<bf16>(vgr + 48));
       // S = exp(g_last) S + k^T (v' gated) (chunk_delta_h.py:163-211)
       const float eg = gexp(gl);
 #pragma unroll
@@ -472,8 +512,8 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
         Frag<bf16> ka[4][2];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          ka[q][0] = lds_frag<bf16>(s_kT, LDT, 16 * (k4 + q), 0);
-          ka[q][1] = lds_frag<bf16>(s_kT, LDT, 16 * (k4 + q), 32);
+          ka[q][0] = k_tr_frag(s_k, 0, 16 * (k4 + q));
+          ka[q][1] = k_tr_frag(s_k, 1, 16 * (k4 + q));
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
