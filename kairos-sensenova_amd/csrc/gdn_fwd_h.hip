@@ -384,6 +384,8 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
   __shared__ __align__(16) bf16 s_w[C * LDW];            // w rows [t][k]
   __shared__ __align__(16) bf16 s_k[C * WK];              // k rows [t][k], 16-byte chunks swizzled (kswz)
   __shared__ __align__(16) bf16 s_vg[WW][16 * LDT];      // per wave: gated v'^T [col][t]
+  __shared__ __align__(16) bf16 s_hs[WW][16 * LDW];      // per wave: h snapshot [col][k] on its way to HBM
+  __shared__ __align__(16) bf16 s_vn[WW][16 * LDT];      // per wave: v_new [col][t] on its way to HBM
 
   const int per_xcd = gridDim.x / 8;                      // XCD-aware order (see fwd_h_kernel)
   const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -460,10 +462,18 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
     }
     const int nv = cur.nv;
     if (active) {
-      // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139)
-      bf16* hrow = hT + ((c * H + h) * V + vcol) * WK + 4 * lg;
+      // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139): through the
+      // wave's LDS tile so that each store instruction writes two whole 512-byte rows of hT
+      bf16* hs = s_hs[wid];
 #pragma unroll
-      for (int kt = 0; kt < 16; ++kt) st4<bf16>(hrow + 16 * kt, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+      for (int kt = 0; kt < 16; ++kt) st4<bf16>(hs + lc * LDW + 16 * kt + 4 * lg, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      bf16* hcol = hT + ((c * H + h) * V + v0) * WK;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int pc = l + 64 * i, r = pc >> 5, ch = pc & 31;   // row (column of S), 16-byte chunk
+        *reinterpret_cast<uint4*>(hcol + r * WK + 8 * ch) = *reinterpret_cast<const uint4*>(hs + r * LDW + 8 * ch);
+      }
       // w @ bf16(S): the B fragment of a 32-deep step is two accumulator tiles; the A
       // fragment takes the same K order (rows 4 lg .. and 16 + 4 lg .. of the step).
       // K steps outermost: one B fragment live, the 4 row tiles' A reads batched.
@@ -488,7 +498,7 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       for (int tm = 0; tm < 4; ++tm) {
         const f32x4 uv = {bf16_lo(cur.u[tm].x), bf16_hi(cur.u[tm].x), bf16_lo(cur.u[tm].y), bf16_hi(cur.u[tm].y)};
         const f32x4 vp = uv - acc[tm];              // v' = u - w h (chunk_delta_h.py:141-157)
-        st4<bf16>(vnT + ((c * H + h) * V + vcol) * C + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
+        st4<bf16>(s_vn[wid] + lc * LDT + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int t = 16 * tm + 4 * lg + j;
@@ -500,8 +510,17 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       for (int tm = 0; tm < 4; ++tm)
         st4<bf16>(vg + lc * LDT + 16 * tm + 4 * lg, vgv[tm][0], vgv[tm][1], vgv[tm][2], vgv[tm][3]);
       // the gated v' tile is read back by other lanes of this wave only, in the accumulator K
-      // order of the transposed k fragments (tokens 32 ks + 4 lg .. and 32 ks + 16 + 4 lg ..)
+      // order of the transposed k fragments (tokens 32 ks + 4 lg .. and 32 ks + 16 + 4 lg ..);
+      // v_new (ungated) leaves through the wave's LDS tile as whole 128-byte rows of vnT
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      {
+        bf16* vcolp = vnT + ((c * H + h) * V + v0) * C;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int pc = l + 64 * i, r = pc >> 3, ch = pc & 7;
+          *reinterpret_cast<uint4*>(vcolp + r * C + 8 * ch) = *reinterpret_cast<const uint4*>(s_vn[wid] + r * LDT + 8 * ch);
+        }
+      }
       const bf16* vgr = vg + lc * LDT + 4 * lg;
       const Frag<bf16> b0 = join<bf16>(ld_half<bf16>(vgr), ld_half<bf16>(vgr + 16));
       const Frag<bf16> b1 = join<bf16>(ld_half<bf16>(vgr + 32), ld_half<bf16>(vgr + 48));
