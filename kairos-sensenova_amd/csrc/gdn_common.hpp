@@ -215,6 +215,63 @@ __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
 }
 
 // ---------------------------------------------------------------------------
+// swizzled row-major bf16 tiles [rows][NC] read transposed
+// ---------------------------------------------------------------------------
+// 16-byte chunk c of row r sits at chunk position c ^ swz(r).  LDS serves 256
+// bytes per clock (64 banks of 4 bytes).  For NC >= 128 (rows of 256 bytes or
+// more) only the position mod 16 decides a 16-byte piece's bank group, and
+// swz(r) = 2 (r mod 8) + (r / 8 mod 2) gives the 8 rows x 2 chunks of a
+// transposed read (ds_read_b64_tr_b16, 32 lanes of 8 bytes) 16 distinct
+// positions; for NC = 64 (two rows per 256-byte bank row) a permutation of r / 2
+// does the same within the row's 8 chunks.
+template <int NC>
+__device__ __forceinline__ int swz_off(int r, int c8) {
+  static_assert(NC == 64 || NC % 128 == 0, "swizzled tiles are 64 or a multiple of 128 columns wide");
+  const int s = NC >= 128 ? ((r & 7) << 1) | ((r >> 3) & 1) : (((r >> 1) & 3) << 1) | ((r >> 3) & 1);
+  return r * NC + ((c8 ^ s) << 3);
+}
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(3))) const void lds_cvoid_t;
+
+// ds_read_b64_tr_b16 of the 8 bytes at p (a pointer into this workgroup's LDS)
+__device__ __forceinline__ s16x4_t lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_s16x4_t*)(uintptr_t)(uint32_t)(uintptr_t)(lds_cvoid_t*)p);
+}
+
+// Transposed MFMA fragment of a swizzled tile t [rows][NC]: lane (l % 16 = j, l / 16 = lg) gets
+// t[32 ks + 4 lg + e][c0 + j] and t[32 ks + 16 + 4 lg + e][c0 + j], e = 0..3 -- as an operand its
+// M / N index is the column c0 + j and its K index the row, in the accumulator order (rows 4 lg ..
+// and 16 + 4 lg .. of the 32-deep step).  Within 16 lanes, lane i reads 4 columns of one row and
+// lane j receives element j % 4 of lane 4e + j / 4's read as its element e.
+template <int NC>
+__device__ __forceinline__ Frag<bf16> tr_frag(const bf16* t, int ks, int c0) {
+  const int l = lane_id();
+  const int lg = l >> 4, i = l & 15;
+  const int col = c0 + 4 * (i & 3);
+  const int r0 = 32 * ks + 4 * lg + (i >> 2);
+  const s16x4_t a = lds_read_tr16(t + swz_off<NC>(r0, col >> 3) + (col & 7));
+  const s16x4_t b = lds_read_tr16(t + swz_off<NC>(r0 + 16, col >> 3) + (col & 7));
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+  return f;
+}
+
+// Row fragment in the accumulator K order: row r, columns 32 ks + 4 lg .. +3 and 32 ks + 16 + 4 lg .. +3
+// of a row-major tile with row stride ld (elements; 8-byte aligned rows).
+__device__ __forceinline__ Frag<bf16> acc_order_row(const bf16* t, int ld, int r, int ks) {
+  const int lg = lane_id() >> 4;
+  const bf16* p = t + r * ld + 32 * ks + 4 * lg;
+  const uint2 a = *reinterpret_cast<const uint2*>(p);
+  const uint2 b = *reinterpret_cast<const uint2*>(p + 16);
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+  return f;
+}
+
+// ---------------------------------------------------------------------------
 // sequence / chunk addressing
 // ---------------------------------------------------------------------------
 // Chunks of all sequences are numbered 0..NC-1 in order (sequence-major).

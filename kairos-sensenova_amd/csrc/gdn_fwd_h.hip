@@ -281,37 +281,10 @@ constexpr int WW = 4;                     // waves (x 16 columns) per workgroup
 constexpr int WK = 256;
 constexpr int LDW = WK + 8;               // w row stride (elements)
 
-// k tile [64 tokens][256] in LDS: 16-byte chunk c of row r at chunk position c ^ kswz(r).  Only the
-// position mod 16 decides the bank group of a 16-byte piece (rows are 512 bytes), and the 8 rows x 2
-// chunks of a transposed read (ds_read_b64_tr_b16, 32 lanes of 8 bytes) get 16 distinct positions.
-__device__ __forceinline__ int kswz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
-__device__ __forceinline__ int kswz_off(int r, int c8) { return r * WK + ((c8 ^ kswz(r)) << 3); }
-
-typedef short wide_s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) wide_s16x4 wide_lds_s16x4;
-typedef __attribute__((address_space(3))) const void wide_lds_void;
-
-// LDS address space pointer of a pointer into this workgroup's shared memory
-__device__ __forceinline__ wide_lds_s16x4* wide_lds_ptr(const void* p) {
-  return (wide_lds_s16x4*)(uintptr_t)(uint32_t)(uintptr_t)(wide_lds_void*)p;
-}
-
-// A fragment of k^T for the update: rows d = d0 + l%16, K index = tokens 32 ks + {4 lg + e, 16 + 4 lg + e}
-// (the accumulator order).  ds_read_b64_tr_b16: within 16 lanes, lane i reads 4 columns of one token
-// row and lane j receives element j % 4 of lane 4e + j / 4's read as its element e.
-__device__ __forceinline__ Frag<bf16> k_tr_frag(const bf16* s_k, int ks, int d0) {
-  const int l = lane_id();
-  const int lg = l >> 4, i = l & 15;
-  const int col = d0 + 4 * (i & 3);
-  const int r0 = 32 * ks + 4 * lg + (i >> 2);
-  const bf16* p0 = s_k + kswz_off(r0, col >> 3) + (col & 7);
-  const bf16* p1 = s_k + kswz_off(r0 + 16, col >> 3) + (col & 7);
-  const wide_s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(wide_lds_ptr(p0));
-  const wide_s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(wide_lds_ptr(p1));
-  Frag<bf16> f;
-  f.v = __builtin_bit_cast(bf16x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
-  return f;
-}
+// k tile [64 tokens][256] in LDS, 16-byte chunks swizzled (swz_off, gdn_common.hpp), read as k^T
+// with the transposed read (tr_frag).
+__device__ __forceinline__ int kswz_off(int r, int c8) { return swz_off<WK>(r, c8); }
+__device__ __forceinline__ Frag<bf16> k_tr_frag(const bf16* s_k, int ks, int d0) { return tr_frag<WK>(s_k, ks, d0); }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
