@@ -259,18 +259,6 @@ __device__ __forceinline__ Frag<bf16> tr_frag(const bf16* t, int ks, int c0) {
   return f;
 }
 
-// Row fragment in the accumulator K order: row r, columns 32 ks + 4 lg .. +3 and 32 ks + 16 + 4 lg .. +3
-// of a row-major tile with row stride ld (elements; 8-byte aligned rows).
-__device__ __forceinline__ Frag<bf16> acc_order_row(const bf16* t, int ld, int r, int ks) {
-  const int lg = lane_id() >> 4;
-  const bf16* p = t + r * ld + 32 * ks + 4 * lg;
-  const uint2 a = *reinterpret_cast<const uint2*>(p);
-  const uint2 b = *reinterpret_cast<const uint2*>(p + 16);
-  Frag<bf16> f;
-  f.v = __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
-  return f;
-}
-
 // ---------------------------------------------------------------------------
 // sequence / chunk addressing
 // ---------------------------------------------------------------------------
