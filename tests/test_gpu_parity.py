@@ -226,6 +226,8 @@ EDGE_CASES = [
     # head_dim=256, expand_v=2: layers/gated_deltanet.py:90-93,122-123)
     ("bf16", 1, 300, 2, 256, 512, None, True, True),
     ("bf16", 1, 400, 2, 256, 512, [0, 1, 130, 400], False, True),
+    # a last chunk of 20 tokens: gate shuffles in ragged chunks must read from active lanes
+    ("bf16", 1, 1300, 2, 256, 512, None, False, True),
     ("fp32", 1, 200, 1, 256, 256, None, False, True),
     ("bf16", 2, 150, 2, 128, 48, None, False, True),
 ]
@@ -393,6 +395,28 @@ def quantize_fp8(x):
 
 def dequant_bf16(codes, scale):
     return O.to_bf16(O.fp8_e4m3_decode(codes) * scale[None, None, :, None])
+
+
+@pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
+def test_fp8_qk_model_head_dims():
+    """fp8 q/k at dk=256, dv=512 (the fused recurrence + output of the stage path), varlen."""
+    B, T, H, K, V = 1, 300, 2, 256, 512
+    cu = [0, 130, 300]
+    note(f"fp8 q/k B={B} T={T} H={H} K={K} V={V} cu={cu}")
+    x = make_inputs(B, T, H, K, V, seed=31, dtype="bf16", n_states=2)
+    qc, qs = quantize_fp8(x["q"])
+    kc, ks = quantize_fp8(x["k"])
+    d = to_dev(x, "bf16")
+    q8 = torch.from_numpy(qc).to("cuda").view(torch.float8_e4m3fn)
+    k8 = torch.from_numpy(kc).to("cuda").view(torch.float8_e4m3fn)
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda")
+    o, ht = kairos_gdn.chunk_gated_delta_rule(q8, k8, d["v"], d["g"], d["beta"], initial_state=d["h0"],
+                                              output_final_state=True, cu_seqlens=cu_t, q_scale=dev(qs),
+                                              k_scale=dev(ks))
+    torch.cuda.synchronize()
+    assert o.dtype == torch.bfloat16
+    xd = dict(x, q=dequant_bf16(qc, qs), k=dequant_bf16(kc, ks))
+    check_against_oracle(xd, "bf16", o, ht, cu=cu)
 
 
 @pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
