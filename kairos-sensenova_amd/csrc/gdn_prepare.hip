@@ -33,27 +33,35 @@ __device__ __forceinline__ void st_pair(TC* p, float a, float b) {
   }
 }
 
-// LDS plan.  Region 0 holds k row-major for K.K^T; once A is formed it is
-// reused for the rounded inverse Ai and, after it, the v^T pass buffer: v is
-// staged VP columns at a time (u is separable over V), so V = 512 fits.
+// LDS plan.  Region 0 holds k row-major for K.K^T.  The A tiles wait in
+// registers until every wave is done with k, then region 0 holds A (fp32), the
+// rounded inverse Ai after it, and after that the v pass buffer: v is staged VP
+// columns at a time (u is separable over V).  VP is the widest pass that keeps
+// the tile within 80 KB (two workgroups per CU, so one's serial phases overlap
+// the other's), else within 160 KB.
 template <typename TC, int K>
 struct PrepLds {
   static constexpr int LDK = K + 8;      // s_k row stride (elements)
   static constexpr int LDT = C + 8;      // transposed tiles / Ai row stride
   static constexpr int LDA = C + 4;      // fp32 A / inverse row stride
+  static constexpr size_t al16(size_t x) { return (x + 15) / 16 * 16; }
   static constexpr size_t k_bytes = sizeof(TC) * C * LDK;
-  static constexpr size_t ai_bytes = (sizeof(TC) * C * LDT + 15) / 16 * 16;
-  static constexpr size_t fixed = sizeof(TC) * K * LDT + sizeof(float) * C * LDA + sizeof(float) * 3 * C;
+  static constexpr size_t a_bytes = al16(sizeof(float) * C * LDA);
+  static constexpr size_t ai_bytes = al16(sizeof(TC) * C * LDT);
+  static constexpr size_t fixed = al16(sizeof(TC) * K * LDT) + sizeof(float) * 3 * C;
   static constexpr size_t region0_for(int vp) {
-    return k_bytes > ai_bytes + sizeof(TC) * vp * LDT ? k_bytes : ai_bytes + sizeof(TC) * vp * LDT;
+    return k_bytes > a_bytes + ai_bytes + sizeof(TC) * vp * LDT ? al16(k_bytes)
+                                                                 : a_bytes + ai_bytes + al16(sizeof(TC) * vp * LDT);
   }
-  static constexpr int VP = region0_for(256) + fixed <= 160 * 1024 ? 256
-                          : region0_for(128) + fixed <= 160 * 1024 ? 128 : 64;   // v columns per pass
-  static constexpr size_t region0 = (region0_for(VP) + 15) / 16 * 16;
-  static constexpr size_t off_vbT = ai_bytes;                   // inside region 0, after Ai
+  static constexpr size_t fits(int vp, size_t cap) { return region0_for(vp) + fixed <= cap; }
+  static constexpr int VP = fits(256, 80 * 1024) ? 256 : fits(128, 80 * 1024) ? 128 : fits(64, 80 * 1024) ? 64
+                          : fits(256, 160 * 1024) ? 256 : fits(128, 160 * 1024) ? 128 : 64;   // v columns per pass
+  static constexpr size_t region0 = region0_for(VP);
+  static constexpr size_t off_A = 0;                            // region 0 after K.K^T
+  static constexpr size_t off_Ai = a_bytes;
+  static constexpr size_t off_vbT = a_bytes + ai_bytes;         // after Ai
   static constexpr size_t off_kbT = region0;
-  static constexpr size_t off_A = off_kbT + sizeof(TC) * K * LDT;
-  static constexpr size_t off_g = off_A + sizeof(float) * C * LDA;
+  static constexpr size_t off_g = off_kbT + al16(sizeof(TC) * K * LDT);
   static constexpr size_t total = off_g + sizeof(float) * 3 * C;
 };
 
@@ -62,10 +70,10 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   using L = PrepLds<TC, K>;
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_k = reinterpret_cast<TC*>(smem);
-  TC* s_Ai = reinterpret_cast<TC*>(smem);                 // aliases s_k once K.K^T is done
-  TC* s_vbT = reinterpret_cast<TC*>(smem + L::off_vbT);   // aliases s_k too (after Ai)
+  float* s_A = reinterpret_cast<float*>(smem + L::off_A);  // aliases s_k once K.K^T is done
+  TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);     // after A
+  TC* s_vbT = reinterpret_cast<TC*>(smem + L::off_vbT);   // after Ai
   TC* s_kbT = reinterpret_cast<TC*>(smem + L::off_kbT);
-  float* s_A = reinterpret_cast<float*>(smem + L::off_A);
   float* s_g = reinterpret_cast<float*>(smem + L::off_g);
   float* s_eg = s_g + C;
   float* s_b = s_g + 2 * C;
@@ -154,8 +162,13 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
   __syncthreads();
 
-  // ---- A = beta exp(dg) K K^T, strictly lower (10 lower 16x16 tiles over 4 waves)
-  for (int tile = wid; tile < 10; tile += 4) {
+  // ---- A = beta exp(dg) K K^T, strictly lower (10 lower 16x16 tiles over 4 waves); the tiles
+  //      stay in registers until every wave has read k, then go to region 0
+  f32x4 av[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int tile = wid + 4 * q;
+    if (tile >= 10) break;                         // uniform per wave
     const int tm = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
     const int tn = tile - tm * (tm + 1) / 2;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -166,10 +179,18 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * tm + 4 * lg + jj;
-      float val = 0.f;
-      if (i > j && i < nv) val = acc[jj] * gexp(s_g[i] - s_g[j]) * s_b[i];
-      s_A[i * L::LDA + j] = val;
+      av[q][jj] = (i > j && i < nv) ? acc[jj] * gexp(s_g[i] - s_g[j]) * s_b[i] : 0.f;
     }
+  }
+  __syncthreads();                                 // k is dead: region 0 becomes A
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int tile = wid + 4 * q;
+    if (tile >= 10) break;
+    const int tm = tile < 1 ? 0 : tile < 3 ? 1 : tile < 6 ? 2 : 3;
+    const int tn = tile - tm * (tm + 1) / 2;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) s_A[(16 * tm + 4 * lg + jj) * L::LDA + 16 * tn + lc] = av[q][jj];
   }
   __syncthreads();
 
@@ -265,8 +286,8 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
     }
   }
   // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
-  //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 (k is dead,
-  //      Ai sits below the pass buffer), so staging overlaps the w products above
+  //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after A and Ai,
+  //      so staging overlaps the w products above
   TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
   for (int p0 = 0; p0 < V; p0 += L::VP) {
     const int vw = min(L::VP, V - p0);             // a multiple of 16
