@@ -4,12 +4,16 @@
 //   o = scale * (q @ h_c) * exp(gc)
 //     + scale * (mask_{i>=j}(q k^T * exp(gc_i - gc_j))).to(storage) @ v_new
 //
-// q and k of the chunk are staged row-major in LDS (K-contiguous for q.k^T and
-// as the B operand of the transposed products).  The kernel computes o^T
+// q of the chunk is staged row-major in LDS (K-contiguous for q.k^T and as the
+// B operand of the transposed products); k is read as 16-byte fragments from
+// global memory when it is stored in the compute type (staged otherwise), so the
+// bf16 K=256 tile takes 43 KB and three workgroups share a CU.  The kernel computes o^T
 // (rows = V columns, cols = tokens): the A operands are then the stored state
 // snapshot hT [NC, H, V, K] and v_new^T [NC, H, V, 64], read as 16-byte
 // fragments straight from global memory, and the accumulator layout gives each
 // lane 4 consecutive V elements of one token, i.e. 8-byte token-major stores.
+#include <type_traits>
+
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
 
@@ -20,11 +24,11 @@ namespace {
 constexpr int NT_O = 256;
 constexpr int LDT = C + 8;
 
-template <typename TC, int K>
+template <typename TC, int K, bool StageK>
 struct OLds {
   static constexpr int LDK = K + 8;
   static constexpr size_t off_k = sizeof(TC) * C * LDK;
-  static constexpr size_t off_A = off_k * 2;
+  static constexpr size_t off_A = off_k * (StageK ? 2 : 1);
   static constexpr size_t off_g = off_A + sizeof(TC) * C * LDT;
   static constexpr size_t total = off_g + sizeof(float) * C;
 };
@@ -42,8 +46,10 @@ __device__ __forceinline__ Frag<TC> gfrag(const TC* p) {   // 8 consecutive elem
 }
 
 template <typename TC, typename TQ, int K>
-__global__ __launch_bounds__(NT_O) void fwd_o_kernel(FwdOArgs a, int V) {
-  using L = OLds<TC, K>;
+// bf16: at most 168 VGPRs, so three workgroups (12 waves) share a CU as the LDS allows
+__global__ __launch_bounds__(NT_O, sizeof(TC) == 2 ? 3 : 1) void fwd_o_kernel(FwdOArgs a, int V) {
+  constexpr bool kStageK = !std::is_same<TC, TQ>::value;   // fp8 k is dequantised into LDS
+  using L = OLds<TC, K, kStageK>;
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_q = reinterpret_cast<TC*>(smem);
   TC* s_k = reinterpret_cast<TC*>(smem + L::off_k);
@@ -67,7 +73,7 @@ __global__ __launch_bounds__(NT_O) void fwd_o_kernel(FwdOArgs a, int V) {
   const TQ* kin = reinterpret_cast<const TQ*>(a.k);
   const float qs = a.q_scale ? a.q_scale[h] : 1.f;
   const float ksc = a.k_scale ? a.k_scale[h] : 1.f;
-  for (int idx = tid; idx < 2 * C * (K / 8); idx += NT_O) {
+  for (int idx = tid; idx < (kStageK ? 2 : 1) * C * (K / 8); idx += NT_O) {
     const int which = idx / (C * (K / 8));
     const int rem = idx % (C * (K / 8));
     const int r = rem / (K / 8), c8 = (rem % (K / 8)) * 8;
@@ -86,9 +92,21 @@ __global__ __launch_bounds__(NT_O) void fwd_o_kernel(FwdOArgs a, int V) {
     const int tm = tile >> 2, tn = tile & 3;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (tn <= tm) {
+      if constexpr (kStageK) {
 #pragma unroll
-      for (int ks = 0; ks < K / 32; ++ks)
-        mma(acc, lds_frag<TC>(s_q, L::LDK, 16 * tm, 32 * ks), lds_frag<TC>(s_k, L::LDK, 16 * tn, 32 * ks));
+        for (int ks = 0; ks < K / 32; ++ks)
+          mma(acc, lds_frag<TC>(s_q, L::LDK, 16 * tm, 32 * ks), lds_frag<TC>(s_k, L::LDK, 16 * tn, 32 * ks));
+      } else {
+        // k row 16 tn + lc; rows past the chunk read as zero (their products are masked anyway,
+        // and the last chunk's rows may lie past the end of the tensor)
+        const int kr = 16 * tn + lc;
+        const TC* krow = reinterpret_cast<const TC*>(a.k) + ((t0 + kr) * H + h) * K + 8 * lg;
+        Frag<TC> kf[K / 32];
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks) kf[ks] = kr < nv ? gfrag<TC>(krow + 32 * ks) : Frag<TC>{};
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks) mma(acc, lds_frag<TC>(s_q, L::LDK, 16 * tm, 32 * ks), kf[ks]);
+      }
     }
     const int j = 16 * tn + lc;
 #pragma unroll
@@ -105,25 +123,41 @@ __global__ __launch_bounds__(NT_O) void fwd_o_kernel(FwdOArgs a, int V) {
   const TC* hT = reinterpret_cast<const TC*>(a.hT) + (c * H + h) * (int64_t)V * K;
   const TC* vnT = reinterpret_cast<const TC*>(a.vnT) + (c * H + h) * (int64_t)V * C;
   TC* o = reinterpret_cast<TC*>(a.o);
-  for (int vt = wid; vt < V / 16; vt += 4) {
-    Frag<TC> hf[K / 32], vf[2];
+  // NP value tiles per wave per step (vt0, vt0 + 4, ..): their loads are all in flight before
+  // the first one's products start (one at K = 256: two would not fit in 168 VGPRs)
+  constexpr int NP = K >= 256 ? 1 : 2;
+  for (int vt0 = wid; vt0 < V / 16; vt0 += 4 * NP) {
+    // compiler-only fence: q is re-read from LDS each step rather than hoisted into
+    // 128 VGPRs, which would leave room for only two workgroups per CU
+    if constexpr (K >= 256) asm volatile("" ::: "memory");
+    Frag<TC> hf[NP][K / 32], vf[NP][2];
 #pragma unroll
-    for (int ks = 0; ks < K / 32; ++ks) hf[ks] = gfrag<TC>(hT + (16 * vt + lc) * K + 32 * ks + 8 * lg);
+    for (int p = 0; p < NP; ++p) {
+      if (vt0 + 4 * p >= V / 16) break;            // uniform per wave
+      const int vt = vt0 + 4 * p;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) vf[ks] = gfrag<TC>(vnT + (16 * vt + lc) * C + 32 * ks + 8 * lg);
+      for (int ks = 0; ks < K / 32; ++ks) hf[p][ks] = gfrag<TC>(hT + (16 * vt + lc) * K + 32 * ks + 8 * lg);
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < 2; ++ks) vf[p][ks] = gfrag<TC>(vnT + (16 * vt + lc) * C + 32 * ks + 8 * lg);
+    }
 #pragma unroll
-      for (int ks = 0; ks < K / 32; ++ks) mma(acc, hf[ks], lds_frag<TC>(s_q, L::LDK, 16 * tn, 32 * ks));
+    for (int p = 0; p < NP; ++p) {
+      if (vt0 + 4 * p >= V / 16) break;
+      const int vt = vt0 + 4 * p;
 #pragma unroll
-      for (int ks = 0; ks <= tn / 2; ++ks) mma(acc2, vf[ks], lds_frag<TC>(s_Aqk, LDT, 16 * tn, 32 * ks));
-      const int t = 16 * tn + lc;
-      const float eg = gexp(s_g[t]);
-      if (t < nv) {
-        st4<TC>(o + ((t0 + t) * H + h) * V + 16 * vt + 4 * lg,
-                acc[0] * eg * a.scale + acc2[0] * a.scale, acc[1] * eg * a.scale + acc2[1] * a.scale,
-                acc[2] * eg * a.scale + acc2[2] * a.scale, acc[3] * eg * a.scale + acc2[3] * a.scale);
+      for (int tn = 0; tn < 4; ++tn) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks) mma(acc, hf[p][ks], lds_frag<TC>(s_q, L::LDK, 16 * tn, 32 * ks));
+#pragma unroll
+        for (int ks = 0; ks <= tn / 2; ++ks) mma(acc2, vf[p][ks], lds_frag<TC>(s_Aqk, LDT, 16 * tn, 32 * ks));
+        const int t = 16 * tn + lc;
+        const float eg = gexp(s_g[t]);
+        if (t < nv) {
+          st4<TC>(o + ((t0 + t) * H + h) * V + 16 * vt + 4 * lg,
+                  acc[0] * eg * a.scale + acc2[0] * a.scale, acc[1] * eg * a.scale + acc2[1] * a.scale,
+                  acc[2] * eg * a.scale + acc2[2] * a.scale, acc[3] * eg * a.scale + acc2[3] * a.scale);
+        }
       }
     }
   }
@@ -131,7 +165,7 @@ __global__ __launch_bounds__(NT_O) void fwd_o_kernel(FwdOArgs a, int V) {
 
 template <typename TC, typename TQ, int K>
 int launch_fwd_o_t(const FwdOArgs& a, int V, int64_t nc_grid, hipStream_t s) {
-  using L = OLds<TC, K>;
+  using L = OLds<TC, K, !std::is_same<TC, TQ>::value>;
   static_assert(L::total <= 160 * 1024, "output tile does not fit in LDS");
   auto kern = fwd_o_kernel<TC, TQ, K>;
   if (L::total > 64 * 1024) {
