@@ -21,7 +21,8 @@ namespace kgdn {
 
 namespace {
 
-constexpr int NT_O = 256;
+// workgroup size: 8 waves at K = 256 (78 VGPRs, 43 KB LDS: 24 waves share a CU), else 4
+template <int K> constexpr int nt_o() { return K >= 256 ? 512 : 256; }
 constexpr int LDT = C + 8;
 
 template <typename TC, int K, bool StageK>
@@ -46,8 +47,10 @@ __device__ __forceinline__ Frag<TC> gfrag(const TC* p) {   // 8 consecutive elem
 }
 
 template <typename TC, typename TQ, int K>
-// bf16: at most 168 VGPRs, so three workgroups (12 waves) share a CU as the LDS allows
-__global__ __launch_bounds__(NT_O, sizeof(TC) == 2 ? 3 : 1) void fwd_o_kernel(FwdOArgs a, int V) {
+// bf16: three workgroups share a CU as the LDS allows (at most 168 VGPRs with 4 waves,
+// 80 with 8)
+__global__ __launch_bounds__(nt_o<K>(), sizeof(TC) == 2 ? 3 * nt_o<K>() / 256 : 1) void fwd_o_kernel(FwdOArgs a, int V) {
+  constexpr int NT_O = nt_o<K>(), NW = NT_O / WAVE;
   constexpr bool kStageK = !std::is_same<TC, TQ>::value;   // fp8 k is dequantised into LDS
   using L = OLds<TC, K, kStageK>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(NT_O, sizeof(TC) == 2 ? 3 : 1) void fwd_o_kernel(Fw
   __syncthreads();
 
   // ---- Aqk = mask_{i>=j}(q k^T exp(gc_i - gc_j)), rounded to the storage type
-  for (int tile = wid; tile < 16; tile += 4) {
+  for (int tile = wid; tile < 16; tile += NW) {
     const int tm = tile >> 2, tn = tile & 3;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (tn <= tm) {
@@ -123,18 +126,18 @@ __global__ __launch_bounds__(NT_O, sizeof(TC) == 2 ? 3 : 1) void fwd_o_kernel(Fw
   const TC* hT = reinterpret_cast<const TC*>(a.hT) + (c * H + h) * (int64_t)V * K;
   const TC* vnT = reinterpret_cast<const TC*>(a.vnT) + (c * H + h) * (int64_t)V * C;
   TC* o = reinterpret_cast<TC*>(a.o);
-  // NP value tiles per wave per step (vt0, vt0 + 4, ..): their loads are all in flight before
+  // NP value tiles per wave per step (vt0, vt0 + NW, ..): their loads are all in flight before
   // the first one's products start (one at K = 256: two would not fit in 168 VGPRs)
   constexpr int NP = K >= 256 ? 1 : 2;
-  for (int vt0 = wid; vt0 < V / 16; vt0 += 4 * NP) {
+  for (int vt0 = wid; vt0 < V / 16; vt0 += NW * NP) {
     // compiler-only fence: q is re-read from LDS each step rather than hoisted into
     // 128 VGPRs, which would leave room for only two workgroups per CU
     if constexpr (K >= 256) asm volatile("" ::: "memory");
     Frag<TC> hf[NP][K / 32], vf[NP][2];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      if (vt0 + 4 * p >= V / 16) break;            // uniform per wave
-      const int vt = vt0 + 4 * p;
+      if (vt0 + NW * p >= V / 16) break;           // uniform per wave
+      const int vt = vt0 + NW * p;
 #pragma unroll
       for (int ks = 0; ks < K / 32; ++ks) hf[p][ks] = gfrag<TC>(hT + (16 * vt + lc) * K + 32 * ks + 8 * lg);
 #pragma unroll
@@ -142,8 +145,8 @@ __global__ __launch_bounds__(NT_O, sizeof(TC) == 2 ? 3 : 1) void fwd_o_kernel(Fw
     }
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      if (vt0 + 4 * p >= V / 16) break;
-      const int vt = vt0 + 4 * p;
+      if (vt0 + NW * p >= V / 16) break;
+      const int vt = vt0 + NW * p;
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
@@ -174,7 +177,7 @@ int launch_fwd_o_t(const FwdOArgs& a, int V, int64_t nc_grid, hipStream_t s) {
       return -1;
   }
   dim3 grid((unsigned)nc_grid, (unsigned)a.H);
-  hipLaunchKernelGGL(kern, grid, dim3(NT_O), L::total, s, a, V);
+  hipLaunchKernelGGL(kern, grid, dim3(nt_o<K>()), L::total, s, a, V);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
