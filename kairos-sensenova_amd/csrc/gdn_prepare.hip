@@ -34,8 +34,8 @@ __device__ __forceinline__ void st_pair(TC* p, float a, float b) {
 }
 
 // LDS plan.  Region 0 holds k row-major for K.K^T.  The A tiles wait in
-// registers until every wave is done with k, then region 0 holds A (fp32), the
-// rounded inverse Ai after it, and after that the v pass buffer: v is staged VP
+// registers until every wave is done with k, then region 0 holds A (fp32), which
+// the rounded inverse Ai later overwrites, and after that the v pass buffer: v is staged VP
 // columns at a time (u is separable over V).  VP is the widest pass that keeps
 // the tile within 80 KB (two workgroups per CU, so one's serial phases overlap
 // the other's), else within 160 KB.
@@ -49,17 +49,17 @@ struct PrepLds {
   static constexpr size_t a_bytes = al16(sizeof(float) * C * LDA);
   static constexpr size_t ai_bytes = al16(sizeof(TC) * C * LDT);
   static constexpr size_t fixed = al16(sizeof(TC) * K * LDT) + sizeof(float) * 3 * C;
+  static constexpr size_t aai_bytes = a_bytes > ai_bytes ? a_bytes : ai_bytes;   // A, then Ai over it
   static constexpr size_t region0_for(int vp) {
-    return k_bytes > a_bytes + ai_bytes + sizeof(TC) * vp * LDT ? al16(k_bytes)
-                                                                 : a_bytes + ai_bytes + al16(sizeof(TC) * vp * LDT);
+    return k_bytes > aai_bytes + sizeof(TC) * vp * LDT ? al16(k_bytes) : aai_bytes + al16(sizeof(TC) * vp * LDT);
   }
   static constexpr size_t fits(int vp, size_t cap) { return region0_for(vp) + fixed <= cap; }
   static constexpr int VP = fits(256, 80 * 1024) ? 256 : fits(128, 80 * 1024) ? 128 : fits(64, 80 * 1024) ? 64
                           : fits(256, 160 * 1024) ? 256 : fits(128, 160 * 1024) ? 128 : 64;   // v columns per pass
   static constexpr size_t region0 = region0_for(VP);
   static constexpr size_t off_A = 0;                            // region 0 after K.K^T
-  static constexpr size_t off_Ai = a_bytes;
-  static constexpr size_t off_vbT = a_bytes + ai_bytes;         // after Ai
+  static constexpr size_t off_Ai = 0;                           // over A once the inverse is read
+  static constexpr size_t off_vbT = aai_bytes;                  // after A / Ai
   static constexpr size_t off_kbT = region0;
   static constexpr size_t off_g = off_kbT + al16(sizeof(TC) * K * LDT);
   static constexpr size_t total = off_g + sizeof(float) * 3 * C;
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_k = reinterpret_cast<TC*>(smem);
   float* s_A = reinterpret_cast<float*>(smem + L::off_A);  // aliases s_k once K.K^T is done
-  TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);     // after A
+  TC* s_Ai = reinterpret_cast<TC*>(smem + L::off_Ai);     // over A
   TC* s_vbT = reinterpret_cast<TC*>(smem + L::off_vbT);   // after Ai
   TC* s_kbT = reinterpret_cast<TC*>(smem + L::off_kbT);
   float* s_g = reinterpret_cast<float*>(smem + L::off_g);
@@ -259,16 +259,28 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
   __syncthreads();
 
-  // ---- Ai (rounded to the storage type) into LDS as the K-contiguous [t][s] operand
-  for (int idx = tid; idx < C * C; idx += NT_PREP) {
+  // ---- Ai (rounded to the storage type) into LDS as the K-contiguous [t][s] operand, over A:
+  //      every thread reads its entries into registers before any is written
+  constexpr int kAiPer = C * C / NT_PREP;
+  static_assert(C * C % NT_PREP == 0, "Ai entries must split evenly over the threads");
+  TC xr[kAiPer];
+#pragma unroll
+  for (int q = 0; q < kAiPer; ++q) {
+    const int idx = tid + q * NT_PREP;
     const int i = idx / C, j = idx % C;
     const int bi = i >> 4, bj = j >> 4;
     float x = 0.f;
     if (bi == bj) x = s_A[i * L::LDA + j];
     else if (bi > bj) x = s_A[(16 * bj + (i & 15)) * L::LDA + 16 * bi + (j & 15)];
-    const TC xs = from_f32<TC>(x);
-    s_Ai[i * L::LDT + j] = xs;
-    if (a.Ai_out && i < nv) reinterpret_cast<TC*>(a.Ai_out)[((t0 + i) * H + h) * C + j] = xs;
+    xr[q] = from_f32<TC>(x);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kAiPer; ++q) {
+    const int idx = tid + q * NT_PREP;
+    const int i = idx / C, j = idx % C;
+    s_Ai[i * L::LDT + j] = xr[q];
+    if (a.Ai_out && i < nv) reinterpret_cast<TC*>(a.Ai_out)[((t0 + i) * H + h) * C + j] = xr[q];
   }
   __syncthreads();
 
@@ -286,7 +298,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
     }
   }
   // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
-  //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after A and Ai,
+  //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after Ai,
   //      so staging overlaps the w products above
   TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
   for (int p0 = 0; p0 < V; p0 += L::VP) {
