@@ -6,23 +6,36 @@ output_final_state=True) with inputs resident in HBM, through the C ABI
 (kairos_gdn_chunk_fwd).  Prints ONE JSON line.
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+  python bench.py --config 1|3|4      # the other BASELINE configs (4: 21-frame fp8 rollout), one line each
+  python bench.py --l2norm            # config 2 with use_qk_l2norm_in_kernel=True (the layer's own mode)
   python bench.py --calibrate-copy 1024     # reference copy kernel for rocprofv3 counter scaling
   python bench.py --epilogue                # the gated RMSNorm output epilogue on config 2's o
   python bench.py --model-shape             # the Kairos 4B layer's head dims dk=256, dv=512
   python bench.py --recurrent               # the short-sequence mode's decoding step (fused_recurrent)
   python bench.py --prologue                # the layer prologue: causal conv + SiLU (+ q/k L2 norm), gates
 
-`value` is tokens/s of whole forward calls (wall clock between two device
-synchronisations around `steps` back-to-back calls).  Per-kernel times come
-from a second loop in which the library records hipEvents on the launch
-stream around each of its kernels (kairos_gdn_profile_begin/_end).  The
-roofline block is the dominant kernel's algorithmic HBM bytes per launch over
-its average duration; `traffic` is that kernel's measured HBM bytes per launch
-from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, when present.
+Timing (every mode): an untimed warm-up of at least --warmup steps AND at
+least --warmup-seconds of wall time (so the timed steps run at steady clocks;
+both figures are in the JSON), then exactly --steps steps between two device
+synchronisations.  `value` and `ms_per_step` come from that wall-clock
+interval; `step_ms` gives the median / p10 / p90 of per-step HIP events
+recorded on the launch stream in the same loop.  `cold_step_ms` times steps
+that each follow an overwrite of a 640 MiB buffer, which evicts the 256 MiB
+Infinity Cache (MALL) and the L2s, so every input comes from HBM.
+
+Roofline: `achieved` = the op's algorithmic HBM bytes (the fused
+minimum, 2*dk*s_qk + 4*dv + 8 bytes per token-head plus the initial and final
+state, 678.8 MB at config 2) over the dominant kernel's average duration;
+`whole_call` puts the same bytes over the median step.  `design_bytes` is what
+this design's dominant kernel must move (its inputs include the chunk records and
+segment states of the fused path).  `traffic` is the whole call's measured HBM
+bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE summed over the call's kernels, from
+the committed summary in profiles/), `traffic_kernel` the dominant kernel's.
 """
 import argparse
 import ctypes
 import json
+import math
 import os
 import re
 import statistics
@@ -41,6 +54,15 @@ C = 64
 RECORD = C * C * 2 + 8 * C * 4      # bytes of one (chunk, head) record written by seg_prep
 KERNELS = ["seg_prep_kernel", "seg_trans_kernel", "seg_combine_kernel", "seg_out_kernel"]
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2_hbm_traffic.md")
+FLUSH_BYTES = 640 << 20
+
+# BASELINE.json configs measured here (config 0 is the CPU plumbing case, a parity test only)
+CONFIGS = {
+    1: dict(B=1, T=8192, H=20, K=128, V=128, cu=None, seed=20261),
+    2: dict(B=1, T=32760, H=20, K=128, V=128, cu=None, seed=20262),
+    3: dict(B=1, T=53040, H=20, K=128, V=128, cu=[0, 1560, 7800, 20280, 53040], seed=20263),
+    4: dict(B=8, T=1560, H=20, K=128, V=128, cu=None, seed=20264, frames=21),
+}
 
 
 def flops_per_tok_head(K, V):
@@ -48,18 +70,23 @@ def flops_per_tok_head(K, V):
     return 6 * K * V + 6 * C * K + 4 * C * V
 
 
+def alg_bytes(tok_heads, n_states, K, V, s_qk=2, s_v=2):
+    """The op's algorithmic (compulsory) HBM bytes as SURVEY 8(d) counts them: q, k, v, o once per
+    token-head plus 8 bytes for the gate and beta, and the initial state read and the final state
+    written (fp32) per (sequence, head): 1,032 B per token-head + 128 KiB per (sequence, head) at d=128."""
+    return tok_heads * (2 * K * s_qk + 2 * V * s_v + 8) + n_states * 2 * K * V * 4
+
+
 def kernel_models(B, T, H, K, V, L, s=2, s_g=4, s_b=2):
-    """Algorithmic HBM bytes (compulsory reads + writes) and FLOPs of one launch of each kernel.
+    """Design HBM bytes (what each kernel of this design reads and writes) and FLOPs of one launch.
 
     seg_prep reads k, g, beta and writes one chunk record per (chunk, head):
-    the bf16 inverse Ai (64 x 64) and eight fp32 vectors of 64 (cumulative
-    gates and the gate / beta products the later kernels use), RECORD bytes.
+    the bf16 inverse Ai (64 x 64) and eight fp32 vectors of 64, RECORD bytes.
     seg_out reads q, k, v, the records and the segment initial states, writes
     o and final_state; seg_trans reads k, v and the records of every segment
     but the last of each sequence and writes its [M | R]; seg_combine reads
     [M | R] and h0 and writes the segment initial states.  FLOPs count every
-    MMA tile at full size: K.K^T (2CK per token) in seg_prep, the rest of the
-    chunk algebra in seg_out, w, u and the two [M | R] products in seg_trans.
+    MMA tile at full size.
     """
     nc = (T + C - 1) // C
     nseg = (nc + L - 1) // L
@@ -85,76 +112,365 @@ def kernel_models(B, T, H, K, V, L, s=2, s_g=4, s_b=2):
     }
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary, or None."""
+def measured_traffic():
+    """{kernel: HBM bytes per launch} from the committed rocprofv3 summary (empty if absent)."""
+    out = {}
     try:
         with open(TRAFFIC_FILE) as f:
             for ln in f:
                 m = re.match(r"\s*traffic_bytes_per_launch\s+(\S+)\s+(\d+)", ln)
-                if m and m.group(1) == kernel:
-                    return int(m.group(2))
+                if m:
+                    out[m.group(1)] = int(m.group(2))
     except OSError:
         pass
-    return None
+    return out
 
 
-def make_inputs(B, T, H, K, V, seed, device):
+def pct(xs, p):
+    """p-th percentile (linear interpolation) of a non-empty list."""
+    s = sorted(xs)
+    i = (len(s) - 1) * p / 100.0
+    lo = int(math.floor(i))
+    hi = min(lo + 1, len(s) - 1)
+    return s[lo] + (s[hi] - s[lo]) * (i - lo)
+
+
+def summary(xs):
+    return {"median": statistics.median(xs), "p10": pct(xs, 10), "p90": pct(xs, 90), "mean": statistics.fmean(xs),
+            "n": len(xs)}
+
+
+class Timer:
+    """Steady-state timing of a step function on the current stream (see the module docstring)."""
+
+    def __init__(self, args):
+        self.steps, self.warmup, self.floor = args.steps, args.warmup, args.warmup_seconds
+        self.cold_steps = 0 if args.no_cold else min(args.steps, 100)
+
+    def warm(self, step):
+        t0 = time.perf_counter()
+        n = 0
+        while n < self.warmup or time.perf_counter() - t0 < self.floor:
+            for _ in range(10):           # bounded queue: synchronise every 10 steps
+                step()
+                n += 1
+            torch.cuda.synchronize()
+        return n, time.perf_counter() - t0
+
+    def run(self, step):
+        n_warm, t_warm = self.warm(step)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(self.steps + 1)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev[0].record()
+        for i in range(self.steps):
+            step()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / self.steps
+        hot = [ev[i].elapsed_time(ev[i + 1]) for i in range(self.steps)]
+        res = {"wall_s": wall, "step_ms": summary(hot), "warmup_steps_run": n_warm, "warmup_wall_s": t_warm}
+        if self.cold_steps:
+            flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+            e0 = [torch.cuda.Event(enable_timing=True) for _ in range(self.cold_steps)]
+            e1 = [torch.cuda.Event(enable_timing=True) for _ in range(self.cold_steps)]
+            for i in range(self.cold_steps):
+                flush.fill_(i & 0xFF)
+                e0[i].record()
+                step()
+                e1[i].record()
+            torch.cuda.synchronize()
+            res["cold_step_ms"] = summary([a.elapsed_time(b) for a, b in zip(e0, e1)])
+            del flush
+        return res
+
+    def fields(self, res):
+        out = {"step_ms": res["step_ms"], "warmup_steps_run": res["warmup_steps_run"],
+               "warmup_wall_s": round(res["warmup_wall_s"], 3), "warmup_floor_s": self.floor}
+        if "cold_step_ms" in res:
+            out["cold_step_ms"] = res["cold_step_ms"]
+            out["cold_flush_bytes"] = FLUSH_BYTES
+        return out
+
+
+# ---------------------------------------------------------------------------
+# inputs
+# ---------------------------------------------------------------------------
+def make_inputs(B, T, H, K, V, seed, n_states=None, device="cpu", dtype=torch.bfloat16):
+    """BASELINE distributions: q, k ~ N(0,1) then L2-normalised per head; v ~ N(0,1); beta = sigmoid(N(0,1));
+    g = -softplus(N(0,1)) fp32; h0 = 0.02 N(0,1) fp32 ([n_states or B, H, K, V])."""
     g_ = torch.Generator(device="cpu").manual_seed(seed)
 
     def unit(shape):
-        x = torch.randn(shape, generator=g_)
-        return torch.nn.functional.normalize(x, dim=-1)
-    q = unit((B, T, H, K)).to(device, torch.bfloat16)
-    k = unit((B, T, H, K)).to(device, torch.bfloat16)
-    v = torch.randn((B, T, H, V), generator=g_).to(device, torch.bfloat16)
-    beta = torch.sigmoid(torch.randn((B, T, H), generator=g_)).to(device, torch.bfloat16)
+        return torch.nn.functional.normalize(torch.randn(shape, generator=g_), dim=-1)
+    q = unit((B, T, H, K)).to(device, dtype)
+    k = unit((B, T, H, K)).to(device, dtype)
+    v = torch.randn((B, T, H, V), generator=g_).to(device, dtype)
+    beta = torch.sigmoid(torch.randn((B, T, H), generator=g_)).to(device, dtype)
     g = (-torch.nn.functional.softplus(torch.randn((B, T, H), generator=g_))).to(device, torch.float32)
-    h0 = (0.02 * torch.randn((B, H, K, V), generator=g_)).to(device, torch.float32)
+    h0 = (0.02 * torch.randn((n_states or B, H, K, V), generator=g_)).to(device, torch.float32)
     return q, k, v, g, beta, h0
 
 
-def cpu_baseline(T, H, K, V, seed, min_seconds=10.0):
-    """Time the numpy oracle (bf16-emulating chunked restatement) on the host cores.
+def quantize_fp8(x):
+    """Per-head e4m3 quantisation of [B, T, H, K] with scale = amax / 448."""
+    xf = x.float()
+    scale = (xf.abs().amax(dim=(0, 1, 3)) / 448.0).clamp_min(1e-12)
+    codes = (xf / scale[None, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return codes, scale
 
-    The sample is the full config (all H heads of T tokens), repeated until at
-    least `min_seconds` of CPU work; the rate is the median over repeats.
-    """
-    sys.path.insert(0, ROOT)
-    import numpy as np
-    from threadpoolctl import threadpool_info, threadpool_limits
-    from oracle import gdn_oracle as O
-    cores = min(os.cpu_count() or 1, 16)
-    rng = np.random.default_rng(seed)
 
-    def unit(shape):
-        x = rng.standard_normal(shape, dtype=np.float32)
-        return O.to_bf16(x / np.sqrt((x * x).sum(-1, keepdims=True)))
-    q, k = unit((1, T, H, K)), unit((1, T, H, K))
-    v = O.to_bf16(rng.standard_normal((1, T, H, V), dtype=np.float32))
-    beta = O.to_bf16(1 / (1 + np.exp(-rng.standard_normal((1, T, H), dtype=np.float32))))
-    g = (-np.logaddexp(0, rng.standard_normal((1, T, H), dtype=np.float32))).astype(np.float32)
-    h0 = (0.02 * rng.standard_normal((1, H, K, V), dtype=np.float32)).astype(np.float32)
-    times = []
-    with threadpool_limits(cores):
-        t_start = time.perf_counter()
-        while not times or (time.perf_counter() - t_start < min_seconds and len(times) < 10):
-            t0 = time.perf_counter()
-            O.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True, dtype="bf16")
-            times.append(time.perf_counter() - t0)
-        blas = [i.get("num_threads") for i in threadpool_info()]
+# ---------------------------------------------------------------------------
+# CPU baseline: the fp32 torch-CPU restatement on the host cores available to this job
+# ---------------------------------------------------------------------------
+def host_threads():
+    """Threads for the CPU leg: the CPUs this process may run on, capped by a cgroup CPU quota."""
+    n_aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
+    threads = n_aff if quota is None else min(n_aff, quota)
+    return threads, {"os_cpu_count": os.cpu_count(), "affinity": n_aff, "cgroup_quota_cpus": quota, "model": model}
+
+
+def cpu_baseline(B, T, H, K, V, cu, seed, tokens_per_run, label, min_seconds=10.0, max_runs=10):
+    """Time oracle/gdn_torch_cpu.py (fp32 chunked restatement, torch-CPU batched matmuls) on the workload's
+    own shape, repeated until min_seconds of CPU work (at most max_runs); rate = tokens_per_run / median."""
+    sys.path.insert(0, ROOT)
+    from oracle import gdn_torch_cpu as TC
+    threads, info = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        N = len(cu) - 1 if cu else B
+        q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, seed, n_states=N, dtype=torch.float32)
+        times = []
+        t_start = time.perf_counter()
+        while not times or (time.perf_counter() - t_start < min_seconds and len(times) < max_runs):
+            t0 = time.perf_counter()
+            TC.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, cu_seqlens=cu)
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
     dt = statistics.median(times)
-    return {"value": T / dt, "unit": "tokens/s", "cores": max(blas) if blas else cores, "kind": "port",
-            "sample": f"numpy oracle (oracle/gdn_oracle.py, bf16 cast points) on the full workload "
-                      f"(T={T}, all {H} heads), {len(times)} runs in {sum(times):.1f} s, median {dt:.2f} s per "
-                      f"forward; host CPU: {model}"}
+    return {"value": tokens_per_run / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/gdn_torch_cpu.py fp32 chunked forward on {label} (all heads), {len(times)} runs in "
+                      f"{sum(times):.1f} s, median {dt:.3f} s per run, torch.set_num_threads({threads}); host: "
+                      f"{info['model']}; os.cpu_count()={info['os_cpu_count']}, affinity={info['affinity']}, "
+                      f"cgroup quota={info['cgroup_quota_cpus']}"}
 
 
+# ---------------------------------------------------------------------------
+# the headline op (configs 1-3, optionally with the in-op L2 norm)
+# ---------------------------------------------------------------------------
+def bench_chunk(args, dev, cfg_id):
+    from kairos_gdn import _lib
+    cfg = CONFIGS[cfg_id]
+    B, T, H, K, V, cu = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], cfg["cu"]
+    N = len(cu) - 1 if cu else B
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, cfg["seed"], n_states=N, device=dev)
+    l2 = int(bool(args.l2norm))
+    if l2:          # the layer hands the op unnormalised q, k (the op normalises them)
+        q = (q.float() * 3.0).to(torch.bfloat16)
+        k = (k.float() * 0.5).to(torch.bfloat16)
+    scale = K ** -0.5
+    lib = _lib.load()
+    n_seqs = N if cu else 0
+    cu_t = torch.tensor(cu, dtype=torch.int64, device=dev) if cu else None
+    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, _lib.BF16, _lib.BF16, l2)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty_like(v)
+    ht = torch.empty(N, H, K, V, dtype=torch.float32, device=dev)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    def step():
+        _lib.call("kairos_gdn_chunk_fwd", P(q), P(k), P(v), P(g), P(beta), None, None, P(h0), P(o), P(ht), P(cu_t),
+                  n_seqs, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, scale, l2, P(ws),
+                  ws_bytes, sp)
+
+    timer = Timer(args)
+    res = timer.run(step)
+    wall = res["wall_s"]
+
+    # per-kernel times: hipEvents recorded by the library on the launch stream around each kernel
+    lib.kairos_gdn_profile_begin()
+    for _ in range(args.steps):
+        step()
+    avg = (ctypes.c_double * len(KERNELS))()
+    ncalls = lib.kairos_gdn_profile_end(avg, len(KERNELS))
+    if ncalls != args.steps:
+        raise RuntimeError(f"kernel timing recorded {ncalls} calls: {lib.kairos_gdn_last_error().decode()}")
+    per = {n: avg[i] for i, n in enumerate(KERNELS)}
+
+    tok_heads = B * T * H
+    alg = alg_bytes(tok_heads, N * H, K, V)
+    flops = tok_heads * flops_per_tok_head(K, V)
+    L = lib.kairos_gdn_segment_chunks(B, T, H, n_seqs)
+    dom = max(KERNELS, key=lambda n: per[n])
+    dom_s = per[dom] / 1e3
+    med_s = res["step_ms"]["median"] / 1e3
+    roof = {"bound": "hbm", "kernel": dom, "achieved": alg / dom_s / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": alg / dom_s / 1e9 / PEAK_HBM_GBS, "alg_bytes": alg,
+            "whole_call": {"achieved": alg / med_s / 1e9, "frac": alg / med_s / 1e9 / PEAK_HBM_GBS},
+            "traffic": None}
+    if cfg_id == 2 and not l2 and cu is None:
+        models = kernel_models(B, T, H, K, V, L)
+        roof["design_bytes"] = models[dom]["bytes"]
+        meas = measured_traffic()
+        if all(n in meas for n in KERNELS):
+            roof["traffic"] = sum(meas[n] for n in KERNELS)
+            roof["traffic_scope"] = "whole call: " + " + ".join(KERNELS)
+            roof["traffic_kernel"] = meas[dom]
+            roof["traffic_over_alg"] = roof["traffic"] / alg
+    name = {1: "BASELINE config 1", 2: "BASELINE config 2", 3: "BASELINE config 3 (varlen)"}[cfg_id]
+    out = {
+        "metric": METRIC if (cfg_id == 2 and not l2) else
+        f"GDN chunk-fwd tokens/s + TFLOP/s at {name}" + (" with use_qk_l2norm_in_kernel=True" if l2 else ""),
+        "value": B * T / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{name}: chunk_gated_delta_rule fwd B={B} T={T} H={H} dk=dv={K} chunk 64, bf16 "
+                               "q/k/v/beta, fp32 g/h0, output_final_state, inputs resident in HBM"
+                               + (f", cu_seqlens={cu}" if cu else "")
+                               + (", use_qk_l2norm_in_kernel=True (unnormalised q, k)" if l2 else ""),
+                   "segments_chunks": L},
+        **timer.fields(res),
+        "tflops": flops / wall / 1e12,
+        "mfma_peak_frac": flops / wall / 1e12 / PEAK_BF16_TFLOPS,
+        "tflops_median_step": flops / med_s / 1e12,
+        "hbm_gbs_whole_op": alg / wall / 1e9,
+        "kernels_ms": per,
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, T, H, K, V, cu, cfg["seed"], B * T, f"the full {name} workload")
+    print(json.dumps(out), flush=True)
+
+
+def bench_streaming(args, dev):
+    """B=8, H=20, dk=dv=128; 21 sequential calls of T=1560 with the fp32 state carried,
+    q/k fp8 e4m3 with per-head scales (amax / 448), v/beta bf16, g fp32.  A step is one 21-frame rollout;
+    per-frame latency from HIP events around each call.  Drift: the streamed end state against one fp32 call
+    over all 21 frames with the unquantised q/k and the rollout's own v, beta, g (this library's fp32 path,
+    itself checked against the oracle by the tests)."""
+    from kairos_gdn import _lib
+    cfg = CONFIGS[4]
+    B, Tf, H, K, V, F = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"], cfg["frames"]
+    frames = []
+    for f in range(F):
+        q, k, v, g, beta, _ = make_inputs(B, Tf, H, K, V, cfg["seed"] * 100 + f, device="cpu", dtype=torch.float32)
+        qc, qs = quantize_fp8(q)
+        kc, ks = quantize_fp8(k)
+        frames.append(dict(q8=qc.to(dev), k8=kc.to(dev), qs=qs.to(dev), ks=ks.to(dev), v=v.to(dev, torch.bfloat16),
+                           g=g.to(dev), beta=beta.to(dev, torch.bfloat16), qf=q, kf=k))
+    h0 = (0.02 * torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(cfg["seed"]))).to(dev)
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, Tf, H, K, V, 0, _lib.F8E4M3, _lib.BF16, 0)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty(B, Tf, H, V, dtype=torch.bfloat16, device=dev)
+    states = [torch.empty(B, H, K, V, dtype=torch.float32, device=dev) for _ in range(2)]
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+    frame_ev = []
+
+    def call(fr, s_in, s_out):
+        _lib.call("kairos_gdn_chunk_fwd", P(fr["q8"]), P(fr["k8"]), P(fr["v"]), P(fr["g"]), P(fr["beta"]),
+                  P(fr["qs"]), P(fr["ks"]), P(s_in), P(o), P(s_out), None, 0, B, Tf, H, K, V, _lib.F8E4M3, _lib.BF16,
+                  _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, P(ws), ws_bytes, sp)
+
+    def step(record=None):
+        s_in = h0
+        for f, fr in enumerate(frames):
+            s_out = states[f % 2]
+            if record is not None:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                call(fr, s_in, s_out)
+                e1.record()
+                record.append((e0, e1))
+            else:
+                call(fr, s_in, s_out)
+            s_in = s_out
+        return s_in
+
+    timer = Timer(args)
+    res = timer.run(step)
+    wall = res["wall_s"]
+    for _ in range(args.steps):
+        step(frame_ev)
+    torch.cuda.synchronize()
+    per_frame = [a.elapsed_time(b) for a, b in frame_ev]
+    end = step().clone()
+    torch.cuda.synchronize()
+
+    # single fp32 call over all frames, unquantised q/k
+    cat = lambda key: torch.cat([fr[key] for fr in frames], dim=1).to(dev).contiguous()  # noqa: E731
+    qf, kf, gf = cat("qf"), cat("kf"), cat("g")
+    vf, bf = cat("v").float(), cat("beta").float()      # the same bf16 values the rollout reads
+    T_all = Tf * F
+    ws32_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T_all, H, K, V, 0, _lib.F32, _lib.F32, 0)
+    ws32 = torch.empty(max(ws32_bytes, 1), dtype=torch.uint8, device=dev)
+    o32 = torch.empty(B, T_all, H, V, dtype=torch.float32, device=dev)
+    ref = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    _lib.call("kairos_gdn_chunk_fwd", P(qf), P(kf), P(vf), P(gf), P(bf), None, None, P(h0), P(o32), P(ref), None, 0,
+              B, T_all, H, K, V, _lib.F32, _lib.F32, _lib.F32, _lib.F32, _lib.F32, K ** -0.5, 0, P(ws32), ws32_bytes,
+              sp)
+    torch.cuda.synchronize()
+    drift = (torch.linalg.vector_norm(end - ref) / torch.linalg.vector_norm(ref)).item()
+    del ws32, o32
+
+    tok_heads = B * Tf * H
+    alg = alg_bytes(tok_heads, B * H, K, V, s_qk=1)
+    flops = tok_heads * flops_per_tok_head(K, V)
+    fs = summary(per_frame)
+    med_s = fs["median"] / 1e3
+    out = {
+        "metric": "GDN chunk-fwd streaming rollout (BASELINE config 4): tokens/s and per-frame latency",
+        "value": B * Tf * F / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": wall * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"BASELINE config 4: {F} sequential chunk_gated_delta_rule calls of B={B} T={Tf} H={H} "
+                               f"dk=dv={K}, fp8 e4m3 q/k with per-head scales, bf16 v/beta, fp32 g, fp32 state "
+                               "carried between calls; a step is one rollout",
+                   "segments_chunks": lib.kairos_gdn_segment_chunks(B, Tf, H, 0)},
+        **timer.fields(res),
+        "frame_ms": fs,
+        "frame_tflops_median": flops / med_s / 1e12,
+        "end_state_drift_rel_l2": drift,
+        "drift_reference": "one fp32 call over all 21 frames (T=32760) with unquantised q/k, same h0",
+        "roofline": {"bound": "hbm", "kernel": "whole call (median frame)", "achieved": alg / med_s / 1e9,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS,
+                     "alg_bytes": alg, "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, Tf, H, K, V, None, cfg["seed"], B * Tf,
+                                           f"one frame of config 4 (B={B}, T={Tf})")
+    print(json.dumps(out), flush=True)
+
+
+# ---------------------------------------------------------------------------
+# other rows of the path (each prints its own line)
+# ---------------------------------------------------------------------------
 def bench_epilogue(args, dev):
     """Gated RMSNorm (fla FusedRMSNormGated, the layer's o_norm) over config 2's output rows:
     algorithmic bytes = rows * V * (2 + 2 + 2) (read o and the gate, write y, bf16)."""
@@ -172,37 +488,30 @@ def bench_epilogue(args, dev):
         _lib.call("kairos_gdn_rms_norm_gated", x.data_ptr(), gate.data_ptr(), w.data_ptr(), None, y.data_ptr(),
                   None, _lib.BF16, _lib.BF16, _lib.F32, rows, V, 1e-5, _lib.ACT_SWISH, sp)
 
-    for _ in range(args.warmup):
-        step()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    timer = Timer(args)
+    res = timer.run(step)
+    ms = res["step_ms"]["median"]
     nbytes = rows * V * 6
     gbs = nbytes / (ms / 1e3) / 1e9
     print(json.dumps({
         "metric": "gated RMSNorm epilogue GB/s at T=32760,H=20,dv=128", "value": gbs, "unit": "GB/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["wall_s"] * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "FusedRMSNormGated(128, eps=1e-5, swish) on o [T*H, 128] bf16, bf16 gate, "
                                "fp32 weight", "rows": rows},
+        **timer.fields(res),
         "roofline": {"bound": "hbm", "kernel": "rmsnorm_gated_kernel", "achieved": gbs, "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "alg_bytes": nbytes, "traffic": None},
     }), flush=True)
 
 
 def bench_model_shape(args, dev):
     """The Kairos 4B layer's own head dims (GatedDeltaNet(hidden_size=2560, num_heads=20) with the
     layer defaults head_dim=256, expand_v=2): B=1, H=20, K=256, V=512 at the headline T, bf16.
-    These dims run the stage kernels (prepare -> fwd_h -> fwd_o) with the reference's
-    intermediates; FLOPs counted as for the headline metric (every MMA tile at full size)."""
+    FLOPs counted as for the headline metric (every MMA tile at full size)."""
     from kairos_gdn import _lib
     B, T, H, K, V = 1, args.T, 20, 256, 512
-    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20270, dev)
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20270, device=dev)
     lib = _lib.load()
     ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -216,24 +525,24 @@ def bench_model_shape(args, dev):
                   B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, P(ws), ws_bytes,
                   sp)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
+    timer = Timer(args)
+    res = timer.run(step)
+    wall = res["wall_s"]
+    med_s = res["step_ms"]["median"] / 1e3
+    alg = alg_bytes(B * T * H, B * H, K, V)
     tflops = B * T * H * flops_per_tok_head(K, V) / wall / 1e12
-    nbytes = B * T * H * (2 * K * 2 + 2 * V * 2 + 4 + 2) + 2 * B * H * K * V * 4
     print(json.dumps({
         "metric": "GDN chunk-fwd tokens/s at the Kairos 4B layer shape T=32760,H=20,dk=256,dv=512", "value": T / wall,
         "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"chunk_gated_delta_rule fwd B={B} T={T} H={H} dk={K} dv={V} chunk 64, bf16 "
-                               "q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM (stage kernels)"},
+                               "q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM", "workspace_bytes": ws_bytes},
+        **timer.fields(res),
         "tflops": tflops, "mfma_peak_frac": tflops / PEAK_BF16_TFLOPS,
-        "hbm_gbs_whole_op": nbytes / wall / 1e9,
+        "hbm_gbs_whole_op": alg / wall / 1e9,
+        "roofline": {"bound": "hbm", "kernel": "whole call (median step)", "achieved": alg / med_s / 1e9,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS,
+                     "alg_bytes": alg, "traffic": None},
     }), flush=True)
 
 
@@ -244,7 +553,7 @@ def bench_recurrent(args, dev):
     token's q, k, v, o, g, beta; the kernel is bound by the two state passes in HBM."""
     from kairos_gdn import _lib
     B, T, H, K, V = 8, 1, 20, 256, 512
-    q, k, v, g, beta, _ = make_inputs(B, T, H, K, V, 20271, dev)
+    q, k, v, g, beta, _ = make_inputs(B, T, H, K, V, 20271, device=dev)
     h0 = (0.02 * torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(1))).to(dev)
     o = torch.empty_like(v)
     ht = torch.empty_like(h0)
@@ -256,26 +565,20 @@ def bench_recurrent(args, dev):
                   None, 0, B, T, H, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.F32, _lib.F32, _lib.BF16, 1, _lib.F32,
                   K ** -0.5, 1, sp)
 
-    for _ in range(args.warmup):
-        step()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    timer = Timer(args)
+    res = timer.run(step)
+    ms = res["step_ms"]["median"]
     nbytes = 2 * B * H * K * V * 4 + B * T * H * (2 * K * 2 + 2 * V * 2 + 4 + 2)
     gbs = nbytes / (ms / 1e3) / 1e9
     print(json.dumps({
         "metric": "GDN fused_recurrent decode step (B=8, T=1, H=20, dk=256, dv=512) GB/s", "value": gbs,
-        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["wall_s"] * 1e3,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": "fused_recurrent_gated_delta_rule fwd, 8 streams x 1 token, H=20 dk=256 dv=512, "
                                "bf16 q/k/v/beta, fp32 g and state, in-kernel q/k L2 norm, state in HBM"},
+        **timer.fields(res),
         "roofline": {"bound": "hbm", "kernel": "fused_recurrent_kernel", "achieved": gbs, "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "alg_bytes": nbytes, "traffic": None},
     }), flush=True)
 
 
@@ -308,27 +611,21 @@ def bench_prologue(args, dev):
         _lib.call("kairos_gdn_gates_fwd", P(a), P(b), P(A_log), P(dt_bias), P(g), P(beta), T, H, _lib.BF16, _lib.BF16,
                   _lib.F32, 0, sp)
 
-    for _ in range(args.warmup):
-        step()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    timer = Timer(args)
+    res = timer.run(step)
+    ms = res["step_ms"]["median"]
     nbytes = sum(x.numel() * 4 + x.shape[1] * W * 2 * 2 for x in xs) + T * H * (2 + 2 + 4 + 2)
     gbs = nbytes / (ms / 1e3) / 1e9
     print(json.dumps({
         "metric": "GDN layer prologue (conv k=4 + SiLU on q/k/v with fused q/k L2 norm, gates) GB/s at "
                   "T=32760, H=20, dk=256, dv=512", "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic",
+        "warmup": args.warmup, "ms_per_step": res["wall_s"] * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "kairos_gdn_causal_conv1d_fwd x3 (q, k: D=5120 with per-head L2 norm; v: D=10240), "
                                "bf16, W=4, caches out, + kairos_gdn_gates_fwd (T x 20)"},
+        **timer.fields(res),
         "roofline": {"bound": "hbm", "kernel": "conv1d_kernel", "achieved": gbs, "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "alg_bytes": nbytes, "traffic": None},
     }), flush=True)
 
 
@@ -337,27 +634,30 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup-seconds", type=float, default=1.5,
+                    help="minimum wall time of the untimed warm-up (clocks reach steady state)")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache (flushed) steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4],
+                    help="BASELINE config to measure (2 = the headline; 4 = the 21-frame fp8 streaming rollout)")
+    ap.add_argument("--l2norm", action="store_true",
+                    help="run the op with use_qk_l2norm_in_kernel=True on unnormalised q, k (configs 1-3)")
     ap.add_argument("--T", type=int, default=32760)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a plain elementwise copy of MIB MiB (fp32 y = x * 1) 5 times and exit: the "
                          "reference kernel of known traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--epilogue", action="store_true",
-                    help="measure only the gated RMSNorm epilogue (kairos_gdn_rms_norm_gated) on o-shaped rows "
-                         "[T*H, V] bf16 with a bf16 gate and fp32 weight; prints its own JSON line")
+                    help="measure only the gated RMSNorm epilogue (kairos_gdn_rms_norm_gated) on o-shaped rows")
     ap.add_argument("--model-shape", action="store_true",
-                    help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T; prints its own "
-                         "JSON line")
+                    help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T")
     ap.add_argument("--recurrent", action="store_true",
-                    help="measure the short-sequence mode's decoding step (kairos_gdn_fused_recurrent_fwd, 8 streams "
-                         "x 1 token at dk=256, dv=512); prints its own JSON line")
+                    help="measure the short-sequence mode's decoding step (8 streams x 1 token at dk=256, dv=512)")
     ap.add_argument("--prologue", action="store_true",
-                    help="measure the layer prologue (causal conv + SiLU + q/k L2 norm, gates) at the model shape; "
-                         "prints its own JSON line")
+                    help="measure the layer prologue (causal conv + SiLU + q/k L2 norm, gates) at the model shape")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only: this build runs the op on a single GPU and has no multi-GPU "
+              f"path (got --gpus {args.gpus})", file=sys.stderr)
         sys.exit(2)
 
     torch.cuda.set_device(0)
@@ -373,99 +673,18 @@ def main():
         return
 
     import kairos_gdn  # noqa: F401
-    from kairos_gdn import _lib
     if args.epilogue:
         bench_epilogue(args, dev)
-        return
-    if args.model_shape:
+    elif args.model_shape:
         bench_model_shape(args, dev)
-        return
-    if args.recurrent:
+    elif args.recurrent:
         bench_recurrent(args, dev)
-        return
-    if args.prologue:
+    elif args.prologue:
         bench_prologue(args, dev)
-        return
-    B, T, H, K, V = 1, args.T, 20, 128, 128
-    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, dev)
-    scale = K ** -0.5
-    lib = _lib.load()
-    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    o = torch.empty_like(v)
-    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
-    P = lambda t: t.data_ptr()  # noqa: E731
-
-    def step():
-        _lib.call("kairos_gdn_chunk_fwd", P(q), P(k), P(v), P(g), P(beta), None, None, P(h0), P(o), P(ht), None, 0,
-                  B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, scale, 0, P(ws), ws_bytes, sp)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
-
-    # ---- per-kernel times: hipEvents recorded by the library on the launch stream
-    lib.kairos_gdn_profile_begin()
-    for _ in range(args.steps):
-        step()
-    avg = (ctypes.c_double * len(KERNELS))()
-    ncalls = lib.kairos_gdn_profile_end(avg, len(KERNELS))
-    if ncalls != args.steps:
-        raise RuntimeError(f"kernel timing recorded {ncalls} calls: {lib.kairos_gdn_last_error().decode()}")
-    per = {n: avg[i] for i, n in enumerate(KERNELS)}
-
-    L = lib.kairos_gdn_segment_chunks(B, T, H, 0)
-    models = kernel_models(B, T, H, K, V, L)
-    dom = max(KERNELS, key=lambda n: per[n])
-    dom_s = per[dom] / 1e3
-    achieved = models[dom]["bytes"] / dom_s / 1e9
-    traffic = measured_traffic(dom)
-    tok = B * T
-    flops = B * T * H * flops_per_tok_head(K, V)
-    tflops = flops / wall / 1e12
-    nc = (T + C - 1) // C
-    out = {
-        "metric": METRIC,
-        "value": tok / wall,
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": wall * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {"workload": f"BASELINE config 2: chunk_gated_delta_rule fwd B={B} T={T} H={H} dk=dv={K} "
-                               "chunk 64, bf16 q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM",
-                   "segments_per_sequence": (nc + L - 1) // L, "chunks_per_segment": L},
-        "tflops": tflops,
-        "mfma_peak_frac": tflops / PEAK_BF16_TFLOPS,
-        "hbm_gbs_whole_op": (B * T * H * (2 * K * 2 + 2 * V * 2 + 4 + 2) + 2 * B * H * K * V * 4) / wall / 1e9,
-        "kernels_ms": per,
-        "kernels_tflops": {n: models[n]["flops"] / (per[n] / 1e3) / 1e12 if per[n] > 0 else 0.0 for n in KERNELS},
-        "kernels_gbs": {n: models[n]["bytes"] / (per[n] / 1e3) / 1e9 if per[n] > 0 else 0.0 for n in KERNELS},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom,
-            "achieved": achieved,
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": achieved / PEAK_HBM_GBS,
-            "traffic": traffic,
-        },
-    }
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(T, H, K, V, 20262)
-    print(json.dumps(out), flush=True)
+    elif args.config == 4:
+        bench_streaming(args, dev)
+    else:
+        bench_chunk(args, dev, args.config)
 
 
 if __name__ == "__main__":

@@ -61,23 +61,26 @@ _validated_cu: tuple | None = None
 
 
 def _prepare_cu_seqlens(cu_seqlens: torch.Tensor, device: torch.device, T: int) -> torch.Tensor:
-    """int64 device copy of cu_seqlens, checked once per tensor object.
+    """int64 device copy of cu_seqlens, checked once per tensor object and version.
 
     The reference reads cu_seqlens on the host as well (prepare_chunk_indices
     calls .tolist(), fla/ops/utils/index.py:118, cached by identity in
-    fla/utils.py:96-133); the same single check here guards the kernels
-    against offsets outside [0, T].
+    fla/utils.py:96-133); the same check here guards the kernels against
+    offsets outside [0, T].  The cache key includes the tensor's version
+    counter, so an in-place edit of a reused buffer is checked again.
     """
     global _validated_cu
     cu = cu_seqlens
     if cu.dim() != 1 or cu.numel() < 2:
         raise ValueError("cu_seqlens must be a 1-D tensor with at least two entries")
-    if _validated_cu is None or _validated_cu[0] is not cu_seqlens or _validated_cu[1] != T:
+    key = (cu_seqlens, cu_seqlens._version, T)
+    if (_validated_cu is None or _validated_cu[0] is not key[0] or _validated_cu[1] != key[1]
+            or _validated_cu[2] != key[2]):
         vals = cu.detach().to("cpu", torch.int64)
         if int(vals[0]) != 0 or int(vals[-1]) != T or bool((vals[1:] < vals[:-1]).any()):
             raise ValueError(
                 f"cu_seqlens must start at 0, end at T={T} and be non-decreasing (got {vals.tolist()[:8]}...)")
-        _validated_cu = (cu_seqlens, T)
+        _validated_cu = key
     return cu.to(device=device, dtype=torch.int64).contiguous()
 
 

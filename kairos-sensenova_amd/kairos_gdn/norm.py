@@ -100,14 +100,11 @@ class FusedRMSNormGated(nn.Module):
         if self.elementwise_affine:
             nn.init.ones_(self.weight)
 
-    def __repr__(self) -> str:
-        s = f"{self.__class__.__name__}({self.hidden_size}"
+    def extra_repr(self) -> str:
+        parts = [str(self.hidden_size), f"eps={self.eps}", f"activation={self.activation!r}"]
         if not self.elementwise_affine:
-            s += f", elementwise_affine={self.elementwise_affine}"
-        s += f", eps={self.eps}"
-        s += f", activation={self.activation}"
-        s += ")"
-        return s
+            parts.insert(1, "elementwise_affine=False")
+        return ", ".join(parts)
 
     def forward(self, x: torch.Tensor, g: torch.Tensor, residual: torch.Tensor | None = None, prenorm: bool = False,
                 residual_in_fp32: bool = False, tp_group=None) -> torch.Tensor:

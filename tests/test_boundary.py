@@ -145,6 +145,21 @@ def test_varlen_initial_state_count():
         kairos_gdn.chunk_gated_delta_rule(q, k, v, g, b, initial_state=h0, cu_seqlens=torch.tensor([0, 8, 16]))
 
 
+def test_cu_seqlens_checked_again_after_in_place_edit():
+    """The host check of cu_seqlens is cached per tensor and version: editing a reused buffer in place
+    (cu[1] beyond T) is caught again instead of reaching the kernels."""
+    from kairos_gdn import chunk as ch
+    cu = torch.tensor([0, 8, 16])
+    assert ch._prepare_cu_seqlens(cu, torch.device("cpu"), 16).tolist() == [0, 8, 16]
+    ch._prepare_cu_seqlens(cu, torch.device("cpu"), 16)          # cached: same object, same version
+    cu[1] = 40
+    with pytest.raises(ValueError, match="non-decreasing"):
+        ch._prepare_cu_seqlens(cu, torch.device("cpu"), 16)
+    cu[1] = 8
+    with pytest.raises(ValueError, match="end at T=20"):
+        ch._prepare_cu_seqlens(cu, torch.device("cpu"), 20)
+
+
 def test_head_first_warns_and_cpu_tensors_are_refused():
     q, k, v, g, b = cpu_inputs()
     with warnings.catch_warnings(record=True) as rec:

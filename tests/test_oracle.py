@@ -334,3 +334,25 @@ def test_fp8_e4m3_codes():
     np.testing.assert_array_equal(O.fp8_e4m3_quantize(vals[finite]), codes[finite])
     # ties go to the even code: halfway between 1.0 (0x38) and 1.125 (0x39)
     assert O.fp8_e4m3_quantize(np.array([1.0625]))[0] == 0x38
+
+
+# ---------------------------------------------------------------------------
+# the fp32 torch-CPU restatement timed as bench.py's CPU baseline
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,T,H,K,V,cu", [(2, 130, 3, 32, 48, None), (1, 150, 2, 64, 64, [0, 70, 71, 71, 150])])
+def test_torch_cpu_restatement(B, T, H, K, V, cu):
+    """oracle/gdn_torch_cpu.py: float64 == the fp64 token recurrence; float32 == the numpy fp32 oracle."""
+    import torch
+    from oracle import gdn_torch_cpu as TC
+    x = rand_case(B, T, H, K, V, seed=41, cu=cu)
+    t = lambda a, dt: torch.from_numpy(np.asarray(a)).to(dt)  # noqa: E731
+    on, hn = O.naive_recurrent(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["h0"], cu_seqlens=cu)
+    args64 = [t(x[n], torch.float64) for n in ("q", "k", "v", "g", "beta")]
+    o64, h64 = TC.chunk_gated_delta_rule(*args64, initial_state=t(x["h0"], torch.float64), cu_seqlens=cu)
+    assert O.rel_l2(o64.numpy(), on) < 1e-10 and O.rel_l2(h64.numpy(), hn) < 1e-10
+    args32 = [t(x[n], torch.float32) for n in ("q", "k", "v", "g", "beta")]
+    o32, h32 = TC.chunk_gated_delta_rule(*args32, initial_state=t(x["h0"], torch.float32), cu_seqlens=cu)
+    f32 = lambda a: np.asarray(a, np.float32)  # noqa: E731
+    oo, ho = O.chunk_gated_delta_rule(*(f32(x[n]) for n in ("q", "k", "v", "g", "beta")),
+                                      initial_state=f32(x["h0"]), output_final_state=True, cu_seqlens=cu, dtype="fp32")
+    assert O.rel_l2(o32.numpy(), oo) < 1e-5 and O.rel_l2(h32.numpy(), ho) < 1e-5
