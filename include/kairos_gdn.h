@@ -82,6 +82,26 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
                          int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* kairos_gdn_chunk_fwd without a workspace argument: the call allocates
+ * nothing (no hipMalloc / hipFree, no allocating library routine) and takes
+ * its scratch memory from a static device array inside the library, of
+ * kairos_gdn_chunk_fwd_noalloc_max_bytes() bytes (256 MiB) on every GPU the
+ * library runs on, held until the process ends.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  A problem
+ * whose kairos_gdn_chunk_fwd_workspace_size() exceeds the array is rejected
+ * with KAIROS_GDN_EWORKSPACE.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (concurrent streams or threads) race and must
+ * be serialised by the caller.  Same results as kairos_gdn_chunk_fwd (same
+ * kernels); calls made through it are not recorded by the timing hook. */
+int kairos_gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                 const float* q_scale, const float* k_scale, const void* initial_state, void* o,
+                                 float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                 int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype,
+                                 int g_dtype, int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm,
+                                 void* stream);
+size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void);
+
 /* Chunks per segment that kairos_gdn_chunk_fwd uses for this problem (the
  * segment plan: sequences are cut into segments of this many 64-token chunks
  * so that (segment, head) work items fill the GPU; the environment variable

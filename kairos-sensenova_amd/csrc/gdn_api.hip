@@ -285,6 +285,43 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Static scratch of kairos_gdn_chunk_fwd_noalloc: a file-scope device array,
+// one copy per GPU the library's code object is loaded on, held until the
+// process ends.  Host code never uses the array's name as an address (on the
+// host it is only a handle): the device address is looked up once per device
+// with hipGetSymbolAddress and kept in g_scratch_ptr.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(256) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch array (looked up on the first call per device).
+int scratch_address(void** out, const char* what) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return fail(KAIROS_GDN_EHIP, "%s: hipGetDevice failed: %s", what, hipGetErrorString(hipGetLastError()));
+  if (dev < 0 || dev >= kMaxDevices) return fail(KAIROS_GDN_EINVAL, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || p == nullptr)
+      return fail(KAIROS_GDN_EHIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                  hipGetErrorString(rc));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KAIROS_GDN_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int kairos_gdn_abi_version(void) { return KAIROS_GDN_ABI_VERSION; }
@@ -306,13 +343,14 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   return total;
 }
 
-int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
-                         const float* q_scale, const float* k_scale, const void* initial_state, void* o,
-                         float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T,
-                         int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype, int g_dtype, int beta_dtype,
-                         int h0_dtype, float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
-                         void* stream) {
-  const char* what = "kairos_gdn_chunk_fwd";
+// Body of kairos_gdn_chunk_fwd and kairos_gdn_chunk_fwd_noalloc: validation, workspace carving and the
+// launches.  Allocates nothing; `profile` lets the call take part in kernel timing (which creates events).
+static int chunk_fwd_impl(const char* what, bool profile, const void* q, const void* k, const void* v,
+                          const void* g, const void* beta, const float* q_scale, const float* k_scale,
+                          const void* initial_state, void* o, float* final_state, const int64_t* cu_seqlens,
+                          int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
+                          int v_dtype, int g_dtype, int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm,
+                          void* workspace, size_t workspace_bytes, void* stream) {
   Geometry G;
   if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
   const int cdt = compute_dtype(qk_dtype, v_dtype);
@@ -397,9 +435,43 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
   a.Ai = Ai; a.nc_grid = nc_grid;
   a.run_trans = P.trans && P.ns > 0;
   a.run_combine = P.combine;
-  a.events = profile_events();
+  a.events = profile ? profile_events() : nullptr;
   if (int rc = from_launch(kgdn::launch_seg_fwd(a, cdt, qk_dtype, (int)K, (int)V, s), "segment forward")) return rc;
   return ok();
+}
+
+int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const float* q_scale, const float* k_scale, const void* initial_state, void* o,
+                         float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T,
+                         int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype, int g_dtype, int beta_dtype,
+                         int h0_dtype, float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  return chunk_fwd_impl("kairos_gdn_chunk_fwd", true, q, k, v, g, beta, q_scale, k_scale, initial_state, o,
+                        final_state, cu_seqlens, n_seqs, B, T, H, K, V, qk_dtype, v_dtype, g_dtype, beta_dtype,
+                        h0_dtype, scale, use_qk_l2norm, workspace, workspace_bytes, stream);
+}
+
+size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int kairos_gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                 const float* q_scale, const float* k_scale, const void* initial_state, void* o,
+                                 float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                 int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype,
+                                 int g_dtype, int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm,
+                                 void* stream) {
+  const char* what = "kairos_gdn_chunk_fwd_noalloc";
+  const size_t need = kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, qk_dtype, v_dtype, use_qk_l2norm);
+  if (need > kScratchBytes)
+    return fail(KAIROS_GDN_EWORKSPACE,
+                "%s: this problem needs %zu bytes of scratch, more than the library's static %zu-byte array; "
+                "call kairos_gdn_chunk_fwd with a workspace instead", what, need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_address(&ws, what)) return rc;
+  }
+  return chunk_fwd_impl(what, false, q, k, v, g, beta, q_scale, k_scale, initial_state, o, final_state, cu_seqlens,
+                        n_seqs, B, T, H, K, V, qk_dtype, v_dtype, g_dtype, beta_dtype, h0_dtype, scale,
+                        use_qk_l2norm, ws, kScratchBytes, stream);
 }
 
 int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs) {
