@@ -53,7 +53,7 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 C = 64
 RECORD = C * C * 2 + 8 * C * 4      # bytes of one (chunk, head) record written by seg_prep
 KERNELS = ["seg_prep_kernel", "seg_trans_kernel", "seg_combine_kernel", "seg_out_kernel"]
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2_hbm_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2.md")
 FLUSH_BYTES = 640 << 20
 
 # BASELINE.json configs measured here (config 0 is the CPU plumbing case, a parity test only)
