@@ -108,6 +108,28 @@ size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void);
  * KAIROS_GDN_SEG_CHUNKS overrides it).  No counterpart in the reference. */
 int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs);
 
+/* ---- backward ---------------------------------------------------------------
+ * Gradients of the forward above: replaces ChunkGatedDeltaRuleFunction.backward
+ * (chunk.py:188-213: chunk_gated_delta_rule_bwd, chunk.py:70-146, then the
+ * l2norm backward of q and k when use_qk_l2norm).  Takes the forward's own
+ * inputs (q, k as given to the forward, i.e. before the in-op L2 norm) and
+ * recomputes what the reference saves (the normalised q, k, gc and Ai) and
+ * what it recomputes (w, u, the state snapshots h and v_new, chunk.py:84-101).
+ * do [B, T, H, V] in v's dtype; dht [N, H, K, V] fp32 or NULL (zero).
+ * Outputs: dq, dk [B, T, H, K] in q's dtype; dv [B, T, H, V] in v's dtype;
+ * dg [B, T, H] fp32; dbeta [B, T, H] in beta's dtype; dh0 [N, H, K, V] fp32, or
+ * NULL (must be NULL when initial_state is).  bf16 or fp32 q/k/v (fp8 is
+ * forward-only); K in {64, 128, 256}, V a multiple of 64 (at most 512 in bf16;
+ * K, V at most 128 in fp32).  Workspace: kairos_gdn_chunk_bwd_workspace_size(). */
+size_t kairos_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                           int64_t n_seqs, int qk_dtype, int v_dtype, int use_qk_l2norm);
+int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const void* initial_state, const void* do_, const float* dht, void* dq, void* dk, void* dv,
+                         float* dg, void* dbeta, float* dh0, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                         int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype, int g_dtype,
+                         int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ---- kernel timing (measurement hook, no counterpart in the reference) ----
  * kairos_gdn_profile_begin() makes every following kairos_gdn_chunk_fwd call
  * of the fused path record hipEvents on its stream around its four kernels

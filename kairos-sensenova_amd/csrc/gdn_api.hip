@@ -240,6 +240,24 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
   return total;
 }
 
+// Workspace of the backward: the recomputed forward (gc, w, u, Ai, h, v_new) and the
+// backward's own intermediates (dv_local, dh, dv2, -dw, dk of the dq/dk stage, dg before the
+// cumsum), plus the normalised q, k and their pre-norm gradients with the in-op L2 norm.
+size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, int use_l2) {
+  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
+  const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
+  const size_t tok = (size_t)(B * T * H);
+  size_t total = stage_ws(n_seqs);
+  total += 2 * align_up(tok * sizeof(float));            // gc, dg1
+  total += 3 * align_up(tok * K * es);                   // w, -dw, dk1
+  total += align_up(nc * H * V * kgdn::C * es);          // uT
+  total += align_up(tok * kgdn::C * es);                 // Ai
+  total += 2 * align_up(nc * H * K * V * es);            // h, dh
+  total += 3 * align_up(tok * V * es);                   // v_new, dv_local, dv2
+  if (use_l2) total += 4 * align_up(tok * K * es);       // qn, kn, dqn, dkn
+  return total;
+}
+
 // Staged forward: prepare (gc, w, u) -> fwd_h (h, v_new, ht) -> fwd_o (o), the
 // reference's stage order with its intermediates in the workspace.  Used for the
 // shapes the fused kernels do not cover: fp32, and the Kairos model's head dims
@@ -472,6 +490,113 @@ int kairos_gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, co
   return chunk_fwd_impl(what, false, q, k, v, g, beta, q_scale, k_scale, initial_state, o, final_state, cu_seqlens,
                         n_seqs, B, T, H, K, V, qk_dtype, v_dtype, g_dtype, beta_dtype, h0_dtype, scale,
                         use_qk_l2norm, ws, kScratchBytes, stream);
+}
+
+size_t kairos_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs,
+                                           int qk_dtype, int v_dtype, int use_qk_l2norm) {
+  if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0) return 0;
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  if (cdt < 0) return 0;
+  return bwd_ws(B, T, H, K, V, n_seqs, cdt, use_qk_l2norm);
+}
+
+int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const void* initial_state, const void* do_, const float* dht, void* dq, void* dk, void* dv,
+                         float* dg, void* dbeta, float* dh0, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                         int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype, int g_dtype,
+                         int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_chunk_bwd";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  if (qk_dtype == KAIROS_GDN_F8E4M3)
+    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: the backward pass takes bf16 or fp32 q/k (not fp8)", what);
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix q/k=%d v=%d", what, qk_dtype, v_dtype);
+  if (!valid_scalar_dt(g_dtype) || !valid_scalar_dt(beta_dtype) || (initial_state && !valid_scalar_dt(h0_dtype)))
+    return fail(KAIROS_GDN_EINVAL, "%s: g, beta and initial_state must be fp32 or bf16", what);
+  if (!kgdn::bwd_supported(cdt, (int)K, (int)V))
+    return fail(KAIROS_GDN_EUNSUPPORTED,
+                "%s: head dims K=%lld V=%lld are not built for the backward (K in {64, 128, 256}, V a multiple of "
+                "64: at most 512 in bf16, K and V at most 128 in fp32)", what, (long long)K, (long long)V);
+  if (!std::isfinite(scale)) return fail(KAIROS_GDN_EINVAL, "%s: scale must be finite", what);
+  const bool any_tokens = G.B * G.T > 0;
+  if (any_tokens && (!q || !k || !v || !g || !beta || !do_ || !dq || !dk || !dv || !dg || !dbeta))
+    return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  if (initial_state == nullptr && dh0 != nullptr)
+    return fail(KAIROS_GDN_EINVAL, "%s: dh0 needs the initial_state it is the gradient of", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(do_) || !aligned16(dq) || !aligned16(dk) ||
+      !aligned16(dv))
+    return fail(KAIROS_GDN_EINVAL, "%s: q, k, v, do, dq, dk and dv must be 16-byte aligned", what);
+  const size_t need = bwd_ws(B, T, H, K, V, n_seqs, cdt, use_qk_l2norm);
+  if (workspace_bytes < need)
+    return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace of %zu bytes is smaller than the %zu required", what,
+                workspace_bytes, need);
+  if (need && !aligned16(workspace)) return fail(KAIROS_GDN_EINVAL, "%s: workspace must be 16-byte aligned", what);
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
+  const size_t tok = (size_t)(B * T * H);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
+  float* dg1 = static_cast<float*>(cv.take(tok * sizeof(float)));
+  void* w = cv.take(tok * K * es);
+  void* dwb = cv.take(tok * K * es);
+  void* dk1 = cv.take(tok * K * es);
+  void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  void* Ai = cv.take(tok * kgdn::C * es);
+  void* hs = cv.take((size_t)G.nc * H * K * V * es);
+  void* dhs = cv.take((size_t)G.nc * H * K * V * es);
+  void* vn = cv.take(tok * V * es);
+  void* dvl = cv.take(tok * V * es);
+  void* dv2 = cv.take(tok * V * es);
+  const void* qx = q;
+  const void* kx = k;
+  void* dq_k = dq;
+  void* dk_k = dk;
+  if (use_qk_l2norm) {
+    void* qn = cv.take(tok * K * es);
+    void* kn = cv.take(tok * K * es);
+    dq_k = cv.take(tok * K * es);
+    dk_k = cv.take(tok * K * es);
+    if (any_tokens) {
+      if (int rc = from_launch(kgdn::launch_l2norm(q, qn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q)")) return rc;
+      if (int rc = from_launch(kgdn::launch_l2norm(k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(k)")) return rc;
+    }
+    qx = qn;
+    kx = kn;
+  }
+  const int N = (int)G.N;
+  if (G.nc > 0 && any_tokens) {
+    kgdn::PrepareArgs pa{};
+    pa.k = kx; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = nullptr;
+    pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
+    pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = T; pa.H = (int)H;
+    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = Ai;
+    if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "prepare")) return rc;
+    kgdn::FwdHArgs ha{};
+    ha.k = kx; ha.k_scale = nullptr; ha.w = w; ha.uT = uT; ha.gc = gc;
+    ha.h0 = initial_state; ha.h0_dtype = h0_dtype;
+    ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = N; ha.T = T; ha.H = (int)H;
+    ha.hT = hs; ha.vnT = vn; ha.ht = nullptr; ha.row_major = true;
+    if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h (recompute)")) return rc;
+  }
+  kgdn::BwdArgs ba{};
+  ba.q = qx; ba.k = kx; ba.v = v; ba.gc = gc; ba.beta = beta; ba.beta_dtype = beta_dtype;
+  ba.do_ = do_; ba.dht = dht; ba.w = w; ba.Ai = Ai; ba.h = hs; ba.vn = vn;
+  ba.dvl = dvl; ba.dh = dhs; ba.dv2 = dv2; ba.dw = dwb; ba.dk1 = dk1; ba.dg1 = dg1;
+  ba.dq = dq_k; ba.dk = dk_k; ba.dv = dv; ba.dg = dg; ba.db = dbeta; ba.dh0 = dh0;
+  ba.cu = cu_seqlens; ba.chunk_off = chunk_off; ba.N = N; ba.T = T; ba.H = (int)H; ba.scale = scale;
+  if (int rc = from_launch(kgdn::launch_bwd(ba, cdt, (int)K, (int)V, any_tokens ? G.nc : 0, s), what)) return rc;
+  if (use_qk_l2norm && any_tokens) {
+    if (int rc = from_launch(kgdn::launch_l2norm_bwd(q, dq_k, dq, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(q)"))
+      return rc;
+    if (int rc = from_launch(kgdn::launch_l2norm_bwd(k, dk_k, dk, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(k)"))
+      return rc;
+  }
+  return ok();
 }
 
 int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs) {

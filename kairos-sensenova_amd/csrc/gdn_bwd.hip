@@ -1,0 +1,924 @@
+// Backward pass of the chunked GatedDeltaNet (fla ops/gated_delta_rule/chunk.py:70-146),
+// after the forward has been recomputed by the stage kernels (prepare: gc, w, u, Ai;
+// fwd_h with row-major outputs: h [NC, H, K, V] and v_new [B*T, H, V]):
+//
+//   bwd_dvl_kernel    dv_local = mask_{j<=i}(scale k_j.q_i e^{g_i-g_j}) @ do   chunk_o.py:413-468
+//   bwd_dhu_kernel    reverse state recurrence of dh, dv2 = gate (k @ dh) + dv_local, dh0
+//                                                                          chunk_delta_h.py:250-438
+//   bwd_dqkwg_kernel  dq, dk (state and intra-chunk terms), -dw, dg        chunk_o.py:147-326
+//   bwd_wy_kernel     WY backward (dk2, dv, dbeta, dg2), dk = dk + dk2 and
+//                     the reverse chunk cumsum of dg                        wy_fast.py:98-210,
+//                                                                          chunk.py:140-145
+//   l2norm_bwd_kernel dx = dy rstd - sum(dy y) y rstd                      l2norm.py:132-154
+//
+// MFMA operands follow one convention in every kernel: the K index of a 32-deep
+// step is taken in "accumulator order" (rows 4 lg .. 4 lg + 3 and 16 + 4 lg ..
+// of the step for lane group lg) whenever one operand is a transposed read or an
+// accumulator tile; row-major tiles read in that order use two 8-byte reads.
+// Tiles in LDS have 64 rows (the chunk's tokens); bf16 tiles are stored as
+// [64][64] column blocks swizzled by swz_off<64>, so 16-byte row reads, 8-byte
+// accumulator-order reads and ds_read_b64_tr_b16 transposed reads (contractions
+// over the token axis) are bank-conflict free; fp32 tiles are padded rows read
+// transposed element by element.
+#include "gdn_common.hpp"
+#include "gdn_kernels.h"
+
+namespace kgdn {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// LDS tiles of 64 rows x ncol columns
+// ---------------------------------------------------------------------------
+template <typename TC>
+__host__ __device__ constexpr int tile_elems(int ncol) {
+  return sizeof(TC) == 2 ? 64 * ncol : 64 * (ncol + 4);
+}
+
+template <typename TC>
+__device__ __forceinline__ int toff(int r, int c, int ncol) {
+  if constexpr (sizeof(TC) == 2) {
+    return (c >> 6) * 4096 + swz_off<64>(r, (c & 63) >> 3) + (c & 7);
+  } else {
+    return r * (ncol + 4) + c;
+  }
+}
+
+// natural K order: M/N index = row r0 + l % 16, K index = k0 + 8 (l / 16) + e
+template <typename TC>
+__device__ __forceinline__ Frag<TC> t_nat(const TC* t, int ncol, int r0, int k0) {
+  const int l = lane_id();
+  const TC* p = t + toff<TC>(r0 + (l & 15), k0 + 8 * (l >> 4), ncol);
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    f.v = *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    f.lo = *reinterpret_cast<const f32x4*>(p);
+    f.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return f;
+}
+
+// accumulator K order: M/N index = row r0 + l % 16, K index = k0 + 4 lg + e and k0 + 16 + 4 lg + e
+template <typename TC>
+__device__ __forceinline__ Frag<TC> t_acc(const TC* t, int ncol, int r0, int k0) {
+  const int l = lane_id();
+  const int r = r0 + (l & 15), lg = l >> 4;
+  const TC* p0 = t + toff<TC>(r, k0 + 4 * lg, ncol);
+  const TC* p1 = t + toff<TC>(r, k0 + 16 + 4 * lg, ncol);
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    const bf16x4 a = *reinterpret_cast<const bf16x4*>(p0);
+    const bf16x4 b = *reinterpret_cast<const bf16x4*>(p1);
+    f.v = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    f.lo = *reinterpret_cast<const f32x4*>(p0);
+    f.hi = *reinterpret_cast<const f32x4*>(p1);
+  }
+  return f;
+}
+
+// transposed: M/N index = column c0 + l % 16, K index = row k0 + (accumulator order), k0 a multiple of 32
+template <typename TC>
+__device__ __forceinline__ Frag<TC> t_tr(const TC* t, int ncol, int k0, int c0) {
+  if constexpr (sizeof(TC) == 2) {
+    return tr_frag<64>(t + (c0 >> 6) * 4096, k0 >> 5, c0 & 63);
+  } else {
+    const int l = lane_id();
+    const int c = c0 + (l & 15), lg = l >> 4;
+    Frag<float> f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f.lo[e] = t[toff<float>(k0 + 4 * lg + e, c, ncol)];
+      f.hi[e] = t[toff<float>(k0 + 16 + 4 * lg + e, c, ncol)];
+    }
+    return f;
+  }
+}
+
+// the row of K index e of an accumulator-order fragment (relative to k0), for per-row operand scaling
+__device__ __forceinline__ int acc_row(int e) { return 4 * (lane_id() >> 4) + (e & 3) + (e >> 2) * 16; }
+
+// 4 consecutive elements (c % 4 == 0) of a tile row as floats
+template <typename TC>
+__device__ __forceinline__ f32x4 t_row4(const TC* t, int ncol, int r, int c) {
+  const TC* p = t + toff<TC>(r, c, ncol);
+  if constexpr (sizeof(TC) == 2) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  } else {
+    return *reinterpret_cast<const f32x4*>(p);
+  }
+}
+
+// fragment element access and scaling with rounding to the operand type
+template <typename TC> __device__ __forceinline__ float fget(const Frag<TC>& f, int e);
+template <> __device__ __forceinline__ float fget<bf16>(const Frag<bf16>& f, int e) { return (float)f.v[e]; }
+template <> __device__ __forceinline__ float fget<float>(const Frag<float>& f, int e) { return e < 4 ? f.lo[e] : f.hi[e - 4]; }
+template <typename TC> __device__ __forceinline__ void fset(Frag<TC>& f, int e, float x);
+template <> __device__ __forceinline__ void fset<bf16>(Frag<bf16>& f, int e, float x) { f.v[e] = (bf16)x; }
+template <> __device__ __forceinline__ void fset<float>(Frag<float>& f, int e, float x) {
+  if (e < 4) f.lo[e] = x; else f.hi[e - 4] = x;
+}
+template <typename TC>
+__device__ __forceinline__ Frag<TC> fscale(Frag<TC> f, float s) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) fset<TC>(f, e, fget<TC>(f, e) * s);
+  return f;
+}
+template <typename TC>
+__device__ __forceinline__ Frag<TC> fzero() {
+  Frag<TC> f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) fset<TC>(f, e, 0.f);
+  return f;
+}
+
+// natural fragment of a row-major tensor in global memory (p = the lane's row start), or zeros
+template <typename TC>
+__device__ __forceinline__ Frag<TC> g_nat(const TC* row, int k0, bool valid) {
+  if (!valid) return fzero<TC>();
+  const TC* p = row + k0 + 8 * (lane_id() >> 4);
+  Frag<TC> f;
+  if constexpr (sizeof(TC) == 2) {
+    f.v = *reinterpret_cast<const bf16x8*>(p);
+  } else {
+    f.lo = *reinterpret_cast<const f32x4*>(p);
+    f.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  return f;
+}
+
+// fragment built from two accumulator tiles (rows 0-15 and 16-31 of a 32-deep K step)
+template <typename TC>
+__device__ __forceinline__ Frag<TC> acc_frag(const f32x4& a, const f32x4& b) {
+  Frag<TC> f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    fset<TC>(f, e, a[e]);
+    fset<TC>(f, e + 4, b[e]);
+  }
+  return f;
+}
+
+// stage 64 token rows [t0, t0 + nv) of a row-major [*, H, ncol] tensor into a tile (zeros past nv)
+template <typename TC>
+__device__ __forceinline__ void stage_rows(TC* tile, const TC* src, int64_t t0, int nv, int H, int h, int ncol) {
+  const int per_row = ncol / 8;
+  for (int idx = threadIdx.x; idx < 64 * per_row; idx += blockDim.x) {
+    const int r = idx / per_row, c8 = (idx % per_row) * 8;
+    Vec8<TC> x = vzero<TC>();
+    if (r < nv) x = ld8<TC>(src + ((t0 + r) * H + h) * (int64_t)ncol + c8);
+    st8<TC>(tile + toff<TC>(r, c8, ncol), x);
+  }
+}
+
+// sum over the 16 lanes of a row group (l % 16) or over the 4 lane groups (l / 16)
+__device__ __forceinline__ float sum16(float x) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, WAVE);
+  return x;
+}
+__device__ __forceinline__ float sum_lg(float x) {
+  x += __shfl_xor(x, 16, WAVE);
+  x += __shfl_xor(x, 32, WAVE);
+  return x;
+}
+__device__ __forceinline__ float sum64(float x) {
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) x += __shfl_xor(x, o, WAVE);
+  return x;
+}
+
+template <typename TC>
+__device__ __forceinline__ void st4v(TC* p, const f32x4& v) { st4<TC>(p, v[0], v[1], v[2], v[3]); }
+
+template <typename TC>
+__device__ __forceinline__ f32x4 g_row4(const TC* p) { return ld4<TC>(p); }
+
+constexpr int NT_B = 256;   // threads of the chunk-parallel backward kernels (4 waves, one per 16 tokens)
+
+// ---------------------------------------------------------------------------
+// dv_local (chunk_o.py:413-468): dv_local[j] = sum_{i >= j} scale (q_i.k_j) e^{g_i - g_j} do_i
+// ---------------------------------------------------------------------------
+template <typename TC>
+__host__ __device__ constexpr size_t dvl_lds(int K, int V) {
+  return sizeof(TC) * (2 * (size_t)tile_elems<TC>(K) + tile_elems<TC>(V) + tile_elems<TC>(64)) + 64 * sizeof(float);
+}
+
+template <typename TC, int K>
+__global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  TC* s_q = reinterpret_cast<TC*>(smem);
+  TC* s_k = s_q + tile_elems<TC>(K);
+  TC* s_do = s_k + tile_elems<TC>(K);
+  TC* s_M = s_do + tile_elems<TC>(V);
+  float* s_g = reinterpret_cast<float*>(s_M + tile_elems<TC>(64));
+  const int h = blockIdx.y, H = a.H;
+  const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
+  if (!loc.ok) return;
+  const int64_t t0 = loc.t0;
+  const int nv = loc.nv;
+  const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  stage_rows<TC>(s_q, reinterpret_cast<const TC*>(a.q), t0, nv, H, h, K);
+  stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+  stage_rows<TC>(s_do, reinterpret_cast<const TC*>(a.do_), t0, nv, H, h, V);
+  if (threadIdx.x < 64) s_g[threadIdx.x] = threadIdx.x < nv ? a.gc[(t0 + threadIdx.x) * H + h] : 0.f;
+  __syncthreads();
+
+  // M^T[j][i], j <= i, rounded to the storage type (the reference's b_A.to(do.dtype))
+  for (int tile = wid; tile < 16; tile += NT_B / WAVE) {
+    const int tj = tile >> 2, ti = tile & 3;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (tj <= ti) {
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks) mma(acc, t_nat<TC>(s_k, K, 16 * tj, 32 * ks), t_nat<TC>(s_q, K, 16 * ti, 32 * ks));
+    }
+    const int i = 16 * ti + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 16 * tj + 4 * lg + jj;
+      const float val = (j <= i && i < nv) ? acc[jj] * a.scale * gexp(s_g[i] - s_g[j]) : 0.f;
+      s_M[toff<TC>(j, i, 64)] = from_f32<TC>(val);
+    }
+  }
+  __syncthreads();
+
+  // dv_local^T[v][j] = sum_i do[i][v] M^T[j][i]
+  TC* out = reinterpret_cast<TC*>(a.dvl);
+  for (int tile = wid; tile < (V / 16) * 4; tile += NT_B / WAVE) {
+    const int tv = tile >> 2, tj = tile & 3;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) mma(acc, t_tr<TC>(s_do, V, 32 * ks, 16 * tv), t_acc<TC>(s_M, 64, 16 * tj, 32 * ks));
+    const int j = 16 * tj + lc;
+    if (j < nv) st4v<TC>(out + ((t0 + j) * H + h) * (int64_t)V + 16 * tv + 4 * lg, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dh recurrence (chunk_delta_h.py:250-438).  One workgroup per (sequence, head,
+// 16 value columns), NW waves splitting the K rows of the state gradient dh
+// [K x 16] (fp32, accumulator layout, in VGPRs).  Per chunk, last to first:
+//   dh[c] = dh (stored, rounded)
+//   dv2   = (k @ bf16(dh)) e^{g_last - gc} + dv_local            (stored)
+//   dh    = e^{g_last} dh + scale (q e^{gc})^T do - w^T bf16(dv2)
+// The q e^{gc} operand is fp32 in the reference; the bf16 path feeds it to the
+// bf16 MFMA as hi + lo = bf16(x) + bf16(x - bf16(x)) (16 significant bits).
+// ---------------------------------------------------------------------------
+constexpr int DBV = 16;
+constexpr int LDT = C + 8;
+
+template <int K> struct DCfg {
+  static constexpr int NW = K == 64 ? 2 : 4;
+  static constexpr int KW = K / NW;
+  static constexpr int KT = KW / 16;
+  static constexpr int KS = KW / 32;
+  static constexpr int OWN = 4 / NW;
+  static constexpr int DO_COLS = DBV / NW;    // do columns each wave stages
+};
+
+template <typename TC, int K>
+struct DhuChunk {
+  using Cfg = DCfg<K>;
+  Frag<TC> kf[4][Cfg::KS];      // k rows 16 tm + lc, the wave's K slice, accumulator order
+  Vec8<TC> qrow[Cfg::KW / 8];   // q[t = lane][wave's K slice]
+  Vec8<TC> wrow[Cfg::KW / 8];   // w[t = lane][wave's K slice]
+  float dov[Cfg::DO_COLS];      // do[t = lane][this wave's columns]
+  f32x4 dvl[Cfg::OWN];          // dv_local of the owned row tiles (C layout)
+  f32x4 gv[Cfg::OWN];           // gc of the owned rows
+  float gt;                     // gc of token lane
+  float gl;
+  int64_t t0;
+  int nv;
+};
+
+template <typename TC, int K>
+__device__ __forceinline__ void dhu_load(DhuChunk<TC, K>& P, const BwdArgs& a, int64_t t0, int nv, int h, int v0,
+                                         int wid, int V) {
+  using Cfg = DCfg<K>;
+  const int l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int H = a.H;
+  P.t0 = t0;
+  P.nv = nv;
+  const TC* k = reinterpret_cast<const TC*>(a.k);
+  const TC* q = reinterpret_cast<const TC*>(a.q);
+  const TC* w = reinterpret_cast<const TC*>(a.w);
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) {
+    const int t = 16 * tm + lc;
+#pragma unroll
+    for (int ks = 0; ks < Cfg::KS; ++ks) {
+      Frag<TC> f = fzero<TC>();
+      if (t < nv) {
+        const TC* p = k + ((t0 + t) * H + h) * (int64_t)K + Cfg::KW * wid + 32 * ks + 4 * lg;
+        const f32x4 x0 = ld4<TC>(p), x1 = ld4<TC>(p + 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          fset<TC>(f, e, x0[e]);
+          fset<TC>(f, e + 4, x1[e]);
+        }
+      }
+      P.kf[tm][ks] = f;
+    }
+  }
+#pragma unroll
+  for (int d8 = 0; d8 < Cfg::KW / 8; ++d8) {
+    P.qrow[d8] = l < nv ? ld8<TC>(q + ((t0 + l) * H + h) * (int64_t)K + Cfg::KW * wid + 8 * d8) : vzero<TC>();
+    P.wrow[d8] = l < nv ? ld8<TC>(w + ((t0 + l) * H + h) * (int64_t)K + Cfg::KW * wid + 8 * d8) : vzero<TC>();
+  }
+  const TC* dov = reinterpret_cast<const TC*>(a.do_);
+#pragma unroll
+  for (int cc = 0; cc < Cfg::DO_COLS; ++cc)
+    P.dov[cc] = l < nv ? to_f32(dov[((t0 + l) * H + h) * (int64_t)V + v0 + Cfg::DO_COLS * wid + cc]) : 0.f;
+  const TC* dvl = reinterpret_cast<const TC*>(a.dvl);
+#pragma unroll
+  for (int o = 0; o < Cfg::OWN; ++o) {
+    const int tm = wid + Cfg::NW * o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tm + 4 * lg + j;
+      P.dvl[o][j] = t < nv ? to_f32(dvl[((t0 + t) * H + h) * (int64_t)V + v0 + lc]) : 0.f;
+      P.gv[o][j] = t < nv ? a.gc[(t0 + t) * H + h] : 0.f;
+    }
+  }
+  P.gt = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
+  P.gl = a.gc[(t0 + nv - 1) * H + h];
+}
+
+template <typename TC, int K>
+__global__ __launch_bounds__(64 * DCfg<K>::NW) void bwd_dhu_kernel(BwdArgs a, int V, int total_units) {
+  using Cfg = DCfg<K>;
+  constexpr int NW = Cfg::NW, KW = Cfg::KW, KT = Cfg::KT, KS = Cfg::KS, OWN = Cfg::OWN;
+  constexpr int NP = sizeof(TC) == 2 ? 2 : 1;          // q e^{gc} parts (hi, lo) for bf16
+  __shared__ __align__(16) f32x4 s_red[NW][4][WAVE];
+  __shared__ __align__(16) TC s_qT[NP][K * LDT];       // rows k (wave slices), cols t
+  __shared__ __align__(16) TC s_wT[K * LDT];           // -w^T
+  __shared__ __align__(16) TC s_doT[DBV * LDT];        // do^T of the 16 columns
+  __shared__ __align__(16) TC s_dvT[DBV * LDT];        // bf16(dv2)^T
+
+  const int per_xcd = gridDim.x / 8;                   // XCD-aware unit order
+  const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (o_idx >= total_units) return;
+  const int nvt = V / DBV;
+  const int unit = o_idx / nvt;
+  const int v0 = (o_idx % nvt) * DBV;
+  const int H = a.H;
+  const int n = unit / H, h = unit % H;
+  const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+
+  int64_t bos, eos, c_first;
+  if (a.cu == nullptr) {
+    bos = (int64_t)n * a.T;
+    eos = bos + a.T;
+    c_first = (int64_t)n * ((a.T + C - 1) / C);
+  } else {
+    bos = a.cu[n];
+    eos = a.cu[n + 1];
+    c_first = a.chunk_off[n];
+  }
+  const int64_t nchunks = (eos - bos + C - 1) / C;
+
+  // dh slice: rows KW wid + 16 tt + 4 lg + j, column v0 + lc; starts at dht
+  f32x4 dh[KT];
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t off = (((int64_t)n * H + h) * K + KW * wid + 16 * tt + 4 * lg + j) * V + v0 + lc;
+      dh[tt][j] = a.dht ? a.dht[off] : 0.f;
+    }
+  }
+
+  DhuChunk<TC, K> cur, nxt;
+  auto chunk_start = [&](int64_t it) { return bos + it * C; };
+  auto chunk_len = [&](int64_t it) { return (int)min((int64_t)C, eos - chunk_start(it)); };
+  if (nchunks > 0) dhu_load<TC, K>(cur, a, chunk_start(nchunks - 1), chunk_len(nchunks - 1), h, v0, wid, V);
+
+  TC* dh_out = reinterpret_cast<TC*>(a.dh);
+  TC* dv2_out = reinterpret_cast<TC*>(a.dv2);
+  for (int64_t it = nchunks - 1; it >= 0; --it) {
+    const int64_t c = c_first + it;
+    if (it > 0) dhu_load<TC, K>(nxt, a, chunk_start(it - 1), chunk_len(it - 1), h, v0, wid, V);
+    const int nv = cur.nv;
+    const int64_t t0 = cur.t0;
+
+    // dh snapshot, row-major [NC, H, K, V]
+    {
+      TC* p = dh_out + ((c * H + h) * K + KW * wid + 4 * lg) * (int64_t)V + v0 + lc;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * (int64_t)V] = from_f32<TC>(dh[tt][j]);
+    }
+    // partial k @ bf16(dh) over this wave's K slice
+    Frag<TC> hb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) hb[ks] = acc_frag<TC>(dh[2 * ks], dh[2 * ks + 1]);
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) mma(acc, cur.kf[tm][ks], hb[ks]);
+      s_red[wid][tm][l] = acc;
+    }
+    // transposed update operands of this wave's K slice (t = lane) and its do columns
+    {
+      const float qs = l < nv ? gexp(cur.gt) * a.scale : 0.f;
+#pragma unroll
+      for (int d8 = 0; d8 < KW / 8; ++d8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = KW * wid + 8 * d8 + e;
+          const float qg = vget<TC>(cur.qrow[d8], e) * qs;
+          const TC hi = from_f32<TC>(qg);
+          s_qT[0][r * LDT + l] = hi;
+          if constexpr (NP == 2) s_qT[NP - 1][r * LDT + l] = from_f32<TC>(qg - to_f32(hi));
+          s_wT[r * LDT + l] = from_f32<TC>(-vget<TC>(cur.wrow[d8], e));
+        }
+      }
+    }
+    __syncthreads();
+
+    // do^T columns of this wave (after the barrier: every wave has finished the previous
+    // chunk's update, which reads s_doT and s_dvT); dv2 of the owned row tiles
+#pragma unroll
+    for (int cc = 0; cc < Cfg::DO_COLS; ++cc) s_doT[(Cfg::DO_COLS * wid + cc) * LDT + l] = from_f32<TC>(cur.dov[cc]);
+#pragma unroll
+    for (int o = 0; o < OWN; ++o) {
+      const int tm = wid + NW * o;
+      f32x4 kd = s_red[0][tm][l];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) kd += s_red[w2][tm][l];
+      float dv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tm + 4 * lg + j;
+        dv[j] = t < nv ? kd[j] * gexp(cur.gl - cur.gv[o][j]) + cur.dvl[o][j] : 0.f;
+        if (t < nv) dv2_out[((t0 + t) * H + h) * (int64_t)V + v0 + lc] = from_f32<TC>(dv[j]);
+      }
+      st4<TC>(s_dvT + lc * LDT + 16 * tm + 4 * lg, dv[0], dv[1], dv[2], dv[3]);
+    }
+    __syncthreads();
+
+    // dh = e^{g_last} dh + (scale q e^{gc})^T do - w^T bf16(dv2)
+    const float eg = gexp(cur.gl);
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      dh[tt] *= eg;
+      const int r0 = KW * wid + 16 * tt;
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        const Frag<TC> bdo = lds_frag<TC>(s_doT, LDT, 0, 32 * ks2);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) mma(dh[tt], lds_frag<TC>(s_qT[p], LDT, r0, 32 * ks2), bdo);
+        mma(dh[tt], lds_frag<TC>(s_wT, LDT, r0, 32 * ks2), lds_frag<TC>(s_dvT, LDT, 0, 32 * ks2));
+      }
+    }
+    cur = nxt;
+  }
+
+  if (a.dh0) {
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (((int64_t)n * H + h) * K + KW * wid + 16 * tt + 4 * lg + j) * V + v0 + lc;
+        a.dh0[off] = dh[tt][j];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq, dk, dw, dg (chunk_o.py:147-326, USE_G and USE_DW).  Wave w owns tokens
+// 16 w .. 16 w + 15 of the chunk.  Outputs are computed transposed ([d][t]
+// tiles) so that each lane stores 4 consecutive d of one token.
+// ---------------------------------------------------------------------------
+template <typename TC>
+__host__ __device__ constexpr size_t dqkwg_lds(int K) {
+  return sizeof(TC) * (2 * (size_t)tile_elems<TC>(K) + tile_elems<TC>(64)) + (6 * 64 + 4) * sizeof(float);
+}
+
+template <typename TC, int K>
+__global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  TC* s_q = reinterpret_cast<TC*>(smem);
+  TC* s_k = s_q + tile_elems<TC>(K);
+  TC* s_ds = s_k + tile_elems<TC>(K);
+  float* s_g = reinterpret_cast<float*>(s_ds + tile_elems<TC>(64));
+  float* s_dgrow = s_g + 64;
+  float* s_dgcol = s_dgrow + 64;                      // [4][64]: one row of column sums per wave
+  float* s_dgl = s_dgcol + 4 * 64;                    // [4]: per-wave parts of the last row's extra term
+  const int h = blockIdx.y, H = a.H;
+  const int64_t c = blockIdx.x;
+  const ChunkLoc loc = locate_chunk(c, a.cu, a.chunk_off, a.N, a.T);
+  if (!loc.ok) return;
+  const int64_t t0 = loc.t0;
+  const int nv = loc.nv;
+  const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  stage_rows<TC>(s_q, reinterpret_cast<const TC*>(a.q), t0, nv, H, h, K);
+  stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+  if (threadIdx.x < 64) s_g[threadIdx.x] = threadIdx.x < nv ? a.gc[(t0 + threadIdx.x) * H + h] : 0.f;
+  __syncthreads();
+  const float gl = s_g[nv - 1];
+
+  const TC* do_ = reinterpret_cast<const TC*>(a.do_);
+  const TC* vn = reinterpret_cast<const TC*>(a.vn);
+  const TC* dv2 = reinterpret_cast<const TC*>(a.dv2);
+  const int tr = 16 * wid + lc;                       // token of this lane's operand rows
+  const bool tr_ok = tr < nv;
+  const TC* do_row = do_ + ((t0 + tr) * H + h) * (int64_t)V;
+
+  // ---- ds = mask_{i>=j}(do v_new^T e^{g_i - g_j}) scale; ds2 = ds * q k^T -> dg row and column sums
+  float rowp[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int tj = 0; tj < 4; ++tj) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, aqk = {0.f, 0.f, 0.f, 0.f};
+    if (tj <= wid) {
+      const int tv = 16 * tj + lc;
+      const TC* vn_row = vn + ((t0 + tv) * H + h) * (int64_t)V;
+      for (int vs = 0; vs < V / 32; ++vs) mma(acc, g_nat<TC>(do_row, 32 * vs, tr_ok), g_nat<TC>(vn_row, 32 * vs, tv < nv));
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks) mma(aqk, t_nat<TC>(s_q, K, 16 * wid, 32 * ks), t_nat<TC>(s_k, K, 16 * tj, 32 * ks));
+    }
+    const int j = 16 * tj + lc;
+    float colp = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int i = 16 * wid + 4 * lg + jj;
+      const bool m = i >= j && i < nv;
+      const float ds = m ? acc[jj] * gexp(s_g[i] - s_g[j]) * a.scale : 0.f;
+      const float ds2 = ds * aqk[jj];
+      rowp[jj] += ds2;
+      colp += ds2;
+      s_ds[toff<TC>(i, j, 64)] = from_f32<TC>(ds);
+    }
+    colp = sum_lg(colp);                              // (plain stores and a fixed-order sum below:
+    if (lg == 0) s_dgcol[wid * 64 + j] = colp;        //  dg is bitwise reproducible)
+  }
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const float r = sum16(rowp[jj]);
+    if (lc == 0) s_dgrow[16 * wid + 4 * lg + jj] = r;
+  }
+  __syncthreads();
+
+  // ---- per 16-row tile of K: dq, dk, -dw for this wave's 16 tokens
+  const TC* hp = reinterpret_cast<const TC*>(a.h) + (c * H + h) * (int64_t)K * V;
+  const TC* dhp = reinterpret_cast<const TC*>(a.dh) + (c * H + h) * (int64_t)K * V;
+  const TC* vn_row = vn + ((t0 + tr) * H + h) * (int64_t)V;
+  const TC* dv2_row = dv2 + ((t0 + tr) * H + h) * (int64_t)V;
+  const int t = tr;                                   // output token of this lane (column lc of the tiles)
+  const float eg = gexp(s_g[t]) * a.scale;
+  const float gate = t < nv ? gexp(gl - s_g[t]) : 0.f;
+  float dgt = 0.f, dglp = 0.f, hdh = 0.f;
+  TC* dq_out = reinterpret_cast<TC*>(a.dq);
+  TC* dk_out = reinterpret_cast<TC*>(a.dk1);
+  TC* dw_out = reinterpret_cast<TC*>(a.dw);
+  for (int kt = 0; kt < K / 16; ++kt) {
+    f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ak = aq, aw = aq, aq2 = aq, ak2 = aq;
+    const TC* hrow = hp + (16 * kt + lc) * (int64_t)V;
+    const TC* dhrow = dhp + (16 * kt + lc) * (int64_t)V;
+    for (int vs = 0; vs < V / 32; ++vs) {
+      const Frag<TC> hf = g_nat<TC>(hrow, 32 * vs, true);
+      const Frag<TC> dhf = g_nat<TC>(dhrow, 32 * vs, true);
+      mma(aq, hf, g_nat<TC>(do_row, 32 * vs, tr_ok));       // sum_v h[k][v] do[t][v]
+      mma(aw, hf, g_nat<TC>(dv2_row, 32 * vs, tr_ok));      // sum_v h[k][v] dv2[t][v]
+      mma(ak, dhf, g_nat<TC>(vn_row, 32 * vs, tr_ok));      // sum_v dh[k][v] v_new[t][v]
+      if (wid == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hdh += fget<TC>(hf, e) * fget<TC>(dhf, e);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      mma(aq2, t_tr<TC>(s_k, K, 32 * s, 16 * kt), t_acc<TC>(s_ds, 64, 16 * wid, 32 * s));   // sum_t' k[t'][k] ds[t][t']
+      mma(ak2, t_tr<TC>(s_q, K, 32 * s, 16 * kt), t_tr<TC>(s_ds, 64, 32 * s, 16 * wid));   // sum_i q[i][k] ds[i][t]
+    }
+    const int k0 = 16 * kt + 4 * lg;
+    const f32x4 qv = t_row4<TC>(s_q, K, t, k0);
+    const f32x4 kv = t_row4<TC>(s_k, K, t, k0);
+    f32x4 dq, dk, dw;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float dq1 = aq[jj] * eg;
+      dgt += dq1 * qv[jj];
+      dq[jj] = dq1 + aq2[jj];
+      const float dk1 = ak[jj] * gate;
+      dgt -= kv[jj] * dk1;
+      dglp += dk1 * kv[jj];
+      dk[jj] = dk1 + ak2[jj];
+      dw[jj] = -aw[jj];
+    }
+    if (t < nv) {
+      const int64_t o = ((t0 + t) * H + h) * (int64_t)K + k0;
+      st4v<TC>(dq_out + o, dq);
+      st4v<TC>(dk_out + o, dk);
+      st4v<TC>(dw_out + o, dw);
+    }
+  }
+  dgt = sum_lg(dgt);
+  dglp = sum64(dglp);
+  if (wid == 0) dglp += sum64(hdh) * gexp(gl);
+  if (l == 0) s_dgl[wid] = dglp;
+  __syncthreads();
+  if (lg == 0 && t < nv) {
+    float dg = s_dgrow[t] - (s_dgcol[t] + s_dgcol[64 + t] + s_dgcol[128 + t] + s_dgcol[192 + t]) + dgt;
+    if (t == nv - 1) dg += s_dgl[0] + s_dgl[1] + s_dgl[2] + s_dgl[3];
+    a.dg1[(t0 + t) * H + h] = dg;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// WY backward (wy_fast.py:98-210, USE_G) with the final sums of chunk.py:140-145:
+// dk = dk1 + dk2 (in the storage type), dg = reverse chunk cumsum of dg1 + dg2.
+// ---------------------------------------------------------------------------
+template <typename TC>
+__host__ __device__ constexpr size_t wy_lds(int K, int V) {
+  return sizeof(TC) * (2 * (size_t)tile_elems<TC>(K) + tile_elems<TC>(V) + 3 * (size_t)tile_elems<TC>(64)) +
+         7 * 64 * sizeof(float);
+}
+
+template <typename TC, int K>
+__global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  TC* s_k = reinterpret_cast<TC*>(smem);
+  TC* s_dw = s_k + tile_elems<TC>(K);
+  TC* s_du = s_dw + tile_elems<TC>(K);
+  TC* s_Ai = s_du + tile_elems<TC>(V);
+  TC* s_dA = s_Ai + tile_elems<TC>(64);
+  TC* s_dA1 = s_dA + tile_elems<TC>(64);
+  float* s_g = reinterpret_cast<float*>(s_dA1 + tile_elems<TC>(64));
+  float* s_b = s_g + 64;
+  float* s_dg = s_b + 64;                             // row parts of dg2 (each token written by its wave)
+  float* s_dgc = s_dg + 64;                           // [4][64]: column parts, one row per wave
+  const int h = blockIdx.y, H = a.H;
+  const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
+  if (!loc.ok) return;
+  const int64_t t0 = loc.t0;
+  const int nv = loc.nv;
+  const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+  stage_rows<TC>(s_dw, reinterpret_cast<const TC*>(a.dw), t0, nv, H, h, K);
+  stage_rows<TC>(s_du, reinterpret_cast<const TC*>(a.dv2), t0, nv, H, h, V);
+  stage_rows<TC>(s_Ai, reinterpret_cast<const TC*>(a.Ai), t0, nv, H, h, 64);
+  if (threadIdx.x < 64) {
+    const int r = threadIdx.x;
+    s_g[r] = r < nv ? a.gc[(t0 + r) * H + h] : 0.f;
+    s_b[r] = r < nv ? ld_scalar(a.beta, (t0 + r) * H + h, a.beta_dtype) : 0.f;
+  }
+  __syncthreads();
+
+  // ---- dA = dw bf16(k beta e^g)^T + du bf16(v beta)^T, strictly lower (rows of this wave)
+  const TC* v = reinterpret_cast<const TC*>(a.v);
+  for (int tj = 0; tj < 4; ++tj) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (tj <= wid) {
+      const int j = 16 * tj + lc;                     // operand row of the B fragments
+      const float fk = s_b[j] * gexp(s_g[j]);
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks)
+        mma(acc, t_nat<TC>(s_dw, K, 16 * wid, 32 * ks), fscale<TC>(t_nat<TC>(s_k, K, 16 * tj, 32 * ks), fk));
+      const TC* vrow = v + ((t0 + j) * H + h) * (int64_t)V;
+      for (int vs = 0; vs < V / 32; ++vs)
+        mma(acc, t_nat<TC>(s_du, V, 16 * wid, 32 * vs), fscale<TC>(g_nat<TC>(vrow, 32 * vs, j < nv), s_b[j]));
+    }
+    const int j = 16 * tj + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int i = 16 * wid + 4 * lg + jj;
+      s_dA[toff<TC>(i, j, 64)] = from_f32<TC>(i > j && i < nv ? acc[jj] : 0.f);
+    }
+  }
+  __syncthreads();
+  // ---- dA1 = bf16(dA) Ai^T
+  for (int tc = 0; tc < 4; ++tc) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) mma(acc, t_nat<TC>(s_dA, 64, 16 * wid, 32 * s), t_nat<TC>(s_Ai, 64, 16 * tc, 32 * s));
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) s_dA1[toff<TC>(16 * wid + 4 * lg + jj, 16 * tc + lc, 64)] = from_f32<TC>(acc[jj]);
+  }
+  __syncthreads();
+  // ---- dA = -(Ai^T bf16(dA1)) e^{g_t - g_c}, strictly lower; AdA = dA * (bf16(k beta) k^T) -> dg
+  float rowp[4] = {0.f, 0.f, 0.f, 0.f};
+  {
+    const float fb = s_b[16 * wid + lc];              // beta of the A fragment's row
+    for (int tc = 0; tc < 4; ++tc) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_Ai, 64, 32 * s, 16 * wid), t_tr<TC>(s_dA1, 64, 32 * s, 16 * tc));
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks)
+        mma(a2, fscale<TC>(t_nat<TC>(s_k, K, 16 * wid, 32 * ks), fb), t_nat<TC>(s_k, K, 16 * tc, 32 * ks));
+      const int cc = 16 * tc + lc;
+      float colp = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int tt = 16 * wid + 4 * lg + jj;
+        const bool m = tt > cc && tt < nv;
+        const float dA = round_to<TC>(m ? -acc[jj] * gexp(s_g[tt] - s_g[cc]) : 0.f);
+        s_dA[toff<TC>(tt, cc, 64)] = from_f32<TC>(dA);
+        const float ada = dA * a2[jj];
+        rowp[jj] += ada;
+        colp += ada;
+      }
+      colp = sum_lg(colp);
+      if (lg == 0) s_dgc[wid * 64 + cc] = -colp;
+    }
+  }
+  float rowsum[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) rowsum[jj] = sum16(rowp[jj]);
+  if (lc == 0) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) s_dg[16 * wid + 4 * lg + jj] = rowsum[jj];
+  }
+  __syncthreads();
+
+  // ---- per token tile (this wave): dk2, dk, dv, dbeta and the dkbg.kbg part of dg
+  const int t = 16 * wid + lc;
+  const float bt = s_b[t], egt = gexp(s_g[t]);
+  Frag<TC> bAi[2], bdA[2], bdAt[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    bAi[s] = t_tr<TC>(s_Ai, 64, 32 * s, 16 * wid);     // B[n = t][j] = Ai[j][t]
+    bdA[s] = t_acc<TC>(s_dA, 64, 16 * wid, 32 * s);    // B[n = t][j] = dA[t][j]
+    bdAt[s] = t_tr<TC>(s_dA, 64, 32 * s, 16 * wid);    // B[n = t][j] = dA[j][t]
+  }
+  float dbt = 0.f, dgt = 0.f;
+  TC* dk_out = reinterpret_cast<TC*>(a.dk);
+  const TC* dk1 = reinterpret_cast<const TC*>(a.dk1);
+  for (int kt = 0; kt < K / 16; ++kt) {
+    f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1, a3 = a1;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      mma(a1, t_tr<TC>(s_dw, K, 32 * s, 16 * kt), bAi[s]);     // dkbg^T[k][t] = sum_j dw[j][k] Ai[j][t]
+      const Frag<TC> kT = t_tr<TC>(s_k, K, 32 * s, 16 * kt);
+      mma(a2, kT, bdA[s]);                                    // dkb^T[k][t] = sum_j k[j][k] dA[t][j]
+      Frag<TC> kbT;                                           // bf16(k beta)^T: K index = row j
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fset<TC>(kbT, e, fget<TC>(kT, e) * s_b[32 * s + acc_row(e)]);
+      mma(a3, kbT, bdAt[s]);                                  // (dA^T kb)^T[k][t]
+    }
+    const int k0 = 16 * kt + 4 * lg;
+    const f32x4 kv = t_row4<TC>(s_k, K, t, k0);
+    f32x4 d1 = {0.f, 0.f, 0.f, 0.f};
+    if (t < nv) d1 = g_row4<TC>(dk1 + ((t0 + t) * H + h) * (int64_t)K + k0);
+    f32x4 dk;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const float dkr = round_to<TC>(a1[jj] * egt * bt);
+      dbt += a1[jj] * kv[jj] * egt + a2[jj] * kv[jj];
+      dgt += a1[jj] * (kv[jj] * bt * egt);
+      const float dk2 = round_to<TC>(dkr + a3[jj] + a2[jj] * bt);
+      dk[jj] = d1[jj] + dk2;
+    }
+    if (t < nv) st4v<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0, dk);
+  }
+  TC* dv_out = reinterpret_cast<TC*>(a.dv);
+  for (int vt = 0; vt < V / 16; ++vt) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_du, V, 32 * s, 16 * vt), bAi[s]);   // dvb^T[v][t]
+    const int v0 = 16 * vt + 4 * lg;
+    if (t < nv) {
+      const f32x4 vv = g_row4<TC>(v + ((t0 + t) * H + h) * (int64_t)V + v0);
+      f32x4 dv;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        dv[jj] = acc[jj] * bt;
+        dbt += acc[jj] * vv[jj];
+      }
+      st4v<TC>(dv_out + ((t0 + t) * H + h) * (int64_t)V + v0, dv);
+    }
+  }
+  dbt = sum_lg(dbt);
+  dgt = sum_lg(dgt);
+  if (lg == 0) {
+    s_dg[t] += dgt;                                   // token t belongs to this wave only
+    if (t < nv) {
+      const int64_t o = (t0 + t) * H + h;
+      if (a.beta_dtype == DT_F32) reinterpret_cast<float*>(a.db)[o] = dbt;
+      else reinterpret_cast<bf16*>(a.db)[o] = (bf16)dbt;
+    }
+  }
+  __syncthreads();
+  // ---- dg = reverse cumsum within the chunk of dg1 + dg2 (valid rows)
+  if (wid == 0) {
+    float x = l < nv ? a.dg1[(t0 + l) * H + h] + s_dg[l] + (s_dgc[l] + s_dgc[64 + l] + s_dgc[128 + l] + s_dgc[192 + l])
+                     : 0.f;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const float y = __shfl_down(x, o, WAVE);
+      if (l + o < WAVE) x += y;
+    }
+    if (l < nv) a.dg[(t0 + l) * H + h] = x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// l2norm backward (l2norm.py:132-154) with rstd and y recomputed from the input x:
+// rstd = 1 / sqrt(sum x^2 + 1e-6), y = x rstd (rounded), dx = dy rstd - sum(dy y) y rstd.
+// One wave per row, D <= 512.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void l2norm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                         T* __restrict__ dx, int64_t rows, int D) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / WAVE;
+  if (row >= rows) return;
+  const int l = lane_id();
+  const bool act = 8 * l < D;
+  Vec8<T> xv = vzero<T>(), gv = vzero<T>();
+  if (act) {
+    xv = ld8<T>(x + row * D + 8 * l);
+    gv = ld8<T>(dy + row * D + 8 * l);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss = fmaf(vget<T>(xv, e), vget<T>(xv, e), ss);
+  ss = sum64(ss);
+  const float rstd = 1.0f / sqrtf(ss + 1e-6f);
+  float y[8], dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    y[e] = round_to<T>(vget<T>(xv, e) * rstd);
+    dot = fmaf(vget<T>(gv, e), y[e], dot);
+  }
+  dot = sum64(dot);
+  if (act) {
+    Vec8<T> o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vset<T>(o, e, vget<T>(gv, e) * rstd - dot * y[e] * rstd);
+    st8<T>(dx + row * D + 8 * l, o);
+  }
+}
+
+template <typename K_>
+int set_lds(K_ kern, size_t bytes) {
+  if (bytes > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) != hipSuccess)
+    return -1;
+  return 0;
+}
+
+template <typename TC, int K>
+int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, hipStream_t s) {
+  const dim3 grid((unsigned)nc_grid, (unsigned)a.H);
+  if (nc_grid > 0) {
+    const size_t l1 = dvl_lds<TC>(K, V);
+    if (l1 > 160 * 1024 || set_lds(bwd_dvl_kernel<TC, K>, l1)) return -1;
+    hipLaunchKernelGGL((bwd_dvl_kernel<TC, K>), grid, dim3(NT_B), l1, s, a, V);
+  }
+  {
+    const int total = a.N * a.H * (V / DBV);
+    const int g8 = (total + 7) / 8 * 8;
+    if (total > 0) hipLaunchKernelGGL((bwd_dhu_kernel<TC, K>), dim3(g8), dim3(64 * DCfg<K>::NW), 0, s, a, V, total);
+  }
+  if (nc_grid > 0) {
+    const size_t l3 = dqkwg_lds<TC>(K);
+    if (set_lds(bwd_dqkwg_kernel<TC, K>, l3)) return -1;
+    hipLaunchKernelGGL((bwd_dqkwg_kernel<TC, K>), grid, dim3(NT_B), l3, s, a, V);
+    const size_t l4 = wy_lds<TC>(K, V);
+    if (l4 > 160 * 1024 || set_lds(bwd_wy_kernel<TC, K>, l4)) return -1;
+    hipLaunchKernelGGL((bwd_wy_kernel<TC, K>), grid, dim3(NT_B), l4, s, a, V);
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+bool bwd_supported(int compute_dtype, int K, int V) {
+  if (V <= 0 || V % 64 != 0 || !(K == 64 || K == 128 || K == 256)) return false;
+  if (compute_dtype == DT_BF16) return V <= 512 && wy_lds<bf16>(K, V) <= 160 * 1024 && dvl_lds<bf16>(K, V) <= 160 * 1024;
+  if (compute_dtype == DT_F32) return K <= 128 && V <= 128;
+  return false;
+}
+
+int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, hipStream_t s) {
+  if (!bwd_supported(compute_dtype, K, V)) return -2;
+#define KGDN_B_CASE(TC, KK) \
+  if (K == KK) return launch_bwd_t<TC, KK>(a, V, nc_grid, s);
+  if (compute_dtype == DT_BF16) { KGDN_B_CASE(bf16, 64) KGDN_B_CASE(bf16, 128) KGDN_B_CASE(bf16, 256) }
+  if (compute_dtype == DT_F32) { KGDN_B_CASE(float, 64) KGDN_B_CASE(float, 128) }
+#undef KGDN_B_CASE
+  return -2;
+}
+
+int launch_l2norm_bwd(const void* x, const void* dy, void* dx, int dtype, int64_t rows, int D, hipStream_t s) {
+  if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (dtype == DT_F32) {
+    hipLaunchKernelGGL(l2norm_bwd_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(x),
+                       static_cast<const float*>(dy), static_cast<float*>(dx), rows, D);
+  } else if (dtype == DT_BF16) {
+    hipLaunchKernelGGL(l2norm_bwd_kernel<bf16>, grid, dim3(256), 0, s, static_cast<const bf16*>(x),
+                       static_cast<const bf16*>(dy), static_cast<bf16*>(dx), rows, D);
+  } else {
+    return -2;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace kgdn

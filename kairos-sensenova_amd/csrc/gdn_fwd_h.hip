@@ -201,9 +201,17 @@ __global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int
     const int nv = cur.nv;
 
     // snapshot of the state before this chunk
-    TC* hrow = hT + ((c * H + h) * V + v0 + lc) * K + KW * wid + 4 * lg;
+    if (a.row_major) {            // h [NC, H, K, V]: 16 lanes write 16 consecutive columns of a row
+      TC* hcol = hT + ((c * H + h) * K + KW * wid + 4 * lg) * (int64_t)V + v0 + lc;
 #pragma unroll
-    for (int tt = 0; tt < KT; ++tt) st4<TC>(hrow + 16 * tt, S[tt][0], S[tt][1], S[tt][2], S[tt][3]);
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hcol[(16 * tt + j) * (int64_t)V] = from_f32<TC>(S[tt][j]);
+    } else {
+      TC* hrow = hT + ((c * H + h) * V + v0 + lc) * K + KW * wid + 4 * lg;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt) st4<TC>(hrow + 16 * tt, S[tt][0], S[tt][1], S[tt][2], S[tt][3]);
+    }
 
     // partial w @ S over this wave's K slice
     Frag<TC> hb[KS];
@@ -233,7 +241,15 @@ __global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int
       f32x4 vp = cur.uv[o];
 #pragma unroll
       for (int w2 = 0; w2 < NW; ++w2) vp -= s_red[w2][tm][l];
-      st4<TC>(vrow + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
+      if (a.row_major) {          // v_new [B*T, H, V]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = 16 * tm + 4 * lg + j;
+          if (t < nv) vnT[((cur.t0 + t) * H + h) * (int64_t)V + v0 + lc] = from_f32<TC>(vp[j]);
+        }
+      } else {
+        st4<TC>(vrow + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
+      }
       float vg[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -437,15 +453,23 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
     if (active) {
       // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139): through the
       // wave's LDS tile so that each store instruction writes two whole 512-byte rows of hT
-      bf16* hs = s_hs[wid];
+      if (a.row_major) {          // h [NC, H, K, V]: 16 lanes write 16 consecutive columns of a row
+        bf16* hrow = hT + ((c * H + h) * WK + 4 * lg) * (int64_t)V + vcol;
 #pragma unroll
-      for (int kt = 0; kt < 16; ++kt) st4<bf16>(hs + lc * LDW + 16 * kt + 4 * lg, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      bf16* hcol = hT + ((c * H + h) * V + v0) * WK;
+        for (int kt = 0; kt < 16; ++kt)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int pc = l + 64 * i, r = pc >> 5, ch = pc & 31;   // row (column of S), 16-byte chunk
-        *reinterpret_cast<uint4*>(hcol + r * WK + 8 * ch) = *reinterpret_cast<const uint4*>(hs + r * LDW + 8 * ch);
+          for (int j = 0; j < 4; ++j) hrow[(16 * kt + j) * (int64_t)V] = (bf16)S[kt][j];
+      } else {
+        bf16* hs = s_hs[wid];
+#pragma unroll
+        for (int kt = 0; kt < 16; ++kt) st4<bf16>(hs + lc * LDW + 16 * kt + 4 * lg, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        bf16* hcol = hT + ((c * H + h) * V + v0) * WK;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int pc = l + 64 * i, r = pc >> 5, ch = pc & 31;   // row (column of S), 16-byte chunk
+          *reinterpret_cast<uint4*>(hcol + r * WK + 8 * ch) = *reinterpret_cast<const uint4*>(hs + r * LDW + 8 * ch);
+        }
       }
       // w @ bf16(S): the B fragment of a 32-deep step is two accumulator tiles; the A
       // fragment takes the same K order (rows 4 lg .. and 16 + 4 lg .. of the step).
@@ -486,7 +510,14 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       // order of the transposed k fragments (tokens 32 ks + 4 lg .. and 32 ks + 16 + 4 lg ..);
       // v_new (ungated) leaves through the wave's LDS tile as whole 128-byte rows of vnT
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      {
+      if (a.row_major) {          // v_new [B*T, H, V] from the wave's [col][t] tile: lane = token
+        if (l < nv) {
+          const int64_t t0 = bos + it * C;
+          bf16* vrow = vnT + ((t0 + l) * H + h) * (int64_t)V + v0;
+#pragma unroll
+          for (int cc = 0; cc < 16; ++cc) vrow[cc] = s_vn[wid][cc * LDT + l];
+        }
+      } else {
         bf16* vcolp = vnT + ((c * H + h) * V + v0) * C;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {

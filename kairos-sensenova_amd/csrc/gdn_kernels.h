@@ -54,6 +54,7 @@ struct FwdHArgs {
   void* hT;               // out [NC, H, V, K] state snapshots (before each chunk)
   void* vnT;              // out [NC, H, V, 64] ungated v_new
   float* ht;              // out [N, H, K, V] fp32 or nullptr
+  bool row_major;         // write the reference layouts instead: hT -> h [NC, H, K, V], vnT -> v_new [B*T, H, V]
 };
 
 struct FwdOArgs {
@@ -115,6 +116,45 @@ struct SegFwdArgs {
   bool run_combine;       // ... or final_state of empty sequences is needed
   hipEvent_t* events;     // optional [5]: recorded before seg_prep, seg_trans, seg_combine, seg_out and after seg_out
 };
+
+// Backward pass (gdn_bwd.hip), after the forward is recomputed by launch_prepare (gc, w, uT, Ai)
+// and launch_fwd_h with row_major (h, v_new).  All token tensors are [B*T, H, *] in the compute
+// dtype; q and k are the (normalised) operands the forward used.
+struct BwdArgs {
+  const void* q;          // [B*T, H, K]
+  const void* k;          // [B*T, H, K]
+  const void* v;          // [B*T, H, V]
+  const float* gc;        // [B*T, H] chunk-local cumsum of g
+  const void* beta;       // [B*T, H] beta_dtype
+  int beta_dtype;
+  const void* do_;        // [B*T, H, V] gradient of o
+  const float* dht;       // [N, H, K, V] gradient of final_state, or nullptr (zero)
+  const void* w;          // [B*T, H, K]
+  const void* Ai;         // [B*T, H, 64] (I + A)^-1 rows
+  const void* h;          // [NC, H, K, V] state snapshots
+  const void* vn;         // [B*T, H, V] v_new
+  void* dvl;              // [B*T, H, V] dv_local (scratch)
+  void* dh;               // [NC, H, K, V] dh snapshots (scratch)
+  void* dv2;              // [B*T, H, V] dv after the state recurrence (scratch)
+  void* dw;               // [B*T, H, K] -dw as the reference stores it (scratch)
+  void* dk1;              // [B*T, H, K] dk of chunk_bwd_dqkwg (scratch)
+  float* dg1;             // [B*T, H] dg of chunk_bwd_dqkwg, before the cumsum (scratch)
+  void* dq;               // out [B*T, H, K]
+  void* dk;               // out [B*T, H, K]
+  void* dv;               // out [B*T, H, V]
+  float* dg;              // out [B*T, H]
+  void* db;               // out [B*T, H] beta_dtype
+  float* dh0;             // out [N, H, K, V] or nullptr
+  const int64_t* cu;
+  const int32_t* chunk_off;
+  int N;
+  int64_t T;
+  int H;
+  float scale;
+};
+bool bwd_supported(int compute_dtype, int K, int V);
+int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, hipStream_t s);
+int launch_l2norm_bwd(const void* x, const void* dy, void* dx, int dtype, int64_t rows, int D, hipStream_t s);
 
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported
 // (dtype, K, V) combination.

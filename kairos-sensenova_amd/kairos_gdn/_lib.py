@@ -35,6 +35,9 @@ SIGNATURES = {
     "kairos_gdn_chunk_fwd_noalloc": (_i, [_p, _p, _p, _p, _p, _fp, _fp, _p, _p, _fp, _p, _i64,
                                          _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _i, _i, _f, _i, _p]),
     "kairos_gdn_chunk_fwd_noalloc_max_bytes": (_sz, []),
+    "kairos_gdn_chunk_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
+    "kairos_gdn_chunk_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _fp, _p, _p, _p, _fp, _p, _fp, _p, _i64, _i64,
+                                  _i64, _i64, _i64, _i64, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p]),
     "kairos_gdn_stage_workspace_size": (_sz, [_i64]),
     "kairos_gdn_chunk_local_cumsum": (_i, [_p, _i, _fp, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "kairos_gdn_prepare_wy": (_i, [_p, _p, _p, _p, _fp, _fp, _p, _p, _fp, _p, _p, _i64,

@@ -144,10 +144,54 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_fi
     return o, ht
 
 
-class ChunkGatedDeltaRuleFunction(torch.autograd.Function):
-    """Forward-only autograd wrapper (the reference's is chunk.py:149-213).
+def chunk_gated_delta_rule_bwd(q, k, v, g, beta, scale, initial_state, do, dht, cu_seqlens=None,
+                               use_qk_l2norm_in_kernel=False):
+    """One native call: gradients of chunk_gated_delta_rule (chunk.py:70-146, 188-213).
 
-    The backward pass is outside this build: calling backward raises.
+    q and k are the forward's own inputs (before the optional in-op L2 norm,
+    which the library recomputes, as it recomputes gc, Ai, w, u, h and v_new).
+    Returns (dq, dk, dv, dg fp32, dbeta, dh0 fp32 or None).
+    """
+    dev = _require_device(q, k, v, g, beta, initial_state, do, dht)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    qk_dt, v_dt = _code(q, "q"), _code(v, "v")
+    if qk_dt == _lib.F8E4M3:
+        raise NotImplementedError("the backward pass takes bf16 or fp32 q/k; fp8 q/k are forward-only")
+    g_dt, b_dt = _code(g, "g"), _code(beta, "beta")
+    q, k, v, g, beta = (x.contiguous() for x in (q, k, v, g, beta))
+    do = do.to(v.dtype).contiguous()
+    n_seqs, cu = 0, None
+    if cu_seqlens is not None:
+        cu = _prepare_cu_seqlens(cu_seqlens, dev, T)
+        n_seqs = cu.numel() - 1
+    N = n_seqs if cu is not None else B
+    h0, h0_dt = None, _lib.F32
+    if initial_state is not None:
+        h0 = initial_state if initial_state.dtype in (torch.float32, torch.bfloat16) else initial_state.float()
+        h0 = h0.contiguous()
+        h0_dt = _code(h0, "initial_state")
+    dht_ = dht.to(torch.float32).contiguous() if dht is not None else None
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    db = torch.empty_like(beta)
+    dh0 = torch.empty(N, H, K, V, device=dev, dtype=torch.float32) if h0 is not None else None
+    l2 = int(bool(use_qk_l2norm_in_kernel))
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_bwd_workspace_size(B, T, H, K, V, n_seqs, qk_dt, v_dt, l2)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("kairos_gdn_chunk_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(h0), _ptr(do), _ptr(dht_),
+              _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(db), _ptr(dh0), _ptr(cu), n_seqs, B, T, H, K, V, qk_dt,
+              v_dt, g_dt, b_dt, h0_dt, float(scale), l2, _ptr(ws), ws_bytes, _stream(dev))
+    return dq, dk, dv, dg, db, dh0
+
+
+class ChunkGatedDeltaRuleFunction(torch.autograd.Function):
+    """Autograd wrapper (the reference's is chunk.py:149-213).
+
+    forward saves the inputs; backward runs the native backward, which
+    recomputes the forward's intermediates (the reference saves the normalised
+    q, k and Ai, chunk.py:182, and recomputes w, u, h and v_new, chunk.py:84-101).
     """
 
     @staticmethod
@@ -155,12 +199,18 @@ class ChunkGatedDeltaRuleFunction(torch.autograd.Function):
                 use_qk_l2norm_in_kernel=False, q_scale=None, k_scale=None):
         o, ht = chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_final_state,
                                            cu_seqlens, use_qk_l2norm_in_kernel, q_scale, k_scale)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, cu_seqlens)
+        ctx.scale = scale
+        ctx.use_qk_l2norm_in_kernel = use_qk_l2norm_in_kernel
         out_dtype = v.dtype if (_FP8 is not None and q.dtype == _FP8) else q.dtype
         return o.to(out_dtype), ht
 
     @staticmethod
     def backward(ctx, do, dht):
-        raise NotImplementedError("kairos_gdn implements the forward pass only; backward is not built")
+        q, k, v, g, beta, initial_state, cu_seqlens = ctx.saved_tensors
+        dq, dk, dv, dg, db, dh0 = chunk_gated_delta_rule_bwd(q, k, v, g, beta, ctx.scale, initial_state, do, dht,
+                                                             cu_seqlens, ctx.use_qk_l2norm_in_kernel)
+        return dq.to(q), dk.to(k), dv.to(v), dg.to(g), db.to(beta), None, dh0, None, None, None, None, None
 
 
 @torch.compiler.disable

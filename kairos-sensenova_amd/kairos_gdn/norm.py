@@ -101,7 +101,7 @@ class FusedRMSNormGated(nn.Module):
             nn.init.ones_(self.weight)
 
     def extra_repr(self) -> str:
-        parts = [str(self.hidden_size), f"eps={self.eps}", f"activation={self.activation!r}"]
+        parts = [str(self.hidden_size), f"eps={self.eps}", f"activation={self.activation}"]
         if not self.elementwise_affine:
             parts.insert(1, "elementwise_affine=False")
         return ", ".join(parts)

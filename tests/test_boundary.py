@@ -176,10 +176,22 @@ def test_stages_refuse_cpu_tensors():
         kairos_gdn.chunk_local_cumsum(torch.randn(1, 64, 2))
 
 
-def test_backward_is_refused():
-    ctx = types.SimpleNamespace()
-    with pytest.raises(NotImplementedError):
-        kairos_gdn.ChunkGatedDeltaRuleFunction.backward(ctx, None, None)
+def test_backward_refuses_cpu_tensors_and_fp8():
+    q, k, v, g, b = cpu_inputs()
+    with pytest.raises(RuntimeError, match="HIP device only"):
+        kairos_gdn.chunk_gated_delta_rule_bwd(q, k, v, g, b, 0.125, None, torch.randn(1, 16, 2, 64), None)
+    lib = _lib.load()
+    x = 16
+    rc = lib.kairos_gdn_chunk_bwd(x, x, x, x, x, None, x, None, x, x, x, x, x, None, None, 0, 1, 64, 2, 64, 64,
+                                  _lib.F8E4M3, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, 0.125, 0, None, 0, None)
+    assert rc == _lib.EUNSUPPORTED and b"fp8" in lib.kairos_gdn_last_error()
+    rc = lib.kairos_gdn_chunk_bwd(x, x, x, x, x, None, x, None, x, x, x, x, x, None, None, 0, 1, 64, 2, 64, 48,
+                                  _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, 0.125, 0, None, 0, None)
+    assert rc == _lib.EUNSUPPORTED
+    rc = lib.kairos_gdn_chunk_bwd(x, x, x, x, x, None, x, None, x, x, x, x, x, x, None, 0, 1, 64, 2, 64, 64,
+                                  _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, 0.125, 0, None, 0, None)
+    assert rc == _lib.EINVAL and b"dh0" in lib.kairos_gdn_last_error()
+    assert lib.kairos_gdn_chunk_bwd_workspace_size(1, 64, 2, 64, 64, 0, _lib.BF16, _lib.BF16, 0) > 0
 
 
 # ---------------------------------------------------------------------------
