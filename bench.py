@@ -469,6 +469,67 @@ def bench_streaming(args, dev):
 
 
 # ---------------------------------------------------------------------------
+# backward (chunk.py:70-146 + the autograd backward, chunk.py:188-213)
+# ---------------------------------------------------------------------------
+def bwd_flops_per_tok_head(K, V):
+    """Algorithmic FLOPs of the reference backward per (token, head), every MMA tile at full size: w, u
+    recompute 2C(K+V); h recompute 4KV; dv_local 2C(K+V); dh recurrence 6KV; dq/dk/dw/dg 6KV + 6CK + 2CV;
+    WY backward 10CK + 4CV + 4C^2 -> 16KV + 20CK + 10CV + 4C^2."""
+    return 16 * K * V + 20 * C * K + 10 * C * V + 4 * C * C
+
+
+def bench_backward(args, dev):
+    """One step = one kairos_gdn_chunk_bwd call (the whole backward: recompute of the forward's
+    intermediates, dv_local, the dh recurrence, dq/dk/dw/dg and the WY backward) at BASELINE config 2,
+    or at the Kairos layer's head dims with --model-shape.  Algorithmic bytes: q, k, v, do read and
+    dq, dk, dv written once per token-head (7 x 2 B x d), g, beta read and dg, dbeta written, plus h0 and
+    dht read and dh0 written per (sequence, head)."""
+    from kairos_gdn import _lib
+    K, V = (256, 512) if args.model_shape else (128, 128)
+    B, T, H = 1, args.T, 20
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, device=dev)
+    gen = torch.Generator(device="cpu").manual_seed(20263)
+    do = torch.randn(B, T, H, V, generator=gen).to(dev, torch.bfloat16)
+    dht = torch.randn(B, H, K, V, generator=gen).to(dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    db = torch.empty_like(beta)
+    dh0 = torch.empty_like(h0)
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_bwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def step():
+        _lib.call("kairos_gdn_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(h0), P(do), P(dht), P(dq), P(dk), P(dv),
+                  P(dg), P(db), P(dh0), None, 0, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32,
+                  K ** -0.5, 0, P(ws), ws_bytes, sp)
+
+    timer = Timer(args)
+    res = timer.run(step)
+    wall = res["wall_s"]
+    med_s = res["step_ms"]["median"] / 1e3
+    tok_heads = B * T * H
+    # q, k, dq, dk (4 x K) and v, do, dv (3 x V) in bf16; g, dg fp32 and beta, dbeta bf16; h0, dht, dh0 fp32
+    alg = tok_heads * (2 * (4 * K + 3 * V) + 12) + B * H * 3 * K * V * 4
+    flops = tok_heads * bwd_flops_per_tok_head(K, V)
+    print(json.dumps({
+        "metric": f"GDN chunk-bwd tokens/s + TFLOP/s at T={T},H={H},dk={K},dv={V}", "value": B * T / wall,
+        "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"kairos_gdn_chunk_bwd B={B} T={T} H={H} dk={K} dv={V} chunk 64, bf16 q/k/v/beta/do, "
+                               "fp32 g/h0/dht, gradients of q, k, v, g, beta, h0; inputs in HBM",
+                   "workspace_bytes": ws_bytes},
+        **timer.fields(res),
+        "tflops": flops / wall / 1e12, "mfma_peak_frac": flops / wall / 1e12 / PEAK_BF16_TFLOPS,
+        "roofline": {"bound": "hbm", "kernel": "whole call (median step)", "achieved": alg / med_s / 1e9,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS,
+                     "alg_bytes": alg, "traffic": None},
+    }), flush=True)
+
+
+# ---------------------------------------------------------------------------
 # other rows of the path (each prints its own line)
 # ---------------------------------------------------------------------------
 def bench_epilogue(args, dev):
@@ -652,6 +713,9 @@ def main():
                     help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T")
     ap.add_argument("--recurrent", action="store_true",
                     help="measure the short-sequence mode's decoding step (8 streams x 1 token at dk=256, dv=512)")
+    ap.add_argument("--backward", action="store_true",
+                    help="measure the backward pass (kairos_gdn_chunk_bwd) at config 2's shape (--model-shape: the "
+                         "Kairos layer's dk=256, dv=512); prints its own JSON line")
     ap.add_argument("--prologue", action="store_true",
                     help="measure the layer prologue (causal conv + SiLU + q/k L2 norm, gates) at the model shape")
     args = ap.parse_args()
@@ -673,7 +737,9 @@ def main():
         return
 
     import kairos_gdn  # noqa: F401
-    if args.epilogue:
+    if args.backward:
+        bench_backward(args, dev)
+    elif args.epilogue:
         bench_epilogue(args, dev)
     elif args.model_shape:
         bench_model_shape(args, dev)
