@@ -108,6 +108,16 @@ size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void);
  * KAIROS_GDN_SEG_CHUNKS overrides it).  No counterpart in the reference. */
 int kairos_gdn_segment_chunks(int64_t B, int64_t T, int64_t H, int64_t n_seqs);
 
+/* The varlen maps every call builds on the device from cu_seqlens (exposed for
+ * testing and for callers that precompute them): chunk_off[n] = index of the
+ * first 64-token chunk of sequence n, chunk_off[n_seqs] = the chunk count --
+ * prepare_chunk_offsets(cu_seqlens, 64) (fla ops/utils/index.py:122-127) as
+ * int32 -- and seg_off[n] = index of the first segment of sequence n when
+ * sequences are cut into segments of seg_chunks chunks (no counterpart in the
+ * reference).  chunk_off, seg_off: device int32 [n_seqs + 1]. */
+int kairos_gdn_varlen_maps(const int64_t* cu_seqlens, int64_t n_seqs, int64_t seg_chunks, int32_t* chunk_off,
+                           int32_t* seg_off, void* stream);
+
 /* ---- backward ---------------------------------------------------------------
  * Gradients of the forward above: replaces ChunkGatedDeltaRuleFunction.backward
  * (chunk.py:188-213: chunk_gated_delta_rule_bwd, chunk.py:70-146, then the

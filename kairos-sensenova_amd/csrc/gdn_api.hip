@@ -355,9 +355,12 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0) return 0;
   const size_t tok = (size_t)(B * T * H);
   const int cdt = compute_dtype(qk_dtype, v_dtype);
-  size_t total = kgdn::seg_fwd_supported(cdt, (int)K, (int)V) ? seg_ws(B, T, H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
-                                                              : staged_ws(B, T, H, K, V, n_seqs, cdt);
-  if (use_qk_l2norm) total += 2 * align_up(tok * K * dt_size(qk_dtype));
+  const bool seg = kgdn::seg_fwd_supported(cdt, (int)K, (int)V);
+  size_t total = seg ? seg_ws(B, T, H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
+                     : staged_ws(B, T, H, K, V, n_seqs, cdt);
+  // in-op L2 norm: the fused path folds it into its kernels; the staged path normalises q and k in a
+  // pass of their own
+  if (use_qk_l2norm && !seg) total += 2 * align_up(tok * K * dt_size(qk_dtype));
   return total;
 }
 
@@ -402,8 +405,8 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
     if (use_qk_l2norm && any_tokens) {
       void* qn = cv.take(tok * K * dt_size(qk_dtype));
       void* kn = cv.take(tok * K * dt_size(qk_dtype));
-      if (int rc = from_launch(kgdn::launch_l2norm(q, qn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q)")) return rc;
-      if (int rc = from_launch(kgdn::launch_l2norm(k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(k)")) return rc;
+      if (int rc = from_launch(kgdn::launch_l2norm2(q, qn, k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q, k)"))
+        return rc;
       q = qn;
       k = kn;
     }
@@ -433,14 +436,6 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
     R = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
     s_init = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
   }
-  if (use_qk_l2norm && any_tokens) {
-    void* qn = cv.take(tok * K * dt_size(qk_dtype));
-    void* kn = cv.take(tok * K * dt_size(qk_dtype));
-    if (int rc = from_launch(kgdn::launch_l2norm(q, qn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q)")) return rc;
-    if (int rc = from_launch(kgdn::launch_l2norm(k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(k)")) return rc;
-    q = qn;
-    k = kn;
-  }
   if (P.ns > 0x7fffffff / 2) return fail(KAIROS_GDN_EINVAL, "%s: too many segments", what);
 
   kgdn::SegFwdArgs a{};
@@ -451,6 +446,7 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
   a.N = (int)G.N; a.T = T; a.H = (int)H; a.L = P.L; a.nseg_fixed = P.nseg_fixed; a.ns_grid = P.ns;
   a.M = M; a.R = R; a.s_init = s_init; a.scale = scale; a.o = o; a.ht = final_state;
   a.Ai = Ai; a.nc_grid = nc_grid;
+  a.l2 = use_qk_l2norm != 0;
   a.run_trans = P.trans && P.ns > 0;
   a.run_combine = P.combine;
   a.events = profile ? profile_events() : nullptr;
@@ -562,8 +558,8 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
     dq_k = cv.take(tok * K * es);
     dk_k = cv.take(tok * K * es);
     if (any_tokens) {
-      if (int rc = from_launch(kgdn::launch_l2norm(q, qn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q)")) return rc;
-      if (int rc = from_launch(kgdn::launch_l2norm(k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(k)")) return rc;
+      if (int rc = from_launch(kgdn::launch_l2norm2(q, qn, k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q, k)"))
+        return rc;
     }
     qx = qn;
     kx = kn;
@@ -596,6 +592,19 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
     if (int rc = from_launch(kgdn::launch_l2norm_bwd(k, dk_k, dk, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(k)"))
       return rc;
   }
+  return ok();
+}
+
+int kairos_gdn_varlen_maps(const int64_t* cu_seqlens, int64_t n_seqs, int64_t seg_chunks, int32_t* chunk_off,
+                           int32_t* seg_off, void* stream) {
+  const char* what = "kairos_gdn_varlen_maps";
+  if (n_seqs <= 0 || n_seqs > 0x7fffffff) return fail(KAIROS_GDN_EINVAL, "%s: n_seqs must be in [1, 2^31)", what);
+  if (seg_chunks <= 0 || seg_chunks > (1 << 20))
+    return fail(KAIROS_GDN_EINVAL, "%s: seg_chunks must be in [1, 2^20]", what);
+  if (!cu_seqlens || !chunk_off || !seg_off) return fail(KAIROS_GDN_EINVAL, "%s: null pointer", what);
+  if (int rc = from_launch(kgdn::launch_seg_map(cu_seqlens, (int)n_seqs, (int)seg_chunks, chunk_off, seg_off,
+                                                static_cast<hipStream_t>(stream)), what))
+    return rc;
   return ok();
 }
 

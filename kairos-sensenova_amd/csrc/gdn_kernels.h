@@ -112,6 +112,7 @@ struct SegFwdArgs {
   float* ht;              // out [N, H, K, V] or nullptr
   void* Ai;               // [nc_grid, H] chunk records of kSegRecordBytes (seg_prep -> seg_trans, seg_out)
   int64_t nc_grid;        // number of chunks (varlen: an upper bound)
+  bool l2;                // the in-op L2 norm of q and k (bf16 q/k), folded into the kernels
   bool run_trans;         // some sequence has more than one segment
   bool run_combine;       // ... or final_state of empty sequences is needed
   hipEvent_t* events;     // optional [5]: recorded before seg_prep, seg_trans, seg_combine, seg_out and after seg_out
@@ -167,6 +168,9 @@ bool seg_fwd_supported(int compute_dtype, int K, int V);
 int launch_seg_fwd(const SegFwdArgs& a, int compute_dtype, int qk_dtype, int K, int V, hipStream_t s);
 int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s);
 int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s);
+// the same for two tensors of equal shape in one launch (x1, y1 may be null)
+int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,
+                   hipStream_t s);
 
 // Gated RMSNorm (gdn_norm.hip): y = x rstd w [+ b] * act(g) per row of D.
 struct NormArgs {

@@ -1,5 +1,6 @@
 // Small kernels around the chunked GatedDeltaNet forward:
 //  * l2norm_kernel     y = x / sqrt(sum x^2 + 1e-6) per row (fla modules/l2norm.py:98-119),
+//                      q and k in one launch,
 //                      the optional q/k prologue of chunk.py:168-170;
 //  * chunk_off_kernel  per-sequence chunk offsets from cu_seqlens
 //                      (fla ops/utils/index.py:122-127), computed on the device so
@@ -13,18 +14,57 @@ namespace kgdn {
 
 namespace {
 
-// One wave per row; D <= 512, a multiple of 8.
+// Rows of D elements (a power of two, 8 <= D <= 512): a row takes LPR = D / 8 lanes
+// (8 elements, one 16-byte load each in bf16), so a wave normalises 64 / LPR rows
+// at once and every lane is busy; each thread handles RPT row groups, their loads
+// all issued before the first reduction.  Up to two tensors per launch
+// (blockIdx.y), each with its own rows.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void l2norm_kernel(const T* __restrict__ x0, T* __restrict__ y0,
+                                                     const T* __restrict__ x1, T* __restrict__ y1, int64_t rows) {
+  constexpr int LPR = D / 8, RPW = WAVE / LPR, RPT = 4;
+  const T* x = blockIdx.y ? x1 : x0;
+  T* y = blockIdx.y ? y1 : y0;
+  const int l = lane_id();
+  const int64_t wave = ((int64_t)blockIdx.x * 4 + threadIdx.x / WAVE) * RPT;
+  const int sub = l / LPR, col = 8 * (l % LPR);
+  Vec8<T> v[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int64_t row = (wave + i) * RPW + sub;
+    v[i] = row < rows ? ld8<T>(x + row * D + col) : vzero<T>();
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int64_t row = (wave + i) * RPW + sub;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = vget<T>(v[i], e);
+      ss = fmaf(f, f, ss);
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    const float rstd = 1.0f / sqrtf(ss + 1e-6f);
+    if (row < rows) {
+      Vec8<T> o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vset<T>(o, e, vget<T>(v[i], e) * rstd);
+      st8<T>(y + row * D + col, o);
+    }
+  }
+}
+
+// Rows of any D (a multiple of 8, at most 512): one wave per row.
 template <typename T>
-__global__ __launch_bounds__(256) void l2norm_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
-                                                     int D) {
+__global__ __launch_bounds__(256) void l2norm_wave_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
+                                                          int D) {
   const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / WAVE;
   if (row >= rows) return;
   const int l = lane_id();
-  const T* xr = x + row * D;
-  T* yr = y + row * D;
   Vec8<T> v = vzero<T>();
   const bool act = 8 * l < D;
-  if (act) v = ld8<T>(xr + 8 * l);
+  if (act) v = ld8<T>(x + row * D + 8 * l);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -38,7 +78,7 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const T* __restrict__ x, T*
     Vec8<T> o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) vset<T>(o, e, vget<T>(v, e) * rstd);
-    st8<T>(yr + 8 * l, o);
+    st8<T>(y + row * D + 8 * l, o);
   }
 }
 
@@ -70,19 +110,43 @@ __global__ __launch_bounds__(64) void cumsum_kernel(const void* g, int g_dtype, 
 
 }  // namespace
 
-int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s) {
-  if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
-  const dim3 grid((unsigned)((rows + 3) / 4));
-  if (dtype == DT_F32) {
-    hipLaunchKernelGGL(l2norm_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(x),
-                       static_cast<float*>(y), rows, D);
-  } else if (dtype == DT_BF16) {
-    hipLaunchKernelGGL(l2norm_kernel<bf16>, grid, dim3(256), 0, s, static_cast<const bf16*>(x),
-                       static_cast<bf16*>(y), rows, D);
-  } else {
-    return -2;
+template <typename T, int D>
+void launch_l2norm_t(const void* x0, void* y0, const void* x1, void* y1, int64_t rows, hipStream_t s) {
+  constexpr int64_t per_block = 4 * 4 * (WAVE / (D / 8));     // waves x row groups x rows per group
+  const dim3 grid((unsigned)((rows + per_block - 1) / per_block), x1 ? 2u : 1u);
+  hipLaunchKernelGGL((l2norm_kernel<T, D>), grid, dim3(256), 0, s, static_cast<const T*>(x0), static_cast<T*>(y0),
+                     static_cast<const T*>(x1), static_cast<T*>(y1), rows);
+}
+
+template <typename T>
+int launch_l2norm_dt(const void* x0, void* y0, const void* x1, void* y1, int64_t rows, int D, hipStream_t s) {
+  switch (D) {
+    case 64: launch_l2norm_t<T, 64>(x0, y0, x1, y1, rows, s); break;
+    case 128: launch_l2norm_t<T, 128>(x0, y0, x1, y1, rows, s); break;
+    case 256: launch_l2norm_t<T, 256>(x0, y0, x1, y1, rows, s); break;
+    case 512: launch_l2norm_t<T, 512>(x0, y0, x1, y1, rows, s); break;
+    default: {
+      const dim3 grid((unsigned)((rows + 3) / 4));
+      hipLaunchKernelGGL(l2norm_wave_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x0), static_cast<T*>(y0),
+                         rows, D);
+      if (x1)
+        hipLaunchKernelGGL(l2norm_wave_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x1),
+                           static_cast<T*>(y1), rows, D);
+    }
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,
+                   hipStream_t s) {
+  if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
+  if (dtype == DT_F32) return launch_l2norm_dt<float>(x0, y0, x1, y1, rows, D, s);
+  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x0, y0, x1, y1, rows, D, s);
+  return -2;
+}
+
+int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s) {
+  return launch_l2norm2(x, y, nullptr, nullptr, dtype, rows, D, s);
 }
 
 int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s) {

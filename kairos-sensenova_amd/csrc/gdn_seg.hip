@@ -390,6 +390,30 @@ __device__ __forceinline__ float dpp_plus(float v) {
   const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, false);
   return v + __int_as_float(s);
 }
+// 1 / sqrt(sum x^2 + 1e-6) of the in-op L2 norm (l2norm.py:115, eps 1e-6), by the hardware
+// reciprocal square root (within 1 ulp); seg_prep and seg_out use this one form, so both
+// normalise k to the same values.
+__device__ __forceinline__ float l2_rstd(float ss) { return __builtin_amdgcn_rsqf(ss + 1e-6f); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// acc + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs (v_dot2_f32_bf16, fp32 accumulate)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                         false);
+}
+
+// Sum over each group of G consecutive lanes (G = 8 or 16, groups aligned), every lane of a group
+// receiving it, with DPP moves (no LDS): quad swaps, then the half-row and row mirrors.
+template <int G>
+__device__ __forceinline__ float row_sum_dpp(float v) {
+  static_assert(G == 8 || G == 16, "row_sum_dpp sums groups of 8 or 16 lanes");
+  v = dpp_plus<0xB1, 0xf>(v);       // quad_perm [1, 0, 3, 2]
+  v = dpp_plus<0x4E, 0xf>(v);       // quad_perm [2, 3, 0, 1]
+  v = dpp_plus<0x141, 0xf>(v);      // row_half_mirror: the other quad of the 8
+  if constexpr (G == 16) v = dpp_plus<0x140, 0xf>(v);   // row_mirror: the other 8 of the row
+  return v;
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave with DPP moves (no LDS):
 // shifts by 1, 2, 4, 8 within each row of 16 lanes, then row_bcast:15 and
 // row_bcast:31 carry the row totals into the rows above.
@@ -436,6 +460,7 @@ struct SegPrepArgs {
   int g_dtype, beta_dtype;
   float scale;                // output scale (the record's exp(gc) * scale vector)
   unsigned char* rec;         // out [chunks, H] records of kSegRecordBytes (see gdn_kernels.h)
+  int l2;                     // in-op L2 norm of k (bf16 k): normalise the rows and record rstd
 };
 
 // One (chunk, head) item of seg_prep: item = chunk * H + head.
@@ -539,6 +564,30 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
 #pragma unroll
     for (int ks = 0; ks < K / 32; ++ks) kf[rt][ks] = k_frag<TQ, K>(row, ks, kscale);
   }
+  // in-op L2 norm of k (chunk.py:168-170, l2norm.py:98-119): y = bf16(k / sqrt(sum k^2 + 1e-6)) per
+  // row; a row is spread over the four lane groups, so two shuffles complete its sum.  K.K^T uses
+  // the normalised rows; the record carries rstd for the two serial kernels, which read raw k.
+  float rs_own = 1.f;                                    // rstd of token lane (row 16 lg + lc)
+  if constexpr (sizeof(TQ) == 2) {
+    if (a.l2) {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf((float)kf[rt][ks].v[e], (float)kf[rt][ks].v[e], ss);
+        ss += __shfl_xor(ss, 16, WAVE);
+        ss += __shfl_xor(ss, 32, WAVE);
+        const float rs = l2_rstd(ss);
+        if (rt == lg) rs_own = rs;
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kf[rt][ks].v[e] = (bf16)((float)kf[rt][ks].v[e] * rs);
+      }
+    }
+  }
 
   // chunk vectors of the record (lane = token)
   unsigned char* rec = a.rec + (it.ci * H + it.h) * (int64_t)kSegRecordBytes;
@@ -559,8 +608,10 @@ __global__ __launch_bounds__(PrepLds::WAVES * WAVE) void seg_prep_kernel(SegPrep
     vec[3 * C + l] = l < it.nv ? gexp(gl - gc) : 0.f;
     vec[4 * C + l] = b;
     vec[5 * C + l] = gexp(gl);
-    vec[6 * C + l] = 0.f;
-    vec[7 * C + l] = 0.f;
+    // with the in-op L2 norm: rstd of k, and the update gate times it (seg_trans folds the
+    // normalisation of k into its w operand and its gated v')
+    vec[6 * C + l] = a.l2 ? rs_own : 0.f;
+    vec[7 * C + l] = a.l2 && l < it.nv ? gexp(gl - gc) * rs_own : 0.f;
   }
 
   // A: ten 16x16 tiles; lane element (jj): i = 16 tm + 4 lg + jj, j = 16 tn + lc
@@ -915,7 +966,8 @@ __device__ __forceinline__ Frag<bf16> scale_frag(const Frag<bf16>& f, const floa
 // The w operand of wy_fast.py:74-78 for the 8 tokens of fragment f (K order as
 // in scale_frag): bf16(bf16(k beta) exp(gc)).  k beta is a bf16 product (exact
 // in fp32, rounded once), then scaled by exp(gc) in fp32 and rounded again.
-__device__ __forceinline__ Frag<bf16> kb_frag(const Frag<bf16>& f, const float* beta, const float* eg, int ks) {
+__device__ __forceinline__ Frag<bf16> kb_frag(const Frag<bf16>& f, const float* beta, const float* eg, int ks,
+                                              const float* rk = nullptr) {
   const int lg = lane_id() >> 4;
   const f32x4 b0 = *reinterpret_cast<const f32x4*>(beta + 32 * ks + 4 * lg);
   const f32x4 b1 = *reinterpret_cast<const f32x4*>(beta + 32 * ks + 16 + 4 * lg);
@@ -923,6 +975,21 @@ __device__ __forceinline__ Frag<bf16> kb_frag(const Frag<bf16>& f, const float* 
   const f32x4 e1 = *reinterpret_cast<const f32x4*>(eg + 32 * ks + 16 + 4 * lg);
   float y[8];
   frag_unpack(f, y);
+  if (rk != nullptr) {                                   // the in-op L2 norm: y = bf16(k rstd) first
+    const f32x4 r0 = *reinterpret_cast<const f32x4*>(rk + 32 * ks + 4 * lg);
+    const f32x4 r1 = *reinterpret_cast<const f32x4*>(rk + 32 * ks + 16 + 4 * lg);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y[e] *= r0[e];
+      y[4 + e] *= r1[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const uint32_t r = cvt_pk_bf16(y[e], y[e + 1]);
+      y[e] = bf16_lo(r);
+      y[e + 1] = bf16_hi(r);
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     y[e] *= b0[e];
@@ -1115,6 +1182,7 @@ struct SegOutArgs {
   float scale;
   void* o;                    // [B*T, H, V]
   float* ht;                  // [N, H, K, V] or nullptr
+  int l2;                     // normalise q and k rows on their way to LDS (the in-op L2 norm)
 };
 
 template <typename TQ, int K, int V>
@@ -1201,13 +1269,34 @@ struct ProdStage {
 #pragma unroll
     for (int i = 0; i < N; ++i) q[i] = *reinterpret_cast<const QT*>(s.q + src_off(i, s.nv, H));
   }
-  __device__ __forceinline__ void store_k(unsigned char* smem, int kb, float ks) const {
+  __device__ __forceinline__ void store_k(unsigned char* smem, int kb, float ks, bool l2) const {
 #pragma unroll
-    for (int i = 0; i < N; ++i) *reinterpret_cast<u32x4*>(smem + P::k_tile(kb) + dst_off(i)) = to_bf16(k[i], ks);
+    for (int i = 0; i < N; ++i) {
+      u32x4 x = to_bf16(k[i], ks);
+      if (l2) x = l2_row(x);
+      *reinterpret_cast<u32x4*>(smem + P::k_tile(kb) + dst_off(i)) = x;
+    }
   }
-  __device__ __forceinline__ void store_q(unsigned char* smem, int qb, float qs) const {
+  // y = bf16(x / sqrt(sum x^2 + 1e-6)) over the row a unit belongs to: the K / 8 units of a row are
+  // held by K / 8 consecutive lanes (l2norm.py:98-119, the in-op L2 norm of q and k).  The squares
+  // are summed by packed bf16 dot products on the raw words, the row by DPP moves.
+  __device__ __forceinline__ static u32x4 l2_row(const u32x4& x) {
+    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < N; ++i) *reinterpret_cast<u32x4*>(smem + P::q_tile(qb) + dst_off(i)) = to_bf16(q[i], qs);
+    for (int e = 0; e < 4; ++e) ss = dot2_bf16(x[e], x[e], ss);
+    const float rs = l2_rstd(row_sum_dpp<K / 8>(ss));
+    u32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = cvt_pk_bf16(__uint_as_float(x[e] << 16) * rs, __uint_as_float(x[e] & 0xffff0000u) * rs);
+    return y;
+  }
+  __device__ __forceinline__ void store_q(unsigned char* smem, int qb, float qs, bool l2) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      u32x4 x = to_bf16(q[i], qs);
+      if (l2) x = l2_row(x);
+      *reinterpret_cast<u32x4*>(smem + P::q_tile(qb) + dst_off(i)) = x;
+    }
   }
 };
 
@@ -1477,8 +1566,8 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     const SRC s0(a, t_seg, chunk_nv(0), h, H, rec0);
     ps.load_q(s0, H);
     ps.load_k(s0, H);
-    ps.store_q(smem, 0, qs);
-    ps.store_k(smem, 0, ks_);
+    ps.store_q(smem, 0, qs, a.l2 != 0);
+    ps.store_k(smem, 0, ks_, a.l2 != 0);
     if (sl.nch > 1) {
       const SRC s1(a, t_seg + C, chunk_nv(1), h, H, rec0 + rec_step);
       ps.load_q(s1, H);
@@ -1496,7 +1585,7 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
       // producers: w and u of chunk c + 1; k of chunk c + 2 goes to a buffer
       // free in this half, then the loads of k of chunk c + 3
       if (c + 2 < sl.nch) {
-        ps.store_k(smem, (c + 2) % 3, ks_);
+        ps.store_k(smem, (c + 2) % 3, ks_, a.l2 != 0);
         if (c + 3 < sl.nch) ps.load_k(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
       }
       if (c + 1 < sl.nch) {
@@ -1582,7 +1671,7 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
         }
       }
       if (c + 2 < sl.nch) {
-        ps.store_q(smem, (c + 2) & 1, qs);
+        ps.store_q(smem, (c + 2) & 1, qs, a.l2 != 0);
         if (c + 3 < sl.nch) ps.load_q(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
       }
       lds_barrier();                                     // B1
@@ -1611,6 +1700,7 @@ struct SegTransArgs {
   const void* Ai;             // [chunks, H] chunk records from seg_prep
   uint16_t* M;                // [NS, H] blocks of K x K bf16 M_hi then M_lo
   float* R;                   // [NS, H] blocks of K x V in accumulator-tile order (see seg_combine)
+  int l2;                     // k is raw and the record carries its rstd (the in-op L2 norm)
 };
 
 template <typename TQ, int K, int V>
@@ -1884,8 +1974,9 @@ __global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_kernel(SegTra
       if (KT % NW != 0 && wid + NW * r >= KT) break;   // uniform per wave
       Frag<bf16> k0, k1;
       tr4<0, 32 * K, 64 * K, 96 * K>(ktr_w[r] + P::k_tile(b), k0, k1);
-      const Frag<bf16> kb0 = kb_frag(k0, vec + 4 * C, vec + 2 * C, 0);
-      const Frag<bf16> kb1 = kb_frag(k1, vec + 4 * C, vec + 2 * C, 1);
+      const float* rk = a.l2 ? vec + 6 * C : nullptr;
+      const Frag<bf16> kb0 = kb_frag(k0, vec + 4 * C, vec + 2 * C, 0, rk);
+      const Frag<bf16> kb1 = kb_frag(k1, vec + 4 * C, vec + 2 * C, 1, rk);
       unsigned char* wt = smem + P::w_tile(cn & 1) + wst[r];
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
@@ -1962,7 +2053,9 @@ __global__ __launch_bounds__((TransPlan<K, V>::NT)) void seg_trans_kernel(SegTra
     // X = exp(gc_last) X + k^T (v' gate)
     const float gamma = vec[5 * C];
     Frag<bf16> vg[2][CT];
-    gate_frags<CT>(Y, vec + 3 * C, vg);
+    // with the in-op L2 norm the update reads raw k: its rstd rides on the gated v' (gate * rstd,
+    // one rounding per element, as the gated v' itself has)
+    gate_frags<CT>(Y, vec + (a.l2 ? 7 : 3) * C, vg);
     const uint32_t kbo = P::k_tile(b);
 #pragma unroll
     for (int tq = 0; tq < KT; tq += 4) {
@@ -2215,7 +2308,8 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   if (p.ns_grid > 0 && p.nc_grid > 0) {
     constexpr size_t lds = PrepLds::total;
     static_assert(lds <= 64 * 1024, "seg_prep tiles exceed the default LDS limit");
-    SegPrepArgs pa{p.k, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, p.scale, static_cast<unsigned char*>(p.Ai)};
+    SegPrepArgs pa{p.k, p.g, p.beta, p.k_scale, p.g_dtype, p.beta_dtype, p.scale, static_cast<unsigned char*>(p.Ai),
+                   p.l2 ? 1 : 0};
     const dim3 pgrid((unsigned)((p.nc_grid * p.H + PrepLds::WAVES - 1) / PrepLds::WAVES));
     const dim3 pblock(PrepLds::WAVES * WAVE);
     if (p.cu != nullptr)
@@ -2227,7 +2321,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   if (!mark(1)) return -1;
   if (p.run_trans) {
     constexpr size_t lds = Eng<TQ, K, V>::total;
-    SegTransArgs ta{p.k, p.v, p.k_scale, Ai, p.M, p.R};
+    SegTransArgs ta{p.k, p.v, p.k_scale, Ai, p.M, p.R, p.l2 ? 1 : 0};
     if constexpr (sizeof(TQ) == 2) {
       constexpr size_t lds_p = TransPlan<K, V>::total;
       auto kt = seg_trans_kernel<K, V>;
@@ -2254,7 +2348,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     auto ko = seg_out_kernel<TQ, K, V>;
     if (set_lds(ko, lds)) return -1;
     SegOutArgs oa{p.q, p.k, p.v, p.q_scale, p.k_scale,
-                  p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht};
+                  p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht, p.l2 ? 1 : 0};
     hipLaunchKernelGGL(ko, grid, dim3(OutPlan<TQ, K, V>::NT), lds, s, oa, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }

@@ -54,6 +54,7 @@ SIGNATURES = {
                                           _p]),
     "kairos_gdn_gates_fwd": (_i, [_p, _p, _p, _p, _fp, _p, _i64, _i64, _i, _i, _i, _i, _p]),
     "kairos_gdn_segment_chunks": (_i, [_i64, _i64, _i64, _i64]),
+    "kairos_gdn_varlen_maps": (_i, [_p, _i64, _i64, _p, _p, _p]),
     "kairos_gdn_profile_begin": (_i, []),
     "kairos_gdn_profile_end": (_i, [ctypes.POINTER(ctypes.c_double), _i]),
 }

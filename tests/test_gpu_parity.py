@@ -230,6 +230,9 @@ EDGE_CASES = [
     ("bf16", 1, 1300, 2, 256, 512, None, False, True),
     ("fp32", 1, 200, 1, 256, 256, None, False, True),
     ("bf16", 2, 150, 2, 128, 48, None, False, True),
+    # the in-op L2 norm on the fused path at K = 64 (8 lanes per row) with ragged varlen chunks
+    ("bf16", 1, 700, 3, 64, 128, [0, 1, 1, 129, 640, 700], True, True),
+    ("bf16", 2, 333, 2, 128, 64, None, True, False),
 ]
 
 
@@ -282,22 +285,50 @@ def test_baseline_config(cfg):
         assert rel(host(o), on) < 1e-4 and rel(host(ht), hn) < 1e-4
 
 
-@pytest.mark.parametrize("cfg,heads", [(2, [0, 9, 19]), (3, [3, 16])])
-def test_baseline_config_full_size(cfg, heads):
+@pytest.mark.parametrize("cfg,l2", [(2, False), (3, False), (2, True)])
+def test_baseline_config_full_size(cfg, l2):
+    """Configs 2 and 3 at full size, every head against the oracle; config 2 also in the layer's own mode,
+    use_qk_l2norm_in_kernel=True on unnormalised q, k."""
     c = CONFIGS[cfg]
-    note(f"config {cfg} (oracle on heads {heads})")
+    note(f"config {cfg}, all heads, l2={l2}")
     cu = c.get("cu")
     x = make_inputs(c["B"], c["T"], c["H"], c["K"], c["V"], seed=20260 + cfg, dtype=c["dtype"],
                     n_states=len(cu) - 1 if cu else None)
-    o, ht = run_gpu(x, c["dtype"], cu=cu)
+    if l2:
+        x["q"] = O.cast(x["q"] * 3.0, c["dtype"])
+        x["k"] = O.cast(x["k"] * 0.5, c["dtype"])
+    o, ht = run_gpu(x, c["dtype"], cu=cu, l2=l2)
     assert bool(torch.isfinite(o).all()) and bool(torch.isfinite(ht).all())
-    check_against_oracle(x, c["dtype"], o, ht, cu=cu, heads=heads)
+    check_against_oracle(x, c["dtype"], o, ht, cu=cu, l2=l2)
+
+
+def test_varlen_maps_bit_exact():
+    """The device-built varlen maps: chunk offsets == prepare_chunk_offsets(cu_seqlens, 64)
+    (index.py:122-127) and segment offsets == the cumulative ceil(chunks / L), bit for bit, with empty
+    and 1-token sequences and lengths at chunk boundaries."""
+    lib = kairos_gdn._lib.load()
+    rng = np.random.default_rng(7)
+    lens = [0, 1, 63, 64, 65, 0, 128, 129, 1, 0, 4095, 4096, 4097, 640, 7]
+    lens += [int(x) for x in rng.integers(0, 3000, 40)]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    N = len(lens)
+    nch = (np.array(lens) + 63) // 64
+    for L in (1, 3, 43, 100000):
+        cu_t = torch.from_numpy(cu).to("cuda")
+        co = torch.full((N + 1,), -1, dtype=torch.int32, device="cuda")
+        so = torch.full((N + 1,), -1, dtype=torch.int32, device="cuda")
+        kairos_gdn._lib.check("kairos_gdn_varlen_maps",
+                              lib.kairos_gdn_varlen_maps(cu_t.data_ptr(), N, L, co.data_ptr(), so.data_ptr(),
+                                                         torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(co.cpu().numpy(), np.concatenate([[0], np.cumsum(nch)]))
+        np.testing.assert_array_equal(so.cpu().numpy(), np.concatenate([[0], np.cumsum((nch + L - 1) // L)]))
 
 
 def test_model_shape_full_size():
     """The Kairos 4B layer at the headline clip length: H=20, K=256, V=512, T=32760, bf16."""
     B, T, H, K, V = 1, 32760, 20, 256, 512
-    heads = [0, 19]
+    heads = [0, 5, 10, 15, 19]
     note(f"model shape B={B} T={T} H={H} K={K} V={V} (oracle on heads {heads})")
     x = make_inputs(B, T, H, K, V, seed=20270, dtype="bf16")
     o, ht = run_gpu(x, "bf16")
@@ -423,11 +454,12 @@ def test_fp8_qk_model_head_dims():
 def test_streaming_fp8_rollout():
     B, H, K, V, Tf, frames = 8, 20, 128, 128, 1560, 21
     note(f"config 4: B={B} H={H} {frames} calls of T={Tf}, fp8 q/k")
-    heads = [0, 13]
-    check_frames = {0, 10, 20}
+    heads = list(range(H))                    # every head on every 5th frame
+    check_frames = {0, 5, 10, 15, 20}
+    dheads = [0, 13]                          # end-state drift (the fp32 single call over all frames)
     h0 = (0.02 * np.random.default_rng(20264).standard_normal((B, H, K, V))).astype(np.float32)
     state = dev(h0)
-    S_in = h0[:, heads]
+    S_in = h0[:, dheads]
     parts = []
     for f in range(frames):
         x = make_inputs(B, Tf, H, K, V, seed=(20264, f), dtype="bf16", h0_scale=0.0)
@@ -438,7 +470,7 @@ def test_streaming_fp8_rollout():
         d = to_dev(x, "bf16")
         o, new_state = kairos_gdn.chunk_gated_delta_rule(q8, k8, d["v"], d["g"], d["beta"], initial_state=state,
                                                          output_final_state=True, q_scale=dev(qs), k_scale=dev(ks))
-        parts.append({k_: x[k_][:, :, heads] for k_ in ("q", "k", "v", "g", "beta")})
+        parts.append({k_: x[k_][:, :, dheads] for k_ in ("q", "k", "v", "g", "beta")})
         if f in check_frames:
             torch.cuda.synchronize()
             assert o.dtype == torch.bfloat16
@@ -457,6 +489,6 @@ def test_streaming_fp8_rollout():
     cat = {k_: np.concatenate([p_[k_] for p_ in parts], axis=1) for k_ in parts[0]}
     _, h_single = O.chunk_gated_delta_rule(cat["q"], cat["k"], cat["v"], cat["g"], cat["beta"],
                                            initial_state=S_in, output_final_state=True, dtype="fp32")
-    drift = rel(host(state)[:, heads], h_single)
+    drift = rel(host(state)[:, dheads], h_single)
     note(f"    end-state drift vs single-call fp32 (unquantised q/k): {drift:.3e}")
     assert math.isfinite(drift) and drift < 0.1

@@ -193,4 +193,12 @@ def test_gpu_gates(bdt):
         g_r, b_r = O.gdn_gates(a, b, A_log, dt, allow_neg_eigval=neg, b_dtype=bdt)
         assert g.dtype == torch.float32 and beta.dtype == tdt
         assert rel(g.cpu().numpy(), g_r) < 1e-5
-        assert rel(beta.float().cpu().numpy(), b_r) < (1e-2 if bdt == "bf16" else 1e-6)
+        got = beta.float().cpu().numpy()
+        if bdt == "bf16":
+            # beta = sigmoid(b) rounded once to bf16: at most one bf16 ulp of the oracle's rounding, and
+            # bitwise equal but for the rare values whose fp32 sigmoid sits at a rounding boundary
+            ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(b_r), 1e-30))) - 7)
+            assert (np.abs(got - b_r) <= ulp).all()
+            assert (got == b_r).mean() > 0.99
+        else:
+            assert rel(got, b_r) < 1e-6
