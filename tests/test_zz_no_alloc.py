@@ -68,7 +68,7 @@ def test_noalloc_refuses_problems_beyond_the_static_array():
     lib = _lib.load()
     cap = lib.kairos_gdn_chunk_fwd_noalloc_max_bytes()
     assert cap == 256 << 20
-    B, T, H, K, V = 1, 32760, 20, 128, 128
+    B, T, H, K, V = 1, 8 * 32760, 20, 128, 128
     assert lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 1) > cap
     x = 16  # any 16-byte aligned non-null address: the size check fails before anything is dereferenced
     rc = lib.kairos_gdn_chunk_fwd_noalloc(x, x, x, x, x, None, None, None, x, None, None, 0, B, T, H, K, V,
