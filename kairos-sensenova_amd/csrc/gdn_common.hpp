@@ -44,18 +44,16 @@ template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf
 // Round a float to the storage precision T and back (identity for float).
 template <typename T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
 
-// OCP fp8 e4m3 ("fn") code -> float, exact: sign, 4-bit exponent (bias 7),
-// 3-bit mantissa, subnormals at exponent 0, code 0x7f/0xff is NaN.
-__device__ __forceinline__ float fp8e4m3_to_f32(uint8_t c) {
-  const uint32_t e = (c >> 3) & 0xF, m = c & 0x7;
-  float mag;
-  if (e == 0) {
-    mag = (float)m * (1.0f / 512.0f);                // m/8 * 2^-6
-  } else {
-    mag = __uint_as_float(((e + 120u) << 23) | (m << 20));  // (1 + m/8) * 2^(e-7)
-  }
-  if (e == 15 && m == 7) mag = __uint_as_float(0x7fc00000u);
-  return (c & 0x80) ? -mag : mag;
+// Four OCP fp8 e4m3 ("fn") codes packed in a dword (byte i = element i) -> four floats, exact.
+// gfx950 decodes the OCP format in hardware, two codes per v_cvt_pk_f32_fp8 (sign, 4-bit exponent of
+// bias 7, 3-bit mantissa, subnormals at exponent 0, 0x7f / 0xff NaN).
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float out[4]) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);    // bytes 0, 1
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);     // bytes 2, 3
+  out[0] = lo[0];
+  out[1] = lo[1];
+  out[2] = hi[0];
+  out[3] = hi[1];
 }
 
 // exp(x) via the native base-2 exponential (v_exp_f32): exp(x) = 2^(x*log2(e)).
@@ -198,10 +196,10 @@ template <typename TK>
 __device__ __forceinline__ void load8_in(const TK* p, float scale, float out[8]) {
   if constexpr (sizeof(TK) == 1) {
     const uint2 raw = *reinterpret_cast<const uint2*>(p);
+    fp8x4_to_f32(raw.x, out);
+    fp8x4_to_f32(raw.y, out + 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) out[e] = fp8e4m3_to_f32((raw.x >> (8 * e)) & 0xFF) * scale;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) out[4 + e] = fp8e4m3_to_f32((raw.y >> (8 * e)) & 0xFF) * scale;
+    for (int e = 0; e < 8; ++e) out[e] *= scale;
   } else {
     const Vec8<TK> x = ld8<TK>(p);
 #pragma unroll

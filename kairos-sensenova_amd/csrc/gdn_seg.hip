@@ -364,11 +364,10 @@ __device__ __forceinline__ void convert_fp8(const unsigned char* raw, bf16* t, f
     const uint32_t lo = *reinterpret_cast<const uint32_t*>(blk + 4 * l);
     const uint32_t hi = *reinterpret_cast<const uint32_t*>(blk + WAVE * 4 + 4 * l);
     float x[8];
+    fp8x4_to_f32(lo, x);
+    fp8x4_to_f32(hi, x + 4);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      x[e] = r < nv ? fp8e4m3_to_f32((lo >> (8 * e)) & 0xFF) * scale : 0.f;
-      x[4 + e] = r < nv ? fp8e4m3_to_f32((hi >> (8 * e)) & 0xFF) * scale : 0.f;
-    }
+    for (int e = 0; e < 8; ++e) x[e] = r < nv ? x[e] * scale : 0.f;
     *reinterpret_cast<Frag<bf16>*>(t + Tile<NC>::off(r, c8)) = frag_pack(x);
   }
 }
@@ -1251,11 +1250,10 @@ struct ProdStage {
   __device__ __forceinline__ static u32x4 to_bf16(const QT& x, float scale) {
     if constexpr (P::FP8) {
       float f[8];
+      fp8x4_to_f32(x[0], f);
+      fp8x4_to_f32(x[1], f + 4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        f[e] = fp8e4m3_to_f32((x[0] >> (8 * e)) & 0xFF) * scale;
-        f[4 + e] = fp8e4m3_to_f32((x[1] >> (8 * e)) & 0xFF) * scale;
-      }
+      for (int e = 0; e < 8; ++e) f[e] *= scale;
       return __builtin_bit_cast(u32x4, frag_pack(f).v);
     } else {
       return x;

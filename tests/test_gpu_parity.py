@@ -429,6 +429,29 @@ def dequant_bf16(codes, scale):
 
 
 @pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
+def test_fp8_decode_every_code():
+    """Every finite e4m3 code through the fused path: with g = 0, beta = 0, h0 = I and scale = 1 the
+    output is q itself, o[t][d] = q[t][d], so o (bf16, exact for e4m3 values) must equal the decoded
+    codes bit for bit (oracle fp8_e4m3_decode).  NaN codes (0x7f, 0xff) are replaced by 0: one NaN
+    would reach every column through the 0 * NaN products of q h."""
+    note("fp8 e4m3: every code decoded exactly")
+    codes = np.arange(256, dtype=np.uint8).reshape(1, 2, 1, 128)
+    codes[(codes & 0x7f) == 0x7f] = 0
+    B, T, H, K, V = 1, 2, 1, 128, 128
+    q8 = torch.from_numpy(codes).to("cuda").view(torch.float8_e4m3fn)
+    k8 = torch.zeros(B, T, H, K, dtype=torch.uint8, device="cuda").view(torch.float8_e4m3fn)
+    v = torch.randn(B, T, H, V, device="cuda").to(torch.bfloat16)
+    g = torch.zeros(B, T, H, device="cuda")
+    beta = torch.zeros(B, T, H, device="cuda", dtype=torch.bfloat16)
+    h0 = torch.eye(K, device="cuda").reshape(1, 1, K, V)
+    one = torch.ones(H, device="cuda")
+    o, _ = kairos_gdn.chunk_gated_delta_rule(q8, k8, v, g, beta, scale=1.0, initial_state=h0,
+                                             output_final_state=True, q_scale=one, k_scale=one)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(o).reshape(2, 128), O.fp8_e4m3_decode(codes).reshape(2, 128))
+
+
+@pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
 def test_fp8_qk_model_head_dims():
     """fp8 q/k at dk=256, dv=512 (the fused recurrence + output of the stage path), varlen."""
     B, T, H, K, V = 1, 300, 2, 256, 512
