@@ -240,14 +240,36 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
   return total;
 }
 
+// The backward's segment scan (bf16, K and V in {64, 128}, more than one segment somewhere): the
+// recomputed states and the dh recurrence run per segment of the forward's plan, from the states a
+// scan over segments supplies (the forward's segment maps M_j and, in reverse, their transposes), so
+// the serial chains are L chunks long instead of a whole sequence.  KAIROS_GDN_BWD_SEG=0 keeps the
+// sequence-long recurrences.
+bool bwd_segmented(int cdt, int64_t K, int64_t V, const SegPlan& P) {
+  if (!kgdn::seg_fwd_supported(cdt, (int)K, (int)V) || !P.trans || P.ns <= 0) return false;
+  const char* e = std::getenv("KAIROS_GDN_BWD_SEG");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
 // Workspace of the backward: the recomputed forward (gc, w, u, Ai, h, v_new) and the
 // backward's own intermediates (dv_local, dh, dv2, -dw, dk of the dq/dk stage, dg before the
-// cumsum), plus the normalised q, k and their pre-norm gradients with the in-op L2 norm.
+// cumsum), plus the normalised q, k and their pre-norm gradients with the in-op L2 norm.  The
+// segment scan adds the forward's chunk records and segment maps and states, and the segments'
+// token and chunk offsets.
 size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, int use_l2) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
   const size_t tok = (size_t)(B * T * H);
   size_t total = stage_ws(n_seqs);
+  const SegPlan P = plan_segments(B, T, H, n_seqs);
+  if (bwd_segmented(cdt, K, V, P)) {
+    total += stage_ws(n_seqs);                                     // seg_off
+    total += align_up(nc * H * kgdn::kSegRecordBytes);            // chunk records
+    const size_t blocks = (size_t)P.ns * H;
+    total += align_up(blocks * K * K * sizeof(float));            // M (bf16 hi, lo)
+    total += 2 * align_up(blocks * K * V * sizeof(float));        // R, then F; s_init, then B
+    total += align_up((P.ns + 1) * sizeof(int64_t)) + align_up((P.ns + 1) * sizeof(int32_t));
+  }
   total += 2 * align_up(tok * sizeof(float));            // gc, dg1
   total += 3 * align_up(tok * K * es);                   // w, -dw, dk1
   total += align_up(nc * H * V * kgdn::C * es);          // uT
@@ -534,8 +556,20 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(B * T * H);
   Carver cv{static_cast<char*>(workspace)};
+  const SegPlan P = plan_segments(B, T, H, n_seqs);
+  const bool segb = any_tokens && bwd_segmented(cdt, K, V, P);
+  if (segb && P.ns > 0x7fffffff / 2) return fail(KAIROS_GDN_EINVAL, "%s: too many segments", what);
   const int32_t* chunk_off = nullptr;
-  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  const int32_t* seg_off = nullptr;
+  if (segb && G.varlen) {
+    int32_t* co = static_cast<int32_t*>(cv.take(sizeof(int32_t) * (G.N + 1)));
+    int32_t* so = static_cast<int32_t*>(cv.take(sizeof(int32_t) * (G.N + 1)));
+    if (int rc = from_launch(kgdn::launch_seg_map(cu_seqlens, (int)G.N, P.L, co, so, s), "segment map")) return rc;
+    chunk_off = co;
+    seg_off = so;
+  } else if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) {
+    return rc;
+  }
   float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
   float* dg1 = static_cast<float*>(cv.take(tok * sizeof(float)));
   void* w = cv.take(tok * K * es);
@@ -572,20 +606,84 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = T; pa.H = (int)H;
     pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = Ai;
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "prepare")) return rc;
-    kgdn::FwdHArgs ha{};
-    ha.k = kx; ha.k_scale = nullptr; ha.w = w; ha.uT = uT; ha.gc = gc;
-    ha.h0 = initial_state; ha.h0_dtype = h0_dtype;
-    ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = N; ha.T = T; ha.H = (int)H;
-    ha.hT = hs; ha.vnT = vn; ha.ht = nullptr; ha.row_major = true;
-    if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h (recompute)")) return rc;
   }
+  kgdn::FwdHArgs ha{};
+  ha.k = kx; ha.k_scale = nullptr; ha.w = w; ha.uT = uT; ha.gc = gc;
+  ha.h0 = initial_state; ha.h0_dtype = h0_dtype;
+  ha.cu = cu_seqlens; ha.chunk_off = chunk_off; ha.N = N; ha.T = T; ha.H = (int)H;
+  ha.hT = hs; ha.vnT = vn; ha.ht = nullptr; ha.row_major = true;
   kgdn::BwdArgs ba{};
   ba.q = qx; ba.k = kx; ba.v = v; ba.gc = gc; ba.beta = beta; ba.beta_dtype = beta_dtype;
   ba.do_ = do_; ba.dht = dht; ba.w = w; ba.Ai = Ai; ba.h = hs; ba.vn = vn;
   ba.dvl = dvl; ba.dh = dhs; ba.dv2 = dv2; ba.dw = dwb; ba.dk1 = dk1; ba.dg1 = dg1;
   ba.dq = dq_k; ba.dk = dk_k; ba.dv = dv; ba.dg = dg; ba.db = dbeta; ba.dh0 = dh0;
   ba.cu = cu_seqlens; ba.chunk_off = chunk_off; ba.N = N; ba.T = T; ba.H = (int)H; ba.scale = scale;
-  if (int rc = from_launch(kgdn::launch_bwd(ba, cdt, (int)K, (int)V, any_tokens ? G.nc : 0, s), what)) return rc;
+  const int64_t nc_b = any_tokens ? G.nc : 0;
+  if (!segb) {
+    if (G.nc > 0 && any_tokens) {
+      if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h (recompute)"))
+        return rc;
+    }
+    if (int rc = from_launch(kgdn::launch_bwd(ba, cdt, (int)K, (int)V, nc_b, kgdn::BWD_ALL, s), what)) return rc;
+  } else {
+    // Segment scan.  The forward's segment kernels (prep, trans, combine) give each segment's start
+    // state; h and v_new are recomputed per segment from it.  dh: pass 1 runs each segment's
+    // recurrence from zero (its dh at the segment start, B_j), a reverse scan with the transposed
+    // segment maps turns these into the dh each segment ends with, and pass 2 reruns the segments
+    // from there, writing the dh snapshots and dv2 the gradient kernels read.
+    const size_t blocks = (size_t)P.ns * H;
+    void* rec = cv.take((size_t)G.nc * H * kgdn::kSegRecordBytes);
+    uint16_t* M = static_cast<uint16_t*>(cv.take(blocks * 2 * K * K * sizeof(uint16_t)));
+    float* R = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
+    float* s_init = static_cast<float*>(cv.take(blocks * K * V * sizeof(float)));
+    int64_t* seg_cu = static_cast<int64_t*>(cv.take((P.ns + 1) * sizeof(int64_t)));
+    int32_t* seg_coff = static_cast<int32_t*>(cv.take((P.ns + 1) * sizeof(int32_t)));
+    kgdn::SegFwdArgs sa{};
+    sa.q = qx; sa.k = kx; sa.v = v; sa.g = g; sa.beta = beta; sa.q_scale = nullptr; sa.k_scale = nullptr;
+    sa.g_dtype = g_dtype; sa.beta_dtype = beta_dtype;
+    sa.h0 = initial_state; sa.h0_dtype = h0_dtype;
+    sa.cu = cu_seqlens; sa.chunk_off = chunk_off; sa.seg_off = seg_off;
+    sa.N = N; sa.T = T; sa.H = (int)H; sa.L = P.L; sa.nseg_fixed = P.nseg_fixed; sa.ns_grid = P.ns;
+    sa.M = M; sa.R = R; sa.s_init = s_init; sa.scale = scale; sa.o = nullptr; sa.ht = nullptr;
+    sa.Ai = rec; sa.nc_grid = G.nc; sa.l2 = false;
+    sa.run_trans = true; sa.run_combine = true; sa.skip_out = true; sa.events = nullptr;
+    if (int rc = from_launch(kgdn::launch_seg_fwd(sa, cdt, qk_dtype, (int)K, (int)V, s), "segment scan (recompute)"))
+      return rc;
+    if (int rc = from_launch(kgdn::launch_seg_place(sa, initial_state, h0_dtype, s_init, (int)K, (int)V, true, s),
+                             "segment start states"))
+      return rc;
+    if (int rc = from_launch(kgdn::launch_seg_seq_map(sa, seg_cu, seg_coff, s), "segment offsets")) return rc;
+    // the stage kernels over segments: segments as sequences of a varlen batch (the last segment of
+    // each sequence has no map; its dh pass starts from dht)
+    const int NS = (int)P.ns;
+    const int64_t T_all = B * T;
+    kgdn::FwdHArgs hs_a = ha;
+    hs_a.h0 = s_init; hs_a.h0_dtype = kgdn::DT_F32;
+    hs_a.cu = seg_cu; hs_a.chunk_off = seg_coff; hs_a.N = NS; hs_a.T = T_all;
+    if (int rc = from_launch(kgdn::launch_fwd_h(hs_a, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h (recompute)"))
+      return rc;
+    kgdn::BwdArgs bs = ba;
+    bs.cu = seg_cu; bs.chunk_off = seg_coff; bs.N = NS; bs.T = T_all;
+    if (int rc = from_launch(kgdn::launch_bwd(bs, cdt, (int)K, (int)V, nc_b, kgdn::BWD_DVL, s), what)) return rc;
+    float* Bseg = s_init;                       // free once h is recomputed
+    float* F = R;                               // free once the forward scan is done
+    kgdn::BwdArgs b1 = bs;
+    b1.dht = nullptr; b1.dh = nullptr; b1.dv2 = nullptr; b1.dh0 = Bseg;
+    if (dht) {                                  // the last segment of each sequence starts from dht
+      if (int rc = from_launch(kgdn::launch_seg_place(sa, dht, kgdn::DT_F32, F, (int)K, (int)V, false, s),
+                               "segment final-state gradients"))
+        return rc;
+      b1.dht = F;
+    }
+    if (int rc = from_launch(kgdn::launch_bwd(b1, cdt, (int)K, (int)V, nc_b, kgdn::BWD_DHU, s), what)) return rc;
+    if (int rc = from_launch(kgdn::launch_seg_bwd_combine(sa, Bseg, dht, F, dh0, (int)K, (int)V, s),
+                             "segment scan of dh"))
+      return rc;
+    kgdn::BwdArgs b2 = bs;
+    b2.dht = F; b2.dh0 = nullptr;
+    if (int rc = from_launch(kgdn::launch_bwd(b2, cdt, (int)K, (int)V, nc_b, kgdn::BWD_DHU, s), what)) return rc;
+    if (int rc = from_launch(kgdn::launch_bwd(bs, cdt, (int)K, (int)V, nc_b, kgdn::BWD_GRADS, s), what)) return rc;
+  }
   if (use_qk_l2norm && any_tokens) {
     if (int rc = from_launch(kgdn::launch_l2norm_bwd(q, dq_k, dq, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(q)"))
       return rc;

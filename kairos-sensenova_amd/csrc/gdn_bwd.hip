@@ -403,8 +403,8 @@ __global__ __launch_bounds__(64 * DCfg<K>::NW) void bwd_dhu_kernel(BwdArgs a, in
     const int nv = cur.nv;
     const int64_t t0 = cur.t0;
 
-    // dh snapshot, row-major [NC, H, K, V]
-    {
+    // dh snapshot, row-major [NC, H, K, V] (no outputs: a segment's first pass, which only needs dh0)
+    if (dh_out) {
       TC* p = dh_out + ((c * H + h) * K + KW * wid + 4 * lg) * (int64_t)V + v0 + lc;
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(64 * DCfg<K>::NW) void bwd_dhu_kernel(BwdArgs a, in
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * tm + 4 * lg + j;
         dv[j] = t < nv ? kd[j] * gexp(cur.gl - cur.gv[o][j]) + cur.dvl[o][j] : 0.f;
-        if (t < nv) dv2_out[((t0 + t) * H + h) * (int64_t)V + v0 + lc] = from_f32<TC>(dv[j]);
+        if (dv2_out && t < nv) dv2_out[((t0 + t) * H + h) * (int64_t)V + v0 + lc] = from_f32<TC>(dv[j]);
       }
       st4<TC>(s_dvT + lc * LDT + 16 * tm + 4 * lg, dv[0], dv[1], dv[2], dv[3]);
     }
@@ -864,19 +864,19 @@ int set_lds(K_ kern, size_t bytes) {
 }
 
 template <typename TC, int K>
-int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, hipStream_t s) {
+int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream_t s) {
   const dim3 grid((unsigned)nc_grid, (unsigned)a.H);
-  if (nc_grid > 0) {
+  if (nc_grid > 0 && (stages & BWD_DVL)) {
     const size_t l1 = dvl_lds<TC>(K, V);
     if (l1 > 160 * 1024 || set_lds(bwd_dvl_kernel<TC, K>, l1)) return -1;
     hipLaunchKernelGGL((bwd_dvl_kernel<TC, K>), grid, dim3(NT_B), l1, s, a, V);
   }
-  {
+  if (stages & BWD_DHU) {
     const int total = a.N * a.H * (V / DBV);
     const int g8 = (total + 7) / 8 * 8;
     if (total > 0) hipLaunchKernelGGL((bwd_dhu_kernel<TC, K>), dim3(g8), dim3(64 * DCfg<K>::NW), 0, s, a, V, total);
   }
-  if (nc_grid > 0) {
+  if (nc_grid > 0 && (stages & BWD_GRADS)) {
     const size_t l3 = dqkwg_lds<TC>(K);
     if (set_lds(bwd_dqkwg_kernel<TC, K>, l3)) return -1;
     hipLaunchKernelGGL((bwd_dqkwg_kernel<TC, K>), grid, dim3(NT_B), l3, s, a, V);
@@ -896,10 +896,10 @@ bool bwd_supported(int compute_dtype, int K, int V) {
   return false;
 }
 
-int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, hipStream_t s) {
+int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, int stages, hipStream_t s) {
   if (!bwd_supported(compute_dtype, K, V)) return -2;
 #define KGDN_B_CASE(TC, KK) \
-  if (K == KK) return launch_bwd_t<TC, KK>(a, V, nc_grid, s);
+  if (K == KK) return launch_bwd_t<TC, KK>(a, V, nc_grid, stages, s);
   if (compute_dtype == DT_BF16) { KGDN_B_CASE(bf16, 64) KGDN_B_CASE(bf16, 128) KGDN_B_CASE(bf16, 256) }
   if (compute_dtype == DT_F32) { KGDN_B_CASE(float, 64) KGDN_B_CASE(float, 128) }
 #undef KGDN_B_CASE

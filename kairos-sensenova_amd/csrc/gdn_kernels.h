@@ -115,6 +115,7 @@ struct SegFwdArgs {
   bool l2;                // the in-op L2 norm of q and k (bf16 q/k), folded into the kernels
   bool run_trans;         // some sequence has more than one segment
   bool run_combine;       // ... or final_state of empty sequences is needed
+  bool skip_out;          // stop after the segment scan (s_init, M): the backward's recomputation
   hipEvent_t* events;     // optional [5]: recorded before seg_prep, seg_trans, seg_combine, seg_out and after seg_out
 };
 
@@ -154,7 +155,10 @@ struct BwdArgs {
   float scale;
 };
 bool bwd_supported(int compute_dtype, int K, int V);
-int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, hipStream_t s);
+// stages: a mask of BWD_DVL (dv_local), BWD_DHU (the dh recurrence: dh, dv2, dh0; dh and dv2 may
+// be null to skip their stores) and BWD_GRADS (dq, dk, dw, dg, then the WY backward: dq .. dbeta)
+enum : int { BWD_DVL = 1, BWD_DHU = 2, BWD_GRADS = 4, BWD_ALL = 7 };
+int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, int stages, hipStream_t s);
 int launch_l2norm_bwd(const void* x, const void* dy, void* dx, int dtype, int64_t rows, int D, hipStream_t s);
 
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported
@@ -167,6 +171,20 @@ int launch_fwd_o(const FwdOArgs& a, int compute_dtype, int qk_dtype, int K, int 
 bool seg_fwd_supported(int compute_dtype, int K, int V);
 int launch_seg_fwd(const SegFwdArgs& a, int compute_dtype, int qk_dtype, int K, int V, hipStream_t s);
 int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s);
+// Segments as sequences for the stage kernels (the backward), from the geometry fields of a
+// SegFwdArgs (cu, chunk_off, seg_off, N, T, H, L, nseg_fixed, ns_grid, M):
+// seg_cu [ns_grid + 1] token and seg_coff [ns_grid + 1] chunk offsets of the segments;
+int launch_seg_seq_map(const SegFwdArgs& p, int64_t* seg_cu, int32_t* seg_coff, hipStream_t s);
+// dst [ns_grid, H, K, V] fp32 = src [N, H, K, V] at the first (first_seg) or last segment of each
+// sequence (src == nullptr: zeros), zeros at the other segments (left alone with first_seg);
+int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float* dst, int K, int V, bool first_seg,
+                     hipStream_t s);
+// the reverse scan of dh over segments with the transposed maps M_j^T: Bseg [ns_grid, H, K, V] holds
+// each segment's dh recurrence from zero (the last segment's: from dht), dht [N, H, K, V] (or null)
+// the final-state gradient; writes
+// F [ns_grid, H, K, V], the dh each segment's last chunk starts from, and dh0 [N, H, K, V] (or null).
+int launch_seg_bwd_combine(const SegFwdArgs& p, const float* Bseg, const float* dht, float* F, float* dh0, int K,
+                           int V, hipStream_t s);
 int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s);
 // the same for two tensors of equal shape in one launch (x1, y1 may be null)
 int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,

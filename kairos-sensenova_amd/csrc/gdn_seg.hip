@@ -2286,6 +2286,123 @@ __global__ void seg_map_kernel(const int64_t* __restrict__ cu, int N, int L, int
   }
 }
 
+// ---------------------------------------------------------------------------
+// Segments as sequences (the backward's recomputation and its dh recurrence run
+// the stage kernels over segments, each from the state the scan gives it)
+// ---------------------------------------------------------------------------
+// seg_cu[s] / seg_coff[s]: first token / first global chunk of segment s (slots past
+// the last segment: empty), seg_cu[ns] / seg_coff[ns]: the totals.
+__global__ void seg_seq_map_kernel(SegGeom G, int ns_grid, int64_t* __restrict__ seg_cu,
+                                   int32_t* __restrict__ seg_coff) {
+  const int64_t end_tok = G.cu ? G.cu[G.N] : (int64_t)G.N * G.T;
+  const int64_t end_ch = G.cu ? (int64_t)G.chunk_off[G.N] : (int64_t)G.N * ((G.T + C - 1) / C);
+  for (int s = blockIdx.x * blockDim.x + threadIdx.x; s <= ns_grid; s += gridDim.x * blockDim.x) {
+    const SegLoc sl = s < ns_grid ? locate_seg(s, G) : SegLoc{};
+    if (s < ns_grid && sl.ok) {
+      seg_cu[s] = sl.bos + sl.c0 * C;
+      seg_coff[s] = (int32_t)(sl.cbase + sl.c0);
+    } else {
+      seg_cu[s] = end_tok;
+      seg_coff[s] = (int32_t)end_ch;
+    }
+  }
+}
+
+// dst[s] = src[n] for the first (first_seg) or the last segment of each sequence n, zeros for the
+// other segments: [ns, H, K * V] fp32 from [N, H, K * V] (src: h0_dtype, or nullptr = zeros).
+// With first_seg the other segments are left alone (seg_combine writes them).
+__global__ __launch_bounds__(256) void seg_place_kernel(SegGeom G, const void* src, int src_dtype, float* dst,
+                                                        int KV, int first_seg) {
+  const int s = blockIdx.x, h = blockIdx.y, H = G.H;
+  const SegLoc sl = locate_seg(s, G);
+  if (!sl.ok) return;
+  const bool pick = first_seg ? sl.j == 0 : sl.j == sl.nseg - 1;
+  if (first_seg && !pick) return;
+  float* d = dst + ((int64_t)s * H + h) * KV;
+  const int64_t so = ((int64_t)sl.n * H + h) * KV;
+  for (int i = threadIdx.x; i < KV; i += blockDim.x) {
+    float x = 0.f;
+    if (pick && src)
+      x = src_dtype == DT_F32 ? reinterpret_cast<const float*>(src)[so + i]
+                              : (float)reinterpret_cast<const bf16*>(src)[so + i];
+    d[i] = x;
+  }
+}
+
+// Reverse scan of the dh recurrence over the segments of a sequence (one workgroup per
+// (sequence, head, 16 value columns)).  Across segment j the state gradient maps as
+// dh_start(j) = M_j^T dh_start(j + 1) + B_j, with M_j the forward's segment map (seg_trans,
+// a bf16 pair hi + lo) and B_j the dh recurrence of segment j run from zero.  The last
+// segment has no map (seg_trans skips it): its Bseg entry is its recurrence from dht, which
+// is dh_start(last) itself.  Writes F_j = dh_start(j + 1) (F_last = dht), the state each
+// segment's final pass starts from, and dh0 = dh_start(0) (when dh0 is not null).
+template <int K>
+__global__ __launch_bounds__(256) void seg_bwd_combine_kernel(SegGeom G, const bf16* __restrict__ M,
+                                                              const float* __restrict__ Bseg,
+                                                              const float* __restrict__ dht, float* __restrict__ F,
+                                                              float* __restrict__ dh0, int V, int total) {
+  constexpr int NT = 256, CPT = 16 * K / NT;              // columns per thread (of the 16)
+  static_assert(CPT % 4 == 0, "float4 column groups");
+  __shared__ __align__(16) float s_X[K][16];
+  const int unit_id = blockIdx.x;
+  if (unit_id >= total) return;
+  const int nvt = V / 16;
+  const int unit = unit_id / nvt, v0 = (unit_id % nvt) * 16;
+  const int H = G.H, n = unit / H, h = unit % H;
+  const int a_row = threadIdx.x % K, c0 = (threadIdx.x / K) * CPT;
+  int nseg, s_first;
+  if (G.cu == nullptr) {
+    nseg = G.T > 0 ? G.nseg_fixed : 0;
+    s_first = n * G.nseg_fixed;
+  } else {
+    nseg = G.seg_off[n + 1] - G.seg_off[n];
+    s_first = G.seg_off[n];
+  }
+  const int64_t KV = (int64_t)K * V;
+  const int64_t col = (int64_t)a_row * V + v0 + c0;       // offset of this thread's columns in a K x V block
+  float x[CPT];
+  if (nseg > 0) {
+    const int64_t last = ((int64_t)(s_first + nseg - 1) * H + h) * KV;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const float d = dht ? dht[((int64_t)n * H + h) * KV + col + c] : 0.f;
+      F[last + col + c] = d;
+      x[c] = Bseg[last + col + c];
+    }
+  } else {                                                // empty sequence: dh0 = dht
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) x[c] = dht ? dht[((int64_t)n * H + h) * KV + col + c] : 0.f;
+  }
+  for (int j = nseg - 2; j >= 0; --j) {
+    const int64_t blk = ((int64_t)(s_first + j) * H + h) * KV;
+#pragma unroll
+    for (int c = 0; c < CPT; c += 4) {
+      const f32x4 v4 = {x[c], x[c + 1], x[c + 2], x[c + 3]};
+      *reinterpret_cast<f32x4*>(&s_X[a_row][c0 + c]) = v4;
+      *reinterpret_cast<f32x4*>(F + blk + col + c) = v4;
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) x[c] = Bseg[blk + col + c];
+    __syncthreads();
+    const bf16* mh = M + ((int64_t)(s_first + j) * H + h) * 2 * K * K + a_row;
+#pragma unroll 16
+    for (int b = 0; b < K; ++b) {                        // (M^T X)[a] = sum_b M[b][a] X[b]
+      const float m = (float)mh[b * K] + (float)mh[K * K + b * K];
+#pragma unroll
+      for (int c = 0; c < CPT; c += 4) {
+        const f32x4 xs = *reinterpret_cast<const f32x4*>(&s_X[b][c0 + c]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[c + e] = fmaf(m, xs[e], x[c + e]);
+      }
+    }
+    __syncthreads();
+  }
+  if (dh0) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) dh0[((int64_t)n * H + h) * KV + col + c] = x[c];
+  }
+}
+
 template <typename Kern>
 int set_lds(Kern kern, size_t bytes) {
   if (bytes > 64 * 1024) {
@@ -2341,7 +2458,7 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(3)) return -1;
-  if (p.ns_grid > 0) {
+  if (p.ns_grid > 0 && !p.skip_out) {
     constexpr size_t lds = OutPlan<TQ, K, V>::total;
     auto ko = seg_out_kernel<TQ, K, V>;
     if (set_lds(ko, lds)) return -1;
@@ -2360,6 +2477,40 @@ bool seg_fwd_supported(int compute_dtype, int K, int V) {
   // bf16 compute only: the transposed operand reads (ds_read_b64_tr_b16) are 16-bit;
   // fp32 problems run the stage kernels
   return compute_dtype == DT_BF16 && (K == 64 || K == 128) && (V == 64 || V == 128);
+}
+
+int launch_seg_seq_map(const SegFwdArgs& p, int64_t* seg_cu, int32_t* seg_coff, hipStream_t s) {
+  const SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
+  const int ns = (int)p.ns_grid;
+  hipLaunchKernelGGL(seg_seq_map_kernel, dim3((unsigned)((ns + 1 + 255) / 256)), dim3(256), 0, s, G, ns, seg_cu,
+                     seg_coff);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float* dst, int K, int V, bool first_seg,
+                     hipStream_t s) {
+  const SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
+  if (p.ns_grid <= 0) return 0;
+  hipLaunchKernelGGL(seg_place_kernel, dim3((unsigned)p.ns_grid, (unsigned)p.H), dim3(256), 0, s, G, src, src_dtype,
+                     dst, K * V, first_seg ? 1 : 0);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_seg_bwd_combine(const SegFwdArgs& p, const float* Bseg, const float* dht, float* F, float* dh0, int K,
+                           int V, hipStream_t s) {
+  const SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
+  const int total = p.N * p.H * (V / 16);
+  if (total <= 0) return 0;
+  const bf16* M = reinterpret_cast<const bf16*>(p.M);
+  if (K == 64)
+    hipLaunchKernelGGL((seg_bwd_combine_kernel<64>), dim3((unsigned)total), dim3(256), 0, s, G, M, Bseg, dht, F, dh0,
+                       V, total);
+  else if (K == 128)
+    hipLaunchKernelGGL((seg_bwd_combine_kernel<128>), dim3((unsigned)total), dim3(256), 0, s, G, M, Bseg, dht, F, dh0,
+                       V, total);
+  else
+    return -2;
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s) {

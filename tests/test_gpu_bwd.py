@@ -90,6 +90,21 @@ def test_bwd_model_shape_varlen():
     run_case(1, 1100, 2, 256, 512, seed=9, cu=[0, 500, 1100], l2=True)
 
 
+@pytest.mark.parametrize("path", ["serial", "segments of 3 chunks", "segments of 1 chunk"])
+def test_bwd_segment_scan_paths(path, monkeypatch):
+    """The backward's segment scan (forward segment maps, dh reverse scan over segments) and the
+    sequence-long recurrences both match the oracle: fixed length with a ragged last chunk, and a
+    varlen batch whose sequences are empty, 1 token, a chunk exactly, and several segments long."""
+    if path == "serial":
+        monkeypatch.setenv("KAIROS_GDN_BWD_SEG", "0")
+    else:
+        monkeypatch.setenv("KAIROS_GDN_SEG_CHUNKS", "3" if "3" in path else "1")
+    note(f"backward {path}: fixed B=2 T=700 H=3")
+    run_case(2, 700, 3, 128, 128, seed=12)
+    note(f"backward {path}: varlen [0, 0, 1, 65, 129, 129, 900] H=2 K=64")
+    run_case(1, 900, 2, 64, 128, seed=13, cu=[0, 0, 1, 65, 129, 129, 900])
+
+
 def test_autograd_matches_direct_call():
     """torch.autograd through chunk_gated_delta_rule gives the direct backward call's gradients bit for bit."""
     B, T, H, K, V = 1, 150, 2, 128, 128
