@@ -226,8 +226,17 @@ hipEvent_t* profile_events() {
   return ev;
 }
 
-// Workspace of the staged path (stage kernels with the reference's intermediates).
-size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt) {
+// Whether the staged path runs the fused K = 256 recurrence + output (bf16 q/k, V a multiple of 64)
+// instead of fwd_h + fwd_o.  KAIROS_GDN_WIDE_FUSED=0 keeps the two stage kernels.
+bool use_wide_fused(int cdt, int qk_dtype, int64_t K, int64_t V) {
+  if (!kgdn::wide_fused_supported(cdt, qk_dtype, (int)K, (int)V)) return false;
+  const char* e = std::getenv("KAIROS_GDN_WIDE_FUSED");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
+// Workspace of the staged path (stage kernels with the reference's intermediates; the fused K = 256
+// form keeps the state snapshots and v_new on chip and adds the per-chunk Aqk instead).
+size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, bool wide) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
   const size_t tok = (size_t)(B * T * H);
@@ -235,8 +244,12 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
   total += align_up(tok * sizeof(float));                 // gc
   total += align_up(tok * K * es);                        // w
   total += align_up(nc * H * V * kgdn::C * es);           // uT
-  total += align_up(nc * H * V * K * es);                 // hT
-  total += align_up(nc * H * V * kgdn::C * es);           // vnT
+  if (wide) {
+    total += align_up(nc * H * kgdn::C * kgdn::C * es);   // Aqk
+  } else {
+    total += align_up(nc * H * V * K * es);               // hT
+    total += align_up(nc * H * V * kgdn::C * es);         // vnT
+  }
   return total;
 }
 
@@ -296,8 +309,16 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
   void* w = cv.take(tok * K * es);
   void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
-  void* hT = cv.take((size_t)G.nc * H * V * K * es);
-  void* vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  const bool wide = use_wide_fused(cdt, qk_dtype, G.K, G.V);
+  void* hT = nullptr;
+  void* vnT = nullptr;
+  void* aqk = nullptr;
+  if (wide) {
+    aqk = cv.take((size_t)G.nc * H * kgdn::C * kgdn::C * es);
+  } else {
+    hT = cv.take((size_t)G.nc * H * V * K * es);
+    vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  }
   const int N = (int)G.N;
   if (G.nc > 0) {
     kgdn::PrepareArgs pa{};
@@ -306,6 +327,18 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
     pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = nullptr;
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, G.nc, s), "prepare")) return rc;
+  }
+  if (wide) {
+    if (G.nc > 0) {
+      if (int rc = from_launch(kgdn::launch_aqk(q, k, gc, cu_seqlens, chunk_off, N, G.T, H, K, aqk, G.nc, s), "aqk"))
+        return rc;
+    }
+    kgdn::WideFusedArgs fa{};
+    fa.q = q; fa.k = k; fa.w = w; fa.uT = uT; fa.gc = gc; fa.aqk = aqk;
+    fa.h0 = h0; fa.h0_dtype = h0_dtype;
+    fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
+    fa.scale = scale; fa.o = o; fa.ht = ht;
+    return from_launch(kgdn::launch_wide_fused(fa, V, s), "wide fused recurrence");
   }
   kgdn::FwdHArgs ha{};
   ha.k = k; ha.k_scale = k_scale; ha.w = w; ha.uT = uT; ha.gc = gc;
@@ -379,7 +412,7 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   const int cdt = compute_dtype(qk_dtype, v_dtype);
   const bool seg = kgdn::seg_fwd_supported(cdt, (int)K, (int)V);
   size_t total = seg ? seg_ws(B, T, H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
-                     : staged_ws(B, T, H, K, V, n_seqs, cdt);
+                     : staged_ws(B, T, H, K, V, n_seqs, cdt, use_wide_fused(cdt, qk_dtype, K, V));
   // in-op L2 norm: the fused path folds it into its kernels; the staged path normalises q and k in a
   // pass of their own
   if (use_qk_l2norm && !seg) total += 2 * align_up(tok * K * dt_size(qk_dtype));

@@ -23,6 +23,9 @@ namespace kgdn {
 
 namespace {
 
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int BV = 16;     // V columns per workgroup
 constexpr int LDT = C + 8; // row stride of the [*][64] LDS tiles
 
@@ -307,9 +310,9 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 
 template <typename TK>
 struct WideChunk {
-  uint4 w[8];            // this thread's 8 x 8 elements of w (row-major items tid + 256 i)
-  uint4 k[8];            // the same items of k, as bf16 (fp8 k dequantised at load)
-  uint2 u[4];            // u of the wave's 16 columns, C layout, 4 row tiles, 4 bf16 each
+  u32x4 w[8];            // this thread's 8 x 8 elements of w (row-major items tid + 256 i)
+  u32x4 k[8];            // the same items of k, as bf16 (fp8 k dequantised at load)
+  u32x2 u[4];            // u of the wave's 16 columns, C layout, 4 row tiles, 4 bf16 each
   float gcl;             // gc of token t0 + lane (0 past the chunk's end); rows get theirs by shuffle
   int nv;
 };
@@ -327,7 +330,7 @@ __device__ __forceinline__ void wide_prefetch(WideChunk<TK>& P, const FwdHArgs& 
   for (int i = 0; i < 8; ++i) {
     const int item = tid + 256 * i;                 // 64 rows x 32 blocks of 8
     const int r = item >> 5, cb = item & 31;
-    P.w[i] = r < nv ? *reinterpret_cast<const uint4*>(w + ((t0 + r) * H + h) * WK + 8 * cb) : make_uint4(0, 0, 0, 0);
+    P.w[i] = r < nv ? *reinterpret_cast<const u32x4*>(w + ((t0 + r) * H + h) * WK + 8 * cb) : u32x4{0u, 0u, 0u, 0u};
   }
   const TK* k = reinterpret_cast<const TK*>(a.k);
   const float ks_ = a.k_scale ? a.k_scale[h] : 1.f;
@@ -336,7 +339,7 @@ __device__ __forceinline__ void wide_prefetch(WideChunk<TK>& P, const FwdHArgs& 
     const int item = tid + 256 * i;
     const int r = item >> 5, cb = item & 31;
     if constexpr (sizeof(TK) == 2) {
-      P.k[i] = r < nv ? *reinterpret_cast<const uint4*>(k + ((t0 + r) * H + h) * WK + 8 * cb) : make_uint4(0, 0, 0, 0);
+      P.k[i] = r < nv ? *reinterpret_cast<const u32x4*>(k + ((t0 + r) * H + h) * WK + 8 * cb) : u32x4{0u, 0u, 0u, 0u};
     } else {                                          // fp8: dequantise to bf16 (scalar locals for the bit casts)
       float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (r < nv) load8_in<TK>(k + ((t0 + r) * H + h) * WK + 8 * cb, ks_, x);
@@ -346,13 +349,13 @@ __device__ __forceinline__ void wide_prefetch(WideChunk<TK>& P, const FwdHArgs& 
         const bf16 lo = (bf16)x[2 * q], hi = (bf16)x[2 * q + 1];
         wd[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
       }
-      P.k[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+      P.k[i] = u32x4{wd[0], wd[1], wd[2], wd[3]};
     }
   }
   if (active) {
     const bf16* uT = reinterpret_cast<const bf16*>(a.uT) + ((c * H + h) * V + vcol) * C;
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) P.u[tm] = *reinterpret_cast<const uint2*>(uT + 16 * tm + 4 * lg);
+    for (int tm = 0; tm < 4; ++tm) P.u[tm] = *reinterpret_cast<const u32x2*>(uT + 16 * tm + 4 * lg);
   }
   P.gcl = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
 }
@@ -437,12 +440,12 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int item = tid + 256 * i;
-      *reinterpret_cast<uint4*>(s_w + (item >> 5) * LDW + 8 * (item & 31)) = cur.w[i];
+      *reinterpret_cast<u32x4*>(s_w + (item >> 5) * LDW + 8 * (item & 31)) = cur.w[i];
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int item = tid + 256 * i;
-      *reinterpret_cast<uint4*>(s_k + kswz_off(item >> 5, item & 31)) = cur.k[i];
+      *reinterpret_cast<u32x4*>(s_k + kswz_off(item >> 5, item & 31)) = cur.k[i];
     }
     wide_lds_barrier();
     if (it + 2 < nchunks) {
@@ -493,7 +496,7 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       const float gl = __shfl(cur.gcl, nv - 1);     // gc of the chunk's last token
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
-        const f32x4 uv = {bf16_lo(cur.u[tm].x), bf16_hi(cur.u[tm].x), bf16_lo(cur.u[tm].y), bf16_hi(cur.u[tm].y)};
+        const f32x4 uv = {bf16_lo(cur.u[tm][0]), bf16_hi(cur.u[tm][0]), bf16_lo(cur.u[tm][1]), bf16_hi(cur.u[tm][1])};
         const f32x4 vp = uv - acc[tm];              // v' = u - w h (chunk_delta_h.py:141-157)
         st4<bf16>(s_vn[wid] + lc * LDT + 16 * tm + 4 * lg, vp[0], vp[1], vp[2], vp[3]);
 #pragma unroll

@@ -29,6 +29,13 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file flags.  gdn_wide.hip: MFMA accumulators in VGPRs (the fused K = 256 kernel scales and packs
+# its state with VALU every chunk; in AGPRs each of those touches costs a copy).
+FILE_FLAGS = {
+    "gdn_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(exe):
@@ -42,7 +49,7 @@ def sources():
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, "-I", INCLUDE_DIR, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-I", INCLUDE_DIR, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

@@ -250,6 +250,18 @@ def test_full_op_edge_cases(dt, B, T, H, K, V, cu, l2, with_h0):
     check_against_oracle(x, dt, o, ht, cu=cu, l2=l2, with_h0=with_h0)
 
 
+@pytest.mark.parametrize("cu", [None, [0, 1, 130, 400]])
+def test_model_head_dims_stage_kernels(cu, monkeypatch):
+    """K=256, V=512 through the stage kernels (fwd_h + fwd_o, KAIROS_GDN_WIDE_FUSED=0) instead of the
+    fused recurrence + output: both forms against the oracle."""
+    monkeypatch.setenv("KAIROS_GDN_WIDE_FUSED", "0")
+    note(f"stage kernels K=256 V=512 cu={cu}")
+    n = len(cu) - 1 if cu else None
+    x = make_inputs(1, 400, 2, 256, 512, seed=41, dtype="bf16", n_states=n)
+    o, ht = run_gpu(x, "bf16", cu=cu)
+    check_against_oracle(x, "bf16", o, ht, cu=cu)
+
+
 def test_empty_sequence_returns_initial_state():
     note("T=0")
     x = make_inputs(2, 0, 2, 64, 64, seed=1, dtype="bf16")
