@@ -326,13 +326,10 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
     pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = nullptr;
+    pa.q = q; pa.aqk_out = aqk;                          // Aqk for the fused K = 256 form
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, G.nc, s), "prepare")) return rc;
   }
   if (wide) {
-    if (G.nc > 0) {
-      if (int rc = from_launch(kgdn::launch_aqk(q, k, gc, cu_seqlens, chunk_off, N, G.T, H, K, aqk, G.nc, s), "aqk"))
-        return rc;
-    }
     kgdn::WideFusedArgs fa{};
     fa.q = q; fa.k = k; fa.w = w; fa.uT = uT; fa.gc = gc; fa.aqk = aqk;
     fa.h0 = h0; fa.h0_dtype = h0_dtype;

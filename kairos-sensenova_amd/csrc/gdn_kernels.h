@@ -36,6 +36,8 @@ struct PrepareArgs {
   void* uT;               // out [NC, H, V, 64]
   float* A_out;           // optional out [B*T, H, 64] fp32
   void* Ai_out;           // optional out [B*T, H, 64]
+  const void* q;          // [B*T, H, K] (qk dtype), read only with aqk_out
+  void* aqk_out;          // optional out [NC, H, 64, 64]: mask_{i>=j}(q k^T exp(gc_i - gc_j)) (compute dtype)
 };
 
 struct FwdHArgs {
@@ -74,15 +76,15 @@ struct FwdOArgs {
   void* o;                // out [B*T, H, V] compute dtype
 };
 
-// Fused recurrence + output for K = 256 (gdn_wide.hip), after launch_prepare (gc, w, uT) and
-// launch_aqk.  bf16 q, k, w, u; V a multiple of 64.
+// Fused recurrence + output for K = 256 (gdn_wide.hip), after launch_prepare (gc, w, uT and, with
+// aqk_out, Aqk).  bf16 q, k, w, u; V a multiple of 64.
 struct WideFusedArgs {
   const void* q;          // [B*T, H, 256] bf16
   const void* k;          // [B*T, H, 256] bf16
   const void* w;          // [B*T, H, 256] bf16
   const void* uT;         // [NC, H, V, 64] bf16
   const float* gc;        // [B*T, H]
-  const void* aqk;        // [NC, H, 64, 64] bf16 (launch_aqk)
+  const void* aqk;        // [NC, H, 64, 64] bf16 (launch_prepare's aqk_out)
   const void* h0;         // [N, H, 256, V] (h0_dtype) or nullptr
   int h0_dtype;
   const int64_t* cu;
@@ -95,9 +97,6 @@ struct WideFusedArgs {
   float* ht;              // out [N, H, 256, V] fp32 or nullptr
 };
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V);
-// Aqk = mask_{i>=j, i<nv}(q k^T exp(gc_i - gc_j)) per (chunk, head), bf16 [NC, H, 64, 64] (K = 256)
-int launch_aqk(const void* q, const void* k, const float* gc, const int64_t* cu, const int32_t* chunk_off, int N,
-               int64_t T, int H, int K, void* aqk, int64_t nc_grid, hipStream_t s);
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s);
 
 // Per (chunk, head) record written by seg_prep and streamed by seg_trans and

@@ -108,6 +108,26 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
   __syncthreads();
 
+  // ---- with aqk_out: q row tile wid as MFMA fragments (rows 16 wid + lc, zero past the chunk's
+  //      end), loaded now so that they arrive during the k staging and K.K^T
+  Frag<TC> qf[K / 32];
+  if (a.aqk_out) {
+    const TK* qin = reinterpret_cast<const TK*>(a.q);
+    const int qr = 16 * wid + lc;
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) {
+      float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (qr < nv) load8_in<TK>(qin + ((t0 + qr) * H + h) * K + 32 * ks + 8 * lg, 1.f, x);
+      if constexpr (sizeof(TC) == 2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[ks].v[e] = (bf16)x[e];
+      } else {
+        qf[ks].lo = f32x4{x[0], x[1], x[2], x[3]};
+        qf[ks].hi = f32x4{x[4], x[5], x[6], x[7]};
+      }
+    }
+  }
+
   // ---- v of the first pass (below) into registers now, so its loads overlap K.K^T and the solve
   const TC* vin = reinterpret_cast<const TC*>(a.v);
   const int pr = tid & 31, cg = tid >> 5;                // token pair (2 pr, 2 pr + 1), column group of 8
@@ -180,6 +200,28 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
     for (int jj = 0; jj < 4; ++jj) {
       const int i = 16 * tm + 4 * lg + jj;
       av[q][jj] = (i > j && i < nv) ? acc[jj] * gexp(s_g[i] - s_g[j]) * s_b[i] : 0.f;
+    }
+  }
+  // ---- optional Aqk = mask_{i>=j, i<nv}(q_i.k_j exp(gc_i - gc_j)) rounded to the storage type,
+  //      [NC, H, 64, 64] with the upper triangle zero (chunk_o.py:84-118), for the fused K = 256
+  //      recurrence + output: wave w forms row tile w from its q fragments (loaded above) and k
+  //      from s_k
+  if (a.aqk_out) {
+    TC* aq = reinterpret_cast<TC*>(a.aqk_out) + ((int64_t)blockIdx.x * H + h) * (C * C);
+    const int tm = wid;
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (tn <= tm) {
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks) mma(acc, qf[ks], lds_frag<TC>(s_k, L::LDK, 16 * tn, 32 * ks));
+      }
+      const int j = 16 * tn + lc;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 16 * tm + 4 * lg + jj;
+        aq[i * C + j] = from_f32<TC>((i >= j && i < nv) ? acc[jj] * gexp(s_g[i] - s_g[j]) : 0.f);
+      }
     }
   }
   __syncthreads();                                 // k is dead: region 0 becomes A

@@ -13,8 +13,8 @@
 //
 // with the same cast points as the stage kernels (h and v' rounded to bf16 where the reference
 // stores them, Aqk rounded before its product).  Aqk = mask_{i>=j}(q k^T exp(gc_i - gc_j)) is
-// state-independent and shared by the V tiles of a head; aqk_kernel forms it per (chunk, head)
-// beforehand, so the serial loop only reads it.
+// state-independent and shared by the V tiles of a head; the prepare kernel forms it per (chunk,
+// head) beforehand (beside w and u, while k is in its LDS), so the serial loop only reads it.
 //
 // Operand layouts: w, q and k of a chunk are staged in LDS as swizzled [64][256] bf16 tiles
 // (swz_off<256>): w and q are read as row pieces in the accumulator K order (the order in which
@@ -56,55 +56,6 @@ __device__ __forceinline__ Frag<bf16> pack_acc(const f32x4& a, const f32x4& b) {
 
 __device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
-// ---------------------------------------------------------------------------
-// Aqk per (chunk, head): mask_{i>=j, i<nv}(q_i.k_j exp(gc_i - gc_j)) rounded to bf16, the upper
-// triangle and the rows past the chunk's end zero (chunk_o.py:84-118).  [NC, H, 64, 64].
-// ---------------------------------------------------------------------------
-constexpr int LDQK = FK + 8;
-
-__global__ __launch_bounds__(256) void aqk_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                  const float* __restrict__ gc, const int64_t* cu,
-                                                  const int32_t* chunk_off, int N, int64_t T, int H,
-                                                  bf16* __restrict__ aqk) {
-  __shared__ __align__(16) bf16 s_q[C * LDQK];
-  __shared__ __align__(16) bf16 s_k[C * LDQK];
-  __shared__ float s_g[C];
-  const int h = blockIdx.y;
-  const int64_t c = blockIdx.x;
-  const ChunkLoc loc = locate_chunk(c, cu, chunk_off, N, T);
-  if (!loc.ok) return;
-  const int tid = threadIdx.x, wid = tid / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
-  const int nv = loc.nv;
-#pragma unroll
-  for (int i = 0; i < 2 * C * (FK / 8) / 256; ++i) {
-    const int idx = tid + 256 * i;
-    const int which = idx / (C * (FK / 8)), rem = idx % (C * (FK / 8));
-    const int r = rem / (FK / 8), c8 = rem % (FK / 8);
-    uint4 x = make_uint4(0u, 0u, 0u, 0u);
-    if (r < nv) x = *reinterpret_cast<const uint4*>((which ? k : q) + ((loc.t0 + r) * H + h) * FK + 8 * c8);
-    *reinterpret_cast<uint4*>((which ? s_k : s_q) + r * LDQK + 8 * c8) = x;
-  }
-  if (tid < C) s_g[tid] = tid < nv ? gc[(loc.t0 + tid) * H + h] : 0.f;
-  __syncthreads();
-  bf16* out = aqk + (c * H + h) * (int64_t)(C * C);
-  for (int tile = wid; tile < 16; tile += 4) {
-    const int tm = tile >> 2, tn = tile & 3;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (tn <= tm) {
-#pragma unroll
-      for (int ks = 0; ks < FK / 32; ++ks)
-        mma(acc, lds_frag<bf16>(s_q, LDQK, 16 * tm, 32 * ks), lds_frag<bf16>(s_k, LDQK, 16 * tn, 32 * ks));
-    }
-    const int j = 16 * tn + lc;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * tm + 4 * lg + jj;
-      const float val = (i >= j && i < nv) ? acc[jj] * gexp(s_g[i] - s_g[j]) : 0.f;
-      out[i * C + j] = (bf16)val;
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // the fused recurrence + output
@@ -151,8 +102,10 @@ typedef __attribute__((address_space(3))) float lds_f32;
 
 // LDS reads at a lane byte address plus an offset that is a constant after unrolling (it lands
 // in the instruction's offset field)
+// (volatile: the compiler would otherwise pair reads that share a base into ds_read2st64_b64, whose
+// register layout does not match the operand fragments, and then copy every fragment)
 __device__ __forceinline__ u32x2 ld64(uint32_t a, uint32_t off) {
-  return *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(a) + off);
+  return *reinterpret_cast<volatile const lds_u32x2*>(reinterpret_cast<lds_b*>(a) + off);
 }
 __device__ __forceinline__ u32x2 ldtr(uint32_t a, uint32_t off) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -504,16 +457,6 @@ __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V
 
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V) {
   return compute_dtype == DT_BF16 && qk_dtype == DT_BF16 && K == FK && V > 0 && V % FVT == 0;
-}
-
-int launch_aqk(const void* q, const void* k, const float* gc, const int64_t* cu, const int32_t* chunk_off, int N,
-               int64_t T, int H, int K, void* aqk, int64_t nc_grid, hipStream_t s) {
-  if (K != FK) return -2;
-  if (nc_grid <= 0) return 0;
-  hipLaunchKernelGGL(aqk_kernel, dim3((unsigned)nc_grid, (unsigned)H), dim3(256), 0, s,
-                     static_cast<const bf16*>(q), static_cast<const bf16*>(k), gc, cu, chunk_off, N, T, H,
-                     static_cast<bf16*>(aqk));
-  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s) {
