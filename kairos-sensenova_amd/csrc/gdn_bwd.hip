@@ -20,12 +20,16 @@
 // accumulator-order reads and ds_read_b64_tr_b16 transposed reads (contractions
 // over the token axis) are bank-conflict free; fp32 tiles are padded rows read
 // transposed element by element.
+#include <cstdlib>
+
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
 
 namespace kgdn {
 
 namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // LDS tiles of 64 rows x ncol columns
@@ -269,6 +273,16 @@ __global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
 constexpr int DBV = 16;
 constexpr int LDT = C + 8;
 
+// Workgroup barrier that waits for LDS operations only (lgkmcnt(0), s_barrier): within a chunk step
+// the waves share only LDS, and __syncthreads() would also wait for the next chunk's loads (vmcnt(0))
+// and this chunk's stores.  The empty asm statements keep memory accesses from moving across it.
+__device__ __forceinline__ void step_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0); vmcnt, expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int K> struct DCfg {
   static constexpr int NW = K == 64 ? 2 : 4;
   static constexpr int KW = K / NW;
@@ -438,7 +452,7 @@ __global__ __launch_bounds__(64 * DCfg<K>::NW) void bwd_dhu_kernel(BwdArgs a, in
         }
       }
     }
-    __syncthreads();
+    step_barrier();
 
     // do^T columns of this wave (after the barrier: every wave has finished the previous
     // chunk's update, which reads s_doT and s_dvT); dv2 of the owned row tiles
@@ -459,7 +473,7 @@ __global__ __launch_bounds__(64 * DCfg<K>::NW) void bwd_dhu_kernel(BwdArgs a, in
       }
       st4<TC>(s_dvT + lc * LDT + 16 * tm + 4 * lg, dv[0], dv[1], dv[2], dv[3]);
     }
-    __syncthreads();
+    step_barrier();
 
     // dh = e^{g_last} dh + (scale q e^{gc})^T do - w^T bf16(dv2)
     const float eg = gexp(cur.gl);
@@ -487,6 +501,221 @@ __global__ __launch_bounds__(64 * DCfg<K>::NW) void bwd_dhu_kernel(BwdArgs a, in
         a.dh0[off] = dh[tt][j];
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dh recurrence, bf16, one workgroup per (sequence, head) with all value columns
+// (chunk_delta_h.py:250-438, the same step as bwd_dhu_kernel).  V / 16 waves, wave w owning
+// columns 16 w .. 16 w + 15 of dh over all K rows (fp32, accumulator layout, in VGPRs); the
+// chunk's k, q e^{gc} scale (as a bf16 pair hi + lo), -w, do and dv_local are staged once in LDS
+// for every wave (the per-16-column form re-stages them for each column slice).  Inputs of the
+// next chunk (in reverse order) are loaded into registers while the current chunk computes.
+//   dv2 = e^{g_last - gc} (k bf16(dh)) + dv_local        A = k rows, K = dh rows (accumulator order)
+//   dh  = e^{g_last} dh + (q e^{gc} scale)^T do - w^T bf16(dv2)   A = transposed tiles, B = do
+//                                                        (transposed) and dv2's accumulator tiles
+// ---------------------------------------------------------------------------
+template <int K, int V>
+struct DW {
+  static constexpr int NW = V / 16, NT = NW * WAVE;
+  static constexpr int KT = K / 16, KS = K / 32;
+  static constexpr int EK = C * K, EV = C * V;            // elements of a [64][K] / [64][V] tile
+  static constexpr int off_k = 0, off_qh = EK, off_ql = 2 * EK, off_w = 3 * EK, off_do = 4 * EK;
+  static constexpr int off_dvl = 4 * EK + EV;              // dv_local [64][V] (same tile layout)
+  static constexpr int n_el = 4 * EK + 2 * EV;
+  static constexpr size_t lds = (size_t)n_el * 2 + C * sizeof(float);
+  static constexpr int UK = EK / 8 / NT, UV = EV / 8 / NT;  // 16-byte units per thread
+  static_assert(EK % (8 * NT) == 0 && EV % (8 * NT) == 0, "units split evenly over the threads");
+};
+
+template <int K, int V>
+struct DWChunk {
+  using D = DW<K, V>;
+  u32x4 q[D::UK], k[D::UK], w[D::UK], dO[D::UV], dvl[D::UV];
+  float qs[D::UK];            // e^{gc} scale of the row of each q unit (0 past the chunk's end)
+  float gt;                   // gc of token = lane (0 past the end)
+  int64_t t0;
+  int nv;
+};
+
+template <int K, int V>
+__device__ __forceinline__ void dw_load(DWChunk<K, V>& P, const BwdArgs& a, int64_t t0, int nv, int h) {
+  using D = DW<K, V>;
+  const int tid = threadIdx.x, l = lane_id();
+  const int H = a.H;
+  P.t0 = t0;
+  P.nv = nv;
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  const bf16* q = reinterpret_cast<const bf16*>(a.q);
+  const bf16* k = reinterpret_cast<const bf16*>(a.k);
+  const bf16* w = reinterpret_cast<const bf16*>(a.w);
+#pragma unroll
+  for (int i = 0; i < D::UK; ++i) {
+    const int u = tid + D::NT * i, r = u / (K / 8), c8 = u % (K / 8);
+    const int64_t off = ((t0 + r) * H + h) * (int64_t)K + 8 * c8;
+    P.q[i] = r < nv ? *reinterpret_cast<const u32x4*>(q + off) : z;
+    P.k[i] = r < nv ? *reinterpret_cast<const u32x4*>(k + off) : z;
+    P.w[i] = r < nv ? *reinterpret_cast<const u32x4*>(w + off) : z;
+    P.qs[i] = r < nv ? a.gc[(t0 + r) * H + h] : 0.f;     // exponentiated at staging
+  }
+  const bf16* dO = reinterpret_cast<const bf16*>(a.do_);
+  const bf16* dvl = reinterpret_cast<const bf16*>(a.dvl);
+#pragma unroll
+  for (int i = 0; i < D::UV; ++i) {
+    const int u = tid + D::NT * i, r = u / (V / 8), c8 = u % (V / 8);
+    const int64_t off = ((t0 + r) * H + h) * (int64_t)V + 8 * c8;
+    P.dO[i] = r < nv ? *reinterpret_cast<const u32x4*>(dO + off) : z;
+    P.dvl[i] = r < nv ? *reinterpret_cast<const u32x4*>(dvl + off) : z;
+  }
+  P.gt = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
+}
+
+template <int K, int V>
+__global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a, int total_units) {
+  using D = DW<K, V>;
+  constexpr int KT = D::KT, KS = D::KS;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* sm = reinterpret_cast<bf16*>(smem);
+  bf16* s_k = sm + D::off_k;
+  bf16* s_qh = sm + D::off_qh;
+  bf16* s_ql = sm + D::off_ql;
+  bf16* s_w = sm + D::off_w;
+  bf16* s_do = sm + D::off_do;
+  bf16* s_dvl = sm + D::off_dvl;
+  float* s_g = reinterpret_cast<float*>(smem + (size_t)D::n_el * 2);
+
+  const int per_xcd = gridDim.x / 8;                   // XCD-aware unit order
+  const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (unit >= total_units) return;
+  const int H = a.H;
+  const int n = unit / H, h = unit % H;
+  const int tid = threadIdx.x, wid = tid / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int c0 = 16 * wid;                             // this wave's columns
+
+  int64_t bos, eos, c_first;
+  if (a.cu == nullptr) {
+    bos = (int64_t)n * a.T;
+    eos = bos + a.T;
+    c_first = (int64_t)n * ((a.T + C - 1) / C);
+  } else {
+    bos = a.cu[n];
+    eos = a.cu[n + 1];
+    c_first = a.chunk_off[n];
+  }
+  const int64_t nchunks = (eos - bos + C - 1) / C;
+
+  // dh: rows 16 tt + 4 lg + j, column c0 + lc; starts at dht
+  f32x4 dh[KT];
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t off = (((int64_t)n * H + h) * K + 16 * tt + 4 * lg + j) * V + c0 + lc;
+      dh[tt][j] = a.dht ? a.dht[off] : 0.f;
+    }
+
+  auto chunk_start = [&](int64_t it) { return bos + it * C; };
+  auto chunk_len = [&](int64_t it) { return (int)min((int64_t)C, eos - chunk_start(it)); };
+  DWChunk<K, V> cur, nxt;
+  if (nchunks > 0) dw_load<K, V>(cur, a, chunk_start(nchunks - 1), chunk_len(nchunks - 1), h);
+  bf16* dh_out = reinterpret_cast<bf16*>(a.dh);
+  bf16* dv2_out = reinterpret_cast<bf16*>(a.dv2);
+
+  for (int64_t it = nchunks - 1; it >= 0; --it) {
+    const int64_t c = c_first + it;
+    const int nv = cur.nv;
+    const int64_t t0 = cur.t0;
+    // ---- stage the chunk: k, q e^{gc} scale as hi + lo, -w, do, dv_local, gc
+#pragma unroll
+    for (int i = 0; i < D::UK; ++i) {
+      const int u = tid + D::NT * i, r = u / (K / 8), cc = 8 * (u % (K / 8));
+      const int o = toff<bf16>(r, cc, K);
+      *reinterpret_cast<u32x4*>(s_k + o) = cur.k[i];
+      u32x4 nw = cur.w[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) nw[e] ^= 0x80008000u;  // -w
+      *reinterpret_cast<u32x4*>(s_w + o) = nw;
+      const float sc = r < nv ? gexp(cur.qs[i]) * a.scale : 0.f;
+      const bf16x8 qv = __builtin_bit_cast(bf16x8, cur.q[i]);
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (float)qv[e] * sc;
+        hi[e] = (bf16)x;
+        lo[e] = (bf16)(x - (float)hi[e]);
+      }
+      *reinterpret_cast<bf16x8*>(s_qh + o) = hi;
+      *reinterpret_cast<bf16x8*>(s_ql + o) = lo;
+    }
+#pragma unroll
+    for (int i = 0; i < D::UV; ++i) {
+      const int u = tid + D::NT * i, r = u / (V / 8), cc = 8 * (u % (V / 8));
+      const int o = toff<bf16>(r, cc, V);
+      *reinterpret_cast<u32x4*>(s_do + o) = cur.dO[i];
+      *reinterpret_cast<u32x4*>(s_dvl + o) = cur.dvl[i];
+    }
+    if (wid == 0) s_g[l] = cur.gt;
+    step_barrier();
+    if (it > 0) dw_load<K, V>(nxt, a, chunk_start(it - 1), chunk_len(it - 1), h);
+
+    // dh snapshot (before this chunk), row-major [NC, H, K, V]
+    if (dh_out) {
+      bf16* p = dh_out + ((c * H + h) * K + 4 * lg) * (int64_t)V + c0 + lc;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * (int64_t)V] = (bf16)dh[tt][j];
+    }
+    // dv2 = e^{g_last - gc} (k bf16(dh)) + dv_local, rows t = 16 tm + 4 lg + j
+    Frag<bf16> hb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) hb[ks] = acc_frag<bf16>(dh[2 * ks], dh[2 * ks + 1]);
+    const float gl = s_g[nv - 1];
+    f32x4 dv[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) mma(acc, t_acc<bf16>(s_k, K, 16 * tm, 32 * ks), hb[ks]);
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(s_g + 16 * tm + 4 * lg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tm + 4 * lg + j;
+        const float dl = (float)s_dvl[toff<bf16>(t, c0 + lc, V)];
+        dv[tm][j] = t < nv ? acc[j] * gexp(gl - g4[j]) + dl : 0.f;
+        if (dv2_out && t < nv) dv2_out[((t0 + t) * H + h) * (int64_t)V + c0 + lc] = (bf16)dv[tm][j];
+      }
+    }
+    // dh = e^{g_last} dh + (q e^{gc} scale)^T do - w^T bf16(dv2)
+    Frag<bf16> bdo[2], bdv[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bdo[ks] = t_tr<bf16>(s_do, V, 32 * ks, c0);
+      bdv[ks] = acc_frag<bf16>(dv[2 * ks], dv[2 * ks + 1]);
+    }
+    const float eg = gexp(gl);
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      dh[tt] *= eg;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        mma(dh[tt], t_tr<bf16>(s_qh, K, 32 * ks, 16 * tt), bdo[ks]);
+        mma(dh[tt], t_tr<bf16>(s_ql, K, 32 * ks, 16 * tt), bdo[ks]);
+        mma(dh[tt], t_tr<bf16>(s_w, K, 32 * ks, 16 * tt), bdv[ks]);
+      }
+    }
+    step_barrier();                                    // the tiles are restaged next chunk
+    cur = nxt;
+  }
+
+  if (a.dh0) {
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (((int64_t)n * H + h) * K + 16 * tt + 4 * lg + j) * V + c0 + lc;
+        a.dh0[off] = dh[tt][j];
+      }
   }
 }
 
@@ -872,9 +1101,37 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
     hipLaunchKernelGGL((bwd_dvl_kernel<TC, K>), grid, dim3(NT_B), l1, s, a, V);
   }
   if (stages & BWD_DHU) {
-    const int total = a.N * a.H * (V / DBV);
-    const int g8 = (total + 7) / 8 * 8;
-    if (total > 0) hipLaunchKernelGGL((bwd_dhu_kernel<TC, K>), dim3(g8), dim3(64 * DCfg<K>::NW), 0, s, a, V, total);
+    bool wide = false;
+    if constexpr (sizeof(TC) == 2 && K <= 128) {
+      if (V == 64 || V == 128) {
+        const char* e = std::getenv("KAIROS_GDN_BWD_DHU_WIDE");
+        wide = !(e && e[0] == '0' && e[1] == 0);
+      }
+      if (wide) {
+        const int total = a.N * a.H;
+        const int g8 = (total + 7) / 8 * 8;
+        if (total > 0) {
+          if (V == 64) {
+            using D = DW<K, 64>;
+            constexpr int nt = D::NT;
+            constexpr size_t lds = D::lds;
+            if (set_lds(bwd_dhu_wide_kernel<K, 64>, lds)) return -1;
+            hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 64>), dim3(g8), dim3(nt), lds, s, a, total);
+          } else {
+            using D = DW<K, 128>;
+            constexpr int nt = D::NT;
+            constexpr size_t lds = D::lds;
+            if (set_lds(bwd_dhu_wide_kernel<K, 128>, lds)) return -1;
+            hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 128>), dim3(g8), dim3(nt), lds, s, a, total);
+          }
+        }
+      }
+    }
+    if (!wide) {
+      const int total = a.N * a.H * (V / DBV);
+      const int g8 = (total + 7) / 8 * 8;
+      if (total > 0) hipLaunchKernelGGL((bwd_dhu_kernel<TC, K>), dim3(g8), dim3(64 * DCfg<K>::NW), 0, s, a, V, total);
+    }
   }
   if (nc_grid > 0 && (stages & BWD_GRADS)) {
     const size_t l3 = dqkwg_lds<TC>(K);

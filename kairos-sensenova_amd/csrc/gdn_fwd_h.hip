@@ -37,6 +37,17 @@ template <int K> struct HCfg {
   static constexpr int OWN = 4 / NW;           // 16-row tiles of v' reduced by each wave
 };
 
+// Workgroup barrier that waits for LDS operations only (lgkmcnt(0), s_barrier): the waves share
+// only LDS within a chunk step, and __syncthreads() would also wait for the next chunk's prefetch
+// (vmcnt(0)) and this chunk's stores.  The empty asm statements keep memory accesses from moving
+// across the barrier.
+__device__ __forceinline__ void step_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0); vmcnt, expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <typename TC> struct Half;             // 4 storage elements (8 B bf16 / 16 B fp32)
 template <> struct Half<bf16> { bf16x4 v; };
 template <> struct Half<float> { f32x4 v; };
@@ -227,7 +238,7 @@ __global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int
       for (int ks = 0; ks < KS; ++ks) mma(acc, cur.wf[tm][ks], hb[ks]);
       s_red[wid][tm][l] = acc;
     }
-    __syncthreads();
+    step_barrier();
 
     // k^T slice of this wave (read only by this wave, in the update below: t = lane)
 #pragma unroll
@@ -261,7 +272,7 @@ __global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int
       }
       st4<TC>(s_vgT + lc * LDT + 16 * tm + 4 * lg, vg[0], vg[1], vg[2], vg[3]);
     }
-    __syncthreads();
+    step_barrier();
 
     // S = exp(g_last) S + k^T (v' gated)
     const float eg = gexp(cur.gl);

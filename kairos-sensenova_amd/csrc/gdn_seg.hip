@@ -2265,7 +2265,7 @@ __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineA
       float* out = a.s_init + ((s_first + j + 1) * (int64_t)H + h) * K * V + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) out[(int64_t)jj * V] = acc[jj];
-      __syncthreads();
+      lds_barrier();                                        // LDS only: the maps' prefetch stays in flight
     }
   }
 }

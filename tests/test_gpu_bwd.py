@@ -90,14 +90,18 @@ def test_bwd_model_shape_varlen():
     run_case(1, 1100, 2, 256, 512, seed=9, cu=[0, 500, 1100], l2=True)
 
 
-@pytest.mark.parametrize("path", ["serial", "segments of 3 chunks", "segments of 1 chunk"])
+@pytest.mark.parametrize("path", ["serial", "segments of 3 chunks", "segments of 1 chunk",
+                                  "16-column dh kernel", "serial, 16-column dh kernel"])
 def test_bwd_segment_scan_paths(path, monkeypatch):
     """The backward's segment scan (forward segment maps, dh reverse scan over segments) and the
-    sequence-long recurrences both match the oracle: fixed length with a ragged last chunk, and a
-    varlen batch whose sequences are empty, 1 token, a chunk exactly, and several segments long."""
-    if path == "serial":
+    sequence-long recurrences both match the oracle, with the dh recurrence in its all-columns form
+    and in its 16-column form: fixed length with a ragged last chunk, and a varlen batch whose
+    sequences are empty, 1 token, a chunk exactly, and several segments long."""
+    if "16-column" in path:
+        monkeypatch.setenv("KAIROS_GDN_BWD_DHU_WIDE", "0")
+    if path.startswith("serial"):
         monkeypatch.setenv("KAIROS_GDN_BWD_SEG", "0")
-    else:
+    elif "segments" in path:
         monkeypatch.setenv("KAIROS_GDN_SEG_CHUNKS", "3" if "3" in path else "1")
     note(f"backward {path}: fixed B=2 T=700 H=3")
     run_case(2, 700, 3, 128, 128, seed=12)
