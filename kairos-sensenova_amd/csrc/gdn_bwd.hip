@@ -24,81 +24,13 @@
 
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
+#include "gdn_tiles.hpp"
 
 namespace kgdn {
 
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// ---------------------------------------------------------------------------
-// LDS tiles of 64 rows x ncol columns
-// ---------------------------------------------------------------------------
-template <typename TC>
-__host__ __device__ constexpr int tile_elems(int ncol) {
-  return sizeof(TC) == 2 ? 64 * ncol : 64 * (ncol + 4);
-}
-
-template <typename TC>
-__device__ __forceinline__ int toff(int r, int c, int ncol) {
-  if constexpr (sizeof(TC) == 2) {
-    return (c >> 6) * 4096 + swz_off<64>(r, (c & 63) >> 3) + (c & 7);
-  } else {
-    return r * (ncol + 4) + c;
-  }
-}
-
-// natural K order: M/N index = row r0 + l % 16, K index = k0 + 8 (l / 16) + e
-template <typename TC>
-__device__ __forceinline__ Frag<TC> t_nat(const TC* t, int ncol, int r0, int k0) {
-  const int l = lane_id();
-  const TC* p = t + toff<TC>(r0 + (l & 15), k0 + 8 * (l >> 4), ncol);
-  Frag<TC> f;
-  if constexpr (sizeof(TC) == 2) {
-    f.v = *reinterpret_cast<const bf16x8*>(p);
-  } else {
-    f.lo = *reinterpret_cast<const f32x4*>(p);
-    f.hi = *reinterpret_cast<const f32x4*>(p + 4);
-  }
-  return f;
-}
-
-// accumulator K order: M/N index = row r0 + l % 16, K index = k0 + 4 lg + e and k0 + 16 + 4 lg + e
-template <typename TC>
-__device__ __forceinline__ Frag<TC> t_acc(const TC* t, int ncol, int r0, int k0) {
-  const int l = lane_id();
-  const int r = r0 + (l & 15), lg = l >> 4;
-  const TC* p0 = t + toff<TC>(r, k0 + 4 * lg, ncol);
-  const TC* p1 = t + toff<TC>(r, k0 + 16 + 4 * lg, ncol);
-  Frag<TC> f;
-  if constexpr (sizeof(TC) == 2) {
-    const bf16x4 a = *reinterpret_cast<const bf16x4*>(p0);
-    const bf16x4 b = *reinterpret_cast<const bf16x4*>(p1);
-    f.v = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  } else {
-    f.lo = *reinterpret_cast<const f32x4*>(p0);
-    f.hi = *reinterpret_cast<const f32x4*>(p1);
-  }
-  return f;
-}
-
-// transposed: M/N index = column c0 + l % 16, K index = row k0 + (accumulator order), k0 a multiple of 32
-template <typename TC>
-__device__ __forceinline__ Frag<TC> t_tr(const TC* t, int ncol, int k0, int c0) {
-  if constexpr (sizeof(TC) == 2) {
-    return tr_frag<64>(t + (c0 >> 6) * 4096, k0 >> 5, c0 & 63);
-  } else {
-    const int l = lane_id();
-    const int c = c0 + (l & 15), lg = l >> 4;
-    Frag<float> f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      f.lo[e] = t[toff<float>(k0 + 4 * lg + e, c, ncol)];
-      f.hi[e] = t[toff<float>(k0 + 16 + 4 * lg + e, c, ncol)];
-    }
-    return f;
-  }
-}
 
 // the row of K index e of an accumulator-order fragment (relative to k0), for per-row operand scaling
 __device__ __forceinline__ int acc_row(int e) { return 4 * (lane_id() >> 4) + (e & 3) + (e >> 2) * 16; }

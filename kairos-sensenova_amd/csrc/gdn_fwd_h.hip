@@ -16,8 +16,11 @@
 // waves are summed through LDS; the gated v' goes through LDS once more as the
 // B operand of the rank-64 update.  Everything the next chunk needs (w, k, u,
 // gc) is prefetched into registers while the current chunk computes.
+#include <cstdlib>
+
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
+#include "gdn_tiles.hpp"
 
 namespace kgdn {
 
@@ -577,6 +580,205 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// All-columns form for bf16 K, V in {64, 128}: one workgroup per (sequence, head), V / 16 waves,
+// wave w owning state columns 16 w .. + 15 over all K rows (fp32 accumulator tiles in VGPRs).  The
+// chunk's w and k are staged in LDS once for every wave (the split-K form stages them once per 16
+// columns); u comes from uT in the accumulator layout, the next chunk's inputs are loaded into
+// registers while the current one computes.  Same outputs and cast points as the other forms.
+// ---------------------------------------------------------------------------
+template <int K, int V>
+struct HCols {
+  static constexpr int NW = V / 16, NT = NW * WAVE;
+  static constexpr int KT = K / 16, KS = K / 32;
+  static constexpr int EK = C * K;
+  static constexpr int UK = EK / 8 / NT;                 // 16-byte units of a [64][K] tile per thread
+  static_assert(EK % (8 * NT) == 0, "units split evenly over the threads");
+  static constexpr size_t lds = (size_t)2 * EK * 2 + C * sizeof(float);
+};
+
+template <int K, int V>
+struct HColsChunk {
+  using P = HCols<K, V>;
+  u32x4 w[P::UK], k[P::UK];
+  u32x2 u[4];                 // u of the wave's column lc, rows 16 tm + 4 lg .. + 3
+  float gt;                   // gc of token = lane (0 past the end)
+  int64_t t0;
+  int nv;
+};
+
+template <int K, int V>
+__device__ __forceinline__ void hcols_load(HColsChunk<K, V>& P, const FwdHArgs& a, int64_t c, int64_t t0, int nv,
+                                           int h, int vcol) {
+  using HP = HCols<K, V>;
+  const int tid = threadIdx.x, l = lane_id(), lg = l >> 4;
+  const int H = a.H;
+  P.t0 = t0;
+  P.nv = nv;
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  const bf16* w = reinterpret_cast<const bf16*>(a.w);
+  const bf16* k = reinterpret_cast<const bf16*>(a.k);
+#pragma unroll
+  for (int i = 0; i < HP::UK; ++i) {
+    const int u = tid + HP::NT * i, r = u / (K / 8), c8 = u % (K / 8);
+    const int64_t off = ((t0 + r) * H + h) * (int64_t)K + 8 * c8;
+    P.w[i] = r < nv ? *reinterpret_cast<const u32x4*>(w + off) : z;
+    P.k[i] = r < nv ? *reinterpret_cast<const u32x4*>(k + off) : z;
+  }
+  const bf16* uT = reinterpret_cast<const bf16*>(a.uT) + ((c * H + h) * V + vcol) * C;
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) P.u[tm] = *reinterpret_cast<const u32x2*>(uT + 16 * tm + 4 * lg);
+  P.gt = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
+}
+
+template <int K, int V>
+__global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs a, int total_units) {
+  using HP = HCols<K, V>;
+  constexpr int KT = HP::KT, KS = HP::KS;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* s_w = reinterpret_cast<bf16*>(smem);
+  bf16* s_k = s_w + HP::EK;
+  float* s_g = reinterpret_cast<float*>(smem + (size_t)2 * HP::EK * 2);
+
+  const int per_xcd = gridDim.x / 8;                      // XCD-aware unit order
+  const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (unit >= total_units) return;
+  const int H = a.H;
+  const int n = unit / H, h = unit % H;
+  const int tid = threadIdx.x, wid = tid / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int c0 = 16 * wid, vcol = c0 + lc;
+
+  int64_t bos, eos, c_first;
+  if (a.cu == nullptr) {
+    bos = (int64_t)n * a.T;
+    eos = bos + a.T;
+    c_first = (int64_t)n * ((a.T + C - 1) / C);
+  } else {
+    bos = a.cu[n];
+    eos = a.cu[n + 1];
+    c_first = a.chunk_off[n];
+  }
+  const int64_t nchunks = (eos - bos + C - 1) / C;
+
+  // state: rows 16 tt + 4 lg + j, column vcol
+  f32x4 S[KT];
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x = 0.f;
+      if (a.h0) {
+        const int64_t off = (((int64_t)n * H + h) * K + 16 * tt + 4 * lg + j) * V + vcol;
+        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
+                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
+      }
+      S[tt][j] = x;
+    }
+
+  auto chunk_start = [&](int64_t it) { return bos + it * C; };
+  auto chunk_len = [&](int64_t it) { return (int)min((int64_t)C, eos - chunk_start(it)); };
+  HColsChunk<K, V> cur, nxt;
+  if (nchunks > 0) hcols_load<K, V>(cur, a, c_first, bos, chunk_len(0), h, vcol);
+  bf16* hT = reinterpret_cast<bf16*>(a.hT);
+  bf16* vnT = reinterpret_cast<bf16*>(a.vnT);
+
+  for (int64_t it = 0; it < nchunks; ++it) {
+    const int64_t c = c_first + it;
+    const int nv = cur.nv;
+    const int64_t t0 = cur.t0;
+#pragma unroll
+    for (int i = 0; i < HP::UK; ++i) {
+      const int u = tid + HP::NT * i, r = u / (K / 8), cc = 8 * (u % (K / 8));
+      const int o = toff<bf16>(r, cc, K);
+      *reinterpret_cast<u32x4*>(s_w + o) = cur.w[i];
+      *reinterpret_cast<u32x4*>(s_k + o) = cur.k[i];
+    }
+    if (wid == 0) s_g[l] = cur.gt;
+    step_barrier();
+    if (it + 1 < nchunks) hcols_load<K, V>(nxt, a, c + 1, chunk_start(it + 1), chunk_len(it + 1), h, vcol);
+
+    // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139)
+    if (a.row_major) {            // h [NC, H, K, V]
+      bf16* p = hT + ((c * H + h) * K + 4 * lg) * (int64_t)V + vcol;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * (int64_t)V] = (bf16)S[tt][j];
+    } else {                      // hT [NC, H, V, K]
+      bf16* p = hT + ((c * H + h) * V + vcol) * (int64_t)K + 4 * lg;
+#pragma unroll
+      for (int tt = 0; tt < KT; ++tt) st4<bf16>(p + 16 * tt, S[tt][0], S[tt][1], S[tt][2], S[tt][3]);
+    }
+    // v' = u - w bf16(S) (chunk_delta_h.py:141-157), rows t = 16 tm + 4 lg + j
+    Frag<bf16> hb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) hb[ks] = frag_from_acc<bf16>(S[2 * ks], S[2 * ks + 1]);
+    const float gl = s_g[nv - 1];
+    f32x4 Y[4], Yg[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) mma(acc, t_acc<bf16>(s_w, K, 16 * tm, 32 * ks), hb[ks]);
+      const f32x4 uv = {bf16_lo(cur.u[tm][0]), bf16_hi(cur.u[tm][0]), bf16_lo(cur.u[tm][1]), bf16_hi(cur.u[tm][1])};
+      Y[tm] = uv - acc;
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(s_g + 16 * tm + 4 * lg);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tm + 4 * lg + j;
+        Yg[tm][j] = t < nv ? Y[tm][j] * gexp(gl - g4[j]) : 0.f;
+      }
+      if (a.row_major) {          // v_new [B*T, H, V]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = 16 * tm + 4 * lg + j;
+          if (t < nv) vnT[((t0 + t) * H + h) * (int64_t)V + vcol] = (bf16)Y[tm][j];
+        }
+      } else {                    // vnT [NC, H, V, 64]
+        st4<bf16>(vnT + ((c * H + h) * V + vcol) * C + 16 * tm + 4 * lg, Y[tm][0], Y[tm][1], Y[tm][2], Y[tm][3]);
+      }
+    }
+    // S = exp(g_last) S + k^T (v' exp(g_last - gc)) (chunk_delta_h.py:163-211)
+    Frag<bf16> vg[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) vg[ks] = frag_from_acc<bf16>(Yg[2 * ks], Yg[2 * ks + 1]);
+    const float eg = gexp(gl);
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      S[tt] *= eg;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) mma(S[tt], t_tr<bf16>(s_k, K, 32 * ks, 16 * tt), vg[ks]);
+    }
+    step_barrier();                                       // the tiles are restaged next chunk
+    cur = nxt;
+  }
+
+  if (a.ht) {
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (((int64_t)n * H + h) * K + 16 * tt + 4 * lg + j) * V + vcol;
+        a.ht[off] = S[tt][j];
+      }
+  }
+}
+
+template <int K, int V>
+int launch_fwd_h_cols(const FwdHArgs& a, hipStream_t s) {
+  using HP = HCols<K, V>;
+  constexpr int nt = HP::NT;
+  constexpr size_t lds = HP::lds;
+  const int total = a.N * a.H;
+  const int grid = (total + 7) / 8 * 8;
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fwd_h_cols_kernel<K, V>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL((fwd_h_cols_kernel<K, V>), dim3(grid), dim3(nt), lds, s, a, total);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 template <typename TK>
 int launch_fwd_h_wide(const FwdHArgs& a, int V, hipStream_t s) {
   const int total = a.N * a.H * ((V + 16 * WW - 1) / (16 * WW));
@@ -600,8 +802,16 @@ int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V
 #define KGDN_H_CASE(TC, TK, KK) \
   if (K == KK) return launch_fwd_h_t<TC, TK, KK>(a, V, s);
 #define KGDN_H_SHAPES(TC, TK) KGDN_H_CASE(TC, TK, 64) KGDN_H_CASE(TC, TK, 128) KGDN_H_CASE(TC, TK, 256)
-  // bf16 K = 256 runs the wide form; the split-K form stays for fp32 (and K <= 128)
+  // bf16 K = 256 runs the wide form; bf16 K, V in {64, 128} the all-columns form
+  // (KAIROS_GDN_FWD_H_COLS=0: the split-K form, which stays for fp32 and fp8 k)
   if (K == 256 && compute_dtype == DT_BF16 && k_dtype == DT_BF16) return launch_fwd_h_wide<bf16>(a, V, s);
+  if (compute_dtype == DT_BF16 && k_dtype == DT_BF16 && (K == 64 || K == 128) && (V == 64 || V == 128)) {
+    const char* e = std::getenv("KAIROS_GDN_FWD_H_COLS");
+    if (!(e && e[0] == '0' && e[1] == 0)) {
+      if (K == 64) return V == 64 ? launch_fwd_h_cols<64, 64>(a, s) : launch_fwd_h_cols<64, 128>(a, s);
+      return V == 64 ? launch_fwd_h_cols<128, 64>(a, s) : launch_fwd_h_cols<128, 128>(a, s);
+    }
+  }
   if (K == 256 && compute_dtype == DT_BF16 && k_dtype == DT_F8E4M3) return launch_fwd_h_wide<uint8_t>(a, V, s);
   if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_H_SHAPES(float, float) }
   if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_H_SHAPES(bf16, bf16) }

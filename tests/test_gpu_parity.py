@@ -184,6 +184,14 @@ def test_fwd_h_and_fwd_o_stages(dt, B, T, H, K, V, cu, with_h0):
     assert rel(host(o), o_r) < TOL[dt]["o"]
 
 
+@pytest.mark.parametrize("dt,B,T,H,K,V,cu,with_h0", [c for c in H_CASES if c[0] == "bf16" and c[4] <= 128])
+def test_fwd_h_split_k_form(dt, B, T, H, K, V, cu, with_h0, monkeypatch):
+    """bf16 K, V <= 128 run the all-columns recurrence; KAIROS_GDN_FWD_H_COLS=0 selects the split-K form,
+    checked here on the same cases."""
+    monkeypatch.setenv("KAIROS_GDN_FWD_H_COLS", "0")
+    test_fwd_h_and_fwd_o_stages(dt, B, T, H, K, V, cu, with_h0)
+
+
 # ---------------------------------------------------------------------------
 # whole op
 # ---------------------------------------------------------------------------
