@@ -736,19 +736,59 @@ __global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
   TC* dq_out = reinterpret_cast<TC*>(a.dq);
   TC* dk_out = reinterpret_cast<TC*>(a.dk1);
   TC* dw_out = reinterpret_cast<TC*>(a.dw);
+  // bf16 with V <= 128: this wave's do, dv2 and v_new rows (the B operands of every K tile) are
+  // loaded once into registers, and each K tile's h and dh fragments are all in flight before its
+  // products
+  constexpr bool kHoist = sizeof(TC) == 2;
+  constexpr int VF = 4;                               // V / 32 fragments held (V <= 128)
+  Frag<TC> fdo[VF], fdv2[VF], fvn[VF];
+  const bool hoist = kHoist && V <= 32 * VF;
+  if (hoist) {
+#pragma unroll
+    for (int vs = 0; vs < VF; ++vs) {
+      if (vs < V / 32) {
+        fdo[vs] = g_nat<TC>(do_row, 32 * vs, tr_ok);
+        fdv2[vs] = g_nat<TC>(dv2_row, 32 * vs, tr_ok);
+        fvn[vs] = g_nat<TC>(vn_row, 32 * vs, tr_ok);
+      }
+    }
+  }
   for (int kt = 0; kt < K / 16; ++kt) {
     f32x4 aq = {0.f, 0.f, 0.f, 0.f}, ak = aq, aw = aq, aq2 = aq, ak2 = aq;
     const TC* hrow = hp + (16 * kt + lc) * (int64_t)V;
     const TC* dhrow = dhp + (16 * kt + lc) * (int64_t)V;
-    for (int vs = 0; vs < V / 32; ++vs) {
-      const Frag<TC> hf = g_nat<TC>(hrow, 32 * vs, true);
-      const Frag<TC> dhf = g_nat<TC>(dhrow, 32 * vs, true);
-      mma(aq, hf, g_nat<TC>(do_row, 32 * vs, tr_ok));       // sum_v h[k][v] do[t][v]
-      mma(aw, hf, g_nat<TC>(dv2_row, 32 * vs, tr_ok));      // sum_v h[k][v] dv2[t][v]
-      mma(ak, dhf, g_nat<TC>(vn_row, 32 * vs, tr_ok));      // sum_v dh[k][v] v_new[t][v]
-      if (wid == 0) {
+    if (hoist) {
+      Frag<TC> hf[VF], dhf[VF];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hdh += fget<TC>(hf, e) * fget<TC>(dhf, e);
+      for (int vs = 0; vs < VF; ++vs) {
+        if (vs < V / 32) {
+          hf[vs] = g_nat<TC>(hrow, 32 * vs, true);
+          dhf[vs] = g_nat<TC>(dhrow, 32 * vs, true);
+        }
+      }
+#pragma unroll
+      for (int vs = 0; vs < VF; ++vs) {
+        if (vs < V / 32) {
+          mma(aq, hf[vs], fdo[vs]);                   // sum_v h[k][v] do[t][v]
+          mma(aw, hf[vs], fdv2[vs]);                  // sum_v h[k][v] dv2[t][v]
+          mma(ak, dhf[vs], fvn[vs]);                  // sum_v dh[k][v] v_new[t][v]
+          if (wid == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hdh += fget<TC>(hf[vs], e) * fget<TC>(dhf[vs], e);
+          }
+        }
+      }
+    } else {
+      for (int vs = 0; vs < V / 32; ++vs) {
+        const Frag<TC> hf = g_nat<TC>(hrow, 32 * vs, true);
+        const Frag<TC> dhf = g_nat<TC>(dhrow, 32 * vs, true);
+        mma(aq, hf, g_nat<TC>(do_row, 32 * vs, tr_ok));     // sum_v h[k][v] do[t][v]
+        mma(aw, hf, g_nat<TC>(dv2_row, 32 * vs, tr_ok));    // sum_v h[k][v] dv2[t][v]
+        mma(ak, dhf, g_nat<TC>(vn_row, 32 * vs, tr_ok));    // sum_v dh[k][v] v_new[t][v]
+        if (wid == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hdh += fget<TC>(hf, e) * fget<TC>(dhf, e);
+        }
       }
     }
 #pragma unroll
