@@ -97,15 +97,23 @@ __device__ __forceinline__ Frag<TC> acc_frag(const f32x4& a, const f32x4& b) {
   return f;
 }
 
-// stage 64 token rows [t0, t0 + nv) of a row-major [*, H, ncol] tensor into a tile (zeros past nv)
+// stage 64 token rows [t0, t0 + nv) of a row-major [*, H, ncol] tensor into a tile (zeros past nv),
+// four units per thread in flight at a time (every load of a batch is issued before its stores)
 template <typename TC>
 __device__ __forceinline__ void stage_rows(TC* tile, const TC* src, int64_t t0, int nv, int H, int h, int ncol) {
-  const int per_row = ncol / 8;
-  for (int idx = threadIdx.x; idx < 64 * per_row; idx += blockDim.x) {
-    const int r = idx / per_row, c8 = (idx % per_row) * 8;
-    Vec8<TC> x = vzero<TC>();
-    if (r < nv) x = ld8<TC>(src + ((t0 + r) * H + h) * (int64_t)ncol + c8);
-    st8<TC>(tile + toff<TC>(r, c8, ncol), x);
+  const int per_row = ncol / 8, total = 64 * per_row, nt = blockDim.x;
+  for (int base = threadIdx.x; base < total; base += 4 * nt) {
+    Vec8<TC> x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = base + i * nt, r = idx / per_row, c8 = (idx % per_row) * 8;
+      x[i] = (idx < total && r < nv) ? ld8<TC>(src + ((t0 + r) * H + h) * (int64_t)ncol + c8) : vzero<TC>();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = base + i * nt, r = idx / per_row, c8 = (idx % per_row) * 8;
+      if (idx < total) st8<TC>(tile + toff<TC>(r, c8, ncol), x[i]);
+    }
   }
 }
 

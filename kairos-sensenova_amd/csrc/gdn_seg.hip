@@ -44,6 +44,7 @@
 
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
+#include "gdn_tiles.hpp"
 
 namespace kgdn {
 
@@ -2320,36 +2321,62 @@ __global__ __launch_bounds__(256) void seg_place_kernel(SegGeom G, const void* s
   if (first_seg && !pick) return;
   float* d = dst + ((int64_t)s * H + h) * KV;
   const int64_t so = ((int64_t)sl.n * H + h) * KV;
-  for (int i = threadIdx.x; i < KV; i += blockDim.x) {
-    float x = 0.f;
-    if (pick && src)
-      x = src_dtype == DT_F32 ? reinterpret_cast<const float*>(src)[so + i]
-                              : (float)reinterpret_cast<const bf16*>(src)[so + i];
-    d[i] = x;
+  for (int i = 4 * threadIdx.x; i < KV; i += 4 * blockDim.x) {     // KV is a multiple of 4
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    if (pick && src) {
+      if (src_dtype == DT_F32) {
+        x = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + so + i);
+      } else {
+        const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const bf16*>(src) + so + i);
+        x = f32x4{bf16_lo(r.x), bf16_hi(r.x), bf16_lo(r.y), bf16_hi(r.y)};
+      }
+    }
+    *reinterpret_cast<f32x4*>(d + i) = x;
   }
 }
 
-// Reverse scan of the dh recurrence over the segments of a sequence (one workgroup per
-// (sequence, head, 16 value columns)).  Across segment j the state gradient maps as
-// dh_start(j) = M_j^T dh_start(j + 1) + B_j, with M_j the forward's segment map (seg_trans,
-// a bf16 pair hi + lo) and B_j the dh recurrence of segment j run from zero.  The last
-// segment has no map (seg_trans skips it): its Bseg entry is its recurrence from dht, which
-// is dh_start(last) itself.  Writes F_j = dh_start(j + 1) (F_last = dht), the state each
-// segment's final pass starts from, and dh0 = dh_start(0) (when dh0 is not null).
+// Reverse scan of the dh recurrence over the segments of a sequence, one workgroup per
+// (sequence, head), V / 16 waves each owning 16 value columns over all K rows (fp32
+// accumulator tiles in VGPRs).  Across segment j the state gradient maps as
+// dh_start(j) = M_j^T dh_start(j + 1) + B_j, with M_j the forward's segment map (seg_trans, a
+// bf16 pair hi + lo) and B_j the dh recurrence of segment j run from zero.  The last segment
+// has no map (seg_trans skips it): its Bseg entry is its recurrence from dht, which is
+// dh_start(last) itself.  Writes F_j = dh_start(j + 1) (F_last = dht), the state each segment's
+// final pass starts from, and dh0 = dh_start(0) (when dh0 is not null).  M_j^T X runs on the
+// bf16 MFMA as hi hi + hi lo + lo hi (x = hi + lo on both sides, fp32 accumulation): M_j is
+// staged in LDS as K / 64 tiles of [64 rows][K] and read transposed; X's accumulator tiles are
+// the B operand.  The next step's map is loaded into registers while the current one computes.
+template <int K, int V>
+struct RCfg {
+  static constexpr int NW = V / 16, NT = NW * WAVE;
+  static constexpr int KT = K / 16, KS = K / 32;
+  static constexpr int EM = K * K;                       // elements of one bf16 half of a map
+  static constexpr int UM = 2 * EM / 8 / NT;             // 16-byte units of (hi, lo) per thread
+  static_assert(2 * EM % (8 * NT) == 0, "units split evenly over the threads");
+  static constexpr size_t lds = (size_t)2 * EM * 2;
+};
+
+// offset of element (r, c) of a [K][K] map staged as K / 64 tiles of 64 rows (toff layout)
 template <int K>
-__global__ __launch_bounds__(256) void seg_bwd_combine_kernel(SegGeom G, const bf16* __restrict__ M,
-                                                              const float* __restrict__ Bseg,
-                                                              const float* __restrict__ dht, float* __restrict__ F,
-                                                              float* __restrict__ dh0, int V, int total) {
-  constexpr int NT = 256, CPT = 16 * K / NT;              // columns per thread (of the 16)
-  static_assert(CPT % 4 == 0, "float4 column groups");
-  __shared__ __align__(16) float s_X[K][16];
-  const int unit_id = blockIdx.x;
-  if (unit_id >= total) return;
-  const int nvt = V / 16;
-  const int unit = unit_id / nvt, v0 = (unit_id % nvt) * 16;
+__device__ __forceinline__ int moff(int r, int c) { return (r >> 6) * 64 * K + toff<bf16>(r & 63, c, K); }
+
+template <int K, int V>
+__global__ __launch_bounds__((RCfg<K, V>::NT)) void seg_bwd_combine_kernel(SegGeom G, const bf16* __restrict__ M,
+                                                                          const float* __restrict__ Bseg,
+                                                                          const float* __restrict__ dht,
+                                                                          float* __restrict__ F,
+                                                                          float* __restrict__ dh0, int total) {
+  using RC = RCfg<K, V>;
+  constexpr int KT = RC::KT, KS = RC::KS;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* s_mh = reinterpret_cast<bf16*>(smem);
+  bf16* s_ml = s_mh + RC::EM;
+  const int per_xcd = gridDim.x / 8;
+  const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (unit >= total) return;
   const int H = G.H, n = unit / H, h = unit % H;
-  const int a_row = threadIdx.x % K, c0 = (threadIdx.x / K) * CPT;
+  const int tid = threadIdx.x, wid = tid / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int col = 16 * wid + lc;
   int nseg, s_first;
   if (G.cu == nullptr) {
     nseg = G.T > 0 ? G.nseg_fixed : 0;
@@ -2359,47 +2386,94 @@ __global__ __launch_bounds__(256) void seg_bwd_combine_kernel(SegGeom G, const b
     s_first = G.seg_off[n];
   }
   const int64_t KV = (int64_t)K * V;
-  const int64_t col = (int64_t)a_row * V + v0 + c0;       // offset of this thread's columns in a K x V block
-  float x[CPT];
+  // lane element (tt, j): row 16 tt + 4 lg + j, column col
+  auto blk = [&](int64_t b) { return b * KV + (int64_t)(4 * lg) * V + col; };
+  f32x4 X[KT];
+  const int64_t dn = ((int64_t)n * H + h);
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) X[tt][j] = dht ? dht[blk(dn) + (16 * tt + j) * V] : 0.f;
   if (nseg > 0) {
-    const int64_t last = ((int64_t)(s_first + nseg - 1) * H + h) * KV;
+    const int64_t last = (int64_t)(s_first + nseg - 1) * H + h;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const float d = dht ? dht[((int64_t)n * H + h) * KV + col + c] : 0.f;
-      F[last + col + c] = d;
-      x[c] = Bseg[last + col + c];
-    }
-  } else {                                                // empty sequence: dh0 = dht
+    for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) x[c] = dht ? dht[((int64_t)n * H + h) * KV + col + c] : 0.f;
+      for (int j = 0; j < 4; ++j) {
+        F[blk(last) + (16 * tt + j) * V] = X[tt][j];
+        X[tt][j] = Bseg[blk(last) + (16 * tt + j) * V];
+      }
   }
+  // maps of step j (hi then lo, row-major) as 16-byte units tid + NT i
+  u32x4 mcur[RC::UM], mnxt[RC::UM];
+  f32x4 bcur[KT], bnxt[KT];
+  auto load = [&](int j, u32x4 (&m)[RC::UM], f32x4 (&b)[KT]) {
+    const int64_t sj = (int64_t)(s_first + j) * H + h;
+    const u32x4* src = reinterpret_cast<const u32x4*>(M + sj * 2 * K * K);
+#pragma unroll
+    for (int i = 0; i < RC::UM; ++i) m[i] = src[tid + RC::NT * i];
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) b[tt][jj] = Bseg[blk(sj) + (16 * tt + jj) * V];
+  };
+  if (nseg >= 2) load(nseg - 2, mcur, bcur);
   for (int j = nseg - 2; j >= 0; --j) {
-    const int64_t blk = ((int64_t)(s_first + j) * H + h) * KV;
+    const int64_t sj = (int64_t)(s_first + j) * H + h;
 #pragma unroll
-    for (int c = 0; c < CPT; c += 4) {
-      const f32x4 v4 = {x[c], x[c + 1], x[c + 2], x[c + 3]};
-      *reinterpret_cast<f32x4*>(&s_X[a_row][c0 + c]) = v4;
-      *reinterpret_cast<f32x4*>(F + blk + col + c) = v4;
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) F[blk(sj) + (16 * tt + jj) * V] = X[tt][jj];
+#pragma unroll
+    for (int i = 0; i < RC::UM; ++i) {
+      const int e = 8 * (tid + RC::NT * i);              // element of [hi | lo]
+      const int half = e / RC::EM, r = (e % RC::EM) / K, c = e % K;
+      *reinterpret_cast<u32x4*>((half ? s_ml : s_mh) + moff<K>(r, c)) = mcur[i];
     }
+    lds_barrier();
+    if (j > 0) load(j - 1, mnxt, bnxt);
+    // X = M_j^T X + B_j: A[a][b] = M[b][a] read transposed (rows b in the accumulator order)
+    Frag<bf16> xh[KS], xl[KS];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) x[c] = Bseg[blk + col + c];
-    __syncthreads();
-    const bf16* mh = M + ((int64_t)(s_first + j) * H + h) * 2 * K * K + a_row;
-#pragma unroll 16
-    for (int b = 0; b < K; ++b) {                        // (M^T X)[a] = sum_b M[b][a] X[b]
-      const float m = (float)mh[b * K] + (float)mh[K * K + b * K];
+    for (int ks = 0; ks < KS; ++ks) {
+      float v8[8];
 #pragma unroll
-      for (int c = 0; c < CPT; c += 4) {
-        const f32x4 xs = *reinterpret_cast<const f32x4*>(&s_X[b][c0 + c]);
+      for (int e = 0; e < 4; ++e) {
+        v8[e] = X[2 * ks][e];
+        v8[4 + e] = X[2 * ks + 1][e];
+      }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[c + e] = fmaf(m, xs[e], x[c + e]);
+      for (int e = 0; e < 8; ++e) {
+        const bf16 hi = (bf16)v8[e];
+        xh[ks].v[e] = hi;
+        xl[ks].v[e] = (bf16)(v8[e] - (float)hi);
       }
     }
-    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < KT; ++rt) {
+      f32x4 acc = bcur[rt], acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int tb = (32 * ks) >> 6, k0 = (32 * ks) & 63;
+        const Frag<bf16> ah = tr_frag<64>(s_mh + tb * 64 * K + (16 * rt >> 6) * 4096, k0 >> 5, (16 * rt) & 63);
+        const Frag<bf16> al = tr_frag<64>(s_ml + tb * 64 * K + (16 * rt >> 6) * 4096, k0 >> 5, (16 * rt) & 63);
+        mma(acc, ah, xh[ks]);
+        mma(acc2, ah, xl[ks]);
+        mma(acc2, al, xh[ks]);
+      }
+      X[rt] = acc + acc2;
+    }
+    lds_barrier();                                      // the map is restaged next step
+#pragma unroll
+    for (int i = 0; i < RC::UM; ++i) mcur[i] = mnxt[i];
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) bcur[tt] = bnxt[tt];
   }
   if (dh0) {
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) dh0[((int64_t)n * H + h) * KV + col + c] = x[c];
+    for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) dh0[blk(dn) + (16 * tt + jj) * V] = X[tt][jj];
   }
 }
 
@@ -2499,18 +2573,23 @@ int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float*
 int launch_seg_bwd_combine(const SegFwdArgs& p, const float* Bseg, const float* dht, float* F, float* dh0, int K,
                            int V, hipStream_t s) {
   const SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
-  const int total = p.N * p.H * (V / 16);
+  const int total = p.N * p.H;
   if (total <= 0) return 0;
+  const int grid = (total + 7) / 8 * 8;
   const bf16* M = reinterpret_cast<const bf16*>(p.M);
-  if (K == 64)
-    hipLaunchKernelGGL((seg_bwd_combine_kernel<64>), dim3((unsigned)total), dim3(256), 0, s, G, M, Bseg, dht, F, dh0,
-                       V, total);
-  else if (K == 128)
-    hipLaunchKernelGGL((seg_bwd_combine_kernel<128>), dim3((unsigned)total), dim3(256), 0, s, G, M, Bseg, dht, F, dh0,
-                       V, total);
-  else
-    return -2;
-  return hipGetLastError() == hipSuccess ? 0 : -1;
+#define KGDN_RC(KK, VV)                                                                                     \
+  if (K == KK && V == VV) {                                                                                 \
+    using RC = RCfg<KK, VV>;                                                                                \
+    constexpr int nt = RC::NT;                                                                              \
+    constexpr size_t lds = RC::lds;                                                                         \
+    if (set_lds(seg_bwd_combine_kernel<KK, VV>, lds)) return -1;                                            \
+    hipLaunchKernelGGL((seg_bwd_combine_kernel<KK, VV>), dim3(grid), dim3(nt), lds, s, G, M, Bseg, dht, F, dh0, \
+                       total);                                                                              \
+    return hipGetLastError() == hipSuccess ? 0 : -1;                                                        \
+  }
+  KGDN_RC(64, 64) KGDN_RC(64, 128) KGDN_RC(128, 64) KGDN_RC(128, 128)
+#undef KGDN_RC
+  return -2;
 }
 
 int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s) {
