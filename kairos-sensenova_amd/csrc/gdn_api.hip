@@ -243,10 +243,12 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
   size_t total = stage_ws(n_seqs);
   total += align_up(tok * sizeof(float));                 // gc
   total += align_up(tok * K * es);                        // w
-  total += align_up(nc * H * V * kgdn::C * es);           // uT
   if (wide) {
     total += align_up(nc * H * kgdn::C * kgdn::C * es);   // Aqk
+    total += align_up(tok * kgdn::C * es);                // Ai
+    total += align_up(tok * sizeof(float));               // beta (fp32)
   } else {
+    total += align_up(nc * H * V * kgdn::C * es);         // uT
     total += align_up(nc * H * V * K * es);               // hT
     total += align_up(nc * H * V * kgdn::C * es);         // vnT
   }
@@ -308,14 +310,19 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
   float* gc = static_cast<float*>(cv.take(tok * sizeof(float)));
   void* w = cv.take(tok * K * es);
-  void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
   const bool wide = use_wide_fused(cdt, qk_dtype, G.K, G.V);
+  void* uT = nullptr;
   void* hT = nullptr;
   void* vnT = nullptr;
   void* aqk = nullptr;
+  void* ai = nullptr;
+  float* bf = nullptr;
   if (wide) {
     aqk = cv.take((size_t)G.nc * H * kgdn::C * kgdn::C * es);
+    ai = cv.take(tok * kgdn::C * es);
+    bf = static_cast<float*>(cv.take(tok * sizeof(float)));
   } else {
+    uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
     hT = cv.take((size_t)G.nc * H * V * K * es);
     vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
   }
@@ -325,13 +332,13 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
     pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
-    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = nullptr;
-    pa.q = q; pa.aqk_out = aqk;                          // Aqk for the fused K = 256 form
+    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = ai;
+    pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;        // the fused K = 256 form: Aqk, Ai, beta, no u
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, G.nc, s), "prepare")) return rc;
   }
   if (wide) {
     kgdn::WideFusedArgs fa{};
-    fa.q = q; fa.k = k; fa.w = w; fa.uT = uT; fa.gc = gc; fa.aqk = aqk;
+    fa.q = q; fa.k = k; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
     fa.h0 = h0; fa.h0_dtype = h0_dtype;
     fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
     fa.scale = scale; fa.o = o; fa.ht = ht;

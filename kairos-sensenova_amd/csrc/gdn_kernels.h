@@ -38,6 +38,8 @@ struct PrepareArgs {
   void* Ai_out;           // optional out [B*T, H, 64]
   const void* q;          // [B*T, H, K] (qk dtype), read only with aqk_out
   void* aqk_out;          // optional out [NC, H, 64, 64]: mask_{i>=j}(q k^T exp(gc_i - gc_j)) (compute dtype)
+  float* beta_out;        // optional out [B*T, H] fp32 beta
+  // uT == nullptr: no u pass (v is not read)
 };
 
 struct FwdHArgs {
@@ -76,13 +78,15 @@ struct FwdOArgs {
   void* o;                // out [B*T, H, V] compute dtype
 };
 
-// Fused recurrence + output for K = 256 (gdn_wide.hip), after launch_prepare (gc, w, uT and, with
-// aqk_out, Aqk).  bf16 q, k, w, u; V a multiple of 64.
+// Fused recurrence + output for K = 256 (gdn_wide.hip), after launch_prepare without its u pass
+// (gc, w, Ai, fp32 beta and Aqk); u = Ai bf16(beta v) is formed in the kernel.  bf16 q, k, w, u; V a multiple of 64.
 struct WideFusedArgs {
   const void* q;          // [B*T, H, 256] bf16
   const void* k;          // [B*T, H, 256] bf16
+  const void* v;          // [B*T, H, V] bf16
   const void* w;          // [B*T, H, 256] bf16
-  const void* uT;         // [NC, H, V, 64] bf16
+  const void* Ai;         // [B*T, H, 64] bf16 (I + A)^-1 rows (launch_prepare's Ai_out)
+  const float* beta;      // [B*T, H] fp32 (launch_prepare's beta_out)
   const float* gc;        // [B*T, H]
   const void* aqk;        // [NC, H, 64, 64] bf16 (launch_prepare's aqk_out)
   const void* h0;         // [N, H, 256, V] (h0_dtype) or nullptr

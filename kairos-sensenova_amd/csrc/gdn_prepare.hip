@@ -105,6 +105,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
     s_eg[l] = gexp(gv);
     s_b[l] = bv;
     if (l < nv) a.gc[(t0 + l) * H + h] = gv;
+    if (a.beta_out && l < nv) a.beta_out[(t0 + l) * H + h] = bv;
   }
   __syncthreads();
 
@@ -146,7 +147,8 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
       }
     }
   };
-  if (v_vec) load_v(0);
+  const bool want_u = a.uT != nullptr;                   // without uT: no u pass (the fused K = 256 form forms u)
+  if (v_vec && want_u) load_v(0);
 
   // ---- stage k (row-major, for K.K^T) and the transposed, scaled operand
   //      kb^T[d][t] = k*beta*exp(gc).  Lane = token pair, so each transposed store packs the pair
@@ -343,7 +345,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after Ai,
   //      so staging overlaps the w products above
   TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
-  for (int p0 = 0; p0 < V; p0 += L::VP) {
+  for (int p0 = 0; want_u && p0 < V; p0 += L::VP) {
     const int vw = min(L::VP, V - p0);             // a multiple of 16
     if (v_vec) {                                   // from registers, token pairs packed per store
       const float b0 = s_b[2 * pr], b1 = s_b[2 * pr + 1];

@@ -37,6 +37,8 @@ constexpr int FK = 256;           // K
 constexpr int FW = 4;             // waves per workgroup, 16 state columns each
 constexpr int FVT = 16 * FW;      // value columns per workgroup
 constexpr int NT_F = FW * WAVE;
+constexpr int kSmallLoads = 6;    // direct loads per wave of a chunk's Aqk, Ai and v tiles (2 each)
+constexpr int kPrefetchLoads = 1; // direct loads per wave of the L2 prefetch (w, q, k rows or Aqk lines)
 
 // Workgroup barrier on LDS only (lgkmcnt(0), s_barrier): the next chunk's global loads and this
 // chunk's o stores stay in flight across it.
@@ -81,6 +83,14 @@ __device__ __forceinline__ void dma4_(const void* base, uint32_t off, uint32_t l
 // vmcnt(0) through the builtin, so the compiler's own wait tracking sees every load complete
 __device__ __forceinline__ void wait_all_loads() {
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
+// vmcnt(N): all but the wave's last N vector memory operations complete (they complete in issue
+// order); expcnt and lgkmcnt at their maxima
+template <int N>
+__device__ __forceinline__ void wait_loads_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
 }
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
@@ -166,17 +176,12 @@ __device__ __forceinline__ void f_addr(FAddr& A, uint32_t w_lds, uint32_t k_lds,
   }
 }
 
-// u of the wave's 16 columns for one chunk, in the accumulator layout (rows 16 tm + 4 lg + j).
-struct FChunk {
-  u32x2 u[4];
-  int nv;
-};
-
 // Lane parts of the global offsets, fixed for the whole sequence.
 struct FOff {
   uint32_t tile[2];           // [64][256] tile direct loads: row tid / 32 (+ 8 i), swizzled chunk, i even / odd
-  uint32_t aqk[2];            // Aqk tile direct loads, i = 0, 1
-  uint32_t u;                 // u of lane (lc, lg) within the wave's uT block
+  uint32_t aqk[2];            // Aqk tile direct loads ([NC, H, 64, 64]), i = 0, 1
+  uint32_t row64[2];          // [64][64] tiles of token-major rows (Ai, v): row p / 8, swizzled chunk, i = 0, 1
+  int r64[2];                 // their rows
   uint32_t o;                 // o of lane: token lc, columns 4 lg .. (bytes from the wave's row-0 base)
 };
 
@@ -193,8 +198,9 @@ __device__ __forceinline__ void f_off(FOff& F, int H, int V) {
   for (int i = 0; i < 2; ++i) {
     const int p = tid + 256 * i, r = p >> 3, ps = p & 7;
     F.aqk[i] = (uint32_t)(r * C + 8 * (ps ^ swz64(r))) * 2u;
+    F.row64[i] = 16u * (uint32_t)(ps ^ swz64(r));
+    F.r64[i] = r;
   }
-  F.u = (uint32_t)(lc * C + 4 * lg) * 2u;
   F.o = ((uint32_t)lc * (uint32_t)(H * V) + 4u * lg) * 2u;
 }
 
@@ -220,15 +226,30 @@ __device__ __forceinline__ void dma_tile256(const void* x, const FOff& F, int64_
   }
 }
 
+// Direct loads of a swizzled [64][64] bf16 tile (swz64) whose token rows are row_bytes apart
+// (rows past the chunk's end read row 0).
+__device__ __forceinline__ void dma_tile64(const unsigned char* base, uint32_t row_bytes, const FOff& F, int nv,
+                                           uint32_t dst) {
+  const int wid = threadIdx.x / WAVE;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t rr = F.r64[i] < nv ? (uint32_t)F.r64[i] : 0u;
+    dma16_(base, rr * row_bytes + F.row64[i], dst + 16u * (256 * i + 64 * wid));
+  }
+}
+
 __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V, int total_units) {
-  // s_w and s_q adjacent (q reads are w reads + 32 KB); the two k / Aqk / gc buffer sets 64 KB,
-  // 8 KB and 256 bytes apart
+  // LDS: w and q of the chunk (adjacent: q reads are w reads + 32 KB), k of the chunk, and two
+  // buffer sets of the chunk's small tiles: Aqk, Ai, the v tile of the workgroup's 64 columns, gc, beta
   __shared__ __align__(16) bf16 s_wq[2 * C * FK];
-  __shared__ __align__(16) bf16 s_k[2 * C * FK];
+  __shared__ __align__(16) bf16 s_k[C * FK];
   __shared__ __align__(16) bf16 s_a[2 * C * C];
+  __shared__ __align__(16) bf16 s_ai[2 * C * C];
+  __shared__ __align__(16) bf16 s_v[2 * C * C];
   __shared__ __align__(16) float s_g[2 * C];
-  __shared__ __align__(16) float s_pf[NT_F];              // landing words of the L2 prefetch
-  constexpr uint32_t QOFF = C * FK * 2, KBUF = C * FK * 2, ABUF = C * C * 2, GBUF = C * 4;
+  __shared__ __align__(16) float s_b[2 * C];
+  __shared__ __align__(16) float s_pf[WAVE];              // landing words of the L2 prefetch
+  constexpr uint32_t QOFF = C * FK * 2, ABUF = C * C * 2, GBUF = C * 4;
 
   // XCD-aware order: the V tiles of one head run on one XCD and share its q, k, w, Aqk in L2
   const int per_xcd = gridDim.x / 8;
@@ -239,7 +260,8 @@ __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V
   const int H = a.H;
   const int n = unit / H, h = unit % H;
   const int tid = threadIdx.x, wid = tid / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
-  const int v0 = __builtin_amdgcn_readfirstlane((o_idx % nvt) * FVT + 16 * wid);   // this wave's first column
+  const int vt0 = __builtin_amdgcn_readfirstlane((o_idx % nvt) * FVT);    // the workgroup's first column
+  const int v0 = vt0 + 16 * wid;                          // this wave's first column
   const int vcol = v0 + lc;
 
   int64_t bos, eos, c_first;
@@ -270,73 +292,76 @@ __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V
       S[kt][j] = x;
     }
   }
-  const uint32_t w_lds = lds_u32(s_wq), k_lds = lds_u32(s_k), a_lds = lds_u32(s_a), g_lds = lds_u32(s_g);
+  const uint32_t w_lds = lds_u32(s_wq), k_lds = lds_u32(s_k), a_lds = lds_u32(s_a), ai_lds = lds_u32(s_ai),
+                 v_lds = lds_u32(s_v), g_lds = lds_u32(s_g), b_lds = lds_u32(s_b);
   FAddr A;
   f_addr(A, w_lds, k_lds, a_lds);
   FOff F;
   f_off(F, H, V);
-  const bf16* uTb = reinterpret_cast<const bf16*>(a.uT);
   const bf16* aqb = reinterpret_cast<const bf16*>(a.aqk);
   unsigned char* ob = reinterpret_cast<unsigned char*>(a.o) + (size_t)v0 * 2;
+  const uint32_t AI_OFF = ai_lds - a_lds;                 // Ai tiles share the Aqk lane addresses
 
-  auto load_u = [&](FChunk& P, int64_t c, int nv) {
-    P.nv = nv;
-    const unsigned char* ub = reinterpret_cast<const unsigned char*>(uTb + ((c * H + h) * V + v0) * C);
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) P.u[tm] = *reinterpret_cast<const u32x2*>(ub + F.u + 32 * tm);
-  };
-  // k tile, Aqk tile and gc of chunk (c, t0) into buffer set B
-  auto dma_kag = [&](int64_t c, int64_t t0, int nv, uint32_t B) {
-    dma_tile256(a.k, F, t0, nv, h, H, k_lds + B * KBUF);
+  // the chunk's small tiles into buffer set B: Aqk, Ai, the v tile, gc (wave 0), beta (wave 1)
+  auto dma_small = [&](int64_t c, int64_t t0, int nv, uint32_t B) {
     const unsigned char* ab = reinterpret_cast<const unsigned char*>(aqb + (c * H + h) * (int64_t)(C * C));
 #pragma unroll
     for (int i = 0; i < 2; ++i) dma16_(ab, F.aqk[i], a_lds + B * ABUF + 16u * (256 * i + 64 * wid));
+    dma_tile64(reinterpret_cast<const unsigned char*>(a.Ai) + (size_t)((t0 * H + h) * C) * 2, (uint32_t)H * C * 2, F,
+               nv, ai_lds + B * ABUF);
+    dma_tile64(reinterpret_cast<const unsigned char*>(a.v) + (size_t)((t0 * H + h) * V + vt0) * 2, (uint32_t)H * V * 2,
+               F, nv, v_lds + B * ABUF);
     if (wid == 0) dma4_(a.gc + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, g_lds + B * GBUF);
+    if (wid == 1) dma4_(a.beta + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, b_lds + B * GBUF);
   };
-
   // L2 prefetch of chunk (c, t0)'s w, q, k rows and Aqk tile: one 4-byte direct load per 128-byte
-  // line into a scratch LDS word, so that the tile loads a step later hit L2 (the V tiles of a head
-  // share it) instead of waiting for HBM.
-  const uint32_t pf_lds = lds_u32(s_pf) + 256u * wid;
+  // line into a scratch LDS word (shared by the waves: never read), so that the tile loads a step
+  // later hit L2 instead of waiting for HBM.  The V tiles of a head share the XCD's L2, so each
+  // workgroup touches a quarter of the lines (rows 16 (vt % 4) .. + 15): waves 0-2 one line per lane
+  // of w, q, k, wave 3 16 lines of Aqk.  The address unit works per line, so a full prefetch per
+  // workgroup would cost as much of it as the tile loads themselves.
+  const uint32_t pf_lds = lds_u32(s_pf);
+  const int pf_r = 16 * ((vt0 / FVT) & 3);
   auto prefetch = [&](int64_t c, int64_t t0, int nv) {
-    const int r = tid >> 2;
-    const uint32_t off = (uint32_t)(r < nv ? r : 0) * (uint32_t)H * FK * 2 + 128u * (tid & 3);
-    const size_t tb = (size_t)((t0 * H + h) * FK) * 2;
-    dma4_(reinterpret_cast<const unsigned char*>(a.w) + tb, off, pf_lds);
-    dma4_(reinterpret_cast<const unsigned char*>(a.q) + tb, off, pf_lds);
-    dma4_(reinterpret_cast<const unsigned char*>(a.k) + tb, off, pf_lds);
-    if (wid == 0) dma4_(aqb + (c * H + h) * (int64_t)(C * C), 128u * l, pf_lds);
+    if (__builtin_amdgcn_readfirstlane(wid) < 3) {
+      const int r = pf_r + (l >> 2);
+      const uint32_t off = (uint32_t)(r < nv ? r : 0) * (uint32_t)H * FK * 2 + 128u * (l & 3);
+      const void* x = wid == 0 ? a.w : wid == 1 ? a.q : a.k;
+      dma4_(reinterpret_cast<const unsigned char*>(x) + (size_t)((t0 * H + h) * FK) * 2, off, pf_lds);
+    } else {
+      dma4_(aqb + (c * H + h) * (int64_t)(C * C), 128u * (pf_r + (l & 15)), pf_lds);
+    }
   };
 
-  // One chunk step, two barriers.  On entry the direct loads of chunk it (w, q into their tiles;
-  // k, Aqk, gc into buffer set B = it % 2) and cur's u are in flight.  After B1 the k / Aqk / gc
-  // loads of chunk it + 1 go out into the other buffer set; w and q of chunk it + 1 go out after B2,
-  // once every wave is done with the w h and h^T q^T products of chunk it.
-  auto step = [&](auto BB, FChunk& cur, FChunk& nxt, int64_t it) {
+  // One chunk step, two barriers.  On entry w and q of chunk it (their tiles) and its small tiles
+  // (buffer set B = it % 2) are in flight.  After B1: k of chunk it, then the small tiles of chunk
+  // it + 1 (other set) and the L2 prefetch of chunk it + 2; then w h and h^T q^T.  B2 waits for k
+  // alone (the later loads stay in flight for a step); after it (every wave is done with w and q):
+  // w and q of chunk it + 1; then u, v', o and the state update.
+  auto step = [&](auto BB, int64_t it) {
     constexpr uint32_t B = decltype(BB)::value;
     const int64_t t0 = bos + it * C;
-    const int nv = cur.nv;
+    const int nv = chunk_nv(it);
     const int64_t in = it + 1 < nchunks ? it + 1 : it;    // the last step reloads its own chunk (unused)
     const int nv1 = chunk_nv(in);
     wait_all_loads();
     f_barrier();                                          // B1
-    dma_kag(c_first + in, bos + in * C, nv1, B ^ 1u);
-    load_u(nxt, c_first + in, nv1);
-    if (it + 2 < nchunks) prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
+    dma_tile256(a.k, F, t0, nv, h, H, k_lds);
+    dma_small(c_first + in, bos + in * C, nv1, B ^ 1u);
+    const bool pf = it + 2 < nchunks;
+    if (pf) prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
     const float* sg = s_g + B * C;
+    const float* sb = s_b + B * C;
 
     // w h (rows t, this wave's columns) and o_inter^T = h^T q^T (rows = columns, cols = t), with
     // h = bf16(S) packed per 32-deep step as the B (w h) and A (h^T q^T) operand: K = state rows
-    // in the accumulator order
+    // in the accumulator order; operand reads one step ahead of the products
     f32x4 acc[4], oi[4];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
       acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
       oi[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    // software pipelined over the eight 32-deep steps: the operand reads of step ks + 1 are issued
-    // before the products of step ks; the scheduling barriers keep the compiler from hoisting more
-    // reads than that (every read in flight holds registers)
     Frag<bf16> wa[2][4], qa[2][4];
     auto read_wq = [&](int ks, Frag<bf16>(&w4)[4], Frag<bf16>(&q4)[4]) {
       const uint32_t ra = A.row[0][ks & 3], rb = A.row[1][ks & 3];
@@ -360,17 +385,47 @@ __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    f_barrier();                                          // B2: w and q tiles free
+    // k of this chunk: the loads issued after it (6 + one gc / beta row in waves 0 and 1, one of
+    // the prefetch) may stay in flight
+    if (__builtin_amdgcn_readfirstlane(wid) < 2) {
+      if (pf) wait_loads_but<kSmallLoads + 1 + kPrefetchLoads>();
+      else wait_loads_but<kSmallLoads + 1>();
+    } else {
+      if (pf) wait_loads_but<kSmallLoads + kPrefetchLoads>();
+      else wait_loads_but<kSmallLoads>();
+    }
+    f_barrier();                                          // B2: k in LDS; w and q tiles free
     dma_tile256(a.w, F, bos + in * C, nv1, h, H, w_lds);
     dma_tile256(a.q, F, bos + in * C, nv1, h, H, w_lds + QOFF);
 
+    // u = Ai bf16(beta v) (wy_fast.py:55-81), rounded to bf16 as the reference stores it; the v tile
+    // is read transposed (rows t in the accumulator order) and scaled by beta per row
+    Frag<bf16> vb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const Frag<bf16> vr = tr_frag<64>(s_v + B * C * C, ks, 16 * wid);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(sb + 32 * ks + 4 * lg);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(sb + 32 * ks + 16 + 4 * lg);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vb[ks].v[e] = (bf16)((float)vr.v[e] * b0[e]);
+        vb[ks].v[4 + e] = (bf16)((float)vr.v[4 + e] * b1[e]);
+      }
+    }
     // v' = u - w h (rows t = 16 tm + 4 lg + j), its bf16 value and the gated form
     const float gl = sg[nv - 1];
     f32x4 Y[4], Yg[4];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
-      const f32x4 uv = {lo16(cur.u[tm][0]), hi16(cur.u[tm][0]), lo16(cur.u[tm][1]), hi16(cur.u[tm][1])};
-      Y[tm] = uv - acc[tm];
+      f32x4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        if (ks <= tm / 2)
+          mma(u, frag2(ld64(A.aq[ks][0], AI_OFF + B * ABUF + 2048u * tm), ld64(A.aq[ks][1], AI_OFF + B * ABUF + 2048u * tm)),
+              vb[ks]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) u[j] = (float)(bf16)u[j];
+      Y[tm] = u - acc[tm];
       const f32x4 g4 = *reinterpret_cast<const f32x4*>(sg + 16 * tm + 4 * lg);
 #pragma unroll
       for (int j = 0; j < 4; ++j) Yg[tm][j] = 16 * tm + 4 * lg + j < nv ? Y[tm][j] * gexp(gl - g4[j]) : 0.f;
@@ -399,15 +454,14 @@ __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V
         *reinterpret_cast<uint2*>(orow + (size_t)(16 * tn) * (size_t)(H * V) * 2 + F.o) = ov;
       }
     }
-    // S = exp(g_last) S + k^T (v' exp(g_last - gc))
+    // S = exp(g_last) S + k^T (v' exp(g_last - gc)), pipelined like the products above
     const float eg = gexp(gl);
-    // (pipelined like the products above, four row tiles of k^T per stage)
     Frag<bf16> ka[2][4][2];
     auto read_k = [&](int k4, Frag<bf16>(&k8)[4][2]) {
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const int tt = k4 + qq;
-        const uint32_t off = B * KBUF + 256u * (tt >> 3);
+        const uint32_t off = 256u * (tt >> 3);
         k8[qq][0] = frag2(ldtr(A.tra[tt & 7], off), ldtr(A.trb[tt & 7], off));
         k8[qq][1] = frag2(ldtr(A.tra[tt & 7], off + 16384u), ldtr(A.trb[tt & 7], off + 16384u));
       }
@@ -427,19 +481,18 @@ __global__ __launch_bounds__(NT_F) void wide_fused_kernel(WideFusedArgs a, int V
     }
   };
 
-  FChunk ca, cb;
   if (nchunks > 1) prefetch(c_first + 1, bos + C, chunk_nv(1));
   if (nchunks > 0) {
     const int nv0 = chunk_nv(0);
-    load_u(ca, c_first, nv0);
-    dma_kag(c_first, bos, nv0, 0u);
+    dma_small(c_first, bos, nv0, 0u);
     dma_tile256(a.w, F, bos, nv0, h, H, w_lds);
     dma_tile256(a.q, F, bos, nv0, h, H, w_lds + QOFF);
   }
   for (int64_t it = 0; it < nchunks; it += 2) {
-    step(std::integral_constant<uint32_t, 0>{}, ca, cb, it);
-    if (it + 1 < nchunks) step(std::integral_constant<uint32_t, 1>{}, cb, ca, it + 1);
+    step(std::integral_constant<uint32_t, 0>{}, it);
+    if (it + 1 < nchunks) step(std::integral_constant<uint32_t, 1>{}, it + 1);
   }
+  wait_all_loads();                                       // no direct load outlives the workgroup's LDS
 
   if (a.ht) {
 #pragma unroll

@@ -237,6 +237,10 @@ EDGE_CASES = [
     # a last chunk of 20 tokens: gate shuffles in ragged chunks must read from active lanes
     ("bf16", 1, 1300, 2, 256, 512, None, False, True),
     ("fp32", 1, 200, 1, 256, 256, None, False, True),
+    # the fused K = 256 kernel with 3 and 1 value tiles per head (its L2 prefetch splits rows over
+    # the tiles), two batch rows with a ragged end, and varlen cuts at chunk edges
+    ("bf16", 2, 260, 3, 256, 192, None, False, True),
+    ("bf16", 1, 500, 2, 256, 64, [0, 63, 64, 65, 500], True, True),
     ("bf16", 2, 150, 2, 128, 48, None, False, True),
     # the in-op L2 norm on the fused path at K = 64 (8 lanes per row) with ragged varlen chunks
     ("bf16", 1, 700, 3, 64, 128, [0, 1, 1, 129, 640, 700], True, True),
