@@ -247,6 +247,7 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
     total += align_up(nc * H * kgdn::C * kgdn::C * es);   // Aqk
     total += align_up(tok * kgdn::C * es);                // Ai
     total += align_up(tok * sizeof(float));               // beta (fp32)
+    total += align_up(nc * H * K * kgdn::C * es);         // k^T per chunk
   } else {
     total += align_up(nc * H * V * kgdn::C * es);         // uT
     total += align_up(nc * H * V * K * es);               // hT
@@ -317,10 +318,12 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   void* aqk = nullptr;
   void* ai = nullptr;
   float* bf = nullptr;
+  void* kt = nullptr;
   if (wide) {
     aqk = cv.take((size_t)G.nc * H * kgdn::C * kgdn::C * es);
     ai = cv.take(tok * kgdn::C * es);
     bf = static_cast<float*>(cv.take(tok * sizeof(float)));
+    kt = cv.take((size_t)G.nc * H * K * kgdn::C * es);
   } else {
     uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
     hT = cv.take((size_t)G.nc * H * V * K * es);
@@ -333,12 +336,13 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
     pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = ai;
-    pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;        // the fused K = 256 form: Aqk, Ai, beta, no u
+    pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;        // the fused K = 256 form: Aqk, Ai, beta, k^T, no u
+    pa.kT_out = kt;
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, G.nc, s), "prepare")) return rc;
   }
   if (wide) {
     kgdn::WideFusedArgs fa{};
-    fa.q = q; fa.k = k; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
+    fa.q = q; fa.kT = kt; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
     fa.h0 = h0; fa.h0_dtype = h0_dtype;
     fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
     fa.scale = scale; fa.o = o; fa.ht = ht;

@@ -39,6 +39,7 @@ struct PrepareArgs {
   const void* q;          // [B*T, H, K] (qk dtype), read only with aqk_out
   void* aqk_out;          // optional out [NC, H, 64, 64]: mask_{i>=j}(q k^T exp(gc_i - gc_j)) (compute dtype)
   float* beta_out;        // optional out [B*T, H] fp32 beta
+  void* kT_out;           // optional out [NC, H, K, 64] k^T per chunk (compute dtype, zero past the chunk's end)
   // uT == nullptr: no u pass (v is not read)
 };
 
@@ -79,10 +80,11 @@ struct FwdOArgs {
 };
 
 // Fused recurrence + output for K = 256 (gdn_wide.hip), after launch_prepare without its u pass
-// (gc, w, Ai, fp32 beta and Aqk); u = Ai bf16(beta v) is formed in the kernel.  bf16 q, k, w, u; V a multiple of 64.
+// (gc, w, Ai, fp32 beta, Aqk and k^T); u = Ai bf16(beta v) is formed in the kernel.  bf16 q, k, w,
+// u; V a multiple of 64.
 struct WideFusedArgs {
   const void* q;          // [B*T, H, 256] bf16
-  const void* k;          // [B*T, H, 256] bf16
+  const void* kT;         // [NC, H, 256, 64] bf16 k^T per chunk (launch_prepare's kT_out)
   const void* v;          // [B*T, H, V] bf16
   const void* w;          // [B*T, H, 256] bf16
   const void* Ai;         // [B*T, H, 64] bf16 (I + A)^-1 rows (launch_prepare's Ai_out)

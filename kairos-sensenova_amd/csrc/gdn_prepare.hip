@@ -11,6 +11,8 @@
 // Output layouts: gc [B*T, H] fp32; w [B*T, H, K] (token-major, as the
 // reference); u per chunk transposed, uT [NC, H, V, 64], which is the
 // K-contiguous operand layout the state kernel reads.
+#include <type_traits>
+
 #include "gdn_common.hpp"
 #include "gdn_kernels.h"
 
@@ -223,6 +225,24 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
       for (int jj = 0; jj < 4; ++jj) {
         const int i = 16 * tm + 4 * lg + jj;
         aq[i * C + j] = from_f32<TC>((i >= j && i < nv) ? acc[jj] * gexp(s_g[i] - s_g[j]) : 0.f);
+      }
+    }
+  }
+  // ---- optional k^T per chunk, [NC, H, K, 64] (zero past the chunk's end), for the fused K = 256
+  //      recurrence's update operand: wave w writes rows d = 16 (w + 4 i) .. + 15 from transposed
+  //      reads of s_k (lane: 4 tokens of one d, one 8-byte store)
+  if constexpr (std::is_same<TC, bf16>::value) {
+    if (a.kT_out) {
+      TC* kt = reinterpret_cast<TC*>(a.kT_out) + ((int64_t)blockIdx.x * H + h) * (K * C);
+#pragma unroll
+      for (int i = 0; i < K / 64; ++i) {
+        const int d0 = 16 * (wid + 4 * i);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+          const int tr = 16 * t4 + 4 * lg + (lc >> 2);
+          const s16x4_t x = lds_read_tr16(s_k + tr * L::LDK + d0 + 4 * (lc & 3));
+          *reinterpret_cast<s16x4_t*>(kt + (d0 + lc) * C + 16 * t4 + 4 * lg) = x;
+        }
       }
     }
   }
