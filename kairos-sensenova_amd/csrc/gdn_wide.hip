@@ -31,6 +31,7 @@
 //   k^T     [256 d][64]  chunk c of row r at c ^ (2 ((r / 8) % 4) + (r / 2) % 2)
 //   Ai, Aqk [64][64]     as k^T
 //   v       [64 t][64]   chunk c of row r at c ^ (2 ((r / 8) % 2) + 4 ((r / 2) % 2)), read transposed
+//   o       [64 t][64]   chunk c of row r at c ^ ((r / 2) % 2 + 2 ((r / 8) % 4))
 // A b128 LDS read serves 16 lanes per pass on gfx950, grouped by lane bit 5 and the parity of lane
 // bits 2-4 (measured with the bank-conflict counter on probe patterns); for the rows rowA the swizzles
 // above give each such group 16 distinct 16-byte bank positions (w, q: position lg ^ lc; the 128-byte
@@ -52,6 +53,7 @@ constexpr int FK = 256;           // K
 constexpr int FW = 4;             // waves per workgroup, 16 state columns each
 constexpr int FVT = 16 * FW;      // value columns per workgroup
 constexpr int NT_F = FW * WAVE;
+constexpr int FL = 4;             // loader waves (direct loads only)
 
 // Workgroup barrier on LDS only (lgkmcnt(0), s_barrier): the next chunk's global loads and this
 // chunk's o stores stay in flight across it.
@@ -111,11 +113,13 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 __device__ __forceinline__ int swz_wq(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
 __device__ __forceinline__ int swz_a(int r) { return (((r >> 3) & 3) << 1) | ((r >> 1) & 1); }
 __device__ __forceinline__ int swz_v(int r) { return (((r >> 3) & 1) << 1) | (((r >> 1) & 1) << 2); }
+__device__ __forceinline__ int swz_o(int t) { return ((t >> 1) & 1) | (((t >> 3) & 3) << 1); }
 
 typedef __attribute__((address_space(3))) unsigned char lds_b;
 typedef short s16x4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4v lds_s16x4v;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 
 // LDS reads at a lane byte address plus an offset that is a constant after unrolling (it lands
 // in the instruction's offset field); volatile keeps them in program order, where the pipelining
@@ -197,7 +201,7 @@ __device__ __forceinline__ void ld_tile64(const unsigned char* base, uint32_t ro
   dma16_(base, rr * row_bytes + 16u * (pos ^ (kSwzA ? swz_a(r) : swz_v(r))), dst + 1024u * i);
 }
 
-__global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a, int V, int total_units) {
+__global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedArgs a, int V, int total_units) {
   // LDS: w and q of the chunk (adjacent: q reads are w reads + 32 KB), k^T of the chunk, and two
   // buffer sets of the chunk's small tiles: Aqk, Ai, the v tile of the workgroup's 64 columns, gc, beta
   __shared__ __align__(16) bf16 s_wq[2 * C * FK];
@@ -207,6 +211,7 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
   __shared__ __align__(16) bf16 s_v[2 * C * C];
   __shared__ __align__(16) float s_g[2 * C];
   __shared__ __align__(16) float s_b[2 * C];
+  __shared__ __align__(16) bf16 s_o[C * C];               // the chunk's o tile [64 t][64 columns]
   __shared__ __align__(16) float s_pf[WAVE];              // landing words of the L2 prefetch
   constexpr uint32_t QOFF = C * FK * 2, ABUF = C * C * 2, GBUF = C * 4;
 
@@ -234,39 +239,45 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
   const int64_t nchunks = (eos - bos + C - 1) / C;
   auto chunk_nv = [&](int64_t it) { return (int)min((int64_t)C, eos - (bos + it * C)); };
   const uint32_t w_lds = lds_u32(s_wq), k_lds = lds_u32(s_k), a_lds = lds_u32(s_a), ai_lds = lds_u32(s_ai),
-                 v_lds = lds_u32(s_v), g_lds = lds_u32(s_g), b_lds = lds_u32(s_b);
+                 v_lds = lds_u32(s_v), g_lds = lds_u32(s_g), b_lds = lds_u32(s_b), o_lds = lds_u32(s_o);
   const bf16* aqb = reinterpret_cast<const bf16*>(a.aqk);
   const bf16* ktb = reinterpret_cast<const bf16*>(a.kT);
 
-  if (wid == FW) {
-    // ---- the loader wave: every direct load of the workgroup, so that the four compute waves never
-    //      stall on the address unit.  Per chunk step it, between the compute waves' two barriers:
-    //      after B1, k^T of chunk it (32 loads), the small tiles of chunk it + 1 into the other buffer
-    //      set (26) and the L2 prefetch of chunk it + 2 (4); before B2 it waits for k^T alone; after
-    //      B2 (the compute waves are done with w and q), w and q of chunk it + 1 (64).
-    constexpr int kSmall = 26, kPf = 4;
+  if (wid >= FW) {
+    // ---- the loader waves: every direct load of the workgroup, so that the four compute waves never
+    //      stall on the address unit; four of them, because one wave keeps at most 63 loads in
+    //      flight.  Loader lw issues load i of each tile for i % FL = lw.  Per chunk step it, between
+    //      the compute waves' two barriers: after B1, k^T of chunk it (8 loads each), the small tiles
+    //      of chunk it + 1 into the other buffer set (6 each, and gc / beta from loaders 0 / 1) and its
+    //      part of the L2 prefetch of chunk it + 2 (1); before B2 each waits for its k^T loads; after
+    //      B2 (the compute waves are done with w and q), w and q of chunk it + 1 (16 each).  The o tile
+    //      the compute waves left in LDS in step it - 1 goes out right after B1, as whole 128-byte
+    //      rows (two 1 KB stores per loader); from the compute waves, whose lanes hold 4 columns of a
+    //      token, the same stores would touch 16 lines each and stall them behind the loads.
+    const int lw = wid - FW;
+    const int kSmall = 6 + (lw < 2 ? 1 : 0);
     const uint32_t RB = (uint32_t)H * FK * 2;
     auto small = [&](int64_t c, int64_t t0, int nv, uint32_t B) {
       const unsigned char* ab = reinterpret_cast<const unsigned char*>(aqb + (c * H + h) * (int64_t)(C * C));
       const unsigned char* aib = reinterpret_cast<const unsigned char*>(a.Ai) + (size_t)((t0 * H + h) * C) * 2;
       const unsigned char* vb = reinterpret_cast<const unsigned char*>(a.v) + (size_t)((t0 * H + h) * V + vt0) * 2;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ld_tile64<true>(ab, 128u, C, i, a_lds + B * ABUF);
+      for (int j = 0; j < 8 / FL; ++j) ld_tile64<true>(ab, 128u, C, FL * j + lw, a_lds + B * ABUF);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ld_tile64<true>(aib, (uint32_t)H * C * 2, nv, i, ai_lds + B * ABUF);
+      for (int j = 0; j < 8 / FL; ++j) ld_tile64<true>(aib, (uint32_t)H * C * 2, nv, FL * j + lw, ai_lds + B * ABUF);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ld_tile64<false>(vb, (uint32_t)H * V * 2, nv, i, v_lds + B * ABUF);
+      for (int j = 0; j < 8 / FL; ++j) ld_tile64<false>(vb, (uint32_t)H * V * 2, nv, FL * j + lw, v_lds + B * ABUF);
       const uint32_t gl_off = (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u;
-      dma4_(a.gc + t0 * H + h, gl_off, g_lds + B * GBUF);
-      dma4_(a.beta + t0 * H + h, gl_off, b_lds + B * GBUF);
+      if (lw == 0) dma4_(a.gc + t0 * H + h, gl_off, g_lds + B * GBUF);
+      if (lw == 1) dma4_(a.beta + t0 * H + h, gl_off, b_lds + B * GBUF);
     };
     auto wq = [&](int64_t t0, int nv) {
       const unsigned char* wb = reinterpret_cast<const unsigned char*>(a.w) + (size_t)((t0 * H + h) * FK) * 2;
       const unsigned char* qb = reinterpret_cast<const unsigned char*>(a.q) + (size_t)((t0 * H + h) * FK) * 2;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) ld_tile256(wb, RB, nv, i, w_lds);
+      for (int j = 0; j < 32 / FL; ++j) ld_tile256(wb, RB, nv, FL * j + lw, w_lds);
 #pragma unroll
-      for (int i = 0; i < 32; ++i) ld_tile256(qb, RB, nv, i, w_lds + QOFF);
+      for (int j = 0; j < 32 / FL; ++j) ld_tile256(qb, RB, nv, FL * j + lw, w_lds + QOFF);
     };
     // L2 prefetch of chunk (c, t0)'s w and q rows and its k^T and Aqk tiles: one 4-byte direct load
     // per 128-byte line into a scratch LDS word (never read), so that the tile loads a step later
@@ -276,13 +287,26 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
     // would cost as much of it as the tile loads themselves.
     const uint32_t pf_lds = lds_u32(s_pf);
     const int pf_q = (vt0 / FVT) & 3;
-    auto prefetch = [&](int64_t c, int64_t t0, int nv) {
-      const int r = 16 * pf_q + (l >> 2);
-      const uint32_t off = (uint32_t)(r < nv ? r : 0) * RB + 128u * (l & 3);
-      dma4_(reinterpret_cast<const unsigned char*>(a.w) + (size_t)((t0 * H + h) * FK) * 2, off, pf_lds);
-      dma4_(reinterpret_cast<const unsigned char*>(a.q) + (size_t)((t0 * H + h) * FK) * 2, off, pf_lds);
-      dma4_(ktb + (c * H + h) * (int64_t)(FK * C), 128u * (64 * pf_q + l), pf_lds);
-      dma4_(aqb + (c * H + h) * (int64_t)(C * C), 128u * (16 * pf_q + (l & 15)), pf_lds);
+    auto prefetch = [&](int64_t c, int64_t t0, int nv) {     // one load per loader wave
+      if (lw < 2) {
+        const int r = 16 * pf_q + (l >> 2);
+        const uint32_t off = (uint32_t)(r < nv ? r : 0) * RB + 128u * (l & 3);
+        dma4_(reinterpret_cast<const unsigned char*>(lw == 0 ? a.w : a.q) + (size_t)((t0 * H + h) * FK) * 2, off, pf_lds);
+      } else if (lw == 2) {
+        dma4_(ktb + (c * H + h) * (int64_t)(FK * C), 128u * (64 * pf_q + l), pf_lds);
+      } else {
+        dma4_(aqb + (c * H + h) * (int64_t)(C * C), 128u * (16 * pf_q + (l & 15)), pf_lds);
+      }
+    };
+    // the o tile of chunk (t0, nv) from LDS to HBM: rows 8 i .. 8 i + 7 for i % FL = lw
+    auto store_o = [&](int64_t t0, int nv) {
+#pragma unroll
+      for (int j = 0; j < 8 / FL; ++j) {
+        const int t = 8 * (FL * j + lw) + (l >> 3), c8 = l & 7;
+        const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (c8 ^ swz_o(t)));
+        if (t < nv)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2) = x;
+      }
     };
     if (nchunks > 1) prefetch(c_first + 1, bos + C, chunk_nv(1));
     if (nchunks > 0) {
@@ -294,19 +318,25 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
       const int64_t in = it + 1 < nchunks ? it + 1 : it;  // the last step reloads its own chunk (unused)
       wait_all_loads();
       f_barrier();                                        // B1
+      if (it > 0) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
       const unsigned char* kb = reinterpret_cast<const unsigned char*>(ktb + ((c_first + it) * H + h) * (int64_t)(FK * C));
 #pragma unroll
-      for (int i = 0; i < 32; ++i) ld_tile64<true>(kb, 128u, FK, i, k_lds);
+      for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(kb, 128u, FK, FL * j + lw, k_lds);
       small(c_first + in, bos + in * C, chunk_nv(in), B ^ 1u);
+      // this wave's k^T loads landed; the later ones (6 + gc / beta + the prefetch) stay in flight
       if (it + 2 < nchunks) {
         prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
-        wait_loads_but<kSmall + kPf>();                   // k^T landed; the later loads stay in flight
+        if (kSmall == 7) wait_loads_but<8>();
+        else wait_loads_but<7>();
       } else {
-        wait_loads_but<kSmall>();
+        if (kSmall == 7) wait_loads_but<7>();
+        else wait_loads_but<6>();
       }
       f_barrier();                                        // B2
       if (it + 1 < nchunks) wq(bos + (it + 1) * C, chunk_nv(it + 1));
     }
+    f_barrier();                                          // the last o tile is in LDS
+    if (nchunks > 0) store_o(bos + (nchunks - 1) * C, chunk_nv(nchunks - 1));
     wait_all_loads();                                     // no direct load outlives the workgroup's LDS
     return;
   }
@@ -332,29 +362,52 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
   }
   FAddr A;
   f_addr(A, w_lds, k_lds, a_lds, v_lds);
-  unsigned char* ob = reinterpret_cast<unsigned char*>(a.o) + (size_t)v0 * 2;
-  const uint32_t o_lane = ((uint32_t)ra0 * (uint32_t)(H * V) + 4u * lg) * 2u;   // token rowA(0, lc), columns 4 lg ..
   const uint32_t AI_OFF = ai_lds - a_lds;                 // Ai tiles share the Aqk lane addresses
 
   // One chunk step between the loader's barriers: after B1 (w, q and the small tiles of chunk it in
   // LDS, buffer set B = it % 2), w h and h^T q^T; after B2 (k^T in LDS), u, v', o and the update.
   auto step = [&](auto BB, int64_t it) {
     constexpr uint32_t B = decltype(BB)::value;
-    const int64_t t0 = bos + it * C;
     const int nv = chunk_nv(it);
     f_barrier();                                          // B1
     const float* sg = s_g + B * C;
     const float* sb = s_b + B * C;
 
-    // w h (rows t in the paired order, this wave's columns) and o_inter^T = h^T q^T (rows =
+    // u = Ai bf16(beta v) (wy_fast.py:55-81), rounded to bf16 as the reference stores it, from tiles
+    // already in LDS at B1: the v tile is read transposed (rows s = 32 ks + 8 lg + e) and scaled by
+    // beta per row.  -bf16(u) starts the w h accumulators, so they end as w h - u = -v'.
+    f32x4 acc[4], oi[4];
+    {
+      Frag<bf16> vb[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t vo = B * ABUF + 4096u * ks;
+        const Frag<bf16> vr = frag2(ldtr(A.vt, vo), ldtr(A.vt, vo + 512u));
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(sb + 32 * ks + 8 * lg);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(sb + 32 * ks + 8 * lg + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vb[ks].v[e] = (bf16)((float)vr.v[e] * b0[e]);
+          vb[ks].v[4 + e] = (bf16)((float)vr.v[4 + e] * b1[e]);
+        }
+      }
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) {
+        acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+        oi[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          if (ks <= tm / 2) mma(acc[tm], ld128(A.ar[ks], AI_OFF + B * ABUF + rowa_off(tm, 128)), vb[ks]);
+      }
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[tm][j] = -(float)(bf16)acc[tm][j];
+    }
+
+    // w h - u (rows t in the paired order, this wave's columns) and o_inter^T = h^T q^T (rows =
     // columns, cols = t = rowA(tn, lc)), with h = bf16(S) packed per 32-deep step as the B (w h)
     // and A (h^T q^T) operand; operand reads one step ahead of the products
-    f32x4 acc[4], oi[4];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-      acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
-      oi[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
     Frag<bf16> wa[2][4], qa[2][4];
     auto read_wq = [&](int ks, Frag<bf16>(&w4)[4], Frag<bf16>(&q4)[4]) {
       const uint32_t ra = A.wq[ks & 3];
@@ -373,40 +426,29 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
       const Frag<bf16> hb = pack_acc(S[2 * ks], S[2 * ks + 1]);
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
-        mma(acc[tm], wa[ks & 1][tm], hb);
         mma(oi[tm], hb, qa[ks & 1][tm]);
+        mma(acc[tm], wa[ks & 1][tm], hb);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     f_barrier();                                          // B2: k^T in LDS; w and q tiles free
 
-    // u = Ai bf16(beta v) (wy_fast.py:55-81), rounded to bf16 as the reference stores it; the v tile
-    // is read transposed (rows s = 32 ks + 8 lg + e) and scaled by beta per row
-    Frag<bf16> vb[2];
+    // the output's LDS operands first (one latency for all): Aqk row pieces and exp(gc_t) per tile
+    Frag<bf16> aq[6];
+    float egt[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const uint32_t vo = B * ABUF + 4096u * ks;
-      const Frag<bf16> vr = frag2(ldtr(A.vt, vo), ldtr(A.vt, vo + 512u));
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(sb + 32 * ks + 8 * lg);
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(sb + 32 * ks + 8 * lg + 4);
+    for (int tn = 0, f = 0; tn < 4; ++tn) {
+      egt[tn] = sg[32 * (tn >> 1) + 4 * (tn & 1) + ra0];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vb[ks].v[e] = (bf16)((float)vr.v[e] * b0[e]);
-        vb[ks].v[4 + e] = (bf16)((float)vr.v[4 + e] * b1[e]);
-      }
+      for (int ks = 0; ks < 2; ++ks)
+        if (ks <= tn / 2) aq[f++] = ld128(A.ar[ks], B * ABUF + rowa_off(tn, 128));
     }
     // v' = u - w h (rows t = 32 (tm / 2) + 8 lg + 4 (tm % 2) + j), its bf16 value and the gated form
     const float gl = sg[nv - 1];
     f32x4 Y[4], Yg[4];
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm) {
-      f32x4 u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        if (ks <= tm / 2) mma(u, ld128(A.ar[ks], AI_OFF + B * ABUF + rowa_off(tm, 128)), vb[ks]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) u[j] = (float)(bf16)u[j];
-      Y[tm] = u - acc[tm];
+      Y[tm] = -acc[tm];
       const int tr = 32 * (tm >> 1) + 8 * lg + 4 * (tm & 1);
       const f32x4 g4 = *reinterpret_cast<const f32x4*>(sg + tr);
 #pragma unroll
@@ -418,22 +460,25 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
       vf[ks] = pack_acc(Y[2 * ks], Y[2 * ks + 1]);
       vg[ks] = pack_acc(Yg[2 * ks], Yg[2 * ks + 1]);
     }
-    // o^T = (o_inter^T exp(gc_t) + v'^T Aqk^T) scale; lane: columns v0 + 4 lg .. + 3 of token rowA(tn, lc)
-    unsigned char* orow = ob + (size_t)((t0 * H + h) * V) * 2;
+    // o^T = (o_inter^T exp(gc_t) + v'^T Aqk^T) scale; lane: columns 16 w + 4 lg .. + 3 of token
+    // rowA(tn, lc), into the LDS o tile (the loader waves store it after the next B1)
+    f32x4 r[4];
+#pragma unroll
+    for (int tn = 0, f = 0; tn < 4; ++tn) {
+      r[tn] = oi[tn] * gexp(egt[tn]);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        if (ks <= tn / 2) mma(r[tn], vf[ks], aq[f++]);
+    }
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) {
       const int t = 32 * (tn >> 1) + 4 * (tn & 1) + ra0;
-      f32x4 r = oi[tn] * gexp(sg[t]);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        if (ks <= tn / 2) mma(r, vf[ks], ld128(A.ar[ks], B * ABUF + rowa_off(tn, 128)));
-      r *= a.scale;
-      if (t < nv) {
-        const uint2 ov = make_uint2(
-            (uint32_t)__builtin_bit_cast(uint16_t, (bf16)r[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)r[1]) << 16),
-            (uint32_t)__builtin_bit_cast(uint16_t, (bf16)r[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)r[3]) << 16));
-        *reinterpret_cast<uint2*>(orow + (size_t)(32 * (tn >> 1) + 4 * (tn & 1)) * (size_t)(H * V) * 2 + o_lane) = ov;
-      }
+      const f32x4 x = r[tn] * a.scale;
+      const u32x2 ov = {
+          (uint32_t)__builtin_bit_cast(uint16_t, (bf16)x[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)x[1]) << 16),
+          (uint32_t)__builtin_bit_cast(uint16_t, (bf16)x[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)x[3]) << 16)};
+      *reinterpret_cast<lds_u32x2*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * ((2 * wid + (lg >> 1)) ^ swz_o(t)) +
+                                    8 * (lg & 1)) = ov;
     }
     // S = exp(g_last) S + k^T (v' exp(g_last - gc)), pipelined like the products above
     const float eg = gexp(gl);
@@ -464,6 +509,7 @@ __global__ __launch_bounds__(NT_F + WAVE) void wide_fused_kernel(WideFusedArgs a
     step(std::integral_constant<uint32_t, 0>{}, it);
     if (it + 1 < nchunks) step(std::integral_constant<uint32_t, 1>{}, it + 1);
   }
+  f_barrier();                                            // the last o tile is in LDS for the loaders
 
   if (a.ht) {
 #pragma unroll
@@ -487,7 +533,7 @@ int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s) {
   if (V % FVT != 0 || a.N * a.H == 0) return -2;
   const int total = a.N * a.H * (V / FVT);
   const int grid = (total + 7) / 8 * 8;
-  hipLaunchKernelGGL(wide_fused_kernel, dim3(grid), dim3(NT_F + WAVE), 0, s, a, V, total);
+  hipLaunchKernelGGL(wide_fused_kernel, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
