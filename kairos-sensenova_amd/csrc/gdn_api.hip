@@ -248,6 +248,7 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
     total += align_up(tok * kgdn::C * es);                // Ai
     total += align_up(tok * sizeof(float));               // beta (fp32)
     total += align_up(nc * H * K * kgdn::C * es);         // k^T per chunk
+    total += align_up((size_t)(n_seqs > 0 ? n_seqs : B) * H * K * V * sizeof(float));   // state between parts
   } else {
     total += align_up(nc * H * V * kgdn::C * es);         // uT
     total += align_up(nc * H * V * K * es);               // hT
@@ -300,10 +301,56 @@ size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_s
 // reference's stage order with its intermediates in the workspace.  Used for the
 // shapes the fused kernels do not cover: fp32, and the Kairos model's head dims
 // K = 256, V = 512 (any K in {64, 128, 256} with V a multiple of 16).
+// The pipelined form of the fused K = 256 path: the chunks of every sequence are cut into P parts;
+// the prepare kernel of part p + 1 runs on a second stream while the recurrence walks part p (whose
+// 64-column workgroups leave CUs idle: 160 of 256 at the Kairos layer shape), the state passing
+// between parts through an fp32 buffer.  KAIROS_GDN_WIDE_PIPE sets P (1: one prepare, then one
+// recurrence); fixed-length sequences only.  Part 0's prepare runs on the caller's stream (the whole
+// GPU), the later prepares on a second stream and the recurrence parts on a third.  Prepare p + 1
+// waits for a one-workgroup marker kernel queued just before recurrence part p, so the recurrence's
+// workgroups are dispatched first and the prepare fills the CUs they leave (were both ready at once,
+// the prepare's 10^4 workgroups could take every CU and hold the recurrence back).  The caller's
+// stream waits for the last recurrence part.
+constexpr int kMaxParts = 16;
+
+int wide_pipe_parts() {
+  const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE");
+  if (e == nullptr) return 4;
+  const int p = std::atoi(e);
+  return p < 1 ? 1 : p > kMaxParts ? kMaxParts : p;
+}
+
+std::mutex g_aux_mu;                                     // held while a pipelined call enqueues its work
+hipStream_t g_aux_stream[64][2] = {};
+hipEvent_t g_aux_events[64][2 * kMaxParts + 1] = {};
+
+// The two streams (prepares, recurrence parts) and the events of the current device, created on
+// first use and kept until the process ends (a recorded event may be recorded again: waits already
+// enqueued keep the record they saw).  Call with g_aux_mu held.
+int aux_streams(hipStream_t* sp, hipStream_t* sr, hipEvent_t** events) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
+  if (g_aux_events[dev][0] == nullptr) {
+    for (int p = 0; p < 2 * kMaxParts + 1; ++p)
+      if (hipEventCreateWithFlags(&g_aux_events[dev][p], hipEventDisableTiming) != hipSuccess) return -1;
+  }
+  *events = g_aux_events[dev];
+  if (g_aux_stream[dev][0] == nullptr) {
+    hipStream_t st[2] = {nullptr, nullptr};
+    for (int j = 0; j < 2; ++j)
+      if (hipStreamCreateWithFlags(&st[j], hipStreamNonBlocking) != hipSuccess) return -1;
+    g_aux_stream[dev][0] = st[0];
+    g_aux_stream[dev][1] = st[1];
+  }
+  *sp = g_aux_stream[dev][0];
+  *sr = g_aux_stream[dev][1];
+  return 0;
+}
+
 int run_staged(const Geometry& G, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
                const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
-               Carver& cv, hipStream_t s) {
+               Carver& cv, hipStream_t s, bool may_fork) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(G.B * G.T * G.H);
   const int K = (int)G.K, V = (int)G.V, H = (int)G.H;
@@ -319,35 +366,92 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   void* ai = nullptr;
   float* bf = nullptr;
   void* kt = nullptr;
+  float* st = nullptr;
   if (wide) {
     aqk = cv.take((size_t)G.nc * H * kgdn::C * kgdn::C * es);
     ai = cv.take(tok * kgdn::C * es);
     bf = static_cast<float*>(cv.take(tok * sizeof(float)));
     kt = cv.take((size_t)G.nc * H * K * kgdn::C * es);
+    st = static_cast<float*>(cv.take((size_t)G.N * H * K * V * sizeof(float)));
   } else {
     uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
     hT = cv.take((size_t)G.nc * H * V * K * es);
     vnT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
   }
   const int N = (int)G.N;
+  kgdn::PrepareArgs pa{};
+  pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
+  pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
+  pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
+  pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = ai;
+  pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;          // the fused K = 256 form: Aqk, Ai, beta, k^T, no u
+  pa.kT_out = kt;
+  kgdn::WideFusedArgs fa{};
+  fa.q = q; fa.kT = kt; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
+  fa.h0 = h0; fa.h0_dtype = h0_dtype;
+  fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
+  fa.scale = scale; fa.o = o; fa.ht = ht;
+  if (wide && G.nc > 0 && may_fork && cu_seqlens == nullptr) {
+    const int64_t nt = (G.T + kgdn::C - 1) / kgdn::C;
+    int P = wide_pipe_parts();
+    if (nt < 2 * P) P = 1;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (P > 1 && (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)) P = 1;
+    std::unique_lock<std::mutex> lk(g_aux_mu, std::defer_lock);
+    hipStream_t s2 = nullptr, s3 = nullptr;
+    hipEvent_t* ev = nullptr;
+    if (P > 1) {
+      lk.lock();
+      if (aux_streams(&s2, &s3, &ev) != 0) {
+        lk.unlock();
+        P = 1;
+      }
+    }
+    if (P > 1) {
+      const int64_t span = (nt + P - 1) / P;
+      int rc = KAIROS_GDN_OK;
+      auto wait = [&](hipStream_t st, hipEvent_t e) {
+        if (rc == KAIROS_GDN_OK && hipStreamWaitEvent(st, e, 0) != hipSuccess) rc = fail(KAIROS_GDN_EHIP, "hipStreamWaitEvent");
+      };
+      auto record = [&](hipEvent_t e, hipStream_t st) {
+        if (rc == KAIROS_GDN_OK && hipEventRecord(e, st) != hipSuccess) rc = fail(KAIROS_GDN_EHIP, "hipEventRecord");
+      };
+      // ev[p]: prepare p done; ev[kMaxParts + p]: recurrence part p about to be dispatched
+      auto prepare = [&](int p, hipStream_t sp) {
+        pa.it0 = p * span;
+        pa.it_span = std::min(span, nt - p * span);
+        if (rc == KAIROS_GDN_OK)
+          rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, (int64_t)N * pa.it_span, sp), "prepare");
+        record(ev[p], sp);
+      };
+      prepare(0, s);
+      for (int p = 0; p < P && rc == KAIROS_GDN_OK; ++p) {
+        wait(s3, ev[p]);
+        if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_marker(s3), "marker");
+        record(ev[kMaxParts + p], s3);
+        kgdn::WideFusedArgs fp = fa;
+        fp.it_begin = p * span;
+        fp.it_end = std::min((p + 1) * span, nt);
+        if (p > 0) {
+          fp.h0 = st;
+          fp.h0_dtype = KAIROS_GDN_F32;
+        }
+        if (p + 1 < P) fp.ht = st;
+        if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_wide_fused(fp, V, s3), "wide fused recurrence");
+        if (p + 1 < P) {
+          wait(s2, ev[kMaxParts + p]);
+          prepare(p + 1, s2);
+        }
+      }
+      record(ev[2 * kMaxParts], s3);                        // the caller's stream waits for the last part
+      wait(s, ev[2 * kMaxParts]);
+      return rc;
+    }
+  }
   if (G.nc > 0) {
-    kgdn::PrepareArgs pa{};
-    pa.k = k; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = k_scale;
-    pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
-    pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = G.T; pa.H = H;
-    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = ai;
-    pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;        // the fused K = 256 form: Aqk, Ai, beta, k^T, no u
-    pa.kT_out = kt;
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, G.nc, s), "prepare")) return rc;
   }
-  if (wide) {
-    kgdn::WideFusedArgs fa{};
-    fa.q = q; fa.kT = kt; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
-    fa.h0 = h0; fa.h0_dtype = h0_dtype;
-    fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
-    fa.scale = scale; fa.o = o; fa.ht = ht;
-    return from_launch(kgdn::launch_wide_fused(fa, V, s), "wide fused recurrence");
-  }
+  if (wide) return from_launch(kgdn::launch_wide_fused(fa, V, s), "wide fused recurrence");
   kgdn::FwdHArgs ha{};
   ha.k = k; ha.k_scale = k_scale; ha.w = w; ha.uT = uT; ha.gc = gc;
   ha.h0 = h0; ha.h0_dtype = h0_dtype;
@@ -474,7 +578,7 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
       k = kn;
     }
     if (int rc = run_staged(G, q, k, v, g, beta, q_scale, k_scale, initial_state, h0_dtype, o, final_state,
-                            cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s))
+                            cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s, profile))
       return rc;
     return ok();
   }

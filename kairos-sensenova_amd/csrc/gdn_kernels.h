@@ -40,6 +40,8 @@ struct PrepareArgs {
   void* aqk_out;          // optional out [NC, H, 64, 64]: mask_{i>=j}(q k^T exp(gc_i - gc_j)) (compute dtype)
   float* beta_out;        // optional out [B*T, H] fp32 beta
   void* kT_out;           // optional out [NC, H, K, 64] k^T per chunk (compute dtype, zero past the chunk's end)
+  int64_t it0, it_span;   // it_span > 0 (cu == nullptr): only local chunks it0 .. it0 + it_span - 1 of each
+                          // sequence, grid N * it_span (chunks past a sequence's end exit)
   // uT == nullptr: no u pass (v is not read)
 };
 
@@ -101,9 +103,13 @@ struct WideFusedArgs {
   float scale;
   void* o;                // out [B*T, H, V] bf16
   float* ht;              // out [N, H, 256, V] fp32 or nullptr
+  int64_t it_begin, it_end;  // the chunks of each sequence to walk (it_end <= 0: to the end); h0 is the
+                             // state before chunk it_begin, ht the one after the last chunk walked
 };
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V);
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s);
+// An empty one-workgroup kernel: a point in a stream's order that an event can mark.
+int launch_marker(hipStream_t s);
 
 // Per (chunk, head) record written by seg_prep and streamed by seg_trans and
 // seg_out: the chunk inverse (I + A)^-1 rounded to bf16 [64][64] (row t holding

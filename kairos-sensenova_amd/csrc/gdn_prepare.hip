@@ -82,7 +82,15 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
 
   const int h = blockIdx.y;
   const int H = a.H;
-  const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
+  // the chunk: blockIdx.x, or with it_span > 0 (fixed-length sequences only) local chunk
+  // it0 + x % it_span of sequence x / it_span
+  int64_t cidx = blockIdx.x;
+  if (a.it_span > 0) {
+    const int64_t nt = (a.T + C - 1) / C, it = a.it0 + blockIdx.x % a.it_span;
+    if (it >= nt) return;
+    cidx = (int64_t)(blockIdx.x / a.it_span) * nt + it;
+  }
+  const ChunkLoc loc = locate_chunk(cidx, a.cu, a.chunk_off, a.N, a.T);
   if (!loc.ok) return;
   const int64_t t0 = loc.t0;
   const int nv = loc.nv;
@@ -211,7 +219,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   //      recurrence + output: wave w forms row tile w from its q fragments (loaded above) and k
   //      from s_k
   if (a.aqk_out) {
-    TC* aq = reinterpret_cast<TC*>(a.aqk_out) + ((int64_t)blockIdx.x * H + h) * (C * C);
+    TC* aq = reinterpret_cast<TC*>(a.aqk_out) + (cidx * H + h) * (C * C);
     const int tm = wid;
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) {
@@ -233,7 +241,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   //      reads of s_k (lane: 4 tokens of one d, one 8-byte store)
   if constexpr (std::is_same<TC, bf16>::value) {
     if (a.kT_out) {
-      TC* kt = reinterpret_cast<TC*>(a.kT_out) + ((int64_t)blockIdx.x * H + h) * (K * C);
+      TC* kt = reinterpret_cast<TC*>(a.kT_out) + (cidx * H + h) * (K * C);
 #pragma unroll
       for (int i = 0; i < K / 64; ++i) {
         const int d0 = 16 * (wid + 4 * i);
@@ -364,7 +372,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
   //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after Ai,
   //      so staging overlaps the w products above
-  TC* uT = reinterpret_cast<TC*>(a.uT) + ((int64_t)blockIdx.x * H + h) * V * C;
+  TC* uT = reinterpret_cast<TC*>(a.uT) + (cidx * H + h) * V * C;
   for (int p0 = 0; want_u && p0 < V; p0 += L::VP) {
     const int vw = min(L::VP, V - p0);             // a multiple of 16
     if (v_vec) {                                   // from registers, token pairs packed per store

@@ -237,6 +237,8 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     c_first = a.chunk_off[n];
   }
   const int64_t nchunks = (eos - bos + C - 1) / C;
+  // the chunks walked: ib .. ie - 1 (h0 is the state before chunk ib)
+  const int64_t ib = min(a.it_begin, nchunks), ie = a.it_end > 0 ? min(a.it_end, nchunks) : nchunks;
   auto chunk_nv = [&](int64_t it) { return (int)min((int64_t)C, eos - (bos + it * C)); };
   const uint32_t w_lds = lds_u32(s_wq), k_lds = lds_u32(s_k), a_lds = lds_u32(s_a), ai_lds = lds_u32(s_ai),
                  v_lds = lds_u32(s_v), g_lds = lds_u32(s_g), b_lds = lds_u32(s_b), o_lds = lds_u32(s_o);
@@ -308,23 +310,23 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
           *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2) = x;
       }
     };
-    if (nchunks > 1) prefetch(c_first + 1, bos + C, chunk_nv(1));
-    if (nchunks > 0) {
-      small(c_first, bos, chunk_nv(0), 0u);
-      wq(bos, chunk_nv(0));
+    if (ie - ib > 1) prefetch(c_first + ib + 1, bos + (ib + 1) * C, chunk_nv(ib + 1));
+    if (ie > ib) {
+      small(c_first + ib, bos + ib * C, chunk_nv(ib), 0u);
+      wq(bos + ib * C, chunk_nv(ib));
     }
-    for (int64_t it = 0; it < nchunks; ++it) {
-      const uint32_t B = (uint32_t)(it & 1);
-      const int64_t in = it + 1 < nchunks ? it + 1 : it;  // the last step reloads its own chunk (unused)
+    for (int64_t it = ib; it < ie; ++it) {
+      const uint32_t B = (uint32_t)((it - ib) & 1);
+      const int64_t in = it + 1 < ie ? it + 1 : it;       // the last step reloads its own chunk (unused)
       wait_all_loads();
       f_barrier();                                        // B1
-      if (it > 0) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
+      if (it > ib) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
       const unsigned char* kb = reinterpret_cast<const unsigned char*>(ktb + ((c_first + it) * H + h) * (int64_t)(FK * C));
 #pragma unroll
       for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(kb, 128u, FK, FL * j + lw, k_lds);
       small(c_first + in, bos + in * C, chunk_nv(in), B ^ 1u);
       // this wave's k^T loads landed; the later ones (6 + gc / beta + the prefetch) stay in flight
-      if (it + 2 < nchunks) {
+      if (it + 2 < ie) {
         prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
         if (kSmall == 7) wait_loads_but<8>();
         else wait_loads_but<7>();
@@ -333,10 +335,10 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         else wait_loads_but<6>();
       }
       f_barrier();                                        // B2
-      if (it + 1 < nchunks) wq(bos + (it + 1) * C, chunk_nv(it + 1));
+      if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
     }
     f_barrier();                                          // the last o tile is in LDS
-    if (nchunks > 0) store_o(bos + (nchunks - 1) * C, chunk_nv(nchunks - 1));
+    if (ie > ib) store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));
     wait_all_loads();                                     // no direct load outlives the workgroup's LDS
     return;
   }
@@ -505,9 +507,9 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     }
   };
 
-  for (int64_t it = 0; it < nchunks; it += 2) {
+  for (int64_t it = ib; it < ie; it += 2) {
     step(std::integral_constant<uint32_t, 0>{}, it);
-    if (it + 1 < nchunks) step(std::integral_constant<uint32_t, 1>{}, it + 1);
+    if (it + 1 < ie) step(std::integral_constant<uint32_t, 1>{}, it + 1);
   }
   f_barrier();                                            // the last o tile is in LDS for the loaders
 
@@ -525,8 +527,15 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
 
 }  // namespace
 
+__global__ void marker_kernel() {}
+
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V) {
   return compute_dtype == DT_BF16 && qk_dtype == DT_BF16 && K == FK && V > 0 && V % FVT == 0;
+}
+
+int launch_marker(hipStream_t s) {
+  hipLaunchKernelGGL(marker_kernel, dim3(1), dim3(WAVE), 0, s);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s) {
