@@ -409,6 +409,7 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     }
     if (P > 1) {
       const int64_t span = (nt + P - 1) / P;
+      P = (int)((nt + span - 1) / span);                  // no empty trailing part (13 chunks in 6: 5 parts of 3)
       int rc = KAIROS_GDN_OK;
       auto wait = [&](hipStream_t st, hipEvent_t e) {
         if (rc == KAIROS_GDN_OK && hipStreamWaitEvent(st, e, 0) != hipSuccess) rc = fail(KAIROS_GDN_EHIP, "hipStreamWaitEvent");
