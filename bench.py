@@ -54,6 +54,7 @@ C = 64
 RECORD = C * C * 2 + 8 * C * 4      # bytes of one (chunk, head) record written by seg_prep
 KERNELS = ["seg_prep_kernel", "seg_trans_kernel", "seg_combine_kernel", "seg_out_kernel"]
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2.md")
+MODEL_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_model_shape.md")
 FLUSH_BYTES = 640 << 20
 
 # BASELINE.json configs measured here (config 0 is the CPU plumbing case, a parity test only)
@@ -124,6 +125,19 @@ def measured_traffic():
     except OSError:
         pass
     return out
+
+
+def measured_call_traffic(path, name):
+    """HBM bytes per call of the workload `name` from a committed rocprofv3 summary (None if absent)."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                m = re.match(r"\s*traffic_bytes_per_call\s+(\S+)\s+(\d+)", ln)
+                if m and m.group(1) == name:
+                    return int(m.group(2))
+    except OSError:
+        pass
+    return None
 
 
 def pct(xs, p):
@@ -603,7 +617,8 @@ def bench_model_shape(args, dev):
         "hbm_gbs_whole_op": alg / wall / 1e9,
         "roofline": {"bound": "hbm", "kernel": "whole call (median step)", "achieved": alg / med_s / 1e9,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS,
-                     "alg_bytes": alg, "traffic": None},
+                     "alg_bytes": alg,
+                     "traffic": measured_call_traffic(MODEL_TRAFFIC_FILE, "chunk_fwd_model_shape")},
     }), flush=True)
 
 
