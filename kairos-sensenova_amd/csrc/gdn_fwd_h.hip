@@ -469,18 +469,28 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
     const int nv = cur.nv;
     if (active) {
       // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139): through the
-      // wave's LDS tile so that each store instruction writes two whole 512-byte rows of hT
-      if (a.row_major) {          // h [NC, H, K, V]: 16 lanes write 16 consecutive columns of a row
-        bf16* hrow = hT + ((c * H + h) * WK + 4 * lg) * (int64_t)V + vcol;
+      // wave's LDS tile [col][k], so that each store instruction writes whole rows
+      bf16* hs = s_hs[wid];
 #pragma unroll
-        for (int kt = 0; kt < 16; ++kt)
+      for (int kt = 0; kt < 16; ++kt) st4<bf16>(hs + lc * LDW + 16 * kt + 4 * lg, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (a.row_major) {
+        // h [NC, H, K, V]: four transposed reads of the tile give lane (lg, i) the wave's 16 columns
+        // of row 16 lg + 64 p + i (read m: lane i fetches rows 16 lg + 64 p + 4 (i % 4) .. + 3 of
+        // column 4 m + i / 4 and receives columns 4 m .. + 3 of row 16 lg + 64 p + i); two 16-byte
+        // stores per row
+        bf16* hrow = hT + ((c * H + h) * WK) * (int64_t)V + v0;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) hrow[(16 * kt + j) * (int64_t)V] = (bf16)S[kt][j];
+        for (int p = 0; p < 4; ++p) {
+          const int r0 = 16 * lg + 64 * p;
+          s16x4_t x[4];
+#pragma unroll
+          for (int m = 0; m < 4; ++m) x[m] = lds_read_tr16(hs + (4 * m + (lc >> 2)) * LDW + r0 + 4 * (lc & 3));
+          uint4* dst = reinterpret_cast<uint4*>(hrow + (int64_t)(r0 + lc) * V);
+          dst[0] = __builtin_bit_cast(uint4, __builtin_shufflevector(x[0], x[1], 0, 1, 2, 3, 4, 5, 6, 7));
+          dst[1] = __builtin_bit_cast(uint4, __builtin_shufflevector(x[2], x[3], 0, 1, 2, 3, 4, 5, 6, 7));
+        }
       } else {
-        bf16* hs = s_hs[wid];
-#pragma unroll
-        for (int kt = 0; kt < 16; ++kt) st4<bf16>(hs + lc * LDW + 16 * kt + 4 * lg, S[kt][0], S[kt][1], S[kt][2], S[kt][3]);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         bf16* hcol = hT + ((c * H + h) * V + v0) * WK;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -527,12 +537,16 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
       // order of the transposed k fragments (tokens 32 ks + 4 lg .. and 32 ks + 16 + 4 lg ..);
       // v_new (ungated) leaves through the wave's LDS tile as whole 128-byte rows of vnT
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (a.row_major) {          // v_new [B*T, H, V] from the wave's [col][t] tile: lane = token
-        if (l < nv) {
-          const int64_t t0 = bos + it * C;
-          bf16* vrow = vnT + ((t0 + l) * H + h) * (int64_t)V + v0;
+      if (a.row_major) {          // v_new [B*T, H, V] from the wave's [col][t] tile, as the h rows above
+        s16x4_t x[4];
 #pragma unroll
-          for (int cc = 0; cc < 16; ++cc) vrow[cc] = s_vn[wid][cc * LDT + l];
+        for (int m = 0; m < 4; ++m) x[m] = lds_read_tr16(s_vn[wid] + (4 * m + (lc >> 2)) * LDT + 16 * lg + 4 * (lc & 3));
+        const int tok = 16 * lg + lc;
+        if (tok < nv) {
+          const int64_t t0 = bos + it * C;
+          uint4* dst = reinterpret_cast<uint4*>(vnT + ((t0 + tok) * H + h) * (int64_t)V + v0);
+          dst[0] = __builtin_bit_cast(uint4, __builtin_shufflevector(x[0], x[1], 0, 1, 2, 3, 4, 5, 6, 7));
+          dst[1] = __builtin_bit_cast(uint4, __builtin_shufflevector(x[2], x[3], 0, 1, 2, 3, 4, 5, 6, 7));
         }
       } else {
         bf16* vcolp = vnT + ((c * H + h) * V + v0) * C;
