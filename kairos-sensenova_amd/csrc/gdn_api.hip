@@ -268,6 +268,14 @@ bool bwd_segmented(int cdt, int64_t K, int64_t V, const SegPlan& P) {
   return !(e && e[0] == '0' && e[1] == 0);
 }
 
+// The dh recurrence for K = 256 in bf16 with 64 value columns per workgroup (KAIROS_GDN_BWD_DHU_WIDE=0
+// selects the 16-column form); it reads q^T and w^T per chunk from the workspace.
+bool wide_dhu_on(int cdt, int64_t K, int64_t V) {
+  if (!kgdn::wide_dhu_supported(cdt, (int)K, (int)V)) return false;
+  const char* e = std::getenv("KAIROS_GDN_BWD_DHU_WIDE");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
 // Workspace of the backward: the recomputed forward (gc, w, u, Ai, h, v_new) and the
 // backward's own intermediates (dv_local, dh, dv2, -dw, dk of the dq/dk stage, dg before the
 // cumsum), plus the normalised q, k and their pre-norm gradients with the in-op L2 norm.  The
@@ -294,6 +302,8 @@ size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_s
   total += 2 * align_up(nc * H * K * V * es);            // h, dh
   total += 3 * align_up(tok * V * es);                   // v_new, dv_local, dv2
   if (use_l2) total += 4 * align_up(tok * K * es);       // qn, kn, dqn, dkn
+  if (!bwd_segmented(cdt, K, V, P) && kgdn::wide_dhu_supported(cdt, (int)K, (int)V))
+    total += 2 * align_up(nc * H * K * kgdn::C * es);    // q^T, w^T per chunk
   return total;
 }
 
@@ -728,6 +738,12 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   void* vn = cv.take(tok * V * es);
   void* dvl = cv.take(tok * V * es);
   void* dv2 = cv.take(tok * V * es);
+  void* qT = nullptr;
+  void* wT = nullptr;
+  if (!segb && wide_dhu_on(cdt, K, V)) {
+    qT = cv.take((size_t)G.nc * H * K * kgdn::C * es);
+    wT = cv.take((size_t)G.nc * H * K * kgdn::C * es);
+  }
   const void* qx = q;
   const void* kx = k;
   void* dq_k = dq;
@@ -750,7 +766,7 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
     pa.k = kx; pa.v = v; pa.g = g; pa.beta = beta; pa.k_scale = nullptr;
     pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = T; pa.H = (int)H;
-    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = Ai;
+    pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = Ai; pa.wT_out = wT;
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "prepare")) return rc;
   }
   kgdn::FwdHArgs ha{};
@@ -764,6 +780,7 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   ba.dvl = dvl; ba.dh = dhs; ba.dv2 = dv2; ba.dw = dwb; ba.dk1 = dk1; ba.dg1 = dg1;
   ba.dq = dq_k; ba.dk = dk_k; ba.dv = dv; ba.dg = dg; ba.db = dbeta; ba.dh0 = dh0;
   ba.cu = cu_seqlens; ba.chunk_off = chunk_off; ba.N = N; ba.T = T; ba.H = (int)H; ba.scale = scale;
+  ba.qT = qT; ba.wT = wT;
   const int64_t nc_b = any_tokens ? G.nc : 0;
   if (!segb) {
     if (G.nc > 0 && any_tokens) {

@@ -170,6 +170,19 @@ __global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
   if (threadIdx.x < 64) s_g[threadIdx.x] = threadIdx.x < nv ? a.gc[(t0 + threadIdx.x) * H + h] : 0.f;
   __syncthreads();
 
+  // optional q^T per chunk, [NC, H, K, 64] (zero past the chunk's end), the K = 256 dh recurrence's
+  // operand: transposed reads of the staged q tile (lane: 4 tokens of one d, one 8-byte store)
+  if constexpr (sizeof(TC) == 2 && K == 256) {
+    if (a.qT) {
+      TC* qt = reinterpret_cast<TC*>(a.qT) + (blockIdx.x * (int64_t)H + h) * (K * C);
+      for (int i = wid; i < (K / 16) * 4; i += NT_B / WAVE) {
+        const int d0 = 16 * (i >> 2), tr0 = 16 * (i & 3) + 4 * lg;
+        const s16x4_t x = lds_read_tr16(s_q + toff<TC>(tr0 + (lc >> 2), d0 + 4 * (lc & 3), K));
+        *reinterpret_cast<s16x4_t*>(qt + (d0 + lc) * C + tr0) = x;
+      }
+    }
+  }
+
   // M^T[j][i], j <= i, rounded to the storage type (the reference's b_A.to(do.dtype))
   for (int tile = wid; tile < 16; tile += NT_B / WAVE) {
     const int tj = tile >> 2, ti = tile & 3;
@@ -1082,6 +1095,12 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
   }
   if (stages & BWD_DHU) {
     bool wide = false;
+    if constexpr (sizeof(TC) == 2 && K == 256) {
+      if (a.qT && a.wT && a.dh && a.dv2) {
+        if (int rc = launch_wide_dhu(a, V, s)) return rc;
+        wide = true;
+      }
+    }
     if constexpr (sizeof(TC) == 2 && K <= 128) {
       if (V == 64 || V == 128) {
         const char* e = std::getenv("KAIROS_GDN_BWD_DHU_WIDE");

@@ -40,6 +40,7 @@ struct PrepareArgs {
   void* aqk_out;          // optional out [NC, H, 64, 64]: mask_{i>=j}(q k^T exp(gc_i - gc_j)) (compute dtype)
   float* beta_out;        // optional out [B*T, H] fp32 beta
   void* kT_out;           // optional out [NC, H, K, 64] k^T per chunk (compute dtype, zero past the chunk's end)
+  void* wT_out;           // optional out [NC, H, K, 64] w^T per chunk (bf16 compute only, zero past the chunk's end)
   int64_t it0, it_span;   // it_span > 0 (cu == nullptr): only local chunks it0 .. it0 + it_span - 1 of each
                           // sequence, grid N * it_span (chunks past a sequence's end exit)
   // uT == nullptr: no u pass (v is not read)
@@ -184,6 +185,9 @@ struct BwdArgs {
   float* dg;              // out [B*T, H]
   void* db;               // out [B*T, H] beta_dtype
   float* dh0;             // out [N, H, K, V] or nullptr
+  void* qT;               // [NC, H, K, 64] q^T per chunk (zero past the chunk's end): written by the
+                          // dv_local stage when set, read by the dh recurrence
+  const void* wT;         // [NC, H, K, 64] w^T per chunk (zero past the chunk's end)
   const int64_t* cu;
   const int32_t* chunk_off;
   int N;
@@ -196,6 +200,9 @@ bool bwd_supported(int compute_dtype, int K, int V);
 // be null to skip their stores) and BWD_GRADS (dq, dk, dw, dg, then the WY backward: dq .. dbeta)
 enum : int { BWD_DVL = 1, BWD_DHU = 2, BWD_GRADS = 4, BWD_ALL = 7 };
 int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_grid, int stages, hipStream_t s);
+// the dh recurrence for K = 256 in bf16 with 64 value columns per workgroup (needs qT, wT, dh and dv2)
+bool wide_dhu_supported(int compute_dtype, int K, int V);
+int launch_wide_dhu(const BwdArgs& a, int V, hipStream_t s);
 int launch_l2norm_bwd(const void* x, const void* dy, void* dx, int dtype, int64_t rows, int D, hipStream_t s);
 
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported

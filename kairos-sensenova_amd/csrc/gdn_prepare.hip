@@ -369,6 +369,24 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
       if (t < nv) st4<TC>(w_out + ((t0 + t) * H + h) * K + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
     }
   }
+  // ---- optional w^T per chunk, [NC, H, K, 64]: the same product with the operands swapped (rows t,
+  //      cols d), so that a lane holds 4 consecutive t of one d (one 8-byte store); rows t past the
+  //      chunk's end are zero (k is zero there and Ai is the identity)
+  if constexpr (std::is_same<TC, bf16>::value) {
+    if (a.wT_out) {
+      TC* wt = reinterpret_cast<TC*>(a.wT_out) + (cidx * H + h) * (K * C);
+      for (int tn = wid; tn < K / 16; tn += 4) {
+#pragma unroll
+        for (int tm = 0; tm < 4; ++tm) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks <= tm / 2; ++ks)
+            mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_kbT, L::LDT, 16 * tn, 32 * ks));
+          st4<TC>(wt + (16 * tn + lc) * C + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
+        }
+      }
+    }
+  }
   // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
   //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after Ai,
   //      so staging overlaps the w products above

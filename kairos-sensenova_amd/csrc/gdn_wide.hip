@@ -525,6 +525,346 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward dh recurrence for K = 256, bf16 (fla ops/common/chunk_delta_h.py:250-438): one workgroup
+// per (sequence, head, 64 value columns), four compute waves of 16 columns each holding dh over all
+// 256 rows (fp32, accumulator layout, the paired row order above) and four loader waves.  Per
+// chunk, last to first:
+//
+//   dh[c] = bf16(dh)                                          stored for the gradient kernels
+//   dv2   = (k bf16(dh)) exp(g_last - gc) + dv_local          0 past the chunk's end; stored
+//   dh    = exp(g_last) dh + q^T (do exp(gc) scale) - w^T bf16(dv2)
+//
+// The reference forms q exp(gc) in fp32 and takes its product with do in fp32; here q stays bf16
+// (exact) and x = do exp(gc) scale enters as hi + lo = bf16(x) + bf16(x - bf16(x)): two bf16
+// products, 16 significant bits in that operand.
+//
+// Operands, all in the contiguous K order: k [64 t][256] as the A operand of k dh (rows rowA, the
+// forward's w tile); q^T and w^T [256 d][64 t] per chunk (written by the dv_local stage and the
+// prepare kernel) as the A operands of the update (rows rowA, the forward's k^T tile); do and
+// dv_local [64 t][64] read transposed (the forward's v tile); dv2 from its accumulator tiles.  After
+// B1 (k, q^T, do, gc in LDS): the snapshot, k dh and the q^T x update; after B2 (w^T, dv_local in
+// LDS): dv2 and the w^T dv2 update.  The snapshot and dv2 leave through LDS tiles that the loader
+// waves store as whole 128-byte rows; chunk c of row r sits at c ^ 2 ((r / 8) % 4), so the four lane
+// groups of a compute wave's 2-byte writes (rows 8 apart) land on distinct banks.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swz_s(int r) { return ((r >> 3) & 3) << 1; }
+
+namespace dhu_lds {
+constexpr uint32_t K_OFF = 0;                        // k [64][256]
+constexpr uint32_t QW_OFF = K_OFF + C * FK * 2;      // q^T [256][64], then w^T
+constexpr uint32_t W_REL = FK * C * 2;               // w^T - q^T
+constexpr uint32_t SNAP_OFF = QW_OFF + 2 * W_REL;    // bf16(dh) [256][64]
+constexpr uint32_t DO_OFF = SNAP_OFF + FK * C * 2;   // do [64][64]
+constexpr uint32_t DL_OFF = DO_OFF + C * C * 2;      // dv_local [64][64]
+constexpr uint32_t DV_OFF = DL_OFF + C * C * 2;      // bf16(dv2) [64][64]
+constexpr uint32_t G_OFF = DV_OFF + C * C * 2;       // gc, two buffers
+constexpr uint32_t PF_OFF = G_OFF + 2 * C * 4;       // landing words of the L2 prefetch
+constexpr uint32_t TOTAL = PF_OFF + WAVE * 4;
+}  // namespace dhu_lds
+
+__device__ __forceinline__ void lds_st16(uint32_t a, uint32_t off, bf16 x) {
+  *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(reinterpret_cast<lds_b*>(a) + off) =
+      __builtin_bit_cast(uint16_t, x);
+}
+
+__global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, int V, int total_units) {
+  using namespace dhu_lds;
+  __shared__ __align__(16) unsigned char smem[TOTAL];
+  const uint32_t base = lds_u32(smem);
+
+  const int per_xcd = gridDim.x / 8;                      // XCD-aware order, as the forward
+  const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (o_idx >= total_units) return;
+  const int nvt = V / FVT;
+  const int unit = o_idx / nvt;
+  const int H = a.H;
+  const int n = unit / H, h = unit % H;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int vt0 = __builtin_amdgcn_readfirstlane((o_idx % nvt) * FVT);
+
+  int64_t bos, eos, c_first;
+  if (a.cu == nullptr) {
+    bos = (int64_t)n * a.T;
+    eos = bos + a.T;
+    c_first = (int64_t)n * ((a.T + C - 1) / C);
+  } else {
+    bos = a.cu[n];
+    eos = a.cu[n + 1];
+    c_first = a.chunk_off[n];
+  }
+  const int64_t nchunks = (eos - bos + C - 1) / C;
+  const int64_t top = nchunks - 1;
+  auto chunk_nv = [&](int64_t it) { return (int)min((int64_t)C, eos - (bos + it * C)); };
+  const bf16* qtb = reinterpret_cast<const bf16*>(a.qT);
+  const bf16* wtb = reinterpret_cast<const bf16*>(a.wT);
+
+  if (wid >= FW) {
+    // ---- the loader waves.  Loader lw issues load i of each tile for i % FL = lw.  After B1: w^T and
+    //      dv_local of chunk it (8 + 2 loads each), then the dv2 tile of chunk it + 1 out (2 stores);
+    //      each waits for its loads before B2.  After B2: k, q^T, do of chunk it - 1 (8 + 8 + 2, and gc
+    //      from loader 0 into the other buffer), its part of the L2 prefetch of chunk it - 2, then the
+    //      snapshot of chunk it out (8 stores); each waits for its loads before the next B1.
+    const int lw = wid - FW;
+    const uint32_t RB = (uint32_t)H * FK * 2, VB = (uint32_t)H * V * 2;
+    auto load_a = [&](int64_t it, uint32_t gb) {
+      const int64_t c = c_first + it, t0 = bos + it * C;
+      const int nv = chunk_nv(it);
+      const unsigned char* kb = reinterpret_cast<const unsigned char*>(a.k) + (size_t)((t0 * H + h) * FK) * 2;
+      const unsigned char* qb = reinterpret_cast<const unsigned char*>(qtb + (c * H + h) * (int64_t)(FK * C));
+      const unsigned char* db = reinterpret_cast<const unsigned char*>(a.do_) + (size_t)((t0 * H + h) * V + vt0) * 2;
+#pragma unroll
+      for (int j = 0; j < 32 / FL; ++j) ld_tile256(kb, RB, nv, FL * j + lw, base + K_OFF);
+#pragma unroll
+      for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(qb, 128u, FK, FL * j + lw, base + QW_OFF);
+#pragma unroll
+      for (int j = 0; j < 8 / FL; ++j) ld_tile64<false>(db, VB, nv, FL * j + lw, base + DO_OFF);
+      if (lw == 0) dma4_(a.gc + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, base + G_OFF + gb * C * 4);
+    };
+    auto load_b = [&](int64_t it) {
+      const int64_t c = c_first + it, t0 = bos + it * C;
+      const int nv = chunk_nv(it);
+      const unsigned char* wb = reinterpret_cast<const unsigned char*>(wtb + (c * H + h) * (int64_t)(FK * C));
+      const unsigned char* lb = reinterpret_cast<const unsigned char*>(a.dvl) + (size_t)((t0 * H + h) * V + vt0) * 2;
+#pragma unroll
+      for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(wb, 128u, FK, FL * j + lw, base + QW_OFF + W_REL);
+#pragma unroll
+      for (int j = 0; j < 8 / FL; ++j) ld_tile64<false>(lb, VB, nv, FL * j + lw, base + DL_OFF);
+    };
+    // L2 prefetch of chunk it: one 4-byte load per 128-byte line; the shared k, q^T, w^T lines split
+    // over the head's V tiles by quarter (loaders 0-2), this tile's do and dv_local rows (loader 3)
+    const int pf_q = (vt0 / FVT) & 3;
+    auto prefetch = [&](int64_t it) {
+      const int64_t c = c_first + it, t0 = bos + it * C;
+      const int nv = chunk_nv(it);
+      const uint32_t pf = base + PF_OFF;
+      if (lw == 0) {
+        const int r = 16 * pf_q + (l >> 2);
+        dma4_(reinterpret_cast<const unsigned char*>(a.k) + (size_t)((t0 * H + h) * FK) * 2,
+              (uint32_t)(r < nv ? r : 0) * RB + 128u * (l & 3), pf);
+      } else if (lw == 1) {
+        dma4_(qtb + (c * H + h) * (int64_t)(FK * C), 128u * (64 * pf_q + l), pf);
+      } else if (lw == 2) {
+        dma4_(wtb + (c * H + h) * (int64_t)(FK * C), 128u * (64 * pf_q + l), pf);
+      } else {
+        const uint32_t off = (uint32_t)(l < nv ? l : 0) * VB;
+        dma4_(reinterpret_cast<const unsigned char*>(a.do_) + (size_t)((t0 * H + h) * V + vt0) * 2, off, pf);
+        dma4_(reinterpret_cast<const unsigned char*>(a.dvl) + (size_t)((t0 * H + h) * V + vt0) * 2, off, pf);
+      }
+    };
+    // LDS tile rows (128 bytes, swizzle swz_s) out to HBM: rows 8 i .. 8 i + 7 for i % FL = lw
+    auto tile_row = [&](uint32_t off, int r) {
+      return *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(base + off) + 128 * r +
+                                                 16 * ((l & 7) ^ swz_s(r)));
+    };
+    auto store_dv = [&](int64_t it) {
+      const int64_t t0 = bos + it * C;
+      const int nv = chunk_nv(it);
+#pragma unroll
+      for (int j = 0; j < 8 / FL; ++j) {
+        const int t = 8 * (FL * j + lw) + (l >> 3);
+        const u32x4 x = tile_row(DV_OFF, t);
+        if (t < nv)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.dv2) + (((t0 + t) * H + h) * V + vt0 + 8 * (l & 7)) * 2) = x;
+      }
+    };
+    auto store_snap = [&](int64_t it) {
+      const int64_t c = c_first + it;
+#pragma unroll
+      for (int j = 0; j < 32 / FL; ++j) {
+        const int d = 8 * (FL * j + lw) + (l >> 3);
+        const u32x4 x = tile_row(SNAP_OFF, d);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.dh) + (((c * H + h) * FK + d) * V + vt0 + 8 * (l & 7)) * 2) = x;
+      }
+    };
+    if (nchunks > 0) {
+      load_a(top, 0u);
+      if (top >= 1) prefetch(top - 1);
+    }
+    wait_all_loads();
+    for (int64_t it = top; it >= 0; --it) {
+      const uint32_t gb = (uint32_t)((top - it) & 1);
+      f_barrier();                                        // B1
+      load_b(it);
+      if (it < top) {
+        store_dv(it + 1);
+        wait_loads_but<8 / FL>();
+      } else {
+        wait_all_loads();
+      }
+      f_barrier();                                        // B2
+      if (it > 0) {
+        load_a(it - 1, gb ^ 1u);
+        if (it > 1) prefetch(it - 2);
+        store_snap(it);
+        if (it > 1) {
+          if (lw == 3) wait_loads_but<32 / FL + 2>();
+          else wait_loads_but<32 / FL + 1>();
+        } else {
+          wait_loads_but<32 / FL>();
+        }
+      } else {
+        store_snap(it);
+      }
+    }
+    f_barrier();                                          // dv2 of the first chunk is in LDS
+    if (nchunks > 0) store_dv(0);
+    wait_all_loads();                                     // no direct load outlives the workgroup's LDS
+    return;
+  }
+
+  // ---- the compute waves: wave wid owns value columns vt0 + 16 wid .. + 15
+  const int vcol = vt0 + 16 * wid + lc;
+  // dh[kt][j] = dh[32 (kt / 2) + 8 lg + 4 (kt % 2) + j][vcol] (the paired row order)
+  f32x4 dh[16];
+#pragma unroll
+  for (int kt = 0; kt < 16; ++kt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t off = (((int64_t)n * H + h) * FK + 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1) + j) * V + vcol;
+      dh[kt][j] = a.dht ? a.dht[off] : 0.f;
+    }
+  // lane addresses: kq[k] the k tile (row rowA(0, lc), chunk 4 ks + lg for ks % 4 = k; ks + 4 adds 256
+  // bytes, tile tm adds rowa_off(tm, 512)); tq[ks] the q^T tile (row rowA(0, lc), chunk 4 ks + lg; tile
+  // kt adds rowa_off(kt, 128), w^T at + W_REL); vt the transposed reads of the do tile (rows 8 lg +
+  // lc / 4, columns 16 wid + 4 (lc % 4); dv_local at + DL_OFF - DO_OFF); sw the 2-byte writes of row
+  // 8 lg, column 16 wid + lc of the snapshot tile (dv2 tile at + DV_OFF - SNAP_OFF)
+  const int r0 = 8 * (lc >> 2) + (lc & 3);
+  uint32_t kq[4], tq[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) kq[k] = base + K_OFF + 512 * r0 + 16 * ((4 * k + lg) ^ swz_wq(r0));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) tq[ks] = base + QW_OFF + 128 * r0 + 16 * ((4 * ks + lg) ^ swz_a(r0));
+  uint32_t vt, sw;
+  {
+    const int rv = 8 * lg + (lc >> 2), cv = 16 * wid + 4 * (lc & 3);
+    vt = base + DO_OFF + 128 * rv + 16 * ((cv >> 3) ^ swz_v(rv)) + 2 * (cv & 7);
+    const int cs = 16 * wid + lc;
+    sw = base + SNAP_OFF + 128 * (8 * lg) + 16 * ((cs >> 3) ^ swz_s(8 * lg)) + 2 * (cs & 7);
+  }
+  constexpr uint32_t DL_REL = DL_OFF - DO_OFF, DV_REL = DV_OFF - SNAP_OFF;
+  const float* s_g = reinterpret_cast<const float*>(smem + G_OFF);
+
+  for (int64_t it = top; it >= 0; --it) {
+    const uint32_t gb = (uint32_t)((top - it) & 1);
+    const int nv = chunk_nv(it);
+    f_barrier();                                          // B1: k, q^T, do, gc of chunk it
+    const float* G = s_g + gb * C;
+    Frag<bf16> xr[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) xr[ks] = frag2(ldtr(vt, 4096u * ks), ldtr(vt, 4096u * ks + 512u));
+    Frag<bf16> ka[2][4], qa[2][4];
+    auto read_a = [&](int g, Frag<bf16>(&k4)[4], Frag<bf16>(&q4)[4]) {
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) k4[tm] = ld128(kq[g & 3], 256u * (g >> 2) + rowa_off(tm, 512));
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) q4[2 * x + ks] = ld128(tq[ks], rowa_off(2 * g + x, 128));
+    };
+    read_a(0, ka[0], qa[0]);
+    const float gl = G[nv - 1];
+    f32x4 gv[4];                                          // gc of tokens 32 (i / 2) + 8 lg + 4 (i % 2) + j
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gv[i] = *reinterpret_cast<const f32x4*>(G + 32 * (i >> 1) + 8 * lg + 4 * (i & 1));
+    // x = do exp(gc) scale (tokens 32 ks + 8 lg + e, 0 past the chunk's end) as hi + lo
+    Frag<bf16> xh[2], xl[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = 32 * ks + 8 * lg + e;
+        const float x = t < nv ? (float)xr[ks].v[e] * (gexp(gv[2 * ks + (e >> 2)][e & 3]) * a.scale) : 0.f;
+        const bf16 hi = (bf16)x;
+        xh[ks].v[e] = hi;
+        xl[ks].v[e] = (bf16)(x - (float)hi);
+      }
+    const float eg = gexp(gl);
+    f32x4 kd[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) kd[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // k bf16(dh) and dh = exp(g_last) dh + q^T x, 32 rows of dh per group (their bf16 values, the B
+    // operand of k dh and the snapshot, packed before the update); operand reads one group ahead
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g + 1 < 8) read_a(g + 1, ka[(g + 1) & 1], qa[(g + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const Frag<bf16> hb = pack_acc(dh[2 * g], dh[2 * g + 1]);
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) mma(kd[tm], ka[g & 1][tm], hb);
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        dh[2 * g + x] *= eg;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          mma(dh[2 * g + x], qa[g & 1][2 * x + ks], xh[ks]);
+          mma(dh[2 * g + x], qa[g & 1][2 * x + ks], xl[ks]);
+        }
+      }
+      // the snapshot rows of this group
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds_st16(sw, rowa_off(2 * g + x, 128) + 128u * j, hb.v[4 * x + j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f_barrier();                                          // B2: w^T, dv_local of chunk it
+
+    // dv2 = k bf16(dh) exp(g_last - gc) + dv_local (rows 32 (tm / 2) + 8 lg + 4 (tm % 2) + j)
+    u32x2 dl[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) dl[tm] = ldtr(vt, DL_REL + rowa_off(tm, 128));
+    Frag<bf16> wa[2][8];
+    auto read_w = [&](int g4, Frag<bf16>(&w8)[8]) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) w8[2 * q + ks] = ld128(tq[ks], W_REL + rowa_off(4 * g4 + q, 128));
+    };
+    read_w(0, wa[0]);
+    f32x4 dv[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      const float d4[4] = {__uint_as_float(dl[tm][0] << 16), __uint_as_float(dl[tm][0] & 0xffff0000u),
+                           __uint_as_float(dl[tm][1] << 16), __uint_as_float(dl[tm][1] & 0xffff0000u)};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 32 * (tm >> 1) + 8 * lg + 4 * (tm & 1) + j;
+        dv[tm][j] = t < nv ? kd[tm][j] * gexp(gl - gv[tm][j]) + d4[j] : 0.f;
+      }
+    }
+    Frag<bf16> nd[2];                                     // -bf16(dv2) as the update's B operand
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) nd[ks] = pack_acc(-dv[2 * ks], -dv[2 * ks + 1]);
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lds_st16(sw, DV_REL + rowa_off(tm, 128) + 128u * j, (bf16)dv[tm][j]);
+    // dh -= w^T bf16(dv2)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      if (g4 + 1 < 4) read_w(g4 + 1, wa[(g4 + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) mma(dh[4 * g4 + q], wa[g4 & 1][2 * q + ks], nd[ks]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  f_barrier();                                            // dv2 of the first chunk is in LDS for the loaders
+
+  if (a.dh0) {
+#pragma unroll
+    for (int kt = 0; kt < 16; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t off = (((int64_t)n * H + h) * FK + 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1) + j) * V + vcol;
+        a.dh0[off] = dh[kt][j];
+      }
+  }
+}
+
 }  // namespace
 
 __global__ void marker_kernel() {}
@@ -535,6 +875,19 @@ bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V) {
 
 int launch_marker(hipStream_t s) {
   hipLaunchKernelGGL(marker_kernel, dim3(1), dim3(WAVE), 0, s);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+bool wide_dhu_supported(int compute_dtype, int K, int V) {
+  return compute_dtype == DT_BF16 && K == FK && V > 0 && V % FVT == 0;
+}
+
+int launch_wide_dhu(const BwdArgs& a, int V, hipStream_t s) {
+  if (V % FVT != 0 || !a.qT || !a.wT || !a.dh || !a.dv2) return -2;
+  const int total = a.N * a.H * (V / FVT);
+  if (total == 0) return 0;
+  const int grid = (total + 7) / 8 * 8;
+  hipLaunchKernelGGL(wide_dhu_kernel, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
