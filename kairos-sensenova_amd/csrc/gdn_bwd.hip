@@ -1133,9 +1133,19 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
     }
   }
   if (nc_grid > 0 && (stages & BWD_GRADS)) {
-    const size_t l3 = dqkwg_lds<TC>(K);
-    if (set_lds(bwd_dqkwg_kernel<TC, K>, l3)) return -1;
-    hipLaunchKernelGGL((bwd_dqkwg_kernel<TC, K>), grid, dim3(NT_B), l3, s, a, V);
+    bool wide = false;
+    if constexpr (sizeof(TC) == 2 && K == 256) {      // eight waves per chunk (KAIROS_GDN_BWD_DQK_WIDE=0: four)
+      const char* e = std::getenv("KAIROS_GDN_BWD_DQK_WIDE");
+      wide = !(e && e[0] == '0' && e[1] == 0);
+      if (wide) {
+        if (int rc = launch_wide_dqkwg(a, V, nc_grid, s)) return rc;
+      }
+    }
+    if (!wide) {
+      const size_t l3 = dqkwg_lds<TC>(K);
+      if (set_lds(bwd_dqkwg_kernel<TC, K>, l3)) return -1;
+      hipLaunchKernelGGL((bwd_dqkwg_kernel<TC, K>), grid, dim3(NT_B), l3, s, a, V);
+    }
     const size_t l4 = wy_lds<TC>(K, V);
     if (l4 > 160 * 1024 || set_lds(bwd_wy_kernel<TC, K>, l4)) return -1;
     hipLaunchKernelGGL((bwd_wy_kernel<TC, K>), grid, dim3(NT_B), l4, s, a, V);

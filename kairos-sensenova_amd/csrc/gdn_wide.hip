@@ -865,6 +865,331 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// dq, dk, dw, dg for K = 256, bf16 (fla ops/common/chunk_o.py:147-326 with USE_G and USE_DW): one
+// workgroup of eight waves per (chunk, head).  Wave w owns K rows 32 w .. 32 w + 31: it reads those
+// rows of h and dh once, straight from global memory as A operands, while do, dv2 and v_new pass
+// through LDS in 64-column blocks (two buffers, direct loads) shared by the eight waves.  The
+// products are formed transposed ([d][t] tiles), so a lane stores 4 consecutive d of one token.
+//
+//   ds  = mask_{i>=j, i<nv}(do v_new^T exp(g_i - g_j)) scale      rounded to bf16 for its products
+//   dq  = (h do)^T exp(gc) scale + ds k
+//   dk  = (dh v_new)^T exp(g_last - gc) + ds^T q                  (dk1 + dk2, the WY stage adds more)
+//   dw  = -(h dv2)^T
+//   dg  = rowsum(ds2) - colsum(ds2) + sum_d (dq1 q - dk1 k), ds2 = ds (q k^T); the last row adds
+//         sum dk1 k + exp(g_last) sum h dh
+//
+// Tiles with natural rows read as b128 row pieces: q, k [64][256] with chunk c of row r at
+// c ^ swz_n(r), the 64-column blocks [64][64] at c ^ swz_v(r); both give the 16 lanes of a pass
+// distinct bank positions for rows 16 x + lc and chunks 4 ks + lg.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swz_n(int r) { return ((r & 1) << 1) | (((r >> 1) & 1) << 2) | (((r >> 3) & 1) << 3); }
+
+constexpr int DQ_NW = 8;
+constexpr int DQ_NT = DQ_NW * WAVE;
+
+namespace dq_lds {
+constexpr uint32_t Q_OFF = 0;                             // q [64][256]
+constexpr uint32_t K_OFF = C * FK * 2;                    // k [64][256]
+constexpr uint32_t BLK_OFF = 2 * C * FK * 2;              // two buffers of do, dv2, v_new [64][64]
+constexpr uint32_t TILE = C * C * 2;
+constexpr uint32_t BLK = 3 * TILE;
+constexpr uint32_t DS_OFF = BLK_OFF + 2 * BLK;            // bf16(ds) [64][64]
+constexpr uint32_t G_OFF = DS_OFF + TILE;                 // gc [64]
+constexpr uint32_t ROW_OFF = G_OFF + C * 4;               // ds2 row sums per lower tile [10][16]
+constexpr uint32_t COL_OFF = ROW_OFF + 10 * 16 * 4;       // ds2 column sums per lower tile [10][16]
+constexpr uint32_t DGT_OFF = COL_OFF + 10 * 16 * 4;       // sum_d (dq1 q - dk1 k) per wave [8][64]
+constexpr uint32_t SC_OFF = DGT_OFF + DQ_NW * C * 4;      // per wave: sum dk1 k [8], sum h dh [8]
+constexpr uint32_t TOTAL = SC_OFF + 2 * DQ_NW * 4;
+}  // namespace dq_lds
+
+// instruction i of a [64][256] tile with natural rows (rows 2 i, 2 i + 1; swizzle swz_n)
+__device__ __forceinline__ void ld_rows256(const unsigned char* base, uint32_t row_bytes, int nv, int i, uint32_t dst) {
+  const int l = lane_id(), r = 2 * i + (l >> 5), pos = l & 31;
+  const uint32_t rr = r < nv ? (uint32_t)r : 0u;
+  dma16_(base, rr * row_bytes + 16u * (pos ^ swz_n(r)), dst + 1024u * i);
+}
+
+__device__ __forceinline__ float wsum_lg(float x) {
+  x += __shfl_xor(x, 16, WAVE);
+  x += __shfl_xor(x, 32, WAVE);
+  return x;
+}
+__device__ __forceinline__ float wsum16(float x) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o, WAVE);
+  return x;
+}
+__device__ __forceinline__ float wsum64(float x) {
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) x += __shfl_xor(x, o, WAVE);
+  return x;
+}
+
+__global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
+  using namespace dq_lds;
+  __shared__ __align__(16) unsigned char smem[TOTAL];
+  const uint32_t base = lds_u32(smem);
+  const int h = blockIdx.y, H = a.H;
+  const int64_t c = blockIdx.x;
+  const ChunkLoc loc = locate_chunk(c, a.cu, a.chunk_off, a.N, a.T);
+  if (!loc.ok) return;
+  const int64_t t0 = loc.t0;
+  const int nv = loc.nv;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int nvb = V / C;                                   // 64-column blocks
+  const uint32_t RB = (uint32_t)H * FK * 2, VB = (uint32_t)H * V * 2;
+  const unsigned char* dob = reinterpret_cast<const unsigned char*>(a.do_) + (size_t)((t0 * H + h) * V) * 2;
+  const unsigned char* dvb = reinterpret_cast<const unsigned char*>(a.dv2) + (size_t)((t0 * H + h) * V) * 2;
+  const unsigned char* vnb = reinterpret_cast<const unsigned char*>(a.vn) + (size_t)((t0 * H + h) * V) * 2;
+  // block vb of do, dv2, v_new into buffer P: 24 loads, 3 per wave
+  auto load_blk = [&](int vb, uint32_t P) {
+    const uint32_t dst = base + BLK_OFF + P * BLK;
+    ld_tile64<false>(dob + (size_t)vb * C * 2, VB, nv, wid, dst);               // rows 8 wid .. + 7 of each
+    ld_tile64<false>(dvb + (size_t)vb * C * 2, VB, nv, wid, dst + TILE);
+    ld_tile64<false>(vnb + (size_t)vb * C * 2, VB, nv, wid, dst + 2 * TILE);
+  };
+  {
+    const unsigned char* qb = reinterpret_cast<const unsigned char*>(a.q) + (size_t)((t0 * H + h) * FK) * 2;
+    const unsigned char* kb = reinterpret_cast<const unsigned char*>(a.k) + (size_t)((t0 * H + h) * FK) * 2;
+#pragma unroll
+    for (int j = 0; j < 32 / DQ_NW; ++j) ld_rows256(qb, RB, nv, DQ_NW * j + wid, base + Q_OFF);
+#pragma unroll
+    for (int j = 0; j < 32 / DQ_NW; ++j) ld_rows256(kb, RB, nv, DQ_NW * j + wid, base + K_OFF);
+    load_blk(0, 0u);
+    if (wid == 0) dma4_(a.gc + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, base + G_OFF);
+  }
+  // this wave's rows of h and dh: A operands of rows d = 32 wid + 16 dt + lc, columns 64 vb + 32 ks + 8 lg ..
+  const bf16* hrow = reinterpret_cast<const bf16*>(a.h) + ((c * H + h) * FK + 32 * wid + lc) * (int64_t)V + 8 * lg;
+  const bf16* dhrow = reinterpret_cast<const bf16*>(a.dh) + ((c * H + h) * FK + 32 * wid + lc) * (int64_t)V + 8 * lg;
+  auto load_hd = [&](int vb, Frag<bf16>(&hf)[4], Frag<bf16>(&df)[4]) {
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int64_t off = 16 * dt * (int64_t)V + C * vb + 32 * ks;
+        hf[2 * dt + ks].v = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(hrow + off));
+        df[2 * dt + ks].v = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(dhrow + off));
+      }
+  };
+  Frag<bf16> hf[2][4], df[2][4];
+  load_hd(0, hf[0], df[0]);
+  wait_all_loads();
+  f_barrier();
+
+  // the lower 16 x 16 tiles (tm >= tn) of ds this wave accumulates: tile wid, and tile wid + 8 for waves 0, 1
+  const int ntile = wid < 2 ? 2 : 1;
+  auto tile_mn = [](int idx, int& tm, int& tn) {
+    tm = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
+    tn = idx - tm * (tm + 1) / 2;
+  };
+  const int r0 = lc;                                       // natural rows 16 x + lc
+  const uint32_t qrd = base + Q_OFF + 512 * r0, krd = base + K_OFF + 512 * r0;
+  // q k^T of the ds tiles (B1 data: q, k)
+  f32x4 aqk[2], dsa[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    aqk[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dsa[s] = aqk[s];
+    if (s < ntile) {
+      int tm, tn;
+      tile_mn(wid + 8 * s, tm, tn);
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const uint32_t co = 16u * ((4 * ks + lg) ^ swz_n(r0));
+        mma(aqk[s], ld128(qrd, 512u * 16 * tm + co), ld128(krd, 512u * 16 * tn + co));
+      }
+    }
+  }
+
+  // the main products over the value columns
+  f32x4 aq[2][4], aw[2][4], ak[2][4];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) aq[dt][tt] = aw[dt][tt] = ak[dt][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float hdh = 0.f;
+  const uint32_t brd = base + BLK_OFF + 128 * r0;          // block tiles, row r0
+  auto block = [&](auto PP, int vb) {
+    constexpr uint32_t P = decltype(PP)::value;
+    if (vb + 1 < nvb) {
+      load_blk(vb + 1, P ^ 1u);
+      load_hd(vb + 1, hf[P ^ 1u], df[P ^ 1u]);
+    }
+    const uint32_t bb = brd + P * BLK;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      Frag<bf16> fdo[2], fdv[2], fvn[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t o = 128u * 16 * tt + 16u * ((4 * ks + lg) ^ swz_v(r0));
+        fdo[ks] = ld128(bb, o);
+        fdv[ks] = ld128(bb, TILE + o);
+        fvn[ks] = ld128(bb, 2 * TILE + o);
+      }
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          mma(aq[dt][tt], hf[P][2 * dt + ks], fdo[ks]);    // sum_v h[d][v] do[t][v]
+          mma(aw[dt][tt], hf[P][2 * dt + ks], fdv[ks]);    // sum_v h[d][v] dv2[t][v]
+          mma(ak[dt][tt], df[P][2 * dt + ks], fvn[ks]);    // sum_v dh[d][v] v_new[t][v]
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (s < ntile) {
+        int tm, tn;
+        tile_mn(wid + 8 * s, tm, tn);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint32_t o = 16u * ((4 * ks + lg) ^ swz_v(r0));
+          mma(dsa[s], ld128(bb, 128u * 16 * tm + o), ld128(bb, 2 * TILE + 128u * 16 * tn + o));   // do v_new^T
+        }
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < 4; ++f)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hdh += (float)hf[P][f].v[e] * (float)df[P][f].v[e];
+    wait_all_loads();
+    f_barrier();
+  };
+  for (int vb = 0; vb < nvb; vb += 2) {
+    block(std::integral_constant<uint32_t, 0>{}, vb);
+    if (vb + 1 < nvb) block(std::integral_constant<uint32_t, 1>{}, vb + 1);
+  }
+
+  // ds (rounded into LDS) and the row / column sums of ds2 = ds (q k^T), per tile
+  const float* s_g = reinterpret_cast<const float*>(smem + G_OFF);
+  float* s_row = reinterpret_cast<float*>(smem + ROW_OFF);
+  float* s_col = reinterpret_cast<float*>(smem + COL_OFF);
+  float* s_dgt = reinterpret_cast<float*>(smem + DGT_OFF);
+  float* s_sc = reinterpret_cast<float*>(smem + SC_OFF);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s < ntile) {
+      const int idx = wid + 8 * s;
+      int tm, tn;
+      tile_mn(idx, tm, tn);
+      const int j = 16 * tn + lc;
+      float colp = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 16 * tm + 4 * lg + jj;
+        const float ds = (i >= j && i < nv) ? dsa[s][jj] * gexp(s_g[i] - s_g[j]) * a.scale : 0.f;
+        const float ds2 = ds * aqk[s][jj];
+        colp += ds2;
+        const float rs = wsum16(ds2);
+        if (lc == 0) s_row[idx * 16 + 4 * lg + jj] = rs;
+        *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
+            reinterpret_cast<lds_b*>(base + DS_OFF) + 128 * i + 16 * ((j >> 3) ^ swz_v(i)) + 2 * (j & 7)) =
+            __builtin_bit_cast(uint16_t, (bf16)ds);
+      }
+      colp = wsum_lg(colp);
+      if (lg == 0) s_col[idx * 16 + lc] = colp;
+    }
+  }
+  if (wid >= 2) {                                          // the six upper tiles of ds are zero
+    const int u = wid - 2, tm = u < 3 ? 0 : u < 5 ? 1 : 2, tn = u < 3 ? u + 1 : u < 5 ? u - 1 : 3;
+    const int j = 16 * tn + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int i = 16 * tm + 4 * lg + jj;
+      *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(
+          reinterpret_cast<lds_b*>(base + DS_OFF) + 128 * i + 16 * ((j >> 3) ^ swz_v(i)) + 2 * (j & 7)) = 0;
+    }
+  }
+  f_barrier();
+
+  // dq = dq1 + ds k, dk = dk1 + ds^T q, dw; the state terms of dg
+  const float gl = s_g[nv - 1];
+  float dglp = 0.f;
+  bf16* dq_out = reinterpret_cast<bf16*>(a.dq);
+  bf16* dk_out = reinterpret_cast<bf16*>(a.dk1);
+  bf16* dw_out = reinterpret_cast<bf16*>(a.dw);
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = 16 * tt + lc;
+    const float egs = gexp(s_g[t]) * a.scale;
+    const float gate = t < nv ? gexp(gl - s_g[t]) : 0.f;
+    float dgt = 0.f;
+    // B operands: row t of ds (dq's ds k, K = t'), column t of ds read transposed (dk's ds^T q, K = i)
+    Frag<bf16> bq[2], bk[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bq[ks] = ld128(base + DS_OFF + 128 * t, 16u * ((4 * ks + lg) ^ swz_v(t)));
+      const int ri = 32 * ks + 8 * lg + (lc >> 2), ci = 16 * tt + 4 * (lc & 3);
+      const uint32_t ta = base + DS_OFF + 128 * ri + 16 * ((ci >> 3) ^ swz_v(ri)) + 2 * (ci & 7);
+      bk[ks] = frag2(ldtr(ta, 0), ldtr(ta, 512u));       // rows ri + 4: the same swizzle (bits 1, 3)
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int d0 = 32 * wid + 16 * dt, k0 = d0 + 4 * lg;
+      const u32x2 qw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + Q_OFF) + 512 * t +
+                                                             16 * ((k0 >> 3) ^ swz_n(t)) + 2 * (k0 & 7));
+      const u32x2 kw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + K_OFF) + 512 * t +
+                                                             16 * ((k0 >> 3) ^ swz_n(t)) + 2 * (k0 & 7));
+      const float qv[4] = {__uint_as_float(qw[0] << 16), __uint_as_float(qw[0] & 0xffff0000u),
+                           __uint_as_float(qw[1] << 16), __uint_as_float(qw[1] & 0xffff0000u)};
+      const float kv[4] = {__uint_as_float(kw[0] << 16), __uint_as_float(kw[0] & 0xffff0000u),
+                           __uint_as_float(kw[1] << 16), __uint_as_float(kw[1] & 0xffff0000u)};
+      f32x4 dq = aq[dt][tt] * egs, dk = ak[dt][tt] * gate;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dgt += dq[j] * qv[j] - kv[j] * dk[j];
+        dglp += dk[j] * kv[j];
+      }
+      // A operands k^T, q^T: rows d0 + lc, K = t' = 32 ks + 8 lg .. + 7 (transposed reads of the row tiles)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int rt = 32 * ks + 8 * lg + (lc >> 2), ct = d0 + 4 * (lc & 3);
+        const uint32_t oa = 512 * rt + 16 * ((ct >> 3) ^ swz_n(rt)) + 2 * (ct & 7);
+        const uint32_t ob = 512 * (rt + 4) + 16 * ((ct >> 3) ^ swz_n(rt + 4)) + 2 * (ct & 7);
+        mma(dq, frag2(ldtr(base + K_OFF + oa, 0), ldtr(base + K_OFF + ob, 0)), bq[ks]);
+        mma(dk, frag2(ldtr(base + Q_OFF + oa, 0), ldtr(base + Q_OFF + ob, 0)), bk[ks]);
+      }
+      if (t < nv) {
+        const int64_t o = ((t0 + t) * H + h) * (int64_t)FK + k0;
+        st4<bf16>(dq_out + o, dq[0], dq[1], dq[2], dq[3]);
+        st4<bf16>(dk_out + o, dk[0], dk[1], dk[2], dk[3]);
+        st4<bf16>(dw_out + o, -aw[dt][tt][0], -aw[dt][tt][1], -aw[dt][tt][2], -aw[dt][tt][3]);
+      }
+    }
+    dgt = wsum_lg(dgt);
+    if (lg == 0) s_dgt[wid * C + t] = dgt;
+  }
+  dglp = wsum64(dglp);
+  hdh = wsum64(hdh);
+  if (l == 0) {
+    s_sc[wid] = dglp;
+    s_sc[DQ_NW + wid] = hdh;
+  }
+  f_barrier();
+  if (threadIdx.x < C) {
+    const int t = threadIdx.x;
+    if (t < nv) {
+      const int tm = t >> 4, r = t & 15;
+      float row = 0.f, col = 0.f, dgt = 0.f;
+      for (int tn = 0; tn <= tm; ++tn) row += s_row[(tm * (tm + 1) / 2 + tn) * 16 + r];
+      for (int m = tm; m < 4; ++m) col += s_col[(m * (m + 1) / 2 + tm) * 16 + r];
+#pragma unroll
+      for (int w = 0; w < DQ_NW; ++w) dgt += s_dgt[w * C + t];
+      float dg = row - col + dgt;
+      if (t == nv - 1) {
+        float sl = 0.f, sh = 0.f;
+#pragma unroll
+        for (int w = 0; w < DQ_NW; ++w) {
+          sl += s_sc[w];
+          sh += s_sc[DQ_NW + w];
+        }
+        dg += sl + sh * gexp(gl);
+      }
+      a.dg1[(t0 + t) * H + h] = dg;
+    }
+  }
+}
+
 }  // namespace
 
 __global__ void marker_kernel() {}
@@ -888,6 +1213,13 @@ int launch_wide_dhu(const BwdArgs& a, int V, hipStream_t s) {
   if (total == 0) return 0;
   const int grid = (total + 7) / 8 * 8;
   hipLaunchKernelGGL(wide_dhu_kernel, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_wide_dqkwg(const BwdArgs& a, int V, int64_t nc_grid, hipStream_t s) {
+  if (V % C != 0 || a.H <= 0) return -2;
+  if (nc_grid <= 0) return 0;
+  hipLaunchKernelGGL(wide_dqkwg_kernel, dim3((unsigned)nc_grid, a.H), dim3(DQ_NT), 0, s, a, V);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
