@@ -1276,6 +1276,13 @@ struct ProdStage {
       *reinterpret_cast<u32x4*>(smem + P::k_tile(kb) + dst_off(i)) = x;
     }
   }
+  // the L2 norm of the k rows in registers, ahead of their store (bf16 k only)
+  __device__ __forceinline__ void norm_k() {
+    if constexpr (!P::FP8) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) k[i] = l2_row(k[i]);
+    }
+  }
   // y = bf16(x / sqrt(sum x^2 + 1e-6)) over the row a unit belongs to: the K / 8 units of a row are
   // held by K / 8 consecutive lanes (l2norm.py:98-119, the in-op L2 norm of q and k).  The squares
   // are summed by packed bf16 dot products on the raw words, the row by DPP moves.
@@ -1298,6 +1305,21 @@ struct ProdStage {
     }
   }
 };
+
+// The in-op L2 norm of a q tile in LDS, in place, by the consumer threads (bf16 q): unit u = thread +
+// threads * i as in the producers' staging, so the K / 8 units of a row sit in consecutive lanes
+template <typename TQ, int K, int V>
+__device__ __forceinline__ void norm_q_tile(unsigned char* tile) {
+  using P = OutPlan<TQ, K, V>;
+  constexpr int CT = P::NCW * WAVE, NU = P::QU / CT;
+  static_assert(P::QU % CT == 0, "q units split evenly over the consumer threads");
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = (int)threadIdx.x + CT * i;
+    u32x4* p = reinterpret_cast<u32x4*>(tile + 2 * Tile<K>::off(u / (K / 8), u % (K / 8)));
+    *p = ProdStage<TQ, K, V>::l2_row(*p);
+  }
+}
 
 template <typename TQ, int K, int V>
 struct ConsStage {
@@ -1385,6 +1407,8 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     }
   }
 
+  // the in-op L2 norm of bf16 q runs on the consumers (norm_q_tile), that of k on the producers
+  const bool q_cons = a.l2 != 0 && !P::FP8;
   // consumer state: lane element (tt, ct, j) = S[16 tt + 4 lg + j][vw + 16 ct + lc]
   const int vw = wid * 16;
   f32x4 S[KT][CTN];
@@ -1427,6 +1451,10 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     if (sl.nch > 1) cs.load(SRC(a, t_seg + C, chunk_nv(1), h, H, rec0 + rec_step), H);
     lds_barrier();
     for (int c = -1; c < sl.nch; ++c) {
+      // with the in-op L2 norm of bf16 q: the q rows of chunk c + 1, stored raw by the producers in
+      // the previous step, are normalised in place in this half step, where the consumers would wait
+      // at B2 for the producers' w and u products; their first reader is Aqk of chunk c + 1 after B2
+      if (q_cons && c + 1 < sl.nch) norm_q_tile<TQ, K, V>(smem + P::q_tile((c + 1) & 1));
       // ---------------- B1 .. B2: h, o_inter, v', o of chunk c
       f32x4 Y[4][CTN];
       if (c >= 0) {
@@ -1565,7 +1593,7 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     const SRC s0(a, t_seg, chunk_nv(0), h, H, rec0);
     ps.load_q(s0, H);
     ps.load_k(s0, H);
-    ps.store_q(smem, 0, qs, a.l2 != 0);
+    ps.store_q(smem, 0, qs, a.l2 != 0 && !q_cons);
     ps.store_k(smem, 0, ks_, a.l2 != 0);
     if (sl.nch > 1) {
       const SRC s1(a, t_seg + C, chunk_nv(1), h, H, rec0 + rec_step);
@@ -1579,12 +1607,16 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     uint32_t ktr_w[OutProducts<K, V>::NWU];
 #pragma unroll
     for (int i = 0; i < OutProducts<K, V>::NWU; ++i) ktr_w[i] = tr_lane_addr<K>(lds0, pw + 4 * i);
+    // with the in-op L2 norm of bf16 k, the k rows loaded in one step are normalised in registers in
+    // that step's second half (where the producers wait for the consumers' state update), so the
+    // first half, which bounds the step, only stores them
+    const bool k_pre = a.l2 != 0 && !P::FP8;
     for (int c = -1; c < sl.nch; ++c) {
       // ---------------- B1 .. B2
       // producers: w and u of chunk c + 1; k of chunk c + 2 goes to a buffer
       // free in this half, then the loads of k of chunk c + 3
       if (c + 2 < sl.nch) {
-        ps.store_k(smem, (c + 2) % 3, ks_, a.l2 != 0);
+        ps.store_k(smem, (c + 2) % 3, ks_, a.l2 != 0 && !(k_pre && c >= 0));
         if (c + 3 < sl.nch) ps.load_k(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
       }
       if (c + 1 < sl.nch) {
@@ -1670,8 +1702,11 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
         }
       }
       if (c + 2 < sl.nch) {
-        ps.store_q(smem, (c + 2) & 1, qs, a.l2 != 0);
-        if (c + 3 < sl.nch) ps.load_q(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
+        ps.store_q(smem, (c + 2) & 1, qs, a.l2 != 0 && !q_cons);
+        if (c + 3 < sl.nch) {
+          ps.load_q(SRC(a, t_seg + (int64_t)(c + 3) * C, chunk_nv(c + 3), h, H, rec0), H);
+          if (k_pre) ps.norm_k();                        // k of chunk c + 3, stored in the next step
+        }
       }
       lds_barrier();                                     // B1
     }
