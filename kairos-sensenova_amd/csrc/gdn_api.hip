@@ -276,12 +276,23 @@ bool wide_dhu_on(int cdt, int64_t K, int64_t V) {
   return !(e && e[0] == '0' && e[1] == 0);
 }
 
+// The backward's recompute of h and v_new at K = 256 in bf16 by the fused forward kernel in its
+// recompute mode (KAIROS_GDN_BWD_RC_WIDE=0 selects prepare's u pass and fwd_h): prepare then writes
+// k^T per chunk (into the q^T buffer, which the dv_local stage fills later) and fp32 beta (into dg1,
+// which the dq/dk stage fills later), and no u.
+bool bwd_rc_wide(int cdt, int qk_dtype, int64_t K, int64_t V, bool segmented) {
+  if (segmented || !kgdn::wide_fused_supported(cdt, qk_dtype, (int)K, (int)V)) return false;
+  const char* e = std::getenv("KAIROS_GDN_BWD_RC_WIDE");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
 // Workspace of the backward: the recomputed forward (gc, w, u, Ai, h, v_new) and the
 // backward's own intermediates (dv_local, dh, dv2, -dw, dk of the dq/dk stage, dg before the
 // cumsum), plus the normalised q, k and their pre-norm gradients with the in-op L2 norm.  The
 // segment scan adds the forward's chunk records and segment maps and states, and the segments'
 // token and chunk offsets.
-size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, int use_l2) {
+size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, int qk_dtype,
+              int use_l2) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
   const size_t tok = (size_t)(B * T * H);
@@ -297,13 +308,17 @@ size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_s
   }
   total += 2 * align_up(tok * sizeof(float));            // gc, dg1
   total += 3 * align_up(tok * K * es);                   // w, -dw, dk1
-  total += align_up(nc * H * V * kgdn::C * es);          // uT
+  const bool seg = bwd_segmented(cdt, K, V, P);
+  const bool rc_wide = bwd_rc_wide(cdt, qk_dtype, K, V, seg);
+  if (!rc_wide) total += align_up(nc * H * V * kgdn::C * es);   // uT
   total += align_up(tok * kgdn::C * es);                 // Ai
   total += 2 * align_up(nc * H * K * V * es);            // h, dh
   total += 3 * align_up(tok * V * es);                   // v_new, dv_local, dv2
   if (use_l2) total += 4 * align_up(tok * K * es);       // qn, kn, dqn, dkn
-  if (!bwd_segmented(cdt, K, V, P) && kgdn::wide_dhu_supported(cdt, (int)K, (int)V))
-    total += 2 * align_up(nc * H * K * kgdn::C * es);    // q^T, w^T per chunk
+  if (!seg && kgdn::wide_dhu_supported(cdt, (int)K, (int)V))
+    total += 2 * align_up(nc * H * K * kgdn::C * es);    // q^T (k^T first with rc_wide), w^T per chunk
+  else if (rc_wide)
+    total += align_up(nc * H * K * kgdn::C * es);        // k^T per chunk
   return total;
 }
 
@@ -671,7 +686,7 @@ size_t kairos_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0) return 0;
   const int cdt = compute_dtype(qk_dtype, v_dtype);
   if (cdt < 0) return 0;
-  return bwd_ws(B, T, H, K, V, n_seqs, cdt, use_qk_l2norm);
+  return bwd_ws(B, T, H, K, V, n_seqs, cdt, qk_dtype, use_qk_l2norm);
 }
 
 int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
@@ -702,7 +717,7 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(do_) || !aligned16(dq) || !aligned16(dk) ||
       !aligned16(dv))
     return fail(KAIROS_GDN_EINVAL, "%s: q, k, v, do, dq, dk and dv must be 16-byte aligned", what);
-  const size_t need = bwd_ws(B, T, H, K, V, n_seqs, cdt, use_qk_l2norm);
+  const size_t need = bwd_ws(B, T, H, K, V, n_seqs, cdt, qk_dtype, use_qk_l2norm);
   if (workspace_bytes < need)
     return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace of %zu bytes is smaller than the %zu required", what,
                 workspace_bytes, need);
@@ -731,19 +746,19 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   void* w = cv.take(tok * K * es);
   void* dwb = cv.take(tok * K * es);
   void* dk1 = cv.take(tok * K * es);
-  void* uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
+  const bool rc_wide = !segb && bwd_rc_wide(cdt, qk_dtype, K, V, false);
+  void* uT = rc_wide ? nullptr : cv.take((size_t)G.nc * H * V * kgdn::C * es);
   void* Ai = cv.take(tok * kgdn::C * es);
   void* hs = cv.take((size_t)G.nc * H * K * V * es);
   void* dhs = cv.take((size_t)G.nc * H * K * V * es);
   void* vn = cv.take(tok * V * es);
   void* dvl = cv.take(tok * V * es);
   void* dv2 = cv.take(tok * V * es);
-  void* qT = nullptr;
+  void* qT = nullptr;                           // with rc_wide it holds k^T until the dv_local stage
   void* wT = nullptr;
-  if (!segb && wide_dhu_on(cdt, K, V)) {
-    qT = cv.take((size_t)G.nc * H * K * kgdn::C * es);
-    wT = cv.take((size_t)G.nc * H * K * kgdn::C * es);
-  }
+  const bool dhu_wide = !segb && wide_dhu_on(cdt, K, V);
+  if (dhu_wide || rc_wide) qT = cv.take((size_t)G.nc * H * K * kgdn::C * es);
+  if (dhu_wide) wT = cv.take((size_t)G.nc * H * K * kgdn::C * es);
   const void* qx = q;
   const void* kx = k;
   void* dq_k = dq;
@@ -767,6 +782,10 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
     pa.g_dtype = g_dtype; pa.beta_dtype = beta_dtype;
     pa.cu = cu_seqlens; pa.chunk_off = chunk_off; pa.N = N; pa.T = T; pa.H = (int)H;
     pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = Ai; pa.wT_out = wT;
+    if (rc_wide) {
+      pa.kT_out = qT;
+      pa.beta_out = dg1;
+    }
     if (int rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, (int)K, (int)V, G.nc, s), "prepare")) return rc;
   }
   kgdn::FwdHArgs ha{};
@@ -780,10 +799,18 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   ba.dvl = dvl; ba.dh = dhs; ba.dv2 = dv2; ba.dw = dwb; ba.dk1 = dk1; ba.dg1 = dg1;
   ba.dq = dq_k; ba.dk = dk_k; ba.dv = dv; ba.dg = dg; ba.db = dbeta; ba.dh0 = dh0;
   ba.cu = cu_seqlens; ba.chunk_off = chunk_off; ba.N = N; ba.T = T; ba.H = (int)H; ba.scale = scale;
-  ba.qT = qT; ba.wT = wT;
+  ba.qT = dhu_wide ? qT : nullptr;
+  ba.wT = wT;
   const int64_t nc_b = any_tokens ? G.nc : 0;
   if (!segb) {
-    if (G.nc > 0 && any_tokens) {
+    if (G.nc > 0 && any_tokens && rc_wide) {
+      kgdn::WideFusedArgs fa{};
+      fa.kT = qT; fa.v = v; fa.w = w; fa.Ai = Ai; fa.beta = dg1; fa.gc = gc;
+      fa.h0 = initial_state; fa.h0_dtype = h0_dtype;
+      fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = T; fa.H = (int)H; fa.scale = scale;
+      fa.h_out = hs; fa.vn_out = vn;
+      if (int rc = from_launch(kgdn::launch_wide_fused(fa, (int)V, s), "fused recompute of h and v_new")) return rc;
+    } else if (G.nc > 0 && any_tokens) {
       if (int rc = from_launch(kgdn::launch_fwd_h(ha, cdt, qk_dtype, (int)K, (int)V, s), "fwd_h (recompute)"))
         return rc;
     }

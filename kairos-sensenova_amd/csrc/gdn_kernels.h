@@ -106,6 +106,9 @@ struct WideFusedArgs {
   float* ht;              // out [N, H, 256, V] fp32 or nullptr
   int64_t it_begin, it_end;  // the chunks of each sequence to walk (it_end <= 0: to the end); h0 is the
                              // state before chunk it_begin, ht the one after the last chunk walked
+  void* h_out;            // recompute mode (the backward's): out [NC, H, 256, V] bf16 state before each
+                          // chunk, row-major; q, aqk and o are not used
+  void* vn_out;           // recompute mode: out [B*T, H, V] bf16 v_new
 };
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V);
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s);

@@ -114,6 +114,8 @@ __device__ __forceinline__ int swz_wq(int r) { return (r & 3) | (((r >> 3) & 3) 
 __device__ __forceinline__ int swz_a(int r) { return (((r >> 3) & 3) << 1) | ((r >> 1) & 1); }
 __device__ __forceinline__ int swz_v(int r) { return (((r >> 3) & 1) << 1) | (((r >> 1) & 1) << 2); }
 __device__ __forceinline__ int swz_o(int t) { return ((t >> 1) & 1) | (((t >> 3) & 3) << 1); }
+// tiles written by a compute wave's 2-byte stores from accumulator tiles (rows 8 apart per lane group)
+__device__ __forceinline__ int swz_s(int r) { return ((r >> 3) & 3) << 1; }
 
 typedef __attribute__((address_space(3))) unsigned char lds_b;
 typedef short s16x4v __attribute__((ext_vector_type(4)));
@@ -133,6 +135,11 @@ __device__ __forceinline__ u32x2 ldtr(uint32_t a, uint32_t off) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                                        reinterpret_cast<lds_s16x4v*>(reinterpret_cast<lds_b*>(a) + off)));
 }
+__device__ __forceinline__ void lds_st16(uint32_t a, uint32_t off, bf16 x) {
+  *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(reinterpret_cast<lds_b*>(a) + off) =
+      __builtin_bit_cast(uint16_t, x);
+}
+
 __device__ __forceinline__ Frag<bf16> frag2(u32x2 a, u32x2 b) {
   Frag<bf16> f;
   f.v = __builtin_bit_cast(bf16x8, u32x4{a[0], a[1], b[0], b[1]});
@@ -201,6 +208,10 @@ __device__ __forceinline__ void ld_tile64(const unsigned char* base, uint32_t ro
   dma16_(base, rr * row_bytes + 16u * (pos ^ (kSwzA ? swz_a(r) : swz_v(r))), dst + 1024u * i);
 }
 
+// kRc: the backward's recompute of the forward (chunk_delta_h.py:52-224 alone): the state before each
+// chunk (bf16, through the q half of the w / q tile, which q does not use here) and v_new (through the o
+// tile) leave as whole rows stored by the loader waves; q, Aqk and the output products are skipped.
+template <bool kRc>
 __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedArgs a, int V, int total_units) {
   // LDS: w and q of the chunk (adjacent: q reads are w reads + 32 KB), k^T of the chunk, and two
   // buffer sets of the chunk's small tiles: Aqk, Ai, the v tile of the workgroup's 64 columns, gc, beta
@@ -264,7 +275,8 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       const unsigned char* aib = reinterpret_cast<const unsigned char*>(a.Ai) + (size_t)((t0 * H + h) * C) * 2;
       const unsigned char* vb = reinterpret_cast<const unsigned char*>(a.v) + (size_t)((t0 * H + h) * V + vt0) * 2;
 #pragma unroll
-      for (int j = 0; j < 8 / FL; ++j) ld_tile64<true>(ab, 128u, C, FL * j + lw, a_lds + B * ABUF);
+      for (int j = 0; j < 8 / FL; ++j)
+        if constexpr (!kRc) ld_tile64<true>(ab, 128u, C, FL * j + lw, a_lds + B * ABUF);
 #pragma unroll
       for (int j = 0; j < 8 / FL; ++j) ld_tile64<true>(aib, (uint32_t)H * C * 2, nv, FL * j + lw, ai_lds + B * ABUF);
 #pragma unroll
@@ -279,7 +291,8 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
 #pragma unroll
       for (int j = 0; j < 32 / FL; ++j) ld_tile256(wb, RB, nv, FL * j + lw, w_lds);
 #pragma unroll
-      for (int j = 0; j < 32 / FL; ++j) ld_tile256(qb, RB, nv, FL * j + lw, w_lds + QOFF);
+      for (int j = 0; j < 32 / FL; ++j)
+        if constexpr (!kRc) ld_tile256(qb, RB, nv, FL * j + lw, w_lds + QOFF);
     };
     // L2 prefetch of chunk (c, t0)'s w and q rows and its k^T and Aqk tiles: one 4-byte direct load
     // per 128-byte line into a scratch LDS word (never read), so that the tile loads a step later
@@ -289,7 +302,8 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     // would cost as much of it as the tile loads themselves.
     const uint32_t pf_lds = lds_u32(s_pf);
     const int pf_q = (vt0 / FVT) & 3;
-    auto prefetch = [&](int64_t c, int64_t t0, int nv) {     // one load per loader wave
+    auto prefetch = [&](int64_t c, int64_t t0, int nv) {     // one load per loader wave (kRc: loaders 0, 2)
+      if (kRc && (lw & 1)) return;
       if (lw < 2) {
         const int r = 16 * pf_q + (l >> 2);
         const uint32_t off = (uint32_t)(r < nv ? r : 0) * RB + 128u * (l & 3);
@@ -307,7 +321,16 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         const int t = 8 * (FL * j + lw) + (l >> 3), c8 = l & 7;
         const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (c8 ^ swz_o(t)));
         if (t < nv)
-          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2) = x;
+          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(kRc ? a.vn_out : a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2) = x;
+      }
+    };
+    // kRc: the state snapshot of chunk c (rows d of the q half of the w / q tile) to h_out [NC, H, 256, V]
+    auto store_h = [&](int64_t c) {
+#pragma unroll
+      for (int j = 0; j < 32 / FL; ++j) {
+        const int d = 8 * (FL * j + lw) + (l >> 3), c8 = l & 7;
+        const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(w_lds + QOFF) + 128 * d + 16 * (c8 ^ swz_s(d)));
+        *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.h_out) + (((c * H + h) * FK + d) * V + vt0 + 8 * c8) * 2) = x;
       }
     };
     if (ie - ib > 1) prefetch(c_first + ib + 1, bos + (ib + 1) * C, chunk_nv(ib + 1));
@@ -326,16 +349,29 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(kb, 128u, FK, FL * j + lw, k_lds);
       small(c_first + in, bos + in * C, chunk_nv(in), B ^ 1u);
       // this wave's k^T loads landed; the later ones (6 + gc / beta + the prefetch) stay in flight
-      if (it + 2 < ie) {
-        prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
-        if (kSmall == 7) wait_loads_but<8>();
-        else wait_loads_but<7>();
+      if constexpr (kRc) {                                // small: 4, and gc / beta from loaders 0 / 1
+        if (it + 2 < ie) {
+          prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
+          if (lw == 0) wait_loads_but<6>();
+          else if (lw == 3) wait_loads_but<4>();
+          else wait_loads_but<5>();
+        } else {
+          if (lw < 2) wait_loads_but<5>();
+          else wait_loads_but<4>();
+        }
       } else {
-        if (kSmall == 7) wait_loads_but<7>();
-        else wait_loads_but<6>();
+        if (it + 2 < ie) {
+          prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
+          if (kSmall == 7) wait_loads_but<8>();
+          else wait_loads_but<7>();
+        } else {
+          if (kSmall == 7) wait_loads_but<7>();
+          else wait_loads_but<6>();
+        }
       }
       f_barrier();                                        // B2
       if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
+      if constexpr (kRc) store_h(c_first + it);           // written by the compute waves before B2
     }
     f_barrier();                                          // the last o tile is in LDS
     if (ie > ib) store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));
@@ -365,6 +401,13 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   FAddr A;
   f_addr(A, w_lds, k_lds, a_lds, v_lds);
   const uint32_t AI_OFF = ai_lds - a_lds;                 // Ai tiles share the Aqk lane addresses
+  // kRc: 2-byte writes of row 8 lg (+ the accumulator row offsets), column 16 wid + lc: the snapshot into
+  // the q half of the w / q tile (swizzle swz_s) and v_new into the o tile (swizzle swz_o, whose row bit
+  // 1 is j / 2 of the accumulator element)
+  const int cs = 16 * wid + lc;
+  const uint32_t snap_w = w_lds + QOFF + 128 * (8 * lg) + 16 * ((cs >> 3) ^ swz_s(8 * lg)) + 2 * (cs & 7);
+  const uint32_t vn_w[2] = {o_lds + 128 * (8 * lg) + 16 * ((cs >> 3) ^ swz_o(8 * lg)) + 2 * (cs & 7),
+                            o_lds + 128 * (8 * lg) + 16 * ((cs >> 3) ^ swz_o(8 * lg + 2)) + 2 * (cs & 7)};
 
   // One chunk step between the loader's barriers: after B1 (w, q and the small tiles of chunk it in
   // LDS, buffer set B = it % 2), w h and h^T q^T; after B2 (k^T in LDS), u, v', o and the update.
@@ -417,7 +460,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
         w4[tm] = ld128(ra, o8 + rowa_off(tm, 512));
-        q4[tm] = ld128(ra, QOFF + o8 + rowa_off(tm, 512));
+        if constexpr (!kRc) q4[tm] = ld128(ra, QOFF + o8 + rowa_off(tm, 512));
       }
     };
     read_wq(0, wa[0], qa[0]);
@@ -428,8 +471,14 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       const Frag<bf16> hb = pack_acc(S[2 * ks], S[2 * ks + 1]);
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
-        mma(oi[tm], hb, qa[ks & 1][tm]);
+        if constexpr (!kRc) mma(oi[tm], hb, qa[ks & 1][tm]);
         mma(acc[tm], wa[ks & 1][tm], hb);
+      }
+      if constexpr (kRc) {                                // the snapshot: rows 32 ks + 8 lg + 4 x + j
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lds_st16(snap_w, 128u * (32 * ks + 4 * x + j), hb.v[4 * x + j]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -438,12 +487,14 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     // the output's LDS operands first (one latency for all): Aqk row pieces and exp(gc_t) per tile
     Frag<bf16> aq[6];
     float egt[4];
+    if constexpr (!kRc) {
 #pragma unroll
-    for (int tn = 0, f = 0; tn < 4; ++tn) {
-      egt[tn] = sg[32 * (tn >> 1) + 4 * (tn & 1) + ra0];
+      for (int tn = 0, f = 0; tn < 4; ++tn) {
+        egt[tn] = sg[32 * (tn >> 1) + 4 * (tn & 1) + ra0];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        if (ks <= tn / 2) aq[f++] = ld128(A.ar[ks], B * ABUF + rowa_off(tn, 128));
+        for (int ks = 0; ks < 2; ++ks)
+          if (ks <= tn / 2) aq[f++] = ld128(A.ar[ks], B * ABUF + rowa_off(tn, 128));
+      }
     }
     // v' = u - w h (rows t = 32 (tm / 2) + 8 lg + 4 (tm % 2) + j), its bf16 value and the gated form
     const float gl = sg[nv - 1];
@@ -462,6 +513,13 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       vf[ks] = pack_acc(Y[2 * ks], Y[2 * ks + 1]);
       vg[ks] = pack_acc(Yg[2 * ks], Yg[2 * ks + 1]);
     }
+    if constexpr (kRc) {                                  // v_new = bf16(v') into the o tile
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          lds_st16(vn_w[j >> 1], 128u * (32 * (tm >> 1) + 4 * (tm & 1) + j), (bf16)Y[tm][j]);
+    } else {
     // o^T = (o_inter^T exp(gc_t) + v'^T Aqk^T) scale; lane: columns 16 w + 4 lg .. + 3 of token
     // rowA(tn, lc), into the LDS o tile (the loader waves store it after the next B1)
     f32x4 r[4];
@@ -481,6 +539,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
           (uint32_t)__builtin_bit_cast(uint16_t, (bf16)x[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)x[3]) << 16)};
       *reinterpret_cast<lds_u32x2*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * ((2 * wid + (lg >> 1)) ^ swz_o(t)) +
                                     8 * (lg & 1)) = ov;
+    }
     }
     // S = exp(g_last) S + k^T (v' exp(g_last - gc)), pipelined like the products above
     const float eg = gexp(gl);
@@ -548,8 +607,6 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
 // waves store as whole 128-byte rows; chunk c of row r sits at c ^ 2 ((r / 8) % 4), so the four lane
 // groups of a compute wave's 2-byte writes (rows 8 apart) land on distinct banks.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int swz_s(int r) { return ((r >> 3) & 3) << 1; }
-
 namespace dhu_lds {
 constexpr uint32_t K_OFF = 0;                        // k [64][256]
 constexpr uint32_t QW_OFF = K_OFF + C * FK * 2;      // q^T [256][64], then w^T
@@ -562,11 +619,6 @@ constexpr uint32_t G_OFF = DV_OFF + C * C * 2;       // gc, two buffers
 constexpr uint32_t PF_OFF = G_OFF + 2 * C * 4;       // landing words of the L2 prefetch
 constexpr uint32_t TOTAL = PF_OFF + WAVE * 4;
 }  // namespace dhu_lds
-
-__device__ __forceinline__ void lds_st16(uint32_t a, uint32_t off, bf16 x) {
-  *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(reinterpret_cast<lds_b*>(a) + off) =
-      __builtin_bit_cast(uint16_t, x);
-}
 
 __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, int V, int total_units) {
   using namespace dhu_lds;
@@ -1227,7 +1279,12 @@ int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s) {
   if (V % FVT != 0 || a.N * a.H == 0) return -2;
   const int total = a.N * a.H * (V / FVT);
   const int grid = (total + 7) / 8 * 8;
-  hipLaunchKernelGGL(wide_fused_kernel, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+  if (a.h_out) {
+    if (!a.vn_out || a.ht) return -2;
+    hipLaunchKernelGGL(wide_fused_kernel<true>, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+  } else {
+    hipLaunchKernelGGL(wide_fused_kernel<false>, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

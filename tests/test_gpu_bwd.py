@@ -90,18 +90,22 @@ def test_bwd_model_shape_varlen():
     run_case(1, 1100, 2, 256, 512, seed=9, cu=[0, 500, 1100], l2=True)
 
 
-@pytest.mark.parametrize("form", ["64-column dh kernel, 8-wave dq kernel", "16-column dh kernel",
-                                  "4-wave dq kernel"])
+@pytest.mark.parametrize("form", ["fused recompute, 64-column dh kernel, 8-wave dq kernel", "16-column dh kernel",
+                                  "4-wave dq kernel", "stage recompute"])
 def test_bwd_model_head_dims_dh_forms(form, monkeypatch):
-    """dk=256: the dh recurrence with 64 value columns per workgroup (the default: q^T and w^T per
-    chunk, loader waves, the snapshot and dv2 stored from LDS) and with 16 columns, and the dq / dk /
-    dw / dg stage with eight waves owning K rows (the default) and with four owning tokens, all match
-    the oracle: a batch of 2 with a ragged last chunk at dv=512, and a varlen batch at dv=256 whose
-    sequences are empty, 1 token, a chunk exactly and several chunks with a ragged end."""
+    """dk=256: h and v_new recomputed by the fused forward kernel in its recompute mode (the default)
+    and by prepare's u pass + fwd_h; the dh recurrence with 64 value columns per workgroup (the
+    default: q^T and w^T per chunk, loader waves, the snapshot and dv2 stored from LDS) and with 16
+    columns; and the dq / dk / dw / dg stage with eight waves owning K rows (the default) and with four
+    owning tokens: all match the oracle on a batch of 2 with a ragged last chunk at dv=512, and a varlen
+    batch at dv=256 whose sequences are empty, 1 token, a chunk exactly and several chunks with a
+    ragged end."""
     if "16-column" in form:
         monkeypatch.setenv("KAIROS_GDN_BWD_DHU_WIDE", "0")
     if "4-wave" in form:
         monkeypatch.setenv("KAIROS_GDN_BWD_DQK_WIDE", "0")
+    if "stage recompute" in form:
+        monkeypatch.setenv("KAIROS_GDN_BWD_RC_WIDE", "0")
     note(f"backward {form}: B=2 T=200 H=2 K=256 V=512")
     run_case(2, 200, 2, 256, 512, seed=31)
     note(f"backward {form}: varlen [0, 0, 1, 65, 400] H=2 K=256 V=256")
