@@ -117,6 +117,38 @@ __device__ __forceinline__ void stage_rows(TC* tile, const TC* src, int64_t t0, 
   }
 }
 
+// The same staging by direct global -> LDS loads (bf16): every load of the tile is in flight at once
+// (one instruction moves 8 rows of a 64-column block, 1 KB); lanes of rows past nv are masked off the
+// loads and write zeros with plain stores instead.  The caller waits for its loads (stage_wait) and
+// barriers before reading.
+__device__ __forceinline__ void stage_dma16(const void* base, uint32_t off, uint32_t lds_dst) {
+  const uint64_t v = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off),
+               "s"(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo)),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds_dst)) : "memory");
+}
+__device__ __forceinline__ void stage_rows_dma(bf16* tile, const bf16* src, int64_t t0, int nv, int H, int h, int ncol) {
+  const int nw = blockDim.x / WAVE, wid = threadIdx.x / WAVE, l = lane_id();
+  const unsigned char* base = reinterpret_cast<const unsigned char*>(src + (t0 * H + h) * (int64_t)ncol);
+  const uint32_t row_bytes = (uint32_t)(H * ncol * 2);
+  const uint32_t tile_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) bf16*)tile;
+  for (int i = wid; i < ncol / 8; i += nw) {
+    const int cb = i >> 3, r = 8 * (i & 7) + (l >> 3);
+    const int c8 = (l & 7) ^ ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));   // swz_off<64>'s chunk order
+    const uint32_t dst = tile_lds + 8192u * cb + 1024u * (i & 7);
+    if (r < nv) {
+      stage_dma16(base, (uint32_t)r * row_bytes + (uint32_t)(64 * cb + 8 * c8) * 2u, dst);
+    } else {
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(dst + 16u * l)) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+__device__ __forceinline__ void stage_wait() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0): the direct loads have landed
+  asm volatile("" ::: "memory");
+}
+
 // sum over the 16 lanes of a row group (l % 16) or over the 4 lane groups (l / 16)
 __device__ __forceinline__ float sum16(float x) {
 #pragma unroll
@@ -164,10 +196,17 @@ __global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
   const int64_t t0 = loc.t0;
   const int nv = loc.nv;
   const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
-  stage_rows<TC>(s_q, reinterpret_cast<const TC*>(a.q), t0, nv, H, h, K);
-  stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
-  stage_rows<TC>(s_do, reinterpret_cast<const TC*>(a.do_), t0, nv, H, h, V);
+  if constexpr (sizeof(TC) == 2) {
+    stage_rows_dma(s_q, reinterpret_cast<const TC*>(a.q), t0, nv, H, h, K);
+    stage_rows_dma(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+    stage_rows_dma(s_do, reinterpret_cast<const TC*>(a.do_), t0, nv, H, h, V);
+  } else {
+    stage_rows<TC>(s_q, reinterpret_cast<const TC*>(a.q), t0, nv, H, h, K);
+    stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+    stage_rows<TC>(s_do, reinterpret_cast<const TC*>(a.do_), t0, nv, H, h, V);
+  }
   if (threadIdx.x < 64) s_g[threadIdx.x] = threadIdx.x < nv ? a.gc[(t0 + threadIdx.x) * H + h] : 0.f;
+  stage_wait();
   __syncthreads();
 
   // optional q^T per chunk, [NC, H, K, 64] (zero past the chunk's end), the K = 256 dh recurrence's
@@ -880,15 +919,23 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   const int64_t t0 = loc.t0;
   const int nv = loc.nv;
   const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
-  stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
-  stage_rows<TC>(s_dw, reinterpret_cast<const TC*>(a.dw), t0, nv, H, h, K);
-  stage_rows<TC>(s_du, reinterpret_cast<const TC*>(a.dv2), t0, nv, H, h, V);
-  stage_rows<TC>(s_Ai, reinterpret_cast<const TC*>(a.Ai), t0, nv, H, h, 64);
+  if constexpr (sizeof(TC) == 2) {
+    stage_rows_dma(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+    stage_rows_dma(s_dw, reinterpret_cast<const TC*>(a.dw), t0, nv, H, h, K);
+    stage_rows_dma(s_du, reinterpret_cast<const TC*>(a.dv2), t0, nv, H, h, V);
+    stage_rows_dma(s_Ai, reinterpret_cast<const TC*>(a.Ai), t0, nv, H, h, 64);
+  } else {
+    stage_rows<TC>(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
+    stage_rows<TC>(s_dw, reinterpret_cast<const TC*>(a.dw), t0, nv, H, h, K);
+    stage_rows<TC>(s_du, reinterpret_cast<const TC*>(a.dv2), t0, nv, H, h, V);
+    stage_rows<TC>(s_Ai, reinterpret_cast<const TC*>(a.Ai), t0, nv, H, h, 64);
+  }
   if (threadIdx.x < 64) {
     const int r = threadIdx.x;
     s_g[r] = r < nv ? a.gc[(t0 + r) * H + h] : 0.f;
     s_b[r] = r < nv ? ld_scalar(a.beta, (t0 + r) * H + h, a.beta_dtype) : 0.f;
   }
+  stage_wait();
   __syncthreads();
 
   // ---- dA = dw bf16(k beta e^g)^T + du bf16(v beta)^T, strictly lower (rows of this wave)
@@ -901,9 +948,16 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
 #pragma unroll
       for (int ks = 0; ks < K / 32; ++ks)
         mma(acc, t_nat<TC>(s_dw, K, 16 * wid, 32 * ks), fscale<TC>(t_nat<TC>(s_k, K, 16 * tj, 32 * ks), fk));
+      // this tile's v rows: every fragment's load in flight before the products
       const TC* vrow = v + ((t0 + j) * H + h) * (int64_t)V;
-      for (int vs = 0; vs < V / 32; ++vs)
-        mma(acc, t_nat<TC>(s_du, V, 16 * wid, 32 * vs), fscale<TC>(g_nat<TC>(vrow, 32 * vs, j < nv), s_b[j]));
+      constexpr int NVF = sizeof(TC) == 2 ? 16 : 4;     // V / 32 at most (bf16 V <= 512, fp32 V <= 128)
+      Frag<TC> vf[NVF];
+#pragma unroll
+      for (int vs = 0; vs < NVF; ++vs)
+        if (vs < V / 32) vf[vs] = g_nat<TC>(vrow, 32 * vs, j < nv);
+#pragma unroll
+      for (int vs = 0; vs < NVF; ++vs)
+        if (vs < V / 32) mma(acc, t_nat<TC>(s_du, V, 16 * wid, 32 * vs), fscale<TC>(vf[vs], s_b[j]));
     }
     const int j = 16 * tj + lc;
 #pragma unroll
@@ -971,6 +1025,11 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   float dbt = 0.f, dgt = 0.f;
   TC* dk_out = reinterpret_cast<TC*>(a.dk);
   const TC* dk1 = reinterpret_cast<const TC*>(a.dk1);
+  f32x4 d1s[K / 16];                                  // dk1 of this lane's token, all loads in flight at once
+#pragma unroll
+  for (int kt = 0; kt < K / 16; ++kt)
+    d1s[kt] = t < nv ? g_row4<TC>(dk1 + ((t0 + t) * H + h) * (int64_t)K + 16 * kt + 4 * lg) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
   for (int kt = 0; kt < K / 16; ++kt) {
     f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1, a3 = a1;
 #pragma unroll
@@ -985,8 +1044,7 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     }
     const int k0 = 16 * kt + 4 * lg;
     const f32x4 kv = t_row4<TC>(s_k, K, t, k0);
-    f32x4 d1 = {0.f, 0.f, 0.f, 0.f};
-    if (t < nv) d1 = g_row4<TC>(dk1 + ((t0 + t) * H + h) * (int64_t)K + k0);
+    const f32x4 d1 = d1s[kt];
     f32x4 dk;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
@@ -999,20 +1057,28 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     if (t < nv) st4v<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0, dk);
   }
   TC* dv_out = reinterpret_cast<TC*>(a.dv);
-  for (int vt = 0; vt < V / 16; ++vt) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // batches of 4 column tiles: the batch's v loads in flight before its products
+  for (int vt0 = 0; vt0 < V / 16; vt0 += 4) {
+    f32x4 vv[4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_du, V, 32 * s, 16 * vt), bAi[s]);   // dvb^T[v][t]
-    const int v0 = 16 * vt + 4 * lg;
-    if (t < nv) {
-      const f32x4 vv = g_row4<TC>(v + ((t0 + t) * H + h) * (int64_t)V + v0);
-      f32x4 dv;
+    for (int e = 0; e < 4; ++e)
+      vv[e] = t < nv ? g_row4<TC>(v + ((t0 + t) * H + h) * (int64_t)V + 16 * (vt0 + e) + 4 * lg) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        dv[jj] = acc[jj] * bt;
-        dbt += acc[jj] * vv[jj];
+    for (int e = 0; e < 4; ++e) {
+      const int vt = vt0 + e;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_du, V, 32 * s, 16 * vt), bAi[s]);   // dvb^T[v][t]
+      const int v0 = 16 * vt + 4 * lg;
+      if (t < nv) {
+        f32x4 dv;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          dv[jj] = acc[jj] * bt;
+          dbt += acc[jj] * vv[e][jj];
+        }
+        st4v<TC>(dv_out + ((t0 + t) * H + h) * (int64_t)V + v0, dv);
       }
-      st4v<TC>(dv_out + ((t0 + t) * H + h) * (int64_t)V + v0, dv);
     }
   }
   dbt = sum_lg(dbt);
