@@ -659,6 +659,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
     //      snapshot of chunk it out (8 stores); each waits for its loads before the next B1.
     const int lw = wid - FW;
     const uint32_t RB = (uint32_t)H * FK * 2, VB = (uint32_t)H * V * 2;
+    // the first half's tiles of chunk it: k and gc (needed at B1), then q^T and do (needed at B1h)
     auto load_a = [&](int64_t it, uint32_t gb) {
       const int64_t c = c_first + it, t0 = bos + it * C;
       const int nv = chunk_nv(it);
@@ -667,11 +668,11 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
       const unsigned char* db = reinterpret_cast<const unsigned char*>(a.do_) + (size_t)((t0 * H + h) * V + vt0) * 2;
 #pragma unroll
       for (int j = 0; j < 32 / FL; ++j) ld_tile256(kb, RB, nv, FL * j + lw, base + K_OFF);
+      if (lw == 0) dma4_(a.gc + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, base + G_OFF + gb * C * 4);
 #pragma unroll
       for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(qb, 128u, FK, FL * j + lw, base + QW_OFF);
 #pragma unroll
       for (int j = 0; j < 8 / FL; ++j) ld_tile64<false>(db, VB, nv, FL * j + lw, base + DO_OFF);
-      if (lw == 0) dma4_(a.gc + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, base + G_OFF + gb * C * 4);
     };
     auto load_b = [&](int64_t it) {
       const int64_t c = c_first + it, t0 = bos + it * C;
@@ -734,29 +735,41 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
       if (top >= 1) prefetch(top - 1);
     }
     wait_all_loads();
+    // vmcnt counts in issue order; the waits below name how many of this wave's operations issued after
+    // the ones waited for may still be in flight: the q^T / do loads (10), the prefetch (1, loader 3: 2),
+    // the w^T / dv_local loads (10), the dv2 stores (2), the snapshot stores (8).  The snapshot leaves
+    // after B1h, a half step before the next chunk's k loads: issued beside them (after B2) its stores
+    // held those loads back by about the length of the second half (measured).
+    static_assert(32 / FL == 8 && 8 / FL == 2, "the wait counts below assume four loader waves");
     for (int64_t it = top; it >= 0; --it) {
       const uint32_t gb = (uint32_t)((top - it) & 1);
       f_barrier();                                        // B1
       load_b(it);
       if (it < top) {
         store_dv(it + 1);
-        wait_loads_but<8 / FL>();
+        if (it >= 1) {                                    // the previous step prefetched chunk it - 1
+          if (lw == 3) wait_loads_but<2 + 10 + 2>();
+          else wait_loads_but<1 + 10 + 2>();
+        } else {
+          wait_loads_but<10 + 2>();
+        }
       } else {
-        wait_all_loads();
+        wait_loads_but<10>();                             // the prologue's loads are complete
       }
+      f_barrier();                                        // B1h: the snapshot of chunk it is in LDS
+      store_snap(it);
+      if (it < top) wait_loads_but<2 + 8>();
+      else wait_loads_but<8>();
       f_barrier();                                        // B2
       if (it > 0) {
         load_a(it - 1, gb ^ 1u);
-        if (it > 1) prefetch(it - 2);
-        store_snap(it);
         if (it > 1) {
-          if (lw == 3) wait_loads_but<32 / FL + 2>();
-          else wait_loads_but<32 / FL + 1>();
+          prefetch(it - 2);
+          if (lw == 3) wait_loads_but<10 + 2>();
+          else wait_loads_but<10 + 1>();
         } else {
-          wait_loads_but<32 / FL>();
+          wait_loads_but<10>();
         }
-      } else {
-        store_snap(it);
       }
     }
     f_barrier();                                          // dv2 of the first chunk is in LDS
@@ -800,25 +813,48 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
   for (int64_t it = top; it >= 0; --it) {
     const uint32_t gb = (uint32_t)((top - it) & 1);
     const int nv = chunk_nv(it);
-    f_barrier();                                          // B1: k, q^T, do, gc of chunk it
+    f_barrier();                                          // B1: k, gc of chunk it
     const float* G = s_g + gb * C;
+    Frag<bf16> ka[2][4];
+    auto read_k = [&](int g, Frag<bf16>(&k4)[4]) {
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) k4[tm] = ld128(kq[g & 3], 256u * (g >> 2) + rowa_off(tm, 512));
+    };
+    read_k(0, ka[0]);
+    const float gl = G[nv - 1];
+    f32x4 gv[4];                                          // gc of tokens 32 (i / 2) + 8 lg + 4 (i % 2) + j
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gv[i] = *reinterpret_cast<const f32x4*>(G + 32 * (i >> 1) + 8 * lg + 4 * (i & 1));
+    f32x4 kd[4];
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) kd[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // k bf16(dh), 32 rows of dh per group (their bf16 values: the B operand and the snapshot); operand
+    // reads one group ahead
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      if (g + 1 < 8) read_k(g + 1, ka[(g + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const Frag<bf16> hb = pack_acc(dh[2 * g], dh[2 * g + 1]);
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) mma(kd[tm], ka[g & 1][tm], hb);
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds_st16(sw, rowa_off(2 * g + x, 128) + 128u * j, hb.v[4 * x + j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f_barrier();                                          // B1h: q^T, do of chunk it
     Frag<bf16> xr[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) xr[ks] = frag2(ldtr(vt, 4096u * ks), ldtr(vt, 4096u * ks + 512u));
-    Frag<bf16> ka[2][4], qa[2][4];
-    auto read_a = [&](int g, Frag<bf16>(&k4)[4], Frag<bf16>(&q4)[4]) {
-#pragma unroll
-      for (int tm = 0; tm < 4; ++tm) k4[tm] = ld128(kq[g & 3], 256u * (g >> 2) + rowa_off(tm, 512));
+    Frag<bf16> qa[2][4];
+    auto read_q = [&](int g, Frag<bf16>(&q4)[4]) {
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) q4[2 * x + ks] = ld128(tq[ks], rowa_off(2 * g + x, 128));
     };
-    read_a(0, ka[0], qa[0]);
-    const float gl = G[nv - 1];
-    f32x4 gv[4];                                          // gc of tokens 32 (i / 2) + 8 lg + 4 (i % 2) + j
-#pragma unroll
-    for (int i = 0; i < 4; ++i) gv[i] = *reinterpret_cast<const f32x4*>(G + 32 * (i >> 1) + 8 * lg + 4 * (i & 1));
+    read_q(0, qa[0]);
     // x = do exp(gc) scale (tokens 32 ks + 8 lg + e, 0 past the chunk's end) as hi + lo
     Frag<bf16> xh[2], xl[2];
 #pragma unroll
@@ -832,18 +868,11 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
         xl[ks].v[e] = (bf16)(x - (float)hi);
       }
     const float eg = gexp(gl);
-    f32x4 kd[4];
-#pragma unroll
-    for (int tm = 0; tm < 4; ++tm) kd[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // k bf16(dh) and dh = exp(g_last) dh + q^T x, 32 rows of dh per group (their bf16 values, the B
-    // operand of k dh and the snapshot, packed before the update); operand reads one group ahead
+    // dh = exp(g_last) dh + q^T x, 32 rows per group, operand reads one group ahead
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
-      if (g + 1 < 8) read_a(g + 1, ka[(g + 1) & 1], qa[(g + 1) & 1]);
+      if (g + 1 < 8) read_q(g + 1, qa[(g + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
-      const Frag<bf16> hb = pack_acc(dh[2 * g], dh[2 * g + 1]);
-#pragma unroll
-      for (int tm = 0; tm < 4; ++tm) mma(kd[tm], ka[g & 1][tm], hb);
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         dh[2 * g + x] *= eg;
@@ -853,11 +882,6 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
           mma(dh[2 * g + x], qa[g & 1][2 * x + ks], xl[ks]);
         }
       }
-      // the snapshot rows of this group
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lds_st16(sw, rowa_off(2 * g + x, 128) + 128u * j, hb.v[4 * x + j]);
       __builtin_amdgcn_sched_barrier(0);
     }
     f_barrier();                                          // B2: w^T, dv_local of chunk it
