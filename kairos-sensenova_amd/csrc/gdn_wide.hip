@@ -370,8 +370,8 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         }
       }
       f_barrier();                                        // B2
-      if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
       if constexpr (kRc) store_h(c_first + it);           // written by the compute waves before B2
+      if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
     }
     f_barrier();                                          // the last o tile is in LDS
     if (ie > ib) store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));
