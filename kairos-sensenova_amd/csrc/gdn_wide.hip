@@ -737,29 +737,29 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_dhu_kernel(BwdArgs a, i
     wait_all_loads();
     // vmcnt counts in issue order; the waits below name how many of this wave's operations issued after
     // the ones waited for may still be in flight: the q^T / do loads (10), the prefetch (1, loader 3: 2),
-    // the w^T / dv_local loads (10), the dv2 stores (2), the snapshot stores (8).  The snapshot leaves
+    // the dv2 stores (2), the w^T / dv_local loads (10), the snapshot stores (8).  The snapshot leaves
     // after B1h, a half step before the next chunk's k loads: issued beside them (after B2) its stores
     // held those loads back by about the length of the second half (measured).
     static_assert(32 / FL == 8 && 8 / FL == 2, "the wait counts below assume four loader waves");
     for (int64_t it = top; it >= 0; --it) {
       const uint32_t gb = (uint32_t)((top - it) & 1);
       f_barrier();                                        // B1
-      load_b(it);
       if (it < top) {
-        store_dv(it + 1);
+        store_dv(it + 1);                                 // the stores first, then this half's loads
+        load_b(it);
         if (it >= 1) {                                    // the previous step prefetched chunk it - 1
-          if (lw == 3) wait_loads_but<2 + 10 + 2>();
-          else wait_loads_but<1 + 10 + 2>();
+          if (lw == 3) wait_loads_but<2 + 2 + 10>();
+          else wait_loads_but<1 + 2 + 10>();
         } else {
-          wait_loads_but<10 + 2>();
+          wait_loads_but<2 + 10>();
         }
       } else {
+        load_b(it);
         wait_loads_but<10>();                             // the prologue's loads are complete
       }
       f_barrier();                                        // B1h: the snapshot of chunk it is in LDS
       store_snap(it);
-      if (it < top) wait_loads_but<2 + 8>();
-      else wait_loads_but<8>();
+      wait_loads_but<8>();
       f_barrier();                                        // B2
       if (it > 0) {
         load_a(it - 1, gb ^ 1u);
