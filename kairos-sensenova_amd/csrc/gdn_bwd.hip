@@ -1200,11 +1200,11 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
   }
   if (nc_grid > 0 && (stages & BWD_GRADS)) {
     bool wide = false;
-    if constexpr (sizeof(TC) == 2 && K == 256) {      // eight waves per chunk (KAIROS_GDN_BWD_DQK_WIDE=0: four)
+    if constexpr (sizeof(TC) == 2 && K >= 128) {      // eight waves per chunk (KAIROS_GDN_BWD_DQK_WIDE=0: four)
       const char* e = std::getenv("KAIROS_GDN_BWD_DQK_WIDE");
       wide = !(e && e[0] == '0' && e[1] == 0);
       if (wide) {
-        if (int rc = launch_wide_dqkwg(a, V, nc_grid, s)) return rc;
+        if (int rc = launch_wide_dqkwg(a, K, V, nc_grid, s)) return rc;
       }
     }
     if (!wide) {

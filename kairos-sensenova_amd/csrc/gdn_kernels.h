@@ -206,8 +206,8 @@ int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_gri
 // the dh recurrence for K = 256 in bf16 with 64 value columns per workgroup (needs qT, wT, dh and dv2)
 bool wide_dhu_supported(int compute_dtype, int K, int V);
 int launch_wide_dhu(const BwdArgs& a, int V, hipStream_t s);
-// dq, dk, dw, dg for K = 256 in bf16, eight waves per (chunk, head) (V a multiple of 64)
-int launch_wide_dqkwg(const BwdArgs& a, int V, int64_t nc_grid, hipStream_t s);
+// dq, dk, dw, dg for K = 128 or 256 in bf16, eight waves per (chunk, head) (V a multiple of 64)
+int launch_wide_dqkwg(const BwdArgs& a, int K, int V, int64_t nc_grid, hipStream_t s);
 int launch_l2norm_bwd(const void* x, const void* dy, void* dx, int dtype, int64_t rows, int D, hipStream_t s);
 
 // Each returns 0 on success, -1 on a HIP launch error, -2 for an unsupported

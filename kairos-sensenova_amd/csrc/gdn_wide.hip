@@ -964,24 +964,29 @@ __device__ __forceinline__ int swz_n(int r) { return ((r & 1) << 1) | (((r >> 1)
 constexpr int DQ_NW = 8;
 constexpr int DQ_NT = DQ_NW * WAVE;
 
-namespace dq_lds {
-constexpr uint32_t Q_OFF = 0;                             // q [64][256]
-constexpr uint32_t K_OFF = C * FK * 2;                    // k [64][256]
-constexpr uint32_t BLK_OFF = 2 * C * FK * 2;              // two buffers of do, dv2, v_new [64][64]
-constexpr uint32_t TILE = C * C * 2;
-constexpr uint32_t BLK = 3 * TILE;
-constexpr uint32_t DS_OFF = BLK_OFF + 2 * BLK;            // bf16(ds) [64][64]
-constexpr uint32_t G_OFF = DS_OFF + TILE;                 // gc [64]
-constexpr uint32_t ROW_OFF = G_OFF + C * 4;               // ds2 row sums per lower tile [10][16]
-constexpr uint32_t COL_OFF = ROW_OFF + 10 * 16 * 4;       // ds2 column sums per lower tile [10][16]
-constexpr uint32_t DGT_OFF = COL_OFF + 10 * 16 * 4;       // sum_d (dq1 q - dk1 k) per wave [8][64]
-constexpr uint32_t SC_OFF = DGT_OFF + DQ_NW * C * 4;      // per wave: sum dk1 k [8], sum h dh [8]
-constexpr uint32_t TOTAL = SC_OFF + 2 * DQ_NW * 4;
-}  // namespace dq_lds
+template <int K>
+struct DqLds {
+  static constexpr uint32_t RB = K * 2;                   // q / k row bytes
+  static constexpr uint32_t Q_OFF = 0;                    // q [64][K]
+  static constexpr uint32_t K_OFF = C * RB;               // k [64][K]
+  static constexpr uint32_t BLK_OFF = 2 * C * RB;         // two buffers of do, dv2, v_new [64][64]
+  static constexpr uint32_t TILE = C * C * 2;
+  static constexpr uint32_t BLK = 3 * TILE;
+  static constexpr uint32_t DS_OFF = BLK_OFF + 2 * BLK;   // bf16(ds) [64][64]
+  static constexpr uint32_t G_OFF = DS_OFF + TILE;        // gc [64]
+  static constexpr uint32_t ROW_OFF = G_OFF + C * 4;      // ds2 row sums per lower tile [10][16]
+  static constexpr uint32_t COL_OFF = ROW_OFF + 10 * 16 * 4;   // ds2 column sums per lower tile [10][16]
+  static constexpr uint32_t DGT_OFF = COL_OFF + 10 * 16 * 4;   // sum_d (dq1 q - dk1 k) per wave [8][64]
+  static constexpr uint32_t SC_OFF = DGT_OFF + DQ_NW * C * 4;  // per wave: sum dk1 k [8], sum h dh [8]
+  static constexpr uint32_t TOTAL = SC_OFF + 2 * DQ_NW * 4;
+};
 
-// instruction i of a [64][256] tile with natural rows (rows 2 i, 2 i + 1; swizzle swz_n)
-__device__ __forceinline__ void ld_rows256(const unsigned char* base, uint32_t row_bytes, int nv, int i, uint32_t dst) {
-  const int l = lane_id(), r = 2 * i + (l >> 5), pos = l & 31;
+// instruction i of a [64][K] tile with natural rows (1 KB: rows (1024 / 2K) i ..; chunk c of row r at
+// c ^ swz_n(r), which for 256- and 512-byte rows gives the 16 lanes of a b128 pass distinct banks)
+template <int K>
+__device__ __forceinline__ void ld_rows(const unsigned char* base, uint32_t row_bytes, int nv, int i, uint32_t dst) {
+  constexpr int CPR = K / 8;                              // 16-byte chunks per row
+  const int l = lane_id(), r = (64 / CPR) * i + l / CPR, pos = l % CPR;
   const uint32_t rr = r < nv ? (uint32_t)r : 0u;
   dma16_(base, rr * row_bytes + 16u * (pos ^ swz_n(r)), dst + 1024u * i);
 }
@@ -1002,9 +1007,14 @@ __device__ __forceinline__ float wsum64(float x) {
   return x;
 }
 
+template <int K>
 __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
-  using namespace dq_lds;
-  __shared__ __align__(16) unsigned char smem[TOTAL];
+  using L = DqLds<K>;
+  constexpr uint32_t RB = L::RB, Q_OFF = L::Q_OFF, K_OFF = L::K_OFF, BLK_OFF = L::BLK_OFF, TILE = L::TILE,
+                     BLK = L::BLK, DS_OFF = L::DS_OFF, G_OFF = L::G_OFF, ROW_OFF = L::ROW_OFF,
+                     COL_OFF = L::COL_OFF, DGT_OFF = L::DGT_OFF, SC_OFF = L::SC_OFF;
+  constexpr int RW = K / DQ_NW, DT = RW / 16;              // K rows per wave, their 16-row tiles
+  __shared__ __align__(16) unsigned char smem[L::TOTAL];
   const uint32_t base = lds_u32(smem);
   const int h = blockIdx.y, H = a.H;
   const int64_t c = blockIdx.x;
@@ -1014,7 +1024,7 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
   const int nv = loc.nv;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), l = lane_id(), lg = l >> 4, lc = l & 15;
   const int nvb = V / C;                                   // 64-column blocks
-  const uint32_t RB = (uint32_t)H * FK * 2, VB = (uint32_t)H * V * 2;
+  const uint32_t RBg = (uint32_t)H * K * 2, VB = (uint32_t)H * V * 2;   // global row strides
   const unsigned char* dob = reinterpret_cast<const unsigned char*>(a.do_) + (size_t)((t0 * H + h) * V) * 2;
   const unsigned char* dvb = reinterpret_cast<const unsigned char*>(a.dv2) + (size_t)((t0 * H + h) * V) * 2;
   const unsigned char* vnb = reinterpret_cast<const unsigned char*>(a.vn) + (size_t)((t0 * H + h) * V) * 2;
@@ -1026,21 +1036,21 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
     ld_tile64<false>(vnb + (size_t)vb * C * 2, VB, nv, wid, dst + 2 * TILE);
   };
   {
-    const unsigned char* qb = reinterpret_cast<const unsigned char*>(a.q) + (size_t)((t0 * H + h) * FK) * 2;
-    const unsigned char* kb = reinterpret_cast<const unsigned char*>(a.k) + (size_t)((t0 * H + h) * FK) * 2;
+    const unsigned char* qb = reinterpret_cast<const unsigned char*>(a.q) + (size_t)((t0 * H + h) * K) * 2;
+    const unsigned char* kb = reinterpret_cast<const unsigned char*>(a.k) + (size_t)((t0 * H + h) * K) * 2;
 #pragma unroll
-    for (int j = 0; j < 32 / DQ_NW; ++j) ld_rows256(qb, RB, nv, DQ_NW * j + wid, base + Q_OFF);
+    for (int j = 0; j < K / 8 / DQ_NW; ++j) ld_rows<K>(qb, RBg, nv, DQ_NW * j + wid, base + Q_OFF);
 #pragma unroll
-    for (int j = 0; j < 32 / DQ_NW; ++j) ld_rows256(kb, RB, nv, DQ_NW * j + wid, base + K_OFF);
+    for (int j = 0; j < K / 8 / DQ_NW; ++j) ld_rows<K>(kb, RBg, nv, DQ_NW * j + wid, base + K_OFF);
     load_blk(0, 0u);
     if (wid == 0) dma4_(a.gc + t0 * H + h, (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u, base + G_OFF);
   }
   // this wave's rows of h and dh: A operands of rows d = 32 wid + 16 dt + lc, columns 64 vb + 32 ks + 8 lg ..
-  const bf16* hrow = reinterpret_cast<const bf16*>(a.h) + ((c * H + h) * FK + 32 * wid + lc) * (int64_t)V + 8 * lg;
-  const bf16* dhrow = reinterpret_cast<const bf16*>(a.dh) + ((c * H + h) * FK + 32 * wid + lc) * (int64_t)V + 8 * lg;
-  auto load_hd = [&](int vb, Frag<bf16>(&hf)[4], Frag<bf16>(&df)[4]) {
+  const bf16* hrow = reinterpret_cast<const bf16*>(a.h) + ((c * H + h) * K + RW * wid + lc) * (int64_t)V + 8 * lg;
+  const bf16* dhrow = reinterpret_cast<const bf16*>(a.dh) + ((c * H + h) * K + RW * wid + lc) * (int64_t)V + 8 * lg;
+  auto load_hd = [&](int vb, Frag<bf16>(&hf)[2 * DT], Frag<bf16>(&df)[2 * DT]) {
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int64_t off = 16 * dt * (int64_t)V + C * vb + 32 * ks;
@@ -1048,7 +1058,7 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
         df[2 * dt + ks].v = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(dhrow + off));
       }
   };
-  Frag<bf16> hf[2][4], df[2][4];
+  Frag<bf16> hf[2][2 * DT], df[2][2 * DT];
   load_hd(0, hf[0], df[0]);
   wait_all_loads();
   f_barrier();
@@ -1060,7 +1070,7 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
     tn = idx - tm * (tm + 1) / 2;
   };
   const int r0 = lc;                                       // natural rows 16 x + lc
-  const uint32_t qrd = base + Q_OFF + 512 * r0, krd = base + K_OFF + 512 * r0;
+  const uint32_t qrd = base + Q_OFF + RB * r0, krd = base + K_OFF + RB * r0;
   // q k^T of the ds tiles (B1 data: q, k)
   f32x4 aqk[2], dsa[2];
 #pragma unroll
@@ -1071,17 +1081,17 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
       int tm, tn;
       tile_mn(wid + 8 * s, tm, tn);
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
+      for (int ks = 0; ks < K / 32; ++ks) {
         const uint32_t co = 16u * ((4 * ks + lg) ^ swz_n(r0));
-        mma(aqk[s], ld128(qrd, 512u * 16 * tm + co), ld128(krd, 512u * 16 * tn + co));
+        mma(aqk[s], ld128(qrd, RB * 16 * tm + co), ld128(krd, RB * 16 * tn + co));
       }
     }
   }
 
   // the main products over the value columns
-  f32x4 aq[2][4], aw[2][4], ak[2][4];
+  f32x4 aq[DT][4], aw[DT][4], ak[DT][4];
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) aq[dt][tt] = aw[dt][tt] = ak[dt][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float hdh = 0.f;
@@ -1104,7 +1114,7 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
         fvn[ks] = ld128(bb, 2 * TILE + o);
       }
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           mma(aq[dt][tt], hf[P][2 * dt + ks], fdo[ks]);    // sum_v h[d][v] do[t][v]
@@ -1125,7 +1135,7 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
       }
     }
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int f = 0; f < 2 * DT; ++f)
 #pragma unroll
       for (int e = 0; e < 8; ++e) hdh += (float)hf[P][f].v[e] * (float)df[P][f].v[e];
     wait_all_loads();
@@ -1200,11 +1210,11 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
       bk[ks] = frag2(ldtr(ta, 0), ldtr(ta, 512u));       // rows ri + 4: the same swizzle (bits 1, 3)
     }
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      const int d0 = 32 * wid + 16 * dt, k0 = d0 + 4 * lg;
-      const u32x2 qw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + Q_OFF) + 512 * t +
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d0 = RW * wid + 16 * dt, k0 = d0 + 4 * lg;
+      const u32x2 qw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + Q_OFF) + RB * t +
                                                              16 * ((k0 >> 3) ^ swz_n(t)) + 2 * (k0 & 7));
-      const u32x2 kw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + K_OFF) + 512 * t +
+      const u32x2 kw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + K_OFF) + RB * t +
                                                              16 * ((k0 >> 3) ^ swz_n(t)) + 2 * (k0 & 7));
       const float qv[4] = {__uint_as_float(qw[0] << 16), __uint_as_float(qw[0] & 0xffff0000u),
                            __uint_as_float(qw[1] << 16), __uint_as_float(qw[1] & 0xffff0000u)};
@@ -1220,13 +1230,13 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int rt = 32 * ks + 8 * lg + (lc >> 2), ct = d0 + 4 * (lc & 3);
-        const uint32_t oa = 512 * rt + 16 * ((ct >> 3) ^ swz_n(rt)) + 2 * (ct & 7);
-        const uint32_t ob = 512 * (rt + 4) + 16 * ((ct >> 3) ^ swz_n(rt + 4)) + 2 * (ct & 7);
+        const uint32_t oa = RB * rt + 16 * ((ct >> 3) ^ swz_n(rt)) + 2 * (ct & 7);
+        const uint32_t ob = RB * (rt + 4) + 16 * ((ct >> 3) ^ swz_n(rt + 4)) + 2 * (ct & 7);
         mma(dq, frag2(ldtr(base + K_OFF + oa, 0), ldtr(base + K_OFF + ob, 0)), bq[ks]);
         mma(dk, frag2(ldtr(base + Q_OFF + oa, 0), ldtr(base + Q_OFF + ob, 0)), bk[ks]);
       }
       if (t < nv) {
-        const int64_t o = ((t0 + t) * H + h) * (int64_t)FK + k0;
+        const int64_t o = ((t0 + t) * H + h) * (int64_t)K + k0;
         st4<bf16>(dq_out + o, dq[0], dq[1], dq[2], dq[3]);
         st4<bf16>(dk_out + o, dk[0], dk[1], dk[2], dk[3]);
         st4<bf16>(dw_out + o, -aw[dt][tt][0], -aw[dt][tt][1], -aw[dt][tt][2], -aw[dt][tt][3]);
@@ -1292,10 +1302,11 @@ int launch_wide_dhu(const BwdArgs& a, int V, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_wide_dqkwg(const BwdArgs& a, int V, int64_t nc_grid, hipStream_t s) {
-  if (V % C != 0 || a.H <= 0) return -2;
+int launch_wide_dqkwg(const BwdArgs& a, int K, int V, int64_t nc_grid, hipStream_t s) {
+  if (V % C != 0 || a.H <= 0 || !(K == 128 || K == 256)) return -2;
   if (nc_grid <= 0) return 0;
-  hipLaunchKernelGGL(wide_dqkwg_kernel, dim3((unsigned)nc_grid, a.H), dim3(DQ_NT), 0, s, a, V);
+  if (K == 256) hipLaunchKernelGGL(wide_dqkwg_kernel<256>, dim3((unsigned)nc_grid, a.H), dim3(DQ_NT), 0, s, a, V);
+  else hipLaunchKernelGGL(wide_dqkwg_kernel<128>, dim3((unsigned)nc_grid, a.H), dim3(DQ_NT), 0, s, a, V);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

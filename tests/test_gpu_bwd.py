@@ -112,6 +112,19 @@ def test_bwd_model_head_dims_dh_forms(form, monkeypatch):
     run_case(1, 400, 2, 256, 256, seed=32, cu=[0, 0, 1, 65, 400])
 
 
+@pytest.mark.parametrize("form", ["8-wave dq kernel", "4-wave dq kernel"])
+def test_bwd_dq_forms_k128(form, monkeypatch):
+    """dk=128: the dq / dk / dw / dg stage with eight waves owning K rows (the default for bf16 K >= 128)
+    and with four owning tokens both match the oracle, on a ragged batch of 2 and a varlen batch with
+    an empty and a 1-token sequence."""
+    if "4-wave" in form:
+        monkeypatch.setenv("KAIROS_GDN_BWD_DQK_WIDE", "0")
+    note(f"backward {form}: B=2 T=333 H=2 K=V=128")
+    run_case(2, 333, 2, 128, 128, seed=41)
+    note(f"backward {form}: varlen [0, 0, 1, 200, 450] H=3 K=128 V=192")
+    run_case(1, 450, 3, 128, 192, seed=42, cu=[0, 0, 1, 200, 450])
+
+
 @pytest.mark.parametrize("path", ["serial", "segments of 3 chunks", "segments of 1 chunk",
                                   "16-column dh kernel", "serial, 16-column dh kernel"])
 def test_bwd_segment_scan_paths(path, monkeypatch):
