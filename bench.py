@@ -546,6 +546,59 @@ def bench_backward(args, dev):
 # ---------------------------------------------------------------------------
 # other rows of the path (each prints its own line)
 # ---------------------------------------------------------------------------
+def bench_gated_norm(args, dev):
+    """Config 2's forward with the layer's output norm (kairos_gdn_chunk_fwd_gated_norm): the norm fused
+    into the segment scan's output kernel against the same call with the separate norm kernel
+    (KAIROS_GDN_FUSED_NORM=0), A/B in one process."""
+    from kairos_gdn import _lib
+    cfg = CONFIGS[2]
+    B, T, H, K, V = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"]
+    q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, cfg["seed"], n_states=B, device=dev)
+    gen = torch.Generator(device="cpu").manual_seed(20263)
+    gate = torch.randn(B, T, H, V, generator=gen).to(dev, torch.bfloat16)
+    w = torch.rand(V, generator=gen).add_(0.5).to(dev)
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    y = torch.empty_like(v)
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+
+    def step():
+        _lib.call("kairos_gdn_chunk_fwd_gated_norm", P(q), P(k), P(v), P(g), P(beta), None, None, P(h0), P(gate),
+                  P(w), None, P(y), P(ht), None, 0, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16,
+                  _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, 1e-5, _lib.ACT_SWISH, P(ws), ws_bytes, sp)
+
+    prev = os.environ.get("KAIROS_GDN_FUSED_NORM")
+    out = {}
+    try:
+        for form, flag in (("separate", "0"), ("fused", "1")):
+            os.environ["KAIROS_GDN_FUSED_NORM"] = flag
+            timer = Timer(args)
+            out[form] = (timer, timer.run(step))
+    finally:
+        if prev is None:
+            os.environ.pop("KAIROS_GDN_FUSED_NORM", None)
+        else:
+            os.environ["KAIROS_GDN_FUSED_NORM"] = prev
+    timer, res = out["fused"]
+    sep = out["separate"][1]
+    med = res["step_ms"]["median"]
+    print(json.dumps({
+        "metric": "GDN chunk-fwd + gated RMSNorm (the layer's o_norm) tokens/s at T=32760,H=20,d=128",
+        "value": B * T / (med / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": res["wall_s"] * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "BASELINE config 2 forward with FusedRMSNormGated(128, eps=1e-5, swish) on o, "
+                               "bf16 gate, fp32 weight, through kairos_gdn_chunk_fwd_gated_norm",
+                   "B": B, "T": T, "H": H, "dk": K, "dv": V},
+        **timer.fields(res),
+        "separate_norm_kernel": {"median_ms": sep["step_ms"]["median"], "cold_median_ms":
+                                 (sep.get("cold_step_ms") or {}).get("median")},
+    }), flush=True)
+
+
 def bench_epilogue(args, dev):
     """Gated RMSNorm (fla FusedRMSNormGated, the layer's o_norm) over config 2's output rows:
     algorithmic bytes = rows * V * (2 + 2 + 2) (read o and the gate, write y, bf16)."""
@@ -724,6 +777,9 @@ def main():
                          "reference kernel of known traffic that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--epilogue", action="store_true",
                     help="measure only the gated RMSNorm epilogue (kairos_gdn_rms_norm_gated) on o-shaped rows")
+    ap.add_argument("--gated-norm", action="store_true",
+                    help="measure config 2's forward with the layer's gated RMSNorm (fused output epilogue "
+                         "against the separate norm kernel)")
     ap.add_argument("--model-shape", action="store_true",
                     help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T")
     ap.add_argument("--recurrent", action="store_true",
@@ -756,6 +812,8 @@ def main():
         bench_backward(args, dev)
     elif args.epilogue:
         bench_epilogue(args, dev)
+    elif args.gated_norm:
+        bench_gated_norm(args, dev)
     elif args.model_shape:
         bench_model_shape(args, dev)
     elif args.recurrent:

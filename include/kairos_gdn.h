@@ -82,6 +82,28 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
                          int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* The forward followed by the layer's output norm: y = o_norm(o, gate) with
+ * o = chunk_gated_delta_rule(q, k, v, g, beta, ...), replacing the pair of
+ * calls at fla layers/gated_deltanet.py:275-311 (chunk_gated_delta_rule, then
+ * FusedRMSNormGated, modules/fused_norm_gate.py:42-127, RMS path, no
+ * residual; the norm is kairos_gdn_rms_norm_gated over rows of V).  The
+ * forward's arguments are kairos_gdn_chunk_fwd's, with y (v's dtype) in place
+ * of o; gate: [B*T, H, V] in gate_dtype (fp32 or bf16, 16-byte aligned);
+ * norm_weight / norm_bias: [V] in norm_w_dtype or NULL; eps and activation as
+ * kairos_gdn_rms_norm_gated.  V at most 512.  The workspace is
+ * kairos_gdn_chunk_fwd_workspace_size()'s.  The norm is applied to o rounded
+ * to its storage dtype, as the two reference calls do; where the segment scan
+ * runs with a bf16 gate it is computed in the output kernel (o never reaches
+ * HBM), otherwise by the norm kernel on y in place. */
+int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                    const float* q_scale, const float* k_scale, const void* initial_state,
+                                    const void* gate, const void* norm_weight, const void* norm_bias, void* y,
+                                    float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                    int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype,
+                                    int g_dtype, int beta_dtype, int h0_dtype, int gate_dtype, int norm_w_dtype,
+                                    float scale, int use_qk_l2norm, float eps, int activation, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* kairos_gdn_chunk_fwd without a workspace argument: the call allocates
  * nothing (no hipMalloc / hipFree, no allocating library routine) and takes
  * its scratch memory from a static device array inside the library, of

@@ -557,14 +557,43 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   return total;
 }
 
-// Body of kairos_gdn_chunk_fwd and kairos_gdn_chunk_fwd_noalloc: validation, workspace carving and the
-// launches.  Allocates nothing; `profile` lets the call take part in kernel timing (which creates events).
+// The layer's gated RMSNorm applied to the forward's output (kairos_gdn_chunk_fwd_gated_norm)
+struct NormEpilogue {
+  const void* gate;
+  const void* w;
+  const void* b;
+  int gate_dtype;
+  int w_dtype;
+  float eps;
+  int sigmoid_only;
+};
+
+// The segment scan's output kernel takes the epilogue itself for a bf16 gate (KAIROS_GDN_FUSED_NORM=0
+// selects the separate norm kernel instead)
+static bool fused_norm_on(const NormEpilogue* epi) {
+  if (epi == nullptr || epi->gate_dtype != KAIROS_GDN_BF16) return false;
+  const char* e = std::getenv("KAIROS_GDN_FUSED_NORM");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
+// y = gated RMSNorm of y in place (each element is read and written by the same lane)
+static int norm_in_place(void* y, int y_dtype, const NormEpilogue& e, int64_t rows, int64_t D, hipStream_t s) {
+  if (rows == 0) return 0;
+  kgdn::NormArgs na{y, e.gate, e.w, e.b, y, nullptr, y_dtype, e.gate_dtype, e.w_dtype, rows, (int)D, e.eps,
+                    e.sigmoid_only};
+  return from_launch(kgdn::launch_rmsnorm_gated(na, s), "gated RMSNorm epilogue");
+}
+
+// Body of kairos_gdn_chunk_fwd, kairos_gdn_chunk_fwd_noalloc and kairos_gdn_chunk_fwd_gated_norm:
+// validation, workspace carving and the launches.  Allocates nothing; `profile` lets the call take part
+// in kernel timing (which creates events); `epi` (or nullptr) is the gated norm applied to o.
 static int chunk_fwd_impl(const char* what, bool profile, const void* q, const void* k, const void* v,
                           const void* g, const void* beta, const float* q_scale, const float* k_scale,
                           const void* initial_state, void* o, float* final_state, const int64_t* cu_seqlens,
                           int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
                           int v_dtype, int g_dtype, int beta_dtype, int h0_dtype, float scale, int use_qk_l2norm,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+                          void* workspace, size_t workspace_bytes, void* stream,
+                          const NormEpilogue* epi = nullptr) {
   Geometry G;
   if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
   const int cdt = compute_dtype(qk_dtype, v_dtype);
@@ -606,6 +635,8 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
     if (int rc = run_staged(G, q, k, v, g, beta, q_scale, k_scale, initial_state, h0_dtype, o, final_state,
                             cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s, profile))
       return rc;
+    if (epi)
+      if (int rc = norm_in_place(o, v_dtype, *epi, (int64_t)tok, V, s)) return rc;
     return ok();
   }
   const SegPlan P = plan_segments(B, T, H, n_seqs);
@@ -643,7 +674,14 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
   a.run_trans = P.trans && P.ns > 0;
   a.run_combine = P.combine;
   a.events = profile ? profile_events() : nullptr;
+  const bool fuse = fused_norm_on(epi);
+  if (fuse) {
+    a.gate = epi->gate; a.nw = epi->w; a.nb = epi->b; a.nw_dtype = epi->w_dtype;
+    a.eps = epi->eps; a.sigmoid_only = epi->sigmoid_only;
+  }
   if (int rc = from_launch(kgdn::launch_seg_fwd(a, cdt, qk_dtype, (int)K, (int)V, s), "segment forward")) return rc;
+  if (epi && !fuse)
+    if (int rc = norm_in_place(o, v_dtype, *epi, (int64_t)tok, V, s)) return rc;
   return ok();
 }
 
@@ -656,6 +694,35 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
   return chunk_fwd_impl("kairos_gdn_chunk_fwd", true, q, k, v, g, beta, q_scale, k_scale, initial_state, o,
                         final_state, cu_seqlens, n_seqs, B, T, H, K, V, qk_dtype, v_dtype, g_dtype, beta_dtype,
                         h0_dtype, scale, use_qk_l2norm, workspace, workspace_bytes, stream);
+}
+
+int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                                    const float* q_scale, const float* k_scale, const void* initial_state,
+                                    const void* gate, const void* norm_weight, const void* norm_bias, void* y,
+                                    float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B,
+                                    int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype, int v_dtype,
+                                    int g_dtype, int beta_dtype, int h0_dtype, int gate_dtype, int norm_w_dtype,
+                                    float scale, int use_qk_l2norm, float eps, int activation, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_chunk_fwd_gated_norm";
+  if (!valid_scalar_dt(gate_dtype)) return fail(KAIROS_GDN_EINVAL, "%s: gate must be fp32 or bf16", what);
+  if ((norm_weight || norm_bias) && !valid_scalar_dt(norm_w_dtype))
+    return fail(KAIROS_GDN_EINVAL, "%s: norm weight and bias must be fp32 or bf16", what);
+  if (activation != KAIROS_GDN_ACT_SWISH && activation != KAIROS_GDN_ACT_SIGMOID)
+    return fail(KAIROS_GDN_EINVAL, "%s: activation must be KAIROS_GDN_ACT_SWISH or KAIROS_GDN_ACT_SIGMOID", what);
+  if (!(eps >= 0.f)) return fail(KAIROS_GDN_EINVAL, "%s: eps must be non-negative", what);
+  if (V > 512)
+    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: the gated norm is built for V up to 512 (got %lld)", what,
+                (long long)V);
+  if (B > 0 && T > 0 && (!gate || !aligned16(gate)))
+    return fail(KAIROS_GDN_EINVAL, "%s: gate must be non-null and 16-byte aligned", what);
+  if ((norm_weight && !aligned16(norm_weight)) || (norm_bias && !aligned16(norm_bias)))
+    return fail(KAIROS_GDN_EINVAL, "%s: norm weight and bias must be 16-byte aligned", what);
+  const NormEpilogue epi{gate, norm_weight, norm_bias, gate_dtype, norm_w_dtype, eps,
+                         activation == KAIROS_GDN_ACT_SIGMOID ? 1 : 0};
+  return chunk_fwd_impl(what, true, q, k, v, g, beta, q_scale, k_scale, initial_state, y, final_state, cu_seqlens,
+                        n_seqs, B, T, H, K, V, qk_dtype, v_dtype, g_dtype, beta_dtype, h0_dtype, scale,
+                        use_qk_l2norm, workspace, workspace_bytes, stream, &epi);
 }
 
 size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void) { return kScratchBytes; }

@@ -158,6 +158,14 @@ struct SegFwdArgs {
   bool run_combine;       // ... or final_state of empty sequences is needed
   bool skip_out;          // stop after the segment scan (s_init, M): the backward's recomputation
   hipEvent_t* events;     // optional [5]: recorded before seg_prep, seg_trans, seg_combine, seg_out and after seg_out
+  // optional gated RMSNorm epilogue fused into the output (fla modules/fused_norm_gate.py:42-127, the
+  // layer's o_norm): with gate set, o receives y = bf16(o) rstd w [+ b] times g sigmoid(g) (or sigmoid(g))
+  const void* gate;       // [B*T, H, V] bf16, or nullptr (no epilogue)
+  const void* nw;         // [V] (nw_dtype) or nullptr
+  const void* nb;         // [V] (nw_dtype) or nullptr
+  int nw_dtype;
+  float eps;
+  int sigmoid_only;
 };
 
 // Backward pass (gdn_bwd.hip), after the forward is recomputed by launch_prepare (gc, w, uT, Ai)

@@ -1183,6 +1183,14 @@ struct SegOutArgs {
   void* o;                    // [B*T, H, V]
   float* ht;                  // [N, H, K, V] or nullptr
   int l2;                     // normalise q and k rows on their way to LDS (the in-op L2 norm)
+  // the layer's gated RMSNorm epilogue fused into the output (seg_out_kernel<..., true>): o is
+  // replaced by y = bf16(o) rstd w [+ b], times g sigmoid(g) (or sigmoid(g)), rstd over the V columns
+  const bf16* gate;           // [B*T, H, V] bf16
+  const void* nw;             // [V] in nw_dtype, or nullptr (ones)
+  const void* nb;             // [V] in nw_dtype, or nullptr (zeros)
+  int nw_dtype;
+  float eps;
+  int sigmoid_only;
 };
 
 template <typename TQ, int K, int V>
@@ -1209,6 +1217,10 @@ struct OutPlan {
   static constexpr uint32_t off_aqk = off_w + C * LDW * 2;
   static constexpr uint32_t off_u = off_aqk + C * LDQ * 2;
   static constexpr uint32_t total = off_u + V * LDU * 2;
+  // with the fused norm epilogue: each consumer wave's sum of squares of its columns per token
+  static constexpr uint32_t off_ss = total;
+  static constexpr uint32_t off_nw = off_ss + C * NCW * 4;   // its weight and bias, fp32 [2][V]
+  static constexpr uint32_t total_norm = off_nw + 2 * V * 4;
   // staging: units of 8 elements (16 bytes bf16, 8 bytes fp8)
   static constexpr int PT = NPW * WAVE;                  // producer threads
   static constexpr int QU = C * K / 8, VU = C * V / 8, RU = kSegRecordBytes / 16, AU = AB / 16;
@@ -1371,7 +1383,12 @@ struct OutProducts {
   uint2 u[NU][4];
 };
 
-template <typename TQ, int K, int V>
+// sigmoid(z) = 1 / (1 + 2^(-z log2 e)) (v_exp_f32, v_rcp_f32), as the standalone epilogue kernel
+__device__ __forceinline__ float norm_sigmoid(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
+}
+
+template <typename TQ, int K, int V, bool kNorm>
 __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOutArgs a, SegGeom G) {
   using P = OutPlan<TQ, K, V>;
   constexpr int KT = P::KT, KS = P::KS, CTN = P::CTN;
@@ -1449,6 +1466,16 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
     cs.load(SRC(a, t_seg, chunk_nv(0), h, H, rec0), H);
     cs.store(smem, 0);
     if (sl.nch > 1) cs.load(SRC(a, t_seg + C, chunk_nv(1), h, H, rec0 + rec_step), H);
+    // the fused epilogue's weight and bias, fp32 in LDS (the consumer threads cover the V columns)
+    if constexpr (kNorm) {
+      float* s_nw = reinterpret_cast<float*>(smem + P::off_nw);
+      for (int col = threadIdx.x; col < V; col += P::NCW * WAVE) {
+        s_nw[col] = a.nw ? (a.nw_dtype == DT_F32 ? reinterpret_cast<const float*>(a.nw)[col]
+                                                 : (float)reinterpret_cast<const bf16*>(a.nw)[col]) : 1.f;
+        s_nw[V + col] = a.nb ? (a.nw_dtype == DT_F32 ? reinterpret_cast<const float*>(a.nb)[col]
+                                                     : (float)reinterpret_cast<const bf16*>(a.nb)[col]) : 0.f;
+      }
+    }
     lds_barrier();
     for (int c = -1; c < sl.nch; ++c) {
       // with the in-op L2 norm of bf16 q: the q rows of chunk c + 1, stored raw by the producers in
@@ -1485,6 +1512,26 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
 #pragma unroll
               for (int ct = 0; ct < CTN; ++ct) mma(Y[tm][ct], wa, hb[ks][ct]);
             }
+        }
+        if constexpr (kNorm) {
+          // the gate of this wave's 16 columns for the epilogue, 64 tokens x 32 bytes, loaded straight
+          // into LDS over this wave's 16 rows of u^T: they were read above and the producers rewrite
+          // them only after B2.  Lane slot s = 64 j + lane holds token s / 2, 8 columns (s & 1);
+          // rows past the chunk end read row 0.
+          __builtin_amdgcn_s_waitcnt(0xC07F);          // this wave's u reads have completed
+          const unsigned char* gbase = reinterpret_cast<const unsigned char*>(a.gate) +
+                                       (((t_seg + (int64_t)c * C) * H + h) * V + vw) * 2;
+          const uint32_t slice = lds0 + P::off_u + 2u * vw * LDU;
+          // the epilogue's lane-derived addresses are formed where they are used: an opaque copy of
+          // the lane index keeps the compiler from holding them in registers across the loop
+          int lk = l;
+          asm volatile("" : "+v"(lk));
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int sl_ = 64 * j + lk, t = sl_ >> 1;
+            dma16(gbase, (uint32_t)((t < nvc ? t : 0) * H * V * 2 + 16 * (sl_ & 1)),
+                  __builtin_amdgcn_readfirstlane(slice + 1024u * j));
+          }
         }
         // o^T = (o_inter^T exp(gc) + v'^T bf16(Aqk)^T) scale  (chunk_o.py:84-128), with
         // o_inter^T = h^T q^T (chunk_o.py:84-107)
@@ -1531,7 +1578,66 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
         unsigned char* ob = reinterpret_cast<unsigned char*>(o + ((t_seg + (int64_t)c * C) * H + h) * V + vw) +
                             8 * lg;
         const uint32_t row_bytes = (uint32_t)H * V * 2;
-        if (nvc == C) {
+        if constexpr (kNorm) {
+          // the epilogue (fused_norm_gate.py:42-127 on the bf16 o): each wave's share of every token's
+          // sum of squares goes to LDS; after a barrier that the producer waves take at the end of
+          // their half (the consumers wait there for them in any case) the shares are summed, and y
+          // replaces o, with the gate that this wave loaded into LDS above.
+          static_assert(CTN == 1, "the epilogue's gate slice holds 16 columns per consumer wave");
+          float* s_ss = reinterpret_cast<float*>(smem + P::off_ss);
+          int lk = l;
+          asm volatile("" : "+v"(lk));
+          const int lg = lk >> 4, lc = lk & 15;
+#pragma unroll
+          for (int tn = 0; tn < 4; ++tn) {
+            float ss = 0.f;
+            const uint32_t wds[2] = {ov[tn][0].x, ov[tn][0].y};
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const float x0 = __uint_as_float(wds[e] << 16), x1 = __uint_as_float(wds[e] & 0xffff0000u);
+              ss = fmaf(x0, x0, ss);
+              ss = fmaf(x1, x1, ss);
+            }
+            ss += __shfl_xor(ss, 16, WAVE);
+            ss += __shfl_xor(ss, 32, WAVE);
+            if (lg == 0) s_ss[(16 * tn + lc) * P::NCW + wid] = ss;
+          }
+          wait_loads();                                  // this wave's gate slice has landed
+          lds_barrier();                                 // the row sums (the producers' matching barrier ends their half)
+          const float* s_nw = reinterpret_cast<const float*>(smem + P::off_nw);
+          const unsigned char* gsl = smem + P::off_u + 2u * vw * LDU + 8 * lg;
+          const f32x4 wv4 = *reinterpret_cast<const f32x4*>(s_nw + vw + 4 * lg);
+          const f32x4 bv4 = *reinterpret_cast<const f32x4*>(s_nw + V + vw + 4 * lg);
+          static_assert(P::NCW % 4 == 0, "row sums are read four shares at a time");
+          // lane i sums the shares of token i; each lane then takes rstd of its four tokens
+          float tot = 0.f;
+#pragma unroll
+          for (int w = 0; w < P::NCW; w += 4) {
+            const f32x4 sh = *reinterpret_cast<const f32x4*>(s_ss + lk * P::NCW + w);
+            tot += (sh[0] + sh[1]) + (sh[2] + sh[3]);
+          }
+          const float r_own = __builtin_amdgcn_rsqf(tot / (float)V + a.eps);
+#pragma unroll
+          for (int tn = 0; tn < 4; ++tn) {
+            const int t = 16 * tn + lc;
+            const float r = __shfl(r_own, t, WAVE);
+            const uint2 gq = *reinterpret_cast<const uint2*>(gsl + 32 * t);
+            const uint32_t xw[2] = {ov[tn][0].x, ov[tn][0].y}, gw[2] = {gq.x, gq.y};
+            float yv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t xb = xw[e >> 1], gbits = gw[e >> 1];
+              const float x = (e & 1) ? __uint_as_float(xb & 0xffff0000u) : __uint_as_float(xb << 16);
+              const float g = (e & 1) ? __uint_as_float(gbits & 0xffff0000u) : __uint_as_float(gbits << 16);
+              const float v = fmaf(x * r, wv4[e], bv4[e]);
+              const float sg = norm_sigmoid(g);
+              yv[e] = a.sigmoid_only ? v * sg : v * g * sg;
+            }
+            if (t < nvc)
+              *reinterpret_cast<uint2*>(ob + t * row_bytes) = make_uint2(pack_bf16x2(yv[0], yv[1]),
+                                                                         pack_bf16x2(yv[2], yv[3]));
+          }
+        } else if (nvc == C) {
 #pragma unroll
           for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
@@ -1680,6 +1786,9 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
       issue(0);
       u_item(std::integral_constant<int, 1>{});
       issue(0);
+      }
+      if constexpr (kNorm) {
+        if (c >= 0) lds_barrier();                       // the consumers' epilogue barrier (row sums in LDS)
       }
       lds_barrier();                                     // B2
       // ---------------- B2 .. B1: w, u of chunk c + 1 and q of chunk c + 2 to LDS
@@ -2568,12 +2677,21 @@ int launch_seg_t(const SegFwdArgs& p, hipStream_t s) {
   }
   if (!mark(3)) return -1;
   if (p.ns_grid > 0 && !p.skip_out) {
-    constexpr size_t lds = OutPlan<TQ, K, V>::total;
-    auto ko = seg_out_kernel<TQ, K, V>;
-    if (set_lds(ko, lds)) return -1;
     SegOutArgs oa{p.q, p.k, p.v, p.q_scale, p.k_scale,
-                  p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht, p.l2 ? 1 : 0};
-    hipLaunchKernelGGL(ko, grid, dim3(OutPlan<TQ, K, V>::NT), lds, s, oa, G);
+                  p.h0, p.h0_dtype, p.s_init, Ai, p.scale, p.o, p.ht, p.l2 ? 1 : 0,
+                  reinterpret_cast<const bf16*>(p.gate), p.nw, p.nb, p.nw_dtype, p.eps, p.sigmoid_only};
+    if (p.gate) {
+      constexpr size_t lds = OutPlan<TQ, K, V>::total_norm;
+      static_assert(lds <= 160 * 1024, "the epilogue's sums must fit beside the output tiles");
+      auto ko = seg_out_kernel<TQ, K, V, true>;
+      if (set_lds(ko, lds)) return -1;
+      hipLaunchKernelGGL(ko, grid, dim3(OutPlan<TQ, K, V>::NT), lds, s, oa, G);
+    } else {
+      constexpr size_t lds = OutPlan<TQ, K, V>::total;
+      auto ko = seg_out_kernel<TQ, K, V, false>;
+      if (set_lds(ko, lds)) return -1;
+      hipLaunchKernelGGL(ko, grid, dim3(OutPlan<TQ, K, V>::NT), lds, s, oa, G);
+    }
     if (hipGetLastError() != hipSuccess) return -1;
   }
   if (!mark(4)) return -1;

@@ -97,12 +97,14 @@ def _scales(q_scale, k_scale, H, device, fp8: bool):
 
 
 def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens=None,
-                               use_qk_l2norm_in_kernel=False, q_scale=None, k_scale=None):
+                               use_qk_l2norm_in_kernel=False, q_scale=None, k_scale=None, _norm=None):
     """One native call: [q/k L2 norm] -> prepare -> state recurrence -> output.
 
     Mirrors chunk_gated_delta_rule_fwd (chunk.py:16-67) plus the optional
     in-kernel L2 norm of ChunkGatedDeltaRuleFunction.forward (chunk.py:168-170).
-    Returns (o in v's dtype, final_state fp32 or None).
+    Returns (o in v's dtype, final_state fp32 or None).  ``_norm`` (gate,
+    weight, bias, eps, activation code) turns o into the layer's gated RMSNorm
+    of o (chunk_gated_delta_rule_gated_norm).
     """
     dev = _require_device(q, k, v, g, beta, initial_state)
     B, T, H, K = q.shape
@@ -138,10 +140,65 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_fi
     ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, qk_dt, v_dt,
                                                        int(bool(use_qk_l2norm_in_kernel)))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    if _norm is not None:
+        gate, nw, nb, eps, act = _norm
+        w_dt = _code(nw if nw is not None else nb, "norm weight") if (nw is not None or nb is not None) else _lib.F32
+        _lib.call("kairos_gdn_chunk_fwd_gated_norm", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(qs),
+                  _ptr(ks), _ptr(h0), _ptr(gate), _ptr(nw), _ptr(nb), _ptr(o), _ptr(ht), _ptr(cu), n_seqs, B, T, H,
+                  K, V, qk_dt, v_dt, g_dt, b_dt, h0_dt, _code(gate, "gate"), w_dt, float(scale),
+                  int(bool(use_qk_l2norm_in_kernel)), float(eps), act, _ptr(ws), ws_bytes, _stream(dev))
+        return o, ht
     _lib.call("kairos_gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(qs), _ptr(ks),
               _ptr(h0), _ptr(o), _ptr(ht), _ptr(cu), n_seqs, B, T, H, K, V, qk_dt, v_dt, g_dt, b_dt, h0_dt,
               float(scale), int(bool(use_qk_l2norm_in_kernel)), _ptr(ws), ws_bytes, _stream(dev))
     return o, ht
+
+
+_NORM_ACT = {"swish": _lib.ACT_SWISH, "silu": _lib.ACT_SWISH, "sigmoid": _lib.ACT_SIGMOID}
+
+
+@torch.no_grad()
+def chunk_gated_delta_rule_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                                      beta: torch.Tensor, gate: torch.Tensor, norm_weight: torch.Tensor | None = None,
+                                      norm_bias: torch.Tensor | None = None, scale: float | None = None,
+                                      initial_state: torch.Tensor | None = None, output_final_state: bool = False,
+                                      cu_seqlens: torch.Tensor | None = None, use_qk_l2norm_in_kernel: bool = False,
+                                      activation: str = "swish", eps: float = 1e-5, q_scale=None, k_scale=None):
+    """Forward of the GatedDeltaNet layer's recurrence and output norm in one call:
+    ``o_norm(chunk_gated_delta_rule(q, k, v, g, beta, ...)[0], gate)``
+    (fla layers/gated_deltanet.py:275-311, o_norm = FusedRMSNormGated on the
+    RMS path without residual, modules/fused_norm_gate.py:42-127).
+
+    Returns (y in v's dtype, final_state fp32 or None).  y equals
+    ``rms_norm_gated(o, gate, norm_weight, norm_bias, activation, eps)`` of the
+    plain forward's o (the norm reads o rounded to its dtype).  Forward only:
+    training keeps the two calls, since the norm's backward needs o.  Where the
+    segment scan runs (bf16, head dims 64 / 128) with a bf16 gate the norm is
+    computed in the output kernel and o is never written.
+    """
+    if activation not in _NORM_ACT:
+        raise ValueError(f"Unsupported activation: {activation}")
+    V = v.shape[-1]
+    if tuple(gate.shape) != tuple(v.shape):
+        raise ValueError(f"gate shape {tuple(gate.shape)} != v shape {tuple(v.shape)}")
+    for name, p in (("norm_weight", norm_weight), ("norm_bias", norm_bias)):
+        if p is not None and tuple(p.shape) != (V,):
+            raise ValueError(f"{name} must have shape ({V},), got {tuple(p.shape)}")
+    if norm_weight is not None and norm_bias is not None and norm_weight.dtype != norm_bias.dtype:
+        raise TypeError("norm_weight and norm_bias must share a dtype")
+    _require_device(gate, norm_weight, norm_bias)
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    if cu_seqlens is not None and q.shape[0] != 1:
+        raise ValueError(
+            f"The batch size is expected to be 1 rather than {q.shape[0]} when using `cu_seqlens`."
+            f"Please flatten variable-length inputs before processing.")
+    gate = gate.contiguous()
+    norm_weight = norm_weight.contiguous() if norm_weight is not None else None
+    norm_bias = norm_bias.contiguous() if norm_bias is not None else None
+    return chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_final_state, cu_seqlens,
+                                      use_qk_l2norm_in_kernel, q_scale, k_scale,
+                                      _norm=(gate, norm_weight, norm_bias, eps, _NORM_ACT[activation]))
 
 
 def chunk_gated_delta_rule_bwd(q, k, v, g, beta, scale, initial_state, do, dht, cu_seqlens=None,
