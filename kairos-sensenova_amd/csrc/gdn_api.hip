@@ -345,6 +345,32 @@ int wide_pipe_parts() {
   return p < 1 ? 1 : p > kMaxParts ? kMaxParts : p;
 }
 
+// Part sizes grow by this factor (KAIROS_GDN_WIDE_PIPE_GROWTH; 1 = equal parts): part 0's prepare
+// runs alone, so a smaller first part shortens the call as long as each later part's prepare, on
+// the CUs the recurrence leaves, still finishes within the previous recurrence part.
+double wide_pipe_growth() {
+  const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE_GROWTH");
+  if (e == nullptr) return 1.0;
+  const double g = std::atof(e);
+  return g < 0.25 ? 0.25 : g > 4.0 ? 4.0 : g;
+}
+
+// Chunk boundaries of P parts of nt chunks with sizes growing by `growth`: b[0] = 0, b[P] = nt, every
+// part at least one chunk (nt >= P)
+void wide_pipe_bounds(int64_t nt, int P, double growth, int64_t* b) {
+  double tot = 0.0, wsum = 0.0;
+  for (int p = 0; p < P; ++p) tot += std::pow(growth, p);
+  b[0] = 0;
+  for (int p = 1; p < P; ++p) {
+    wsum += std::pow(growth, p - 1);
+    int64_t x = (int64_t)std::llround((double)nt * wsum / tot);
+    x = std::max<int64_t>(x, b[p - 1] + 1);
+    x = std::min<int64_t>(x, nt - (P - p));
+    b[p] = x;
+  }
+  b[P] = nt;
+}
+
 std::mutex g_aux_mu;                                     // held while a pipelined call enqueues its work
 hipStream_t g_aux_stream[64][2] = {};
 hipEvent_t g_aux_events[64][2 * kMaxParts + 1] = {};
@@ -433,8 +459,15 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
       }
     }
     if (P > 1) {
-      const int64_t span = (nt + P - 1) / P;
-      P = (int)((nt + span - 1) / span);                  // no empty trailing part (13 chunks in 6: 5 parts of 3)
+      const double growth = wide_pipe_growth();
+      int64_t bnd[kMaxParts + 1];
+      if (growth == 1.0) {
+        const int64_t span = (nt + P - 1) / P;
+        P = (int)((nt + span - 1) / span);                // no empty trailing part (13 chunks in 6: 5 parts of 3)
+        for (int p = 0; p <= P; ++p) bnd[p] = std::min<int64_t>(p * span, nt);
+      } else {
+        wide_pipe_bounds(nt, P, growth, bnd);
+      }
       int rc = KAIROS_GDN_OK;
       auto wait = [&](hipStream_t st, hipEvent_t e) {
         if (rc == KAIROS_GDN_OK && hipStreamWaitEvent(st, e, 0) != hipSuccess) rc = fail(KAIROS_GDN_EHIP, "hipStreamWaitEvent");
@@ -444,8 +477,8 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
       };
       // ev[p]: prepare p done; ev[kMaxParts + p]: recurrence part p about to be dispatched
       auto prepare = [&](int p, hipStream_t sp) {
-        pa.it0 = p * span;
-        pa.it_span = std::min(span, nt - p * span);
+        pa.it0 = bnd[p];
+        pa.it_span = bnd[p + 1] - bnd[p];
         if (rc == KAIROS_GDN_OK)
           rc = from_launch(kgdn::launch_prepare(pa, cdt, qk_dtype, K, V, (int64_t)N * pa.it_span, sp), "prepare");
         record(ev[p], sp);
@@ -456,8 +489,8 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
         if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_marker(s3), "marker");
         record(ev[kMaxParts + p], s3);
         kgdn::WideFusedArgs fp = fa;
-        fp.it_begin = p * span;
-        fp.it_end = std::min((p + 1) * span, nt);
+        fp.it_begin = bnd[p];
+        fp.it_end = bnd[p + 1];
         if (p > 0) {
           fp.h0 = st;
           fp.h0_dtype = KAIROS_GDN_F32;

@@ -11,6 +11,7 @@
 // Output layouts: gc [B*T, H] fp32; w [B*T, H, K] (token-major, as the
 // reference); u per chunk transposed, uT [NC, H, V, 64], which is the
 // K-contiguous operand layout the state kernel reads.
+#include <cstdlib>
 #include <type_traits>
 
 #include "gdn_common.hpp"
@@ -41,6 +42,29 @@ __device__ __forceinline__ void st_pair(TC* p, float a, float b) {
 // columns at a time (u is separable over V).  VP is the widest pass that keeps
 // the tile within 80 KB (two workgroups per CU, so one's serial phases overlap
 // the other's), else within 160 KB.
+//
+// Compact plan (bf16, no u pass): k stays row-major for the whole kernel and the w operand
+// (k beta e^gc)^T is formed from transposed reads of it (ds_read_b64_tr_b16) instead of a
+// tile of its own; A / Ai sit beside k.  At K = 256 that is 52 KB, three workgroups per CU
+// (the full plan's 72 KB allows two).
+template <typename TC, int K>
+struct PrepLdsCompact {
+  static constexpr int LDK = K + 8;
+  static constexpr int LDT = C + 8;
+  static constexpr int LDA = C + 4;
+  static constexpr size_t al16(size_t x) { return (x + 15) / 16 * 16; }
+  static constexpr size_t k_bytes = al16(sizeof(TC) * C * LDK);
+  static constexpr size_t a_bytes = al16(sizeof(float) * C * LDA);
+  static constexpr size_t ai_bytes = al16(sizeof(TC) * C * LDT);
+  static constexpr int VP = 64;                                 // unused: no u pass
+  static constexpr size_t off_A = k_bytes;
+  static constexpr size_t off_Ai = k_bytes;                     // over A once the inverse is read
+  static constexpr size_t off_vbT = 0;                          // unused
+  static constexpr size_t off_kbT = 0;                          // unused: read from k
+  static constexpr size_t off_g = off_A + (a_bytes > ai_bytes ? a_bytes : ai_bytes);
+  static constexpr size_t total = off_g + sizeof(float) * 3 * C;
+};
+
 template <typename TC, int K>
 struct PrepLds {
   static constexpr int LDK = K + 8;      // s_k row stride (elements)
@@ -67,9 +91,60 @@ struct PrepLds {
   static constexpr size_t total = off_g + sizeof(float) * 3 * C;
 };
 
-template <typename TC, typename TK, int K>
+// (k beta e^gc)^T as an MMA operand from the row-major k tile: rows d = d0 + l % 16, tokens
+// t0 + 8 (l / 16) .. + 7, by two transposed reads (tokens + 0..3 and + 4..7); k beta is rounded
+// when beta is bf16 (wy_fast.py:77) and the product once more, as the staged tile stores it.
+template <int LDK>
+__device__ __forceinline__ Frag<bf16> kbT_frag(const bf16* s_k, int d0, int t0, const float* s_b, const float* s_eg,
+                                               bool beta_bf16) {
+  const int l = lane_id();
+  const int lg = l >> 4, lc = l & 15;
+  const int tb = t0 + 8 * lg;
+  const s16x4_t x0 = lds_read_tr16(s_k + (tb + (lc >> 2)) * LDK + d0 + 4 * (lc & 3));
+  const s16x4_t x1 = lds_read_tr16(s_k + (tb + 4 + (lc >> 2)) * LDK + d0 + 4 * (lc & 3));
+  const f32x4 b0 = *reinterpret_cast<const f32x4*>(s_b + tb), b1 = *reinterpret_cast<const f32x4*>(s_b + tb + 4);
+  const f32x4 e0 = *reinterpret_cast<const f32x4*>(s_eg + tb), e1 = *reinterpret_cast<const f32x4*>(s_eg + tb + 4);
+  Frag<bf16> f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const short bits = e < 4 ? x0[e] : x1[e - 4];
+    const float kv = __uint_as_float((uint32_t)(uint16_t)bits << 16);
+    float kb = kv * (e < 4 ? b0[e] : b1[e - 4]);
+    if (beta_bf16) kb = (float)(bf16)kb;
+    f.v[e] = (bf16)(kb * (e < 4 ? e0[e] : e1[e - 4]));
+  }
+  return f;
+}
+
+// g and beta of one token row, fp32 or bf16 each (0 / 1), both loads issued before either value
+// is used (one memory latency for the pair, not two)
+__device__ __forceinline__ void ld_gate_pair(const void* g, int g_dt, const void* b, int b_dt, int64_t i, float& gv,
+                                             float& bv) {
+  if (g_dt == 0 && b_dt == 0) {
+    const float x = reinterpret_cast<const float*>(g)[i], y = reinterpret_cast<const float*>(b)[i];
+    gv = x;
+    bv = y;
+  } else if (g_dt == 0) {
+    const float x = reinterpret_cast<const float*>(g)[i];
+    const bf16 y = reinterpret_cast<const bf16*>(b)[i];
+    gv = x;
+    bv = (float)y;
+  } else if (b_dt == 0) {
+    const bf16 x = reinterpret_cast<const bf16*>(g)[i];
+    const float y = reinterpret_cast<const float*>(b)[i];
+    gv = (float)x;
+    bv = y;
+  } else {
+    const bf16 x = reinterpret_cast<const bf16*>(g)[i], y = reinterpret_cast<const bf16*>(b)[i];
+    gv = (float)x;
+    bv = (float)y;
+  }
+}
+
+template <typename TC, typename TK, int K, bool kCompact>
 __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) {
-  using L = PrepLds<TC, K>;
+  using L = std::conditional_t<kCompact, PrepLdsCompact<TC, K>, PrepLds<TC, K>>;
+  static_assert(!kCompact || std::is_same<TC, bf16>::value, "the compact plan reads k with 16-bit transposed reads");
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_k = reinterpret_cast<TC*>(smem);
   float* s_A = reinterpret_cast<float*>(smem + L::off_A);  // aliases s_k once K.K^T is done
@@ -99,13 +174,53 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   const int l = lane_id();
   const int lg = l >> 4, lc = l & 15;
 
+  // ---- the chunk's k rows (token pair pr, column group cg) and, with aqk_out, q row tile wid are
+  //      loaded first, raw, so that their latency overlaps the gates and each other.  Every load is
+  //      issued unconditionally, rows past the chunk's end reading row 0: k is zeroed there when it
+  //      is staged, and q rows past the end only feed Aqk rows that are stored as zero.  (Loads in
+  //      a branch of their own would each be waited for before the next is issued.)
+  const int pr = tid & 31, cg = tid >> 5;                // token pair (2 pr, 2 pr + 1), column group of 8
+  using Raw = std::conditional_t<sizeof(TK) == 1, uint2, Vec8<TK>>;
+  auto ld_raw = [](const TK* p) -> Raw {
+    if constexpr (sizeof(TK) == 1) return *reinterpret_cast<const uint2*>(p);
+    else return ld8<TK>(p);
+  };
+  auto cvt_raw = [](const Raw& r, float scale, float (&out)[8]) {
+    if constexpr (sizeof(TK) == 1) {
+      fp8x4_to_f32(r.x, out);
+      fp8x4_to_f32(r.y, out + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] *= scale;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = vget<TK>(r, e);
+    }
+  };
+  const TK* kin = reinterpret_cast<const TK*>(a.k);
+  const bool ok0 = 2 * pr < nv, ok1 = 2 * pr + 1 < nv;
+  Raw kraw[K / 64][2];
+  {
+    const TK* krow0 = kin + ((t0 + (ok0 ? 2 * pr : 0)) * H + h) * K + cg * (K / 8);
+    const TK* krow1 = kin + ((t0 + (ok1 ? 2 * pr + 1 : 0)) * H + h) * K + cg * (K / 8);
+#pragma unroll
+    for (int ch = 0; ch < K / 64; ++ch) {
+      kraw[ch][0] = ld_raw(krow0 + 8 * ch);
+      kraw[ch][1] = ld_raw(krow1 + 8 * ch);
+    }
+  }
+  Raw qraw[K / 32];
+  if (a.aqk_out) {
+    const int qr = 16 * wid + lc;
+    const TK* qrow = reinterpret_cast<const TK*>(a.q) + ((t0 + (qr < nv ? qr : 0)) * H + h) * K + 8 * lg;
+#pragma unroll
+    for (int ks = 0; ks < K / 32; ++ks) qraw[ks] = ld_raw(qrow + 32 * ks);
+  }
+
   // ---- gates: chunk-local cumsum of g (one wave, inclusive scan over 64 lanes)
   if (wid == 0) {
     float gv = 0.f, bv = 0.f;
-    if (l < nv) {
-      gv = ld_scalar(a.g, (t0 + l) * H + h, a.g_dtype);
-      bv = ld_scalar(a.beta, (t0 + l) * H + h, a.beta_dtype);
-    }
+    ld_gate_pair(a.g, a.g_dtype, a.beta, a.beta_dtype, (t0 + (l < nv ? l : 0)) * H + h, gv, bv);
+    if (l >= nv) gv = bv = 0.f;
 #pragma unroll
     for (int off = 1; off < WAVE; off <<= 1) {
       const float o = __shfl_up(gv, off, WAVE);
@@ -119,29 +234,29 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
   __syncthreads();
 
-  // ---- with aqk_out: q row tile wid as MFMA fragments (rows 16 wid + lc, zero past the chunk's
-  //      end), loaded now so that they arrive during the k staging and K.K^T
+  // ---- with aqk_out: q row tile wid as MFMA fragments (rows 16 wid + lc), from the raw loads
   Frag<TC> qf[K / 32];
   if (a.aqk_out) {
-    const TK* qin = reinterpret_cast<const TK*>(a.q);
-    const int qr = 16 * wid + lc;
 #pragma unroll
     for (int ks = 0; ks < K / 32; ++ks) {
-      float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (qr < nv) load8_in<TK>(qin + ((t0 + qr) * H + h) * K + 32 * ks + 8 * lg, 1.f, x);
-      if constexpr (sizeof(TC) == 2) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks].v[e] = (bf16)x[e];
+      if constexpr (sizeof(TC) == 2 && sizeof(TK) == 2) {
+        qf[ks].v = __builtin_bit_cast(bf16x8, qraw[ks]);
       } else {
-        qf[ks].lo = f32x4{x[0], x[1], x[2], x[3]};
-        qf[ks].hi = f32x4{x[4], x[5], x[6], x[7]};
+        float x[8];
+        cvt_raw(qraw[ks], 1.f, x);
+        if constexpr (sizeof(TC) == 2) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qf[ks].v[e] = (bf16)x[e];
+        } else {
+          qf[ks].lo = f32x4{x[0], x[1], x[2], x[3]};
+          qf[ks].hi = f32x4{x[4], x[5], x[6], x[7]};
+        }
       }
     }
   }
 
   // ---- v of the first pass (below) into registers now, so its loads overlap K.K^T and the solve
   const TC* vin = reinterpret_cast<const TC*>(a.v);
-  const int pr = tid & 31, cg = tid >> 5;                // token pair (2 pr, 2 pr + 1), column group of 8
   const bool v_vec = V % 64 == 0;                         // every pass width a multiple of 64 (VP is)
   Vec8<TC> vr[2][L::VP / 64];
   auto load_v = [&](int p0) {
@@ -151,9 +266,9 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
       if (8 * ch >= cpg) break;
       const int c = p0 + cg * cpg + 8 * ch;
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
+      for (int rr = 0; rr < 2; ++rr) {                    // rows past the end read row 0, masked at use
         const int r = 2 * pr + rr;
-        vr[rr][ch] = r < nv ? ld8<TC>(vin + ((t0 + r) * H + h) * V + c) : vzero<TC>();
+        vr[rr][ch] = ld8<TC>(vin + ((t0 + (r < nv ? r : 0)) * H + h) * V + c);
       }
     }
   };
@@ -164,29 +279,33 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   //      kb^T[d][t] = k*beta*exp(gc).  Lane = token pair, so each transposed store packs the pair
   //      (one 4-byte store in bf16) and the 32 lanes of a group hit 32 consecutive banks.
   const float kscale = a.k_scale ? a.k_scale[h] : 1.f;
-  const TK* kin = reinterpret_cast<const TK*>(a.k);
   {
     const float b0 = s_b[2 * pr], b1 = s_b[2 * pr + 1], e0 = s_eg[2 * pr], e1 = s_eg[2 * pr + 1];
 #pragma unroll
     for (int ch = 0; ch < K / 64; ++ch) {
       const int c8 = cg * (K / 8) + 8 * ch;
       float x0[8], x1[8];
+      cvt_raw(kraw[ch][0], kscale, x0);
+      cvt_raw(kraw[ch][1], kscale, x1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x0[e] = x1[e] = 0.f;
-      if (2 * pr < nv) load8_in<TK>(kin + ((t0 + 2 * pr) * H + h) * K + c8, kscale, x0);
-      if (2 * pr + 1 < nv) load8_in<TK>(kin + ((t0 + 2 * pr + 1) * H + h) * K + c8, kscale, x1);
+      for (int e = 0; e < 8; ++e) {
+        x0[e] = ok0 ? x0[e] : 0.f;
+        x1[e] = ok1 ? x1[e] : 0.f;
+      }
       Vec8<TC> r0, r1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float kv0 = round_to<TC>(x0[e]), kv1 = round_to<TC>(x1[e]);   // stored k (fp8: dequantised)
         vset<TC>(r0, e, kv0);
         vset<TC>(r1, e, kv1);
-        float kb0 = kv0 * b0, kb1 = kv1 * b1;
-        if (a.beta_dtype == 1) {                           // bf16*bf16 -> bf16 (wy_fast.py:77)
-          kb0 = round_to<TC>(kb0);
-          kb1 = round_to<TC>(kb1);
+        if constexpr (!kCompact) {
+          float kb0 = kv0 * b0, kb1 = kv1 * b1;
+          if (a.beta_dtype == 1) {                         // bf16*bf16 -> bf16 (wy_fast.py:77)
+            kb0 = round_to<TC>(kb0);
+            kb1 = round_to<TC>(kb1);
+          }
+          st_pair<TC>(s_kbT + (c8 + e) * L::LDT + 2 * pr, kb0 * e0, kb1 * e1);
         }
-        st_pair<TC>(s_kbT + (c8 + e) * L::LDT + 2 * pr, kb0 * e0, kb1 * e1);
       }
       st8<TC>(s_k + (2 * pr) * L::LDK + c8, r0);
       st8<TC>(s_k + (2 * pr + 1) * L::LDK + c8, r1);
@@ -358,13 +477,17 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
 
   // ---- w^T = kb^T Ai^T  (rows d, cols t) -> token-major w, 4 consecutive d per lane
   TC* w_out = reinterpret_cast<TC*>(a.w);
+  auto kb_op = [&](int d0, int tk) {                    // rows d0 + lc, tokens tk + 8 lg .. + 7
+    if constexpr (kCompact) return kbT_frag<L::LDK>(s_k, d0, tk, s_b, s_eg, a.beta_dtype == 1);
+    else return lds_frag<TC>(s_kbT, L::LDT, d0, tk);
+  };
   for (int tm = wid; tm < K / 16; tm += 4) {
+    const Frag<TC> kf0 = kb_op(16 * tm, 0), kf1 = kb_op(16 * tm, 32);
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks <= tn / 2; ++ks)
-        mma(acc, lds_frag<TC>(s_kbT, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_Ai, L::LDT, 16 * tn, 32 * ks));
+      mma(acc, kf0, lds_frag<TC>(s_Ai, L::LDT, 16 * tn, 0));
+      if (tn >= 2) mma(acc, kf1, lds_frag<TC>(s_Ai, L::LDT, 16 * tn, 32));
       const int t = 16 * tn + lc;
       if (t < nv) st4<TC>(w_out + ((t0 + t) * H + h) * K + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
     }
@@ -376,12 +499,12 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
     if (a.wT_out) {
       TC* wt = reinterpret_cast<TC*>(a.wT_out) + (cidx * H + h) * (K * C);
       for (int tn = wid; tn < K / 16; tn += 4) {
+        const Frag<TC> kf0 = kb_op(16 * tn, 0), kf1 = kb_op(16 * tn, 32);
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks <= tm / 2; ++ks)
-            mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 32 * ks), lds_frag<TC>(s_kbT, L::LDT, 16 * tn, 32 * ks));
+          mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 0), kf0);
+          if (tm >= 2) mma(acc, lds_frag<TC>(s_Ai, L::LDT, 16 * tm, 32), kf1);
           st4<TC>(wt + (16 * tn + lc) * C + 16 * tm + 4 * lg, acc[0], acc[1], acc[2], acc[3]);
         }
       }
@@ -390,6 +513,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   // ---- u = Ai vb  (rows t, cols v) -> uT[c][h][v][t], 4 consecutive t per lane;
   //      vb^T[v][t] = v*beta staged VP columns at a time into region 0 after Ai,
   //      so staging overlaps the w products above
+  if constexpr (kCompact) return;
   TC* uT = reinterpret_cast<TC*>(a.uT) + (cidx * H + h) * V * C;
   for (int p0 = 0; want_u && p0 < V; p0 += L::VP) {
     const int vw = min(L::VP, V - p0);             // a multiple of 16
@@ -402,7 +526,8 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
         const int c8 = cg * cpg + 8 * ch;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          st_pair<TC>(s_vbT + (c8 + e) * L::LDT + 2 * pr, vget<TC>(vr[0][ch], e) * b0, vget<TC>(vr[1][ch], e) * b1);
+          st_pair<TC>(s_vbT + (c8 + e) * L::LDT + 2 * pr, 2 * pr < nv ? vget<TC>(vr[0][ch], e) * b0 : 0.f,
+                      2 * pr + 1 < nv ? vget<TC>(vr[1][ch], e) * b1 : 0.f);
       }
       if (p0 + L::VP < V) load_v(p0 + L::VP);      // the next pass's loads overlap this pass's products
     } else {
@@ -429,11 +554,11 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
 }
 
-template <typename TC, typename TK, int K>
+template <typename TC, typename TK, int K, bool kCompact>
 int launch_prepare_t(const PrepareArgs& a, int V, int64_t nc_grid, hipStream_t s) {
-  using L = PrepLds<TC, K>;
+  using L = std::conditional_t<kCompact, PrepLdsCompact<TC, K>, PrepLds<TC, K>>;
   static_assert(L::total <= 160 * 1024, "prepare tile does not fit in LDS");
-  auto kern = prepare_kernel<TC, TK, K>;
+  auto kern = prepare_kernel<TC, TK, K, kCompact>;
   if (L::total > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)L::total) != hipSuccess)
@@ -449,8 +574,15 @@ int launch_prepare_t(const PrepareArgs& a, int V, int64_t nc_grid, hipStream_t s
 int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, int V, int64_t nc_grid,
                    hipStream_t s) {
   if (V <= 0 || V % 16 != 0) return -2;
-#define KGDN_PREP_CASE(TC, TK, KK) \
-  if (K == KK) return launch_prepare_t<TC, TK, KK>(a, V, nc_grid, s);
+  // the compact LDS plan for bf16 without the u pass (KAIROS_GDN_PREP_COMPACT=0 selects the full one)
+  const char* e = std::getenv("KAIROS_GDN_PREP_COMPACT");
+  const bool compact = a.uT == nullptr && compute_dtype == DT_BF16 && !(e && e[0] == '0' && e[1] == 0);
+#define KGDN_PREP_CASE(TC, TK, KK)                                                                  \
+  if (K == KK) {                                                                                    \
+    if constexpr (std::is_same<TC, bf16>::value)                                                    \
+      if (compact) return launch_prepare_t<TC, TK, KK, true>(a, V, nc_grid, s);                     \
+    return launch_prepare_t<TC, TK, KK, false>(a, V, nc_grid, s);                                   \
+  }
 #define KGDN_PREP_SHAPES(TC, TK) KGDN_PREP_CASE(TC, TK, 64) KGDN_PREP_CASE(TC, TK, 128) KGDN_PREP_CASE(TC, TK, 256)
   if (compute_dtype == DT_F32 && k_dtype == DT_F32) { KGDN_PREP_SHAPES(float, float) }
   if (compute_dtype == DT_BF16 && k_dtype == DT_BF16) { KGDN_PREP_SHAPES(bf16, bf16) }

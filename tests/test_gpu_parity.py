@@ -278,17 +278,19 @@ def test_model_head_dims_stage_kernels(cu, monkeypatch):
 def test_model_head_dims_pipeline_parts(with_h0, monkeypatch):
     """The K=256 forward cut into P parts along each sequence (prepare of the next part on a second
     stream beside the recurrence of this one, the state carried in fp32 between parts) gives the
-    same bits as one part: two sequences, a ragged last chunk, 13 chunks in 2, 3, 4 and 6 parts."""
+    same bits as one part: two sequences, a ragged last chunk, 13 chunks in 2, 3, 4 and 6 equal parts
+    and in parts that grow or shrink along the sequence."""
     note(f"K=256 pipeline parts h0={with_h0}")
     x = make_inputs(2, 64 * 12 + 37, 2, 256, 128, seed=43, dtype="bf16", h0_scale=0.02 if with_h0 else 0.0)
     monkeypatch.setenv("KAIROS_GDN_WIDE_PIPE", "1")
     o1, ht1 = run_gpu(x, "bf16", with_h0=with_h0)
     check_against_oracle(x, "bf16", o1, ht1, with_h0=with_h0)
-    for parts in ("2", "3", "4", "6"):
+    for parts, growth in (("2", "1"), ("3", "1"), ("4", "1"), ("6", "1"), ("4", "1.3"), ("3", "2.5"), ("6", "0.7")):
         monkeypatch.setenv("KAIROS_GDN_WIDE_PIPE", parts)
+        monkeypatch.setenv("KAIROS_GDN_WIDE_PIPE_GROWTH", growth)
         o, ht = run_gpu(x, "bf16", with_h0=with_h0)
-        assert torch.equal(o, o1), parts
-        assert torch.equal(ht, ht1), parts
+        assert torch.equal(o, o1), (parts, growth)
+        assert torch.equal(ht, ht1), (parts, growth)
 
 
 def test_empty_sequence_returns_initial_state():
