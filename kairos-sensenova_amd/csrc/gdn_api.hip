@@ -326,13 +326,14 @@ size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_s
 // reference's stage order with its intermediates in the workspace.  Used for the
 // shapes the fused kernels do not cover: fp32, and the Kairos model's head dims
 // K = 256, V = 512 (any K in {64, 128, 256} with V a multiple of 16).
-// The pipelined form of the fused K = 256 path: the chunks of every sequence are cut into P parts;
+// The pipelined form of the fused K = 256 path: the chunks of every sequence are cut into P parts
+// (5 by default, growing by 1.3 along the sequence);
 // the prepare kernel of part p + 1 runs on a second stream while the recurrence walks part p (whose
 // 64-column workgroups leave CUs idle: 160 of 256 at the Kairos layer shape), the state passing
 // between parts through an fp32 buffer.  KAIROS_GDN_WIDE_PIPE sets P (1: one prepare, then one
 // recurrence); fixed-length sequences only.  Part 0's prepare runs on the caller's stream (the whole
 // GPU), the later prepares on a second stream and the recurrence parts on a third.  Prepare p + 1
-// waits for a one-workgroup marker kernel queued just before recurrence part p, so the recurrence's
+// waits for an event recorded just before recurrence part p (wide_mark_mode), so the recurrence's
 // workgroups are dispatched first and the prepare fills the CUs they leave (were both ready at once,
 // the prepare's 10^4 workgroups could take every CU and hold the recurrence back).  The caller's
 // stream waits for the last recurrence part.
@@ -340,7 +341,7 @@ constexpr int kMaxParts = 16;
 
 int wide_pipe_parts() {
   const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE");
-  if (e == nullptr) return 4;
+  if (e == nullptr) return 5;
   const int p = std::atoi(e);
   return p < 1 ? 1 : p > kMaxParts ? kMaxParts : p;
 }
@@ -350,7 +351,7 @@ int wide_pipe_parts() {
 // the CUs the recurrence leaves, still finishes within the previous recurrence part.
 double wide_pipe_growth() {
   const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE_GROWTH");
-  if (e == nullptr) return 1.0;
+  if (e == nullptr) return 1.3;
   const double g = std::atof(e);
   return g < 0.25 ? 0.25 : g > 4.0 ? 4.0 : g;
 }
@@ -372,29 +373,41 @@ void wide_pipe_bounds(int64_t nt, int P, double growth, int64_t* b) {
 }
 
 std::mutex g_aux_mu;                                     // held while a pipelined call enqueues its work
-hipStream_t g_aux_stream[64][2] = {};
-hipEvent_t g_aux_events[64][2 * kMaxParts + 1] = {};
+hipStream_t g_aux_stream[64][3] = {};
+hipEvent_t g_aux_events[64][3 * kMaxParts + 1] = {};
 
-// The two streams (prepares, recurrence parts) and the events of the current device, created on
-// first use and kept until the process ends (a recorded event may be recorded again: waits already
-// enqueued keep the record they saw).  Call with g_aux_mu held.
-int aux_streams(hipStream_t* sp, hipStream_t* sr, hipEvent_t** events) {
+// What releases prepare p + 1 (KAIROS_GDN_WIDE_PIPE_MARK): 0, a one-workgroup marker kernel on the
+// recurrence stream just before part p; 1, that marker on a stream of its own once recurrence part
+// p - 1 has finished, beside the dispatch of part p; 2 (default), an event recorded on the
+// recurrence stream just before part p (no kernel: the recurrence parts follow each other directly).
+// At the Kairos layer shape 1 and 2 measure alike, 0 about 10 us slower per call.
+int wide_mark_mode() {
+  const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE_MARK");
+  if (e == nullptr) return 2;
+  const int m = std::atoi(e);
+  return m < 0 || m > 2 ? 2 : m;
+}
+
+// The three streams (prepares, recurrence parts, markers) and the events of the current device,
+// created on first use and kept until the process ends (a recorded event may be recorded again:
+// waits already enqueued keep the record they saw).  Call with g_aux_mu held.
+int aux_streams(hipStream_t* sp, hipStream_t* sr, hipStream_t* sm, hipEvent_t** events) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
   if (g_aux_events[dev][0] == nullptr) {
-    for (int p = 0; p < 2 * kMaxParts + 1; ++p)
+    for (int p = 0; p < 3 * kMaxParts + 1; ++p)
       if (hipEventCreateWithFlags(&g_aux_events[dev][p], hipEventDisableTiming) != hipSuccess) return -1;
   }
   *events = g_aux_events[dev];
   if (g_aux_stream[dev][0] == nullptr) {
-    hipStream_t st[2] = {nullptr, nullptr};
-    for (int j = 0; j < 2; ++j)
+    hipStream_t st[3] = {nullptr, nullptr, nullptr};
+    for (int j = 0; j < 3; ++j)
       if (hipStreamCreateWithFlags(&st[j], hipStreamNonBlocking) != hipSuccess) return -1;
-    g_aux_stream[dev][0] = st[0];
-    g_aux_stream[dev][1] = st[1];
+    for (int j = 0; j < 3; ++j) g_aux_stream[dev][j] = st[j];
   }
   *sp = g_aux_stream[dev][0];
   *sr = g_aux_stream[dev][1];
+  *sm = g_aux_stream[dev][2];
   return 0;
 }
 
@@ -449,11 +462,11 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (P > 1 && (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)) P = 1;
     std::unique_lock<std::mutex> lk(g_aux_mu, std::defer_lock);
-    hipStream_t s2 = nullptr, s3 = nullptr;
+    hipStream_t s2 = nullptr, s3 = nullptr, s4 = nullptr;
     hipEvent_t* ev = nullptr;
     if (P > 1) {
       lk.lock();
-      if (aux_streams(&s2, &s3, &ev) != 0) {
+      if (aux_streams(&s2, &s3, &s4, &ev) != 0) {
         lk.unlock();
         P = 1;
       }
@@ -475,7 +488,10 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
       auto record = [&](hipEvent_t e, hipStream_t st) {
         if (rc == KAIROS_GDN_OK && hipEventRecord(e, st) != hipSuccess) rc = fail(KAIROS_GDN_EHIP, "hipEventRecord");
       };
-      // ev[p]: prepare p done; ev[kMaxParts + p]: recurrence part p about to be dispatched
+      // ev[p]: prepare p done; ev[kMaxParts + p]: recurrence part p about to be dispatched (its
+      // marker done); ev[2 kMaxParts + p]: recurrence part p done
+      const int mark = wide_mark_mode();
+      const bool beside = mark == 1;
       auto prepare = [&](int p, hipStream_t sp) {
         pa.it0 = bnd[p];
         pa.it_span = bnd[p + 1] - bnd[p];
@@ -486,8 +502,17 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
       prepare(0, s);
       for (int p = 0; p < P && rc == KAIROS_GDN_OK; ++p) {
         wait(s3, ev[p]);
-        if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_marker(s3), "marker");
-        record(ev[kMaxParts + p], s3);
+        if (p + 1 < P) {
+          if (beside) {                                   // the marker waits for what part p waits for
+            wait(s4, ev[p]);
+            if (p > 0) wait(s4, ev[2 * kMaxParts + p - 1]);
+            if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_marker(s4), "marker");
+            record(ev[kMaxParts + p], s4);
+          } else {
+            if (mark == 0 && rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_marker(s3), "marker");
+            record(ev[kMaxParts + p], s3);
+          }
+        }
         kgdn::WideFusedArgs fp = fa;
         fp.it_begin = bnd[p];
         fp.it_end = bnd[p + 1];
@@ -497,13 +522,14 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
         }
         if (p + 1 < P) fp.ht = st;
         if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_wide_fused(fp, V, s3), "wide fused recurrence");
+        if (beside && p + 2 < P) record(ev[2 * kMaxParts + p], s3);
         if (p + 1 < P) {
           wait(s2, ev[kMaxParts + p]);
           prepare(p + 1, s2);
         }
       }
-      record(ev[2 * kMaxParts], s3);                        // the caller's stream waits for the last part
-      wait(s, ev[2 * kMaxParts]);
+      record(ev[3 * kMaxParts], s3);                        // the caller's stream waits for the last part
+      wait(s, ev[3 * kMaxParts]);
       return rc;
     }
   }
