@@ -70,17 +70,26 @@ __device__ __forceinline__ Frag<TC> fzero() {
   return f;
 }
 
-// natural fragment of a row-major tensor in global memory (p = the lane's row start), or zeros
+// natural fragment of a row-major tensor in global memory (row = the lane's row start), or zeros
+// where !valid.  The load is issued unconditionally and masked after, so that the loads of
+// consecutive fragments go out together (a load in a branch of its own is waited for before the
+// next is issued): row must be readable, so callers clamp rows past the chunk's end to its first.
 template <typename TC>
 __device__ __forceinline__ Frag<TC> g_nat(const TC* row, int k0, bool valid) {
-  if (!valid) return fzero<TC>();
   const TC* p = row + k0 + 8 * (lane_id() >> 4);
   Frag<TC> f;
   if constexpr (sizeof(TC) == 2) {
-    f.v = *reinterpret_cast<const bf16x8*>(p);
+    uint4 x = *reinterpret_cast<const uint4*>(p);
+    x.x = valid ? x.x : 0u;
+    x.y = valid ? x.y : 0u;
+    x.z = valid ? x.z : 0u;
+    x.w = valid ? x.w : 0u;
+    f.v = __builtin_bit_cast(bf16x8, x);
   } else {
-    f.lo = *reinterpret_cast<const f32x4*>(p);
-    f.hi = *reinterpret_cast<const f32x4*>(p + 4);
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f.lo = valid ? lo : z;
+    f.hi = valid ? hi : z;
   }
   return f;
 }
@@ -749,7 +758,7 @@ __global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
   const TC* dv2 = reinterpret_cast<const TC*>(a.dv2);
   const int tr = 16 * wid + lc;                       // token of this lane's operand rows
   const bool tr_ok = tr < nv;
-  const TC* do_row = do_ + ((t0 + tr) * H + h) * (int64_t)V;
+  const TC* do_row = do_ + ((t0 + (tr_ok ? tr : 0)) * H + h) * (int64_t)V;
 
   // ---- ds = mask_{i>=j}(do v_new^T e^{g_i - g_j}) scale; ds2 = ds * q k^T -> dg row and column sums
   float rowp[4] = {0.f, 0.f, 0.f, 0.f};
@@ -757,7 +766,7 @@ __global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f}, aqk = {0.f, 0.f, 0.f, 0.f};
     if (tj <= wid) {
       const int tv = 16 * tj + lc;
-      const TC* vn_row = vn + ((t0 + tv) * H + h) * (int64_t)V;
+      const TC* vn_row = vn + ((t0 + (tv < nv ? tv : 0)) * H + h) * (int64_t)V;
       for (int vs = 0; vs < V / 32; ++vs) mma(acc, g_nat<TC>(do_row, 32 * vs, tr_ok), g_nat<TC>(vn_row, 32 * vs, tv < nv));
 #pragma unroll
       for (int ks = 0; ks < K / 32; ++ks) mma(aqk, t_nat<TC>(s_q, K, 16 * wid, 32 * ks), t_nat<TC>(s_k, K, 16 * tj, 32 * ks));
@@ -787,8 +796,8 @@ __global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
   // ---- per 16-row tile of K: dq, dk, -dw for this wave's 16 tokens
   const TC* hp = reinterpret_cast<const TC*>(a.h) + (c * H + h) * (int64_t)K * V;
   const TC* dhp = reinterpret_cast<const TC*>(a.dh) + (c * H + h) * (int64_t)K * V;
-  const TC* vn_row = vn + ((t0 + tr) * H + h) * (int64_t)V;
-  const TC* dv2_row = dv2 + ((t0 + tr) * H + h) * (int64_t)V;
+  const TC* vn_row = vn + ((t0 + (tr_ok ? tr : 0)) * H + h) * (int64_t)V;
+  const TC* dv2_row = dv2 + ((t0 + (tr_ok ? tr : 0)) * H + h) * (int64_t)V;
   const int t = tr;                                   // output token of this lane (column lc of the tiles)
   const float eg = gexp(s_g[t]) * a.scale;
   const float gate = t < nv ? gexp(gl - s_g[t]) : 0.f;
@@ -949,15 +958,18 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
       for (int ks = 0; ks < K / 32; ++ks)
         mma(acc, t_nat<TC>(s_dw, K, 16 * wid, 32 * ks), fscale<TC>(t_nat<TC>(s_k, K, 16 * tj, 32 * ks), fk));
       // this tile's v rows: every fragment's load in flight before the products
-      const TC* vrow = v + ((t0 + j) * H + h) * (int64_t)V;
+      const TC* vrow = v + ((t0 + (j < nv ? j : 0)) * H + h) * (int64_t)V;
       constexpr int NVF = sizeof(TC) == 2 ? 16 : 4;     // V / 32 at most (bf16 V <= 512, fp32 V <= 128)
+      // (raw loads in the V-guarded blocks, the mask of rows past the end applied at the products:
+      // a use of the value inside its block would wait for each load before the next is issued)
       Frag<TC> vf[NVF];
 #pragma unroll
       for (int vs = 0; vs < NVF; ++vs)
-        if (vs < V / 32) vf[vs] = g_nat<TC>(vrow, 32 * vs, j < nv);
+        if (vs < V / 32) vf[vs] = g_nat<TC>(vrow, 32 * vs, true);
+      const bool jv = j < nv;
 #pragma unroll
       for (int vs = 0; vs < NVF; ++vs)
-        if (vs < V / 32) mma(acc, t_nat<TC>(s_du, V, 16 * wid, 32 * vs), fscale<TC>(vf[vs], s_b[j]));
+        if (vs < V / 32) mma(acc, t_nat<TC>(s_du, V, 16 * wid, 32 * vs), fscale<TC>(jv ? vf[vs] : fzero<TC>(), s_b[j]));
     }
     const int j = 16 * tj + lc;
 #pragma unroll
@@ -1027,8 +1039,8 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   const TC* dk1 = reinterpret_cast<const TC*>(a.dk1);
   f32x4 d1s[K / 16];                                  // dk1 of this lane's token, all loads in flight at once
 #pragma unroll
-  for (int kt = 0; kt < K / 16; ++kt)
-    d1s[kt] = t < nv ? g_row4<TC>(dk1 + ((t0 + t) * H + h) * (int64_t)K + 16 * kt + 4 * lg) : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kt = 0; kt < K / 16; ++kt)                  // (rows past the end read row 0: dk is not stored there)
+    d1s[kt] = g_row4<TC>(dk1 + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)K + 16 * kt + 4 * lg);
 #pragma unroll
   for (int kt = 0; kt < K / 16; ++kt) {
     f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1, a3 = a1;
@@ -1061,8 +1073,8 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   for (int vt0 = 0; vt0 < V / 16; vt0 += 4) {
     f32x4 vv[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      vv[e] = t < nv ? g_row4<TC>(v + ((t0 + t) * H + h) * (int64_t)V + 16 * (vt0 + e) + 4 * lg) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < 4; ++e)                       // (rows past the end read row 0: their dbeta is not stored)
+      vv[e] = g_row4<TC>(v + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)V + 16 * (vt0 + e) + 4 * lg);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int vt = vt0 + e;

@@ -207,6 +207,22 @@ __device__ __forceinline__ void load8_in(const TK* p, float scale, float out[8])
   }
 }
 
+// Calls f(ld) with ld(off) reading entry off of an initial state that is fp32 or bf16 (dt 0 / 1),
+// or returning 0 without one: the dtype branch sits outside the caller's loops, so that all of
+// its loads go out together (a per-element branch waits for each load before the next).
+template <typename F>
+__device__ __forceinline__ void with_state_loader(const void* h0, int dt, F&& f) {
+  if (h0 == nullptr) {
+    f([](int64_t) { return 0.f; });
+  } else if (dt == 0) {
+    const float* p = reinterpret_cast<const float*>(h0);
+    f([p](int64_t off) { return p[off]; });
+  } else {
+    const bf16* p = reinterpret_cast<const bf16*>(h0);
+    f([p](int64_t off) { return (float)p[off]; });
+  }
+}
+
 // Load one scalar of a runtime-typed per-token array (g, beta): 0 = fp32, 1 = bf16.
 __device__ __forceinline__ float ld_scalar(const void* p, int64_t i, int dt) {
   return dt == 0 ? reinterpret_cast<const float*>(p)[i] : (float)reinterpret_cast<const bf16*>(p)[i];

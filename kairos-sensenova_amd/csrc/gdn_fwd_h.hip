@@ -188,19 +188,13 @@ __global__ __launch_bounds__(64 * HCfg<K>::NW) void fwd_h_kernel(FwdHArgs a, int
 
   // state slice: rows KW*wid + 16*tt + 4*lg + j, column v0 + lc
   f32x4 S[KT];
+  with_state_loader(a.h0, a.h0_dtype == DT_F32 ? 0 : 1, [&](auto ld) {
 #pragma unroll
-  for (int tt = 0; tt < KT; ++tt) {
+    for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x = 0.f;
-      if (a.h0) {
-        const int64_t off = (((int64_t)n * H + h) * K + KW * wid + 16 * tt + 4 * lg + j) * V + v0 + lc;
-        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
-                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
-      }
-      S[tt][j] = x;
-    }
-  }
+      for (int j = 0; j < 4; ++j)
+        S[tt][j] = ld((((int64_t)n * H + h) * K + KW * wid + 16 * tt + 4 * lg + j) * V + v0 + lc);
+  });
 
   ChunkPrefetch<TC, TK, K> cur, nxt;
   if (nchunks > 0) prefetch_chunk<TC, TK, K>(cur, a, c_first, bos, (int)min((int64_t)C, eos - bos), h, v0, wid, V);
@@ -421,19 +415,12 @@ __global__ __launch_bounds__(64 * WW) void fwd_h_wide_kernel(FwdHArgs a, int V, 
 
   // state: rows 16 kt + 4 lg + j, column vcol
   f32x4 S[16];
+  with_state_loader(active ? a.h0 : nullptr, a.h0_dtype == DT_F32 ? 0 : 1, [&](auto ld) {
 #pragma unroll
-  for (int kt = 0; kt < 16; ++kt) {
+    for (int kt = 0; kt < 16; ++kt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x = 0.f;
-      if (a.h0 && active) {
-        const int64_t off = (((int64_t)n * H + h) * WK + 16 * kt + 4 * lg + j) * V + vcol;
-        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
-                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
-      }
-      S[kt][j] = x;
-    }
-  }
+      for (int j = 0; j < 4; ++j) S[kt][j] = ld((((int64_t)n * H + h) * WK + 16 * kt + 4 * lg + j) * V + vcol);
+  });
 
   // two chunks of loads in flight: a chunk's loads are issued two steps before it is staged
   // (measured: with one step of distance the step waits on its global loads for most of its time)
@@ -676,18 +663,12 @@ __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs 
 
   // state: rows 16 tt + 4 lg + j, column vcol
   f32x4 S[KT];
+  with_state_loader(a.h0, a.h0_dtype == DT_F32 ? 0 : 1, [&](auto ld) {
 #pragma unroll
-  for (int tt = 0; tt < KT; ++tt)
+    for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x = 0.f;
-      if (a.h0) {
-        const int64_t off = (((int64_t)n * H + h) * K + 16 * tt + 4 * lg + j) * V + vcol;
-        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
-                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
-      }
-      S[tt][j] = x;
-    }
+      for (int j = 0; j < 4; ++j) S[tt][j] = ld((((int64_t)n * H + h) * K + 16 * tt + 4 * lg + j) * V + vcol);
+  });
 
   auto chunk_start = [&](int64_t it) { return bos + it * C; };
   auto chunk_len = [&](int64_t it) { return (int)min((int64_t)C, eos - chunk_start(it)); };

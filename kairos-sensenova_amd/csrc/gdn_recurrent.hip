@@ -120,15 +120,10 @@ __global__ __launch_bounds__(WAVE * kRecWaves) void fused_recurrent_kernel(RecAr
   // state rows kq*RK + j of column col
   float S[RK];
   const int64_t st0 = ((int64_t)n * a.HV + hv) * K * a.V + (int64_t)(kq * RK) * a.V + col;
+  with_state_loader(col_ok ? a.h0 : nullptr, a.h0_dtype == DT_F32 ? 0 : 1, [&](auto ld) {
 #pragma unroll
-  for (int j = 0; j < RK; ++j) {
-    float x = 0.f;
-    if (a.h0 && col_ok) {
-      const int64_t off = st0 + (int64_t)j * a.V;
-      x = a.h0_dtype == DT_F32 ? static_cast<const float*>(a.h0)[off] : (float)static_cast<const bf16*>(a.h0)[off];
-    }
-    S[j] = x;
-  }
+    for (int j = 0; j < RK; ++j) S[j] = ld(st0 + (int64_t)j * a.V);
+  });
 
   TokIn<TQ, TV, RK> cur, nxt;
   if (T > 0) load_token<TQ, TV, RK>(cur, a, bos, i_h, hv, col, col_ok, kq);

@@ -384,19 +384,23 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   const int vcol = v0 + lc;
   const int ra0 = 8 * (lc >> 2) + (lc & 3);               // rowA(0, lc)
   // state: S[kt][j] = S[32 (kt / 2) + 8 lg + 4 (kt % 2) + j][vcol] (the paired row order)
+  // (the dtype branch outside the loops, so that the 64 loads go out together)
   f32x4 S[16];
+  auto load_state = [&](auto ld) {
 #pragma unroll
-  for (int kt = 0; kt < 16; ++kt) {
+    for (int kt = 0; kt < 16; ++kt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x = 0.f;
-      if (a.h0) {
-        const int64_t off = (((int64_t)n * H + h) * FK + 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1) + j) * V + vcol;
-        x = a.h0_dtype == DT_F32 ? reinterpret_cast<const float*>(a.h0)[off]
-                                 : (float)reinterpret_cast<const bf16*>(a.h0)[off];
-      }
-      S[kt][j] = x;
-    }
+      for (int j = 0; j < 4; ++j)
+        S[kt][j] = ld((((int64_t)n * H + h) * FK + 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1) + j) * V + vcol);
+  };
+  if (a.h0 == nullptr) {
+    load_state([](int64_t) { return 0.f; });
+  } else if (a.h0_dtype == DT_F32) {
+    const float* h0 = reinterpret_cast<const float*>(a.h0);
+    load_state([h0](int64_t off) { return h0[off]; });
+  } else {
+    const bf16* h0 = reinterpret_cast<const bf16*>(a.h0);
+    load_state([h0](int64_t off) { return (float)h0[off]; });
   }
   FAddr A;
   f_addr(A, w_lds, k_lds, a_lds, v_lds);
