@@ -213,6 +213,38 @@ int kairos_gdn_fwd_o(const void* q, const void* k, const float* q_scale, const f
                      int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
                      int v_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- the same stages in the reference's layouts --------------------------
+ * u and v_new [B, T, H, V] as recompute_w_u_fwd and chunk_gated_delta_rule_fwd_h
+ * return them (wy_fast.py:213-248, chunk_delta_h.py:454-500); h [NCb, H, K, V],
+ * the reference's h [B, NT, H, K, V] (varlen: [1, NT, H, K, V]) in its first
+ * NT = number-of-real-chunks rows, zeros after them.  K and V multiples of 64.
+ * Workspace: kairos_gdn_stage_tokens_workspace_size(..., dtype = v's dtype);
+ * each call moves its operands between the two layouts at its boundary. */
+size_t kairos_gdn_stage_tokens_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs,
+                                              int dtype);
+
+/* kairos_gdn_prepare_wy with u [B, T, H, V] (wy_fast.py:213-248 recompute_w_u_fwd's u). */
+int kairos_gdn_prepare_wy_tokens(const void* k, const void* v, const void* g, const void* beta, const float* k_scale,
+                                 float* gc, void* w, void* u, float* A, void* Ai, const int64_t* cu_seqlens,
+                                 int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int k_dtype,
+                                 int v_dtype, int g_dtype, int beta_dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/* chunk_gated_delta_rule_fwd_h (chunk_delta_h.py:454-500) in its own layouts: u in, h and
+ * v_new (ungated) out as above; final_state [N, H, K, V] fp32 or NULL. */
+int kairos_gdn_fwd_h_tokens(const void* k, const float* k_scale, const void* w, const void* u, const float* gc,
+                            const void* initial_state, void* h, void* v_new, float* final_state,
+                            const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K,
+                            int64_t V, int k_dtype, int v_dtype, int h0_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* chunk_fwd_o (chunk_o.py:498-535) in its own layouts: h [NCb, H, K, V], v_new [B, T, H, V]
+ * in; o [B, T, H, V] in v's dtype. */
+int kairos_gdn_fwd_o_tokens(const void* q, const void* k, const float* q_scale, const float* k_scale, const void* h,
+                            const void* v_new, const float* gc, void* o, float scale, const int64_t* cu_seqlens,
+                            int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
+                            int v_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* l2norm_fwd (fla modules/l2norm.py:157-196), y = x / sqrt(sum x^2 + 1e-6) over
  * the last dim D (multiple of 8, <= 512), in x's dtype (fp32 or bf16). */
 int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream);

@@ -1168,6 +1168,144 @@ int kairos_gdn_fwd_o(const void* q, const void* k, const float* q_scale, const f
   return ok();
 }
 
+// ---- the same stages in the reference's layouts: u and v_new [B, T, H, V], h [NCb, H, K, V] ----
+// Each converts at its boundary (gdn_layout.hip) and runs the stage above on its own layout in the
+// workspace: [stage chunk map | uT | hT | vnT].
+namespace {
+
+size_t tokens_ws(const Geometry& G, int cdt) {
+  const size_t es = dt_size(cdt);
+  const size_t tiles = (size_t)G.nc * G.H * G.V * kgdn::C * es;
+  return stage_ws(G.n_seqs) + 2 * align_up(tiles) + align_up((size_t)G.nc * G.H * G.K * G.V * es);
+}
+
+int check_tokens(const Geometry& G, int cdt, size_t workspace_bytes, const char* what) {
+  if (G.K % 64 != 0 || G.V % 64 != 0)
+    return fail(KAIROS_GDN_EINVAL, "%s: K and V must be multiples of 64", what);
+  if (workspace_bytes < tokens_ws(G, cdt)) return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace too small", what);
+  return KAIROS_GDN_OK;
+}
+
+struct TokensWs {
+  void *uT, *hT, *vnT;
+};
+
+TokensWs carve_tokens(const Geometry& G, int cdt, void* workspace) {
+  const size_t es = dt_size(cdt);
+  Carver cv{static_cast<char*>(workspace)};
+  cv.take(stage_ws(G.n_seqs));
+  TokensWs t;
+  t.uT = cv.take((size_t)G.nc * G.H * G.V * kgdn::C * es);
+  t.hT = cv.take((size_t)G.nc * G.H * G.K * G.V * es);
+  t.vnT = cv.take((size_t)G.nc * G.H * G.V * kgdn::C * es);
+  return t;
+}
+
+}  // namespace
+
+size_t kairos_gdn_stage_tokens_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs,
+                                              int dtype) {
+  if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0 || !valid_scalar_dt(dtype)) return 0;
+  Geometry G{B, T, H, K, V, n_seqs, n_seqs > 0 ? n_seqs : B, chunks_bound(B, T, n_seqs), n_seqs > 0};
+  return tokens_ws(G, dtype);
+}
+
+int kairos_gdn_prepare_wy_tokens(const void* k, const void* v, const void* g, const void* beta, const float* k_scale,
+                                 float* gc, void* w, void* u, float* A, void* Ai, const int64_t* cu_seqlens,
+                                 int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int k_dtype,
+                                 int v_dtype, int g_dtype, int beta_dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  const char* what = "kairos_gdn_prepare_wy_tokens";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(k_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix k=%d v=%d", what, k_dtype, v_dtype);
+  if (int rc = check_tokens(G, cdt, workspace_bytes, what)) return rc;
+  if (G.nc == 0) return ok();
+  if (!u) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  const TokensWs t = carve_tokens(G, cdt, workspace);
+  if (int rc = kairos_gdn_prepare_wy(k, v, g, beta, k_scale, gc, w, t.uT, A, Ai, cu_seqlens, n_seqs, B, T, H, K, V,
+                                     k_dtype, v_dtype, g_dtype, beta_dtype, workspace, stage_ws(n_seqs), stream))
+    return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t* chunk_off = G.varlen ? static_cast<const int32_t*>(workspace) : nullptr;   // built by the stage
+  if (int rc = from_launch(kgdn::launch_chunk_tiles(t.uT, u, 0, (int)dt_size(cdt), cu_seqlens, chunk_off, (int)G.N,
+                                                    T, (int)H, (int)V, G.nc, s),
+                           what))
+    return rc;
+  return ok();
+}
+
+int kairos_gdn_fwd_h_tokens(const void* k, const float* k_scale, const void* w, const void* u, const float* gc,
+                            const void* initial_state, void* h, void* v_new, float* final_state,
+                            const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K,
+                            int64_t V, int k_dtype, int v_dtype, int h0_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_fwd_h_tokens";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(k_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix k=%d v=%d", what, k_dtype, v_dtype);
+  if (int rc = check_tokens(G, cdt, workspace_bytes, what)) return rc;
+  if (G.nc > 0 && (!u || !h || !v_new)) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  const TokensWs t = carve_tokens(G, cdt, workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int es = (int)dt_size(cdt);
+  if (G.nc > 0) {
+    Carver cv{static_cast<char*>(workspace)};
+    const int32_t* chunk_off = nullptr;
+    if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+    if (int rc = from_launch(kgdn::launch_chunk_tiles(u, t.uT, 1, es, cu_seqlens, chunk_off, (int)G.N, T, (int)H,
+                                                      (int)V, G.nc, s),
+                             what))
+      return rc;
+  }
+  if (int rc = kairos_gdn_fwd_h(k, k_scale, w, t.uT, gc, initial_state, t.hT, t.vnT, final_state, cu_seqlens, n_seqs,
+                                B, T, H, K, V, k_dtype, v_dtype, h0_dtype, workspace, stage_ws(n_seqs), stream))
+    return rc;
+  if (G.nc == 0) return ok();
+  const int32_t* chunk_off = G.varlen ? static_cast<const int32_t*>(workspace) : nullptr;
+  if (int rc = from_launch(kgdn::launch_state_tiles(t.hT, h, es, cu_seqlens, chunk_off, (int)G.N, T, (int)H, (int)V,
+                                                    (int)K, G.nc, s),
+                           what))
+    return rc;
+  if (int rc = from_launch(kgdn::launch_chunk_tiles(t.vnT, v_new, 0, es, cu_seqlens, chunk_off, (int)G.N, T, (int)H,
+                                                    (int)V, G.nc, s),
+                           what))
+    return rc;
+  return ok();
+}
+
+int kairos_gdn_fwd_o_tokens(const void* q, const void* k, const float* q_scale, const float* k_scale, const void* h,
+                            const void* v_new, const float* gc, void* o, float scale, const int64_t* cu_seqlens,
+                            int64_t n_seqs, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int qk_dtype,
+                            int v_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "kairos_gdn_fwd_o_tokens";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  if (cdt < 0) return fail(KAIROS_GDN_EINVAL, "%s: unsupported dtype mix q/k=%d v=%d", what, qk_dtype, v_dtype);
+  if (int rc = check_tokens(G, cdt, workspace_bytes, what)) return rc;
+  if (G.nc == 0) return ok();
+  if (!h || !v_new) return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  const TokensWs t = carve_tokens(G, cdt, workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int es = (int)dt_size(cdt);
+  Carver cv{static_cast<char*>(workspace)};
+  const int32_t* chunk_off = nullptr;
+  if (int rc = chunk_map(G, cu_seqlens, cv, &chunk_off, s)) return rc;
+  if (int rc = from_launch(kgdn::launch_state_tiles(h, t.hT, es, cu_seqlens, chunk_off, (int)G.N, T, (int)H, (int)K,
+                                                    (int)V, G.nc, s),
+                           what))
+    return rc;
+  if (int rc = from_launch(kgdn::launch_chunk_tiles(v_new, t.vnT, 1, es, cu_seqlens, chunk_off, (int)G.N, T, (int)H,
+                                                    (int)V, G.nc, s),
+                           what))
+    return rc;
+  return kairos_gdn_fwd_o(q, k, q_scale, k_scale, t.hT, t.vnT, gc, o, scale, cu_seqlens, n_seqs, B, T, H, K, V,
+                          qk_dtype, v_dtype, workspace, stage_ws(n_seqs), stream);
+}
+
 int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream) {
   const char* what = "kairos_gdn_l2norm_fwd";
   if (rows < 0 || D <= 0 || D % 8 != 0 || D > 512)

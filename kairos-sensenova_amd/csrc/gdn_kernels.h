@@ -226,6 +226,13 @@ int launch_fwd_h(const FwdHArgs& a, int compute_dtype, int k_dtype, int K, int V
 int launch_fwd_o(const FwdOArgs& a, int compute_dtype, int qk_dtype, int K, int V, int64_t nc_grid,
                  hipStream_t s);
 bool seg_fwd_supported(int compute_dtype, int K, int V);
+// Layout moves of the reference-layout stage entry points (gdn_layout.hip): token rows
+// [B*T, H, D] <-> per-chunk transposed tiles [NCb, H, D, 64] (to_tiles selects the
+// direction), and per-chunk states [NCb, H, R, S] -> [NCb, H, S, R].  D, R, S multiples of 64.
+int launch_chunk_tiles(const void* src, void* dst, int to_tiles, int elem_bytes, const int64_t* cu,
+                       const int32_t* chunk_off, int N, int64_t T, int H, int D, int64_t nc_grid, hipStream_t s);
+int launch_state_tiles(const void* src, void* dst, int elem_bytes, const int64_t* cu, const int32_t* chunk_off, int N,
+                       int64_t T, int H, int R, int S, int64_t nc_grid, hipStream_t s);
 int launch_seg_fwd(const SegFwdArgs& a, int compute_dtype, int qk_dtype, int K, int V, hipStream_t s);
 int launch_seg_map(const int64_t* cu, int N, int L, int32_t* chunk_off, int32_t* seg_off, hipStream_t s);
 // Segments as sequences for the stage kernels (the backward), from the geometry fields of a

@@ -10,8 +10,10 @@ from .chunk import (
     CHUNK,
     ChunkGatedDeltaRuleFunction,
     chunk_gated_delta_rule,
+    chunk_fwd_o,
     chunk_gated_delta_rule_bwd,
     chunk_gated_delta_rule_fwd,
+    chunk_gated_delta_rule_fwd_h,
     chunk_gated_delta_rule_gated_norm,
     chunk_local_cumsum,
     fwd_h,
@@ -19,6 +21,7 @@ from .chunk import (
     l2norm_fwd,
     num_chunks_bound,
     prepare_wy,
+    recompute_w_u_fwd,
 )
 from .norm import FusedRMSNormGated, rms_norm_gated, rms_norm_gated_fwd
 from .recurrent import FusedRecurrentFunction, fused_recurrent_gated_delta_rule, fused_recurrent_gated_delta_rule_fwd
@@ -27,8 +30,8 @@ from . import swap
 
 __all__ = [
     "CHUNK", "ChunkGatedDeltaRuleFunction", "KairosGdnError", "LIB_PATH", "chunk_gated_delta_rule",
-    "chunk_gated_delta_rule_bwd", "chunk_gated_delta_rule_fwd", "chunk_gated_delta_rule_gated_norm", "chunk_local_cumsum", "fwd_h", "fwd_o", "l2norm_fwd", "num_chunks_bound",
-    "prepare_wy", "swap", "FusedRMSNormGated", "rms_norm_gated", "rms_norm_gated_fwd",
+    "chunk_fwd_o", "chunk_gated_delta_rule_bwd", "chunk_gated_delta_rule_fwd_h", "chunk_gated_delta_rule_fwd", "chunk_gated_delta_rule_gated_norm", "chunk_local_cumsum", "fwd_h", "fwd_o", "l2norm_fwd", "num_chunks_bound",
+    "prepare_wy", "recompute_w_u_fwd", "swap", "FusedRMSNormGated", "rms_norm_gated", "rms_norm_gated_fwd",
     "FusedRecurrentFunction", "fused_recurrent_gated_delta_rule", "fused_recurrent_gated_delta_rule_fwd",
     "ShortConvolution", "causal_conv1d", "gdn_gates",
 ]

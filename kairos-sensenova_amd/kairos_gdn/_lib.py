@@ -49,6 +49,13 @@ SIGNATURES = {
                               _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _sz, _p]),
     "kairos_gdn_fwd_o": (_i, [_p, _p, _fp, _fp, _p, _p, _fp, _p, _f, _p, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i, _i, _p, _sz, _p]),
+    "kairos_gdn_stage_tokens_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i]),
+    "kairos_gdn_prepare_wy_tokens": (_i, [_p, _p, _p, _p, _fp, _fp, _p, _p, _fp, _p, _p, _i64,
+                                          _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _i, _p, _sz, _p]),
+    "kairos_gdn_fwd_h_tokens": (_i, [_p, _fp, _p, _p, _fp, _p, _p, _p, _fp, _p, _i64,
+                                     _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _sz, _p]),
+    "kairos_gdn_fwd_o_tokens": (_i, [_p, _p, _fp, _fp, _p, _p, _fp, _p, _f, _p, _i64,
+                                     _i64, _i64, _i64, _i64, _i64, _i, _i, _p, _sz, _p]),
     "kairos_gdn_l2norm_fwd": (_i, [_p, _p, _i, _i64, _i64, _p]),
     "kairos_gdn_rms_norm_gated": (_i, [_p, _p, _p, _p, _p, _fp, _i, _i, _i, _i64, _i64, _f, _i, _p]),
     "kairos_gdn_fused_recurrent_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _fp, _p, _i64, _i64, _i64, _i64,

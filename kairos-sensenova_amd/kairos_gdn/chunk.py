@@ -407,6 +407,89 @@ def fwd_o(q, k, hT, vnT, gc, scale=None, cu_seqlens=None, q_scale=None, k_scale=
     return o
 
 
+def _tokens_ws(ref, cu_seqlens, T, H, K, V, dtype):
+    dev, cu, n_seqs, _, _ = _stage_setup(ref, cu_seqlens, T)
+    B = ref.shape[0]
+    nbytes = _lib.load().kairos_gdn_stage_tokens_workspace_size(B, T, H, K, V, n_seqs, _lib_dtype(dtype))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    return dev, cu, n_seqs, ws, nbytes
+
+
+def _lib_dtype(dtype):
+    return {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}[dtype]
+
+
+def recompute_w_u_fwd(k, v, g, beta, cu_seqlens=None, k_scale=None):
+    """Fused cumsum + K.K^T + (I+A)^-1 + w/u with u in the reference's layout.
+
+    Returns (gc [B,T,H] fp32, w [B,T,H,K], u [B,T,H,V]): wy_fast.py:213-248's w and u, from
+    raw gates (the cumsum, chunk_scaled_dot_kkt_fwd and solve_tril stages fused in front).
+    """
+    _require_device(k, v, g, beta)
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    k, v, g, beta = (x.contiguous() for x in (k, v, g, beta))
+    dev, cu, n_seqs, ws, wsb = _tokens_ws(k, cu_seqlens, T, H, K, V, v.dtype)
+    gc = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    w = torch.empty(B, T, H, K, device=dev, dtype=v.dtype)
+    u = torch.empty(B, T, H, V, device=dev, dtype=v.dtype)
+    ks = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+    _lib.call("kairos_gdn_prepare_wy_tokens", _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(ks), _ptr(gc), _ptr(w),
+              _ptr(u), None, None, _ptr(cu), n_seqs, B, T, H, K, V, _code(k, "k"), _code(v, "v"), _code(g, "g"),
+              _code(beta, "beta"), _ptr(ws), wsb, _stream(dev))
+    return gc, w, u
+
+
+def chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state=None, output_final_state=False, cu_seqlens=None,
+                                 k_scale=None):
+    """State recurrence in the reference's layouts (fla ops/common/chunk_delta_h.py:454-500).
+
+    g is the chunk-local cumsum of the gates (fp32), as the reference passes it.  Returns
+    (h [NCb,H,K,V], v_new [B,T,H,V], final_state [N,H,K,V] fp32 or None); h's first NT rows
+    (the real chunks, sequence-major) are the reference's h [B, NT, H, K, V] flattened, the
+    rest zeros.
+    """
+    _require_device(k, w, u, g, initial_state)
+    B, T, H, K = k.shape
+    V = u.shape[-1]
+    dev, cu, n_seqs, ws, wsb = _tokens_ws(k, cu_seqlens, T, H, K, V, w.dtype)
+    nc = num_chunks_bound(B, T, n_seqs)
+    N = n_seqs if cu is not None else B
+    h = torch.empty(nc, H, K, V, device=dev, dtype=w.dtype)
+    v_new = torch.empty(B, T, H, V, device=dev, dtype=w.dtype)
+    ht = torch.empty(N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
+    h0 = initial_state.contiguous() if initial_state is not None else None
+    h0_dt = _code(h0, "initial_state") if h0 is not None else _lib.F32
+    ks = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+    _lib.call("kairos_gdn_fwd_h_tokens", _ptr(k.contiguous()), _ptr(ks), _ptr(w.contiguous()), _ptr(u.contiguous()),
+              _ptr(g.contiguous()), _ptr(h0), _ptr(h), _ptr(v_new), _ptr(ht), _ptr(cu), n_seqs, B, T, H, K, V,
+              _code(k, "k"), _code(w, "w"), h0_dt, _ptr(ws), wsb, _stream(dev))
+    return h, v_new, ht
+
+
+def chunk_fwd_o(q, k, v, h, g, scale=None, cu_seqlens=None, q_scale=None, k_scale=None):
+    """Output stage in the reference's layouts (fla ops/common/chunk_o.py:498-535).
+
+    v is v_new [B,T,H,V], h [NCb,H,K,V] as chunk_gated_delta_rule_fwd_h returns it, g the
+    cumsummed gates; o [B,T,H,V] in v's dtype.
+    """
+    _require_device(q, k, v, h, g)
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if scale is None:
+        scale = K ** -0.5
+    dev, cu, n_seqs, ws, wsb = _tokens_ws(q, cu_seqlens, T, H, K, V, v.dtype)
+    if h.shape[0] < num_chunks_bound(B, T, n_seqs):
+        raise ValueError(f"h holds {h.shape[0]} chunks; {num_chunks_bound(B, T, n_seqs)} are expected")
+    o = torch.empty(B, T, H, V, device=dev, dtype=v.dtype)
+    qs = q_scale.to(device=dev, dtype=torch.float32).contiguous() if q_scale is not None else None
+    ks = k_scale.to(device=dev, dtype=torch.float32).contiguous() if k_scale is not None else None
+    _lib.call("kairos_gdn_fwd_o_tokens", _ptr(q.contiguous()), _ptr(k.contiguous()), _ptr(qs), _ptr(ks),
+              _ptr(h.contiguous()), _ptr(v.contiguous()), _ptr(g.contiguous()), _ptr(o), float(scale), _ptr(cu),
+              n_seqs, B, T, H, K, V, _code(q, "q"), _code(v, "v"), _ptr(ws), wsb, _stream(dev))
+    return o
+
+
 def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """Row L2 normalisation (fla modules/l2norm.py:157-196); eps is fixed at 1e-6."""
     if eps != 1e-6:

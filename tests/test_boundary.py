@@ -124,6 +124,31 @@ def test_stage_abi_rejects_invalid_arguments():
     assert rc == _lib.EWORKSPACE
 
 
+def test_reference_layout_stage_abi_workspace_and_errors():
+    """The reference-layout stages size their workspace as stage map + uT + hT + vnT, and reject
+    head dims that are not multiples of 64 and short workspaces before touching the device."""
+    lib = _lib.load()
+    B, T, H, K, V = 2, 130, 3, 128, 64
+    nc = lib.kairos_gdn_num_chunks_bound(B, T, 0)
+    al = lambda x: (x + 255) // 256 * 256
+    want = 2 * al(nc * H * V * 64 * 2) + al(nc * H * K * V * 2)
+    assert lib.kairos_gdn_stage_tokens_workspace_size(B, T, H, K, V, 0, _lib.BF16) == want
+    n_seqs = 3
+    nc_v = lib.kairos_gdn_num_chunks_bound(1, T, n_seqs)
+    want_v = al(4 * (n_seqs + 1)) + 2 * al(nc_v * H * V * 64 * 4) + al(nc_v * H * K * V * 4)
+    assert lib.kairos_gdn_stage_tokens_workspace_size(1, T, H, K, V, n_seqs, _lib.F32) == want_v
+    assert lib.kairos_gdn_stage_tokens_workspace_size(1, T, H, K, V, 0, _lib.F8E4M3) == 0
+    rc = lib.kairos_gdn_fwd_h_tokens(FAKE, None, FAKE, FAKE, FAKE, None, FAKE, FAKE, None, None, 0, 1, 64, 1, 96, 64,
+                                     _lib.BF16, _lib.BF16, _lib.F32, FAKE, 1 << 30, None)
+    assert rc == _lib.EINVAL and b"multiples of 64" in lib.kairos_gdn_last_error()
+    rc = lib.kairos_gdn_fwd_o_tokens(FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0.1, None, 0, 1, 64, 1, 64, 64,
+                                     _lib.BF16, _lib.BF16, FAKE, 16, None)
+    assert rc == _lib.EWORKSPACE and b"workspace" in lib.kairos_gdn_last_error()
+    rc = lib.kairos_gdn_prepare_wy_tokens(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, None, None, None, 0, 1, 64, 1,
+                                          64, 64, _lib.F32, _lib.BF16, _lib.F32, _lib.F32, FAKE, 1 << 30, None)
+    assert rc == _lib.EINVAL and b"dtype mix" in lib.kairos_gdn_last_error()
+
+
 # ---------------------------------------------------------------------------
 # Python host mirror: the reference's checks and messages (chunk.py:292-310)
 # ---------------------------------------------------------------------------

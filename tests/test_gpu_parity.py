@@ -184,6 +184,55 @@ def test_fwd_h_and_fwd_o_stages(dt, B, T, H, K, V, cu, with_h0):
     assert rel(host(o), o_r) < TOL[dt]["o"]
 
 
+@pytest.mark.parametrize("dt,B,T,H,K,V,cu,with_h0", H_CASES)
+def test_reference_layout_stages(dt, B, T, H, K, V, cu, with_h0):
+    """recompute_w_u_fwd / chunk_gated_delta_rule_fwd_h / chunk_fwd_o in the reference's layouts:
+    u, v_new [B,T,H,V] and h [NT,H,K,V] compared with the oracle's intermediates as they are,
+    with no layout helper of the tests in between; h's slack chunks are zeros and the layout
+    moves are exact (the tokens form equals the tiled form bit for bit)."""
+    note(f"reference-layout stages {dt} B={B} T={T} H={H} K={K} V={V} cu={cu} h0={with_h0}")
+    x = make_inputs(B, T, H, K, V, seed=11 * T + K, dtype=dt, n_states=len(cu) - 1 if cu else None,
+                    h0_scale=0.02 if with_h0 else 0.0)
+    cu_np = np.array(cu) if cu else None
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
+    o_r, ht_r, inter = O.chunk_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["h0"],
+                                                output_final_state=True, cu_seqlens=cu_np, dtype=dt,
+                                                return_intermediates=True)
+    cm = O.ChunkMap(B, T, cu_np)
+    d = to_dev(x, dt)
+    gc, w, u = kairos_gdn.recompute_w_u_fwd(d["k"], d["v"], d["g"], d["beta"], cu_seqlens=cu_t)
+    _, w2, uT, _, _ = kairos_gdn.prepare_wy(d["k"], d["v"], d["g"], d["beta"], cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert torch.equal(w, w2)
+    ncb = kairos_gdn.num_chunks_bound(B, T, len(cu) - 1 if cu else 0)
+    assert np.array_equal(host(u), chunk_T_to_tokens(host(uT), cm))
+    assert rel(host(u), inter["u"]) < TOL[dt]["mid"]
+    # the recurrence fed the oracle's own w, u (reference layouts)
+    gc_r = dev(inter["gc"])
+    h, v_new, ht = kairos_gdn.chunk_gated_delta_rule_fwd_h(d["k"], dev(inter["w"], TDT[dt]), dev(inter["u"], TDT[dt]),
+                                                           gc_r, initial_state=d["h0"], output_final_state=True,
+                                                           cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert tuple(h.shape) == (ncb, H, K, V)
+    assert rel(host(h)[:cm.nc], inter["h"]) < TOL[dt]["mid"]
+    assert np.all(host(h)[cm.nc:] == 0)
+    assert rel(host(v_new), inter["v_new"]) < TOL[dt]["mid"]
+    assert rel(host(ht), ht_r) < TOL[dt]["ht"]
+    hT, vnT, _ = kairos_gdn.fwd_h(d["k"], dev(inter["w"], TDT[dt]),
+                                  dev(tokens_to_chunk_T(inter["u"], cm, ncb), TDT[dt]), gc_r,
+                                  initial_state=d["h0"], cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(h)[:cm.nc], np.swapaxes(host(hT)[:cm.nc], 2, 3))
+    assert np.array_equal(host(v_new), chunk_T_to_tokens(host(vnT), cm))
+    # the output stage fed the oracle's own h and v_new (reference layouts)
+    h_r = np.zeros((ncb, H, K, V), np.float32)
+    h_r[:cm.nc] = inter["h"]
+    o = kairos_gdn.chunk_fwd_o(d["q"], d["k"], dev(inter["v_new"], TDT[dt]), dev(h_r, TDT[dt]), gc_r,
+                               cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert rel(host(o), o_r) < TOL[dt]["o"]
+
+
 @pytest.mark.parametrize("dt,B,T,H,K,V,cu,with_h0", [c for c in H_CASES if c[0] == "bf16" and c[4] <= 128])
 def test_fwd_h_split_k_form(dt, B, T, H, K, V, cu, with_h0, monkeypatch):
     """bf16 K, V <= 128 run the all-columns recurrence; KAIROS_GDN_FWD_H_COLS=0 selects the split-K form,
