@@ -327,7 +327,7 @@ size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_s
 // shapes the fused kernels do not cover: fp32, and the Kairos model's head dims
 // K = 256, V = 512 (any K in {64, 128, 256} with V a multiple of 16).
 // The pipelined form of the fused K = 256 path: the chunks of every sequence are cut into P parts
-// (5 by default, growing by 1.3 along the sequence);
+// (4 by default, growing by 1.4 along the sequence);
 // the prepare kernel of part p + 1 runs on a second stream while the recurrence walks part p (whose
 // 64-column workgroups leave CUs idle: 160 of 256 at the Kairos layer shape), the state passing
 // between parts through an fp32 buffer.  KAIROS_GDN_WIDE_PIPE sets P (1: one prepare, then one
@@ -341,7 +341,7 @@ constexpr int kMaxParts = 16;
 
 int wide_pipe_parts() {
   const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE");
-  if (e == nullptr) return 5;
+  if (e == nullptr) return 4;
   const int p = std::atoi(e);
   return p < 1 ? 1 : p > kMaxParts ? kMaxParts : p;
 }
@@ -351,7 +351,7 @@ int wide_pipe_parts() {
 // the CUs the recurrence leaves, still finishes within the previous recurrence part.
 double wide_pipe_growth() {
   const char* e = std::getenv("KAIROS_GDN_WIDE_PIPE_GROWTH");
-  if (e == nullptr) return 1.3;
+  if (e == nullptr) return 1.4;
   const double g = std::atof(e);
   return g < 0.25 ? 0.25 : g > 4.0 ? 4.0 : g;
 }
