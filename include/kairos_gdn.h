@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define KAIROS_GDN_ABI_VERSION 1
+#define KAIROS_GDN_ABI_VERSION 2
 
 #define KAIROS_GDN_F32 0
 #define KAIROS_GDN_BF16 1
@@ -246,8 +246,10 @@ int kairos_gdn_fwd_o_tokens(const void* q, const void* k, const float* q_scale, 
                             int v_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* l2norm_fwd (fla modules/l2norm.py:157-196), y = x / sqrt(sum x^2 + 1e-6) over
- * the last dim D (multiple of 8, <= 512), in x's dtype (fp32 or bf16). */
-int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream);
+ * the last dim D (multiple of 8, <= 512), in x's dtype (fp32 or bf16), and, if
+ * rstd is not null, rstd = 1 / sqrt(sum x^2 + 1e-6) per row in fp32 (the
+ * reference returns (y, rstd)). */
+int kairos_gdn_l2norm_fwd(const void* x, void* y, float* rstd, int dtype, int64_t rows, int64_t D, void* stream);
 
 /* ---- output epilogue -------------------------------------------------------
  * Gated RMSNorm of the GatedDeltaNet layer's output (o_norm = FusedRMSNormGated,

@@ -374,7 +374,7 @@ void wide_pipe_bounds(int64_t nt, int P, double growth, int64_t* b) {
 
 std::mutex g_aux_mu;                                     // held while a pipelined call enqueues its work
 hipStream_t g_aux_stream[64][3] = {};
-hipEvent_t g_aux_events[64][3 * kMaxParts + 1] = {};
+hipEvent_t g_aux_events[64][3 * kMaxParts + 3] = {};   // + 3 join events
 
 // What releases prepare p + 1 (KAIROS_GDN_WIDE_PIPE_MARK): 0, a one-workgroup marker kernel on the
 // recurrence stream just before part p; 1, that marker on a stream of its own once recurrence part
@@ -395,7 +395,7 @@ int aux_streams(hipStream_t* sp, hipStream_t* sr, hipStream_t* sm, hipEvent_t** 
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
   if (g_aux_events[dev][0] == nullptr) {
-    for (int p = 0; p < 3 * kMaxParts + 1; ++p)
+    for (int p = 0; p < 3 * kMaxParts + 3; ++p)
       if (hipEventCreateWithFlags(&g_aux_events[dev][p], hipEventDisableTiming) != hipSuccess) return -1;
   }
   *events = g_aux_events[dev];
@@ -528,8 +528,22 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
           prepare(p + 1, s2);
         }
       }
-      record(ev[3 * kMaxParts], s3);                        // the caller's stream waits for the last part
-      wait(s, ev[3 * kMaxParts]);
+      // Join, also after a failed launch or event call above: the caller's stream waits for all
+      // that was queued on the library streams (prepares on s2, recurrence parts on s3, markers on
+      // s4), so the caller may release the workspace once its own stream has passed this point.
+      // If the join itself cannot be enqueued, the library streams are drained on the host.
+      const hipStream_t lib_streams[3] = {s2, s3, s4};
+      bool joined = true;
+      for (int j = 0; j < 3; ++j) {
+        if (j == 2 && !beside) continue;                    // s4 carries work only with markers beside
+        const hipEvent_t e = ev[3 * kMaxParts + j];
+        if (hipEventRecord(e, lib_streams[j]) != hipSuccess || hipStreamWaitEvent(s, e, 0) != hipSuccess)
+          joined = false;
+      }
+      if (!joined) {
+        for (int j = 0; j < 3; ++j) (void)hipStreamSynchronize(lib_streams[j]);
+        if (rc == KAIROS_GDN_OK) rc = fail(KAIROS_GDN_EHIP, "joining the pipelined forward's streams failed");
+      }
       return rc;
     }
   }
@@ -1306,7 +1320,7 @@ int kairos_gdn_fwd_o_tokens(const void* q, const void* k, const float* q_scale, 
                           qk_dtype, v_dtype, workspace, stage_ws(n_seqs), stream);
 }
 
-int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64_t D, void* stream) {
+int kairos_gdn_l2norm_fwd(const void* x, void* y, float* rstd, int dtype, int64_t rows, int64_t D, void* stream) {
   const char* what = "kairos_gdn_l2norm_fwd";
   if (rows < 0 || D <= 0 || D % 8 != 0 || D > 512)
     return fail(KAIROS_GDN_EINVAL, "%s: D must be a positive multiple of 8, at most 512", what);
@@ -1314,7 +1328,10 @@ int kairos_gdn_l2norm_fwd(const void* x, void* y, int dtype, int64_t rows, int64
   if (rows == 0) return ok();
   if (!x || !y || !aligned16(x) || !aligned16(y))
     return fail(KAIROS_GDN_EINVAL, "%s: x and y must be non-null and 16-byte aligned", what);
-  if (int rc = from_launch(kgdn::launch_l2norm(x, y, dtype, rows, (int)D, static_cast<hipStream_t>(stream)), what))
+  if (rstd != nullptr && reinterpret_cast<uintptr_t>(rstd) % 4 != 0)
+    return fail(KAIROS_GDN_EINVAL, "%s: rstd must be 4-byte aligned", what);
+  if (int rc = from_launch(kgdn::launch_l2norm(x, y, rstd, dtype, rows, (int)D, static_cast<hipStream_t>(stream)),
+                           what))
     return rc;
   return ok();
 }

@@ -46,7 +46,12 @@ template <typename T> __device__ __forceinline__ float round_to(float x) { retur
 
 // Four OCP fp8 e4m3 ("fn") codes packed in a dword (byte i = element i) -> four floats, exact.
 // gfx950 decodes the OCP format in hardware, two codes per v_cvt_pk_f32_fp8 (sign, 4-bit exponent of
-// bias 7, 3-bit mantissa, subnormals at exponent 0, 0x7f / 0xff NaN).
+// bias 7, 3-bit mantissa, subnormals at exponent 0, 0x7f / 0xff NaN).  The same instruction decodes
+// the FNUZ format (bias 8, one NaN) on earlier targets, so device code for any other target is
+// refused here rather than decoding with another meaning.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "kairos_gdn device code is written for gfx950 (OCP fp8 decode, 16-bit transposed LDS reads)"
+#endif
 __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float out[4]) {
   const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);    // bytes 0, 1
   const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);     // bytes 2, 3

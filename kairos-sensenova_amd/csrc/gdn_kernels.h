@@ -249,7 +249,7 @@ int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float*
 // F [ns_grid, H, K, V], the dh each segment's last chunk starts from, and dh0 [N, H, K, V] (or null).
 int launch_seg_bwd_combine(const SegFwdArgs& p, const float* Bseg, const float* dht, float* F, float* dh0, int K,
                            int V, hipStream_t s);
-int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s);
+int launch_l2norm(const void* x, void* y, float* rstd, int dtype, int64_t rows, int D, hipStream_t s);
 // the same for two tensors of equal shape in one launch (x1, y1 may be null)
 int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,
                    hipStream_t s);

@@ -18,13 +18,16 @@ namespace {
 // (8 elements, one 16-byte load each in bf16), so a wave normalises 64 / LPR rows
 // at once and every lane is busy; each thread handles RPT row groups, their loads
 // all issued before the first reduction.  Up to two tensors per launch
-// (blockIdx.y), each with its own rows.
+// (blockIdx.y), each with its own rows.  rstd (fp32 per row) is written where
+// its pointer is not null (l2norm.py:115-119 returns it beside y).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void l2norm_kernel(const T* __restrict__ x0, T* __restrict__ y0,
-                                                     const T* __restrict__ x1, T* __restrict__ y1, int64_t rows) {
+                                                     const T* __restrict__ x1, T* __restrict__ y1,
+                                                     float* __restrict__ r0, int64_t rows) {
   constexpr int LPR = D / 8, RPW = WAVE / LPR, RPT = 4;
   const T* x = blockIdx.y ? x1 : x0;
   T* y = blockIdx.y ? y1 : y0;
+  float* r = blockIdx.y ? nullptr : r0;
   const int l = lane_id();
   const int64_t wave = ((int64_t)blockIdx.x * 4 + threadIdx.x / WAVE) * RPT;
   const int sub = l / LPR, col = 8 * (l % LPR);
@@ -51,14 +54,15 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const T* __restrict__ x0, T
 #pragma unroll
       for (int e = 0; e < 8; ++e) vset<T>(o, e, vget<T>(v[i], e) * rstd);
       st8<T>(y + row * D + col, o);
+      if (r != nullptr && col == 0) r[row] = rstd;
     }
   }
 }
 
 // Rows of any D (a multiple of 8, at most 512): one wave per row.
 template <typename T>
-__global__ __launch_bounds__(256) void l2norm_wave_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
-                                                          int D) {
+__global__ __launch_bounds__(256) void l2norm_wave_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                          float* __restrict__ r, int64_t rows, int D) {
   const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / WAVE;
   if (row >= rows) return;
   const int l = lane_id();
@@ -80,6 +84,7 @@ __global__ __launch_bounds__(256) void l2norm_wave_kernel(const T* __restrict__ 
     for (int e = 0; e < 8; ++e) vset<T>(o, e, vget<T>(v, e) * rstd);
     st8<T>(y + row * D + 8 * l, o);
   }
+  if (r != nullptr && l == 0) r[row] = rstd;
 }
 
 __global__ void chunk_off_kernel(const int64_t* __restrict__ cu, int N, int32_t* __restrict__ off) {
@@ -111,27 +116,28 @@ __global__ __launch_bounds__(64) void cumsum_kernel(const void* g, int g_dtype, 
 }  // namespace
 
 template <typename T, int D>
-void launch_l2norm_t(const void* x0, void* y0, const void* x1, void* y1, int64_t rows, hipStream_t s) {
+void launch_l2norm_t(const void* x0, void* y0, const void* x1, void* y1, float* r0, int64_t rows, hipStream_t s) {
   constexpr int64_t per_block = 4 * 4 * (WAVE / (D / 8));     // waves x row groups x rows per group
   const dim3 grid((unsigned)((rows + per_block - 1) / per_block), x1 ? 2u : 1u);
   hipLaunchKernelGGL((l2norm_kernel<T, D>), grid, dim3(256), 0, s, static_cast<const T*>(x0), static_cast<T*>(y0),
-                     static_cast<const T*>(x1), static_cast<T*>(y1), rows);
+                     static_cast<const T*>(x1), static_cast<T*>(y1), r0, rows);
 }
 
 template <typename T>
-int launch_l2norm_dt(const void* x0, void* y0, const void* x1, void* y1, int64_t rows, int D, hipStream_t s) {
+int launch_l2norm_dt(const void* x0, void* y0, const void* x1, void* y1, float* r0, int64_t rows, int D,
+                     hipStream_t s) {
   switch (D) {
-    case 64: launch_l2norm_t<T, 64>(x0, y0, x1, y1, rows, s); break;
-    case 128: launch_l2norm_t<T, 128>(x0, y0, x1, y1, rows, s); break;
-    case 256: launch_l2norm_t<T, 256>(x0, y0, x1, y1, rows, s); break;
-    case 512: launch_l2norm_t<T, 512>(x0, y0, x1, y1, rows, s); break;
+    case 64: launch_l2norm_t<T, 64>(x0, y0, x1, y1, r0, rows, s); break;
+    case 128: launch_l2norm_t<T, 128>(x0, y0, x1, y1, r0, rows, s); break;
+    case 256: launch_l2norm_t<T, 256>(x0, y0, x1, y1, r0, rows, s); break;
+    case 512: launch_l2norm_t<T, 512>(x0, y0, x1, y1, r0, rows, s); break;
     default: {
       const dim3 grid((unsigned)((rows + 3) / 4));
       hipLaunchKernelGGL(l2norm_wave_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x0), static_cast<T*>(y0),
-                         rows, D);
+                         r0, rows, D);
       if (x1)
         hipLaunchKernelGGL(l2norm_wave_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x1),
-                           static_cast<T*>(y1), rows, D);
+                           static_cast<T*>(y1), nullptr, rows, D);
     }
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -140,13 +146,16 @@ int launch_l2norm_dt(const void* x0, void* y0, const void* x1, void* y1, int64_t
 int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,
                    hipStream_t s) {
   if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
-  if (dtype == DT_F32) return launch_l2norm_dt<float>(x0, y0, x1, y1, rows, D, s);
-  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x0, y0, x1, y1, rows, D, s);
+  if (dtype == DT_F32) return launch_l2norm_dt<float>(x0, y0, x1, y1, nullptr, rows, D, s);
+  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x0, y0, x1, y1, nullptr, rows, D, s);
   return -2;
 }
 
-int launch_l2norm(const void* x, void* y, int dtype, int64_t rows, int D, hipStream_t s) {
-  return launch_l2norm2(x, y, nullptr, nullptr, dtype, rows, D, s);
+int launch_l2norm(const void* x, void* y, float* rstd, int dtype, int64_t rows, int D, hipStream_t s) {
+  if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
+  if (dtype == DT_F32) return launch_l2norm_dt<float>(x, y, nullptr, nullptr, rstd, rows, D, s);
+  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x, y, nullptr, nullptr, rstd, rows, D, s);
+  return -2;
 }
 
 int launch_chunk_offsets(const int64_t* cu, int N, int32_t* chunk_off, hipStream_t s) {

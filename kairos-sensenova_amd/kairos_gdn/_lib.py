@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 F32, BF16, F8E4M3 = 0, 1, 2
 ACT_SWISH, ACT_SIGMOID = 0, 1
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, EHIP = 0, 1, 2, 3, 4
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # every symbol the header declares, with (restype, argtypes)
 _p = ctypes.c_void_p
@@ -56,7 +56,7 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _sz, _p]),
     "kairos_gdn_fwd_o_tokens": (_i, [_p, _p, _fp, _fp, _p, _p, _fp, _p, _f, _p, _i64,
                                      _i64, _i64, _i64, _i64, _i64, _i, _i, _p, _sz, _p]),
-    "kairos_gdn_l2norm_fwd": (_i, [_p, _p, _i, _i64, _i64, _p]),
+    "kairos_gdn_l2norm_fwd": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
     "kairos_gdn_rms_norm_gated": (_i, [_p, _p, _p, _p, _p, _fp, _i, _i, _i, _i64, _i64, _f, _i, _p]),
     "kairos_gdn_fused_recurrent_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _fp, _p, _i64, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p]),

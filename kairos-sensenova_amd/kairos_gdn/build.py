@@ -18,7 +18,11 @@ INCLUDE_DIR = os.path.join(os.path.dirname(os.path.dirname(PKG_DIR)), "include")
 BUILD_DIR = os.path.join(os.path.dirname(PKG_DIR), "_build")
 LIB_NAME = "libkairos_gdn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-ARCH = os.environ.get("KAIROS_GDN_ARCH", "gfx950")
+# gfx950 only: the kernels use its OCP fp8 decode, 16-bit transposed LDS reads and 160 KB of LDS
+# per CU (gdn_common.hpp also refuses device code for any other target).
+ARCH = "gfx950"
+if os.environ.get("KAIROS_GDN_ARCH", ARCH) != ARCH:
+    raise RuntimeError(f"KAIROS_GDN_ARCH={os.environ['KAIROS_GDN_ARCH']}: libkairos_gdn is built for gfx950 only")
 
 # -packed-fp32-ops: keep the compiler from forming packed fp32 VALU ops (the
 # host pass warns that it does not know the feature; that is harmless).

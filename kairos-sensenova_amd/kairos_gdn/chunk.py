@@ -67,20 +67,28 @@ def _prepare_cu_seqlens(cu_seqlens: torch.Tensor, device: torch.device, T: int) 
     calls .tolist(), fla/ops/utils/index.py:118, cached by identity in
     fla/utils.py:96-133); the same check here guards the kernels against
     offsets outside [0, T].  The cache key includes the tensor's version
-    counter, so an in-place edit of a reused buffer is checked again.
+    counter, so an in-place edit of a reused buffer is checked again.  A tensor
+    made under ``torch.inference_mode()`` has no version counter: it is checked
+    on every call.
     """
     global _validated_cu
     cu = cu_seqlens
     if cu.dim() != 1 or cu.numel() < 2:
         raise ValueError("cu_seqlens must be a 1-D tensor with at least two entries")
-    key = (cu_seqlens, cu_seqlens._version, T)
-    if (_validated_cu is None or _validated_cu[0] is not key[0] or _validated_cu[1] != key[1]
+    version = None
+    if not cu_seqlens.is_inference():
+        try:
+            version = cu_seqlens._version
+        except RuntimeError:                      # no version counter to key on
+            version = None
+    key = (cu_seqlens, version, T)
+    if (version is None or _validated_cu is None or _validated_cu[0] is not key[0] or _validated_cu[1] != key[1]
             or _validated_cu[2] != key[2]):
         vals = cu.detach().to("cpu", torch.int64)
         if int(vals[0]) != 0 or int(vals[-1]) != T or bool((vals[1:] < vals[:-1]).any()):
             raise ValueError(
                 f"cu_seqlens must start at 0, end at T={T} and be non-decreasing (got {vals.tolist()[:8]}...)")
-        _validated_cu = key
+        _validated_cu = key if version is not None else None
     return cu.to(device=device, dtype=torch.int64).contiguous()
 
 
@@ -101,8 +109,11 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_fi
     """One native call: [q/k L2 norm] -> prepare -> state recurrence -> output.
 
     Mirrors chunk_gated_delta_rule_fwd (chunk.py:16-67) plus the optional
-    in-kernel L2 norm of ChunkGatedDeltaRuleFunction.forward (chunk.py:168-170).
-    Returns (o in v's dtype, final_state fp32 or None).  ``_norm`` (gate,
+    in-kernel L2 norm of ChunkGatedDeltaRuleFunction.forward (chunk.py:168-170),
+    with the same positional arguments.  Returns (o in v's dtype, final_state
+    fp32 or None); the reference returns (g, o, A, final_state), the cumsummed
+    gates and A being its saved intermediates, which this library recomputes
+    in the backward instead of keeping.  ``_norm`` (gate,
     weight, bias, eps, activation code) turns o into the layer's gated RMSNorm
     of o (chunk_gated_delta_rule_gated_norm).
     """
@@ -201,13 +212,16 @@ def chunk_gated_delta_rule_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch
                                       _norm=(gate, norm_weight, norm_bias, eps, _NORM_ACT[activation]))
 
 
-def chunk_gated_delta_rule_bwd(q, k, v, g, beta, scale, initial_state, do, dht, cu_seqlens=None,
-                               use_qk_l2norm_in_kernel=False):
+def chunk_gated_delta_rule_bwd_native(q, k, v, g, beta, scale, initial_state, do, dht, cu_seqlens=None,
+                                      use_qk_l2norm_in_kernel=False):
     """One native call: gradients of chunk_gated_delta_rule (chunk.py:70-146, 188-213).
 
-    q and k are the forward's own inputs (before the optional in-op L2 norm,
-    which the library recomputes, as it recomputes gc, Ai, w, u, h and v_new).
-    Returns (dq, dk, dv, dg fp32, dbeta, dh0 fp32 or None).
+    Not the reference's ``chunk_gated_delta_rule_bwd(q, k, v, g, beta, A, ...)``,
+    which takes the cumsummed gates and the forward's A: here ``g`` is the raw
+    log-space gate and q, k are the forward's own inputs (before the optional
+    in-op L2 norm); the library recomputes the norm, gc, Ai, w, u, h and v_new.
+    Returns (dq, dk, dv, dbeta, dg fp32, dh0 fp32 or None), the reference's
+    order (chunk.py:146).
     """
     dev = _require_device(q, k, v, g, beta, initial_state, do, dht)
     B, T, H, K = q.shape
@@ -240,7 +254,7 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, scale, initial_state, do, dht, 
     _lib.call("kairos_gdn_chunk_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(h0), _ptr(do), _ptr(dht_),
               _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(db), _ptr(dh0), _ptr(cu), n_seqs, B, T, H, K, V, qk_dt,
               v_dt, g_dt, b_dt, h0_dt, float(scale), l2, _ptr(ws), ws_bytes, _stream(dev))
-    return dq, dk, dv, dg, db, dh0
+    return dq, dk, dv, db, dg, dh0
 
 
 class ChunkGatedDeltaRuleFunction(torch.autograd.Function):
@@ -265,8 +279,8 @@ class ChunkGatedDeltaRuleFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do, dht):
         q, k, v, g, beta, initial_state, cu_seqlens = ctx.saved_tensors
-        dq, dk, dv, dg, db, dh0 = chunk_gated_delta_rule_bwd(q, k, v, g, beta, ctx.scale, initial_state, do, dht,
-                                                             cu_seqlens, ctx.use_qk_l2norm_in_kernel)
+        dq, dk, dv, db, dg, dh0 = chunk_gated_delta_rule_bwd_native(q, k, v, g, beta, ctx.scale, initial_state, do,
+                                                                    dht, cu_seqlens, ctx.use_qk_l2norm_in_kernel)
         return dq.to(q), dk.to(k), dv.to(v), dg.to(g), db.to(beta), None, dh0, None, None, None, None, None
 
 
@@ -327,10 +341,19 @@ def num_chunks_bound(B: int, T: int, n_seqs: int = 0) -> int:
     return int(_lib.load().kairos_gdn_num_chunks_bound(B, T, n_seqs))
 
 
-def chunk_local_cumsum(g: torch.Tensor, chunk_size: int = CHUNK, cu_seqlens=None) -> torch.Tensor:
-    """Chunk-local prefix sum of scalar gates (fla ops/utils/cumsum.py:247-279), fp32 out."""
+def chunk_local_cumsum(g: torch.Tensor, chunk_size: int = CHUNK, reverse: bool = False, scale: float = None,
+                       cu_seqlens=None, head_first: bool = False, output_dtype: torch.dtype | None = torch.float,
+                       **kwargs) -> torch.Tensor:
+    """Chunk-local prefix sum of scalar gates (fla ops/utils/cumsum.py:425-462, scalar form
+    :247-279), fp32 out; the reference's arguments in its order.  Built: chunk_size 64, forward
+    direction, no scale, [B, T, H] layout, fp32 output; anything else raises."""
     if chunk_size != CHUNK:
         raise ValueError("only chunk_size=64 is built")
+    if reverse or scale is not None or head_first or output_dtype not in (None, torch.float32):
+        raise NotImplementedError("chunk_local_cumsum: only reverse=False, scale=None, head_first=False and an fp32 "
+                                  "output are built")
+    if g.dim() != 3:
+        raise NotImplementedError("chunk_local_cumsum: only scalar gates [B, T, H] are built")
     _require_device(g)
     B, T, H = g.shape
     g = g.contiguous()
@@ -419,12 +442,21 @@ def _lib_dtype(dtype):
     return {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}[dtype]
 
 
-def recompute_w_u_fwd(k, v, g, beta, cu_seqlens=None, k_scale=None):
+def recompute_w_u_fwd(k, v, beta=None, A=None, g=None, cu_seqlens=None, *, g_raw=None, k_scale=None):
     """Fused cumsum + K.K^T + (I+A)^-1 + w/u with u in the reference's layout.
 
-    Returns (gc [B,T,H] fp32, w [B,T,H,K], u [B,T,H,V]): wy_fast.py:213-248's w and u, from
-    raw gates (the cumsum, chunk_scaled_dot_kkt_fwd and solve_tril stages fused in front).
+    The reference (wy_fast.py:213-248) takes A = (I+A)^-1 and the cumsummed g from
+    earlier stages; this stage forms both itself from the raw log-space gates, which are
+    passed as the keyword ``g_raw``.  A call in the reference's form (A or g given) raises
+    instead of reading its arguments with another meaning.  Returns (gc [B,T,H] fp32,
+    w [B,T,H,K], u [B,T,H,V]).
     """
+    if A is not None or g is not None:
+        raise NotImplementedError("recompute_w_u_fwd forms A and the cumsummed gates itself: pass the raw gates as "
+                                  "g_raw= and no A / g")
+    if beta is None or g_raw is None:
+        raise TypeError("recompute_w_u_fwd needs beta and g_raw")
+    g = g_raw
     _require_device(k, v, g, beta)
     B, T, H, K = k.shape
     V = v.shape[-1]
@@ -440,15 +472,24 @@ def recompute_w_u_fwd(k, v, g, beta, cu_seqlens=None, k_scale=None):
     return gc, w, u
 
 
-def chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state=None, output_final_state=False, cu_seqlens=None,
+def chunk_gated_delta_rule_fwd_h(k, w, u, g=None, gk=None, initial_state=None, output_final_state=False,
+                                 chunk_size: int = CHUNK, save_new_value: bool = True, cu_seqlens=None, *,
                                  k_scale=None):
-    """State recurrence in the reference's layouts (fla ops/common/chunk_delta_h.py:454-500).
+    """State recurrence in the reference's layouts and argument order
+    (fla ops/common/chunk_delta_h.py:454-500).
 
-    g is the chunk-local cumsum of the gates (fp32), as the reference passes it.  Returns
-    (h [NCb,H,K,V], v_new [B,T,H,V], final_state [N,H,K,V] fp32 or None); h's first NT rows
-    (the real chunks, sequence-major) are the reference's h [B, NT, H, K, V] flattened, the
-    rest zeros.
+    g is the chunk-local cumsum of the gates (fp32), as the reference passes it; per-key
+    gates (gk) and chunk sizes other than 64 are not built and raise.  Returns
+    (h [NCb,H,K,V], v_new [B,T,H,V] or None without save_new_value, final_state [N,H,K,V]
+    fp32 or None); h's first NT rows (the real chunks, sequence-major) are the reference's
+    h [B, NT, H, K, V] flattened, the rest zeros.
     """
+    if gk is not None:
+        raise NotImplementedError("chunk_gated_delta_rule_fwd_h: per-key gates (gk) are not built")
+    if chunk_size != CHUNK:
+        raise ValueError("only chunk_size=64 is built")
+    if g is None:
+        raise NotImplementedError("chunk_gated_delta_rule_fwd_h: the scalar gates g are required")
     _require_device(k, w, u, g, initial_state)
     B, T, H, K = k.shape
     V = u.shape[-1]
@@ -464,15 +505,23 @@ def chunk_gated_delta_rule_fwd_h(k, w, u, g, initial_state=None, output_final_st
     _lib.call("kairos_gdn_fwd_h_tokens", _ptr(k.contiguous()), _ptr(ks), _ptr(w.contiguous()), _ptr(u.contiguous()),
               _ptr(g.contiguous()), _ptr(h0), _ptr(h), _ptr(v_new), _ptr(ht), _ptr(cu), n_seqs, B, T, H, K, V,
               _code(k, "k"), _code(w, "w"), h0_dt, _ptr(ws), wsb, _stream(dev))
-    return h, v_new, ht
+    return h, (v_new if save_new_value else None), ht
 
 
-def chunk_fwd_o(q, k, v, h, g, scale=None, cu_seqlens=None, q_scale=None, k_scale=None):
-    """Output stage in the reference's layouts (fla ops/common/chunk_o.py:498-535).
+def chunk_fwd_o(q, k, v, h, g=None, g_gamma=None, scale=None, cu_seqlens=None, chunk_size: int = CHUNK, *,
+                q_scale=None, k_scale=None):
+    """Output stage in the reference's layouts and argument order (fla ops/common/chunk_o.py:498-535).
 
     v is v_new [B,T,H,V], h [NCb,H,K,V] as chunk_gated_delta_rule_fwd_h returns it, g the
-    cumsummed gates; o [B,T,H,V] in v's dtype.
+    cumsummed gates; o [B,T,H,V] in v's dtype.  Per-head constant decays (g_gamma) and chunk
+    sizes other than 64 are not built and raise.
     """
+    if g_gamma is not None:
+        raise NotImplementedError("chunk_fwd_o: g_gamma is not built")
+    if chunk_size != CHUNK:
+        raise ValueError("only chunk_size=64 is built")
+    if g is None:
+        raise NotImplementedError("chunk_fwd_o: the scalar gates g are required")
     _require_device(q, k, v, h, g)
     B, T, H, K = q.shape
     V = v.shape[-1]
@@ -490,13 +539,19 @@ def chunk_fwd_o(q, k, v, h, g, scale=None, cu_seqlens=None, q_scale=None, k_scal
     return o
 
 
-def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """Row L2 normalisation (fla modules/l2norm.py:157-196); eps is fixed at 1e-6."""
+def l2norm_fwd(x: torch.Tensor, eps: float = 1e-6, output_dtype: torch.dtype | None = None):
+    """Row L2 normalisation (fla modules/l2norm.py:157-196): returns (y, rstd) as the reference
+    does, y in x's dtype, rstd fp32 of shape x.shape[:-1].  eps is fixed at 1e-6 and y keeps
+    x's dtype; other values raise."""
     if eps != 1e-6:
         raise ValueError("only eps=1e-6 is built (the reference default)")
+    if output_dtype not in (None, x.dtype):
+        raise NotImplementedError("l2norm_fwd: the output keeps x's dtype")
     _require_device(x)
     x = x.contiguous()
     y = torch.empty_like(x)
     D = x.shape[-1]
-    _lib.call("kairos_gdn_l2norm_fwd", _ptr(x), _ptr(y), _code(x, "x"), x.numel() // D, D, _stream(x.device))
-    return y
+    rstd = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
+    _lib.call("kairos_gdn_l2norm_fwd", _ptr(x), _ptr(y), _ptr(rstd), _code(x, "x"), x.numel() // D, D,
+              _stream(x.device))
+    return y, rstd

@@ -114,7 +114,7 @@ def test_c_abi_rejects_invalid_arguments(over, code, msg):
 
 def test_stage_abi_rejects_invalid_arguments():
     lib = _lib.load()
-    rc = lib.kairos_gdn_l2norm_fwd(FAKE, FAKE, _lib.BF16, 10, 100, None)
+    rc = lib.kairos_gdn_l2norm_fwd(FAKE, FAKE, None, _lib.BF16, 10, 100, None)
     assert rc == _lib.EINVAL and b"multiple of 8" in lib.kairos_gdn_last_error()
     rc = lib.kairos_gdn_fwd_o(FAKE, FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 0.1, None, 0, 1, 64, 1, 64, 64,
                               _lib.F8E4M3, _lib.BF16, None, 0, None)
@@ -185,6 +185,21 @@ def test_cu_seqlens_checked_again_after_in_place_edit():
         ch._prepare_cu_seqlens(cu, torch.device("cpu"), 20)
 
 
+def test_cu_seqlens_made_under_inference_mode():
+    """A tensor made under torch.inference_mode() has no version counter: the host check runs on every
+    call instead of failing on the missing counter, and still catches a bad edit."""
+    from kairos_gdn import chunk as ch
+    with torch.inference_mode():
+        cu = torch.tensor([0, 8, 16])
+        assert ch._prepare_cu_seqlens(cu, torch.device("cpu"), 16).tolist() == [0, 8, 16]
+        assert ch._prepare_cu_seqlens(cu, torch.device("cpu"), 16).tolist() == [0, 8, 16]
+        cu[1] = 40
+        with pytest.raises(ValueError, match="non-decreasing"):
+            ch._prepare_cu_seqlens(cu, torch.device("cpu"), 16)
+    cu2 = torch.tensor([0, 4, 16])                      # an ordinary tensor after it is still cached and checked
+    assert ch._prepare_cu_seqlens(cu2, torch.device("cpu"), 16).tolist() == [0, 4, 16]
+
+
 def test_head_first_warns_and_cpu_tensors_are_refused():
     q, k, v, g, b = cpu_inputs()
     with warnings.catch_warnings(record=True) as rec:
@@ -204,7 +219,7 @@ def test_stages_refuse_cpu_tensors():
 def test_backward_refuses_cpu_tensors_and_fp8():
     q, k, v, g, b = cpu_inputs()
     with pytest.raises(RuntimeError, match="HIP device only"):
-        kairos_gdn.chunk_gated_delta_rule_bwd(q, k, v, g, b, 0.125, None, torch.randn(1, 16, 2, 64), None)
+        kairos_gdn.chunk_gated_delta_rule_bwd_native(q, k, v, g, b, 0.125, None, torch.randn(1, 16, 2, 64), None)
     lib = _lib.load()
     x = 16
     rc = lib.kairos_gdn_chunk_bwd(x, x, x, x, x, None, x, None, x, x, x, x, x, None, None, 0, 1, 64, 2, 64, 64,

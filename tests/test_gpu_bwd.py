@@ -35,12 +35,12 @@ def run_case(B, T, H, K, V, seed, dtype="bf16", cu=None, h0=True, dht=True, l2=F
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     dev = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dt)  # noqa: E731
     cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
-    got = kairos_gdn.chunk_gated_delta_rule_bwd(
+    dq, dk, dv, db, dg, dh0 = kairos_gdn.chunk_gated_delta_rule_bwd_native(
         dev(x["q"], tdt), dev(x["k"], tdt), dev(x["v"], tdt), dev(x["g"], torch.float32), dev(x["beta"], tdt),
         K ** -0.5, dev(x["h0"], torch.float32) if h0 else None, dev(do, tdt),
         dev(dht_, torch.float32) if dht else None, cu_t, l2)
     torch.cuda.synchronize()
-    got = [g_.float().cpu().numpy() if g_ is not None else None for g_ in got]
+    got = [g_.float().cpu().numpy() if g_ is not None else None for g_ in (dq, dk, dv, dg, db, dh0)]
     sel = (lambda a: a[:, :, heads]) if heads is not None else (lambda a: a)
     sel_s = (lambda a: a[:, heads]) if heads is not None else (lambda a: a)
     ref = OB.chunk_gated_delta_rule_bwd(sel(x["q"]), sel(x["k"]), sel(x["v"]), sel(x["g"]), sel(x["beta"]), sel(do),
@@ -160,8 +160,8 @@ def test_autograd_matches_direct_call():
     do = torch.randn(o.shape, generator=gen).to("cuda", bf)
     dht = torch.randn(ht.shape, generator=gen).to("cuda")
     torch.autograd.backward([o, ht], [do, dht])
-    direct = kairos_gdn.chunk_gated_delta_rule_bwd(*(leaves[n].detach() for n in ("q", "k", "v", "g", "beta")),
-                                                   K ** -0.5, leaves["h0"].detach(), do, dht)
-    for n, d in zip(("q", "k", "v", "g", "beta", "h0"), direct):
+    direct = kairos_gdn.chunk_gated_delta_rule_bwd_native(*(leaves[n].detach() for n in ("q", "k", "v", "g", "beta")),
+                                                          K ** -0.5, leaves["h0"].detach(), do, dht)
+    for n, d in zip(("q", "k", "v", "beta", "g", "h0"), direct):
         assert leaves[n].grad is not None and leaves[n].grad.dtype == leaves[n].dtype, n
         assert torch.equal(leaves[n].grad, d.to(leaves[n].dtype)), n

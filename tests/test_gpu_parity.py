@@ -79,9 +79,12 @@ def test_l2norm(dt):
     note(f"l2norm {dt}")
     rng = np.random.default_rng(0)
     x = O.cast(rng.standard_normal((3, 777, 128)).astype(np.float32) * 3, dt)
-    y = host(kairos_gdn.l2norm_fwd(dev(x, TDT[dt])))
+    y, rstd = kairos_gdn.l2norm_fwd(dev(x, TDT[dt]))
     ref = O.l2norm(x, dtype=dt)
-    assert rel(y, ref) < (4e-3 if dt == "bf16" else 1e-6)
+    assert rel(host(y), ref) < (4e-3 if dt == "bf16" else 1e-6)
+    assert tuple(rstd.shape) == x.shape[:-1] and rstd.dtype == torch.float32
+    rs_ref = 1.0 / np.sqrt((x.astype(np.float64) ** 2).sum(-1) + 1e-6)
+    assert rel(host(rstd), rs_ref) < 1e-6
 
 
 @pytest.mark.parametrize("cu", [None, [0, 1, 64, 65, 200, 330]])
@@ -200,7 +203,7 @@ def test_reference_layout_stages(dt, B, T, H, K, V, cu, with_h0):
                                                 return_intermediates=True)
     cm = O.ChunkMap(B, T, cu_np)
     d = to_dev(x, dt)
-    gc, w, u = kairos_gdn.recompute_w_u_fwd(d["k"], d["v"], d["g"], d["beta"], cu_seqlens=cu_t)
+    gc, w, u = kairos_gdn.recompute_w_u_fwd(d["k"], d["v"], d["beta"], g_raw=d["g"], cu_seqlens=cu_t)
     _, w2, uT, _, _ = kairos_gdn.prepare_wy(d["k"], d["v"], d["g"], d["beta"], cu_seqlens=cu_t)
     torch.cuda.synchronize()
     assert torch.equal(w, w2)

@@ -173,6 +173,39 @@ def test_gpu_short_convolution_module_prefill_then_decode():
 
 
 @pytest.mark.gpu
+def test_gpu_inference_mode_cu_seqlens():
+    """cu_seqlens made under torch.inference_mode() (no version counter), as a serving loop builds it:
+    the chunked forward and ShortConvolution both run and match the same calls with an ordinary tensor."""
+    import kairos_gdn
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    print("inference-mode cu_seqlens: chunk forward + ShortConvolution", flush=True)
+    torch.manual_seed(1)
+    T, H, K, D = 200, 2, 64, 128
+    cu_list = [0, 70, 71, 200]
+    q = torch.nn.functional.normalize(torch.randn(1, T, H, K), dim=-1).to("cuda", torch.bfloat16)
+    k = torch.nn.functional.normalize(torch.randn(1, T, H, K), dim=-1).to("cuda", torch.bfloat16)
+    v = torch.randn(1, T, H, K).to("cuda", torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn(1, T, H)).to("cuda")
+    beta = torch.sigmoid(torch.randn(1, T, H)).to("cuda", torch.bfloat16)
+    x = torch.randn(1, T, D).to("cuda", torch.bfloat16)
+    conv = kairos_gdn.ShortConvolution(D, 4, bias=False, activation="silu").to("cuda", torch.bfloat16)
+    cu_plain = torch.tensor(cu_list, dtype=torch.int64, device="cuda")
+    with torch.no_grad():
+        o_ref, _ = kairos_gdn.chunk_gated_delta_rule(q, k, v, g, beta, cu_seqlens=cu_plain)
+        y_ref, _ = conv(x, cu_seqlens=cu_plain)
+    with torch.inference_mode():
+        cu_inf = torch.tensor(cu_list, dtype=torch.int64, device="cuda")
+        assert cu_inf.is_inference()
+        for _ in range(2):                                    # the second call finds nothing cached
+            o, _ = kairos_gdn.chunk_gated_delta_rule(q, k, v, g, beta, cu_seqlens=cu_inf)
+            y, _ = conv(x, cu_seqlens=cu_inf)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref)
+    assert torch.equal(y, y_ref)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("bdt", ["bf16", "fp32"])
 def test_gpu_gates(bdt):
     import kairos_gdn

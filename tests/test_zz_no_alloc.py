@@ -4,7 +4,11 @@ It takes its scratch memory from the library's static device array instead of
 a caller workspace.  The GPU test calls it through the C ABI twice in a row,
 the second time on a smaller problem (so the array still holds the first
 call's contents), and checks each result bit-for-bit against
-kairos_gdn_chunk_fwd with a freshly allocated workspace on the same inputs.
+kairos_gdn_chunk_fwd with a freshly allocated workspace on the same inputs.  The cases cover each way the
+forward carves the array: the segment scan (bf16, K = V <= 128), the staged
+kernels at the model head dims (bf16, K = 256, V = 512, one part: no library
+streams) and the staged in-op L2 norm (fp32, K = V = 64), whose normalised q
+and k sit at the front of the array.
 The CPU test checks that a problem larger than the array is refused before
 any GPU work.
 """
@@ -16,15 +20,21 @@ from kairos_gdn import _lib
 from gdn_inputs import make_inputs
 
 
-def _problem(B, T, H, K, V, seed, cu=None):
+def _problem(B, T, H, K, V, seed, cu=None, dtype="bf16", l2=0):
     n_states = len(cu) - 1 if cu else B
-    x = make_inputs(B, T, H, K, V, seed=seed, dtype="bf16", n_states=n_states)
-    bf = torch.bfloat16
+    x = make_inputs(B, T, H, K, V, seed=seed, dtype=dtype, n_states=n_states)
+    if l2:                                   # unnormalised q, k: the op normalises them
+        rng = np.random.default_rng(seed + 1)
+        for n in ("q", "k"):
+            x[n] = x[n] * rng.uniform(0.5, 3.0, x[n].shape[:-1] + (1,)).astype(np.float32)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     dev = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dt)  # noqa: E731
-    d = dict(q=dev(x["q"], bf), k=dev(x["k"], bf), v=dev(x["v"], bf), g=dev(x["g"], torch.float32),
-             beta=dev(x["beta"], bf), h0=dev(x["h0"], torch.float32))
+    d = dict(q=dev(x["q"], tdt), k=dev(x["k"], tdt), v=dev(x["v"], tdt), g=dev(x["g"], torch.float32),
+             beta=dev(x["beta"], tdt), h0=dev(x["h0"], torch.float32))
     d["cu"] = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
     d["shape"] = (B, T, H, K, V, n_states)
+    d["dt"] = _lib.BF16 if dtype == "bf16" else _lib.F32
+    d["l2"] = l2
     return d
 
 
@@ -35,13 +45,14 @@ def _run(d, noalloc):
     ht = torch.full((N, H, K, V), float("nan"), dtype=torch.float32, device="cuda")
     P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     sp = torch.cuda.current_stream().cuda_stream
+    dt = d["dt"]
     args = (P(d["q"]), P(d["k"]), P(d["v"]), P(d["g"]), P(d["beta"]), None, None, P(d["h0"]), P(o), P(ht),
-            P(d["cu"]), n_seqs, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0)
+            P(d["cu"]), n_seqs, B, T, H, K, V, dt, dt, _lib.F32, dt, _lib.F32, K ** -0.5, d["l2"])
     if noalloc:
         _lib.call("kairos_gdn_chunk_fwd_noalloc", *args, sp)
     else:
         lib = _lib.load()
-        wsb = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, _lib.BF16, _lib.BF16, 0)
+        wsb = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, dt, dt, d["l2"])
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
         _lib.call("kairos_gdn_chunk_fwd", *args, P(ws), wsb, sp)
     torch.cuda.synchronize()
@@ -54,6 +65,12 @@ def test_noalloc_matches_chunk_fwd_on_two_calls():
         ("B=2 T=3000 H=4 K=V=128 (several segments per sequence)", _problem(2, 3000, 4, 128, 128, seed=71)),
         ("varlen T=700 H=2 K=V=64, cu=[0, 1, 300, 700] (smaller)",
          _problem(1, 700, 2, 64, 64, seed=72, cu=[0, 1, 300, 700])),
+        ("model head dims B=1 T=1100 H=2 K=256 V=512 (staged, fused recurrence)",
+         _problem(1, 1100, 2, 256, 512, seed=73)),
+        ("fp32 K=V=64 with the in-op L2 norm, varlen T=400 (staged, normalised q/k at the array's front)",
+         _problem(1, 400, 2, 64, 64, seed=74, cu=[0, 150, 151, 400], dtype="fp32", l2=1)),
+        ("bf16 K=V=128 with the in-op L2 norm T=500 (segment scan, smaller)", _problem(1, 500, 2, 128, 128, seed=75,
+                                                                                      l2=1)),
     ]
     for name, d in cases:
         print(f"noalloc vs chunk_fwd: {name}", flush=True)
