@@ -640,8 +640,12 @@ def bench_model_shape(args, dev):
     from kairos_gdn import _lib
     B, T, H, K, V = 1, args.T, 20, 256, 512
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20270, device=dev)
+    l2 = int(bool(args.l2norm))
+    if l2:          # the layer hands the op unnormalised q, k and asks it to normalise them
+        q = (q.float() * 3.0).to(torch.bfloat16)
+        k = (k.float() * 0.5).to(torch.bfloat16)
     lib = _lib.load()
-    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, l2)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     o = torch.empty_like(v)
     ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
@@ -650,7 +654,7 @@ def bench_model_shape(args, dev):
 
     def step():
         _lib.call("kairos_gdn_chunk_fwd", P(q), P(k), P(v), P(g), P(beta), None, None, P(h0), P(o), P(ht), None, 0,
-                  B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, P(ws), ws_bytes,
+                  B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, l2, P(ws), ws_bytes,
                   sp)
 
     timer = Timer(args)
@@ -660,18 +664,21 @@ def bench_model_shape(args, dev):
     alg = alg_bytes(B * T * H, B * H, K, V)
     tflops = B * T * H * flops_per_tok_head(K, V) / wall / 1e12
     print(json.dumps({
-        "metric": "GDN chunk-fwd tokens/s at the Kairos 4B layer shape T=32760,H=20,dk=256,dv=512", "value": T / wall,
+        "metric": "GDN chunk-fwd tokens/s at the Kairos 4B layer shape T=32760,H=20,dk=256,dv=512"
+                  + (" with use_qk_l2norm_in_kernel=True" if l2 else ""), "value": T / wall,
         "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"chunk_gated_delta_rule fwd B={B} T={T} H={H} dk={K} dv={V} chunk 64, bf16 "
-                               "q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM", "workspace_bytes": ws_bytes},
+                               "q/k/v/beta, fp32 g/h0, output_final_state, inputs in HBM"
+                               + (", use_qk_l2norm_in_kernel=True (unnormalised q, k)" if l2 else ""),
+                   "workspace_bytes": ws_bytes},
         **timer.fields(res),
         "tflops": tflops, "mfma_peak_frac": tflops / PEAK_BF16_TFLOPS,
         "hbm_gbs_whole_op": alg / wall / 1e9,
         "roofline": {"bound": "hbm", "kernel": "whole call (median step)", "achieved": alg / med_s / 1e9,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS,
                      "alg_bytes": alg,
-                     "traffic": measured_call_traffic(MODEL_TRAFFIC_FILE, "chunk_fwd_model_shape")},
+                     "traffic": None if l2 else measured_call_traffic(MODEL_TRAFFIC_FILE, "chunk_fwd_model_shape")},
     }), flush=True)
 
 
@@ -770,7 +777,8 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4],
                     help="BASELINE config to measure (2 = the headline; 4 = the 21-frame fp8 streaming rollout)")
     ap.add_argument("--l2norm", action="store_true",
-                    help="run the op with use_qk_l2norm_in_kernel=True on unnormalised q, k (configs 1-3)")
+                    help="run the op with use_qk_l2norm_in_kernel=True on unnormalised q, k (configs 1-3 and "
+                         "--model-shape)")
     ap.add_argument("--T", type=int, default=32760)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="run only a plain elementwise copy of MIB MiB (fp32 y = x * 1) 5 times and exit: the "

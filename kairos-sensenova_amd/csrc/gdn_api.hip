@@ -236,7 +236,8 @@ bool use_wide_fused(int cdt, int qk_dtype, int64_t K, int64_t V) {
 
 // Workspace of the staged path (stage kernels with the reference's intermediates; the fused K = 256
 // form keeps the state snapshots and v_new on chip and adds the per-chunk Aqk instead).
-size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, bool wide) {
+size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_seqs, int cdt, bool wide,
+                 bool l2) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t nc = (size_t)chunks_bound(B, T, n_seqs);
   const size_t tok = (size_t)(B * T * H);
@@ -249,6 +250,7 @@ size_t staged_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t 
     total += align_up(tok * sizeof(float));               // beta (fp32)
     total += align_up(nc * H * K * kgdn::C * es);         // k^T per chunk
     total += align_up((size_t)(n_seqs > 0 ? n_seqs : B) * H * K * V * sizeof(float));   // state between parts
+    if (l2) total += align_up(tok * sizeof(float));       // rstd of the q rows (the in-op L2 norm, folded)
   } else {
     total += align_up(nc * H * V * kgdn::C * es);         // uT
     total += align_up(nc * H * V * K * es);               // hT
@@ -414,7 +416,7 @@ int aux_streams(hipStream_t* sp, hipStream_t* sr, hipStream_t* sm, hipEvent_t** 
 int run_staged(const Geometry& G, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
                const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
-               Carver& cv, hipStream_t s, bool may_fork) {
+               Carver& cv, hipStream_t s, bool may_fork, bool l2 = false) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(G.B * G.T * G.H);
   const int K = (int)G.K, V = (int)G.V, H = (int)G.H;
@@ -437,6 +439,8 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     bf = static_cast<float*>(cv.take(tok * sizeof(float)));
     kt = cv.take((size_t)G.nc * H * K * kgdn::C * es);
     st = static_cast<float*>(cv.take((size_t)G.N * H * K * V * sizeof(float)));
+  } else if (l2) {
+    return fail(KAIROS_GDN_EINVAL, "the in-op L2 norm is folded only into the fused K = 256 form");
   } else {
     uT = cv.take((size_t)G.nc * H * V * kgdn::C * es);
     hT = cv.take((size_t)G.nc * H * V * K * es);
@@ -450,11 +454,15 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = ai;
   pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;          // the fused K = 256 form: Aqk, Ai, beta, k^T, no u
   pa.kT_out = kt;
+  float* qs = (wide && l2) ? static_cast<float*>(cv.take(tok * sizeof(float))) : nullptr;
+  pa.l2 = qs != nullptr;
+  pa.qs_out = qs;
   kgdn::WideFusedArgs fa{};
   fa.q = q; fa.kT = kt; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
   fa.h0 = h0; fa.h0_dtype = h0_dtype;
   fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
   fa.scale = scale; fa.o = o; fa.ht = ht;
+  fa.qs = qs;
   if (wide && G.nc > 0 && may_fork && cu_seqlens == nullptr) {
     const int64_t nt = (G.T + kgdn::C - 1) / kgdn::C;
     int P = wide_pipe_parts();
@@ -622,11 +630,12 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   const size_t tok = (size_t)(B * T * H);
   const int cdt = compute_dtype(qk_dtype, v_dtype);
   const bool seg = kgdn::seg_fwd_supported(cdt, (int)K, (int)V);
+  const bool wide = !seg && use_wide_fused(cdt, qk_dtype, K, V);
   size_t total = seg ? seg_ws(B, T, H, K, V, n_seqs, plan_segments(B, T, H, n_seqs))
-                     : staged_ws(B, T, H, K, V, n_seqs, cdt, use_wide_fused(cdt, qk_dtype, K, V));
-  // in-op L2 norm: the fused path folds it into its kernels; the staged path normalises q and k in a
-  // pass of their own
-  if (use_qk_l2norm && !seg) total += 2 * align_up(tok * K * dt_size(qk_dtype));
+                     : staged_ws(B, T, H, K, V, n_seqs, cdt, wide, use_qk_l2norm != 0);
+  // in-op L2 norm: the segment scan and the fused K = 256 form fold it into their kernels; the stage
+  // kernels normalise q and k in a pass of their own
+  if (use_qk_l2norm && !seg && !wide) total += 2 * align_up(tok * K * dt_size(qk_dtype));
   return total;
 }
 
@@ -697,7 +706,8 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
   const size_t tok = (size_t)(B * T * H);
   Carver cv{static_cast<char*>(workspace)};
   if (!kgdn::seg_fwd_supported(cdt, (int)K, (int)V)) {
-    if (use_qk_l2norm && any_tokens) {
+    const bool wide = use_wide_fused(cdt, qk_dtype, K, V);
+    if (use_qk_l2norm && any_tokens && !wide) {
       void* qn = cv.take(tok * K * dt_size(qk_dtype));
       void* kn = cv.take(tok * K * dt_size(qk_dtype));
       if (int rc = from_launch(kgdn::launch_l2norm2(q, qn, k, kn, qk_dtype, (int64_t)tok, (int)K, s), "l2norm(q, k)"))
@@ -706,7 +716,8 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
       k = kn;
     }
     if (int rc = run_staged(G, q, k, v, g, beta, q_scale, k_scale, initial_state, h0_dtype, o, final_state,
-                            cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s, profile))
+                            cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s, profile,
+                            wide && use_qk_l2norm != 0))
       return rc;
     if (epi)
       if (int rc = norm_in_place(o, v_dtype, *epi, (int64_t)tok, V, s)) return rc;

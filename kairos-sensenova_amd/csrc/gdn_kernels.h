@@ -44,6 +44,9 @@ struct PrepareArgs {
   int64_t it0, it_span;   // it_span > 0 (cu == nullptr): only local chunks it0 .. it0 + it_span - 1 of each
                           // sequence, grid N * it_span (chunks past a sequence's end exit)
   // uT == nullptr: no u pass (v is not read)
+  int l2;                 // the in-op L2 norm (the compact bf16 plan only): k rows normalised and rounded
+                          // as they are staged, q rows of Aqk likewise
+  float* qs_out;          // with l2 and aqk_out: out [B*T, H] fp32 rstd of each q row
 };
 
 struct FwdHArgs {
@@ -109,6 +112,8 @@ struct WideFusedArgs {
   void* h_out;            // recompute mode (the backward's): out [NC, H, 256, V] bf16 state before each
                           // chunk, row-major; q, aqk and o are not used
   void* vn_out;           // recompute mode: out [B*T, H, V] bf16 v_new
+  const float* qs;        // [B*T, H] fp32 rstd of the q rows (the in-op L2 norm: q is raw, k^T, w and Aqk
+                          // come normalised from prepare), or nullptr
 };
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V);
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s);

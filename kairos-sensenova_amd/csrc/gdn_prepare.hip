@@ -215,6 +215,28 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
 #pragma unroll
     for (int ks = 0; ks < K / 32; ++ks) qraw[ks] = ld_raw(qrow + 32 * ks);
   }
+  // in-op L2 norm of k (chunk.py:168-170, l2norm.py:98-119; compact plan): each thread's share of the
+  // sum of squares of its two rows goes to the A region, free until K.K^T, and is summed after the
+  // gates' barrier
+  const bool l2 = kCompact && a.l2 != 0;
+  if constexpr (kCompact) {
+    if (l2) {
+      float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+      for (int ch = 0; ch < K / 64; ++ch) {
+        float x0[8], x1[8];
+        cvt_raw(kraw[ch][0], 1.f, x0);
+        cvt_raw(kraw[ch][1], 1.f, x1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ss0 = fmaf(x0[e], x0[e], ss0);
+          ss1 = fmaf(x1[e], x1[e], ss1);
+        }
+      }
+      s_A[(2 * pr) * 8 + cg] = ss0;
+      s_A[(2 * pr + 1) * 8 + cg] = ss1;
+    }
+  }
 
   // ---- gates: chunk-local cumsum of g (one wave, inclusive scan over 64 lanes)
   if (wid == 0) {
@@ -234,13 +256,33 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   }
   __syncthreads();
 
-  // ---- with aqk_out: q row tile wid as MFMA fragments (rows 16 wid + lc), from the raw loads
+  // ---- with aqk_out: q row tile wid as MFMA fragments (rows 16 wid + lc), from the raw loads; with
+  //      the in-op L2 norm the row (spread over the four lane groups) is normalised and rounded, and
+  //      its rstd recorded for the output's q h product, which reads raw q
   Frag<TC> qf[K / 32];
   if (a.aqk_out) {
 #pragma unroll
     for (int ks = 0; ks < K / 32; ++ks) {
       if constexpr (sizeof(TC) == 2 && sizeof(TK) == 2) {
         qf[ks].v = __builtin_bit_cast(bf16x8, qraw[ks]);
+        if constexpr (kCompact) {
+          if (ks == K / 32 - 1 && l2) {
+            float ss = 0.f;
+#pragma unroll
+            for (int k2 = 0; k2 < K / 32; ++k2)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) ss = fmaf((float)qf[k2].v[e], (float)qf[k2].v[e], ss);
+            ss += __shfl_xor(ss, 16, WAVE);
+            ss += __shfl_xor(ss, 32, WAVE);
+            const float rs = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int k2 = 0; k2 < K / 32; ++k2)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) qf[k2].v[e] = (bf16)((float)qf[k2].v[e] * rs);
+            const int qr = 16 * wid + lc;
+            if (lg == 0 && qr < nv && a.qs_out) a.qs_out[(t0 + qr) * H + h] = rs;
+          }
+        }
       } else {
         float x[8];
         cvt_raw(qraw[ks], 1.f, x);
@@ -279,6 +321,17 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   //      kb^T[d][t] = k*beta*exp(gc).  Lane = token pair, so each transposed store packs the pair
   //      (one 4-byte store in bf16) and the 32 lanes of a group hit 32 consecutive banks.
   const float kscale = a.k_scale ? a.k_scale[h] : 1.f;
+  float rk0 = 1.f, rk1 = 1.f;                            // rstd of k rows 2 pr, 2 pr + 1 (in-op L2 norm)
+  if (l2) {
+    float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      ss0 += s_A[(2 * pr) * 8 + c];
+      ss1 += s_A[(2 * pr + 1) * 8 + c];
+    }
+    rk0 = 1.0f / sqrtf(ss0 + 1e-6f);
+    rk1 = 1.0f / sqrtf(ss1 + 1e-6f);
+  }
   {
     const float b0 = s_b[2 * pr], b1 = s_b[2 * pr + 1], e0 = s_eg[2 * pr], e1 = s_eg[2 * pr + 1];
 #pragma unroll
@@ -295,7 +348,11 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
       Vec8<TC> r0, r1;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float kv0 = round_to<TC>(x0[e]), kv1 = round_to<TC>(x1[e]);   // stored k (fp8: dequantised)
+        float kv0 = round_to<TC>(x0[e]), kv1 = round_to<TC>(x1[e]);         // stored k (fp8: dequantised)
+        if (l2) {                                          // y = bf16(x rstd), as l2norm_fwd stores it
+          kv0 = round_to<TC>(kv0 * rk0);
+          kv1 = round_to<TC>(kv1 * rk1);
+        }
         vset<TC>(r0, e, kv0);
         vset<TC>(r1, e, kv1);
         if constexpr (!kCompact) {
@@ -577,6 +634,7 @@ int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, 
   // the compact LDS plan for bf16 without the u pass (KAIROS_GDN_PREP_COMPACT=0 selects the full one)
   const char* e = std::getenv("KAIROS_GDN_PREP_COMPACT");
   const bool compact = a.uT == nullptr && compute_dtype == DT_BF16 && !(e && e[0] == '0' && e[1] == 0);
+  if (a.l2 && !(compact && k_dtype == DT_BF16)) return -2;   // the folded L2 norm lives in the compact plan
 #define KGDN_PREP_CASE(TC, TK, KK)                                                                  \
   if (K == KK) {                                                                                    \
     if constexpr (std::is_same<TC, bf16>::value)                                                    \

@@ -222,6 +222,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   __shared__ __align__(16) bf16 s_v[2 * C * C];
   __shared__ __align__(16) float s_g[2 * C];
   __shared__ __align__(16) float s_b[2 * C];
+  __shared__ __align__(16) float s_qs[2 * C];             // rstd of the q rows (the in-op L2 norm)
   __shared__ __align__(16) bf16 s_o[C * C];               // the chunk's o tile [64 t][64 columns]
   __shared__ __align__(16) float s_pf[WAVE];              // landing words of the L2 prefetch
   constexpr uint32_t QOFF = C * FK * 2, ABUF = C * C * 2, GBUF = C * 4;
@@ -252,7 +253,11 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   const int64_t ib = min(a.it_begin, nchunks), ie = a.it_end > 0 ? min(a.it_end, nchunks) : nchunks;
   auto chunk_nv = [&](int64_t it) { return (int)min((int64_t)C, eos - (bos + it * C)); };
   const uint32_t w_lds = lds_u32(s_wq), k_lds = lds_u32(s_k), a_lds = lds_u32(s_a), ai_lds = lds_u32(s_ai),
-                 v_lds = lds_u32(s_v), g_lds = lds_u32(s_g), b_lds = lds_u32(s_b), o_lds = lds_u32(s_o);
+                 v_lds = lds_u32(s_v), g_lds = lds_u32(s_g), b_lds = lds_u32(s_b), o_lds = lds_u32(s_o),
+                 qs_lds = lds_u32(s_qs);
+  // the in-op L2 norm: q arrives raw and o_inter's column t (token t) is scaled by rstd of q row t,
+  // which prepare recorded beside the normalised k^T, w and Aqk
+  const bool qn = !kRc && a.qs != nullptr;
   const bf16* aqb = reinterpret_cast<const bf16*>(a.aqk);
   const bf16* ktb = reinterpret_cast<const bf16*>(a.kT);
 
@@ -262,13 +267,14 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     //      flight.  Loader lw issues load i of each tile for i % FL = lw.  Per chunk step it, between
     //      the compute waves' two barriers: after B1, k^T of chunk it (8 loads each), the small tiles
     //      of chunk it + 1 into the other buffer set (6 each, and gc / beta from loaders 0 / 1) and its
-    //      part of the L2 prefetch of chunk it + 2 (1); before B2 each waits for its k^T loads; after
+    //      part of the L2 prefetch of chunk it + 2 (1); with the in-op L2 norm loader 2 also brings the
+    //      rstd of the q rows (a word per token, beside gc); before B2 each waits for its k^T loads; after
     //      B2 (the compute waves are done with w and q), w and q of chunk it + 1 (16 each).  The o tile
     //      the compute waves left in LDS in step it - 1 goes out right after B1, as whole 128-byte
     //      rows (two 1 KB stores per loader); from the compute waves, whose lanes hold 4 columns of a
     //      token, the same stores would touch 16 lines each and stall them behind the loads.
     const int lw = wid - FW;
-    const int kSmall = 6 + (lw < 2 ? 1 : 0);
+    const int kSmall = 6 + (lw < 2 || (qn && lw == 2) ? 1 : 0);
     const uint32_t RB = (uint32_t)H * FK * 2;
     auto small = [&](int64_t c, int64_t t0, int nv, uint32_t B) {
       const unsigned char* ab = reinterpret_cast<const unsigned char*>(aqb + (c * H + h) * (int64_t)(C * C));
@@ -284,6 +290,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       const uint32_t gl_off = (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u;
       if (lw == 0) dma4_(a.gc + t0 * H + h, gl_off, g_lds + B * GBUF);
       if (lw == 1) dma4_(a.beta + t0 * H + h, gl_off, b_lds + B * GBUF);
+      if (qn && lw == 2) dma4_(a.qs + t0 * H + h, gl_off, qs_lds + B * GBUF);
     };
     auto wq = [&](int64_t t0, int nv) {
       const unsigned char* wb = reinterpret_cast<const unsigned char*>(a.w) + (size_t)((t0 * H + h) * FK) * 2;
@@ -488,13 +495,15 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     }
     f_barrier();                                          // B2: k^T in LDS; w and q tiles free
 
-    // the output's LDS operands first (one latency for all): Aqk row pieces and exp(gc_t) per tile
+    // the output's LDS operands first (one latency for all): Aqk row pieces, exp(gc_t) per tile and
+    // with the in-op L2 norm rstd of q row t
     Frag<bf16> aq[6];
-    float egt[4];
+    float egt[4], qst[4];
     if constexpr (!kRc) {
 #pragma unroll
       for (int tn = 0, f = 0; tn < 4; ++tn) {
         egt[tn] = sg[32 * (tn >> 1) + 4 * (tn & 1) + ra0];
+        qst[tn] = qn ? s_qs[B * C + 32 * (tn >> 1) + 4 * (tn & 1) + ra0] : 1.f;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
           if (ks <= tn / 2) aq[f++] = ld128(A.ar[ks], B * ABUF + rowa_off(tn, 128));
@@ -529,7 +538,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     f32x4 r[4];
 #pragma unroll
     for (int tn = 0, f = 0; tn < 4; ++tn) {
-      r[tn] = oi[tn] * gexp(egt[tn]);
+      r[tn] = oi[tn] * (gexp(egt[tn]) * qst[tn]);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         if (ks <= tn / 2) mma(r[tn], vf[ks], aq[f++]);

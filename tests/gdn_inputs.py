@@ -30,6 +30,18 @@ def make_inputs(B, T, H, K, V, seed, dtype="bf16", n_states=None, h0_scale=0.02,
     return dict(q=q, k=k, v=v, g=g, beta=beta, h0=h0)
 
 
+def quantize_fp8(x):
+    """Per-head e4m3 quantisation with scale = amax / 448."""
+    amax = np.abs(x).max(axis=(0, 1, 3))                               # [H]
+    scale = (amax / 448.0).astype(np.float32)
+    codes = O.fp8_e4m3_quantize(x / scale[None, None, :, None])
+    return codes, scale
+
+
+def dequant_bf16(codes, scale):
+    return O.to_bf16(O.fp8_e4m3_decode(codes) * scale[None, None, :, None])
+
+
 # BASELINE.json configs (the streaming config 4 is built by its own test)
 CONFIGS = {
     0: dict(B=1, T=512, H=4, K=64, V=64, dtype="fp32", zero_h0=True),

@@ -84,6 +84,47 @@ def test_bwd_config1_all_heads():
     run_case(1, 8192, 20, 128, 128, seed=20261)
 
 
+def _full_size_all_heads(B, T, H, K, V, seed, l2):
+    """Backward at a full clip length on every head (oracle over head groups in child processes)."""
+    import oracle_pool
+    x = make_inputs(B, T, H, K, V, seed=seed, dtype="bf16")
+    rng = np.random.default_rng(seed + 7)
+    if l2:                                   # unnormalised q, k: the op normalises them
+        for n in ("q", "k"):
+            x[n] = O.cast(x[n] * rng.uniform(0.5, 3.0, x[n].shape[:-1] + (1,)).astype(np.float32), "bf16")
+    do = O.cast(rng.standard_normal((B, T, H, V)).astype(np.float32), "bf16")
+    dht = rng.standard_normal((B, H, K, V)).astype(np.float32)
+    bf = torch.bfloat16
+    dev = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dt)  # noqa: E731
+    dq, dk, dv, db, dg, dh0 = kairos_gdn.chunk_gated_delta_rule_bwd_native(
+        dev(x["q"], bf), dev(x["k"], bf), dev(x["v"], bf), dev(x["g"], torch.float32), dev(x["beta"], bf),
+        K ** -0.5, dev(x["h0"], torch.float32), dev(do, bf), dev(dht, torch.float32), None, l2)
+    torch.cuda.synchronize()
+    host = lambda t: t.float().cpu().numpy()  # noqa: E731
+    grads = dict(dq=host(dq), dk=host(dk), dv=host(dv), dg=host(dg), dbeta=host(db), dh0=host(dh0))
+    for n, a_ in grads.items():
+        assert np.isfinite(a_).all(), n
+    note("    HIP backward done; oracle on every head")
+    errs = oracle_pool.backward_all_heads(x, do, dht, grads, "bf16", workers=8, group=2, log=note,
+                                          use_qk_l2norm_in_kernel=l2)
+    note("    " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()))
+    assert all(e < 1e-2 for e in errs.values()), errs
+
+
+def test_bwd_config2_shape_full_size():
+    """The headline shape (T=32760, H=20, dk=dv=128, bf16, h0 and dht): the backward's segment scan (12
+    segments per head) on every head against the oracle."""
+    note("backward config 2 shape: B=1 T=32760 H=20 K=V=128, all heads")
+    _full_size_all_heads(1, 32760, 20, 128, 128, seed=20262, l2=False)
+
+
+def test_bwd_model_shape_full_size():
+    """The Kairos layer in training: T=32760, H=20, dk=256, dv=512, the in-op L2 norm on unnormalised
+    q, k, h0 and dht, on every head against the oracle."""
+    note("backward model shape: B=1 T=32760 H=20 K=256 V=512 l2, all heads")
+    _full_size_all_heads(1, 32760, 20, 256, 512, seed=20272, l2=True)
+
+
 def test_bwd_model_shape_varlen():
     """The Kairos layer's head dims (dk=256, dv=512) at a varlen batch with initial states and the L2 norm."""
     note("backward K=256 V=512 varlen [0, 500, 1100] H=2 l2")

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import gdn_oracle as O
-from gdn_inputs import CONFIGS, make_inputs
+from gdn_inputs import CONFIGS, dequant_bf16, make_inputs, quantize_fp8
 import kairos_gdn
 
 pytestmark = pytest.mark.gpu
@@ -420,15 +420,27 @@ def test_varlen_maps_bit_exact():
         np.testing.assert_array_equal(so.cpu().numpy(), np.concatenate([[0], np.cumsum((nch + L - 1) // L)]))
 
 
-def test_model_shape_full_size():
-    """The Kairos 4B layer at the headline clip length: H=20, K=256, V=512, T=32760, bf16."""
+@pytest.mark.parametrize("l2", [False, True], ids=["plain", "l2norm"])
+def test_model_shape_full_size(l2):
+    """The Kairos 4B layer at the headline clip length: H=20, K=256, V=512, T=32760, bf16, against the
+    oracle on every head (child processes over head groups, tests/oracle_pool.py).  With l2, the
+    layer's own mode: unnormalised q, k and use_qk_l2norm_in_kernel=True (gated_deltanet.py:275-285),
+    which the fused K = 256 path folds into prepare and the recurrence."""
+    import oracle_pool
     B, T, H, K, V = 1, 32760, 20, 256, 512
-    heads = [0, 5, 10, 15, 19]
-    note(f"model shape B={B} T={T} H={H} K={K} V={V} (oracle on heads {heads})")
+    note(f"model shape B={B} T={T} H={H} K={K} V={V} l2={l2} (oracle on all {H} heads)")
     x = make_inputs(B, T, H, K, V, seed=20270, dtype="bf16")
-    o, ht = run_gpu(x, "bf16")
+    if l2:
+        rng = np.random.default_rng(20271)
+        for n in ("q", "k"):
+            x[n] = O.to_bf16(x[n] * rng.uniform(0.5, 3.0, x[n].shape[:-1] + (1,)).astype(np.float32))
+    o, ht = run_gpu(x, "bf16", l2=l2)
     assert bool(torch.isfinite(o).all()) and bool(torch.isfinite(ht).all())
-    check_against_oracle(x, "bf16", o, ht, heads=heads)
+    note("    HIP forward done; oracle on every head")
+    e = oracle_pool.forward_all_heads(x, host(o), host(ht), "bf16", workers=8, group=2, log=note,
+                                      use_qk_l2norm_in_kernel=l2)
+    note(f"    rel-L2 over all heads o={e['o']:.3e} ht={e['ht']:.3e}")
+    assert e["o"] < TOL["bf16"]["o"] and e["ht"] < TOL["bf16"]["ht"]
 
 
 # ---------------------------------------------------------------------------
@@ -511,18 +523,6 @@ def test_fp32_against_recurrence():
 # ---------------------------------------------------------------------------
 # config 4: streaming frame-by-frame rollout with fp8 q/k
 # ---------------------------------------------------------------------------
-def quantize_fp8(x):
-    """Per-head e4m3 quantisation with scale = amax / 448."""
-    amax = np.abs(x).max(axis=(0, 1, 3))                               # [H]
-    scale = (amax / 448.0).astype(np.float32)
-    codes = O.fp8_e4m3_quantize(x / scale[None, None, :, None])
-    return codes, scale
-
-
-def dequant_bf16(codes, scale):
-    return O.to_bf16(O.fp8_e4m3_decode(codes) * scale[None, None, :, None])
-
-
 @pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
 def test_fp8_decode_every_code():
     """Every finite e4m3 code through the fused path: with g = 0, beta = 0, h0 = I and scale = 1 the
@@ -570,43 +570,48 @@ def test_fp8_qk_model_head_dims():
 
 @pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8_e4m3fn")
 def test_streaming_fp8_rollout():
+    """Config 4: 21 calls of T = 1560 with the fp32 state carried, fp8 q/k.  Every frame's o and state on
+    every head against the oracle run from the same input state (child processes over frames and head
+    groups, tests/oracle_pool.py), and the end state's drift against one unquantised fp32 call."""
+    import oracle_pool
     B, H, K, V, Tf, frames = 8, 20, 128, 128, 1560, 21
+    seed = 20264
     note(f"config 4: B={B} H={H} {frames} calls of T={Tf}, fp8 q/k")
-    heads = list(range(H))                    # every head on every 5th frame
-    check_frames = {0, 5, 10, 15, 20}
-    dheads = [0, 13]                          # end-state drift (the fp32 single call over all frames)
-    h0 = (0.02 * np.random.default_rng(20264).standard_normal((B, H, K, V))).astype(np.float32)
+    dheads = [0, 7, 13, 19]                   # end-state drift (the fp32 single call over all frames)
+    h0 = (0.02 * np.random.default_rng(seed).standard_normal((B, H, K, V))).astype(np.float32)
     state = dev(h0)
     S_in = h0[:, dheads]
     parts = []
-    for f in range(frames):
-        x = make_inputs(B, Tf, H, K, V, seed=(20264, f), dtype="bf16", h0_scale=0.0)
-        qc, qs = quantize_fp8(x["q"])
-        kc, ks = quantize_fp8(x["k"])
-        q8 = torch.from_numpy(qc).to("cuda").view(torch.float8_e4m3fn)
-        k8 = torch.from_numpy(kc).to("cuda").view(torch.float8_e4m3fn)
-        d = to_dev(x, "bf16")
-        o, new_state = kairos_gdn.chunk_gated_delta_rule(q8, k8, d["v"], d["g"], d["beta"], initial_state=state,
-                                                         output_final_state=True, q_scale=dev(qs), k_scale=dev(ks))
-        parts.append({k_: x[k_][:, :, dheads] for k_ in ("q", "k", "v", "g", "beta")})
-        if f in check_frames:
+    with oracle_pool.Scratch() as sc:
+        for f in range(frames):
+            x = make_inputs(B, Tf, H, K, V, seed=(seed, f), dtype="bf16", h0_scale=0.0)
+            qc, qs = quantize_fp8(x["q"])
+            kc, ks = quantize_fp8(x["k"])
+            q8 = torch.from_numpy(qc).to("cuda").view(torch.float8_e4m3fn)
+            k8 = torch.from_numpy(kc).to("cuda").view(torch.float8_e4m3fn)
+            d = to_dev(x, "bf16")
+            o, new_state = kairos_gdn.chunk_gated_delta_rule(q8, k8, d["v"], d["g"], d["beta"], initial_state=state,
+                                                             output_final_state=True, q_scale=dev(qs),
+                                                             k_scale=dev(ks))
             torch.cuda.synchronize()
             assert o.dtype == torch.bfloat16
-            qd, kd = dequant_bf16(qc, qs), dequant_bf16(kc, ks)
-            o_r, S_next = O.chunk_gated_delta_rule(qd[:, :, heads], kd[:, :, heads], x["v"][:, :, heads],
-                                                   x["g"][:, :, heads], x["beta"][:, :, heads],
-                                                   initial_state=host(state)[:, heads], output_final_state=True,
-                                                   dtype="bf16")
-            eo = rel(host(o)[:, :, heads], o_r)
-            eh = rel(host(new_state)[:, heads], S_next)
-            note(f"    frame {f}: rel-L2 o={eo:.3e} state={eh:.3e}")
-            assert eo < 1e-2 and eh < 5e-3
-        state = new_state
+            sc.put(f"o{f}", host(o), bf16=True)
+            sc.put(f"si{f}", host(state))
+            sc.put(f"so{f}", host(new_state))
+            parts.append({k_: x[k_][:, :, dheads] for k_ in ("q", "k", "v", "g", "beta")})
+            state = new_state
+        note("    GPU rollout done; oracle per frame on every head")
+        e = oracle_pool.run_heads(oracle_pool.fp8_frame_job, sc, H, group=10, workers=8, log=lambda m: None,
+                                  kw=dict(shape=(B, Tf, H, K, V), seed=seed, frames=frames), frames=frames)
+    for f in range(frames):
+        note(f"    frame {f}: rel-L2 o={e[f'o{f}']:.3e} state={e[f'h{f}']:.3e}")
+    assert all(e[f"o{f}"] < 1e-2 and e[f"h{f}"] < 5e-3 for f in range(frames))
     torch.cuda.synchronize()
-    # drift of the streamed end state against one fp32 call over all 21 frames (unquantised q/k)
+    # drift of the streamed end state against one fp32 call over all 21 frames (unquantised q/k): the
+    # e4m3 rounding of q and k (3 mantissa bits) bounds it; measured 2.7e-2
     cat = {k_: np.concatenate([p_[k_] for p_ in parts], axis=1) for k_ in parts[0]}
     _, h_single = O.chunk_gated_delta_rule(cat["q"], cat["k"], cat["v"], cat["g"], cat["beta"],
                                            initial_state=S_in, output_final_state=True, dtype="fp32")
     drift = rel(host(state)[:, dheads], h_single)
     note(f"    end-state drift vs single-call fp32 (unquantised q/k): {drift:.3e}")
-    assert math.isfinite(drift) and drift < 0.1
+    assert math.isfinite(drift) and drift < 0.05

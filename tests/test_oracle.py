@@ -356,3 +356,20 @@ def test_torch_cpu_restatement(B, T, H, K, V, cu):
     oo, ho = O.chunk_gated_delta_rule(*(f32(x[n]) for n in ("q", "k", "v", "g", "beta")),
                                       initial_state=f32(x["h0"]), output_final_state=True, cu_seqlens=cu, dtype="fp32")
     assert O.rel_l2(o32.numpy(), oo) < 1e-5 and O.rel_l2(h32.numpy(), ho) < 1e-5
+
+
+def test_oracle_pool_combines_head_groups():
+    """The child-process oracle used for full-size checks on every head (tests/oracle_pool.py) gives the
+    single-process rel-L2: 0 for the oracle's own outputs, and the error of a planted change in one head."""
+    import oracle_pool
+    from gdn_inputs import make_inputs
+    B, T, H, K, V = 1, 200, 5, 64, 64
+    x = make_inputs(B, T, H, K, V, seed=5, dtype="bf16")
+    o, ht = O.chunk_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["h0"],
+                                     output_final_state=True, dtype="bf16")
+    e = oracle_pool.forward_all_heads(x, o, ht, "bf16", workers=2, group=2, log=lambda m: None)
+    assert e["o"] == 0.0 and e["ht"] == 0.0
+    o2 = o.copy()
+    o2[:, :, 3] = O.to_bf16(o2[:, :, 3] * 1.5)                # a planted error in one head
+    e2 = oracle_pool.forward_all_heads(x, o2, ht, "bf16", workers=2, group=2, log=lambda m: None)
+    assert abs(e2["o"] - O.rel_l2(o2, o)) < 1e-6 and e2["o"] > 1e-2
