@@ -308,6 +308,33 @@ int kairos_gdn_causal_conv1d_fwd(const void* x, const void* weight, const void* 
                                  int64_t T, int64_t D, int64_t W, int x_dtype, int w_dtype, int activation_silu,
                                  int l2norm_head_dim, void* stream);
 
+/* The layer's prologue folded into the chunked forward: the q_conv1d / k_conv1d / v_conv1d
+ * ShortConvolutions (kernel size 4, activation 'silu') of fla layers/gated_deltanet.py:234-253
+ * followed by chunk_gated_delta_rule (:275-285), in one call that takes the projections
+ * q_proj(h), k_proj(h), v_proj(h) instead of q, k, v.  Same result as
+ * kairos_gdn_causal_conv1d_fwd on each projection, then kairos_gdn_chunk_fwd on the outputs
+ * (use_qk_l2norm: q and k normalised as the op would).  At the Kairos layer's head dims
+ * (K = 256, V a multiple of 64) the convolution runs where the forward stages its rows: k and q
+ * in the prepare kernel, v in the recurrence's loader waves; q leaves prepare once, convolved
+ * (and normalised), for the recurrence.  Other head dims convolve into the workspace first.
+ * xq, xk: [B*T, H*K] bf16; xv: [B*T, H*V] bf16 (16-byte aligned); wq, wk: [H*K, 4],
+ * wv: [H*V, 4] and biases bq, bk, bv ([D] or NULL) in w_dtype (fp32 or bf16); conv caches in
+ * cq_in, ck_in, cv_in ([N, D, 4] bf16 or NULL = zeros) and out cq_out, ck_out, cv_out (the last
+ * 4 entries of [cache, x] per sequence, NULL = not wanted, not aliasing the cache in).  The rest
+ * as kairos_gdn_chunk_fwd with bf16 q/k/v; workspace from
+ * kairos_gdn_chunk_fwd_conv_workspace_size.  No counterpart in the reference as one call: it
+ * replaces the layer's three ShortConvolution calls and its chunk_gated_delta_rule call. */
+size_t kairos_gdn_chunk_fwd_conv_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                                int64_t n_seqs, int use_qk_l2norm);
+int kairos_gdn_chunk_fwd_conv(const void* xq, const void* xk, const void* xv, const void* wq, const void* wk,
+                              const void* wv, const void* bq, const void* bk, const void* bv, const void* cq_in,
+                              const void* ck_in, const void* cv_in, void* cq_out, void* ck_out, void* cv_out,
+                              int w_dtype, const void* g, const void* beta, const void* initial_state, void* o,
+                              float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T,
+                              int64_t H, int64_t K, int64_t V, int g_dtype, int beta_dtype, int h0_dtype,
+                              float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* Gates of the GatedDeltaNet layer (fla layers/gated_deltanet.py:265-271):
  * g = -exp(A_log) softplus(a + dt_bias) (fp32, softplus threshold 20) and
  * beta = sigmoid(b) in b's dtype, doubled when allow_neg_eigval.  a, b: [rows, HV]

@@ -416,7 +416,8 @@ int aux_streams(hipStream_t* sp, hipStream_t* sr, hipStream_t* sm, hipEvent_t** 
 int run_staged(const Geometry& G, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
                const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
-               Carver& cv, hipStream_t s, bool may_fork, bool l2 = false) {
+               Carver& cv, hipStream_t s, bool may_fork, bool l2 = false,
+               const kgdn::ConvIn* conv3 = nullptr) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(G.B * G.T * G.H);
   const int K = (int)G.K, V = (int)G.V, H = (int)G.H;
@@ -454,15 +455,29 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   pa.gc = gc; pa.w = w; pa.uT = uT; pa.A_out = nullptr; pa.Ai_out = ai;
   pa.q = q; pa.aqk_out = aqk; pa.beta_out = bf;          // the fused K = 256 form: Aqk, Ai, beta, k^T, no u
   pa.kT_out = kt;
-  float* qs = (wide && l2) ? static_cast<float*>(cv.take(tok * sizeof(float))) : nullptr;
-  pa.l2 = qs != nullptr;
+  // the in-op L2 norm folded into prepare; without the folded convolution the recurrence reads raw q
+  // and scales q h by the rstd prepare records, with it prepare writes q normalised
+  float* qs = (wide && l2 && conv3 == nullptr) ? static_cast<float*>(cv.take(tok * sizeof(float))) : nullptr;
+  pa.l2 = wide && l2;
   pa.qs_out = qs;
+  void* q_conv = nullptr;
+  if (conv3) {                                            // the layer's prologue folded in (K = 256 form only)
+    if (!wide) return fail(KAIROS_GDN_EINVAL, "the convolution is folded only into the fused K = 256 form");
+    q_conv = cv.take(tok * K * es);
+    pa.cq = conv3[0];
+    pa.ck = conv3[1];
+    pa.q_out = q_conv;
+  }
   kgdn::WideFusedArgs fa{};
   fa.q = q; fa.kT = kt; fa.v = v; fa.w = w; fa.Ai = ai; fa.beta = bf; fa.gc = gc; fa.aqk = aqk;
   fa.h0 = h0; fa.h0_dtype = h0_dtype;
   fa.cu = cu_seqlens; fa.chunk_off = chunk_off; fa.N = N; fa.T = G.T; fa.H = H;
   fa.scale = scale; fa.o = o; fa.ht = ht;
   fa.qs = qs;
+  if (conv3) {
+    fa.q = q_conv;
+    fa.cv = conv3[2];
+  }
   if (wide && G.nc > 0 && may_fork && cu_seqlens == nullptr) {
     const int64_t nt = (G.T + kgdn::C - 1) / kgdn::C;
     int P = wide_pipe_parts();
@@ -810,6 +825,125 @@ int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v,
 }
 
 size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void) { return kScratchBytes; }
+
+// ---------------------------------------------------------------------------
+// The layer's prologue folded into the forward (kairos_gdn_chunk_fwd_conv)
+// ---------------------------------------------------------------------------
+// Where the fused K = 256 form runs (bf16, K = 256, V a multiple of 64), prepare forms k and q from
+// their projections and the recurrence's loader waves form v: the convolved q, k, v never reach HBM
+// but q once (normalised with the in-op L2 norm), which the recurrence's value tiles share.  Other head
+// dims run the standalone convolution (with the per-head L2 norm) into the workspace and then the
+// forward.
+static bool conv_folded(int64_t K, int64_t V) {
+  return K == 256 && use_wide_fused(KAIROS_GDN_BF16, KAIROS_GDN_BF16, K, V);
+}
+
+size_t kairos_gdn_chunk_fwd_conv_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                                int64_t n_seqs, int use_qk_l2norm) {
+  if (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0) return 0;
+  const size_t tok = (size_t)(B * T * H);
+  size_t total = 2 * align_up((size_t)(H * K) * 5 * sizeof(float)) + align_up((size_t)(H * V) * 5 * sizeof(float));
+  if (conv_folded(K, V))
+    return total + staged_ws(B, T, H, K, V, n_seqs, KAIROS_GDN_BF16, true, false) + align_up(tok * K * 2);
+  total += 2 * align_up(tok * K * 2) + align_up(tok * V * 2);
+  return total + kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, KAIROS_GDN_BF16, KAIROS_GDN_BF16, 0);
+}
+
+int kairos_gdn_chunk_fwd_conv(const void* xq, const void* xk, const void* xv, const void* wq, const void* wk,
+                              const void* wv, const void* bq, const void* bk, const void* bv, const void* cq_in,
+                              const void* ck_in, const void* cv_in, void* cq_out, void* ck_out, void* cv_out,
+                              int w_dtype, const void* g, const void* beta, const void* initial_state, void* o,
+                              float* final_state, const int64_t* cu_seqlens, int64_t n_seqs, int64_t B, int64_t T,
+                              int64_t H, int64_t K, int64_t V, int g_dtype, int beta_dtype, int h0_dtype,
+                              float scale, int use_qk_l2norm, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  const char* what = "kairos_gdn_chunk_fwd_conv";
+  Geometry G;
+  if (int rc = check_geometry(G, cu_seqlens, n_seqs, B, T, H, K, V, what)) return rc;
+  if (!valid_scalar_dt(w_dtype)) return fail(KAIROS_GDN_EINVAL, "%s: conv weights must be fp32 or bf16", what);
+  if (!valid_scalar_dt(g_dtype) || !valid_scalar_dt(beta_dtype) || (initial_state && !valid_scalar_dt(h0_dtype)))
+    return fail(KAIROS_GDN_EINVAL, "%s: g, beta and initial_state must be fp32 or bf16", what);
+  if (!(K == 64 || K == 128 || K == 256) || V % 16 != 0 || V > 1024)
+    return fail(KAIROS_GDN_EUNSUPPORTED, "%s: head dims K=%lld V=%lld are not built", what, (long long)K,
+                (long long)V);
+  if (!std::isfinite(scale)) return fail(KAIROS_GDN_EINVAL, "%s: scale must be finite", what);
+  const bool any_tokens = G.B * G.T > 0;
+  if (any_tokens && (!xq || !xk || !xv || !wq || !wk || !wv || !g || !beta || !o))
+    return fail(KAIROS_GDN_EINVAL, "%s: null tensor pointer", what);
+  for (const void* p : {xq, xk, xv, wq, wk, wv, bq, bk, bv, static_cast<const void*>(o)})
+    if (!aligned16(p)) return fail(KAIROS_GDN_EINVAL, "%s: projections, weights, biases and o must be 16-byte aligned",
+                                   what);
+  if ((cq_out && cq_out == cq_in) || (ck_out && ck_out == ck_in) || (cv_out && cv_out == cv_in))
+    return fail(KAIROS_GDN_EINVAL, "%s: a conv cache out must not alias its cache in", what);
+  const size_t need = kairos_gdn_chunk_fwd_conv_workspace_size(B, T, H, K, V, n_seqs, use_qk_l2norm);
+  if (workspace_bytes < need)
+    return fail(KAIROS_GDN_EWORKSPACE, "%s: workspace of %zu bytes is smaller than the %zu required", what,
+                workspace_bytes, need);
+  if (need && !aligned16(workspace)) return fail(KAIROS_GDN_EINVAL, "%s: workspace must be 16-byte aligned", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t DK = H * K, DV = H * V;
+  Carver cv{static_cast<char*>(workspace)};
+  // fp32 taps [D, 4] and biases [D] of the three projections
+  const void* xs[3] = {xq, xk, xv};
+  const void* ws3[3] = {wq, wk, wv};
+  const void* bs3[3] = {bq, bk, bv};
+  const void* cin[3] = {cq_in, ck_in, cv_in};
+  void* cout[3] = {cq_out, ck_out, cv_out};
+  const int64_t D3[3] = {DK, DK, DV};
+  kgdn::ConvIn c3[3];
+  for (int i = 0; i < 3; ++i) {
+    float* tw = static_cast<float*>(cv.take((size_t)D3[i] * 5 * sizeof(float)));
+    float* tb = bs3[i] ? tw + D3[i] * 4 : nullptr;
+    if (any_tokens) {
+      if (int rc = from_launch(kgdn::launch_to_f32(ws3[i], w_dtype, tw, D3[i] * 4, s), what)) return rc;
+      if (tb)
+        if (int rc = from_launch(kgdn::launch_to_f32(bs3[i], w_dtype, tb, D3[i], s), what)) return rc;
+    }
+    c3[i] = kgdn::ConvIn{xs[i], tw, tb, cin[i], KAIROS_GDN_F32, (int)D3[i]};
+  }
+  if (any_tokens) {
+    if (conv_folded(K, V)) {
+      if (int rc = run_staged(G, xq, xk, xv, g, beta, nullptr, nullptr, initial_state, h0_dtype, o, final_state,
+                              cu_seqlens, KAIROS_GDN_BF16, KAIROS_GDN_BF16, g_dtype, beta_dtype, scale, cv, s, true,
+                              use_qk_l2norm != 0, c3))
+        return rc;
+    } else {
+      // the standalone convolution (the per-head L2 norm fused into it), then the forward
+      void* y3[3];
+      for (int i = 0; i < 3; ++i) {
+        y3[i] = cv.take((size_t)(B * T) * D3[i] * 2);
+        kgdn::ConvArgs ca{};
+        ca.x = xs[i]; ca.y = y3[i]; ca.w = c3[i].w; ca.bias = c3[i].b; ca.h0 = cin[i]; ca.ht = nullptr;
+        ca.cu = cu_seqlens; ca.T = T; ca.total_tokens = B * T; ca.N = (int)G.N; ca.D = (int)D3[i]; ca.W = kgdn::kConvW;
+        ca.x_dtype = KAIROS_GDN_BF16; ca.w_dtype = KAIROS_GDN_F32; ca.silu = 1;
+        ca.head_lanes = (use_qk_l2norm && i < 2) ? (int)(K / 8) : 0;
+        if (int rc = from_launch(kgdn::launch_conv1d(ca, s), what)) return rc;
+      }
+      const size_t rest = workspace_bytes - cv.off;
+      if (int rc = chunk_fwd_impl(what, false, y3[0], y3[1], y3[2], g, beta, nullptr, nullptr, initial_state, o,
+                                  final_state, cu_seqlens, n_seqs, B, T, H, K, V, KAIROS_GDN_BF16, KAIROS_GDN_BF16,
+                                  g_dtype, beta_dtype, h0_dtype, scale, 0, static_cast<char*>(workspace) + cv.off,
+                                  rest, stream))
+        return rc;
+    }
+  } else if (final_state) {
+    // no tokens: the final state is the initial one (zeros without it)
+    if (int rc = kairos_gdn_chunk_fwd(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, initial_state,
+                                      nullptr, final_state, cu_seqlens, n_seqs, B, T, H, K, V, KAIROS_GDN_BF16,
+                                      KAIROS_GDN_BF16, g_dtype, beta_dtype, h0_dtype, scale, 0, workspace,
+                                      workspace_bytes, stream))
+      return rc;
+  }
+  // the final caches, after every kernel that reads the caches in (stream order)
+  for (int i = 0; i < 3; ++i) {
+    if (!cout[i]) continue;
+    kgdn::ConvArgs ca{};
+    ca.x = xs[i]; ca.h0 = cin[i]; ca.ht = cout[i]; ca.cu = cu_seqlens; ca.T = T; ca.total_tokens = B * T;
+    ca.N = (int)G.N; ca.D = (int)D3[i]; ca.W = kgdn::kConvW; ca.x_dtype = KAIROS_GDN_BF16;
+    if (int rc = from_launch(kgdn::launch_conv_state(ca, s), what)) return rc;
+  }
+  return ok();
+}
 
 int kairos_gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g, const void* beta,
                                  const float* q_scale, const float* k_scale, const void* initial_state, void* o,

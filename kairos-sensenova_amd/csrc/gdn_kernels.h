@@ -19,6 +19,21 @@ struct SeqArgs {
   int H;
 };
 
+constexpr int kConvW = 4;              // taps of the folded convolution (the layer's conv_size)
+
+// A projection the op convolves (short causal convolution + SiLU, taps of width 4) as it stages its
+// rows, the layer's prologue folded into the op's loads (gdn_conv.hpp): x [B*T, D] bf16 with D = H * Dh,
+// taps w [D, 4] and bias b [D] (or nullptr) fp32 (the C ABI converts bf16 taps into its workspace),
+// cache [N, D, 4] bf16 or nullptr.  x == nullptr: the op reads the tensor itself.
+struct ConvIn {
+  const void* x;
+  const void* w;
+  const void* b;
+  const void* cache;
+  int w_dtype;
+  int D;
+};
+
 struct PrepareArgs {
   const void* k;          // [B*T, H, K]  k_dtype
   const void* v;          // [B*T, H, V]  compute dtype
@@ -47,6 +62,9 @@ struct PrepareArgs {
   int l2;                 // the in-op L2 norm (the compact bf16 plan only): k rows normalised and rounded
                           // as they are staged, q rows of Aqk likewise
   float* qs_out;          // with l2 and aqk_out: out [B*T, H] fp32 rstd of each q row
+  ConvIn ck, cq;          // with ck.x / cq.x (compact plan): k, q formed from their projections
+  void* q_out;            // with cq.x: out [B*T, H, K] bf16 q as the recurrence reads it (convolved and, with
+                          // l2, normalised)
 };
 
 struct FwdHArgs {
@@ -114,6 +132,7 @@ struct WideFusedArgs {
   void* vn_out;           // recompute mode: out [B*T, H, V] bf16 v_new
   const float* qs;        // [B*T, H] fp32 rstd of the q rows (the in-op L2 norm: q is raw, k^T, w and Aqk
                           // come normalised from prepare), or nullptr
+  ConvIn cv;              // with cv.x: v formed from its projection by the loader waves (v unused)
 };
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V);
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s);
@@ -314,6 +333,8 @@ struct ConvArgs {
   int head_lanes;         // 0, or hd / 8: L2-normalise the rounded y per head of hd channels
 };
 int launch_conv1d(const ConvArgs& a, hipStream_t s);
+int launch_conv_state(const ConvArgs& a, hipStream_t s);   // the final cache only
+int launch_to_f32(const void* src, int dtype, float* dst, int64_t n, hipStream_t s);
 
 // GatedDeltaNet gates (gdn_prologue.hip), layers/gated_deltanet.py:265-271.
 struct GateArgs {

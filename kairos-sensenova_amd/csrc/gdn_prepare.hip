@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "gdn_common.hpp"
+#include "gdn_conv.hpp"
 #include "gdn_kernels.h"
 
 namespace kgdn {
@@ -141,8 +142,8 @@ __device__ __forceinline__ void ld_gate_pair(const void* g, int g_dt, const void
   }
 }
 
-template <typename TC, typename TK, int K, bool kCompact>
-__global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) {
+template <typename TC, typename TK, int K, bool kCompact, bool kConv>
+__device__ __forceinline__ void prepare_body(const PrepareArgs& a, int V) {
   using L = std::conditional_t<kCompact, PrepLdsCompact<TC, K>, PrepLds<TC, K>>;
   static_assert(!kCompact || std::is_same<TC, bf16>::value, "the compact plan reads k with 16-bit transposed reads");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -199,7 +200,38 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   const TK* kin = reinterpret_cast<const TK*>(a.k);
   const bool ok0 = 2 * pr < nv, ok1 = 2 * pr + 1 < nv;
   Raw kraw[K / 64][2];
-  {
+  // with the layer's prologue folded in (compact bf16 plan): k and q are formed here from their
+  // projections, each staged row piece convolved from its own window of raw rows (gdn_conv.hpp)
+  constexpr bool kConvOk = kConv && kCompact && std::is_same<TK, bf16>::value;
+  const bool conv_k = kConvOk && a.ck.x != nullptr, conv_q = kConvOk && a.cq.x != nullptr;
+  // the taps of both projections in the A region (free until K.K^T; the L2 norm's row sums use its
+  // first 2 KB): k at +2 KB, q after them, 5 K floats each
+  float* s_tk = s_A + 512;
+  float* s_tq = s_tk + 5 * K;
+  if constexpr (kConvOk) {
+    static_assert(512 + 10 * K <= C * L::LDA, "the taps fit in the A region");
+    if (conv_k) stage_taps<K, NT_PREP>(s_tk, a.ck, h);
+    if (conv_q) stage_taps<K, NT_PREP>(s_tq, a.cq, h);
+    __syncthreads();
+  }
+  if (conv_k) {
+    if constexpr (kConvOk) {
+#pragma unroll
+      for (int ch = 0; ch < K / 64; ++ch) {
+        const int cl = cg * (K / 8) + 8 * ch;            // channel within the head
+        const int64_t c0 = (int64_t)h * K + cl;
+        ConvWin<2> win;
+        win.issue(a.ck, t0 + 2 * pr, loc.bos, t0 + nv, c0);
+        const ConvTapsLds tp{s_tk + 4 * cl, a.ck.b ? s_tk + 4 * K + cl : nullptr};
+        cvx4 y[2];
+        win.finish(a.ck, tp, t0 + 2 * pr, loc.bos, loc.n, c0, y);
+        kraw[ch][0].v = __builtin_bit_cast(bf16x8, y[0]);
+        kraw[ch][1].v = __builtin_bit_cast(bf16x8, y[1]);
+        asm volatile("" ::: "memory");                   // one window's registers live at a time
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
     const TK* krow0 = kin + ((t0 + (ok0 ? 2 * pr : 0)) * H + h) * K + cg * (K / 8);
     const TK* krow1 = kin + ((t0 + (ok1 ? 2 * pr + 1 : 0)) * H + h) * K + cg * (K / 8);
 #pragma unroll
@@ -211,9 +243,28 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
   Raw qraw[K / 32];
   if (a.aqk_out) {
     const int qr = 16 * wid + lc;
-    const TK* qrow = reinterpret_cast<const TK*>(a.q) + ((t0 + (qr < nv ? qr : 0)) * H + h) * K + 8 * lg;
+    if (conv_q) {
+      if constexpr (kConvOk) {
 #pragma unroll
-    for (int ks = 0; ks < K / 32; ++ks) qraw[ks] = ld_raw(qrow + 32 * ks);
+        for (int ks = 0; ks < K / 32; ++ks) {
+          const int cl = 32 * ks + 8 * lg;
+          const int64_t c0 = (int64_t)h * K + cl;
+          const int64_t t = t0 + (qr < nv ? qr : 0);
+          ConvWin<1> win;
+          win.issue(a.cq, t, loc.bos, t0 + nv, c0);
+          const ConvTapsLds tp{s_tq + 4 * cl, a.cq.b ? s_tq + 4 * K + cl : nullptr};
+          cvx4 y[1];
+          win.finish(a.cq, tp, t, loc.bos, loc.n, c0, y);
+          qraw[ks].v = __builtin_bit_cast(bf16x8, y[0]);
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+      const TK* qrow = reinterpret_cast<const TK*>(a.q) + ((t0 + (qr < nv ? qr : 0)) * H + h) * K + 8 * lg;
+#pragma unroll
+      for (int ks = 0; ks < K / 32; ++ks) qraw[ks] = ld_raw(qrow + 32 * ks);
+    }
   }
   // in-op L2 norm of k (chunk.py:168-170, l2norm.py:98-119; compact plan): each thread's share of the
   // sum of squares of its two rows goes to the A region, free until K.K^T, and is summed after the
@@ -280,7 +331,7 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
 #pragma unroll
               for (int e = 0; e < 8; ++e) qf[k2].v[e] = (bf16)((float)qf[k2].v[e] * rs);
             const int qr = 16 * wid + lc;
-            if (lg == 0 && qr < nv && a.qs_out) a.qs_out[(t0 + qr) * H + h] = rs;
+            if (lg == 0 && qr < nv && a.qs_out && !conv_q) a.qs_out[(t0 + qr) * H + h] = rs;
           }
         }
       } else {
@@ -293,6 +344,16 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
           qf[ks].lo = f32x4{x[0], x[1], x[2], x[3]};
           qf[ks].hi = f32x4{x[4], x[5], x[6], x[7]};
         }
+      }
+    }
+    // q formed here (the folded prologue): the recurrence reads it as prepare leaves it (convolved and,
+    // with the in-op L2 norm, normalised), one 16-byte row piece per fragment
+    if constexpr (kConvOk) {
+      const int qr = 16 * wid + lc;
+      if (conv_q && a.q_out && qr < nv) {
+        bf16* qo = reinterpret_cast<bf16*>(a.q_out) + ((t0 + qr) * H + h) * K + 8 * lg;
+#pragma unroll
+        for (int ks = 0; ks < K / 32; ++ks) *reinterpret_cast<bf16x8*>(qo + 32 * ks) = qf[ks].v;
       }
     }
   }
@@ -612,10 +673,27 @@ __global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) 
 }
 
 template <typename TC, typename TK, int K, bool kCompact>
+__global__ __launch_bounds__(NT_PREP) void prepare_kernel(PrepareArgs a, int V) {
+  prepare_body<TC, TK, K, kCompact, false>(a, V);
+}
+
+// The compact plan with the layer's prologue folded in (k and q convolved from their projections as
+// they are staged): the windows need more registers than the plain form's 127, so two workgroups per CU
+// instead of three.
+template <typename TC, typename TK, int K>
+__global__ __launch_bounds__(NT_PREP) __attribute__((amdgpu_waves_per_eu(2, 2))) void prepare_conv_kernel(
+    PrepareArgs a, int V) {
+  prepare_body<TC, TK, K, true, true>(a, V);
+}
+
+template <typename TC, typename TK, int K, bool kCompact>
 int launch_prepare_t(const PrepareArgs& a, int V, int64_t nc_grid, hipStream_t s) {
   using L = std::conditional_t<kCompact, PrepLdsCompact<TC, K>, PrepLds<TC, K>>;
   static_assert(L::total <= 160 * 1024, "prepare tile does not fit in LDS");
   auto kern = prepare_kernel<TC, TK, K, kCompact>;
+  if constexpr (kCompact && std::is_same<TK, bf16>::value && K == 256) {
+    if (a.ck.x || a.cq.x) kern = prepare_conv_kernel<TC, TK, K>;
+  }
   if (L::total > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)L::total) != hipSuccess)
@@ -634,7 +712,10 @@ int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, 
   // the compact LDS plan for bf16 without the u pass (KAIROS_GDN_PREP_COMPACT=0 selects the full one)
   const char* e = std::getenv("KAIROS_GDN_PREP_COMPACT");
   const bool compact = a.uT == nullptr && compute_dtype == DT_BF16 && !(e && e[0] == '0' && e[1] == 0);
-  if (a.l2 && !(compact && k_dtype == DT_BF16)) return -2;   // the folded L2 norm lives in the compact plan
+  // the folded L2 norm and the folded convolution live in the compact plan
+  if ((a.l2 || a.ck.x || a.cq.x) && !(compact && k_dtype == DT_BF16)) return -2;
+  if ((a.ck.x || a.cq.x) && K != 256) return -2;        // the folded convolution is built for K = 256
+  if ((a.ck.x || a.cq.x) && (a.aqk_out == nullptr) != (a.cq.x == nullptr)) return -2;
 #define KGDN_PREP_CASE(TC, TK, KK)                                                                  \
   if (K == KK) {                                                                                    \
     if constexpr (std::is_same<TC, bf16>::value)                                                    \

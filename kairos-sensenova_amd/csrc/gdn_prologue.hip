@@ -208,6 +208,12 @@ __global__ __launch_bounds__(256) void gates_kernel(GateArgs a) {
   static_cast<TB*>(a.beta)[i] = from_f32<TB>(beta);
 }
 
+// fp32 copy of n values of a runtime-typed array (the folded convolution reads fp32 taps)
+__global__ __launch_bounds__(256) void to_f32_kernel(const void* src, int dt, float* dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = ld_scalar(src, i, dt);
+}
+
 template <typename TX, int W>
 int launch_conv_w(const ConvArgs& a, int64_t n_runs, hipStream_t s) {
   const int64_t waves = n_runs * ((a.D + 511) / 512);
@@ -250,6 +256,24 @@ int launch_conv1d(const ConvArgs& a, hipStream_t s) {
   if (a.x_dtype == DT_BF16) return launch_conv_t<bf16>(a, s);
   if (a.x_dtype == DT_F32) return launch_conv_t<float>(a, s);
   return -2;
+}
+
+int launch_conv_state(const ConvArgs& a, hipStream_t s) {
+  if (!a.ht || a.N <= 0) return 0;
+  const int64_t total = (int64_t)a.N * a.D;
+  if (a.x_dtype == DT_BF16)
+    hipLaunchKernelGGL(conv_state_kernel<bf16>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+  else if (a.x_dtype == DT_F32)
+    hipLaunchKernelGGL(conv_state_kernel<float>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+  else
+    return -2;
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_to_f32(const void* src, int dtype, float* dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dtype, dst, n);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_gates(const GateArgs& a, hipStream_t s) {

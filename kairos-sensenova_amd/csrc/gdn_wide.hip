@@ -40,6 +40,7 @@
 #include <type_traits>
 
 #include "gdn_common.hpp"
+#include "gdn_conv.hpp"
 #include "gdn_kernels.h"
 
 namespace kgdn {
@@ -104,6 +105,16 @@ __device__ __forceinline__ void wait_loads_but() {
   static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
+}
+// the same for a count known only at run time (wave-uniform, 4 .. 8)
+__device__ __forceinline__ void wait_loads_but_n(int n) {
+  switch (n) {
+    case 4: wait_loads_but<4>(); break;
+    case 5: wait_loads_but<5>(); break;
+    case 6: wait_loads_but<6>(); break;
+    case 7: wait_loads_but<7>(); break;
+    default: wait_loads_but<8>(); break;
+  }
 }
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
@@ -258,6 +269,9 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   // the in-op L2 norm: q arrives raw and o_inter's column t (token t) is scaled by rstd of q row t,
   // which prepare recorded beside the normalised k^T, w and Aqk
   const bool qn = !kRc && a.qs != nullptr;
+  // the layer's prologue folded in: the loader waves form the workgroup's v tile from the projection
+  // (short convolution + SiLU) instead of loading v
+  const bool cvm = !kRc && a.cv.x != nullptr;
   const bf16* aqb = reinterpret_cast<const bf16*>(a.aqk);
   const bf16* ktb = reinterpret_cast<const bf16*>(a.kT);
 
@@ -274,7 +288,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     //      rows (two 1 KB stores per loader); from the compute waves, whose lanes hold 4 columns of a
     //      token, the same stores would touch 16 lines each and stall them behind the loads.
     const int lw = wid - FW;
-    const int kSmall = 6 + (lw < 2 || (qn && lw == 2) ? 1 : 0);
+    const int kSmall = (cvm ? 4 : 6) + (lw < 2 || (qn && lw == 2) ? 1 : 0);
     const uint32_t RB = (uint32_t)H * FK * 2;
     auto small = [&](int64_t c, int64_t t0, int nv, uint32_t B) {
       const unsigned char* ab = reinterpret_cast<const unsigned char*>(aqb + (c * H + h) * (int64_t)(C * C));
@@ -285,8 +299,10 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         if constexpr (!kRc) ld_tile64<true>(ab, 128u, C, FL * j + lw, a_lds + B * ABUF);
 #pragma unroll
       for (int j = 0; j < 8 / FL; ++j) ld_tile64<true>(aib, (uint32_t)H * C * 2, nv, FL * j + lw, ai_lds + B * ABUF);
+      if (!cvm) {
 #pragma unroll
-      for (int j = 0; j < 8 / FL; ++j) ld_tile64<false>(vb, (uint32_t)H * V * 2, nv, FL * j + lw, v_lds + B * ABUF);
+        for (int j = 0; j < 8 / FL; ++j) ld_tile64<false>(vb, (uint32_t)H * V * 2, nv, FL * j + lw, v_lds + B * ABUF);
+      }
       const uint32_t gl_off = (uint32_t)(l < nv ? l : 0) * (uint32_t)H * 4u;
       if (lw == 0) dma4_(a.gc + t0 * H + h, gl_off, g_lds + B * GBUF);
       if (lw == 1) dma4_(a.beta + t0 * H + h, gl_off, b_lds + B * GBUF);
@@ -340,16 +356,47 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.h_out) + (((c * H + h) * FK + d) * V + vt0 + 8 * c8) * 2) = x;
       }
     };
+    // the folded convolution of v: loader lane L = 64 lw + l forms rows 2 (L / 8), + 1 of 16-byte
+    // column chunk L % 8 of the workgroup's 64 columns, with that chunk's taps in registers for the
+    // whole walk.  The window of chunk it + 1 is loaded after B2 of step it - 1 (compiler-visible
+    // loads, complete at the next step's wait for all loads) and convolved into its buffer after B1
+    // of step it, once the compute waves are done with the chunk that buffer held.
+    const int cL = 64 * lw + l, cch = cL & 7, crp = cL >> 3;
+    const int64_t cc0 = (int64_t)h * V + vt0 + 8 * cch;
+    ConvTaps ctp;
+    ConvWin<2> cwin;
+    if (cvm) load_taps(ctp, a.cv, cc0);
+    auto conv_issue = [&](int64_t it) {
+      const int64_t t0 = bos + it * C;
+      cwin.issue(a.cv, t0 + 2 * crp, bos, t0 + chunk_nv(it), cc0);
+    };
+    auto conv_store = [&](int64_t it, uint32_t Bv) {
+      const int64_t t0 = bos + it * C;
+      cvx4 y[2];
+      cwin.finish(a.cv, ctp, t0 + 2 * crp, bos, n, cc0, y);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = 2 * crp + j;
+        *reinterpret_cast<lds_u32x4*>(reinterpret_cast<lds_b*>(v_lds + Bv * ABUF) + 128 * r + 16 * (cch ^ swz_v(r))) =
+            y[j];
+      }
+    };
     if (ie - ib > 1) prefetch(c_first + ib + 1, bos + (ib + 1) * C, chunk_nv(ib + 1));
     if (ie > ib) {
       small(c_first + ib, bos + ib * C, chunk_nv(ib), 0u);
       wq(bos + ib * C, chunk_nv(ib));
+      if (cvm) {
+        conv_issue(ib);
+        conv_store(ib, 0u);
+        if (ie - ib > 1) conv_issue(ib + 1);
+      }
     }
     for (int64_t it = ib; it < ie; ++it) {
       const uint32_t B = (uint32_t)((it - ib) & 1);
       const int64_t in = it + 1 < ie ? it + 1 : it;       // the last step reloads its own chunk (unused)
       wait_all_loads();
       f_barrier();                                        // B1
+      if (cvm && it + 1 < ie) conv_store(it + 1, B ^ 1u);  // its window arrived with the wait above
       if (it > ib) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
       const unsigned char* kb = reinterpret_cast<const unsigned char*>(ktb + ((c_first + it) * H + h) * (int64_t)(FK * C));
 #pragma unroll
@@ -369,16 +416,15 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       } else {
         if (it + 2 < ie) {
           prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
-          if (kSmall == 7) wait_loads_but<8>();
-          else wait_loads_but<7>();
+          wait_loads_but_n(kSmall + 1);
         } else {
-          if (kSmall == 7) wait_loads_but<7>();
-          else wait_loads_but<6>();
+          wait_loads_but_n(kSmall);
         }
       }
       f_barrier();                                        // B2
       if constexpr (kRc) store_h(c_first + it);           // written by the compute waves before B2
       if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
+      if (cvm && it + 2 < ie) conv_issue(it + 2);
     }
     f_barrier();                                          // the last o tile is in LDS
     if (ie > ib) store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));

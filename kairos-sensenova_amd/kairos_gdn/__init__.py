@@ -12,6 +12,7 @@ from .chunk import (
     chunk_gated_delta_rule,
     chunk_fwd_o,
     chunk_gated_delta_rule_bwd_native,
+    chunk_gated_delta_rule_conv,
     chunk_gated_delta_rule_fwd,
     chunk_gated_delta_rule_fwd_h,
     chunk_gated_delta_rule_gated_norm,
@@ -30,7 +31,7 @@ from . import swap
 
 __all__ = [
     "CHUNK", "ChunkGatedDeltaRuleFunction", "KairosGdnError", "LIB_PATH", "chunk_gated_delta_rule",
-    "chunk_fwd_o", "chunk_gated_delta_rule_bwd_native", "chunk_gated_delta_rule_fwd_h", "chunk_gated_delta_rule_fwd", "chunk_gated_delta_rule_gated_norm", "chunk_local_cumsum", "fwd_h", "fwd_o", "l2norm_fwd", "num_chunks_bound",
+    "chunk_fwd_o", "chunk_gated_delta_rule_bwd_native", "chunk_gated_delta_rule_conv", "chunk_gated_delta_rule_fwd_h", "chunk_gated_delta_rule_fwd", "chunk_gated_delta_rule_gated_norm", "chunk_local_cumsum", "fwd_h", "fwd_o", "l2norm_fwd", "num_chunks_bound",
     "prepare_wy", "recompute_w_u_fwd", "swap", "FusedRMSNormGated", "rms_norm_gated", "rms_norm_gated_fwd",
     "FusedRecurrentFunction", "fused_recurrent_gated_delta_rule", "fused_recurrent_gated_delta_rule_fwd",
     "ShortConvolution", "causal_conv1d", "gdn_gates",

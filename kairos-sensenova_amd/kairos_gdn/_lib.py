@@ -62,6 +62,10 @@ SIGNATURES = {
                                             _i64, _i64, _i64, _i, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p]),
     "kairos_gdn_causal_conv1d_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _i,
                                           _p]),
+    "kairos_gdn_chunk_fwd_conv_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i]),
+    "kairos_gdn_chunk_fwd_conv": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i,
+                                       _p, _p, _p, _p, _fp, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _i,
+                                       _f, _i, _p, _sz, _p]),
     "kairos_gdn_gates_fwd": (_i, [_p, _p, _p, _p, _fp, _p, _i64, _i64, _i, _i, _i, _i, _p]),
     "kairos_gdn_segment_chunks": (_i, [_i64, _i64, _i64, _i64]),
     "kairos_gdn_varlen_maps": (_i, [_p, _i64, _i64, _p, _p, _p]),

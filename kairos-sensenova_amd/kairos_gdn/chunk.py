@@ -212,6 +212,96 @@ def chunk_gated_delta_rule_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch
                                       _norm=(gate, norm_weight, norm_bias, eps, _NORM_ACT[activation]))
 
 
+@torch.no_grad()
+def chunk_gated_delta_rule_conv(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor, g: torch.Tensor,
+                                beta: torch.Tensor, q_conv_weight: torch.Tensor, k_conv_weight: torch.Tensor,
+                                v_conv_weight: torch.Tensor, q_conv_bias: torch.Tensor | None = None,
+                                k_conv_bias: torch.Tensor | None = None, v_conv_bias: torch.Tensor | None = None,
+                                scale: float | None = None, initial_state: torch.Tensor | None = None,
+                                output_final_state: bool = False, conv_state: tuple | None = None,
+                                output_conv_state: bool = False, cu_seqlens: torch.Tensor | None = None,
+                                use_qk_l2norm_in_kernel: bool = False):
+    """The GatedDeltaNet layer's prologue and recurrence in one call: the three ShortConvolutions
+    (kernel size 4, SiLU; fla layers/gated_deltanet.py:234-253) on the projections and
+    chunk_gated_delta_rule on their outputs (:275-285).
+
+    xq, xk [B, T, H*K] and xv [B, T, H*V] are q_proj(h), k_proj(h), v_proj(h) in bf16; g, beta
+    [B, T, H] as for chunk_gated_delta_rule; the conv weights are the ShortConvolutions' ([D, 1, 4]
+    or [D, 4]) with optional biases; conv_state = (q, k, v) caches [N, D, 4] of the previous call or
+    None.  Returns (o [B, T, H, V], final_state fp32 or None, (q, k, v) caches or None), the same
+    values as causal_conv1d on each projection followed by chunk_gated_delta_rule.  At the layer's
+    head dims (K = 256, V a multiple of 64) the convolution runs where the forward stages its rows
+    (no convolved q / k / v round trip through HBM but q once); forward only.
+    """
+    dev = _require_device(xq, xk, xv, g, beta, q_conv_weight, k_conv_weight, v_conv_weight, initial_state)
+    B, T, H = g.shape
+    if beta.shape != g.shape:
+        raise ValueError(f"beta {tuple(beta.shape)} and g {tuple(g.shape)} must have one shape")
+    for n, x in (("xq", xq), ("xk", xk), ("xv", xv)):
+        if x.dim() != 3 or x.shape[:2] != (B, T) or x.shape[-1] % H:
+            raise ValueError(f"{n} must be [B, T, H * d] with B, T, H of g; got {tuple(x.shape)}")
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"{n}: the projections are taken in bf16 (got {x.dtype})")
+    if xk.shape != xq.shape:
+        raise ValueError(f"xq {tuple(xq.shape)} and xk {tuple(xk.shape)} must have one shape")
+    K, V = xq.shape[-1] // H, xv.shape[-1] // H
+    if cu_seqlens is not None and B != 1:
+        raise ValueError(
+            f"The batch size is expected to be 1 rather than {B} when using `cu_seqlens`."
+            f"Please flatten variable-length inputs before processing.")
+    if scale is None:
+        scale = K ** -0.5
+    ws3 = []
+    for n, w, D in (("q", q_conv_weight, H * K), ("k", k_conv_weight, H * K), ("v", v_conv_weight, H * V)):
+        w = w.reshape(w.shape[0], -1)
+        if tuple(w.shape) != (D, 4):
+            raise ValueError(f"{n}_conv_weight must hold [{D}, 4] taps (kernel size 4), got {tuple(w.shape)}")
+        ws3.append(w.contiguous())
+    w_dt = _code(ws3[0], "conv weight")
+    if any(w.dtype != ws3[0].dtype for w in ws3):
+        raise TypeError("the three conv weights must share a dtype")
+    bs3 = []
+    for n, b, D in (("q", q_conv_bias, H * K), ("k", k_conv_bias, H * K), ("v", v_conv_bias, H * V)):
+        if b is not None:
+            if b.numel() != D:
+                raise ValueError(f"{n}_conv_bias must have {D} entries")
+            b = b.reshape(-1).to(ws3[0].dtype).contiguous()
+        bs3.append(b)
+    n_seqs, cu = 0, None
+    if cu_seqlens is not None:
+        cu = _prepare_cu_seqlens(cu_seqlens, dev, T)
+        n_seqs = cu.numel() - 1
+    N = n_seqs if cu is not None else B
+    cin = [None, None, None]
+    if conv_state is not None:
+        for i, (c, D) in enumerate(zip(conv_state, (H * K, H * K, H * V))):
+            if c is not None:
+                if tuple(c.shape) != (N, D, 4):
+                    raise ValueError(f"conv_state[{i}] must have shape {(N, D, 4)}, got {tuple(c.shape)}")
+                cin[i] = c.to(torch.bfloat16).contiguous()
+    cout = [torch.empty(N, D, 4, device=dev, dtype=torch.bfloat16) for D in (H * K, H * K, H * V)] \
+        if output_conv_state else [None, None, None]
+    h0, h0_dt = None, _lib.F32
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (N, H, K, V):
+            raise ValueError(f"initial_state must have shape {(N, H, K, V)}, got {tuple(initial_state.shape)}")
+        h0 = initial_state if initial_state.dtype in (torch.float32, torch.bfloat16) else initial_state.float()
+        h0 = h0.contiguous()
+        h0_dt = _code(h0, "initial_state")
+    xq, xk, xv, g, beta = (x.contiguous() for x in (xq, xk, xv, g, beta))
+    o = torch.empty(B, T, H, V, device=dev, dtype=torch.bfloat16)
+    ht = torch.empty(N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
+    l2 = int(bool(use_qk_l2norm_in_kernel))
+    lib = _lib.load()
+    ws_bytes = lib.kairos_gdn_chunk_fwd_conv_workspace_size(B, T, H, K, V, n_seqs, l2)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("kairos_gdn_chunk_fwd_conv", _ptr(xq), _ptr(xk), _ptr(xv), *(_ptr(w) for w in ws3),
+              *(_ptr(b) for b in bs3), *(_ptr(c) for c in cin), *(_ptr(c) for c in cout), w_dt, _ptr(g),
+              _ptr(beta), _ptr(h0), _ptr(o), _ptr(ht), _ptr(cu), n_seqs, B, T, H, K, V, _code(g, "g"),
+              _code(beta, "beta"), h0_dt, float(scale), l2, _ptr(ws), ws_bytes, _stream(dev))
+    return o, ht, (tuple(cout) if output_conv_state else None)
+
+
 def chunk_gated_delta_rule_bwd_native(q, k, v, g, beta, scale, initial_state, do, dht, cu_seqlens=None,
                                       use_qk_l2norm_in_kernel=False):
     """One native call: gradients of chunk_gated_delta_rule (chunk.py:70-146, 188-213).
