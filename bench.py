@@ -765,6 +765,74 @@ def bench_prologue(args, dev):
     }), flush=True)
 
 
+def bench_prologue_fused(args, dev):
+    """The layer's prologue folded into the forward (kairos_gdn_chunk_fwd_conv) against the same work
+    as two steps (kairos_gdn_causal_conv1d_fwd on q, k with the per-head L2 norm and on v, then
+    kairos_gdn_chunk_fwd), one process, same inputs: the Kairos 4B layer's shape (T=32760, H=20,
+    dk=256, dv=512), bf16 projections, conv caches in and out, h0 and final state.  The value is the
+    fused call's tokens/s; algorithmic bytes = the projections, gates and output once, the states
+    and caches (the convolved q, k, v are not counted: the fused call need not store them)."""
+    from kairos_gdn import _lib
+    B, T, H, K, V, W = 1, args.T, 20, 256, 512, 4
+    gen = torch.Generator(device="cpu").manual_seed(20274)
+    DK, DV = H * K, H * V
+    xs = [torch.randn(B * T, D, generator=gen).to(dev, torch.bfloat16) for D in (DK, DK, DV)]
+    ws = [(0.5 * torch.randn(x.shape[1], W, generator=gen)).to(dev, torch.bfloat16) for x in xs]
+    cin = [torch.randn(B, x.shape[1], W, generator=gen).to(dev, torch.bfloat16) for x in xs]
+    cout = [torch.empty_like(c) for c in cin]
+    ys = [torch.empty_like(x) for x in xs]
+    g = (-torch.nn.functional.softplus(torch.randn(B, T, H, generator=gen))).to(dev)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen)).to(dev, torch.bfloat16)
+    h0 = (0.02 * torch.randn(B, H, K, V, generator=gen)).to(dev)
+    o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws_f = lib.kairos_gdn_chunk_fwd_conv_workspace_size(B, T, H, K, V, 0, 1)
+    ws_s = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    wsf = torch.empty(max(ws_f, 1), dtype=torch.uint8, device=dev)
+    wss = torch.empty(max(ws_s, 1), dtype=torch.uint8, device=dev)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def fused():
+        _lib.call("kairos_gdn_chunk_fwd_conv", *(P(x) for x in xs), *(P(w) for w in ws), None, None, None,
+                  *(P(c) for c in cin), *(P(c) for c in cout), _lib.BF16, P(g), P(beta), P(h0), P(o), P(ht), None, 0,
+                  B, T, H, K, V, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 1, P(wsf), ws_f, sp)
+
+    def two_step():
+        for x, w, y, c0, c1, hd in zip(xs, ws, ys, cin, cout, (K, K, 0)):
+            _lib.call("kairos_gdn_causal_conv1d_fwd", P(x), P(w), None, P(c0), P(y), P(c1), None, 0, B, T, x.shape[1],
+                      W, _lib.BF16, _lib.BF16, 1, hd, sp)
+        _lib.call("kairos_gdn_chunk_fwd", P(ys[0]), P(ys[1]), P(ys[2]), P(g), P(beta), None, None, P(h0), P(o), P(ht),
+                  None, 0, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, P(wss),
+                  ws_s, sp)
+
+    timer = Timer(args)
+    res = timer.run(fused)
+    res2 = Timer(args).run(two_step)
+    wall = res["wall_s"]
+    med_s = res["step_ms"]["median"] / 1e3
+    alg = B * T * (2 * DK + DV) * 2 + B * T * H * (4 + 2) + B * T * H * V * 2 + 2 * B * H * K * V * 4 \
+        + 2 * sum(c.numel() * 2 for c in cin)
+    print(json.dumps({
+        "metric": "GDN layer prologue + chunk-fwd in one call, tokens/s at T=32760,H=20,dk=256,dv=512",
+        "value": T / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": wall * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"kairos_gdn_chunk_fwd_conv B={B} T={T} H={H} dk={K} dv={V}: conv k=4 + SiLU on "
+                               "the q/k/v projections, in-op L2 norm, conv caches in/out, h0, final state; "
+                               "against kairos_gdn_causal_conv1d_fwd x3 + kairos_gdn_chunk_fwd",
+                   "workspace_bytes": ws_f},
+        **timer.fields(res),
+        "two_step_ms": {"median": res2["step_ms"]["median"], "wall": res2["wall_s"] * 1e3,
+                        "cold_median": res2.get("cold_step_ms", {}).get("median")},
+        "speedup_vs_two_step": res2["step_ms"]["median"] / res["step_ms"]["median"],
+        "roofline": {"bound": "hbm", "kernel": "whole call (median step)", "achieved": alg / med_s / 1e9,
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS, "alg_bytes": alg,
+                     "traffic": None},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -795,6 +863,9 @@ def main():
     ap.add_argument("--backward", action="store_true",
                     help="measure the backward pass (kairos_gdn_chunk_bwd) at config 2's shape (--model-shape: the "
                          "Kairos layer's dk=256, dv=512); prints its own JSON line")
+    ap.add_argument("--prologue-fused", action="store_true",
+                    help="the layer's prologue folded into the forward (kairos_gdn_chunk_fwd_conv) against the "
+                         "two-step conv + forward, at the Kairos 4B layer shape")
     ap.add_argument("--prologue", action="store_true",
                     help="measure the layer prologue (causal conv + SiLU + q/k L2 norm, gates) at the model shape")
     args = ap.parse_args()
@@ -826,6 +897,8 @@ def main():
         bench_model_shape(args, dev)
     elif args.recurrent:
         bench_recurrent(args, dev)
+    elif args.prologue_fused:
+        bench_prologue_fused(args, dev)
     elif args.prologue:
         bench_prologue(args, dev)
     elif args.config == 4:

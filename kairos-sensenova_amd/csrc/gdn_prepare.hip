@@ -227,8 +227,6 @@ __device__ __forceinline__ void prepare_body(const PrepareArgs& a, int V) {
         win.finish(a.ck, tp, t0 + 2 * pr, loc.bos, loc.n, c0, y);
         kraw[ch][0].v = __builtin_bit_cast(bf16x8, y[0]);
         kraw[ch][1].v = __builtin_bit_cast(bf16x8, y[1]);
-        asm volatile("" ::: "memory");                   // one window's registers live at a time
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
   } else {
@@ -256,8 +254,6 @@ __device__ __forceinline__ void prepare_body(const PrepareArgs& a, int V) {
           cvx4 y[1];
           win.finish(a.cq, tp, t, loc.bos, loc.n, c0, y);
           qraw[ks].v = __builtin_bit_cast(bf16x8, y[0]);
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_sched_barrier(0);
         }
       }
     } else {
@@ -715,7 +711,8 @@ int launch_prepare(const PrepareArgs& a, int compute_dtype, int k_dtype, int K, 
   // the folded L2 norm and the folded convolution live in the compact plan
   if ((a.l2 || a.ck.x || a.cq.x) && !(compact && k_dtype == DT_BF16)) return -2;
   if ((a.ck.x || a.cq.x) && K != 256) return -2;        // the folded convolution is built for K = 256
-  if ((a.ck.x || a.cq.x) && (a.aqk_out == nullptr) != (a.cq.x == nullptr)) return -2;
+  if ((a.ck.x || a.cq.x) && ((a.aqk_out == nullptr) != (a.cq.x == nullptr) || (a.ck.x == nullptr) != (a.cq.x == nullptr)))
+    return -2;                                            // k and q are convolved together, q for Aqk
 #define KGDN_PREP_CASE(TC, TK, KK)                                                                  \
   if (K == KK) {                                                                                    \
     if constexpr (std::is_same<TC, bf16>::value)                                                    \

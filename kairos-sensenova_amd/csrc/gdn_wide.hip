@@ -106,14 +106,15 @@ __device__ __forceinline__ void wait_loads_but() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
 }
-// the same for a count known only at run time (wave-uniform, 4 .. 8)
+// the same for a count known only at run time (wave-uniform, 4 .. 15; larger counts wait for 15)
 __device__ __forceinline__ void wait_loads_but_n(int n) {
   switch (n) {
-    case 4: wait_loads_but<4>(); break;
-    case 5: wait_loads_but<5>(); break;
-    case 6: wait_loads_but<6>(); break;
-    case 7: wait_loads_but<7>(); break;
-    default: wait_loads_but<8>(); break;
+#define KGDN_WAIT_CASE(N) \
+    case N: wait_loads_but<N>(); break;
+    KGDN_WAIT_CASE(4) KGDN_WAIT_CASE(5) KGDN_WAIT_CASE(6) KGDN_WAIT_CASE(7) KGDN_WAIT_CASE(8) KGDN_WAIT_CASE(9)
+    KGDN_WAIT_CASE(10) KGDN_WAIT_CASE(11) KGDN_WAIT_CASE(12) KGDN_WAIT_CASE(13) KGDN_WAIT_CASE(14)
+#undef KGDN_WAIT_CASE
+    default: wait_loads_but<15>(); break;
   }
 }
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
@@ -358,22 +359,23 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     };
     // the folded convolution of v: loader lane L = 64 lw + l forms rows 2 (L / 8), + 1 of 16-byte
     // column chunk L % 8 of the workgroup's 64 columns, with that chunk's taps in registers for the
-    // whole walk.  The window of chunk it + 1 is loaded after B2 of step it - 1 (compiler-visible
-    // loads, complete at the next step's wait for all loads) and convolved into its buffer after B1
-    // of step it, once the compute waves are done with the chunk that buffer held.
+    // whole walk.  The window of chunk c (window buffer (c - ib) % 2) is loaded after B1 of step c - 2
+    // (compiler-visible loads, counted in the wait for k^T and complete at the next step's wait for
+    // all loads) and convolved into its v buffer after B2 of step c - 1, where the loader waves are
+    // otherwise idle and the compute waves are done with the chunk that buffer held.
     const int cL = 64 * lw + l, cch = cL & 7, crp = cL >> 3;
     const int64_t cc0 = (int64_t)h * V + vt0 + 8 * cch;
     ConvTaps ctp;
-    ConvWin<2> cwin;
+    ConvWin<2> cwa, cwb;                              // windows of chunks ib, ib + 2, ... / ib + 1, ...
     if (cvm) load_taps(ctp, a.cv, cc0);
-    auto conv_issue = [&](int64_t it) {
+    auto conv_issue = [&](ConvWin<2>& w, int64_t it) {
       const int64_t t0 = bos + it * C;
-      cwin.issue(a.cv, t0 + 2 * crp, bos, t0 + chunk_nv(it), cc0);
+      w.issue(a.cv, t0 + 2 * crp, bos, t0 + chunk_nv(it), cc0);
     };
-    auto conv_store = [&](int64_t it, uint32_t Bv) {
+    auto conv_store = [&](ConvWin<2>& w, int64_t it, uint32_t Bv) {
       const int64_t t0 = bos + it * C;
       cvx4 y[2];
-      cwin.finish(a.cv, ctp, t0 + 2 * crp, bos, n, cc0, y);
+      w.finish(a.cv, ctp, t0 + 2 * crp, bos, n, cc0, y);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int r = 2 * crp + j;
@@ -386,22 +388,28 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       small(c_first + ib, bos + ib * C, chunk_nv(ib), 0u);
       wq(bos + ib * C, chunk_nv(ib));
       if (cvm) {
-        conv_issue(ib);
-        conv_store(ib, 0u);
-        if (ie - ib > 1) conv_issue(ib + 1);
+        conv_issue(cwa, ib);
+        conv_store(cwa, ib, 0u);
+        if (ie - ib > 1) conv_issue(cwb, ib + 1);
       }
     }
-    for (int64_t it = ib; it < ie; ++it) {
-      const uint32_t B = (uint32_t)((it - ib) & 1);
+    // one step; PB = (it - ib) % 2 at compile time, so that the window buffers are named registers
+    auto loader_step = [&](auto PB, int64_t it) {
+      constexpr int PAR = decltype(PB)::value;
+      ConvWin<2>& w_next = PAR ? cwb : cwa;              // chunk it + 2
+      ConvWin<2>& w_now = PAR ? cwa : cwb;               // chunk it + 1
+      const uint32_t B = (uint32_t)PAR;
       const int64_t in = it + 1 < ie ? it + 1 : it;       // the last step reloads its own chunk (unused)
       wait_all_loads();
       f_barrier();                                        // B1
-      if (cvm && it + 1 < ie) conv_store(it + 1, B ^ 1u);  // its window arrived with the wait above
       if (it > ib) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
       const unsigned char* kb = reinterpret_cast<const unsigned char*>(ktb + ((c_first + it) * H + h) * (int64_t)(FK * C));
 #pragma unroll
       for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(kb, 128u, FK, FL * j + lw, k_lds);
       small(c_first + in, bos + in * C, chunk_nv(in), B ^ 1u);
+      // the window of chunk it + 2 (convolved after B2 of step it + 1)
+      const int nwin = (cvm && it + 2 < ie) ? kConvW + 1 : 0;
+      if (nwin) conv_issue(w_next, it + 2);
       // this wave's k^T loads landed; the later ones (6 + gc / beta + the prefetch) stay in flight
       if constexpr (kRc) {                                // small: 4, and gc / beta from loaders 0 / 1
         if (it + 2 < ie) {
@@ -416,7 +424,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       } else {
         if (it + 2 < ie) {
           prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
-          wait_loads_but_n(kSmall + 1);
+          wait_loads_but_n(kSmall + nwin + 1);
         } else {
           wait_loads_but_n(kSmall);
         }
@@ -424,7 +432,11 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       f_barrier();                                        // B2
       if constexpr (kRc) store_h(c_first + it);           // written by the compute waves before B2
       if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
-      if (cvm && it + 2 < ie) conv_issue(it + 2);
+      if (cvm && it + 1 < ie) conv_store(w_now, it + 1, B ^ 1u);  // its window arrived before B1
+    };
+    for (int64_t it = ib; it < ie; it += 2) {
+      loader_step(std::integral_constant<int, 0>{}, it);
+      if (it + 1 < ie) loader_step(std::integral_constant<int, 1>{}, it + 1);
     }
     f_barrier();                                          // the last o tile is in LDS
     if (ie > ib) store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));
