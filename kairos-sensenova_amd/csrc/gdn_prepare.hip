@@ -216,15 +216,21 @@ __device__ __forceinline__ void prepare_body(const PrepareArgs& a, int V) {
   }
   if (conv_k) {
     if constexpr (kConvOk) {
+      // two windows in flight: the next one's loads go out before the current one is convolved
+      ConvWin<2> wa, wb;
+      auto k_issue = [&](ConvWin<2>& w, int ch) {
+        w.issue(a.ck, t0 + 2 * pr, loc.bos, t0 + nv, (int64_t)h * K + cg * (K / 8) + 8 * ch);
+      };
+      k_issue(wa, 0);
 #pragma unroll
       for (int ch = 0; ch < K / 64; ++ch) {
+        ConvWin<2>& cur = (ch & 1) ? wb : wa;
+        ConvWin<2>& nxt = (ch & 1) ? wa : wb;
+        if (ch + 1 < K / 64) k_issue(nxt, ch + 1);
         const int cl = cg * (K / 8) + 8 * ch;            // channel within the head
-        const int64_t c0 = (int64_t)h * K + cl;
-        ConvWin<2> win;
-        win.issue(a.ck, t0 + 2 * pr, loc.bos, t0 + nv, c0);
         const ConvTapsLds tp{s_tk + 4 * cl, a.ck.b ? s_tk + 4 * K + cl : nullptr};
         cvx4 y[2];
-        win.finish(a.ck, tp, t0 + 2 * pr, loc.bos, loc.n, c0, y);
+        cur.finish(a.ck, tp, t0 + 2 * pr, loc.bos, loc.n, (int64_t)h * K + cl, y);
         kraw[ch][0].v = __builtin_bit_cast(bf16x8, y[0]);
         kraw[ch][1].v = __builtin_bit_cast(bf16x8, y[1]);
       }
@@ -243,16 +249,21 @@ __device__ __forceinline__ void prepare_body(const PrepareArgs& a, int V) {
     const int qr = 16 * wid + lc;
     if (conv_q) {
       if constexpr (kConvOk) {
+        const int64_t t = t0 + (qr < nv ? qr : 0);
+        ConvWin<1> wa, wb;
+        auto q_issue = [&](ConvWin<1>& w, int ks) {
+          w.issue(a.cq, t, loc.bos, t0 + nv, (int64_t)h * K + 32 * ks + 8 * lg);
+        };
+        q_issue(wa, 0);
 #pragma unroll
         for (int ks = 0; ks < K / 32; ++ks) {
+          ConvWin<1>& cur = (ks & 1) ? wb : wa;
+          ConvWin<1>& nxt = (ks & 1) ? wa : wb;
+          if (ks + 1 < K / 32) q_issue(nxt, ks + 1);
           const int cl = 32 * ks + 8 * lg;
-          const int64_t c0 = (int64_t)h * K + cl;
-          const int64_t t = t0 + (qr < nv ? qr : 0);
-          ConvWin<1> win;
-          win.issue(a.cq, t, loc.bos, t0 + nv, c0);
           const ConvTapsLds tp{s_tq + 4 * cl, a.cq.b ? s_tq + 4 * K + cl : nullptr};
           cvx4 y[1];
-          win.finish(a.cq, tp, t, loc.bos, loc.n, c0, y);
+          cur.finish(a.cq, tp, t, loc.bos, loc.n, (int64_t)h * K + cl, y);
           qraw[ks].v = __builtin_bit_cast(bf16x8, y[0]);
         }
       }
