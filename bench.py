@@ -547,18 +547,32 @@ def bench_backward(args, dev):
 # other rows of the path (each prints its own line)
 # ---------------------------------------------------------------------------
 def bench_gated_norm(args, dev):
-    """Config 2's forward with the layer's output norm (kairos_gdn_chunk_fwd_gated_norm): the norm fused
-    into the segment scan's output kernel against the same call with the separate norm kernel
-    (KAIROS_GDN_FUSED_NORM=0), A/B in one process."""
+    """The forward with the layer's output norm (kairos_gdn_chunk_fwd_gated_norm): the norm folded into
+    the forward (the segment scan's output kernel at config 2; with --model-shape, dk=256 / dv=512, the
+    fused K = 256 kernel's loader waves) against the same call with the separate norm kernel
+    (KAIROS_GDN_FUSED_NORM=0), A/B in one process.  --l2norm passes unnormalised q, k with the in-op
+    L2 norm (the layer's own mode)."""
     from kairos_gdn import _lib
     cfg = CONFIGS[2]
     B, T, H, K, V = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"]
+    if args.model_shape:
+        B, T, H, K, V = 1, args.T, 20, 256, 512
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, cfg["seed"], n_states=B, device=dev)
+    l2 = 1 if args.l2norm else 0
     gen = torch.Generator(device="cpu").manual_seed(20263)
+    if l2:
+        q = (q.float() * torch.rand(B, T, H, 1, generator=gen).add_(0.5).to(dev)).to(torch.bfloat16)
+        k = (k.float() * torch.rand(B, T, H, 1, generator=gen).add_(0.5).to(dev)).to(torch.bfloat16)
     gate = torch.randn(B, T, H, V, generator=gen).to(dev, torch.bfloat16)
     w = torch.rand(V, generator=gen).add_(0.5).to(dev)
     lib = _lib.load()
-    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    fold_prev = os.environ.get("KAIROS_GDN_WIDE_NORM_FOLD")
+    os.environ["KAIROS_GDN_WIDE_NORM_FOLD"] = "1"        # size the workspace for either form
+    ws_bytes = lib.kairos_gdn_chunk_fwd_gated_norm_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, l2)
+    if fold_prev is None:
+        os.environ.pop("KAIROS_GDN_WIDE_NORM_FOLD")
+    else:
+        os.environ["KAIROS_GDN_WIDE_NORM_FOLD"] = fold_prev
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     y = torch.empty_like(v)
     ht = torch.empty(B, H, K, V, dtype=torch.float32, device=dev)
@@ -568,31 +582,38 @@ def bench_gated_norm(args, dev):
     def step():
         _lib.call("kairos_gdn_chunk_fwd_gated_norm", P(q), P(k), P(v), P(g), P(beta), None, None, P(h0), P(gate),
                   P(w), None, P(y), P(ht), None, 0, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16,
-                  _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, 0, 1e-5, _lib.ACT_SWISH, P(ws), ws_bytes, sp)
+                  _lib.F32, _lib.BF16, _lib.F32, K ** -0.5, l2, 1e-5, _lib.ACT_SWISH, P(ws), ws_bytes, sp)
 
-    prev = os.environ.get("KAIROS_GDN_FUSED_NORM")
+    # at the layer shape "fused" is the norm folded into the fused K = 256 kernel (opt-in there)
+    names = ("KAIROS_GDN_FUSED_NORM", "KAIROS_GDN_WIDE_NORM_FOLD")
+    prev = {n: os.environ.get(n) for n in names}
     out = {}
     try:
         for form, flag in (("separate", "0"), ("fused", "1")):
             os.environ["KAIROS_GDN_FUSED_NORM"] = flag
+            os.environ["KAIROS_GDN_WIDE_NORM_FOLD"] = flag
             timer = Timer(args)
             out[form] = (timer, timer.run(step))
     finally:
-        if prev is None:
-            os.environ.pop("KAIROS_GDN_FUSED_NORM", None)
-        else:
-            os.environ["KAIROS_GDN_FUSED_NORM"] = prev
+        for n, v in prev.items():
+            if v is None:
+                os.environ.pop(n, None)
+            else:
+                os.environ[n] = v
     timer, res = out["fused"]
     sep = out["separate"][1]
     med = res["step_ms"]["median"]
+    shape = f"T={T},H={H},dk={K},dv={V}" if args.model_shape else "T=32760,H=20,d=128"
     print(json.dumps({
-        "metric": "GDN chunk-fwd + gated RMSNorm (the layer's o_norm) tokens/s at T=32760,H=20,d=128",
+        "metric": f"GDN chunk-fwd + gated RMSNorm (the layer's o_norm) tokens/s at {shape}",
         "value": B * T / (med / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": res["wall_s"] * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "BASELINE config 2 forward with FusedRMSNormGated(128, eps=1e-5, swish) on o, "
-                               "bf16 gate, fp32 weight, through kairos_gdn_chunk_fwd_gated_norm",
-                   "B": B, "T": T, "H": H, "dk": K, "dv": V},
+        "config": {"workload": ("the Kairos layer shape" if args.model_shape else "BASELINE config 2") +
+                               f" forward with FusedRMSNormGated({V}, eps=1e-5, swish) on o, bf16 gate, fp32 "
+                               "weight, through kairos_gdn_chunk_fwd_gated_norm" +
+                               (", use_qk_l2norm_in_kernel=True (unnormalised q, k)" if l2 else ""),
+                   "B": B, "T": T, "H": H, "dk": K, "dv": V, "workspace_bytes": ws_bytes},
         **timer.fields(res),
         "separate_norm_kernel": {"median_ms": sep["step_ms"]["median"], "cold_median_ms":
                                  (sep.get("cold_step_ms") or {}).get("median")},
@@ -854,8 +875,8 @@ def main():
     ap.add_argument("--epilogue", action="store_true",
                     help="measure only the gated RMSNorm epilogue (kairos_gdn_rms_norm_gated) on o-shaped rows")
     ap.add_argument("--gated-norm", action="store_true",
-                    help="measure config 2's forward with the layer's gated RMSNorm (fused output epilogue "
-                         "against the separate norm kernel)")
+                    help="measure the forward with the layer's gated RMSNorm (folded into the forward against "
+                         "the separate norm kernel); config 2, or the layer shape with --model-shape")
     ap.add_argument("--model-shape", action="store_true",
                     help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T")
     ap.add_argument("--recurrent", action="store_true",

@@ -91,10 +91,16 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
  * of o; gate: [B*T, H, V] in gate_dtype (fp32 or bf16, 16-byte aligned);
  * norm_weight / norm_bias: [V] in norm_w_dtype or NULL; eps and activation as
  * kairos_gdn_rms_norm_gated.  V at most 512.  The workspace is
- * kairos_gdn_chunk_fwd_workspace_size()'s.  The norm is applied to o rounded
- * to its storage dtype, as the two reference calls do; where the segment scan
- * runs with a bf16 gate it is computed in the output kernel (o never reaches
- * HBM), otherwise by the norm kernel on y in place. */
+ * kairos_gdn_chunk_fwd_gated_norm_workspace_size()'s (a workspace of
+ * kairos_gdn_chunk_fwd_workspace_size() bytes is also accepted: the norm then
+ * runs as a pass of its own).  The norm is applied to o rounded to its storage
+ * dtype, as the two reference calls do.  With a bf16 gate and head dims 64 /
+ * 128 it is computed in the segment scan's output kernel (o never reaches
+ * HBM); with the environment variable KAIROS_GDN_WIDE_NORM_FOLD=1 also in the
+ * fused K = 256 kernel (V a multiple of 64), whose workgroups of one head
+ * exchange per-token sums of squares through the workspace (off by default:
+ * slower there than the norm kernel after the forward); otherwise the norm
+ * kernel runs on y in place. */
 int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
                                     const float* q_scale, const float* k_scale, const void* initial_state,
                                     const void* gate, const void* norm_weight, const void* norm_bias, void* y,
@@ -103,6 +109,15 @@ int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v,
                                     int g_dtype, int beta_dtype, int h0_dtype, int gate_dtype, int norm_w_dtype,
                                     float scale, int use_qk_l2norm, float eps, int activation, void* workspace,
                                     size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace kairos_gdn_chunk_fwd_gated_norm needs:
+ * kairos_gdn_chunk_fwd_workspace_size() plus, when the norm is folded into
+ * the fused K = 256 form (KAIROS_GDN_WIDE_NORM_FOLD=1), 4 KiB per (chunk,
+ * head) for the exchanged sums of squares.  No counterpart in the reference
+ * (its norm is a separate module). */
+size_t kairos_gdn_chunk_fwd_gated_norm_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                                      int64_t n_seqs, int qk_dtype, int v_dtype,
+                                                      int use_qk_l2norm);
 
 /* kairos_gdn_chunk_fwd without a workspace argument: the call allocates
  * nothing (no hipMalloc / hipFree, no allocating library routine) and takes

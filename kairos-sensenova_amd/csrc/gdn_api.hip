@@ -9,8 +9,12 @@
 // The stage entry points (kairos_gdn_prepare_wy, _fwd_h, _fwd_o, ...) run
 // one reference stage each with the stage kernels and the reference's
 // intermediate tensors.
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <ctime>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -417,7 +421,7 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
                const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
                const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
                Carver& cv, hipStream_t s, bool may_fork, bool l2 = false,
-               const kgdn::ConvIn* conv3 = nullptr) {
+               const kgdn::ConvIn* conv3 = nullptr, const kgdn::WideFusedArgs* wnorm = nullptr) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(G.B * G.T * G.H);
   const int K = (int)G.K, V = (int)G.V, H = (int)G.H;
@@ -477,6 +481,12 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
   if (conv3) {
     fa.q = q_conv;
     fa.cv = conv3[2];
+  }
+  if (wnorm) {                                            // the gated norm in place of the o stores
+    if (!wide) return fail(KAIROS_GDN_EINVAL, "the gated norm is folded only into the fused K = 256 form");
+    fa.ngate = wnorm->ngate; fa.nw = wnorm->nw; fa.nb = wnorm->nb; fa.nw_dtype = wnorm->nw_dtype;
+    fa.neps = wnorm->neps; fa.nsigmoid_only = wnorm->nsigmoid_only; fa.nss = wnorm->nss; fa.nepoch = wnorm->nepoch;
+    fa.nss_chunks = G.nc;
   }
   if (wide && G.nc > 0 && may_fork && cu_seqlens == nullptr) {
     const int64_t nt = (G.T + kgdn::C - 1) / kgdn::C;
@@ -673,6 +683,28 @@ static bool fused_norm_on(const NormEpilogue* epi) {
   return !(e && e[0] == '0' && e[1] == 0);
 }
 
+// With KAIROS_GDN_WIDE_NORM_FOLD=1 the fused K = 256 form takes the epilogue in its loader waves (bf16
+// gate, V a multiple of 64 up to 512) when the workspace also holds its exchange buffer
+// (kairos_gdn_chunk_fwd_gated_norm_workspace_size counts it then).  Off by default: measured at the Kairos
+// layer shape the folded norm makes the call slower than the forward followed by the norm kernel
+// (3.04 against 1.90 ms): the fused kernel's step is bound by its loader waves, which share the SIMDs
+// with the compute waves, and the norm adds its gate and o rows to their loads and its sigmoid and
+// scaling to their VALU issue.
+static bool wide_norm_on(const NormEpilogue* epi, int cdt, int qk_dtype, int64_t K, int64_t V) {
+  const char* e = std::getenv("KAIROS_GDN_WIDE_NORM_FOLD");
+  return e && e[0] == '1' && e[1] == 0 && fused_norm_on(epi) && !kgdn::seg_fwd_supported(cdt, (int)K, (int)V) &&
+         use_wide_fused(cdt, qk_dtype, K, V) && V % 64 == 0 && V <= 512;
+}
+
+// Tag of one call's exchange entries: a per-process start (time and pid) plus a call count, never 0
+static unsigned next_norm_epoch() {
+  static std::atomic<unsigned> ctr{0};
+  static const unsigned start = (unsigned)std::time(nullptr) * 2654435761u ^ (unsigned)getpid() * 40503u;
+  unsigned e;
+  do e = start + ctr.fetch_add(1, std::memory_order_relaxed); while (e == 0);
+  return e;
+}
+
 // y = gated RMSNorm of y in place (each element is read and written by the same lane)
 static int norm_in_place(void* y, int y_dtype, const NormEpilogue& e, int64_t rows, int64_t D, hipStream_t s) {
   if (rows == 0) return 0;
@@ -722,6 +754,16 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
   Carver cv{static_cast<char*>(workspace)};
   if (!kgdn::seg_fwd_supported(cdt, (int)K, (int)V)) {
     const bool wide = use_wide_fused(cdt, qk_dtype, K, V);
+    // the gated norm in the fused K = 256 form, given room for its exchange buffer beyond `need`
+    kgdn::WideFusedArgs wn{};
+    const size_t nb = kgdn::wide_norm_bytes(G.nc, H);
+    const bool wfold = any_tokens && wide_norm_on(epi, cdt, qk_dtype, K, V) && workspace_bytes >= need + nb;
+    if (wfold) {
+      wn.ngate = epi->gate; wn.nw = epi->w; wn.nb = epi->b; wn.nw_dtype = epi->w_dtype;
+      wn.neps = epi->eps; wn.nsigmoid_only = epi->sigmoid_only;
+      wn.nss = reinterpret_cast<unsigned long long*>(static_cast<char*>(workspace) + need);
+      wn.nepoch = next_norm_epoch();
+    }
     if (use_qk_l2norm && any_tokens && !wide) {
       void* qn = cv.take(tok * K * dt_size(qk_dtype));
       void* kn = cv.take(tok * K * dt_size(qk_dtype));
@@ -732,9 +774,9 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
     }
     if (int rc = run_staged(G, q, k, v, g, beta, q_scale, k_scale, initial_state, h0_dtype, o, final_state,
                             cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s, profile,
-                            wide && use_qk_l2norm != 0))
+                            wide && use_qk_l2norm != 0, nullptr, wfold ? &wn : nullptr))
       return rc;
-    if (epi)
+    if (epi && !wfold)
       if (int rc = norm_in_place(o, v_dtype, *epi, (int64_t)tok, V, s)) return rc;
     return ok();
   }
@@ -822,6 +864,16 @@ int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v,
   return chunk_fwd_impl(what, true, q, k, v, g, beta, q_scale, k_scale, initial_state, y, final_state, cu_seqlens,
                         n_seqs, B, T, H, K, V, qk_dtype, v_dtype, g_dtype, beta_dtype, h0_dtype, scale,
                         use_qk_l2norm, workspace, workspace_bytes, stream, &epi);
+}
+
+size_t kairos_gdn_chunk_fwd_gated_norm_workspace_size(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                                                      int64_t n_seqs, int qk_dtype, int v_dtype, int use_qk_l2norm) {
+  const size_t need = kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, qk_dtype, v_dtype, use_qk_l2norm);
+  if (need == 0 && (B <= 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || n_seqs < 0)) return 0;
+  const int cdt = compute_dtype(qk_dtype, v_dtype);
+  const NormEpilogue probe{nullptr, nullptr, nullptr, KAIROS_GDN_BF16, KAIROS_GDN_F32, 0.f, 0};
+  if (cdt < 0 || !wide_norm_on(&probe, cdt, qk_dtype, K, V)) return need;
+  return need + kgdn::wide_norm_bytes(chunks_bound(B, T, n_seqs), H);
 }
 
 size_t kairos_gdn_chunk_fwd_noalloc_max_bytes(void) { return kScratchBytes; }

@@ -133,7 +133,23 @@ struct WideFusedArgs {
   const float* qs;        // [B*T, H] fp32 rstd of the q rows (the in-op L2 norm: q is raw, k^T, w and Aqk
                           // come normalised from prepare), or nullptr
   ConvIn cv;              // with cv.x: v formed from its projection by the loader waves (v unused)
+  // The layer's gated RMSNorm on o (fla modules/fused_norm_gate.py:42-127), with ngate: o is replaced
+  // by y = bf16(o) rstd w [+ b] times g sigmoid(g) (or sigmoid(g)), rstd over the V columns of a token.
+  // A token's row spans the V / 64 workgroups of its head, which exchange per-token sums of squares
+  // through nss: entry ((chunk H + h) 64 + t) 8 + tile holds the sum in its low word and nepoch, the
+  // call's tag, in its high word (no reset between calls; V <= 512).
+  const void* ngate;      // [B*T, H, V] bf16, or nullptr (no norm)
+  const void* nw;         // [V] in nw_dtype, or nullptr (ones)
+  const void* nb;         // [V] in nw_dtype, or nullptr (zeros)
+  int nw_dtype;
+  float neps;
+  int nsigmoid_only;
+  unsigned long long* nss;  // [nss_chunks, H, 64, 8] tagged sums, then a 1 KB line that is written, never read
+  int64_t nss_chunks;
+  unsigned int nepoch;
 };
+// Bytes of WideFusedArgs::nss for nc chunks of H heads
+inline size_t wide_norm_bytes(int64_t nc, int64_t H) { return (size_t)nc * H * 64 * 8 * 8 + 1024; }
 bool wide_fused_supported(int compute_dtype, int qk_dtype, int K, int V);
 int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s);
 // An empty one-workgroup kernel: a point in a stream's order that an event can mark.

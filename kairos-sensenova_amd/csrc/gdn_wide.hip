@@ -106,15 +106,17 @@ __device__ __forceinline__ void wait_loads_but() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
 }
-// the same for a count known only at run time (wave-uniform, 4 .. 15; larger counts wait for 15)
+// the same for a count known only at run time (wave-uniform, 4 .. 24; larger counts wait for 24)
 __device__ __forceinline__ void wait_loads_but_n(int n) {
   switch (n) {
 #define KGDN_WAIT_CASE(N) \
     case N: wait_loads_but<N>(); break;
     KGDN_WAIT_CASE(4) KGDN_WAIT_CASE(5) KGDN_WAIT_CASE(6) KGDN_WAIT_CASE(7) KGDN_WAIT_CASE(8) KGDN_WAIT_CASE(9)
     KGDN_WAIT_CASE(10) KGDN_WAIT_CASE(11) KGDN_WAIT_CASE(12) KGDN_WAIT_CASE(13) KGDN_WAIT_CASE(14)
+    KGDN_WAIT_CASE(15) KGDN_WAIT_CASE(16) KGDN_WAIT_CASE(17) KGDN_WAIT_CASE(18) KGDN_WAIT_CASE(19)
+    KGDN_WAIT_CASE(20) KGDN_WAIT_CASE(21) KGDN_WAIT_CASE(22) KGDN_WAIT_CASE(23)
 #undef KGDN_WAIT_CASE
-    default: wait_loads_but<15>(); break;
+    default: wait_loads_but<24>(); break;
   }
 }
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
@@ -223,7 +225,12 @@ __device__ __forceinline__ void ld_tile64(const unsigned char* base, uint32_t ro
 // kRc: the backward's recompute of the forward (chunk_delta_h.py:52-224 alone): the state before each
 // chunk (bf16, through the q half of the w / q tile, which q does not use here) and v_new (through the o
 // tile) leave as whole rows stored by the loader waves; q, Aqk and the output products are skipped.
-template <bool kRc>
+// the gated norm's exchange: how many times a workgroup loads a share again while the other workgroups of
+// its head have not yet published it (each try a sleep of ~128 clocks and a load, ~1-2 us: ~25 ms in all);
+// a share still missing then makes its token's rows NaN rather than holding the GPU
+constexpr int kNormSpinMax = 1 << 14;
+
+template <bool kRc, bool kNorm>
 __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedArgs a, int V, int total_units) {
   // LDS: w and q of the chunk (adjacent: q reads are w reads + 32 KB), k^T of the chunk, and two
   // buffer sets of the chunk's small tiles: Aqk, Ai, the v tile of the workgroup's 64 columns, gc, beta
@@ -272,7 +279,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
   const bool qn = !kRc && a.qs != nullptr;
   // the layer's prologue folded in: the loader waves form the workgroup's v tile from the projection
   // (short convolution + SiLU) instead of loading v
-  const bool cvm = !kRc && a.cv.x != nullptr;
+  const bool cvm = !kRc && !kNorm && a.cv.x != nullptr;
   const bf16* aqb = reinterpret_cast<const bf16*>(a.aqk);
   const bf16* ktb = reinterpret_cast<const bf16*>(a.kT);
 
@@ -357,6 +364,129 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(a.h_out) + (((c * H + h) * FK + d) * V + vt0 + 8 * c8) * 2) = x;
       }
     };
+    // ---- kNorm: the layer's gated RMSNorm (fused_norm_gate.py:42-127) over the o the loaders store.
+    //      Lane (lw, l) owns the rows store_o moves, tokens t_j = 8 (FL j + lw) + l / 8, columns
+    //      vt0 + 8 (l % 8) .. + 7.  Chunk c: in step c + 1 o goes out as before and the workgroup's
+    //      share of each token's sum of squares (its 64 columns, from the o tile in LDS) is published
+    //      to nss, tagged with the call's epoch; in step c + 3 the head's V / 64 shares of each token,
+    //      its gate row and its o row (back from L2) are loaded; in step c + 4, any share without the
+    //      call's tag is loaded again until it has it, and y replaces o.  The shares travel as single
+    //      8-byte agent-scope atomics, so a matching tag vouches for its value; the head's workgroups run
+    //      in step, so a share is normally in place two steps before it is loaded.  The loaders bound
+    //      the step: everything here runs after the k^T loads are issued, while the loaders would wait
+    //      for them anyway, and every memory instruction from the publication on executes on all lanes
+    //      (masked rows go to a dummy line past the shares), so the counted wait before B2 stays exact.
+    const int nvt_h = V / FVT, vtile = vt0 / FVT, nc8 = l & 7;
+    u32x4 no[2], ng[2];
+    unsigned long long nps[2];
+    float nsh[2];
+    float nwv[8], nbv[8];
+    if constexpr (kNorm) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int col = vt0 + 8 * nc8 + e;
+        nwv[e] = a.nw == nullptr ? 1.f
+                 : a.nw_dtype == DT_F32 ? reinterpret_cast<const float*>(a.nw)[col]
+                                        : (float)reinterpret_cast<const bf16*>(a.nw)[col];
+        nbv[e] = a.nb == nullptr ? 0.f
+                 : a.nw_dtype == DT_F32 ? reinterpret_cast<const float*>(a.nb)[col]
+                                        : (float)reinterpret_cast<const bf16*>(a.nb)[col];
+      }
+    }
+    const unsigned long long ntag = (unsigned long long)a.nepoch << 32;
+    auto ntok = [&](int j) { return 8 * (FL * j + lw) + (l >> 3); };
+    auto nslot = [&](int64_t c, int t) { return a.nss + (((c_first + c) * H + h) * C + t) * 8; };
+    // the dummy line: one 16-byte slot per lane past the last share (written, never read)
+    u32x4* const ndummy = reinterpret_cast<u32x4*>(a.nss + (size_t)a.nss_chunks * H * C * 8) + l;
+    // o of chunk c from LDS to HBM (store_o's rows) and the workgroup's shares of its tokens into nsh
+    auto n_store_share = [&](int64_t c) {
+      const int64_t t0 = bos + c * C;
+      const int nv = chunk_nv(c);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int t = ntok(j);
+        const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (nc8 ^ swz_o(t)));
+        if (t < nv) *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(a.o) + ((t0 + t) * H + h) * V + vt0 + 8 * nc8) = x;
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = __uint_as_float(x[e] << 16), x1 = __uint_as_float(x[e] & 0xffff0000u);
+          ss = fmaf(x0, x0, ss);
+          ss = fmaf(x1, x1, ss);
+        }
+        ss += __shfl_xor(ss, 4, WAVE);
+        ss += __shfl_xor(ss, 2, WAVE);
+        ss += __shfl_xor(ss, 1, WAVE);
+        nsh[j] = ss;
+      }
+    };
+    // two store instructions (the 8 lanes of a token store the same word)
+    auto n_publish = [&](int64_t c) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        __hip_atomic_store(nslot(c, ntok(j)) + vtile, ntag | __float_as_uint(nsh[j]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    };
+    // six load instructions: the shares, the gate row, the o row
+    auto n_fetch = [&](int64_t c) {
+      const int64_t t0 = bos + c * C;
+      const int nv = chunk_nv(c);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int t = ntok(j);
+        const unsigned long long sh =
+            __hip_atomic_load(nslot(c, t) + min(nc8, nvt_h - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        nps[j] = nc8 < nvt_h ? sh : ntag;
+        const int tr = t < nv ? t : 0;
+        const int64_t off = ((t0 + tr) * H + h) * V + vt0 + 8 * nc8;
+        ng[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const bf16*>(a.ngate) + off);
+        no[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const bf16*>(a.o) + off);
+      }
+    };
+    // y of chunk c from the fetched rows; two store instructions
+    auto n_finish = [&](int64_t c) {
+      const int64_t t0 = bos + c * C;
+      const int nv = chunk_nv(c);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int t = ntok(j);
+#pragma unroll 1
+        for (int spins = 0;; ++spins) {                 // wave-uniform exit
+          const bool bad = (nps[j] & 0xffffffff00000000ull) != ntag;
+          if (__ballot(bad) == 0) break;
+          if (spins == kNormSpinMax) {
+            if (bad) nps[j] = ntag | 0x7fc00000u;        // NaN: the share never arrived
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          if (bad) nps[j] = __hip_atomic_load(nslot(c, t) + nc8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        float tot = __uint_as_float((uint32_t)nps[j]);
+        tot += __shfl_xor(tot, 4, WAVE);
+        tot += __shfl_xor(tot, 2, WAVE);
+        tot += __shfl_xor(tot, 1, WAVE);
+        const float r = __builtin_amdgcn_rsqf(tot / (float)V + a.neps);
+        const u32x4 x = no[j], gq = ng[j];
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float yv[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float xf = hh ? __uint_as_float(x[e] & 0xffff0000u) : __uint_as_float(x[e] << 16);
+            const float gf = hh ? __uint_as_float(gq[e] & 0xffff0000u) : __uint_as_float(gq[e] << 16);
+            const float v = fmaf(xf * r, nwv[2 * e + hh], nbv[2 * e + hh]);
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gf * 1.4426950408889634f));
+            yv[hh] = a.nsigmoid_only ? v * sg : v * gf * sg;
+          }
+          y[e] = (uint32_t)__builtin_bit_cast(uint16_t, (bf16)yv[0]) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (bf16)yv[1]) << 16);
+        }
+        u32x4* dst = t < nv ? reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(a.o) + ((t0 + t) * H + h) * V + vt0 + 8 * nc8)
+                            : ndummy;
+        *dst = y;
+      }
+    };
     // the folded convolution of v: loader lane L = 64 lw + l forms rows 2 (L / 8), + 1 of 16-byte
     // column chunk L % 8 of the workgroup's 64 columns, with that chunk's taps in registers for the
     // whole walk.  The window of chunk c (window buffer (c - ib) % 2) is loaded after B1 of step c - 2
@@ -398,18 +528,25 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       constexpr int PAR = decltype(PB)::value;
       ConvWin<2>& w_next = PAR ? cwb : cwa;              // chunk it + 2
       ConvWin<2>& w_now = PAR ? cwa : cwb;               // chunk it + 1
-      const uint32_t B = (uint32_t)PAR;
+      // the buffer set of chunk it (with kNorm the step is instantiated once, for code size)
+      const uint32_t B = kNorm ? (uint32_t)((it - ib) & 1) : (uint32_t)PAR;
       const int64_t in = it + 1 < ie ? it + 1 : it;       // the last step reloads its own chunk (unused)
       wait_all_loads();
       f_barrier();                                        // B1
-      if (it > ib) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
+      if constexpr (!kNorm) {
+        if (it > ib) store_o(bos + (it - 1) * C, chunk_nv(it - 1));
+      }
       const unsigned char* kb = reinterpret_cast<const unsigned char*>(ktb + ((c_first + it) * H + h) * (int64_t)(FK * C));
 #pragma unroll
       for (int j = 0; j < 32 / FL; ++j) ld_tile64<true>(kb, 128u, FK, FL * j + lw, k_lds);
+      if constexpr (kNorm) {
+        if (it > ib) n_store_share(it - 1);
+      }
       small(c_first + in, bos + in * C, chunk_nv(in), B ^ 1u);
       // the window of chunk it + 2 (convolved after B2 of step it + 1)
       const int nwin = (cvm && it + 2 < ie) ? kConvW + 1 : 0;
       if (nwin) conv_issue(w_next, it + 2);
+
       // this wave's k^T loads landed; the later ones (6 + gc / beta + the prefetch) stay in flight
       if constexpr (kRc) {                                // small: 4, and gc / beta from loaders 0 / 1
         if (it + 2 < ie) {
@@ -422,24 +559,57 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
           else wait_loads_but<4>();
         }
       } else {
-        if (it + 2 < ie) {
-          prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
-          wait_loads_but_n(kSmall + nwin + 1);
-        } else {
-          wait_loads_but_n(kSmall);
+        const int npf = it + 2 < ie ? 1 : 0;
+        if (npf) prefetch(c_first + it + 2, bos + (it + 2) * C, chunk_nv(it + 2));
+        // kNorm: the shares of chunk it - 1, y of chunk it - 4, the rows of chunk it - 3; all left in
+        // flight across B2 (two, two and six instructions)
+        int nnorm = 0;
+        if constexpr (kNorm) {
+          if (it > ib) {
+            n_publish(it - 1);
+            nnorm += 2;
+          }
+          if (it - 4 >= ib) {
+            n_finish(it - 4);
+            nnorm += 2;
+          }
+          if (it - 3 >= ib) {
+            n_fetch(it - 3);
+            nnorm += 6;
+          }
         }
+        wait_loads_but_n(kSmall + nwin + npf + nnorm);
       }
       f_barrier();                                        // B2
       if constexpr (kRc) store_h(c_first + it);           // written by the compute waves before B2
       if (it + 1 < ie) wq(bos + (it + 1) * C, chunk_nv(it + 1));
       if (cvm && it + 1 < ie) conv_store(w_now, it + 1, B ^ 1u);  // its window arrived before B1
     };
-    for (int64_t it = ib; it < ie; it += 2) {
-      loader_step(std::integral_constant<int, 0>{}, it);
-      if (it + 1 < ie) loader_step(std::integral_constant<int, 1>{}, it + 1);
+    if constexpr (kNorm) {
+      for (int64_t it = ib; it < ie; ++it) loader_step(std::integral_constant<int, 0>{}, it);
+    } else {
+      for (int64_t it = ib; it < ie; it += 2) {
+        loader_step(std::integral_constant<int, 0>{}, it);
+        if (it + 1 < ie) loader_step(std::integral_constant<int, 1>{}, it + 1);
+      }
     }
     f_barrier();                                          // the last o tile is in LDS
-    if (ie > ib) store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));
+    if (ie > ib) {
+      if constexpr (kNorm) {
+        // y of chunk L - 3 (loaded in step L), then of chunks L - 2, L - 1 (published) and L (in LDS)
+        const int64_t L = ie - 1;
+        n_store_share(L);
+        n_publish(L);
+        wait_all_loads();                                 // this workgroup's o rows and shares are in place
+        if (L - 3 >= ib) n_finish(L - 3);
+        for (int64_t c = L - 2 >= ib ? L - 2 : ib; c <= L; ++c) {
+          n_fetch(c);
+          n_finish(c);
+        }
+      } else {
+        store_o(bos + (ie - 1) * C, chunk_nv(ie - 1));
+      }
+    }
     wait_all_loads();                                     // no direct load outlives the workgroup's LDS
     return;
   }
@@ -1386,10 +1556,13 @@ int launch_wide_fused(const WideFusedArgs& a, int V, hipStream_t s) {
   const int total = a.N * a.H * (V / FVT);
   const int grid = (total + 7) / 8 * 8;
   if (a.h_out) {
-    if (!a.vn_out || a.ht) return -2;
-    hipLaunchKernelGGL(wide_fused_kernel<true>, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+    if (!a.vn_out || a.ht || a.ngate) return -2;
+    hipLaunchKernelGGL((wide_fused_kernel<true, false>), dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+  } else if (a.ngate) {
+    if (V > 8 * FVT || a.nss == nullptr) return -2;
+    hipLaunchKernelGGL((wide_fused_kernel<false, true>), dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
   } else {
-    hipLaunchKernelGGL(wide_fused_kernel<false>, dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
+    hipLaunchKernelGGL((wide_fused_kernel<false, false>), dim3(grid), dim3(NT_F + FL * WAVE), 0, s, a, V, total);
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

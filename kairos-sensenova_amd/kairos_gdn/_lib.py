@@ -30,6 +30,7 @@ SIGNATURES = {
     "kairos_gdn_last_error": (ctypes.c_char_p, []),
     "kairos_gdn_num_chunks_bound": (_i64, [_i64, _i64, _i64]),
     "kairos_gdn_chunk_fwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
+    "kairos_gdn_chunk_fwd_gated_norm_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _i]),
     "kairos_gdn_chunk_fwd": (_i, [_p, _p, _p, _p, _p, _fp, _fp, _p, _p, _fp, _p, _i64,
                                   _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p]),
     "kairos_gdn_chunk_fwd_gated_norm": (_i, [_p, _p, _p, _p, _p, _fp, _fp, _p, _p, _p, _p, _p, _fp, _p, _i64,

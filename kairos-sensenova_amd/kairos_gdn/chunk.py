@@ -92,6 +92,18 @@ def _prepare_cu_seqlens(cu_seqlens: torch.Tensor, device: torch.device, T: int) 
     return cu.to(device=device, dtype=torch.int64).contiguous()
 
 
+def _f16_as_f32(*xs):
+    """fp16 tensors as fp32 (others unchanged); with fp16 q, k or v all three are taken in fp32.
+
+    The reference op is dtype-generic (chunk.py:149-186 under autocast_custom_fwd): with fp16
+    inputs its kernels take fp16 operands and round Ai, w, u, h, v_new and o to fp16.  The
+    kernels here are built for bf16 and fp32 storage, so fp16 inputs run the fp32 kernels on
+    exact fp32 copies and o is rounded to fp16 once, at the end: no fp16 intermediate rounding,
+    hence at least as close to the exact recurrence as the reference's fp16 path.
+    """
+    return tuple(x.float() if (x is not None and x.dtype == torch.float16) else x for x in xs)
+
+
 def _scales(q_scale, k_scale, H, device, fp8: bool):
     if not fp8:
         return None, None
@@ -120,6 +132,16 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_fi
     dev = _require_device(q, k, v, g, beta, initial_state)
     B, T, H, K = q.shape
     V = v.shape[-1]
+    if torch.float16 in (q.dtype, k.dtype, v.dtype):
+        if _norm is not None:
+            raise TypeError("the fused gated norm takes bf16 or fp32 q/k/v (fp16 given)")
+        if q.dtype != k.dtype:
+            raise TypeError("q and k must share a dtype")
+        out_dt = v.dtype
+        o, ht = chunk_gated_delta_rule_fwd(q.float(), k.float(), v.float(), *_f16_as_f32(g, beta), scale,
+                                           *_f16_as_f32(initial_state), output_final_state, cu_seqlens,
+                                           use_qk_l2norm_in_kernel, q_scale, k_scale)
+        return o.to(out_dt), ht
     if k.shape != q.shape or v.shape[:3] != (B, T, H) or g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(
             f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}, g {tuple(g.shape)}, "
@@ -148,8 +170,9 @@ def chunk_gated_delta_rule_fwd(q, k, v, g, beta, scale, initial_state, output_fi
     o = torch.empty_like(v)
     ht = torch.empty(N, H, K, V, device=dev, dtype=torch.float32) if output_final_state else None
     lib = _lib.load()
-    ws_bytes = lib.kairos_gdn_chunk_fwd_workspace_size(B, T, H, K, V, n_seqs, qk_dt, v_dt,
-                                                       int(bool(use_qk_l2norm_in_kernel)))
+    ws_fn = lib.kairos_gdn_chunk_fwd_gated_norm_workspace_size if _norm is not None \
+        else lib.kairos_gdn_chunk_fwd_workspace_size
+    ws_bytes = ws_fn(B, T, H, K, V, n_seqs, qk_dt, v_dt, int(bool(use_qk_l2norm_in_kernel)))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     if _norm is not None:
         gate, nw, nb, eps, act = _norm
@@ -316,6 +339,14 @@ def chunk_gated_delta_rule_bwd_native(q, k, v, g, beta, scale, initial_state, do
     dev = _require_device(q, k, v, g, beta, initial_state, do, dht)
     B, T, H, K = q.shape
     V = v.shape[-1]
+    if torch.float16 in (q.dtype, k.dtype, v.dtype):
+        # fp16 runs the fp32 kernels (see _f16_as_f32); gradients come back in the inputs' dtypes
+        dts = (q.dtype, k.dtype, v.dtype, beta.dtype)
+        dq, dk, dv, db, dg, dh0 = chunk_gated_delta_rule_bwd_native(
+            q.float(), k.float(), v.float(), *_f16_as_f32(g, beta), scale, *_f16_as_f32(initial_state), do.float(),
+            dht, cu_seqlens,
+            use_qk_l2norm_in_kernel)
+        return dq.to(dts[0]), dk.to(dts[1]), dv.to(dts[2]), db.to(dts[3]), dg, dh0
     qk_dt, v_dt = _code(q, "q"), _code(v, "v")
     if qk_dt == _lib.F8E4M3:
         raise NotImplementedError("the backward pass takes bf16 or fp32 q/k; fp8 q/k are forward-only")
@@ -388,6 +419,7 @@ def chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g:
       [N, H, K, V] fp32 or None).  ``scale`` defaults to K ** -0.5.
     Extension: q/k may be torch.float8_e4m3fn with per-head fp32 dequantisation
     scales passed as ``q_scale=`` / ``k_scale=`` (shape [H]); o then has v's dtype.
+    fp16 inputs are accepted and computed by the fp32 kernels (o is returned in fp16).
     """
     if 'head_first' in kwargs:
         warnings.warn(

@@ -206,3 +206,34 @@ def test_autograd_matches_direct_call():
     for n, d in zip(("q", "k", "v", "beta", "g", "h0"), direct):
         assert leaves[n].grad is not None and leaves[n].grad.dtype == leaves[n].dtype, n
         assert torch.equal(leaves[n].grad, d.to(leaves[n].dtype)), n
+
+
+def test_fp16_autograd_matches_fp32_inputs():
+    """fp16 q/k/v/beta through autograd: the fp32 kernels on the same values, gradients returned in
+    fp16 (dg and dh0 fp32); equal to the fp32-input call up to the fp16 rounding of the outputs."""
+    B, T, H, K, V = 1, 200, 2, 128, 128
+    x = make_inputs(B, T, H, K, V, seed=21, dtype="fp32")
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)  # noqa: E731
+    for n in ("q", "k", "v", "beta"):
+        x[n] = f16(x[n])
+    rng = np.random.default_rng(22)
+    do = f16(rng.standard_normal((B, T, H, V)).astype(np.float32))
+    grads = {}
+    for dt in (torch.float16, torch.float32):
+        t = {n: torch.from_numpy(x[n]).to("cuda", dt).requires_grad_() for n in ("q", "k", "v", "beta")}
+        g = torch.from_numpy(x["g"]).to("cuda").requires_grad_()
+        h0 = torch.from_numpy(x["h0"]).to("cuda").requires_grad_()
+        o, ht = kairos_gdn.chunk_gated_delta_rule(t["q"], t["k"], t["v"], g, t["beta"], initial_state=h0,
+                                                  output_final_state=True, use_qk_l2norm_in_kernel=True)
+        assert o.dtype == dt
+        (o.float() * torch.from_numpy(do).cuda()).sum().add_(ht.square().sum() * 0.01).backward()
+        torch.cuda.synchronize()
+        for n in ("q", "k", "v", "beta"):
+            assert t[n].grad.dtype == dt, n
+        grads[dt] = [t[n].grad.float().cpu().numpy() for n in ("q", "k", "v", "beta")] + \
+            [g.grad.cpu().numpy(), h0.grad.cpu().numpy()]
+    errs = [O.rel_l2(a, b) for a, b in zip(grads[torch.float16], grads[torch.float32])]
+    note("    fp16 vs fp32 inputs: " + " ".join(f"{e:.2e}" for e in errs))
+    assert all(np.isfinite(a).all() for a in grads[torch.float16])
+    assert all(e < 2e-3 for e in errs), errs
+

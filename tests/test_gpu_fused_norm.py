@@ -8,9 +8,10 @@ runs the plain forward for o, then the combined call, and checks:
   - y against the oracle's whole layer (chunk_gated_delta_rule then rms_norm_gated on bf16 o):
     relative L2 <= 1e-2, the forward's own bar;
   - the separate-kernel form (KAIROS_GDN_FUSED_NORM=0) against the same oracle bar.
-Cases cover the fused output kernel (bf16, head dims 64 / 128, bf16 gate), ragged and varlen
-chunks, the in-op L2 norm, and the forms that run the norm kernel after the output (fp32 gate,
-K = 256, fp32 v).
+Cases cover the fused output kernel (bf16, head dims 64 / 128, bf16 gate), the fused K = 256 kernel
+with the norm folded in (KAIROS_GDN_WIDE_NORM_FOLD=1: its workgroups of 64 value columns exchange
+per-token sums of squares), ragged and varlen chunks,
+the in-op L2 norm, and the forms that run the norm kernel after the output (fp32 gate, fp32 v).
 """
 import sys
 
@@ -86,9 +87,16 @@ CASES = [
     ("bf16", 1, 700, 3, 64, 128, [0, 1, 1, 129, 640, 700], False, "bf16", "silu", None, False),
     ("bf16", 3, 200, 2, 128, 64, None, True, "bf16", "swish", "f32", True),
     ("bf16", 1, 4100, 4, 128, 128, [0, 63, 64, 65, 2000, 4100], True, "bf16", "swish", "bf16", True),
-    # the norm kernel after the output: fp32 gate, K = 256 (staged form), fp32 v
-    ("bf16", 1, 300, 2, 128, 128, None, False, "fp32", "swish", "f32", False),
+    # the fused K = 256 form (workgroups of 64 value columns exchange sums of squares): varlen with a
+    # 1-token sequence, the pipelined parts (T = 700: 11 chunks in 4 parts), one value tile, one chunk
     ("bf16", 1, 400, 2, 256, 512, [0, 1, 130, 400], False, "bf16", "swish", "bf16", False),
+    ("bf16", 1, 700, 2, 256, 512, None, True, "bf16", "swish", "f32", True),
+    ("bf16", 2, 130, 3, 256, 64, None, False, "bf16", "sigmoid", None, False),
+    ("bf16", 1, 64, 1, 256, 192, None, False, "bf16", "swish", "bf16", True),
+    ("bf16", 1, 257, 2, 256, 256, [0, 1, 1, 200, 257], True, "bf16", "silu", "f32", False),
+    # the norm kernel after the output: fp32 gate, K = 256 with an fp32 gate, fp32 v
+    ("bf16", 1, 300, 2, 128, 128, None, False, "fp32", "swish", "f32", False),
+    ("bf16", 1, 300, 2, 256, 512, None, False, "fp32", "swish", "f32", False),
     ("fp32", 2, 150, 2, 128, 64, None, False, "fp32", "sigmoid", "f32", True),
 ]
 
@@ -130,8 +138,10 @@ def test_gated_norm_forward(dt, B, T, H, K, V, cu, l2, gdt, act, wkind, use_b, m
                                        output_final_state=True, cu_seqlens=np.array(cu) if cu else None,
                                        use_qk_l2norm_in_kernel=l2, dtype=dt)
     y_layer, _ = O.rms_norm_gated(o_or.reshape(-1, V), gate_np.reshape(-1, V), w_np, b_np, act, eps, dtype=dt)
-    for fused in ("1", "0"):
-        monkeypatch.setenv("KAIROS_GDN_FUSED_NORM", fused)
+    for fused in ("1", "0", "fold"):
+        # "fold": the K = 256 form's norm in the fused kernel (opt-in), elsewhere as "1"
+        monkeypatch.setenv("KAIROS_GDN_FUSED_NORM", "0" if fused == "0" else "1")
+        monkeypatch.setenv("KAIROS_GDN_WIDE_NORM_FOLD", "1" if fused == "fold" else "0")
         y, ht2 = kairos_gdn.chunk_gated_delta_rule_gated_norm(
             d["q"], d["k"], d["v"], d["g"], d["beta"], gate, w_t, b_t, initial_state=h0, output_final_state=True,
             cu_seqlens=cu_t, use_qk_l2norm_in_kernel=l2, activation=act, eps=eps)
@@ -174,6 +184,57 @@ def test_gated_norm_config2_full_size(monkeypatch):
     ulp = y_sep.float().abs().clamp_min(1e-30) * 2.0 ** -7
     assert bool((diff <= ulp).all())
     assert float((diff == 0).float().mean()) >= 0.99
+
+
+@pytest.mark.parametrize("l2", [True, False])
+def test_gated_norm_model_shape_full_size(l2, monkeypatch):
+    """The Kairos layer (T=32760, H=20, dk=256, dv=512, bf16, in-op L2 norm as the layer calls it):
+    the norm folded into the fused K = 256 kernel (KAIROS_GDN_WIDE_NORM_FOLD=1) against the plain
+    forward followed by the norm
+    kernel on every token (one bf16 ulp, >= 99% identical), and against the oracle's norm of the
+    plain forward's o on every 97th token."""
+    B, T, H, K, V = 1, 32760, 20, 256, 512
+    note(f"chunk_fwd_gated_norm full size B={B} T={T} H={H} K={K} V={V} l2={l2}")
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    r = lambda *sh: torch.randn(*sh, device="cuda", generator=gen)  # noqa: E731
+    q = r(B, T, H, K)
+    k = r(B, T, H, K)
+    if not l2:
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = k / k.norm(dim=-1, keepdim=True)
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    v = r(B, T, H, V).to(torch.bfloat16)
+    beta = torch.sigmoid(r(B, T, H)).to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(r(B, T, H))
+    h0 = 0.02 * r(B, H, K, V)
+    gate = (r(B, T, H, V) * 2.0).to(torch.bfloat16)
+    w = torch.linspace(0.5, 1.5, V, device="cuda")
+    bias = torch.linspace(-0.1, 0.1, V, device="cuda")
+    o, ht = kairos_gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True,
+                                              use_qk_l2norm_in_kernel=l2)
+    monkeypatch.setenv("KAIROS_GDN_FUSED_NORM", "1")
+    monkeypatch.setenv("KAIROS_GDN_WIDE_NORM_FOLD", "1")
+    y, ht2 = kairos_gdn.chunk_gated_delta_rule_gated_norm(q, k, v, g, beta, gate, w, bias, initial_state=h0,
+                                                          output_final_state=True, use_qk_l2norm_in_kernel=l2)
+    torch.cuda.synchronize()
+    assert torch.equal(ht2, ht)
+    assert bool(torch.isfinite(y).all())
+    y_sep = kairos_gdn.rms_norm_gated_fwd(o.reshape(-1, V), gate.reshape(-1, V), w, bias, "swish", 1e-5)
+    diff = (y.reshape(-1, V).float() - y_sep.float()).abs()
+    mag = (o.reshape(-1, V).float().abs() * w.abs() + bias.abs()) * gate.reshape(-1, V).float().abs()
+    ulp = y_sep.float().abs().clamp_min(1e-30) * 2.0 ** -7 + mag * 2.0 ** -20
+    assert bool((diff <= ulp).all()), float((diff - ulp).max())
+    same = float((diff == 0).float().mean())
+    note(f"    identical to the two-step form: {same:.4f}")
+    assert same >= 0.99
+    sel = slice(0, T, 97)
+    o_s = o[:, sel].float().cpu().numpy().reshape(-1, V)
+    g_s = gate[:, sel].float().cpu().numpy().reshape(-1, V).astype(np.float64)
+    y_ref, _ = O.rms_norm_gated(o_s, g_s, w.cpu().numpy().astype(np.float64), bias.cpu().numpy().astype(np.float64),
+                                "swish", 1e-5, dtype="bf16")
+    mag_s = _magnitude(o_s, g_s, w.cpu().numpy().astype(np.float64), bias.cpu().numpy().astype(np.float64),
+                       "swish", 1e-5)
+    _within_ulp(y[:, sel].reshape(-1, V), y_ref, "bf16", mag_s)
 
 
 def test_gated_norm_argument_errors():

@@ -365,6 +365,39 @@ def test_bf16_gates_and_state_inputs():
     check_against_oracle(x, "bf16", o, ht)
 
 
+@pytest.mark.parametrize("K,V,cu,l2", [(128, 128, None, False), (64, 128, [0, 1, 130, 300], True),
+                                      (256, 512, None, True)])
+def test_fp16_inputs(K, V, cu, l2):
+    """fp16 q/k/v/beta (the reference op is dtype-generic): computed by the fp32 kernels, o in fp16.
+    Against the fp32-cast-point oracle on the same fp16 values: o within its own fp16 rounding
+    (<= 2e-3), final_state <= 1e-4; against the fp64 token recurrence within the north-star bar."""
+    note(f"fp16 inputs K={K} V={V} cu={cu} l2={l2}")
+    T = 300
+    x = make_inputs(1, T, 2, K, V, seed=11, dtype="fp32", n_states=len(cu) - 1 if cu else 1)
+    f16 = lambda a: a.astype(np.float16).astype(np.float32)  # noqa: E731
+    for n in ("q", "k", "v", "beta"):
+        x[n] = f16(x[n] * (1.7 if (l2 and n in ("q", "k")) else 1.0))
+    d = {n: dev(x[n], torch.float16) for n in ("q", "k", "v", "beta")}
+    cu_t = torch.tensor(cu, dtype=torch.int64, device="cuda") if cu else None
+    o, ht = kairos_gdn.chunk_gated_delta_rule(d["q"], d["k"], d["v"], dev(x["g"]), d["beta"],
+                                              initial_state=dev(x["h0"]), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=l2, cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16 and ht.dtype == torch.float32
+    o_r, ht_r = O.chunk_gated_delta_rule(x["q"], x["k"], x["v"], x["g"], x["beta"], initial_state=x["h0"],
+                                         output_final_state=True, use_qk_l2norm_in_kernel=l2,
+                                         cu_seqlens=np.array(cu) if cu else None, dtype="fp32")
+    eo, eh = rel(host(o), o_r), rel(host(ht), ht_r)
+    nrm = (lambda a: a / np.sqrt(np.sum(np.square(a.astype(np.float64)), -1, keepdims=True) + 1e-6)) if l2 \
+        else (lambda a: a)
+    o_n, ht_n = O.naive_recurrent(nrm(x["q"]), nrm(x["k"]), x["v"], x["g"], x["beta"], initial_state=x["h0"],
+                                  cu_seqlens=np.array(cu) if cu else None)
+    en, ehn = rel(host(o), o_n), rel(host(ht), ht_n)
+    note(f"    rel-L2 vs fp32 oracle: o={eo:.3e} ht={eh:.3e}; vs fp64 recurrence: o={en:.3e} ht={ehn:.3e}")
+    assert eo < 2e-3 and eh < 1e-4
+    assert en < 1e-2 and ehn < 5e-3
+
+
 @pytest.mark.parametrize("cfg", [0, 1])
 def test_baseline_config(cfg):
     c = CONFIGS[cfg]
