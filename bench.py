@@ -21,10 +21,11 @@ synchronisations.  `value` and `ms_per_step` come from that wall-clock
 interval; `step_ms` gives the median / p10 / p90 of per-step HIP events
 recorded on the launch stream in the same loop.  `cold_step_ms` times steps
 that each follow an overwrite of a 640 MiB buffer, which evicts the 256 MiB
-Infinity Cache (MALL) and the L2s, so every input comes from HBM.
+Infinity Cache (MALL) and the L2s, so every input comes from HBM: a fixed 100 of
+them (after 5 discarded), whatever --steps is, so runs of any length agree.
 
-Roofline: `achieved` = the op's algorithmic HBM bytes (the fused
-minimum, 2*dk*s_qk + 4*dv + 8 bytes per token-head plus the initial and final
+Roofline: `achieved` = the op's algorithmic HBM bytes (the fused minimum:
+q, k, v and o once, 2*dk*s_qk + 4*dv + 8 bytes per token-head plus the initial and final
 state, 678.8 MB at config 2) over the dominant kernel's average duration;
 `whole_call` puts the same bytes over the median step.  `design_bytes` is what
 this design's dominant kernel must move (its inputs include the chunk records and
@@ -56,6 +57,8 @@ KERNELS = ["seg_prep_kernel", "seg_trans_kernel", "seg_combine_kernel", "seg_out
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2.md")
 MODEL_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_model_shape.md")
 FLUSH_BYTES = 640 << 20
+COLD_STEPS = 100           # cold (flushed) steps timed in every mode, whatever --steps is
+COLD_DISCARD = 5          # cold steps run first and not counted
 
 # BASELINE.json configs measured here (config 0 is the CPU plumbing case, a parity test only)
 CONFIGS = {
@@ -72,7 +75,7 @@ def flops_per_tok_head(K, V):
 
 
 def alg_bytes(tok_heads, n_states, K, V, s_qk=2, s_v=2):
-    """The op's algorithmic (compulsory) HBM bytes as SURVEY 8(d) counts them: q, k, v, o once per
+    """The op's algorithmic (compulsory) HBM bytes, the fused minimum: q, k, v, o once per
     token-head plus 8 bytes for the gate and beta, and the initial state read and the final state
     written (fp32) per (sequence, head): 1,032 B per token-head + 128 KiB per (sequence, head) at d=128."""
     return tok_heads * (2 * K * s_qk + 2 * V * s_v + 8) + n_states * 2 * K * V * 4
@@ -159,7 +162,10 @@ class Timer:
 
     def __init__(self, args):
         self.steps, self.warmup, self.floor = args.steps, args.warmup, args.warmup_seconds
-        self.cold_steps = 0 if args.no_cold else min(args.steps, 100)
+        # cold steps: a fixed count, whatever --steps is, after a few discarded ones (the first flushes
+        # change the clocks), so that runs of any length report the same measurement
+        self.cold_steps = 0 if args.no_cold else COLD_STEPS
+        self.cold_discard = COLD_DISCARD
 
     def warm(self, step):
         t0 = time.perf_counter()
@@ -186,15 +192,16 @@ class Timer:
         res = {"wall_s": wall, "step_ms": summary(hot), "warmup_steps_run": n_warm, "warmup_wall_s": t_warm}
         if self.cold_steps:
             flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
-            e0 = [torch.cuda.Event(enable_timing=True) for _ in range(self.cold_steps)]
-            e1 = [torch.cuda.Event(enable_timing=True) for _ in range(self.cold_steps)]
-            for i in range(self.cold_steps):
+            n = self.cold_discard + self.cold_steps
+            e0 = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+            e1 = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+            for i in range(n):
                 flush.fill_(i & 0xFF)
                 e0[i].record()
                 step()
                 e1[i].record()
             torch.cuda.synchronize()
-            res["cold_step_ms"] = summary([a.elapsed_time(b) for a, b in zip(e0, e1)])
+            res["cold_step_ms"] = summary([a.elapsed_time(b) for a, b in zip(e0, e1)][self.cold_discard:])
             del flush
         return res
 

@@ -29,7 +29,16 @@
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
  *    is stream-ordered: no entry point synchronises or allocates.  Scratch
  *    memory comes from the caller's `workspace`.  Entry points are reentrant;
- *    concurrent calls must use distinct workspaces.
+ *    concurrent calls must use distinct workspaces.  One exception in how the
+ *    work is queued: the fixed-length K = 256 forward of kairos_gdn_chunk_fwd
+ *    (and of the _gated_norm / _conv calls) runs in parts on two library
+ *    streams of the current device, shared by every caller in the process
+ *    (created on first use, default priority, kept until exit, enqueued under
+ *    one process-wide lock), joined to `stream` by events: work queued on
+ *    `stream` after the call sees its results, but such calls issued from
+ *    different caller streams run one after another on the library streams.
+ *    Under graph capture, for varlen batches, in kairos_gdn_chunk_fwd_noalloc
+ *    and with KAIROS_GDN_WIDE_PIPE=1 everything runs on `stream`.
  *  - Return value: KAIROS_GDN_OK or an error code; kairos_gdn_last_error()
  *    returns the message of the calling thread's last failure.  No exception
  *    crosses the ABI.
@@ -123,8 +132,10 @@ size_t kairos_gdn_chunk_fwd_gated_norm_workspace_size(int64_t B, int64_t T, int6
  * nothing (no hipMalloc / hipFree, no allocating library routine) and takes
  * its scratch memory from a static device array inside the library, of
  * kairos_gdn_chunk_fwd_noalloc_max_bytes() bytes (256 MiB) on every GPU the
- * library runs on, held until the process ends.  No counterpart in the
- * reference: it is for callers that cannot allocate (code under HIP graph
+ * library runs on, committed at the first call on a device (a process that
+ * never calls it does not pay for it) and held until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation).  A problem
  * whose kairos_gdn_chunk_fwd_workspace_size() exceeds the array is rejected
  * with KAIROS_GDN_EWORKSPACE.  Every call on one GPU shares that GPU's array:
