@@ -56,6 +56,7 @@ RECORD = C * C * 2 + 8 * C * 4      # bytes of one (chunk, head) record written 
 KERNELS = ["seg_prep_kernel", "seg_trans_kernel", "seg_combine_kernel", "seg_out_kernel"]
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_config2.md")
 MODEL_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_model_shape.md")
+MODEL_L2_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_fwd_model_shape_l2norm.md")
 FLUSH_BYTES = 640 << 20
 COLD_STEPS = 100           # cold (flushed) steps timed in every mode, whatever --steps is
 COLD_DISCARD = 5          # cold steps run first and not counted
@@ -706,7 +707,8 @@ def bench_model_shape(args, dev):
         "roofline": {"bound": "hbm", "kernel": "whole call (median step)", "achieved": alg / med_s / 1e9,
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": alg / med_s / 1e9 / PEAK_HBM_GBS,
                      "alg_bytes": alg,
-                     "traffic": None if l2 else measured_call_traffic(MODEL_TRAFFIC_FILE, "chunk_fwd_model_shape")},
+                     "traffic": measured_call_traffic(MODEL_L2_TRAFFIC_FILE, "chunk_fwd_model_shape_l2norm") if l2
+                     else measured_call_traffic(MODEL_TRAFFIC_FILE, "chunk_fwd_model_shape")},
     }), flush=True)
 
 
