@@ -31,8 +31,9 @@
  *    memory comes from the caller's `workspace`.  Entry points are reentrant;
  *    concurrent calls must use distinct workspaces.  One exception in how the
  *    work is queued: the fixed-length K = 256 forward of kairos_gdn_chunk_fwd
- *    (and of the _gated_norm / _conv calls) runs in parts on two library
- *    streams of the current device, shared by every caller in the process
+ *    (and of the _gated_norm / _conv calls) runs in parts on library streams
+ *    of the current device (two, three with the gated norm, which runs by
+ *    parts beside the last recurrence part), shared by every caller in the process
  *    (created on first use, default priority, kept until exit, enqueued under
  *    one process-wide lock), joined to `stream` by events: work queued on
  *    `stream` after the call sees its results, but such calls issued from
@@ -109,7 +110,9 @@ int kairos_gdn_chunk_fwd(const void* q, const void* k, const void* v, const void
  * fused K = 256 kernel (V a multiple of 64), whose workgroups of one head
  * exchange per-token sums of squares through the workspace (off by default:
  * slower there than the norm kernel after the forward); otherwise the norm
- * kernel runs on y in place. */
+ * kernel runs on y in place: for the pipelined K = 256 forward by parts, the
+ * rows of every part but the last beside the last recurrence part
+ * (KAIROS_GDN_NORM_PARTS=0: one pass after the forward), else after it. */
 int kairos_gdn_chunk_fwd_gated_norm(const void* q, const void* k, const void* v, const void* g, const void* beta,
                                     const float* q_scale, const float* k_scale, const void* initial_state,
                                     const void* gate, const void* norm_weight, const void* norm_bias, void* y,

@@ -379,8 +379,8 @@ void wide_pipe_bounds(int64_t nt, int P, double growth, int64_t* b) {
 }
 
 std::mutex g_aux_mu;                                     // held while a pipelined call enqueues its work
-hipStream_t g_aux_stream[64][3] = {};
-hipEvent_t g_aux_events[64][3 * kMaxParts + 3] = {};   // + 3 join events
+hipStream_t g_aux_stream[64][4] = {};
+hipEvent_t g_aux_events[64][3 * kMaxParts + 4] = {};   // + 4 join events
 
 // What releases prepare p + 1 (KAIROS_GDN_WIDE_PIPE_MARK): 0, a one-workgroup marker kernel on the
 // recurrence stream just before part p; 1, that marker on a stream of its own once recurrence part
@@ -394,34 +394,69 @@ int wide_mark_mode() {
   return m < 0 || m > 2 ? 2 : m;
 }
 
-// The three streams (prepares, recurrence parts, markers) and the events of the current device,
-// created on first use and kept until the process ends (a recorded event may be recorded again:
-// waits already enqueued keep the record they saw).  Call with g_aux_mu held.
-int aux_streams(hipStream_t* sp, hipStream_t* sr, hipStream_t* sm, hipEvent_t** events) {
+// The four streams (prepares, recurrence parts, markers, the per-part gated norm) and the events of
+// the current device, created on first use and kept until the process ends (a recorded event may be
+// recorded again: waits already enqueued keep the record they saw).  Call with g_aux_mu held.
+int aux_streams(hipStream_t* sp, hipStream_t* sr, hipStream_t* sm, hipStream_t* sn, hipEvent_t** events) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
   if (g_aux_events[dev][0] == nullptr) {
-    for (int p = 0; p < 3 * kMaxParts + 3; ++p)
+    for (int p = 0; p < 3 * kMaxParts + 4; ++p)
       if (hipEventCreateWithFlags(&g_aux_events[dev][p], hipEventDisableTiming) != hipSuccess) return -1;
   }
   *events = g_aux_events[dev];
   if (g_aux_stream[dev][0] == nullptr) {
-    hipStream_t st[3] = {nullptr, nullptr, nullptr};
-    for (int j = 0; j < 3; ++j)
+    hipStream_t st[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (int j = 0; j < 4; ++j)
       if (hipStreamCreateWithFlags(&st[j], hipStreamNonBlocking) != hipSuccess) return -1;
-    for (int j = 0; j < 3; ++j) g_aux_stream[dev][j] = st[j];
+    for (int j = 0; j < 4; ++j) g_aux_stream[dev][j] = st[j];
   }
   *sp = g_aux_stream[dev][0];
   *sr = g_aux_stream[dev][1];
   *sm = g_aux_stream[dev][2];
+  *sn = g_aux_stream[dev][3];
   return 0;
+}
+
+// The layer's gated RMSNorm applied to the forward's output (kairos_gdn_chunk_fwd_gated_norm)
+struct NormEpilogue {
+  const void* gate;
+  const void* w;
+  const void* b;
+  int gate_dtype;
+  int w_dtype;
+  float eps;
+  int sigmoid_only;
+};
+
+// Rows [row0, row0 + rows) of y replaced by their gated RMSNorm, in place (each element is read and
+// written by the same lane)
+int norm_in_place(void* y, int y_dtype, const NormEpilogue& e, int64_t rows, int64_t D, hipStream_t s,
+                  int64_t row0 = 0) {
+  if (rows == 0) return 0;
+  char* yp = static_cast<char*>(y) + row0 * D * (int64_t)dt_size(y_dtype);
+  const char* gp = static_cast<const char*>(e.gate) + row0 * D * (int64_t)dt_size(e.gate_dtype);
+  kgdn::NormArgs na{yp, gp, e.w, e.b, yp, nullptr, y_dtype, e.gate_dtype, e.w_dtype, rows, (int)D, e.eps,
+                    e.sigmoid_only};
+  return from_launch(kgdn::launch_rmsnorm_gated(na, s), "gated RMSNorm epilogue");
+}
+
+// Whether the pipelined K = 256 forward applies the gated norm by parts (KAIROS_GDN_NORM_PARTS=0: one
+// pass over all rows after the forward): the rows of every part but the last on a library stream of
+// their own beside the last recurrence part (when no prepare runs any more), the last part's after it.
+// Measured at the Kairos layer shape with the in-op L2 norm: 1.83 against 1.88 ms; each part's rows
+// released as soon as that part is done (competing with the prepares) 2.09 ms.
+bool norm_parts_on() {
+  const char* e = std::getenv("KAIROS_GDN_NORM_PARTS");
+  return !(e && e[0] == '0' && e[1] == 0);
 }
 
 int run_staged(const Geometry& G, const void* q, const void* k, const void* v, const void* g, const void* beta,
                const float* q_scale, const float* k_scale, const void* h0, int h0_dtype, void* o, float* ht,
                const int64_t* cu_seqlens, int qk_dtype, int cdt, int g_dtype, int beta_dtype, float scale,
                Carver& cv, hipStream_t s, bool may_fork, bool l2 = false,
-               const kgdn::ConvIn* conv3 = nullptr, const kgdn::WideFusedArgs* wnorm = nullptr) {
+               const kgdn::ConvIn* conv3 = nullptr, const kgdn::WideFusedArgs* wnorm = nullptr,
+               const NormEpilogue* epi = nullptr, int y_dtype = 0, bool* epi_done = nullptr) {
   const size_t es = cdt == KAIROS_GDN_F32 ? 4 : 2;
   const size_t tok = (size_t)(G.B * G.T * G.H);
   const int K = (int)G.K, V = (int)G.V, H = (int)G.H;
@@ -495,11 +530,11 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (P > 1 && (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)) P = 1;
     std::unique_lock<std::mutex> lk(g_aux_mu, std::defer_lock);
-    hipStream_t s2 = nullptr, s3 = nullptr, s4 = nullptr;
+    hipStream_t s2 = nullptr, s3 = nullptr, s4 = nullptr, s5 = nullptr;
     hipEvent_t* ev = nullptr;
     if (P > 1) {
       lk.lock();
-      if (aux_streams(&s2, &s3, &s4, &ev) != 0) {
+      if (aux_streams(&s2, &s3, &s4, &s5, &ev) != 0) {
         lk.unlock();
         P = 1;
       }
@@ -525,6 +560,14 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
       // marker done); ev[2 kMaxParts + p]: recurrence part p done
       const int mark = wide_mark_mode();
       const bool beside = mark == 1;
+      // the gated norm of part p's rows (per sequence: tokens [64 bnd[p], 64 bnd[p + 1]) of each)
+      // on s5 once recurrence part p is done, beside the next part's recurrence
+      const bool nparts = epi != nullptr && N <= 8 && norm_parts_on();
+      auto norm_part = [&](int p) {
+        const int64_t t0 = bnd[p] * kgdn::C, t1 = std::min<int64_t>(bnd[p + 1] * kgdn::C, G.T);
+        for (int n = 0; n < N && rc == KAIROS_GDN_OK; ++n)
+          rc = norm_in_place(o, y_dtype, *epi, (t1 - t0) * H, V, s5, ((int64_t)n * G.T + t0) * H);
+      };
       auto prepare = [&](int p, hipStream_t sp) {
         pa.it0 = bnd[p];
         pa.it_span = bnd[p + 1] - bnd[p];
@@ -555,28 +598,36 @@ int run_staged(const Geometry& G, const void* q, const void* k, const void* v, c
         }
         if (p + 1 < P) fp.ht = st;
         if (rc == KAIROS_GDN_OK) rc = from_launch(kgdn::launch_wide_fused(fp, V, s3), "wide fused recurrence");
-        if (beside && p + 2 < P) record(ev[2 * kMaxParts + p], s3);
+        if ((beside && p + 2 < P) || nparts) record(ev[2 * kMaxParts + p], s3);
         if (p + 1 < P) {
           wait(s2, ev[kMaxParts + p]);
           prepare(p + 1, s2);
         }
       }
+      if (nparts) {                                         // parts 0 .. P - 2 once part P - 2 is done
+        wait(s5, ev[2 * kMaxParts + P - 2]);
+        for (int p = 0; p + 1 < P; ++p) norm_part(p);
+        wait(s5, ev[2 * kMaxParts + P - 1]);
+        norm_part(P - 1);
+      }
       // Join, also after a failed launch or event call above: the caller's stream waits for all
       // that was queued on the library streams (prepares on s2, recurrence parts on s3, markers on
-      // s4), so the caller may release the workspace once its own stream has passed this point.
-      // If the join itself cannot be enqueued, the library streams are drained on the host.
-      const hipStream_t lib_streams[3] = {s2, s3, s4};
+      // s4, norm parts on s5), so the caller may release the workspace once its own stream has passed
+      // this point.  If the join itself cannot be enqueued, the library streams are drained on the host.
+      const hipStream_t lib_streams[4] = {s2, s3, s4, s5};
       bool joined = true;
-      for (int j = 0; j < 3; ++j) {
+      for (int j = 0; j < 4; ++j) {
         if (j == 2 && !beside) continue;                    // s4 carries work only with markers beside
+        if (j == 3 && !nparts) continue;                    // s5 only with the norm by parts
         const hipEvent_t e = ev[3 * kMaxParts + j];
         if (hipEventRecord(e, lib_streams[j]) != hipSuccess || hipStreamWaitEvent(s, e, 0) != hipSuccess)
           joined = false;
       }
       if (!joined) {
-        for (int j = 0; j < 3; ++j) (void)hipStreamSynchronize(lib_streams[j]);
+        for (int j = 0; j < 4; ++j) (void)hipStreamSynchronize(lib_streams[j]);
         if (rc == KAIROS_GDN_OK) rc = fail(KAIROS_GDN_EHIP, "joining the pipelined forward's streams failed");
       }
+      if (epi_done) *epi_done = nparts && rc == KAIROS_GDN_OK;
       return rc;
     }
   }
@@ -664,16 +715,6 @@ size_t kairos_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t H, int6
   return total;
 }
 
-// The layer's gated RMSNorm applied to the forward's output (kairos_gdn_chunk_fwd_gated_norm)
-struct NormEpilogue {
-  const void* gate;
-  const void* w;
-  const void* b;
-  int gate_dtype;
-  int w_dtype;
-  float eps;
-  int sigmoid_only;
-};
 
 // The segment scan's output kernel takes the epilogue itself for a bf16 gate (KAIROS_GDN_FUSED_NORM=0
 // selects the separate norm kernel instead)
@@ -705,13 +746,6 @@ static unsigned next_norm_epoch() {
   return e;
 }
 
-// y = gated RMSNorm of y in place (each element is read and written by the same lane)
-static int norm_in_place(void* y, int y_dtype, const NormEpilogue& e, int64_t rows, int64_t D, hipStream_t s) {
-  if (rows == 0) return 0;
-  kgdn::NormArgs na{y, e.gate, e.w, e.b, y, nullptr, y_dtype, e.gate_dtype, e.w_dtype, rows, (int)D, e.eps,
-                    e.sigmoid_only};
-  return from_launch(kgdn::launch_rmsnorm_gated(na, s), "gated RMSNorm epilogue");
-}
 
 // Body of kairos_gdn_chunk_fwd, kairos_gdn_chunk_fwd_noalloc and kairos_gdn_chunk_fwd_gated_norm:
 // validation, workspace carving and the launches.  Allocates nothing; `profile` lets the call take part
@@ -772,11 +806,13 @@ static int chunk_fwd_impl(const char* what, bool profile, const void* q, const v
       q = qn;
       k = kn;
     }
+    bool epi_done = false;
     if (int rc = run_staged(G, q, k, v, g, beta, q_scale, k_scale, initial_state, h0_dtype, o, final_state,
                             cu_seqlens, qk_dtype, cdt, g_dtype, beta_dtype, scale, cv, s, profile,
-                            wide && use_qk_l2norm != 0, nullptr, wfold ? &wn : nullptr))
+                            wide && use_qk_l2norm != 0, nullptr, wfold ? &wn : nullptr,
+                            wfold ? nullptr : epi, v_dtype, &epi_done))
       return rc;
-    if (epi && !wfold)
+    if (epi && !wfold && !epi_done)
       if (int rc = norm_in_place(o, v_dtype, *epi, (int64_t)tok, V, s)) return rc;
     return ok();
   }

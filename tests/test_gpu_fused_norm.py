@@ -98,6 +98,10 @@ CASES = [
     ("bf16", 1, 300, 2, 128, 128, None, False, "fp32", "swish", "f32", False),
     ("bf16", 1, 300, 2, 256, 512, None, False, "fp32", "swish", "f32", False),
     ("fp32", 2, 150, 2, 128, 64, None, False, "fp32", "sigmoid", "f32", True),
+    # the pipelined K = 256 forward with the norm applied part by part: two sequences (one norm launch
+    # per sequence and part), an fp32 gate
+    ("bf16", 2, 600, 2, 256, 128, None, True, "bf16", "swish", "bf16", False),
+    ("bf16", 1, 650, 2, 256, 512, None, False, "fp32", "swish", "f32", True),
 ]
 
 
@@ -139,8 +143,11 @@ def test_gated_norm_forward(dt, B, T, H, K, V, cu, l2, gdt, act, wkind, use_b, m
                                        use_qk_l2norm_in_kernel=l2, dtype=dt)
     y_layer, _ = O.rms_norm_gated(o_or.reshape(-1, V), gate_np.reshape(-1, V), w_np, b_np, act, eps, dtype=dt)
     for fused in ("1", "0", "fold"):
-        # "fold": the K = 256 form's norm in the fused kernel (opt-in), elsewhere as "1"
+        # "1": the default (at K = 256 with pipelined parts the norm kernel part by part); "0": the norm
+        # kernel over all rows after the forward; "fold": the K = 256 form's norm in the fused kernel
+        # (opt-in), elsewhere as "1"
         monkeypatch.setenv("KAIROS_GDN_FUSED_NORM", "0" if fused == "0" else "1")
+        monkeypatch.setenv("KAIROS_GDN_NORM_PARTS", "0" if fused == "0" else "1")
         monkeypatch.setenv("KAIROS_GDN_WIDE_NORM_FOLD", "1" if fused == "fold" else "0")
         y, ht2 = kairos_gdn.chunk_gated_delta_rule_gated_norm(
             d["q"], d["k"], d["v"], d["g"], d["beta"], gate, w_t, b_t, initial_state=h0, output_final_state=True,
@@ -186,15 +193,17 @@ def test_gated_norm_config2_full_size(monkeypatch):
     assert float((diff == 0).float().mean()) >= 0.99
 
 
+@pytest.mark.parametrize("form", ["parts", "fold"])
 @pytest.mark.parametrize("l2", [True, False])
-def test_gated_norm_model_shape_full_size(l2, monkeypatch):
-    """The Kairos layer (T=32760, H=20, dk=256, dv=512, bf16, in-op L2 norm as the layer calls it):
-    the norm folded into the fused K = 256 kernel (KAIROS_GDN_WIDE_NORM_FOLD=1) against the plain
-    forward followed by the norm
-    kernel on every token (one bf16 ulp, >= 99% identical), and against the oracle's norm of the
-    plain forward's o on every 97th token."""
+def test_gated_norm_model_shape_full_size(l2, form, monkeypatch):
+    """The Kairos layer (T=32760, H=20, dk=256, dv=512, bf16, in-op L2 norm as the layer calls it),
+    against the plain forward followed by the norm kernel on every token, and against the oracle's
+    norm of the plain forward's o on every 97th token.  "parts" (the default): the norm kernel on each
+    pipelined part's rows beside the next part's recurrence, bit-identical to the two-step form (every
+    row normalised exactly once); "fold": the norm in the fused K = 256 kernel
+    (KAIROS_GDN_WIDE_NORM_FOLD=1), within one bf16 ulp and >= 99% identical."""
     B, T, H, K, V = 1, 32760, 20, 256, 512
-    note(f"chunk_fwd_gated_norm full size B={B} T={T} H={H} K={K} V={V} l2={l2}")
+    note(f"chunk_fwd_gated_norm full size B={B} T={T} H={H} K={K} V={V} l2={l2} form={form}")
     gen = torch.Generator(device="cuda").manual_seed(11)
     r = lambda *sh: torch.randn(*sh, device="cuda", generator=gen)  # noqa: E731
     q = r(B, T, H, K)
@@ -213,13 +222,16 @@ def test_gated_norm_model_shape_full_size(l2, monkeypatch):
     o, ht = kairos_gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True,
                                               use_qk_l2norm_in_kernel=l2)
     monkeypatch.setenv("KAIROS_GDN_FUSED_NORM", "1")
-    monkeypatch.setenv("KAIROS_GDN_WIDE_NORM_FOLD", "1")
+    monkeypatch.setenv("KAIROS_GDN_NORM_PARTS", "1")
+    monkeypatch.setenv("KAIROS_GDN_WIDE_NORM_FOLD", "1" if form == "fold" else "0")
     y, ht2 = kairos_gdn.chunk_gated_delta_rule_gated_norm(q, k, v, g, beta, gate, w, bias, initial_state=h0,
                                                           output_final_state=True, use_qk_l2norm_in_kernel=l2)
     torch.cuda.synchronize()
     assert torch.equal(ht2, ht)
     assert bool(torch.isfinite(y).all())
     y_sep = kairos_gdn.rms_norm_gated_fwd(o.reshape(-1, V), gate.reshape(-1, V), w, bias, "swish", 1e-5)
+    if form == "parts":
+        assert torch.equal(y.reshape(-1, V), y_sep)
     diff = (y.reshape(-1, V).float() - y_sep.float()).abs()
     mag = (o.reshape(-1, V).float().abs() * w.abs() + bias.abs()) * gate.reshape(-1, V).float().abs()
     ulp = y_sep.float().abs().clamp_min(1e-30) * 2.0 ** -7 + mag * 2.0 ** -20
