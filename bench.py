@@ -597,7 +597,10 @@ def bench_gated_norm(args, dev):
     prev = {n: os.environ.get(n) for n in names}
     out = {}
     try:
+        default = "separate" if args.model_shape else "fused"
         for form, flag in (("separate", "0"), ("fused", "1")):
+            if args.default_form_only and form != default:
+                continue
             os.environ["KAIROS_GDN_FUSED_NORM"] = flag
             os.environ["KAIROS_GDN_WIDE_NORM_FOLD"] = flag
             timer = Timer(args)
@@ -609,8 +612,7 @@ def bench_gated_norm(args, dev):
             else:
                 os.environ[n] = v
     # `value` is the library's default form: folded into seg_out at config 2, the separate norm kernel
-    # after the fused K = 256 kernel at the layer shape (the fold there is opt-in: measured slower)
-    default = "separate" if args.model_shape else "fused"
+    # (by parts beside the pipelined forward) at the layer shape (the fold there is opt-in: measured slower)
     timer, res = out[default]
     med = res["step_ms"]["median"]
     shape = f"T={T},H={H},dk={K},dv={V}" if args.model_shape else "T=32760,H=20,d=128"
@@ -890,6 +892,8 @@ def main():
     ap.add_argument("--gated-norm", action="store_true",
                     help="measure the forward with the layer's gated RMSNorm (folded into the forward against "
                          "the separate norm kernel); config 2, or the layer shape with --model-shape")
+    ap.add_argument("--default-form-only", action="store_true",
+                    help="with --gated-norm: time only the library's default form (for a profile of it alone)")
     ap.add_argument("--model-shape", action="store_true",
                     help="measure the Kairos 4B layer's head dims (dk=256, dv=512, H=20) at --T")
     ap.add_argument("--recurrent", action="store_true",
