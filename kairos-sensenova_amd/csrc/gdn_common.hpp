@@ -36,6 +36,27 @@ typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(float x) { return x; }
 
+// Device-memory accesses through address-space-1 pointers.  A plain pointer that the compiler cannot
+// place in an address space (here: one computed from a pointer field of a kernel's argument struct)
+// is accessed with FLAT instructions, which also count against lgkmcnt: every later wait for an LDS
+// access of the wave then waits for those stores to reach memory too.
+// (T is moved as a plain vector of 4-byte words of its size: HIP's vector structs have no assignment
+// through an address-space-1 pointer.)
+template <int N> struct GWords { typedef __attribute__((ext_vector_type(N))) unsigned type; };
+template <> struct GWords<1> { typedef unsigned type; };
+template <typename T>
+__device__ __forceinline__ void st_global(void* p, const T& x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 16, "4, 8 or 16 bytes");
+  using W = typename GWords<sizeof(T) / 4>::type;
+  *(__attribute__((address_space(1))) W*)p = __builtin_bit_cast(W, x);
+}
+template <typename T>
+__device__ __forceinline__ T ld_global(const void* p) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8 || sizeof(T) == 16, "4, 8 or 16 bytes");
+  using W = typename GWords<sizeof(T) / 4>::type;
+  return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) W*)p);
+}
+
 template <typename T> __device__ __forceinline__ T from_f32(float x);
 template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 // float -> bf16 with round-to-nearest-even (the hardware conversion on gfx950).

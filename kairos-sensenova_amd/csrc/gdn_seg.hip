@@ -1574,7 +1574,10 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
             ov[tn][ct] = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
           }
         }
-        // store o (token 16 tn + lc, columns vw + 16 ct + 4 lg .. +3)
+        // store o (token 16 tn + lc, columns vw + 16 ct + 4 lg .. +3).  These compile to FLAT stores
+        // (the pointer comes from the argument struct), whose completion the LDS wait of the barrier
+        // below includes; as global stores (st_global) the streaming rollout ran 0.1294 ms per frame
+        // against 0.1238, config 2 alike.
         unsigned char* ob = reinterpret_cast<unsigned char*>(o + ((t_seg + (int64_t)c * C) * H + h) * V + vw) +
                             8 * lg;
         const uint32_t row_bytes = (uint32_t)H * V * 2;
@@ -1634,8 +1637,7 @@ __global__ __launch_bounds__((OutPlan<TQ, K, V>::NT)) void seg_out_kernel(SegOut
               yv[e] = a.sigmoid_only ? v * sg : v * g * sg;
             }
             if (t < nvc)
-              *reinterpret_cast<uint2*>(ob + t * row_bytes) = make_uint2(pack_bf16x2(yv[0], yv[1]),
-                                                                         pack_bf16x2(yv[2], yv[3]));
+              *reinterpret_cast<uint2*>(ob + t * row_bytes) = make_uint2(pack_bf16x2(yv[0], yv[1]), pack_bf16x2(yv[2], yv[3]));
           }
         } else if (nvc == C) {
 #pragma unroll
@@ -2293,6 +2295,25 @@ template <int K> struct CombCfg {
   static constexpr int LDS_T = K + 8;                       // row stride (bf16) of a transposed state half
 };
 
+// f(integral_constant<int, I>, j0 + I) for I = I0 .. N - 1, unrolled
+template <int I, int N, typename F>
+__device__ __forceinline__ void unroll_steps(F& f, int j0) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{}, j0 + I);
+    unroll_steps<I + 1, N>(f, j0);
+  }
+}
+// the same for the first `rem` of them, each nested in the branch of the one before
+template <int I, int N, typename F>
+__device__ __forceinline__ void unroll_steps_upto(F& f, int j0, int rem) {
+  if constexpr (I < N) {
+    if (rem > I) {
+      f(std::integral_constant<int, I>{}, j0 + I);
+      unroll_steps_upto<I + 1, N>(f, j0, rem);
+    }
+  }
+}
+
 template <int K>
 __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineArgs a, SegGeom G, int total) {
   constexpr int NT = CombCfg<K>::NT;
@@ -2322,10 +2343,12 @@ __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineA
     nseg = G.seg_off[n + 1] - G.seg_off[n];
     s_first = G.seg_off[n];
   }
-  // Maps of steps j, j + 1, j + 2 in flight (stage j % 3).  Every stage is
+  // Maps of steps j .. j + NST - 1 in flight (stage j % NST).  Every stage is
   // loaded unconditionally (past the last step: the last step's maps again) so
   // that the number of loads issued after each stage is fixed and the wait for
-  // a stage counts only the loads before it.
+  // a stage counts only the loads before it.  Three stages measured best (28 us
+  // at config 2 against 30 with four and 36 with five): the step is bound by the
+  // rate at which a CU takes in its 72 KB of maps, not by their latency.
   constexpr int NST = 3;
   const int nsteps = nseg - 1;
   const bf16* Mb = reinterpret_cast<const bf16*>(a.M);
@@ -2348,6 +2371,8 @@ __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineA
     }
     return;
   }
+  // one segment: its initial state is h0, which seg_out reads itself
+  if (nsteps <= 0) return;
   // S_0 = h0: its loads go out before the maps', so that waiting for them does
   // not wait for the maps
   float x0[K * 16 / NT];
@@ -2362,10 +2387,8 @@ __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineA
                                    : (float)reinterpret_cast<const bf16*>(a.h0)[off];
     }
   }
-  if (nsteps > 0) {
 #pragma unroll
-    for (int u = 0; u < NST; ++u) issue(st[u], u);
-  }
+  for (int u = 0; u < NST; ++u) issue(st[u], u);
 #pragma unroll
   for (int e = 0; e < K * 16 / NT; ++e) {
     const int idx = threadIdx.x + NT * e;
@@ -2375,44 +2398,50 @@ __global__ __launch_bounds__(CombCfg<K>::NT) void seg_combine_kernel(SegCombineA
     s_S[0][1][c][r] = (bf16)(x0[e] - (float)hi);
   }
   __syncthreads();
-  for (int j0 = 0; j0 < nsteps; j0 += 2 * NST) {
+  // One step of the chain: U2 (a compile-time count) picks the map stage (U2 % NST) and the state
+  // buffer (j % 2 = U2 % 2)
+  auto step = [&](auto U2, int j) {
+    constexpr int u = decltype(U2)::value % NST, b = decltype(U2)::value & 1;
+    Frag<bf16> sh[K / 32], sl[K / 32];
 #pragma unroll
-    for (int u2 = 0; u2 < 2 * NST; ++u2) {
-      const int u = u2 % NST, b = u2 & 1;                   // map stage, state buffer (j % 2)
-      const int j = j0 + u2;
-      if (j >= nsteps) break;                               // uniform
-      Frag<bf16> sh[K / 32], sl[K / 32];
-#pragma unroll
-      for (int kb = 0; kb < K / 32; ++kb) {
-        sh[kb].v = *reinterpret_cast<const bf16x8*>(&s_S[b][0][lc][32 * kb + 8 * lg]);
-        sl[kb].v = *reinterpret_cast<const bf16x8*>(&s_S[b][1][lc][32 * kb + 8 * lg]);
-      }
-      f32x4 acc = st[u].r, acc2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < K / 32; ++kb) {
-        mma(acc2, st[u].ml[kb], sh[kb]);
-        mma(acc2, st[u].mh[kb], sl[kb]);
-        mma(acc, st[u].mh[kb], sh[kb]);
-      }
-      acc += acc2;
-      issue(st[u], j + NST);                                // this stage's registers are free again
-      // S_{j+1}: rows r0 + 4 lg + jj, column lc -> the other buffer, and s_init
-      uint32_t ph[2], pl[2];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const bf16 h0_ = (bf16)acc[2 * q], h1_ = (bf16)acc[2 * q + 1];
-        ph[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0_) | ((uint32_t)__builtin_bit_cast(uint16_t, h1_) << 16);
-        const bf16 l0_ = (bf16)(acc[2 * q] - (float)h0_), l1_ = (bf16)(acc[2 * q + 1] - (float)h1_);
-        pl[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0_) | ((uint32_t)__builtin_bit_cast(uint16_t, l1_) << 16);
-      }
-      *reinterpret_cast<uint2*>(&s_S[b ^ 1][0][lc][r0 + 4 * lg]) = make_uint2(ph[0], ph[1]);
-      *reinterpret_cast<uint2*>(&s_S[b ^ 1][1][lc][r0 + 4 * lg]) = make_uint2(pl[0], pl[1]);
-      float* out = a.s_init + ((s_first + j + 1) * (int64_t)H + h) * K * V + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) out[(int64_t)jj * V] = acc[jj];
-      lds_barrier();                                        // LDS only: the maps' prefetch stays in flight
+    for (int kb = 0; kb < K / 32; ++kb) {
+      sh[kb].v = *reinterpret_cast<const bf16x8*>(&s_S[b][0][lc][32 * kb + 8 * lg]);
+      sl[kb].v = *reinterpret_cast<const bf16x8*>(&s_S[b][1][lc][32 * kb + 8 * lg]);
     }
-  }
+    f32x4 acc = st[u].r, acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < K / 32; ++kb) {
+      mma(acc2, st[u].ml[kb], sh[kb]);
+      mma(acc2, st[u].mh[kb], sl[kb]);
+      mma(acc, st[u].mh[kb], sh[kb]);
+    }
+    acc += acc2;
+    issue(st[u], j + NST);                                  // this stage's registers are free again
+    // S_{j+1}: rows r0 + 4 lg + jj, column lc -> the other buffer, and s_init
+    uint32_t ph[2], pl[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const bf16 h0_ = (bf16)acc[2 * q], h1_ = (bf16)acc[2 * q + 1];
+      ph[q] = (uint32_t)__builtin_bit_cast(uint16_t, h0_) | ((uint32_t)__builtin_bit_cast(uint16_t, h1_) << 16);
+      const bf16 l0_ = (bf16)(acc[2 * q] - (float)h0_), l1_ = (bf16)(acc[2 * q + 1] - (float)h1_);
+      pl[q] = (uint32_t)__builtin_bit_cast(uint16_t, l0_) | ((uint32_t)__builtin_bit_cast(uint16_t, l1_) << 16);
+    }
+    *reinterpret_cast<uint2*>(&s_S[b ^ 1][0][lc][r0 + 4 * lg]) = make_uint2(ph[0], ph[1]);
+    *reinterpret_cast<uint2*>(&s_S[b ^ 1][1][lc][r0 + 4 * lg]) = make_uint2(pl[0], pl[1]);
+    float* out = a.s_init + ((s_first + j + 1) * (int64_t)H + h) * K * V + (int64_t)(r0 + 4 * lg) * V + v0 + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) out[(int64_t)jj * V] = acc[jj];
+    lds_barrier();                                          // LDS only: the maps' prefetch stays in flight
+  };
+  // Whole rounds of RL steps (RL a multiple of NST and of 2: the stage and the state buffer repeat),
+  // then the rest in nested branches.  Nothing leaves a round from inside: the compiler counts the
+  // loads in flight at each wait over every path that reaches it, and an exit inside an unrolled
+  // round also reached the loop header, so every step waited for the maps issued one step before
+  // instead of NST steps before.
+  constexpr int RL = NST % 2 ? 2 * NST : NST;
+  int j0 = 0;
+  for (; j0 + RL <= nsteps; j0 += RL) unroll_steps<0, RL>(step, j0);
+  unroll_steps_upto<0, RL - 1>(step, j0, nsteps - j0);       // uniform remainder, 0 .. RL - 1 steps
 }
 
 __global__ void seg_map_kernel(const int64_t* __restrict__ cu, int N, int L, int32_t* __restrict__ chunk_off,

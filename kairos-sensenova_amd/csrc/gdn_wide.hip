@@ -352,7 +352,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         const int t = 8 * (FL * j + lw) + (l >> 3), c8 = l & 7;
         const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (c8 ^ swz_o(t)));
         if (t < nv)
-          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(kRc ? a.vn_out : a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2) = x;
+          st_global(reinterpret_cast<unsigned char*>(kRc ? a.vn_out : a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2, x);
       }
     };
     // kRc: the state snapshot of chunk c (rows d of the q half of the w / q tile) to h_out [NC, H, 256, V]
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
       for (int j = 0; j < 2; ++j) {
         const int t = ntok(j);
         const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (nc8 ^ swz_o(t)));
-        if (t < nv) *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(a.o) + ((t0 + t) * H + h) * V + vt0 + 8 * nc8) = x;
+        if (t < nv) st_global(reinterpret_cast<bf16*>(a.o) + ((t0 + t) * H + h) * V + vt0 + 8 * nc8, x);
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -439,8 +439,8 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         nps[j] = nc8 < nvt_h ? sh : ntag;
         const int tr = t < nv ? t : 0;
         const int64_t off = ((t0 + tr) * H + h) * V + vt0 + 8 * nc8;
-        ng[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const bf16*>(a.ngate) + off);
-        no[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const bf16*>(a.o) + off);
+        ng[j] = ld_global<u32x4>(reinterpret_cast<const bf16*>(a.ngate) + off);
+        no[j] = ld_global<u32x4>(reinterpret_cast<const bf16*>(a.o) + off);
       }
     };
     // y of chunk c from the fetched rows; two store instructions
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
         }
         u32x4* dst = t < nv ? reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(a.o) + ((t0 + t) * H + h) * V + vt0 + 8 * nc8)
                             : ndummy;
-        *dst = y;
+        st_global(dst, y);
       }
     };
     // the folded convolution of v: loader lane L = 64 lw + l forms rows 2 (L / 8), + 1 of 16-byte
