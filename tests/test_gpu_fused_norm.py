@@ -249,6 +249,39 @@ def test_gated_norm_model_shape_full_size(l2, form, monkeypatch):
     _within_ulp(y[:, sel].reshape(-1, V), y_ref, "bf16", mag_s)
 
 
+@pytest.mark.parametrize("parts,growth", [("2", "1.4"), ("5", "1"), ("10", "1.4")])
+def test_gated_norm_by_parts_pipeline_shapes(parts, growth, monkeypatch):
+    """The norm by parts over other pipeline cuts of the K = 256 forward (two parts; five equal parts;
+    ten parts) on two sequences: bit-identical to the forward followed by the
+    norm kernel over all rows (every row normalised exactly once).  T = 1300: 21 chunks, so ten
+    parts (the most a sequence of 21 chunks is cut into) hold two or three chunks each."""
+    B, T, H, K, V = 2, 1300, 2, 256, 128
+    note(f"gated norm by parts: parts={parts} growth={growth} B={B} T={T} H={H} K={K} V={V}")
+    monkeypatch.setenv("KAIROS_GDN_WIDE_PIPE", parts)
+    monkeypatch.setenv("KAIROS_GDN_WIDE_PIPE_GROWTH", growth)
+    monkeypatch.setenv("KAIROS_GDN_WIDE_NORM_FOLD", "0")
+    gen = torch.Generator(device="cuda").manual_seed(int(parts) + 17)
+    r = lambda *sh: torch.randn(*sh, device="cuda", generator=gen)  # noqa: E731
+    q = r(B, T, H, K).to(torch.bfloat16)
+    k = r(B, T, H, K).to(torch.bfloat16)
+    v = r(B, T, H, V).to(torch.bfloat16)
+    beta = torch.sigmoid(r(B, T, H)).to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(r(B, T, H))
+    h0 = 0.02 * r(B, H, K, V)
+    gate = (r(B, T, H, V) * 2.0).to(torch.bfloat16)
+    w = torch.linspace(0.5, 1.5, V, device="cuda")
+    o, ht = kairos_gdn.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=h0, output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    y_ref = kairos_gdn.rms_norm_gated_fwd(o.reshape(-1, V), gate.reshape(-1, V), w, None, "swish", 1e-5)
+    for mode in ("1", "0"):
+        monkeypatch.setenv("KAIROS_GDN_NORM_PARTS", mode)
+        y, ht2 = kairos_gdn.chunk_gated_delta_rule_gated_norm(q, k, v, g, beta, gate, w, initial_state=h0,
+                                                              output_final_state=True, use_qk_l2norm_in_kernel=True)
+        torch.cuda.synchronize()
+        assert torch.equal(ht2, ht)
+        assert torch.equal(y.reshape(-1, V), y_ref), f"norm parts={mode}"
+
+
 def test_gated_norm_argument_errors():
     x = make_inputs(1, 64, 1, 64, 64, seed=1, dtype="bf16")
     d = {k: dev(x[k], torch.bfloat16) for k in ("q", "k", "v", "beta")}
