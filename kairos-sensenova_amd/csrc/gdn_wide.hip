@@ -347,12 +347,19 @@ __global__ __launch_bounds__(NT_F + FL * WAVE) void wide_fused_kernel(WideFusedA
     };
     // the o tile of chunk (t0, nv) from LDS to HBM: rows 8 i .. 8 i + 7 for i % FL = lw
     auto store_o = [&](int64_t t0, int nv) {
+      const int c8 = l & 7;
+      u32x4 x[8 / FL];                                   // both rows read before either store: one LDS wait
 #pragma unroll
       for (int j = 0; j < 8 / FL; ++j) {
-        const int t = 8 * (FL * j + lw) + (l >> 3), c8 = l & 7;
-        const u32x4 x = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (c8 ^ swz_o(t)));
+        const int t = 8 * (FL * j + lw) + (l >> 3);
+        x[j] = *reinterpret_cast<const lds_u32x4*>(reinterpret_cast<lds_b*>(o_lds) + 128 * t + 16 * (c8 ^ swz_o(t)));
+      }
+#pragma unroll
+      for (int j = 0; j < 8 / FL; ++j) {
+        const int t = 8 * (FL * j + lw) + (l >> 3);
         if (t < nv)
-          st_global(reinterpret_cast<unsigned char*>(kRc ? a.vn_out : a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2, x);
+          st_global(reinterpret_cast<unsigned char*>(kRc ? a.vn_out : a.o) + (((t0 + t) * H + h) * V + vt0 + 8 * c8) * 2,
+                    x[j]);
       }
     };
     // kRc: the state snapshot of chunk c (rows d of the q half of the w / q tile) to h_out [NC, H, 256, V]
