@@ -78,6 +78,41 @@ def test_bwd_against_oracle(name, c):
     run_case(**c)
 
 
+def _random_cases(n=12, seed=20264):
+    """Seeded random shapes for the backward: head dims (64, 128, 256 with value dims up to 256; fp32 at
+    most 128), batch or varlen layouts with an empty or one-token sequence, in-op L2 norm, initial state
+    and final-state gradient present or absent, bf16 or fp32."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        K = int(rng.choice([64, 128, 256]))
+        V = int(rng.choice([64, 128] if K < 256 else [64, 128, 256]))
+        dtype = "fp32" if rng.random() < 0.2 else "bf16"
+        if dtype == "fp32":                  # the fp32 backward is built for K, V <= 128
+            K, V = min(K, 128), min(V, 128)
+        H = int(rng.integers(1, 3))
+        c = dict(T=0, H=H, K=K, V=V, seed=100 + i, dtype=dtype, h0=bool(rng.random() < 0.7),
+                 dht=bool(rng.random() < 0.7), l2=bool(rng.random() < 0.4) and dtype == "bf16")
+        if rng.random() < 0.4:
+            n_seq = int(rng.integers(2, 5))
+            lens = [int(x) for x in rng.integers(2, 250, n_seq)]
+            lens[int(rng.integers(0, n_seq))] = int(rng.choice([0, 1]))
+            c.update(B=1, T=sum(lens), cu=[0] + [int(x) for x in np.cumsum(lens)])
+        else:
+            c.update(B=int(rng.integers(1, 3)), T=int(rng.integers(1, 300)))
+        out.append((f"b{i:02d}", c))
+    return out
+
+
+RANDOM_CASES = _random_cases()
+
+
+@pytest.mark.parametrize("name,c", RANDOM_CASES, ids=[c[0] for c in RANDOM_CASES])
+def test_bwd_random_shapes(name, c):
+    note(f"backward random {name}: {c}")
+    run_case(**c)
+
+
 def test_bwd_config1_all_heads():
     """BASELINE config 1 shape (B=1, T=8192, H=20, dk=dv=128, bf16, h0) with final-state gradient, every head."""
     note("backward config 1: B=1 T=8192 H=20 K=V=128 bf16")
