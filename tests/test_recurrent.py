@@ -169,6 +169,36 @@ GPU_CASES = [
 ]
 
 
+def _random_gpu_cases(n=12, seed=20265):
+    """Seeded random draws over the same space: K in {16, .., 256} (the vector form where K is 64, 128
+    or 256 and V a multiple of 16, the scalar form otherwise), ragged V, grouped value heads, batch or
+    varlen (with an empty sequence), and the optional gates, per-column beta, no beta, no g, no initial
+    state and the L2 norm."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        K = int(rng.choice([16, 32, 64, 128, 256]))
+        V = int(rng.choice([16, 40, 64, 128])) if K < 256 else int(rng.choice([64, 128]))
+        H = int(rng.integers(1, 4))
+        HV = H * int(rng.choice([1, 2]))
+        dt = "fp32" if rng.random() < 0.3 else "bf16"
+        if rng.random() < 0.35:
+            lens = [int(x) for x in rng.integers(1, 50, int(rng.integers(2, 5)))]
+            lens[int(rng.integers(0, len(lens)))] = 0
+            B, T, cu = 1, sum(lens), [0] + [int(x) for x in np.cumsum(lens)]
+        else:
+            B, T, cu = int(rng.integers(1, 5)), int(rng.integers(1, 40)), None
+        extras = [e for e, p_ in (("gk", 0.3), ("gv", 0.3), ("colbeta", 0.25), ("nog", 0.15), ("noh0", 0.2),
+                                  ("l2", 0.3)) if rng.random() < p_]
+        if "colbeta" not in extras and rng.random() < 0.1:
+            extras.append("nobeta")
+        out.append((f"rand{i:02d}", B, T, H, HV, K, V, cu, dt, ",".join(extras)))
+    return out
+
+
+GPU_CASES += _random_gpu_cases()
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("cid,B,T,H,HV,K,V,cu,dt,extras", GPU_CASES, ids=[c[0] for c in GPU_CASES])
 def test_gpu_fused_recurrent(cid, B, T, H, HV, K, V, cu, dt, extras):
@@ -187,8 +217,8 @@ def test_gpu_fused_recurrent(cid, B, T, H, HV, K, V, cu, dt, extras):
     if "gv" in extras:
         ex["gv"] = (-rng.random((B, T, HV, V)) * 0.2).astype(np.float32)
     beta = x["beta"]
-    if "colbeta" in extras:
-        beta = rng.random((B, T, HV, V)).astype(np.float32)
+    if "colbeta" in extras:                  # in the call's dtype, as the kernel receives it
+        beta = O.cast(rng.random((B, T, HV, V)).astype(np.float32), dt)
     if "nobeta" in extras:
         beta = None
     g = None if "nog" in extras else x["g"]
