@@ -944,6 +944,18 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     s_g[r] = r < nv ? a.gc[(t0 + r) * H + h] : 0.f;
     s_b[r] = r < nv ? ld_scalar(a.beta, (t0 + r) * H + h, a.beta_dtype) : 0.f;
   }
+  // this lane's token of the last phase: its dk1 row and the first batch of its v row go out now, so
+  // that their latency passes under the staging and the dA phases instead of after them
+  const int t = 16 * wid + lc;
+  const TC* dk1 = reinterpret_cast<const TC*>(a.dk1);
+  f32x4 d1s[K / 16];                                  // (rows past the end read row 0: dk is not stored there)
+#pragma unroll
+  for (int kt = 0; kt < K / 16; ++kt)
+    d1s[kt] = g_row4<TC>(dk1 + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)K + 16 * kt + 4 * lg);
+  const TC* vtok = reinterpret_cast<const TC*>(a.v) + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)V + 4 * lg;
+  f32x4 vnext[4];                                     // v of column tiles vt0 .. vt0 + 3 (rows past the end: row 0)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) vnext[e] = 16 * e < V ? g_row4<TC>(vtok + 16 * e) : f32x4{0.f, 0.f, 0.f, 0.f};
   stage_wait();
   __syncthreads();
 
@@ -1025,7 +1037,6 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   __syncthreads();
 
   // ---- per token tile (this wave): dk2, dk, dv, dbeta and the dkbg.kbg part of dg
-  const int t = 16 * wid + lc;
   const float bt = s_b[t], egt = gexp(s_g[t]);
   Frag<TC> bAi[2], bdA[2], bdAt[2];
 #pragma unroll
@@ -1036,11 +1047,6 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   }
   float dbt = 0.f, dgt = 0.f;
   TC* dk_out = reinterpret_cast<TC*>(a.dk);
-  const TC* dk1 = reinterpret_cast<const TC*>(a.dk1);
-  f32x4 d1s[K / 16];                                  // dk1 of this lane's token, all loads in flight at once
-#pragma unroll
-  for (int kt = 0; kt < K / 16; ++kt)                  // (rows past the end read row 0: dk is not stored there)
-    d1s[kt] = g_row4<TC>(dk1 + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)K + 16 * kt + 4 * lg);
 #pragma unroll
   for (int kt = 0; kt < K / 16; ++kt) {
     f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1, a3 = a1;
@@ -1069,12 +1075,14 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     if (t < nv) st4v<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0, dk);
   }
   TC* dv_out = reinterpret_cast<TC*>(a.dv);
-  // batches of 4 column tiles: the batch's v loads in flight before its products
+  // batches of 4 column tiles, the next batch's v loads issued before this batch's products
   for (int vt0 = 0; vt0 < V / 16; vt0 += 4) {
     f32x4 vv[4];
 #pragma unroll
+    for (int e = 0; e < 4; ++e) vv[e] = vnext[e];
+#pragma unroll
     for (int e = 0; e < 4; ++e)                       // (rows past the end read row 0: their dbeta is not stored)
-      vv[e] = g_row4<TC>(v + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)V + 16 * (vt0 + e) + 4 * lg);
+      vnext[e] = 16 * (vt0 + 4 + e) < V ? g_row4<TC>(vtok + 16 * (vt0 + 4 + e)) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int vt = vt0 + e;
