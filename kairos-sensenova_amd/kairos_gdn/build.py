@@ -35,10 +35,12 @@ HIP_FLAGS = [
 
 # Per-file flags.  MFMA accumulators in VGPRs: the fused K = 256 kernel scales and packs its state with
 # VALU every chunk (in AGPRs each of those touches costs a copy); the segment scan's kernels measured
-# alike at config 2 and 0.8% faster on the streaming rollout (A/B in one GPU call).
+# alike at config 2 and 0.8% faster on the streaming rollout, the backward's 0.2% faster at the layer
+# shape (A/B in one GPU call).
 FILE_FLAGS = {
     "gdn_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "gdn_seg.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "gdn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 
