@@ -902,15 +902,22 @@ __global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
 // ---------------------------------------------------------------------------
 // WY backward (wy_fast.py:98-210, USE_G) with the final sums of chunk.py:140-145:
 // dk = dk1 + dk2 (in the storage type), dg = reverse chunk cumsum of dg1 + dg2.
+//
+// G groups of four waves per chunk: wave w works on token tile ti = w % 4 and, within each phase, on
+// the column tiles of group gq = w / 4: every G-th dA, dA1 and dA tile from gq, and the gq-th of G
+// equal runs of consecutive K tiles of dk and V tiles of dv (so that each token's dk and dv row pieces
+// of one wave fill whole 128-byte lines).  Sums over a token's columns (dg, dbeta) leave each group as one LDS row
+// per group and are added in group order by the last phase, so the gradients are reproducible.
 // ---------------------------------------------------------------------------
-template <typename TC>
+template <typename TC, int G = 1>
 __host__ __device__ constexpr size_t wy_lds(int K, int V) {
   return sizeof(TC) * (2 * (size_t)tile_elems<TC>(K) + tile_elems<TC>(V) + 3 * (size_t)tile_elems<TC>(64)) +
-         7 * 64 * sizeof(float);
+         (6 + 2 * G) * 64 * sizeof(float);
 }
 
-template <typename TC, int K>
-__global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
+template <typename TC, int K, int G>
+__global__ __launch_bounds__(NT_B * G) void bwd_wy_kernel(BwdArgs a, int V) {
+  static_assert(G == 1 || G == 2 || G == 4, "four, eight or sixteen waves");
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_k = reinterpret_cast<TC*>(smem);
   TC* s_dw = s_k + tile_elems<TC>(K);
@@ -920,14 +927,16 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   TC* s_dA1 = s_dA + tile_elems<TC>(64);
   float* s_g = reinterpret_cast<float*>(s_dA1 + tile_elems<TC>(64));
   float* s_b = s_g + 64;
-  float* s_dg = s_b + 64;                             // row parts of dg2 (each token written by its wave)
-  float* s_dgc = s_dg + 64;                           // [4][64]: column parts, one row per wave
+  float* s_dgc = s_b + 64;                            // [4][64]: column parts of dg2, one row per token tile
+  float* s_dgp = s_dgc + 4 * 64;                      // [G][64]: row parts of dg2 (+ dkbg.kbg), one row per group
+  float* s_dbp = s_dgp + G * 64;                      // [G][64]: dbeta, one row per group
   const int h = blockIdx.y, H = a.H;
   const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
   if (!loc.ok) return;
   const int64_t t0 = loc.t0;
   const int nv = loc.nv;
   const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  const int ti = wid & 3, gq = wid >> 2;              // token tile, group
   if constexpr (sizeof(TC) == 2) {
     stage_rows_dma(s_k, reinterpret_cast<const TC*>(a.k), t0, nv, H, h, K);
     stage_rows_dma(s_dw, reinterpret_cast<const TC*>(a.dw), t0, nv, H, h, K);
@@ -944,78 +953,100 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     s_g[r] = r < nv ? a.gc[(t0 + r) * H + h] : 0.f;
     s_b[r] = r < nv ? ld_scalar(a.beta, (t0 + r) * H + h, a.beta_dtype) : 0.f;
   }
-  // this lane's token of the last phase: its dk1 row and the first batch of its v row go out now, so
-  // that their latency passes under the staging and the dA phases instead of after them
-  const int t = 16 * wid + lc;
+  // this lane's token of the last phase: its dk1 row pieces (the group's K tiles) and the first batch
+  // of its v row pieces.  With four waves they go out now, so that their latency passes under the
+  // staging and the dA phases; with more waves (a quarter of the registers each) before the last phase.
+  const int t = 16 * ti + lc;
+  constexpr int NKT = K / 16 / G;                     // K tiles of this group: kt = NKT gq + i
   const TC* dk1 = reinterpret_cast<const TC*>(a.dk1);
-  f32x4 d1s[K / 16];                                  // (rows past the end read row 0: dk is not stored there)
-#pragma unroll
-  for (int kt = 0; kt < K / 16; ++kt)
-    d1s[kt] = g_row4<TC>(dk1 + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)K + 16 * kt + 4 * lg);
+  f32x4 d1s[NKT];                                     // (rows past the end read row 0: dk is not stored there)
   const TC* vtok = reinterpret_cast<const TC*>(a.v) + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)V + 4 * lg;
-  f32x4 vnext[4];                                     // v of column tiles vt0 .. vt0 + 3 (rows past the end: row 0)
+  const int nvt = V / 16, vt0 = nvt / G * gq, vt1 = vt0 + nvt / G;   // V tiles; this group's: vt0 .. vt1 - 1
+  f32x4 vnext[4];                                     // v of this group's V tiles m .. m + 3
+  auto load_dk1 = [&]() {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) vnext[e] = 16 * e < V ? g_row4<TC>(vtok + 16 * e) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NKT; ++i)
+      d1s[i] = g_row4<TC>(dk1 + ((t0 + (t < nv ? t : 0)) * H + h) * (int64_t)K + 16 * (NKT * gq + i) + 4 * lg);
+  };
+  auto load_v = [&](int m) {                          // (rows past the end read row 0: their dbeta is not stored)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int vt = vt0 + m + e;
+      vnext[e] = vt < vt1 ? g_row4<TC>(vtok + 16 * vt) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  if constexpr (G == 1) {
+    load_dk1();
+    load_v(0);
+  }
   stage_wait();
   __syncthreads();
 
-  // ---- dA = dw bf16(k beta e^g)^T + du bf16(v beta)^T, strictly lower (rows of this wave)
+  // ---- dA = dw bf16(k beta e^g)^T + du bf16(v beta)^T, strictly lower (tile ti x tj; zeros above)
   const TC* v = reinterpret_cast<const TC*>(a.v);
-  for (int tj = 0; tj < 4; ++tj) {
+  for (int tj = gq; tj < 4; tj += G) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (tj <= wid) {
+    if (tj <= ti) {
       const int j = 16 * tj + lc;                     // operand row of the B fragments
       const float fk = s_b[j] * gexp(s_g[j]);
 #pragma unroll
       for (int ks = 0; ks < K / 32; ++ks)
-        mma(acc, t_nat<TC>(s_dw, K, 16 * wid, 32 * ks), fscale<TC>(t_nat<TC>(s_k, K, 16 * tj, 32 * ks), fk));
-      // this tile's v rows: every fragment's load in flight before the products
+        mma(acc, t_nat<TC>(s_dw, K, 16 * ti, 32 * ks), fscale<TC>(t_nat<TC>(s_k, K, 16 * tj, 32 * ks), fk));
+      // this tile's v rows: every fragment's load of a batch in flight before its products (all of
+      // them with four waves, four at a time with more)
       const TC* vrow = v + ((t0 + (j < nv ? j : 0)) * H + h) * (int64_t)V;
       constexpr int NVF = sizeof(TC) == 2 ? 16 : 4;     // V / 32 at most (bf16 V <= 512, fp32 V <= 128)
+      constexpr int NVB = G == 1 ? NVF : 4;
       // (raw loads in the V-guarded blocks, the mask of rows past the end applied at the products:
       // a use of the value inside its block would wait for each load before the next is issued)
-      Frag<TC> vf[NVF];
-#pragma unroll
-      for (int vs = 0; vs < NVF; ++vs)
-        if (vs < V / 32) vf[vs] = g_nat<TC>(vrow, 32 * vs, true);
       const bool jv = j < nv;
 #pragma unroll
-      for (int vs = 0; vs < NVF; ++vs)
-        if (vs < V / 32) mma(acc, t_nat<TC>(s_du, V, 16 * wid, 32 * vs), fscale<TC>(jv ? vf[vs] : fzero<TC>(), s_b[j]));
+      for (int vb = 0; vb < NVF; vb += NVB) {
+        if (32 * vb < V) {
+          Frag<TC> vf[NVB];
+#pragma unroll
+          for (int vs = 0; vs < NVB; ++vs)
+            if (vb + vs < V / 32) vf[vs] = g_nat<TC>(vrow, 32 * (vb + vs), true);
+#pragma unroll
+          for (int vs = 0; vs < NVB; ++vs)
+            if (vb + vs < V / 32)
+              mma(acc, t_nat<TC>(s_du, V, 16 * ti, 32 * (vb + vs)), fscale<TC>(jv ? vf[vs] : fzero<TC>(), s_b[j]));
+        }
+      }
     }
     const int j = 16 * tj + lc;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const int i = 16 * wid + 4 * lg + jj;
+      const int i = 16 * ti + 4 * lg + jj;
       s_dA[toff<TC>(i, j, 64)] = from_f32<TC>(i > j && i < nv ? acc[jj] : 0.f);
     }
   }
   __syncthreads();
   // ---- dA1 = bf16(dA) Ai^T
-  for (int tc = 0; tc < 4; ++tc) {
+  for (int tc = gq; tc < 4; tc += G) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 2; ++s) mma(acc, t_nat<TC>(s_dA, 64, 16 * wid, 32 * s), t_nat<TC>(s_Ai, 64, 16 * tc, 32 * s));
+    for (int s = 0; s < 2; ++s) mma(acc, t_nat<TC>(s_dA, 64, 16 * ti, 32 * s), t_nat<TC>(s_Ai, 64, 16 * tc, 32 * s));
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) s_dA1[toff<TC>(16 * wid + 4 * lg + jj, 16 * tc + lc, 64)] = from_f32<TC>(acc[jj]);
+    for (int jj = 0; jj < 4; ++jj) s_dA1[toff<TC>(16 * ti + 4 * lg + jj, 16 * tc + lc, 64)] = from_f32<TC>(acc[jj]);
   }
   __syncthreads();
   // ---- dA = -(Ai^T bf16(dA1)) e^{g_t - g_c}, strictly lower; AdA = dA * (bf16(k beta) k^T) -> dg
   float rowp[4] = {0.f, 0.f, 0.f, 0.f};
   {
-    const float fb = s_b[16 * wid + lc];              // beta of the A fragment's row
-    for (int tc = 0; tc < 4; ++tc) {
+    const float fb = s_b[16 * ti + lc];               // beta of the A fragment's row
+    for (int tc = gq; tc < 4; tc += G) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_Ai, 64, 32 * s, 16 * wid), t_tr<TC>(s_dA1, 64, 32 * s, 16 * tc));
+      for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_Ai, 64, 32 * s, 16 * ti), t_tr<TC>(s_dA1, 64, 32 * s, 16 * tc));
 #pragma unroll
       for (int ks = 0; ks < K / 32; ++ks)
-        mma(a2, fscale<TC>(t_nat<TC>(s_k, K, 16 * wid, 32 * ks), fb), t_nat<TC>(s_k, K, 16 * tc, 32 * ks));
+        mma(a2, fscale<TC>(t_nat<TC>(s_k, K, 16 * ti, 32 * ks), fb), t_nat<TC>(s_k, K, 16 * tc, 32 * ks));
       const int cc = 16 * tc + lc;
       float colp = 0.f;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int tt = 16 * wid + 4 * lg + jj;
+        const int tt = 16 * ti + 4 * lg + jj;
         const bool m = tt > cc && tt < nv;
         const float dA = round_to<TC>(m ? -acc[jj] * gexp(s_g[tt] - s_g[cc]) : 0.f);
         s_dA[toff<TC>(tt, cc, 64)] = from_f32<TC>(dA);
@@ -1024,7 +1055,7 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
         colp += ada;
       }
       colp = sum_lg(colp);
-      if (lg == 0) s_dgc[wid * 64 + cc] = -colp;
+      if (lg == 0) s_dgc[ti * 64 + cc] = -colp;
     }
   }
   float rowsum[4];
@@ -1032,23 +1063,28 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
   for (int jj = 0; jj < 4; ++jj) rowsum[jj] = sum16(rowp[jj]);
   if (lc == 0) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) s_dg[16 * wid + 4 * lg + jj] = rowsum[jj];
+    for (int jj = 0; jj < 4; ++jj) s_dgp[gq * 64 + 16 * ti + 4 * lg + jj] = rowsum[jj];
   }
   __syncthreads();
 
-  // ---- per token tile (this wave): dk2, dk, dv, dbeta and the dkbg.kbg part of dg
+  // ---- per token tile ti, this group's K and V tiles: dk2, dk, dv, dbeta and the dkbg.kbg part of dg
+  if constexpr (G > 1) {
+    load_dk1();
+    load_v(0);
+  }
   const float bt = s_b[t], egt = gexp(s_g[t]);
   Frag<TC> bAi[2], bdA[2], bdAt[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    bAi[s] = t_tr<TC>(s_Ai, 64, 32 * s, 16 * wid);     // B[n = t][j] = Ai[j][t]
-    bdA[s] = t_acc<TC>(s_dA, 64, 16 * wid, 32 * s);    // B[n = t][j] = dA[t][j]
-    bdAt[s] = t_tr<TC>(s_dA, 64, 32 * s, 16 * wid);    // B[n = t][j] = dA[j][t]
+    bAi[s] = t_tr<TC>(s_Ai, 64, 32 * s, 16 * ti);      // B[n = t][j] = Ai[j][t]
+    bdA[s] = t_acc<TC>(s_dA, 64, 16 * ti, 32 * s);     // B[n = t][j] = dA[t][j]
+    bdAt[s] = t_tr<TC>(s_dA, 64, 32 * s, 16 * ti);     // B[n = t][j] = dA[j][t]
   }
   float dbt = 0.f, dgt = 0.f;
   TC* dk_out = reinterpret_cast<TC*>(a.dk);
 #pragma unroll
-  for (int kt = 0; kt < K / 16; ++kt) {
+  for (int i = 0; i < NKT; ++i) {
+    const int kt = NKT * gq + i;
     f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = a1, a3 = a1;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -1062,7 +1098,7 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     }
     const int k0 = 16 * kt + 4 * lg;
     const f32x4 kv = t_row4<TC>(s_k, K, t, k0);
-    const f32x4 d1 = d1s[kt];
+    const f32x4 d1 = d1s[i];
     f32x4 dk;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
@@ -1075,47 +1111,54 @@ __global__ __launch_bounds__(NT_B) void bwd_wy_kernel(BwdArgs a, int V) {
     if (t < nv) st4v<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0, dk);
   }
   TC* dv_out = reinterpret_cast<TC*>(a.dv);
-  // batches of 4 column tiles, the next batch's v loads issued before this batch's products
-  for (int vt0 = 0; vt0 < V / 16; vt0 += 4) {
+  // batches of 4 of this group's V tiles, the next batch's v loads issued before this batch's products
+  for (int m0 = 0; vt0 + m0 < vt1; m0 += 4) {
     f32x4 vv[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) vv[e] = vnext[e];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)                       // (rows past the end read row 0: their dbeta is not stored)
-      vnext[e] = 16 * (vt0 + 4 + e) < V ? g_row4<TC>(vtok + 16 * (vt0 + 4 + e)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    load_v(m0 + 4);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int vt = vt0 + e;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const int vt = vt0 + m0 + e;
+      if (vt < vt1) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_du, V, 32 * s, 16 * vt), bAi[s]);   // dvb^T[v][t]
-      const int v0 = 16 * vt + 4 * lg;
-      if (t < nv) {
-        f32x4 dv;
+        for (int s = 0; s < 2; ++s) mma(acc, t_tr<TC>(s_du, V, 32 * s, 16 * vt), bAi[s]);   // dvb^T[v][t]
+        const int v0 = 16 * vt + 4 * lg;
+        if (t < nv) {
+          f32x4 dv;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          dv[jj] = acc[jj] * bt;
-          dbt += acc[jj] * vv[e][jj];
+          for (int jj = 0; jj < 4; ++jj) {
+            dv[jj] = acc[jj] * bt;
+            dbt += acc[jj] * vv[e][jj];
+          }
+          st4v<TC>(dv_out + ((t0 + t) * H + h) * (int64_t)V + v0, dv);
         }
-        st4v<TC>(dv_out + ((t0 + t) * H + h) * (int64_t)V + v0, dv);
       }
     }
   }
   dbt = sum_lg(dbt);
   dgt = sum_lg(dgt);
   if (lg == 0) {
-    s_dg[t] += dgt;                                   // token t belongs to this wave only
-    if (t < nv) {
-      const int64_t o = (t0 + t) * H + h;
-      if (a.beta_dtype == DT_F32) reinterpret_cast<float*>(a.db)[o] = dbt;
-      else reinterpret_cast<bf16*>(a.db)[o] = (bf16)dbt;
-    }
+    s_dgp[gq * 64 + t] += dgt;                        // token t's entry of this group's row is this wave's
+    s_dbp[gq * 64 + t] = dbt;
   }
   __syncthreads();
-  // ---- dg = reverse cumsum within the chunk of dg1 + dg2 (valid rows)
+  // ---- dbeta = the groups' parts in group order; dg = reverse cumsum within the chunk of dg1 + dg2
   if (wid == 0) {
-    float x = l < nv ? a.dg1[(t0 + l) * H + h] + s_dg[l] + (s_dgc[l] + s_dgc[64 + l] + s_dgc[128 + l] + s_dgc[192 + l])
-                     : 0.f;
+    float x = 0.f, db = 0.f;
+    if (l < nv) {
+      float rp = s_dgp[l];
+#pragma unroll
+      for (int q = 1; q < G; ++q) rp += s_dgp[q * 64 + l];
+      x = a.dg1[(t0 + l) * H + h] + rp + (s_dgc[l] + s_dgc[64 + l] + s_dgc[128 + l] + s_dgc[192 + l]);
+      db = s_dbp[l];
+#pragma unroll
+      for (int q = 1; q < G; ++q) db += s_dbp[q * 64 + l];
+      const int64_t o = (t0 + l) * H + h;
+      if (a.beta_dtype == DT_F32) reinterpret_cast<float*>(a.db)[o] = db;
+      else reinterpret_cast<bf16*>(a.db)[o] = (bf16)db;
+    }
 #pragma unroll
     for (int o = 1; o < WAVE; o <<= 1) {
       const float y = __shfl_down(x, o, WAVE);
@@ -1232,9 +1275,32 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
       if (set_lds(bwd_dqkwg_kernel<TC, K>, l3)) return -1;
       hipLaunchKernelGGL((bwd_dqkwg_kernel<TC, K>), grid, dim3(NT_B), l3, s, a, V);
     }
-    const size_t l4 = wy_lds<TC>(K, V);
-    if (l4 > 160 * 1024 || set_lds(bwd_wy_kernel<TC, K>, l4)) return -1;
-    hipLaunchKernelGGL((bwd_wy_kernel<TC, K>), grid, dim3(NT_B), l4, s, a, V);
+    // WY: groups of four waves per chunk (bf16).  Sixteen waves where a workgroup's LDS leaves room
+    // for no second one on a CU (dk = 256: with four waves, 4 per CU), eight where two fit (16 per
+    // CU, the two overlapping each other's staging).  Measured, sixteen / eight / four waves: 7.89 /
+    // 8.02 / 8.24 ms for the backward at dk = 256, dv = 512, T = 32760, H = 20; 2.79 / 2.67 / 2.72 ms
+    // at dk = dv = 128.  KAIROS_GDN_BWD_WY_WAVES=4, 8 or 16 forces one.
+    int wg = 1;
+    if constexpr (sizeof(TC) == 2) {
+      const char* e = std::getenv("KAIROS_GDN_BWD_WY_WAVES");
+      const int want = e ? std::atoi(e) : 0;
+      wg = want == 4 ? 1 : want == 8 ? 2 : want == 16 ? 4 : (wy_lds<TC, 2>(K, V) > 80 * 1024 ? 4 : 2);
+      if (wy_lds<TC, 4>(K, V) > 160 * 1024) wg = 1;
+      if (wg == 4) {
+        const size_t l4 = wy_lds<TC, 4>(K, V);
+        if (set_lds(bwd_wy_kernel<TC, K, 4>, l4)) return -1;
+        hipLaunchKernelGGL((bwd_wy_kernel<TC, K, 4>), grid, dim3(NT_B * 4), l4, s, a, V);
+      } else if (wg == 2) {
+        const size_t l4 = wy_lds<TC, 2>(K, V);
+        if (set_lds(bwd_wy_kernel<TC, K, 2>, l4)) return -1;
+        hipLaunchKernelGGL((bwd_wy_kernel<TC, K, 2>), grid, dim3(NT_B * 2), l4, s, a, V);
+      }
+    }
+    if (wg == 1) {
+      const size_t l4 = wy_lds<TC, 1>(K, V);
+      if (l4 > 160 * 1024 || set_lds(bwd_wy_kernel<TC, K, 1>, l4)) return -1;
+      hipLaunchKernelGGL((bwd_wy_kernel<TC, K, 1>), grid, dim3(NT_B), l4, s, a, V);
+    }
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

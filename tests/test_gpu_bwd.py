@@ -188,6 +188,21 @@ def test_bwd_model_head_dims_dh_forms(form, monkeypatch):
     run_case(1, 400, 2, 256, 256, seed=32, cu=[0, 0, 1, 65, 400])
 
 
+@pytest.mark.parametrize("waves", ["16", "8", "4"])
+def test_bwd_wy_forms(waves, monkeypatch):
+    """The WY backward with sixteen, eight and four waves per chunk (groups of four waves, each group
+    on every G-th column tile; bf16 takes sixteen at dk = 256 and four below): every form matches the
+    oracle at every head dim the backward takes, on ragged batches and on a varlen batch with an empty
+    and a 1-token sequence."""
+    monkeypatch.setenv("KAIROS_GDN_BWD_WY_WAVES", waves)
+    note(f"backward, {waves}-wave WY: B=2 T=333 H=2 K=64 V=64")
+    run_case(2, 333, 2, 64, 64, seed=51)
+    note(f"backward, {waves}-wave WY: varlen [0, 0, 1, 200, 450] H=2 K=128 V=192")
+    run_case(1, 450, 2, 128, 192, seed=52, cu=[0, 0, 1, 200, 450])
+    note(f"backward, {waves}-wave WY: B=1 T=300 H=2 K=256 V=512 l2")
+    run_case(1, 300, 2, 256, 512, seed=53, l2=True)
+
+
 @pytest.mark.parametrize("form", ["8-wave dq kernel", "4-wave dq kernel"])
 def test_bwd_dq_forms_k128(form, monkeypatch):
     """dk=128: the dq / dk / dw / dg stage with eight waves owning K rows (the default for bf16 K >= 128)
