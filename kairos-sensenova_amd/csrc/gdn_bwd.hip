@@ -191,8 +191,8 @@ __host__ __device__ constexpr size_t dvl_lds(int K, int V) {
   return sizeof(TC) * (2 * (size_t)tile_elems<TC>(K) + tile_elems<TC>(V) + tile_elems<TC>(64)) + 64 * sizeof(float);
 }
 
-template <typename TC, int K>
-__global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
+template <typename TC, int K, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void bwd_dvl_kernel(BwdArgs a, int V) {
   extern __shared__ __align__(16) unsigned char smem[];
   TC* s_q = reinterpret_cast<TC*>(smem);
   TC* s_k = s_q + tile_elems<TC>(K);
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
   if constexpr (sizeof(TC) == 2 && K == 256) {
     if (a.qT) {
       TC* qt = reinterpret_cast<TC*>(a.qT) + (blockIdx.x * (int64_t)H + h) * (K * C);
-      for (int i = wid; i < (K / 16) * 4; i += NT_B / WAVE) {
+      for (int i = wid; i < (K / 16) * 4; i += NW) {
         const int d0 = 16 * (i >> 2), tr0 = 16 * (i & 3) + 4 * lg;
         const s16x4_t x = lds_read_tr16(s_q + toff<TC>(tr0 + (lc >> 2), d0 + 4 * (lc & 3), K));
         *reinterpret_cast<s16x4_t*>(qt + (d0 + lc) * C + tr0) = x;
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
   }
 
   // M^T[j][i], j <= i, rounded to the storage type (the reference's b_A.to(do.dtype))
-  for (int tile = wid; tile < 16; tile += NT_B / WAVE) {
+  for (int tile = wid; tile < 16; tile += NW) {
     const int tj = tile >> 2, ti = tile & 3;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (tj <= ti) {
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(NT_B) void bwd_dvl_kernel(BwdArgs a, int V) {
 
   // dv_local^T[v][j] = sum_i do[i][v] M^T[j][i]
   TC* out = reinterpret_cast<TC*>(a.dvl);
-  for (int tile = wid; tile < (V / 16) * 4; tile += NT_B / WAVE) {
+  for (int tile = wid; tile < (V / 16) * 4; tile += NW) {
     const int tv = tile >> 2, tj = tile & 3;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1218,9 +1218,25 @@ template <typename TC, int K>
 int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream_t s) {
   const dim3 grid((unsigned)nc_grid, (unsigned)a.H);
   if (nc_grid > 0 && (stages & BWD_DVL)) {
+    // eight waves where the tiles leave room for one workgroup per CU, sixteen where two fit
+    // (KAIROS_GDN_BWD_DVL_WAVES=4, 8 or 16 forces one).  Backward measured with 16 / 8 / 4 waves:
+    // 7.79 / 7.74 / 7.75 ms at dk = 256, dv = 512, T = 32760, H = 20; 2.633 / 2.637 / 2.652 ms at
+    // dk = dv = 128.
     const size_t l1 = dvl_lds<TC>(K, V);
-    if (l1 > 160 * 1024 || set_lds(bwd_dvl_kernel<TC, K>, l1)) return -1;
-    hipLaunchKernelGGL((bwd_dvl_kernel<TC, K>), grid, dim3(NT_B), l1, s, a, V);
+    if (l1 > 160 * 1024) return -1;
+    const char* e = std::getenv("KAIROS_GDN_BWD_DVL_WAVES");
+    const int want = e ? std::atoi(e) : 0;
+    const int nw = want == 4 || want == 8 || want == 16 ? want : l1 > 80 * 1024 ? 8 : 16;
+    if (nw == 16) {
+      if (set_lds(bwd_dvl_kernel<TC, K, 16>, l1)) return -1;
+      hipLaunchKernelGGL((bwd_dvl_kernel<TC, K, 16>), grid, dim3(64 * 16), l1, s, a, V);
+    } else if (nw == 8) {
+      if (set_lds(bwd_dvl_kernel<TC, K, 8>, l1)) return -1;
+      hipLaunchKernelGGL((bwd_dvl_kernel<TC, K, 8>), grid, dim3(64 * 8), l1, s, a, V);
+    } else {
+      if (set_lds(bwd_dvl_kernel<TC, K, 4>, l1)) return -1;
+      hipLaunchKernelGGL((bwd_dvl_kernel<TC, K, 4>), grid, dim3(64 * 4), l1, s, a, V);
+    }
   }
   if (stages & BWD_DHU) {
     bool wide = false;

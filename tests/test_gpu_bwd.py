@@ -190,16 +190,18 @@ def test_bwd_model_head_dims_dh_forms(form, monkeypatch):
 
 @pytest.mark.parametrize("waves", ["16", "8", "4"])
 def test_bwd_wy_forms(waves, monkeypatch):
-    """The WY backward with sixteen, eight and four waves per chunk (groups of four waves, each group
-    on every G-th column tile; bf16 takes sixteen at dk = 256 and four below): every form matches the
-    oracle at every head dim the backward takes, on ragged batches and on a varlen batch with an empty
-    and a 1-token sequence."""
+    """The WY backward and the dv_local stage with sixteen, eight and four waves per chunk (WY: groups
+    of four waves, each group on its share of the column tiles; bf16 takes sixteen where one
+    workgroup fills a CU's LDS and eight where two fit): every form matches the oracle at every head
+    dim the backward takes, on ragged batches and on a varlen batch with an empty and a 1-token
+    sequence."""
     monkeypatch.setenv("KAIROS_GDN_BWD_WY_WAVES", waves)
-    note(f"backward, {waves}-wave WY: B=2 T=333 H=2 K=64 V=64")
+    monkeypatch.setenv("KAIROS_GDN_BWD_DVL_WAVES", waves)
+    note(f"backward, {waves}-wave WY and dv_local: B=2 T=333 H=2 K=64 V=64")
     run_case(2, 333, 2, 64, 64, seed=51)
-    note(f"backward, {waves}-wave WY: varlen [0, 0, 1, 200, 450] H=2 K=128 V=192")
+    note(f"backward, {waves}-wave WY and dv_local: varlen [0, 0, 1, 200, 450] H=2 K=128 V=192")
     run_case(1, 450, 2, 128, 192, seed=52, cu=[0, 0, 1, 200, 450])
-    note(f"backward, {waves}-wave WY: B=1 T=300 H=2 K=256 V=512 l2")
+    note(f"backward, {waves}-wave WY and dv_local: B=1 T=300 H=2 K=256 V=512 l2")
     run_case(1, 300, 2, 256, 512, seed=53, l2=True)
 
 
