@@ -39,6 +39,8 @@
 // o is computed transposed, so each lane stores 4 consecutive columns of one token.
 #include <type_traits>
 
+#include <cstdlib>
+
 #include "gdn_common.hpp"
 #include "gdn_conv.hpp"
 #include "gdn_kernels.h"
@@ -1212,15 +1214,15 @@ __device__ __forceinline__ int swz_n(int r) { return ((r & 1) << 1) | (((r >> 1)
 constexpr int DQ_NW = 8;
 constexpr int DQ_NT = DQ_NW * WAVE;
 
-template <int K>
+template <int K, int NB>
 struct DqLds {
   static constexpr uint32_t RB = K * 2;                   // q / k row bytes
   static constexpr uint32_t Q_OFF = 0;                    // q [64][K]
   static constexpr uint32_t K_OFF = C * RB;               // k [64][K]
-  static constexpr uint32_t BLK_OFF = 2 * C * RB;         // two buffers of do, dv2, v_new [64][64]
+  static constexpr uint32_t BLK_OFF = 2 * C * RB;         // NB buffers of do, dv2, v_new [64][64]
   static constexpr uint32_t TILE = C * C * 2;
   static constexpr uint32_t BLK = 3 * TILE;
-  static constexpr uint32_t DS_OFF = BLK_OFF + 2 * BLK;   // bf16(ds) [64][64]
+  static constexpr uint32_t DS_OFF = BLK_OFF + NB * BLK;  // bf16(ds) [64][64]
   static constexpr uint32_t G_OFF = DS_OFF + TILE;        // gc [64]
   static constexpr uint32_t ROW_OFF = G_OFF + C * 4;      // ds2 row sums per lower tile [10][16]
   static constexpr uint32_t COL_OFF = ROW_OFF + 10 * 16 * 4;   // ds2 column sums per lower tile [10][16]
@@ -1255,9 +1257,13 @@ __device__ __forceinline__ float wsum64(float x) {
   return x;
 }
 
-template <int K>
-__global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
-  using L = DqLds<K>;
+// NB = 2: the next value block's tiles (and h / dh fragments) load into the other buffer during this
+// block's products; NB = 1 (dk = 128: 68 KB, two workgroups per CU, each hiding the other's loads):
+// after them.
+template <int K, int NB>
+__global__ __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(NB == 1 ? 4 : 1))) void wide_dqkwg_kernel(
+    BwdArgs a, int V) {
+  using L = DqLds<K, NB>;
   constexpr uint32_t RB = L::RB, Q_OFF = L::Q_OFF, K_OFF = L::K_OFF, BLK_OFF = L::BLK_OFF, TILE = L::TILE,
                      BLK = L::BLK, DS_OFF = L::DS_OFF, G_OFF = L::G_OFF, ROW_OFF = L::ROW_OFF,
                      COL_OFF = L::COL_OFF, DGT_OFF = L::DGT_OFF, SC_OFF = L::SC_OFF;
@@ -1345,12 +1351,15 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
   float hdh = 0.f;
   const uint32_t brd = base + BLK_OFF + 128 * r0;          // block tiles, row r0
   auto block = [&](auto PP, int vb) {
-    constexpr uint32_t P = decltype(PP)::value;
-    if (vb + 1 < nvb) {
-      load_blk(vb + 1, P ^ 1u);
-      load_hd(vb + 1, hf[P ^ 1u], df[P ^ 1u]);
+    constexpr uint32_t P = decltype(PP)::value;            // register set of the h / dh fragments
+    constexpr uint32_t PB = NB == 2 ? P : 0u;              // LDS buffer of the block's tiles
+    if constexpr (NB == 2) {
+      if (vb + 1 < nvb) {
+        load_blk(vb + 1, P ^ 1u);
+        load_hd(vb + 1, hf[P ^ 1u], df[P ^ 1u]);
+      }
     }
-    const uint32_t bb = brd + P * BLK;
+    const uint32_t bb = brd + PB * BLK;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       Frag<bf16> fdo[2], fdv[2], fvn[2];
@@ -1386,6 +1395,13 @@ __global__ __launch_bounds__(DQ_NT) void wide_dqkwg_kernel(BwdArgs a, int V) {
     for (int f = 0; f < 2 * DT; ++f)
 #pragma unroll
       for (int e = 0; e < 8; ++e) hdh += (float)hf[P][f].v[e] * (float)df[P][f].v[e];
+    if constexpr (NB == 1) {                               // (the h / dh fragments too: fewer registers)
+      if (vb + 1 < nvb) {
+        load_hd(vb + 1, hf[P ^ 1u], df[P ^ 1u]);
+        f_barrier();                                       // every wave is done with this block's tiles
+        load_blk(vb + 1, 0u);
+      }
+    }
     wait_all_loads();
     f_barrier();
   };
@@ -1553,8 +1569,14 @@ int launch_wide_dhu(const BwdArgs& a, int V, hipStream_t s) {
 int launch_wide_dqkwg(const BwdArgs& a, int K, int V, int64_t nc_grid, hipStream_t s) {
   if (V % C != 0 || a.H <= 0 || !(K == 128 || K == 256)) return -2;
   if (nc_grid <= 0) return 0;
-  if (K == 256) hipLaunchKernelGGL(wide_dqkwg_kernel<256>, dim3((unsigned)nc_grid, a.H), dim3(DQ_NT), 0, s, a, V);
-  else hipLaunchKernelGGL(wide_dqkwg_kernel<128>, dim3((unsigned)nc_grid, a.H), dim3(DQ_NT), 0, s, a, V);
+  // dk = 128: one block buffer, two workgroups per CU (backward 2.633 -> 2.544 ms at config 2's shape,
+  // 8 VGPRs spilled at four waves per SIMD), unless KAIROS_GDN_BWD_DQK_BUFS=2
+  const char* e = std::getenv("KAIROS_GDN_BWD_DQK_BUFS");
+  const bool two = e && e[0] == '2' && e[1] == 0;
+  const dim3 grid((unsigned)nc_grid, (unsigned)a.H);
+  if (K == 256) hipLaunchKernelGGL((wide_dqkwg_kernel<256, 2>), grid, dim3(DQ_NT), 0, s, a, V);
+  else if (two) hipLaunchKernelGGL((wide_dqkwg_kernel<128, 2>), grid, dim3(DQ_NT), 0, s, a, V);
+  else hipLaunchKernelGGL((wide_dqkwg_kernel<128, 1>), grid, dim3(DQ_NT), 0, s, a, V);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

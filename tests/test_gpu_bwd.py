@@ -205,13 +205,16 @@ def test_bwd_wy_forms(waves, monkeypatch):
     run_case(1, 300, 2, 256, 512, seed=53, l2=True)
 
 
-@pytest.mark.parametrize("form", ["8-wave dq kernel", "4-wave dq kernel"])
+@pytest.mark.parametrize("form", ["8-wave dq kernel", "8-wave dq kernel, two block buffers", "4-wave dq kernel"])
 def test_bwd_dq_forms_k128(form, monkeypatch):
-    """dk=128: the dq / dk / dw / dg stage with eight waves owning K rows (the default for bf16 K >= 128)
-    and with four owning tokens both match the oracle, on a ragged batch of 2 and a varlen batch with
-    an empty and a 1-token sequence."""
+    """dk=128: the dq / dk / dw / dg stage with eight waves owning K rows (the default for bf16 K >= 128;
+    one buffer of value-block tiles, two workgroups per CU, or two buffers) and with four owning tokens
+    all match the oracle, on a ragged batch of 2 and a varlen batch with an empty and a 1-token
+    sequence."""
     if "4-wave" in form:
         monkeypatch.setenv("KAIROS_GDN_BWD_DQK_WIDE", "0")
+    if "two block buffers" in form:
+        monkeypatch.setenv("KAIROS_GDN_BWD_DQK_BUFS", "2")
     note(f"backward {form}: B=2 T=333 H=2 K=V=128")
     run_case(2, 333, 2, 128, 128, seed=41)
     note(f"backward {form}: varlen [0, 0, 1, 200, 450] H=3 K=128 V=192")
