@@ -41,8 +41,9 @@ __device__ __forceinline__ void st_pair(TC* p, float a, float b) {
 // registers until every wave is done with k, then region 0 holds A (fp32), which
 // the rounded inverse Ai later overwrites, and after that the v pass buffer: v is staged VP
 // columns at a time (u is separable over V).  VP is the widest pass that keeps
-// the tile within 80 KB (two workgroups per CU, so one's serial phases overlap
-// the other's), else within 160 KB.
+// the tile within a third of the LDS (three workgroups per CU, so one's serial
+// phases overlap the others'; at K = 128 two passes of 64 columns: the backward
+// at config 2's shape 2.548 -> 2.504 ms), else within 80 KB (two), else 160 KB.
 //
 // Compact plan (bf16, no u pass): k stays row-major for the whole kernel and the w operand
 // (k beta e^gc)^T is formed from transposed reads of it (ds_read_b64_tr_b16) instead of a
@@ -81,7 +82,9 @@ struct PrepLds {
     return k_bytes > aai_bytes + sizeof(TC) * vp * LDT ? al16(k_bytes) : aai_bytes + al16(sizeof(TC) * vp * LDT);
   }
   static constexpr size_t fits(int vp, size_t cap) { return region0_for(vp) + fixed <= cap; }
-  static constexpr int VP = fits(256, 80 * 1024) ? 256 : fits(128, 80 * 1024) ? 128 : fits(64, 80 * 1024) ? 64
+  static constexpr size_t kThird = 160 * 1024 / 3 / 16 * 16;
+  static constexpr int VP = fits(256, kThird) ? 256 : fits(128, kThird) ? 128 : fits(64, kThird) ? 64
+                          : fits(256, 80 * 1024) ? 256 : fits(128, 80 * 1024) ? 128 : fits(64, 80 * 1024) ? 64
                           : fits(256, 160 * 1024) ? 256 : fits(128, 160 * 1024) ? 128 : 64;   // v columns per pass
   static constexpr size_t region0 = region0_for(VP);
   static constexpr size_t off_A = 0;                            // region 0 after K.K^T
