@@ -524,7 +524,11 @@ struct DW {
   static constexpr int off_k = 0, off_qh = EK, off_ql = 2 * EK, off_w = 3 * EK, off_do = 4 * EK;
   static constexpr int off_dvl = 4 * EK + EV;              // dv_local [64][V] (same tile layout)
   static constexpr int n_el = 4 * EK + 2 * EV;
-  static constexpr size_t lds = (size_t)n_el * 2 + C * sizeof(float);
+  // the outputs of a chunk step, bf16 row-major with 16-byte chunks swizzled by row (swz_out): the dh
+  // snapshot [K][V] and dv2 [64][V], written out as whole rows by every thread after the step
+  static constexpr size_t off_hs = (size_t)n_el * 2 + C * sizeof(float);
+  static constexpr size_t off_dv2 = off_hs + (size_t)K * V * 2;
+  static constexpr size_t lds = off_dv2 + (size_t)C * V * 2;
   static constexpr int UK = EK / 8 / NT, UV = EV / 8 / NT;  // 16-byte units per thread
   static_assert(EK % (8 * NT) == 0 && EV % (8 * NT) == 0, "units split evenly over the threads");
 };
@@ -571,7 +575,13 @@ __device__ __forceinline__ void dw_load(DWChunk<K, V>& P, const BwdArgs& a, int6
   P.gt = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
 }
 
-template <int K, int V>
+// 16-byte chunk ch of row r of an output tile with V / 8 chunks per row: rows 4 apart (the rows of one
+// lane group's 2-byte writes) land on distinct pairs of chunks
+template <int V>
+__device__ __forceinline__ int swz_out(int r, int ch) { return ch ^ ((2 * (r >> 2)) & (V / 8 - 1)); }
+
+// kOut: the pass that writes the dh snapshots and dv2 (a.dh or a.dv2 set); without, only dh0
+template <int K, int V, bool kOut>
 __global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a, int total_units) {
   using D = DW<K, V>;
   constexpr int KT = D::KT, KS = D::KS;
@@ -584,6 +594,8 @@ __global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a,
   bf16* s_do = sm + D::off_do;
   bf16* s_dvl = sm + D::off_dvl;
   float* s_g = reinterpret_cast<float*>(smem + (size_t)D::n_el * 2);
+  bf16* s_hs = reinterpret_cast<bf16*>(smem + D::off_hs);
+  bf16* s_dv2 = reinterpret_cast<bf16*>(smem + D::off_dv2);
 
   const int per_xcd = gridDim.x / 8;                   // XCD-aware unit order
   const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -621,11 +633,38 @@ __global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a,
   if (nchunks > 0) dw_load<K, V>(cur, a, chunk_start(nchunks - 1), chunk_len(nchunks - 1), h);
   bf16* dh_out = reinterpret_cast<bf16*>(a.dh);
   bf16* dv2_out = reinterpret_cast<bf16*>(a.dv2);
+  // a step's dh snapshot and dv2, from their LDS tiles to HBM as 16-byte row pieces (every thread)
+  auto flush = [&](int64_t c, int64_t t0, int nv) {
+    if (dh_out) {
+      bf16* base = dh_out + (c * H + h) * (int64_t)K * V;            // [K][V], contiguous
+#pragma unroll
+      for (int i = 0; i < K * V / 8 / D::NT; ++i) {
+        const int u = tid + D::NT * i, r = u / (V / 8), ch = u % (V / 8);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(s_hs + r * V + 8 * swz_out<V>(r, ch));
+        st_global(base + (int64_t)r * V + 8 * ch, x);
+      }
+    }
+    if (dv2_out) {
+#pragma unroll
+      for (int i = 0; i < C * V / 8 / D::NT; ++i) {
+        const int u = tid + D::NT * i, t = u / (V / 8), ch = u % (V / 8);
+        const u32x4 x = *reinterpret_cast<const u32x4*>(s_dv2 + t * V + 8 * swz_out<V>(t, ch));
+        if (t < nv) st_global(dv2_out + ((t0 + t) * H + h) * (int64_t)V + 8 * ch, x);
+      }
+    }
+  };
+  int64_t prev_c = 0, prev_t0 = 0;
+  int prev_nv = 0;
 
   for (int64_t it = nchunks - 1; it >= 0; --it) {
     const int64_t c = c_first + it;
     const int nv = cur.nv;
     const int64_t t0 = cur.t0;
+    if (kOut && it < nchunks - 1) flush(prev_c, prev_t0, prev_nv);   // the previous step's outputs (published
+                                                              // by its closing barrier)
+    prev_c = c;
+    prev_t0 = t0;
+    prev_nv = nv;
     // ---- stage the chunk: k, q e^{gc} scale as hi + lo, -w, do, dv_local, gc
 #pragma unroll
     for (int i = 0; i < D::UK; ++i) {
@@ -659,13 +698,15 @@ __global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a,
     step_barrier();
     if (it > 0) dw_load<K, V>(nxt, a, chunk_start(it - 1), chunk_len(it - 1), h);
 
-    // dh snapshot (before this chunk), row-major [NC, H, K, V]
-    if (dh_out) {
-      bf16* p = dh_out + ((c * H + h) * K + 4 * lg) * (int64_t)V + c0 + lc;
+    // dh snapshot (before this chunk), row-major [NC, H, K, V], into its LDS tile
+    if constexpr (kOut) {
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * (int64_t)V] = (bf16)dh[tt][j];
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * tt + 4 * lg + j, col = c0 + lc;
+          s_hs[r * V + 8 * swz_out<V>(r, col >> 3) + (col & 7)] = (bf16)dh[tt][j];
+        }
     }
     // dv2 = e^{g_last - gc} (k bf16(dh)) + dv_local, rows t = 16 tm + 4 lg + j
     Frag<bf16> hb[KS];
@@ -684,7 +725,10 @@ __global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a,
         const int t = 16 * tm + 4 * lg + j;
         const float dl = (float)s_dvl[toff<bf16>(t, c0 + lc, V)];
         dv[tm][j] = t < nv ? acc[j] * gexp(gl - g4[j]) + dl : 0.f;
-        if (dv2_out && t < nv) dv2_out[((t0 + t) * H + h) * (int64_t)V + c0 + lc] = (bf16)dv[tm][j];
+        if constexpr (kOut) {
+          const int col = c0 + lc;
+          s_dv2[t * V + 8 * swz_out<V>(t, col >> 3) + (col & 7)] = (bf16)dv[tm][j];
+        }
       }
     }
     // dh = e^{g_last} dh + (q e^{gc} scale)^T do - w^T bf16(dv2)
@@ -708,6 +752,7 @@ __global__ __launch_bounds__((DW<K, V>::NT)) void bwd_dhu_wide_kernel(BwdArgs a,
     step_barrier();                                    // the tiles are restaged next chunk
     cur = nxt;
   }
+  if (kOut && nchunks > 0) flush(prev_c, prev_t0, prev_nv);
 
   if (a.dh0) {
 #pragma unroll
@@ -1259,14 +1304,24 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
             using D = DW<K, 64>;
             constexpr int nt = D::NT;
             constexpr size_t lds = D::lds;
-            if (set_lds(bwd_dhu_wide_kernel<K, 64>, lds)) return -1;
-            hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 64>), dim3(g8), dim3(nt), lds, s, a, total);
+            if (a.dh || a.dv2) {
+              if (set_lds(bwd_dhu_wide_kernel<K, 64, true>, lds)) return -1;
+              hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 64, true>), dim3(g8), dim3(nt), lds, s, a, total);
+            } else {
+              if (set_lds(bwd_dhu_wide_kernel<K, 64, false>, lds)) return -1;
+              hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 64, false>), dim3(g8), dim3(nt), lds, s, a, total);
+            }
           } else {
             using D = DW<K, 128>;
             constexpr int nt = D::NT;
             constexpr size_t lds = D::lds;
-            if (set_lds(bwd_dhu_wide_kernel<K, 128>, lds)) return -1;
-            hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 128>), dim3(g8), dim3(nt), lds, s, a, total);
+            if (a.dh || a.dv2) {
+              if (set_lds(bwd_dhu_wide_kernel<K, 128, true>, lds)) return -1;
+              hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 128, true>), dim3(g8), dim3(nt), lds, s, a, total);
+            } else {
+              if (set_lds(bwd_dhu_wide_kernel<K, 128, false>, lds)) return -1;
+              hipLaunchKernelGGL((bwd_dhu_wide_kernel<K, 128, false>), dim3(g8), dim3(nt), lds, s, a, total);
+            }
           }
         }
       }
