@@ -595,8 +595,18 @@ struct HCols {
   static constexpr int EK = C * K;
   static constexpr int UK = EK / 8 / NT;                 // 16-byte units of a [64][K] tile per thread
   static_assert(EK % (8 * NT) == 0, "units split evenly over the threads");
+  // row-major outputs of a step (bf16, 16-byte chunks swizzled by row, hcols_swz): the snapshot
+  // [K][V] and v_new [64][V], written out as whole rows by every thread after the step
+  static constexpr size_t off_hs = (size_t)2 * EK * 2 + C * sizeof(float);
+  static constexpr size_t off_vn = off_hs + (size_t)K * V * 2;
+  static constexpr size_t lds_rm = off_vn + (size_t)C * V * 2;
   static constexpr size_t lds = (size_t)2 * EK * 2 + C * sizeof(float);
 };
+
+// 16-byte chunk ch of row r of an output tile with V / 8 chunks per row: rows 4 apart (one lane
+// group's 2-byte writes) land on distinct pairs of chunks
+template <int V>
+__device__ __forceinline__ int hcols_swz(int r, int ch) { return ch ^ ((2 * (r >> 2)) & (V / 8 - 1)); }
 
 template <int K, int V>
 struct HColsChunk {
@@ -632,7 +642,8 @@ __device__ __forceinline__ void hcols_load(HColsChunk<K, V>& P, const FwdHArgs& 
   P.gt = l < nv ? a.gc[(t0 + l) * H + h] : 0.f;
 }
 
-template <int K, int V>
+// kRM: row-major outputs (h [NC, H, K, V], v_new [B*T, H, V], through LDS tiles), else hT and vnT
+template <int K, int V, bool kRM>
 __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs a, int total_units) {
   using HP = HCols<K, V>;
   constexpr int KT = HP::KT, KS = HP::KS;
@@ -640,6 +651,8 @@ __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs 
   bf16* s_w = reinterpret_cast<bf16*>(smem);
   bf16* s_k = s_w + HP::EK;
   float* s_g = reinterpret_cast<float*>(smem + (size_t)2 * HP::EK * 2);
+  bf16* s_hs = reinterpret_cast<bf16*>(smem + HP::off_hs);   // (kRM only)
+  bf16* s_vn = reinterpret_cast<bf16*>(smem + HP::off_vn);
 
   const int per_xcd = gridDim.x / 8;                      // XCD-aware unit order
   const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -676,11 +689,34 @@ __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs 
   if (nchunks > 0) hcols_load<K, V>(cur, a, c_first, bos, chunk_len(0), h, vcol);
   bf16* hT = reinterpret_cast<bf16*>(a.hT);
   bf16* vnT = reinterpret_cast<bf16*>(a.vnT);
+  // a step's row-major snapshot and v_new, from their LDS tiles to HBM as 16-byte row pieces
+  auto flush = [&](int64_t c, int64_t t0, int nv) {
+    bf16* base = hT + (c * H + h) * (int64_t)K * V;       // [K][V], contiguous
+#pragma unroll
+    for (int i = 0; i < K * V / 8 / HP::NT; ++i) {
+      const int u = tid + HP::NT * i, r = u / (V / 8), ch = u % (V / 8);
+      const u32x4 x = *reinterpret_cast<const u32x4*>(s_hs + r * V + 8 * hcols_swz<V>(r, ch));
+      st_global(base + (int64_t)r * V + 8 * ch, x);
+    }
+#pragma unroll
+    for (int i = 0; i < C * V / 8 / HP::NT; ++i) {
+      const int u = tid + HP::NT * i, t = u / (V / 8), ch = u % (V / 8);
+      const u32x4 x = *reinterpret_cast<const u32x4*>(s_vn + t * V + 8 * hcols_swz<V>(t, ch));
+      if (t < nv) st_global(vnT + ((t0 + t) * H + h) * (int64_t)V + 8 * ch, x);
+    }
+  };
+  int64_t prev_c = 0, prev_t0 = 0;
+  int prev_nv = 0;
 
   for (int64_t it = 0; it < nchunks; ++it) {
     const int64_t c = c_first + it;
     const int nv = cur.nv;
     const int64_t t0 = cur.t0;
+    if (kRM && it > 0) flush(prev_c, prev_t0, prev_nv);   // the previous step's outputs (published by
+                                                          // its closing barrier)
+    prev_c = c;
+    prev_t0 = t0;
+    prev_nv = nv;
 #pragma unroll
     for (int i = 0; i < HP::UK; ++i) {
       const int u = tid + HP::NT * i, r = u / (K / 8), cc = 8 * (u % (K / 8));
@@ -693,12 +729,14 @@ __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs 
     if (it + 1 < nchunks) hcols_load<K, V>(nxt, a, c + 1, chunk_start(it + 1), chunk_len(it + 1), h, vcol);
 
     // snapshot of the state before this chunk, rounded (chunk_delta_h.py:129-139)
-    if (a.row_major) {            // h [NC, H, K, V]
-      bf16* p = hT + ((c * H + h) * K + 4 * lg) * (int64_t)V + vcol;
+    if constexpr (kRM) {          // h [NC, H, K, V], into its LDS tile
 #pragma unroll
       for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[(16 * tt + j) * (int64_t)V] = (bf16)S[tt][j];
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * tt + 4 * lg + j;
+          s_hs[r * V + 8 * hcols_swz<V>(r, vcol >> 3) + (vcol & 7)] = (bf16)S[tt][j];
+        }
     } else {                      // hT [NC, H, V, K]
       bf16* p = hT + ((c * H + h) * V + vcol) * (int64_t)K + 4 * lg;
 #pragma unroll
@@ -723,11 +761,11 @@ __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs 
         const int t = 16 * tm + 4 * lg + j;
         Yg[tm][j] = t < nv ? Y[tm][j] * gexp(gl - g4[j]) : 0.f;
       }
-      if (a.row_major) {          // v_new [B*T, H, V]
+      if constexpr (kRM) {        // v_new [B*T, H, V], into its LDS tile
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int t = 16 * tm + 4 * lg + j;
-          if (t < nv) vnT[((t0 + t) * H + h) * (int64_t)V + vcol] = (bf16)Y[tm][j];
+          s_vn[t * V + 8 * hcols_swz<V>(t, vcol >> 3) + (vcol & 7)] = (bf16)Y[tm][j];
         }
       } else {                    // vnT [NC, H, V, 64]
         st4<bf16>(vnT + ((c * H + h) * V + vcol) * C + 16 * tm + 4 * lg, Y[tm][0], Y[tm][1], Y[tm][2], Y[tm][3]);
@@ -747,6 +785,7 @@ __global__ __launch_bounds__((HCols<K, V>::NT)) void fwd_h_cols_kernel(FwdHArgs 
     step_barrier();                                       // the tiles are restaged next chunk
     cur = nxt;
   }
+  if (kRM && nchunks > 0) flush(prev_c, prev_t0, prev_nv);
 
   if (a.ht) {
 #pragma unroll
@@ -763,14 +802,18 @@ template <int K, int V>
 int launch_fwd_h_cols(const FwdHArgs& a, hipStream_t s) {
   using HP = HCols<K, V>;
   constexpr int nt = HP::NT;
-  constexpr size_t lds = HP::lds;
   const int total = a.N * a.H;
   const int grid = (total + 7) / 8 * 8;
-  if (lds > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(fwd_h_cols_kernel<K, V>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-    return -1;
-  hipLaunchKernelGGL((fwd_h_cols_kernel<K, V>), dim3(grid), dim3(nt), lds, s, a, total);
+  auto go = [&](auto kern, size_t lds) -> int {
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return -1;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(nt), lds, s, a, total);
+    return 0;
+  };
+  if (int rc = a.row_major ? go(fwd_h_cols_kernel<K, V, true>, HP::lds_rm) : go(fwd_h_cols_kernel<K, V, false>, HP::lds))
+    return rc;
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
