@@ -505,12 +505,17 @@ def bench_backward(args, dev):
     intermediates, dv_local, the dh recurrence, dq/dk/dw/dg and the WY backward) at BASELINE config 2,
     or at the Kairos layer's head dims with --model-shape.  Algorithmic bytes: q, k, v, do read and
     dq, dk, dv written once per token-head (7 x 2 B x d), g, beta read and dg, dbeta written, plus h0 and
-    dht read and dh0 written per (sequence, head)."""
+    dht read and dh0 written per (sequence, head).  --l2norm passes unnormalised q, k with the in-op L2
+    norm (the layer's own mode: the op normalises them and its backward goes through the norm)."""
     from kairos_gdn import _lib
     K, V = (256, 512) if args.model_shape else (128, 128)
     B, T, H = 1, args.T, 20
     q, k, v, g, beta, h0 = make_inputs(B, T, H, K, V, 20262, device=dev)
     gen = torch.Generator(device="cpu").manual_seed(20263)
+    l2 = 1 if args.l2norm else 0
+    if l2:
+        q = (q.float() * torch.rand(B, T, H, 1, generator=gen).add_(0.5).to(dev)).to(torch.bfloat16)
+        k = (k.float() * torch.rand(B, T, H, 1, generator=gen).add_(0.5).to(dev)).to(torch.bfloat16)
     do = torch.randn(B, T, H, V, generator=gen).to(dev, torch.bfloat16)
     dht = torch.randn(B, H, K, V, generator=gen).to(dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
@@ -518,7 +523,7 @@ def bench_backward(args, dev):
     db = torch.empty_like(beta)
     dh0 = torch.empty_like(h0)
     lib = _lib.load()
-    ws_bytes = lib.kairos_gdn_chunk_bwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, 0)
+    ws_bytes = lib.kairos_gdn_chunk_bwd_workspace_size(B, T, H, K, V, 0, _lib.BF16, _lib.BF16, l2)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     sp = torch.cuda.current_stream(dev).cuda_stream
     P = lambda t: t.data_ptr()  # noqa: E731
@@ -526,7 +531,7 @@ def bench_backward(args, dev):
     def step():
         _lib.call("kairos_gdn_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(h0), P(do), P(dht), P(dq), P(dk), P(dv),
                   P(dg), P(db), P(dh0), None, 0, B, T, H, K, V, _lib.BF16, _lib.BF16, _lib.F32, _lib.BF16, _lib.F32,
-                  K ** -0.5, 0, P(ws), ws_bytes, sp)
+                  K ** -0.5, l2, P(ws), ws_bytes, sp)
 
     timer = Timer(args)
     res = timer.run(step)
@@ -537,7 +542,8 @@ def bench_backward(args, dev):
     alg = tok_heads * (2 * (4 * K + 3 * V) + 12) + B * H * 3 * K * V * 4
     flops = tok_heads * bwd_flops_per_tok_head(K, V)
     print(json.dumps({
-        "metric": f"GDN chunk-bwd tokens/s + TFLOP/s at T={T},H={H},dk={K},dv={V}", "value": B * T / wall,
+        "metric": f"GDN chunk-bwd tokens/s + TFLOP/s at T={T},H={H},dk={K},dv={V}"
+                  + (" with use_qk_l2norm_in_kernel=True" if l2 else ""), "value": B * T / wall,
         "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall * 1e3,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"kairos_gdn_chunk_bwd B={B} T={T} H={H} dk={K} dv={V} chunk 64, bf16 q/k/v/beta/do, "

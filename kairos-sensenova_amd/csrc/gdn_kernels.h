@@ -239,6 +239,12 @@ struct BwdArgs {
   void* qT;               // [NC, H, K, 64] q^T per chunk (zero past the chunk's end): written by the
                           // dv_local stage when set, read by the dh recurrence
   const void* wT;         // [NC, H, K, 64] w^T per chunk (zero past the chunk's end)
+  // the in-op L2 norm's backward (l2norm.py:132-154) folded into the kernels that form the final dq
+  // (the eight-wave dq / dk kernel) and dk (WY): rstd of each q / k row [B*T, H] from the forward
+  // norm pass, q / k above being the normalised rows; dq / dk then receive the gradients of the raw
+  // rows.  Null: dq / dk are the gradients of the normalised rows.
+  const float* rq;
+  const float* rk;
   const int64_t* cu;
   const int32_t* chunk_off;
   int N;
@@ -247,6 +253,8 @@ struct BwdArgs {
   float scale;
 };
 bool bwd_supported(int compute_dtype, int K, int V);
+// whether the dq / dk / dw / dg stage runs the eight-wave kernel (the one that takes BwdArgs::rq)
+bool bwd_dqk_wide(int compute_dtype, int K);
 // stages: a mask of BWD_DVL (dv_local), BWD_DHU (the dh recurrence: dh, dv2, dh0; dh and dv2 may
 // be null to skip their stores) and BWD_GRADS (dq, dk, dw, dg, then the WY backward: dq .. dbeta)
 enum : int { BWD_DVL = 1, BWD_DHU = 2, BWD_GRADS = 4, BWD_ALL = 7 };
@@ -290,9 +298,10 @@ int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float*
 int launch_seg_bwd_combine(const SegFwdArgs& p, const float* Bseg, const float* dht, float* F, float* dh0, int K,
                            int V, hipStream_t s);
 int launch_l2norm(const void* x, void* y, float* rstd, int dtype, int64_t rows, int D, hipStream_t s);
-// the same for two tensors of equal shape in one launch (x1, y1 may be null)
+// the same for two tensors of equal shape in one launch (x1, y1 may be null), rstd of each row into
+// r0 / r1 where not null
 int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,
-                   hipStream_t s);
+                   hipStream_t s, float* r0 = nullptr, float* r1 = nullptr);
 
 // Gated RMSNorm (gdn_norm.hip): y = x rstd w [+ b] * act(g) per row of D.
 struct NormArgs {

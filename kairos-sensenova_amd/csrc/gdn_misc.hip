@@ -23,11 +23,11 @@ namespace {
 template <typename T, int D>
 __global__ __launch_bounds__(256) void l2norm_kernel(const T* __restrict__ x0, T* __restrict__ y0,
                                                      const T* __restrict__ x1, T* __restrict__ y1,
-                                                     float* __restrict__ r0, int64_t rows) {
+                                                     float* __restrict__ r0, float* __restrict__ r1, int64_t rows) {
   constexpr int LPR = D / 8, RPW = WAVE / LPR, RPT = 4;
   const T* x = blockIdx.y ? x1 : x0;
   T* y = blockIdx.y ? y1 : y0;
-  float* r = blockIdx.y ? nullptr : r0;
+  float* r = blockIdx.y ? r1 : r0;
   const int l = lane_id();
   const int64_t wave = ((int64_t)blockIdx.x * 4 + threadIdx.x / WAVE) * RPT;
   const int sub = l / LPR, col = 8 * (l % LPR);
@@ -116,45 +116,46 @@ __global__ __launch_bounds__(64) void cumsum_kernel(const void* g, int g_dtype, 
 }  // namespace
 
 template <typename T, int D>
-void launch_l2norm_t(const void* x0, void* y0, const void* x1, void* y1, float* r0, int64_t rows, hipStream_t s) {
+void launch_l2norm_t(const void* x0, void* y0, const void* x1, void* y1, float* r0, float* r1, int64_t rows,
+                     hipStream_t s) {
   constexpr int64_t per_block = 4 * 4 * (WAVE / (D / 8));     // waves x row groups x rows per group
   const dim3 grid((unsigned)((rows + per_block - 1) / per_block), x1 ? 2u : 1u);
   hipLaunchKernelGGL((l2norm_kernel<T, D>), grid, dim3(256), 0, s, static_cast<const T*>(x0), static_cast<T*>(y0),
-                     static_cast<const T*>(x1), static_cast<T*>(y1), r0, rows);
+                     static_cast<const T*>(x1), static_cast<T*>(y1), r0, r1, rows);
 }
 
 template <typename T>
-int launch_l2norm_dt(const void* x0, void* y0, const void* x1, void* y1, float* r0, int64_t rows, int D,
+int launch_l2norm_dt(const void* x0, void* y0, const void* x1, void* y1, float* r0, float* r1, int64_t rows, int D,
                      hipStream_t s) {
   switch (D) {
-    case 64: launch_l2norm_t<T, 64>(x0, y0, x1, y1, r0, rows, s); break;
-    case 128: launch_l2norm_t<T, 128>(x0, y0, x1, y1, r0, rows, s); break;
-    case 256: launch_l2norm_t<T, 256>(x0, y0, x1, y1, r0, rows, s); break;
-    case 512: launch_l2norm_t<T, 512>(x0, y0, x1, y1, r0, rows, s); break;
+    case 64: launch_l2norm_t<T, 64>(x0, y0, x1, y1, r0, r1, rows, s); break;
+    case 128: launch_l2norm_t<T, 128>(x0, y0, x1, y1, r0, r1, rows, s); break;
+    case 256: launch_l2norm_t<T, 256>(x0, y0, x1, y1, r0, r1, rows, s); break;
+    case 512: launch_l2norm_t<T, 512>(x0, y0, x1, y1, r0, r1, rows, s); break;
     default: {
       const dim3 grid((unsigned)((rows + 3) / 4));
       hipLaunchKernelGGL(l2norm_wave_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x0), static_cast<T*>(y0),
                          r0, rows, D);
       if (x1)
         hipLaunchKernelGGL(l2norm_wave_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x1),
-                           static_cast<T*>(y1), nullptr, rows, D);
+                           static_cast<T*>(y1), r1, rows, D);
     }
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_l2norm2(const void* x0, void* y0, const void* x1, void* y1, int dtype, int64_t rows, int D,
-                   hipStream_t s) {
+                   hipStream_t s, float* r0, float* r1) {
   if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
-  if (dtype == DT_F32) return launch_l2norm_dt<float>(x0, y0, x1, y1, nullptr, rows, D, s);
-  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x0, y0, x1, y1, nullptr, rows, D, s);
+  if (dtype == DT_F32) return launch_l2norm_dt<float>(x0, y0, x1, y1, r0, r1, rows, D, s);
+  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x0, y0, x1, y1, r0, r1, rows, D, s);
   return -2;
 }
 
 int launch_l2norm(const void* x, void* y, float* rstd, int dtype, int64_t rows, int D, hipStream_t s) {
   if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
-  if (dtype == DT_F32) return launch_l2norm_dt<float>(x, y, nullptr, nullptr, rstd, rows, D, s);
-  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x, y, nullptr, nullptr, rstd, rows, D, s);
+  if (dtype == DT_F32) return launch_l2norm_dt<float>(x, y, nullptr, nullptr, rstd, nullptr, rows, D, s);
+  if (dtype == DT_BF16) return launch_l2norm_dt<bf16>(x, y, nullptr, nullptr, rstd, nullptr, rows, D, s);
   return -2;
 }
 

@@ -1228,7 +1228,8 @@ struct DqLds {
   static constexpr uint32_t COL_OFF = ROW_OFF + 10 * 16 * 4;   // ds2 column sums per lower tile [10][16]
   static constexpr uint32_t DGT_OFF = COL_OFF + 10 * 16 * 4;   // sum_d (dq1 q - dk1 k) per wave [8][64]
   static constexpr uint32_t SC_OFF = DGT_OFF + DQ_NW * C * 4;  // per wave: sum dk1 k [8], sum h dh [8]
-  static constexpr uint32_t TOTAL = SC_OFF + 2 * DQ_NW * 4;
+  static constexpr uint32_t L2_OFF = SC_OFF + 2 * DQ_NW * 4;   // the L2 backward's sum_d dq q per wave [8][64]
+  static constexpr uint32_t TOTAL = L2_OFF + DQ_NW * C * 4;
 };
 
 // instruction i of a [64][K] tile with natural rows (1 KB: rows (1024 / 2K) i ..; chunk c of row r at
@@ -1458,12 +1459,17 @@ __global__ __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(NB == 1 ?
   bf16* dq_out = reinterpret_cast<bf16*>(a.dq);
   bf16* dk_out = reinterpret_cast<bf16*>(a.dk1);
   bf16* dw_out = reinterpret_cast<bf16*>(a.dw);
+  // with the in-op L2 norm (a.rq): dq of the normalised row y_q = q, rounded as the two-step form
+  // stores it, is kept here until the row sums sum_d dq y_q are complete across the waves
+  const bool l2q = a.rq != nullptr;
+  float* s_l2 = reinterpret_cast<float*>(smem + L::L2_OFF);
+  u32x2 dqy[4][DT];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     const int t = 16 * tt + lc;
     const float egs = gexp(s_g[t]) * a.scale;
     const float gate = t < nv ? gexp(gl - s_g[t]) : 0.f;
-    float dgt = 0.f;
+    float dgt = 0.f, dqq = 0.f;
     // B operands: row t of ds (dq's ds k, K = t'), column t of ds read transposed (dk's ds^T q, K = i)
     Frag<bf16> bq[2], bk[2];
 #pragma unroll
@@ -1499,15 +1505,24 @@ __global__ __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(NB == 1 ?
         mma(dq, frag2(ldtr(base + K_OFF + oa, 0), ldtr(base + K_OFF + ob, 0)), bq[ks]);
         mma(dk, frag2(ldtr(base + Q_OFF + oa, 0), ldtr(base + Q_OFF + ob, 0)), bk[ks]);
       }
+      if (l2q) {
+        dqy[tt][dt] = u32x2{cv_pack(dq[0], dq[1]), cv_pack(dq[2], dq[3])};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dqq = fmaf(j & 1 ? cv_hi(dqy[tt][dt][j >> 1]) : cv_lo(dqy[tt][dt][j >> 1]), qv[j], dqq);
+      }
       if (t < nv) {
         const int64_t o = ((t0 + t) * H + h) * (int64_t)K + k0;
-        st4<bf16>(dq_out + o, dq[0], dq[1], dq[2], dq[3]);
+        if (!l2q) st4<bf16>(dq_out + o, dq[0], dq[1], dq[2], dq[3]);
         st4<bf16>(dk_out + o, dk[0], dk[1], dk[2], dk[3]);
         st4<bf16>(dw_out + o, -aw[dt][tt][0], -aw[dt][tt][1], -aw[dt][tt][2], -aw[dt][tt][3]);
       }
     }
     dgt = wsum_lg(dgt);
     if (lg == 0) s_dgt[wid * C + t] = dgt;
+    if (l2q) {
+      dqq = wsum_lg(dqq);
+      if (lg == 0) s_l2[wid * C + t] = dqq;
+    }
   }
   dglp = wsum64(dglp);
   hdh = wsum64(hdh);
@@ -1516,6 +1531,34 @@ __global__ __launch_bounds__(DQ_NT) __attribute__((amdgpu_waves_per_eu(NB == 1 ?
     s_sc[DQ_NW + wid] = hdh;
   }
   f_barrier();
+  // the L2 norm's backward of q (l2norm.py:132-154): dq_raw = dq rstd - (sum_d dq y_q) y_q rstd, the
+  // row sum added over the eight waves in a fixed order
+  if (l2q) {
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int t = 16 * tt + lc;
+      if (t < nv) {
+        float dot = s_l2[t];
+#pragma unroll
+        for (int w = 1; w < DQ_NW; ++w) dot += s_l2[w * C + t];
+        const float rs = a.rq[(t0 + t) * H + h];
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int k0 = RW * wid + 16 * dt + 4 * lg;
+          const u32x2 qw = *reinterpret_cast<const lds_u32x2*>(reinterpret_cast<lds_b*>(base + Q_OFF) + RB * t +
+                                                                 16 * ((k0 >> 3) ^ swz_n(t)) + 2 * (k0 & 7));
+          float x[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t yw = dqy[tt][dt][j >> 1], qq = qw[j >> 1];
+            const float y = j & 1 ? cv_hi(yw) : cv_lo(yw), qn = j & 1 ? cv_hi(qq) : cv_lo(qq);
+            x[j] = y * rs - dot * qn * rs;
+          }
+          st4<bf16>(dq_out + ((t0 + t) * H + h) * (int64_t)K + k0, x[0], x[1], x[2], x[3]);
+        }
+      }
+    }
+  }
   if (threadIdx.x < C) {
     const int t = threadIdx.x;
     if (t < nv) {

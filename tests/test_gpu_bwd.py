@@ -209,8 +209,9 @@ def test_bwd_wy_forms(waves, monkeypatch):
 def test_bwd_dq_forms_k128(form, monkeypatch):
     """dk=128: the dq / dk / dw / dg stage with eight waves owning K rows (the default for bf16 K >= 128;
     one buffer of value-block tiles, two workgroups per CU, or two buffers) and with four owning tokens
-    all match the oracle, on a ragged batch of 2 and a varlen batch with an empty and a 1-token
-    sequence."""
+    all match the oracle, on a ragged batch of 2, a varlen batch with an empty and a 1-token sequence,
+    and with the in-op L2 norm (whose backward of q the eight-wave kernel applies itself and the
+    four-wave form leaves to a pass of its own)."""
     if "4-wave" in form:
         monkeypatch.setenv("KAIROS_GDN_BWD_DQK_WIDE", "0")
     if "two block buffers" in form:
@@ -219,6 +220,8 @@ def test_bwd_dq_forms_k128(form, monkeypatch):
     run_case(2, 333, 2, 128, 128, seed=41)
     note(f"backward {form}: varlen [0, 0, 1, 200, 450] H=3 K=128 V=192")
     run_case(1, 450, 3, 128, 192, seed=42, cu=[0, 0, 1, 200, 450])
+    note(f"backward {form}: B=1 T=300 H=2 K=V=128 l2 (the norm's backward of q in the dq kernel or after it)")
+    run_case(1, 300, 2, 128, 128, seed=43, l2=True)
 
 
 @pytest.mark.parametrize("path", ["serial", "segments of 3 chunks", "segments of 1 chunk",
