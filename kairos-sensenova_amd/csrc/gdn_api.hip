@@ -320,9 +320,9 @@ size_t bwd_ws(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int64_t n_s
   total += align_up(tok * kgdn::C * es);                 // Ai
   total += 2 * align_up(nc * H * K * V * es);            // h, dh
   total += 3 * align_up(tok * V * es);                   // v_new, dv_local, dv2
-  if (use_l2) {                                          // qn, kn, rstd of each (the L2 backward of k is
-    total += 2 * align_up(tok * K * es) + 2 * align_up(tok * sizeof(float));   // folded into WY) and dqn
-    if (!kgdn::bwd_dqk_wide(cdt, (int)K)) total += align_up(tok * K * es);      // where dq's is not
+  if (use_l2) {                                          // qn, kn, dkn, rstd of q, and dqn where the
+    total += 3 * align_up(tok * K * es) + align_up(tok * sizeof(float));         // dq kernel does not
+    if (!kgdn::bwd_dqk_wide(cdt, (int)K)) total += align_up(tok * K * es);      // take q's norm backward
   }
   if (!seg && kgdn::wide_dhu_supported(cdt, (int)K, (int)V))
     total += 2 * align_up(nc * H * K * kgdn::C * es);    // q^T (k^T first with rc_wide), w^T per chunk
@@ -1138,20 +1138,19 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   const void* qx = q;
   const void* kx = k;
   void* dq_k = dq;
+  void* dk_k = dk;
   float* rq = nullptr;
-  float* rk = nullptr;
-  // the L2 norm's backward: folded into the kernels that form the final dq (the eight-wave dq / dk
-  // kernel) and dk (WY), from the rstd of each row the forward norm pass records; dq's runs as its own
-  // pass (l2norm_bwd) where the four-wave dq kernel runs
+  // the L2 norm's backward: q's folded into the eight-wave dq / dk kernel (from the rstd of each q row
+  // the forward norm pass records), else a pass of its own (l2norm_bwd) like k's
   const bool l2q_fold = use_qk_l2norm && kgdn::bwd_dqk_wide(cdt, (int)K);
   if (use_qk_l2norm) {
     void* qn = cv.take(tok * K * es);
     void* kn = cv.take(tok * K * es);
     rq = static_cast<float*>(cv.take(tok * sizeof(float)));
-    rk = static_cast<float*>(cv.take(tok * sizeof(float)));
+    dk_k = cv.take(tok * K * es);
     if (!l2q_fold) dq_k = cv.take(tok * K * es);
     if (any_tokens) {
-      if (int rc = from_launch(kgdn::launch_l2norm2(q, qn, k, kn, qk_dtype, (int64_t)tok, (int)K, s, rq, rk),
+      if (int rc = from_launch(kgdn::launch_l2norm2(q, qn, k, kn, qk_dtype, (int64_t)tok, (int)K, s, rq, nullptr),
                                "l2norm(q, k)"))
         return rc;
     }
@@ -1180,9 +1179,8 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
   ba.q = qx; ba.k = kx; ba.v = v; ba.gc = gc; ba.beta = beta; ba.beta_dtype = beta_dtype;
   ba.do_ = do_; ba.dht = dht; ba.w = w; ba.Ai = Ai; ba.h = hs; ba.vn = vn;
   ba.dvl = dvl; ba.dh = dhs; ba.dv2 = dv2; ba.dw = dwb; ba.dk1 = dk1; ba.dg1 = dg1;
-  ba.dq = dq_k; ba.dk = dk; ba.dv = dv; ba.dg = dg; ba.db = dbeta; ba.dh0 = dh0;
+  ba.dq = dq_k; ba.dk = dk_k; ba.dv = dv; ba.dg = dg; ba.db = dbeta; ba.dh0 = dh0;
   ba.rq = l2q_fold ? rq : nullptr;
-  ba.rk = rk;
   ba.cu = cu_seqlens; ba.chunk_off = chunk_off; ba.N = N; ba.T = T; ba.H = (int)H; ba.scale = scale;
   ba.qT = dhu_wide ? qT : nullptr;
   ba.wT = wT;
@@ -1259,8 +1257,12 @@ int kairos_gdn_chunk_bwd(const void* q, const void* k, const void* v, const void
     if (int rc = from_launch(kgdn::launch_bwd(b2, cdt, (int)K, (int)V, nc_b, kgdn::BWD_DHU, s), what)) return rc;
     if (int rc = from_launch(kgdn::launch_bwd(bs, cdt, (int)K, (int)V, nc_b, kgdn::BWD_GRADS, s), what)) return rc;
   }
-  if (use_qk_l2norm && !l2q_fold && any_tokens) {
-    if (int rc = from_launch(kgdn::launch_l2norm_bwd(q, dq_k, dq, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(q)"))
+  if (use_qk_l2norm && any_tokens) {
+    if (!l2q_fold) {
+      if (int rc = from_launch(kgdn::launch_l2norm_bwd(q, dq_k, dq, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(q)"))
+        return rc;
+    }
+    if (int rc = from_launch(kgdn::launch_l2norm_bwd(k, dk_k, dk, qk_dtype, (int64_t)tok, (int)K, s), "l2norm_bwd(k)"))
       return rc;
   }
   return ok();

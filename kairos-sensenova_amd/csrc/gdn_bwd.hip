@@ -178,7 +178,6 @@ __device__ __forceinline__ float sum64(float x) {
 template <typename TC>
 __device__ __forceinline__ void st4v(TC* p, const f32x4& v) { st4<TC>(p, v[0], v[1], v[2], v[3]); }
 
-
 template <typename TC>
 __device__ __forceinline__ f32x4 g_row4(const TC* p) { return ld4<TC>(p); }
 
@@ -958,11 +957,10 @@ __global__ __launch_bounds__(NT_B) void bwd_dqkwg_kernel(BwdArgs a, int V) {
 template <typename TC, int G = 1>
 __host__ __device__ constexpr size_t wy_lds(int K, int V) {
   return sizeof(TC) * (2 * (size_t)tile_elems<TC>(K) + tile_elems<TC>(V) + 3 * (size_t)tile_elems<TC>(64)) +
-         (6 + 3 * G) * 64 * sizeof(float);
+         (6 + 2 * G) * 64 * sizeof(float);
 }
 
-// L2: the in-op L2 norm's backward of k folded in (a.rk set)
-template <typename TC, int K, int G, bool L2>
+template <typename TC, int K, int G>
 __global__ __launch_bounds__(NT_B * G) void bwd_wy_kernel(BwdArgs a, int V) {
   static_assert(G == 1 || G == 2 || G == 4, "four, eight or sixteen waves");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -977,7 +975,6 @@ __global__ __launch_bounds__(NT_B * G) void bwd_wy_kernel(BwdArgs a, int V) {
   float* s_dgc = s_b + 64;                            // [4][64]: column parts of dg2, one row per token tile
   float* s_dgp = s_dgc + 4 * 64;                      // [G][64]: row parts of dg2 (+ dkbg.kbg), one row per group
   float* s_dbp = s_dgp + G * 64;                      // [G][64]: dbeta, one row per group
-  float* s_l2 = s_dbp + G * 64;                       // [G][64]: the L2 backward's sum_d dk y_k, one row per group
   const int h = blockIdx.y, H = a.H;
   const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
   if (!loc.ok) return;
@@ -1131,12 +1128,6 @@ __global__ __launch_bounds__(NT_B * G) void bwd_wy_kernel(BwdArgs a, int V) {
   }
   float dbt = 0.f, dgt = 0.f;
   TC* dk_out = reinterpret_cast<TC*>(a.dk);
-  // with the in-op L2 norm (L2, a.rk): dk of the normalised row y_k = k (staged above) goes to dk
-  // rounded, as the two-step form stores it, and is read back (this lane's own stores) once the row
-  // sums sum_d dk y_k are complete across the groups (held in registers instead, the kept rows spill
-  // at sixteen waves)
-  constexpr bool l2k = L2;
-  float dkk = 0.f;
 #pragma unroll
   for (int i = 0; i < NKT; ++i) {
     const int kt = NKT * gq + i;
@@ -1162,10 +1153,6 @@ __global__ __launch_bounds__(NT_B * G) void bwd_wy_kernel(BwdArgs a, int V) {
       dgt += a1[jj] * (kv[jj] * bt * egt);
       const float dk2 = round_to<TC>(dkr + a3[jj] + a2[jj] * bt);
       dk[jj] = d1[jj] + dk2;
-    }
-    if constexpr (l2k) {
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dkk = fmaf(round_to<TC>(dk[jj]), kv[jj], dkk);
     }
     if (t < nv) st4v<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0, dk);
   }
@@ -1198,33 +1185,11 @@ __global__ __launch_bounds__(NT_B * G) void bwd_wy_kernel(BwdArgs a, int V) {
   }
   dbt = sum_lg(dbt);
   dgt = sum_lg(dgt);
-  if (l2k) dkk = sum_lg(dkk);
   if (lg == 0) {
     s_dgp[gq * 64 + t] += dgt;                        // token t's entry of this group's row is this wave's
     s_dbp[gq * 64 + t] = dbt;
-    if (l2k) s_l2[gq * 64 + t] = dkk;
   }
   __syncthreads();
-  // the L2 norm's backward of k (l2norm.py:132-154): dk_raw = dk rstd - (sum_d dk y_k) y_k rstd, the
-  // row sum added over the groups in a fixed order
-  if constexpr (l2k) {
-    if (t < nv) {
-    float dot = s_l2[t];
-#pragma unroll
-    for (int q = 1; q < G; ++q) dot += s_l2[q * 64 + t];
-    const float rs = a.rk[(t0 + t) * H + h];
-#pragma unroll 1
-    for (int i = 0; i < NKT; ++i) {                   // (one K tile at a time: few live registers)
-      const int k0 = 16 * (NKT * gq + i) + 4 * lg;
-      const f32x4 kv = t_row4<TC>(s_k, K, t, k0);
-      const f32x4 y = g_row4<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0);   // stored before the barrier
-      f32x4 dx;
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) dx[jj] = y[jj] * rs - dot * kv[jj] * rs;
-      st4v<TC>(dk_out + ((t0 + t) * H + h) * (int64_t)K + k0, dx);
-    }
-    }
-  }
   // ---- dbeta = the groups' parts in group order; dg = reverse cumsum within the chunk of dg1 + dg2
   if (wid == 0) {
     float x = 0.f, db = 0.f;
@@ -1292,19 +1257,6 @@ int set_lds(K_ kern, size_t bytes) {
       hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)bytes) != hipSuccess)
     return -1;
-  return 0;
-}
-
-template <typename TC, int K, int G>
-int launch_wy(const BwdArgs& a, int V, dim3 grid, hipStream_t s) {
-  const size_t l4 = wy_lds<TC, G>(K, V);
-  if (a.rk) {
-    if (set_lds(bwd_wy_kernel<TC, K, G, true>, l4)) return -1;
-    hipLaunchKernelGGL((bwd_wy_kernel<TC, K, G, true>), grid, dim3(NT_B * G), l4, s, a, V);
-  } else {
-    if (set_lds(bwd_wy_kernel<TC, K, G, false>, l4)) return -1;
-    hipLaunchKernelGGL((bwd_wy_kernel<TC, K, G, false>), grid, dim3(NT_B * G), l4, s, a, V);
-  }
   return 0;
 }
 
@@ -1407,14 +1359,19 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
       wg = want == 4 ? 1 : want == 8 ? 2 : want == 16 ? 4 : (wy_lds<TC, 2>(K, V) > 80 * 1024 ? 4 : 2);
       if (wy_lds<TC, 4>(K, V) > 160 * 1024) wg = 1;
       if (wg == 4) {
-        if (int rc = launch_wy<TC, K, 4>(a, V, grid, s)) return rc;
+        const size_t l4 = wy_lds<TC, 4>(K, V);
+        if (set_lds(bwd_wy_kernel<TC, K, 4>, l4)) return -1;
+        hipLaunchKernelGGL((bwd_wy_kernel<TC, K, 4>), grid, dim3(NT_B * 4), l4, s, a, V);
       } else if (wg == 2) {
-        if (int rc = launch_wy<TC, K, 2>(a, V, grid, s)) return rc;
+        const size_t l4 = wy_lds<TC, 2>(K, V);
+        if (set_lds(bwd_wy_kernel<TC, K, 2>, l4)) return -1;
+        hipLaunchKernelGGL((bwd_wy_kernel<TC, K, 2>), grid, dim3(NT_B * 2), l4, s, a, V);
       }
     }
     if (wg == 1) {
-      if (wy_lds<TC, 1>(K, V) > 160 * 1024) return -1;
-      if (int rc = launch_wy<TC, K, 1>(a, V, grid, s)) return rc;
+      const size_t l4 = wy_lds<TC, 1>(K, V);
+      if (l4 > 160 * 1024 || set_lds(bwd_wy_kernel<TC, K, 1>, l4)) return -1;
+      hipLaunchKernelGGL((bwd_wy_kernel<TC, K, 1>), grid, dim3(NT_B), l4, s, a, V);
     }
   }
   return hipGetLastError() == hipSuccess ? 0 : -1;

@@ -239,12 +239,10 @@ struct BwdArgs {
   void* qT;               // [NC, H, K, 64] q^T per chunk (zero past the chunk's end): written by the
                           // dv_local stage when set, read by the dh recurrence
   const void* wT;         // [NC, H, K, 64] w^T per chunk (zero past the chunk's end)
-  // the in-op L2 norm's backward (l2norm.py:132-154) folded into the kernels that form the final dq
-  // (the eight-wave dq / dk kernel) and dk (WY): rstd of each q / k row [B*T, H] from the forward
-  // norm pass, q / k above being the normalised rows; dq / dk then receive the gradients of the raw
-  // rows.  Null: dq / dk are the gradients of the normalised rows.
+  // the in-op L2 norm's backward of q (l2norm.py:132-154) folded into the eight-wave dq / dk kernel:
+  // rstd of each q row [B*T, H] from the forward norm pass, q above being the normalised rows; dq then
+  // receives the gradient of the raw rows.  Null: dq is the gradient of the normalised rows.
   const float* rq;
-  const float* rk;
   const int64_t* cu;
   const int32_t* chunk_off;
   int N;
