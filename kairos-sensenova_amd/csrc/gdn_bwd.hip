@@ -1251,6 +1251,49 @@ __global__ __launch_bounds__(256) void l2norm_bwd_kernel(const T* __restrict__ x
   }
 }
 
+// The same for D a power of two (8 .. 512): a row takes LPR = D / 8 lanes, a wave holds 64 / LPR rows,
+// and each thread handles RPT row groups with all their loads issued before the first reduction (the
+// one-wave-per-row form leaves lanes idle below D = 512 and keeps one row's loads in flight).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void l2norm_bwd_rows_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                              T* __restrict__ dx, int64_t rows) {
+  constexpr int LPR = D / 8, RPW = WAVE / LPR, RPT = 4;
+  const int l = lane_id();
+  const int64_t wave = ((int64_t)blockIdx.x * 4 + threadIdx.x / WAVE) * RPT;
+  const int sub = l / LPR, col = 8 * (l % LPR);
+  Vec8<T> xv[RPT], gv[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int64_t row = (wave + i) * RPW + sub;
+    xv[i] = row < rows ? ld8<T>(x + row * D + col) : vzero<T>();
+    gv[i] = row < rows ? ld8<T>(dy + row * D + col) : vzero<T>();
+  }
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int64_t row = (wave + i) * RPW + sub;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(vget<T>(xv[i], e), vget<T>(xv[i], e), ss);
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, WAVE);
+    const float rstd = 1.0f / sqrtf(ss + 1e-6f);
+    float y[8], dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y[e] = round_to<T>(vget<T>(xv[i], e) * rstd);
+      dot = fmaf(vget<T>(gv[i], e), y[e], dot);
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) dot += __shfl_xor(dot, off, WAVE);
+    if (row < rows) {
+      Vec8<T> o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vset<T>(o, e, vget<T>(gv[i], e) * rstd - dot * y[e] * rstd);
+      st8<T>(dx + row * D + col, o);
+    }
+  }
+}
+
 template <typename K_>
 int set_lds(K_ kern, size_t bytes) {
   if (bytes > 64 * 1024 &&
@@ -1402,8 +1445,29 @@ int launch_bwd(const BwdArgs& a, int compute_dtype, int K, int V, int64_t nc_gri
   return -2;
 }
 
+template <typename T>
+bool launch_l2norm_bwd_rows(const void* x, const void* dy, void* dx, int64_t rows, int D, hipStream_t s) {
+  auto go = [&](auto kern, int lpr) {
+    const int64_t per_block = 4 * 4 * (WAVE / lpr);        // waves x row groups x rows per group
+    hipLaunchKernelGGL(kern, dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256), 0, s,
+                       static_cast<const T*>(x), static_cast<const T*>(dy), static_cast<T*>(dx), rows);
+    return true;
+  };
+  switch (D) {
+    case 64: return go(l2norm_bwd_rows_kernel<T, 64>, 8);
+    case 128: return go(l2norm_bwd_rows_kernel<T, 128>, 16);
+    case 256: return go(l2norm_bwd_rows_kernel<T, 256>, 32);
+    case 512: return go(l2norm_bwd_rows_kernel<T, 512>, 64);
+    default: return false;
+  }
+}
+
 int launch_l2norm_bwd(const void* x, const void* dy, void* dx, int dtype, int64_t rows, int D, hipStream_t s) {
   if (D % 8 != 0 || D > 512 || rows <= 0) return -2;
+  if (dtype == DT_F32 && launch_l2norm_bwd_rows<float>(x, dy, dx, rows, D, s))
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+  if (dtype == DT_BF16 && launch_l2norm_bwd_rows<bf16>(x, dy, dx, rows, D, s))
+    return hipGetLastError() == hipSuccess ? 0 : -1;
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (dtype == DT_F32) {
     hipLaunchKernelGGL(l2norm_bwd_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(x),
