@@ -2484,7 +2484,8 @@ __global__ void seg_seq_map_kernel(SegGeom G, int ns_grid, int64_t* __restrict__
 
 // dst[s] = src[n] for the first (first_seg) or the last segment of each sequence n, zeros for the
 // other segments: [ns, H, K * V] fp32 from [N, H, K * V] (src: h0_dtype, or nullptr = zeros).
-// With first_seg the other segments are left alone (seg_combine writes them).
+// With first_seg the other segments are left alone (seg_combine writes them).  blockIdx.z splits
+// each K * V state into gridDim.z slices (a (segment, head) grid alone is too few workgroups).
 __global__ __launch_bounds__(256) void seg_place_kernel(SegGeom G, const void* src, int src_dtype, float* dst,
                                                         int KV, int first_seg) {
   const int s = blockIdx.x, h = blockIdx.y, H = G.H;
@@ -2494,7 +2495,8 @@ __global__ __launch_bounds__(256) void seg_place_kernel(SegGeom G, const void* s
   if (first_seg && !pick) return;
   float* d = dst + ((int64_t)s * H + h) * KV;
   const int64_t so = ((int64_t)sl.n * H + h) * KV;
-  for (int i = 4 * threadIdx.x; i < KV; i += 4 * blockDim.x) {     // KV is a multiple of 4
+  const int span = (KV / 4 + gridDim.z - 1) / gridDim.z * 4, i0 = span * blockIdx.z, i1 = min(KV, i0 + span);
+  for (int i = i0 + 4 * threadIdx.x; i < i1; i += 4 * blockDim.x) {   // KV and span are multiples of 4
     f32x4 x = {0.f, 0.f, 0.f, 0.f};
     if (pick && src) {
       if (src_dtype == DT_F32) {
@@ -2747,8 +2749,8 @@ int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float*
                      hipStream_t s) {
   const SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
   if (p.ns_grid <= 0) return 0;
-  hipLaunchKernelGGL(seg_place_kernel, dim3((unsigned)p.ns_grid, (unsigned)p.H), dim3(256), 0, s, G, src, src_dtype,
-                     dst, K * V, first_seg ? 1 : 0);
+  hipLaunchKernelGGL(seg_place_kernel, dim3((unsigned)p.ns_grid, (unsigned)p.H, 8u), dim3(256), 0, s, G, src,
+                     src_dtype, dst, K * V, first_seg ? 1 : 0);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
