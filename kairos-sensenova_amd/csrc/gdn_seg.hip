@@ -2521,9 +2521,10 @@ __global__ __launch_bounds__(256) void seg_place_kernel(SegGeom G, const void* s
 // bf16 MFMA as hi hi + hi lo + lo hi (x = hi + lo on both sides, fp32 accumulation): M_j is
 // staged in LDS as K / 64 tiles of [64 rows][K] and read transposed; X's accumulator tiles are
 // the B operand.  The next step's map is loaded into registers while the current one computes.
-template <int K, int V>
+// S: workgroups per (sequence, head), each on V / S of the value columns (each stages the whole map)
+template <int K, int V, int S>
 struct RCfg {
-  static constexpr int NW = V / 16, NT = NW * WAVE;
+  static constexpr int NW = V / 16 / S, NT = NW * WAVE;
   static constexpr int KT = K / 16, KS = K / 32;
   static constexpr int EM = K * K;                       // elements of one bf16 half of a map
   static constexpr int UM = 2 * EM / 8 / NT;             // 16-byte units of (hi, lo) per thread
@@ -2535,23 +2536,24 @@ struct RCfg {
 template <int K>
 __device__ __forceinline__ int moff(int r, int c) { return (r >> 6) * 64 * K + toff<bf16>(r & 63, c, K); }
 
-template <int K, int V>
-__global__ __launch_bounds__((RCfg<K, V>::NT)) void seg_bwd_combine_kernel(SegGeom G, const bf16* __restrict__ M,
+template <int K, int V, int S>
+__global__ __launch_bounds__((RCfg<K, V, S>::NT)) void seg_bwd_combine_kernel(SegGeom G, const bf16* __restrict__ M,
                                                                           const float* __restrict__ Bseg,
                                                                           const float* __restrict__ dht,
                                                                           float* __restrict__ F,
                                                                           float* __restrict__ dh0, int total) {
-  using RC = RCfg<K, V>;
+  using RC = RCfg<K, V, S>;
   constexpr int KT = RC::KT, KS = RC::KS;
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* s_mh = reinterpret_cast<bf16*>(smem);
   bf16* s_ml = s_mh + RC::EM;
   const int per_xcd = gridDim.x / 8;
-  const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (unit >= total) return;
+  const int o_idx = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (o_idx >= total) return;
+  const int unit = o_idx / S, slice = o_idx % S;       // the slices of a head are neighbours on one XCD
   const int H = G.H, n = unit / H, h = unit % H;
   const int tid = threadIdx.x, wid = tid / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
-  const int col = 16 * wid + lc;
+  const int col = 16 * (wid + RC::NW * slice) + lc;
   int nseg, s_first;
   if (G.cu == nullptr) {
     nseg = G.T > 0 ? G.nseg_fixed : 0;
@@ -2757,21 +2759,23 @@ int launch_seg_place(const SegFwdArgs& p, const void* src, int src_dtype, float*
 int launch_seg_bwd_combine(const SegFwdArgs& p, const float* Bseg, const float* dht, float* F, float* dh0, int K,
                            int V, hipStream_t s) {
   const SegGeom G{p.cu, p.chunk_off, p.seg_off, p.N, p.T, p.H, p.L, p.nseg_fixed};
-  const int total = p.N * p.H;
-  if (total <= 0) return 0;
-  const int grid = (total + 7) / 8 * 8;
+  if (p.N * p.H <= 0) return 0;
   const bf16* M = reinterpret_cast<const bf16*>(p.M);
-#define KGDN_RC(KK, VV)                                                                                     \
+  // V = 128: two workgroups per (sequence, head) of four waves (each reads the transposed map once
+  // per step instead of eight waves on one CU); fewer threads would hold more of the map each
+#define KGDN_RC(KK, VV, SS)                                                                                 \
   if (K == KK && V == VV) {                                                                                 \
-    using RC = RCfg<KK, VV>;                                                                                \
+    using RC = RCfg<KK, VV, SS>;                                                                            \
     constexpr int nt = RC::NT;                                                                              \
     constexpr size_t lds = RC::lds;                                                                         \
-    if (set_lds(seg_bwd_combine_kernel<KK, VV>, lds)) return -1;                                            \
-    hipLaunchKernelGGL((seg_bwd_combine_kernel<KK, VV>), dim3(grid), dim3(nt), lds, s, G, M, Bseg, dht, F, dh0, \
-                       total);                                                                              \
+    const int total = p.N * p.H * SS;                                                                       \
+    const int grid = (total + 7) / 8 * 8;                                                                   \
+    if (set_lds(seg_bwd_combine_kernel<KK, VV, SS>, lds)) return -1;                                        \
+    hipLaunchKernelGGL((seg_bwd_combine_kernel<KK, VV, SS>), dim3(grid), dim3(nt), lds, s, G, M, Bseg, dht, F, \
+                       dh0, total);                                                                         \
     return hipGetLastError() == hipSuccess ? 0 : -1;                                                        \
   }
-  KGDN_RC(64, 64) KGDN_RC(64, 128) KGDN_RC(128, 64) KGDN_RC(128, 128)
+  KGDN_RC(64, 64, 1) KGDN_RC(64, 128, 2) KGDN_RC(128, 64, 1) KGDN_RC(128, 128, 2)
 #undef KGDN_RC
   return -2;
 }
