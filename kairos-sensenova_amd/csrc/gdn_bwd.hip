@@ -261,6 +261,108 @@ __global__ __launch_bounds__(64 * NW) void bwd_dvl_kernel(BwdArgs a, int V) {
   }
 }
 
+// The same stage for bf16 dk = 256 with dv a multiple of 256, its tiles staged in halves through one
+// 32 KB buffer (q and k in two halves of 128 columns, M accumulated across them in registers, then
+// do in blocks of 256 columns): 40 KB of LDS, three workgroups per CU instead of one (136 KB).
+__device__ __forceinline__ void stage_rows_dma_cols(bf16* tile, const bf16* src, int64_t t0, int nv, int H, int h,
+                                                    int row_len, int c0, int ncol) {
+  const int nw = blockDim.x / WAVE, wid = threadIdx.x / WAVE, l = lane_id();
+  const unsigned char* base = reinterpret_cast<const unsigned char*>(src + (t0 * H + h) * (int64_t)row_len + c0);
+  const uint32_t row_bytes = (uint32_t)(H * row_len * 2);
+  const uint32_t tile_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) bf16*)tile;
+  for (int i = wid; i < ncol / 8; i += nw) {
+    const int cb = i >> 3, r = 8 * (i & 7) + (l >> 3);
+    const int c8 = (l & 7) ^ ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));   // swz_off<64>'s chunk order
+    const uint32_t dst = tile_lds + 8192u * cb + 1024u * (i & 7);
+    if (r < nv) {
+      stage_dma16(base, (uint32_t)r * row_bytes + (uint32_t)(64 * cb + 8 * c8) * 2u, dst);
+    } else {
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>((uintptr_t)(dst + 16u * l)) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+constexpr int DVL_SPLIT_NW = 8;
+constexpr size_t dvl_split_lds = (size_t)2 * 64 * 256 + (size_t)2 * 64 * 64 + 64 * sizeof(float);
+
+__global__ __launch_bounds__(64 * DVL_SPLIT_NW) void bwd_dvl_split_kernel(BwdArgs a, int V) {
+  constexpr int K = 256, KH = 128, VB = 256, NW = DVL_SPLIT_NW;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* s_buf = reinterpret_cast<bf16*>(smem);          // q, k halves [64][128] each, or a do block [64][256]
+  bf16* s_qh = s_buf;
+  bf16* s_kh = s_buf + 64 * KH;
+  bf16* s_M = s_buf + 64 * VB;
+  float* s_g = reinterpret_cast<float*>(s_M + 64 * 64);
+  const int h = blockIdx.y, H = a.H;
+  const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
+  if (!loc.ok) return;
+  const int64_t t0 = loc.t0;
+  const int nv = loc.nv;
+  const int wid = threadIdx.x / WAVE, l = lane_id(), lg = l >> 4, lc = l & 15;
+  const bf16* q = reinterpret_cast<const bf16*>(a.q);
+  const bf16* k = reinterpret_cast<const bf16*>(a.k);
+  if (threadIdx.x < 64) s_g[threadIdx.x] = threadIdx.x < nv ? a.gc[(t0 + threadIdx.x) * H + h] : 0.f;
+  // M^T[j][i] = k_j . q_i over the two halves of the head dim, tiles wid and wid + 8 of this wave
+  f32x4 acc[16 / NW];
+#pragma unroll
+  for (int u = 0; u < 16 / NW; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16* qt = a.qT ? reinterpret_cast<bf16*>(a.qT) + (blockIdx.x * (int64_t)H + h) * (K * C) : nullptr;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    if (half) __syncthreads();                          // every wave is done with the first half
+    stage_rows_dma_cols(s_qh, q, t0, nv, H, h, K, KH * half, KH);
+    stage_rows_dma_cols(s_kh, k, t0, nv, H, h, K, KH * half, KH);
+    stage_wait();
+    __syncthreads();
+    // q^T per chunk, [NC, H, K, 64] (zero past the chunk's end): rows d of this half
+    if (qt) {
+      for (int i = wid; i < (KH / 16) * 4; i += NW) {
+        const int d0 = 16 * (i >> 2), tr0 = 16 * (i & 3) + 4 * lg;
+        const s16x4_t x = lds_read_tr16(s_qh + toff<bf16>(tr0 + (lc >> 2), d0 + 4 * (lc & 3), KH));
+        *reinterpret_cast<s16x4_t*>(qt + (KH * half + d0 + lc) * C + tr0) = x;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 16 / NW; ++u) {
+      const int tile = wid + NW * u, tj = tile >> 2, ti = tile & 3;
+      if (tj <= ti) {
+#pragma unroll
+        for (int ks = 0; ks < KH / 32; ++ks)
+          mma(acc[u], t_nat<bf16>(s_kh, KH, 16 * tj, 32 * ks), t_nat<bf16>(s_qh, KH, 16 * ti, 32 * ks));
+      }
+    }
+  }
+  // M^T rounded to bf16 (the reference's b_A.to(do.dtype))
+#pragma unroll
+  for (int u = 0; u < 16 / NW; ++u) {
+    const int tile = wid + NW * u, tj = tile >> 2, ti = tile & 3;
+    const int i = 16 * ti + lc;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 16 * tj + 4 * lg + jj;
+      const float val = (j <= i && i < nv) ? acc[u][jj] * a.scale * gexp(s_g[i] - s_g[j]) : 0.f;
+      s_M[toff<bf16>(j, i, 64)] = (bf16)val;
+    }
+  }
+  // dv_local^T[v][j] = sum_i do[i][v] M^T[j][i], do in blocks of 256 columns
+  bf16* out = reinterpret_cast<bf16*>(a.dvl);
+  const bf16* dO = reinterpret_cast<const bf16*>(a.do_);
+  for (int vb = 0; vb < V; vb += VB) {
+    __syncthreads();                                    // s_M written / the previous block read
+    stage_rows_dma_cols(s_buf, dO, t0, nv, H, h, V, vb, VB);
+    stage_wait();
+    __syncthreads();
+    for (int tile = wid; tile < (VB / 16) * 4; tile += NW) {
+      const int tv = tile >> 2, tj = tile & 3;
+      f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) mma(r, t_tr<bf16>(s_buf, VB, 32 * ks, 16 * tv), t_acc<bf16>(s_M, 64, 16 * tj, 32 * ks));
+      const int j = 16 * tj + lc;
+      if (j < nv) st4v<bf16>(out + ((t0 + j) * H + h) * (int64_t)V + vb + 16 * tv + 4 * lg, r);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dh recurrence (chunk_delta_h.py:250-438).  One workgroup per (sequence, head,
 // 16 value columns), NW waves splitting the K rows of the state gradient dh
@@ -1315,8 +1417,17 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
     if (l1 > 160 * 1024) return -1;
     const char* e = std::getenv("KAIROS_GDN_BWD_DVL_WAVES");
     const int want = e ? std::atoi(e) : 0;
+    bool split = false;
+    if constexpr (sizeof(TC) == 2 && K == 256) {       // the halves form (KAIROS_GDN_BWD_DVL_SPLIT=0: whole tiles)
+      const char* es = std::getenv("KAIROS_GDN_BWD_DVL_SPLIT");
+      if (V % 256 == 0 && want == 0 && !(es && es[0] == '0' && es[1] == 0)) {
+        hipLaunchKernelGGL(bwd_dvl_split_kernel, grid, dim3(64 * DVL_SPLIT_NW), dvl_split_lds, s, a, V);
+        split = true;
+      }
+    }
     const int nw = want == 4 || want == 8 || want == 16 ? want : l1 > 80 * 1024 ? 8 : 16;
-    if (nw == 16) {
+    if (split) {
+    } else if (nw == 16) {
       if (set_lds(bwd_dvl_kernel<TC, K, 16>, l1)) return -1;
       hipLaunchKernelGGL((bwd_dvl_kernel<TC, K, 16>), grid, dim3(64 * 16), l1, s, a, V);
     } else if (nw == 8) {
