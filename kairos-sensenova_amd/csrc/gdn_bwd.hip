@@ -261,9 +261,10 @@ __global__ __launch_bounds__(64 * NW) void bwd_dvl_kernel(BwdArgs a, int V) {
   }
 }
 
-// The same stage for bf16 dk = 256 with dv a multiple of 256, its tiles staged in halves through one
-// 32 KB buffer (q and k in two halves of 128 columns, M accumulated across them in registers, then
-// do in blocks of 256 columns): 40 KB of LDS, three workgroups per CU instead of one (136 KB).
+// The same stage for bf16 with its tiles staged in parts through one buffer: q and k in two halves
+// of K / 2 columns (M accumulated across them in registers), then do in blocks of VB columns.  At
+// dk = 256 (VB = 256) 40 KB of LDS, three workgroups per CU instead of one (136 KB); at dk = 128
+// (VB = 128) 24 KB.
 __device__ __forceinline__ void stage_rows_dma_cols(bf16* tile, const bf16* src, int64_t t0, int nv, int H, int h,
                                                     int row_len, int c0, int ncol) {
   const int nw = blockDim.x / WAVE, wid = threadIdx.x / WAVE, l = lane_id();
@@ -283,15 +284,20 @@ __device__ __forceinline__ void stage_rows_dma_cols(bf16* tile, const bf16* src,
 }
 
 constexpr int DVL_SPLIT_NW = 8;
-constexpr size_t dvl_split_lds = (size_t)2 * 64 * 256 + (size_t)2 * 64 * 64 + 64 * sizeof(float);
+template <int K, int VB>
+constexpr size_t dvl_split_lds() {
+  return (size_t)2 * 64 * (K > VB ? K : VB) + (size_t)2 * 64 * 64 + 64 * sizeof(float);
+}
 
+template <int K, int VB>
 __global__ __launch_bounds__(64 * DVL_SPLIT_NW) void bwd_dvl_split_kernel(BwdArgs a, int V) {
-  constexpr int K = 256, KH = 128, VB = 256, NW = DVL_SPLIT_NW;
+  constexpr int KH = K / 2, NW = DVL_SPLIT_NW, BUF = K > VB ? K : VB;
+  static_assert(KH % 32 == 0 && VB % 64 == 0, "halves of whole MMA steps, blocks of whole column tiles");
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* s_buf = reinterpret_cast<bf16*>(smem);          // q, k halves [64][128] each, or a do block [64][256]
   bf16* s_qh = s_buf;
   bf16* s_kh = s_buf + 64 * KH;
-  bf16* s_M = s_buf + 64 * VB;
+  bf16* s_M = s_buf + 64 * BUF;
   float* s_g = reinterpret_cast<float*>(s_M + 64 * 64);
   const int h = blockIdx.y, H = a.H;
   const ChunkLoc loc = locate_chunk(blockIdx.x, a.cu, a.chunk_off, a.N, a.T);
@@ -1418,10 +1424,12 @@ int launch_bwd_t(const BwdArgs& a, int V, int64_t nc_grid, int stages, hipStream
     const char* e = std::getenv("KAIROS_GDN_BWD_DVL_WAVES");
     const int want = e ? std::atoi(e) : 0;
     bool split = false;
-    if constexpr (sizeof(TC) == 2 && K == 256) {       // the halves form (KAIROS_GDN_BWD_DVL_SPLIT=0: whole tiles)
+    if constexpr (sizeof(TC) == 2 && K >= 128) {       // the halves form (KAIROS_GDN_BWD_DVL_SPLIT=0: whole tiles)
       const char* es = std::getenv("KAIROS_GDN_BWD_DVL_SPLIT");
-      if (V % 256 == 0 && want == 0 && !(es && es[0] == '0' && es[1] == 0)) {
-        hipLaunchKernelGGL(bwd_dvl_split_kernel, grid, dim3(64 * DVL_SPLIT_NW), dvl_split_lds, s, a, V);
+      constexpr int VB = K;
+      if (V % VB == 0 && want == 0 && !(es && es[0] == '0' && es[1] == 0)) {
+        constexpr size_t lds_s = dvl_split_lds<K, VB>();
+        hipLaunchKernelGGL((bwd_dvl_split_kernel<K, VB>), grid, dim3(64 * DVL_SPLIT_NW), lds_s, s, a, V);
         split = true;
       }
     }
