@@ -3,6 +3,7 @@
 // fwd_h with row-major outputs: h [NC, H, K, V] and v_new [B*T, H, V]):
 //
 //   bwd_dvl_kernel    dv_local = mask_{j<=i}(scale k_j.q_i e^{g_i-g_j}) @ do   chunk_o.py:413-468
+//                     (bwd_dvl_split_kernel: the same with its tiles staged in parts)
 //   bwd_dhu_kernel    reverse state recurrence of dh, dv2 = gate (k @ dh) + dv_local, dh0
 //                                                                          chunk_delta_h.py:250-438
 //   bwd_dqkwg_kernel  dq, dk (state and intra-chunk terms), -dw, dg        chunk_o.py:147-326
@@ -10,6 +11,7 @@
 //                     the reverse chunk cumsum of dg                        wy_fast.py:98-210,
 //                                                                          chunk.py:140-145
 //   l2norm_bwd_kernel dx = dy rstd - sum(dy y) y rstd                      l2norm.py:132-154
+//                     (l2norm_bwd_rows_kernel: D / 8 lanes per row for power-of-two D)
 //
 // MFMA operands follow one convention in every kernel: the K index of a 32-deep
 // step is taken in "accumulator order" (rows 4 lg .. 4 lg + 3 and 16 + 4 lg ..
